@@ -1,0 +1,853 @@
+"""CPU oracle for the SCAO optimizer step -- TEST INFRASTRUCTURE ONLY.
+
+This module is the checker, never the product.  Only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import it.  The product (``scao_amd``) never imports, links or calls anything
+under ``oracle/``; on a machine without the HIP library the product raises.
+
+What it is: a restatement, in plain PyTorch on the CPU and in float32, of the
+reference optimizer's per-step data path (whispering3/scao).  Every function
+names the reference lines it follows.  Operation order, the dtype of every
+intermediate and the Python-float/ fp32 boundaries are kept as in the
+reference, because parity is judged against the reference's own CPU path:
+run on the same torch build it reproduces the reference bit for bit.
+
+How it is pinned (see tests/test_oracle_*.py):
+  * golden trajectories written by tests/golden/make_goldens.py from the
+    reference itself (imported once, in the build container only);
+  * closed forms: int8 quantisation known answers (1e-4*I -> code 127 on the
+    diagonal, zeros -> scale 1.0, ties to even), projection identities
+    (s = 1 gives identity, the complement of U_l/U_r is untouched), Phase 1
+    against torch.optim.AdamW(foreach=False), rank selection known answers.
+
+Parity-profile features (the ones the product accelerates) are restated in
+full.  The sparse gradient filter and noise injection are restated too
+(reference ``scao/optimizer.py:42-99, 544-545``) so that the oracle covers
+the reference's defaults; gSNR clip, lazy trigger, adaptive warmup and
+adaptive rank are restated from ``scao/optimizer.py:106-214, 383-401``.
+"""
+
+from __future__ import annotations
+
+import math
+import warnings
+from typing import Callable, Iterable, Optional
+
+import torch
+from torch import Tensor
+
+PRECOND_DTYPE = torch.float32
+
+
+# ---------------------------------------------------------------------------
+# utils  (reference scao/utils.py)
+# ---------------------------------------------------------------------------
+
+def to_2d(g: Tensor):
+    """scao/utils.py:208-219 -- 1-D -> (1, n); N-D -> (shape[0], rest)."""
+    shape = g.shape
+    if g.ndim == 1:
+        return g.unsqueeze(0), shape
+    if g.ndim == 2:
+        return g, shape
+    return g.reshape(shape[0], -1), shape
+
+
+def from_2d(g2: Tensor, shape) -> Tensor:
+    """scao/utils.py:222-226."""
+    return g2.reshape(shape)
+
+
+def quantize_sym_int8(x: Tensor):
+    """scao/utils.py:170-189.  Per-tensor symmetric int8.
+
+    The absmax is read to the host as a Python float (double); the scale is
+    the double quotient absmax/127; the division of x by the scale happens in
+    fp32 with the scale rounded to fp32; torch.round is half-to-even.
+    """
+    amax = x.abs().max().item()
+    if amax < 1e-30:
+        return torch.zeros_like(x, dtype=torch.int8), 1.0
+    scale = amax / 127.0
+    codes = (x / scale).round_().clamp_(-127, 127).to(torch.int8)
+    return codes, scale
+
+
+def dequantize_sym_int8(q: Tensor, scale: float) -> Tensor:
+    """scao/utils.py:192-203: fp32(code) * fp32(scale)."""
+    return q.to(torch.float32).mul_(scale)
+
+
+def low_rank_matrix_power_neg_quarter(U: Tensor, S: Tensor, eps: float = 1e-8):
+    """scao/utils.py:96-114: (U, clamp(S, eps)^(-1/4))."""
+    return U, S.clamp(min=eps).pow(-0.25)
+
+
+def adaptive_rank(eigenvalues: Tensor, epsilon: float = 0.05, k_min: int = 4,
+                  k_max: int = 128) -> int:
+    """scao/utils.py:121-151: smallest k whose leading (descending) eigenvalues
+    hold (1 - epsilon) of the spectral mass, clamped to [k_min, k_max]."""
+    total = eigenvalues.sum().item()
+    if total < 1e-12:
+        return k_min
+    thresh = (1.0 - epsilon) * total
+    csum = torch.cumsum(eigenvalues, dim=0)
+    hits = (csum >= thresh).nonzero(as_tuple=True)[0]
+    k = int(hits[0].item()) + 1 if hits.numel() > 0 else len(eigenvalues)
+    return int(min(k_max, max(k_min, k)))
+
+
+def matrix_power_neg_quarter(A: Tensor, eps: float = 1e-8) -> Tensor:
+    """scao/utils.py:88-93 (eigendecomposition branch): A^(-1/4)."""
+    w, V = torch.linalg.eigh(A)
+    w = w.clamp(min=eps)
+    return (V * w.pow(-0.25).unsqueeze(0)) @ V.T
+
+
+# ---------------------------------------------------------------------------
+# operator fallbacks  (reference scao/cuda/__init__.py:78-142)
+# ---------------------------------------------------------------------------
+
+def fused_kronecker_precond(U_l: Tensor, s_l_inv4: Tensor, U_r: Tensor,
+                            s_r_inv4: Tensor, G: Tensor) -> Tensor:
+    """scao/cuda/__init__.py:78-99:
+    P = (U_l^T G) U_r;  D = (s_l s_r^T - 1) * P;  out = G + (U_l D) U_r^T."""
+    proj = (U_l.T @ G) @ U_r
+    outer = s_l_inv4.unsqueeze(1) * s_r_inv4.unsqueeze(0)
+    delta = (outer - 1.0) * proj
+    return G + U_l @ delta @ U_r.T
+
+
+def low_rank_precond_mm(U: Tensor, s: Tensor, G: Tensor, left: bool = True) -> Tensor:
+    """scao/cuda/__init__.py:102-119."""
+    Us = U * s.unsqueeze(0)
+    if left:
+        return Us @ (U.T @ G)
+    return (G @ Us) @ U.T
+
+
+def int8_ema_update(ema_q: Tensor, ema_scale: float, new_val: Tensor, rho: float):
+    """scao/cuda/__init__.py:122-142: requantisation multiplies by the fp32
+    reciprocal of the new scale (unlike utils.quantize_sym_int8, which
+    divides)."""
+    x = ema_q.to(torch.float32).mul_(ema_scale)
+    x = x.mul_(rho).add_(new_val)
+    amax = x.abs().max().item()
+    scale = amax / 127.0 if amax > 1e-30 else 1.0
+    inv = 1.0 / scale if scale > 1e-30 else 0.0
+    q = x.mul_(inv).round_().clamp_(-127, 127).to(torch.int8)
+    return q, scale
+
+
+# ---------------------------------------------------------------------------
+# SparsePreconditioner  (reference scao/preconditioner.py:72-644)
+# ---------------------------------------------------------------------------
+
+class RefPreconditioner:
+    """Restatement of scao/preconditioner.py:72-644 (one parameter)."""
+
+    def __init__(self, param: Tensor, epsilon_sparse: float = 0.05, k_min: int = 8,
+                 k_max: int = 128, rho: float = 0.999, max_precond_dim: int = 4096,
+                 use_newton_schulz: bool = False, use_int8_ema: bool = False) -> None:
+        # preconditioner.py:108-134
+        p2, _ = to_2d(param)
+        m, n = p2.shape
+        self.original_shape = param.shape
+        self.m, self.n = m, n
+        self.epsilon_sparse = epsilon_sparse
+        dmin = min(m, n)
+        self.k_min = min(k_min, dmin)
+        self.k_max = min(k_max, dmin // 2) if dmin > 2 * self.k_min else self.k_min
+        self.rho = rho
+        self.use_newton_schulz = use_newton_schulz
+        self.use_int8_ema = use_int8_ema
+        self.device = param.device
+        self.param_dtype = param.dtype
+        # preconditioner.py:142-153 -- mode selection
+        two_d = param.ndim >= 2 and m > 1 and n > 1
+        self.use_block_diagonal = two_d and max(m, n) > max_precond_dim
+        self.use_kronecker = two_d and max(m, n) <= max_precond_dim
+        if self.use_kronecker and not use_newton_schulz:      # :160-161 (unused)
+            use_newton_schulz = min(m, n) > 512
+        if self.use_block_diagonal:
+            # preconditioner.py:163-194 -- split the larger dim into D-sized
+            # pieces plus a remainder; each piece gets its own preconditioner
+            # built from the caller's (unclamped) k_min/k_max.
+            rows_split = m >= n
+            big, small = (m, n) if rows_split else (n, m)
+            self._block_dim = 0 if rows_split else 1
+            sizes = [max_precond_dim] * (big // max_precond_dim)
+            if big % max_precond_dim:
+                sizes.append(big % max_precond_dim)
+            self._block_sizes = sizes
+            self._blocks = []
+            for bs in sizes:
+                shp = (bs, small) if rows_split else (small, bs)
+                self._blocks.append(RefPreconditioner(
+                    param.new_empty(shp), epsilon_sparse=epsilon_sparse, k_min=k_min,
+                    k_max=k_max, rho=rho, max_precond_dim=max_precond_dim,
+                    use_newton_schulz=use_newton_schulz, use_int8_ema=use_int8_ema))
+            self._k = self._blocks[0]._k if self._blocks else k_min
+        elif self.use_kronecker:
+            # preconditioner.py:196-231
+            k0 = min(k_min, min(m, n))
+            self._k = k0
+            L0 = torch.eye(m, device=self.device, dtype=PRECOND_DTYPE) * 1e-4
+            R0 = torch.eye(n, device=self.device, dtype=PRECOND_DTYPE) * 1e-4
+            if use_int8_ema:
+                self.L_ema_q, self.L_ema_scale = quantize_sym_int8(L0)
+                self.R_ema_q, self.R_ema_scale = quantize_sym_int8(R0)
+            else:
+                self.L_ema, self.R_ema = L0, R0
+            self.U_l = torch.eye(m, k0, device=self.device, dtype=PRECOND_DTYPE)
+            self.S_l = torch.ones(k0, device=self.device, dtype=PRECOND_DTYPE)
+            self.U_r = torch.eye(n, k0, device=self.device, dtype=PRECOND_DTYPE)
+            self.S_r = torch.ones(k0, device=self.device, dtype=PRECOND_DTYPE)
+        else:
+            # preconditioner.py:232-236 -- diagonal (1-D) mode
+            self.diag_ema = torch.zeros(param.shape, device=self.device, dtype=PRECOND_DTYPE)
+            self._diag_bias_factor = 1e-8
+            self._k = 1
+        self.precond_step = 0
+
+    # preconditioner.py:245-291
+    @property
+    def k(self) -> int:
+        return self._k
+
+    @k.setter
+    def k(self, new_k: int) -> None:
+        new_k = int(min(self.k_max, max(self.k_min, new_k)))
+        if self.use_block_diagonal:
+            for b in self._blocks:
+                b.k = new_k
+            self._k = sum(b._k for b in self._blocks) // max(len(self._blocks), 1)
+            return
+        if self.use_kronecker:
+            if new_k < self._k:
+                self.U_l = self.U_l[:, :new_k].contiguous()
+                self.S_l = self.S_l[:new_k].contiguous()
+                self.U_r = self.U_r[:, :new_k].contiguous()
+                self.S_r = self.S_r[:new_k].contiguous()
+            elif new_k > self._k:
+                cols = self.U_l.shape[1]
+                new_k = min(new_k, cols) if new_k > cols else new_k
+        self._k = new_k
+
+    def _slices(self, g2: Tensor):
+        off = 0
+        for bs, blk in zip(self._block_sizes, self._blocks):
+            if self._block_dim == 0:
+                yield blk, g2[off:off + bs, :], (slice(off, off + bs), slice(None))
+            else:
+                yield blk, g2[:, off:off + bs], (slice(None), slice(off, off + bs))
+            off += bs
+
+    @torch.no_grad()
+    def update_curvature(self, grad: Tensor) -> None:
+        """preconditioner.py:297-361."""
+        self.precond_step += 1
+        g2, _ = to_2d(grad.to(PRECOND_DTYPE))
+        if self.use_block_diagonal:
+            for blk, gb, _ in self._slices(g2):
+                blk.update_curvature(gb)
+            self._k = sum(b._k for b in self._blocks) // max(len(self._blocks), 1)
+            return
+        if not self.use_kronecker:
+            sq = g2.squeeze(0) if g2.shape[0] == 1 else g2
+            self.diag_ema.mul_(self.rho).add_((1.0 - self.rho) * sq.reshape_as(self.diag_ema).pow(2))
+            self._diag_bias_factor = max(1.0 - self.rho ** self.precond_step, 1e-8)
+            return
+        a = 1.0 - self.rho
+        if self.use_int8_ema:
+            Lf = dequantize_sym_int8(self.L_ema_q, self.L_ema_scale)
+            Lf = Lf.mul_(self.rho).add_(a * (g2 @ g2.T))
+            self.L_ema_q, self.L_ema_scale = quantize_sym_int8(Lf)
+            Rf = dequantize_sym_int8(self.R_ema_q, self.R_ema_scale)
+            Rf = Rf.mul_(self.rho).add_(a * (g2.T @ g2))
+            self.R_ema_q, self.R_ema_scale = quantize_sym_int8(Rf)
+        else:
+            self.L_ema.mul_(self.rho).add_(a * (g2 @ g2.T))
+            self.R_ema.mul_(self.rho).add_(a * (g2.T @ g2))
+        self._update_eigenfactors(1.0 - self.rho ** self.precond_step)
+
+    @staticmethod
+    def _eig_desc(A: Tensor, eps: float):
+        """preconditioner.py:412-428 -- eigh with one diagonal-shift retry, then
+        descending order with eigenvalues clamped at 0."""
+        try:
+            w, V = torch.linalg.eigh(A)
+        except torch.linalg.LinAlgError:
+            A.diagonal().add_(eps)
+            w, V = torch.linalg.eigh(A)
+        return w.flip(0).clamp(min=0.0), V.flip(1)
+
+    @torch.no_grad()
+    def _update_eigenfactors(self, bias_factor: float = 1.0) -> None:
+        """preconditioner.py:365-451."""
+        eps = 1e-8
+        if self.use_int8_ema:
+            Lf = dequantize_sym_int8(self.L_ema_q, self.L_ema_scale)
+            Rf = dequantize_sym_int8(self.R_ema_q, self.R_ema_scale)
+        else:
+            Lf, Rf = self.L_ema, self.R_ema
+        Ld = Lf / max(bias_factor, eps)
+        Rd = Rf / max(bias_factor, eps)
+        tik_l = max(eps, 1e-4 * Ld.trace().item() / self.m)
+        tik_r = max(eps, 1e-4 * Rd.trace().item() / self.n)
+        Lreg = Ld.clone()
+        Lreg.diagonal().add_(tik_l)
+        Rreg = Rd.clone()
+        Rreg.diagonal().add_(tik_r)
+        rng = torch.get_rng_state()
+        S_l, U_l = self._eig_desc(Lreg, eps)
+        S_r, U_r = self._eig_desc(Rreg, eps)
+        torch.set_rng_state(rng)
+        kl = adaptive_rank(S_l, self.epsilon_sparse, self.k_min, self.k_max)
+        kr = adaptive_rank(S_r, self.epsilon_sparse, self.k_min, self.k_max)
+        k = min(kl, kr)
+        k = max(k, self._k - 1)
+        k = min(k, self._k + 4)
+        k = int(min(self.k_max, max(self.k_min, k)))
+        self._k = k
+        self.U_l = U_l[:, :k].contiguous()
+        self.S_l = S_l[:k].contiguous()
+        self.U_r = U_r[:, :k].contiguous()
+        self.S_r = S_r[:k].contiguous()
+
+    @torch.no_grad()
+    def precondition(self, grad: Tensor) -> Tensor:
+        """preconditioner.py:457-521."""
+        dt = grad.dtype
+        g2, shape = to_2d(grad.to(PRECOND_DTYPE))
+        if self.use_block_diagonal:
+            out = torch.zeros_like(g2)
+            for blk, gb, idx in self._slices(g2):
+                out[idx] = blk.precondition(gb).to(PRECOND_DTYPE)
+            return from_2d(out, shape).to(dt)
+        if not self.use_kronecker:
+            bias = getattr(self, "_diag_bias_factor", 1.0)
+            den = (self.diag_ema / bias).reshape_as(g2).pow(0.25).add_(1e-8)
+            return from_2d(g2 / den, shape).to(dt)
+        _, sl = low_rank_matrix_power_neg_quarter(self.U_l, self.S_l, 1e-8)
+        _, sr = low_rank_matrix_power_neg_quarter(self.U_r, self.S_r, 1e-8)
+        out = fused_kronecker_precond(self.U_l, sl, self.U_r, sr, g2)
+        return from_2d(out, shape).to(dt)
+
+    @torch.no_grad()
+    def natural_grad_norm(self, grad: Tensor, eps: float = 1e-8) -> Tensor:
+        """preconditioner.py:527-564."""
+        g2, _ = to_2d(grad.to(PRECOND_DTYPE))
+        if self.use_block_diagonal:
+            parts = [blk.natural_grad_norm(gb, eps=eps).pow(2) for blk, gb, _ in self._slices(g2)]
+            return torch.stack(parts).sum().sqrt()
+        if not self.use_kronecker:
+            den = self.diag_ema.reshape_as(g2).pow(0.5).add_(eps)
+            return (g2.pow(2) / den).sum().sqrt()
+        il = self.S_l.clamp(min=eps).pow(-0.5)
+        ir = self.S_r.clamp(min=eps).pow(-0.5)
+        proj = (self.U_l.T @ g2) @ self.U_r
+        return (il.unsqueeze(1) * proj * ir.unsqueeze(0)).norm(p="fro")
+
+    def state_dict(self) -> dict:
+        """preconditioner.py:570-600."""
+        d = {"precond_step": self.precond_step, "k": self._k,
+             "use_kronecker": self.use_kronecker,
+             "use_block_diagonal": self.use_block_diagonal}
+        if self.use_block_diagonal:
+            d["blocks"] = [b.state_dict() for b in self._blocks]
+        elif self.use_kronecker:
+            if self.use_int8_ema:
+                d.update({"L_ema_q": self.L_ema_q, "L_ema_scale": self.L_ema_scale,
+                          "R_ema_q": self.R_ema_q, "R_ema_scale": self.R_ema_scale})
+            else:
+                d.update({"L_ema": self.L_ema, "R_ema": self.R_ema})
+            d.update({"U_l": self.U_l, "S_l": self.S_l, "U_r": self.U_r, "S_r": self.S_r})
+        else:
+            d["diag_ema"] = self.diag_ema
+        return d
+
+    def memory_bytes(self) -> int:
+        """preconditioner.py:602-619."""
+        if self.use_block_diagonal:
+            return sum(b.memory_bytes() for b in self._blocks)
+        tot = 0
+        if self.use_kronecker:
+            if self.use_int8_ema:
+                tot += self.L_ema_q.numel() + 8 + self.R_ema_q.numel() + 8
+            else:
+                tot += self.L_ema.numel() * self.L_ema.element_size()
+                tot += self.R_ema.numel() * self.R_ema.element_size()
+            for t in (self.U_l, self.S_l, self.U_r, self.S_r):
+                tot += t.numel() * t.element_size()
+        else:
+            tot += self.diag_ema.numel() * self.diag_ema.element_size()
+        return tot
+
+    def load_state_dict(self, st: dict) -> None:
+        """preconditioner.py:621-644."""
+        self.precond_step = st["precond_step"]
+        self._k = st["k"]
+        if self.use_block_diagonal:
+            for b, bs in zip(self._blocks, st["blocks"]):
+                b.load_state_dict(bs)
+        elif self.use_kronecker:
+            if self.use_int8_ema:
+                self.L_ema_q = st["L_ema_q"].to(device=self.device, dtype=torch.int8)
+                self.L_ema_scale = float(st["L_ema_scale"])
+                self.R_ema_q = st["R_ema_q"].to(device=self.device, dtype=torch.int8)
+                self.R_ema_scale = float(st["R_ema_scale"])
+            else:
+                self.L_ema.copy_(st["L_ema"])
+                self.R_ema.copy_(st["R_ema"])
+            for name in ("U_l", "S_l", "U_r", "S_r"):
+                setattr(self, name, st[name].to(device=self.device, dtype=PRECOND_DTYPE))
+        else:
+            self.diag_ema.copy_(st["diag_ema"])
+
+
+# ---------------------------------------------------------------------------
+# v3 helpers  (reference scao/optimizer.py:42-214)
+# ---------------------------------------------------------------------------
+
+class RefSparseFilter:
+    """scao/optimizer.py:42-57: EMA-of-magnitude mask at the `sparsity` quantile."""
+
+    def __init__(self, sparsity: float = 0.7, ema: float = 0.99):
+        self.sparsity, self.ema, self.mag_ema = sparsity, ema, None
+
+    def __call__(self, grad: Tensor) -> Tensor:
+        mag = grad.abs().detach()
+        if self.mag_ema is None:
+            self.mag_ema = mag.clone()
+        else:
+            self.mag_ema.mul_(self.ema).add_((1.0 - self.ema) * mag)
+        thr = torch.quantile(self.mag_ema.float(), self.sparsity)
+        return grad * (self.mag_ema >= thr).to(grad.dtype)
+
+
+class RefDynamicSparseFilter(RefSparseFilter):
+    """scao/optimizer.py:60-99."""
+
+    def __init__(self, base_sparsity=0.7, min_sparsity=0.3, max_sparsity=0.9, ema=0.99,
+                 norm_ema=0.95):
+        super().__init__(sparsity=base_sparsity, ema=ema)
+        self.base_sparsity, self.min_sparsity, self.max_sparsity = base_sparsity, min_sparsity, max_sparsity
+        self.norm_ema_coeff = norm_ema
+        self._norm_ema = 1.0
+        self._global_norm_ema = 1.0
+
+    def set_global_norm_ref(self, v: float) -> None:
+        self._global_norm_ema = max(v, 1e-8)
+
+    def __call__(self, grad: Tensor) -> Tensor:
+        ln = float(grad.norm())
+        self._norm_ema = self.norm_ema_coeff * self._norm_ema + (1.0 - self.norm_ema_coeff) * ln
+        ratio = self._norm_ema / self._global_norm_ema
+        margin = 0.2 * (1.0 - min(ratio, 2.0) / 2.0)
+        self.sparsity = float(max(self.min_sparsity, min(self.max_sparsity, self.base_sparsity + margin)))
+        return super().__call__(grad)
+
+
+class RefWarmupScheduler:
+    """scao/optimizer.py:106-154."""
+
+    def __init__(self, warmup_steps=100, stability_threshold=0.05, patience=5, min_warmup=20):
+        self.warmup_steps, self.stability_threshold = warmup_steps, stability_threshold
+        self.patience, self.min_warmup = patience, min_warmup
+        self._prev_norm = float("inf")
+        self._stable_count = 0
+        self._early_exit_step = None
+
+    def update(self, step: int, avg: float) -> bool:
+        if step < self.min_warmup:
+            return True
+        if self._prev_norm > 0:
+            rel = abs(avg - self._prev_norm) / (self._prev_norm + 1e-8)
+            self._stable_count = self._stable_count + 1 if rel < self.stability_threshold else 0
+        self._prev_norm = avg
+        if self._stable_count >= self.patience:
+            self._early_exit_step = self._early_exit_step or step
+            return False
+        return step < self.warmup_steps
+
+    @property
+    def exited_early(self) -> bool:
+        return self._early_exit_step is not None
+
+    @property
+    def actual_warmup_steps(self) -> int:
+        return self._early_exit_step or self.warmup_steps
+
+
+def gsnr_clip(grad, m, v, eps, thr):
+    """scao/optimizer.py:161-175."""
+    snr = m.abs() / (v.sqrt() + eps)
+    return grad * (snr >= thr).to(grad.dtype)
+
+
+class RefLazyTrigger:
+    """scao/optimizer.py:182-214."""
+
+    def __init__(self, delta_threshold=0.1, max_skip=50):
+        self.delta_threshold, self.max_skip = delta_threshold, max_skip
+        self._prev_grad_norm = 0.0
+        self._steps_since_update = 0
+
+    def should_update(self, gn: float) -> bool:
+        self._steps_since_update += 1
+        if self._steps_since_update >= self.max_skip:
+            self._steps_since_update = 0
+            self._prev_grad_norm = gn
+            return True
+        if self._prev_grad_norm > 0:
+            rel = abs(gn - self._prev_grad_norm) / (self._prev_grad_norm + 1e-8)
+            if rel > self.delta_threshold:
+                self._steps_since_update = 0
+                self._prev_grad_norm = gn
+                return True
+        self._prev_grad_norm = gn
+        return False
+
+
+# ---------------------------------------------------------------------------
+# SCAO  (reference scao/optimizer.py:221-801)
+# ---------------------------------------------------------------------------
+
+class RefSCAO(torch.optim.Optimizer):
+    """Restatement of scao/optimizer.py:221-801 on the CPU.
+
+    ``async_precond`` is accepted and ignored: on the CPU the reference runs
+    the refresh inline (optimizer.py:317-319, 660-665).
+    """
+
+    def __init__(self, params: Iterable, lr=1e-3, betas=(0.9, 0.999), eps=1e-8,
+                 weight_decay=0.01, precond_freq=20, epsilon_sparse=0.05, k_min=8,
+                 k_max=128, rho=0.999, tau: Optional[float] = 1.0, warmup_steps=100,
+                 blend_steps=50, min_precond_updates=10, max_precond_dim=4096,
+                 use_newton_schulz=False, use_int8_ema=False, async_precond=True,
+                 beta3=0.99, sparsity=0.7, noise_std_init=0.01, noise_anneal=0.998,
+                 lars_coeff=1e-3, lookahead_k=5, lookahead_alpha=0.5,
+                 dynamic_sparsity=False, adaptive_warmup=False,
+                 warmup_stability_threshold=0.05, warmup_patience=5, lazy_precond=False,
+                 lazy_delta_threshold=0.1, lazy_max_skip=50, use_gsnr_clip=False,
+                 gsnr_threshold=0.5, adaptive_rank=False) -> None:
+        # optimizer.py:297-304
+        if lr < 0:
+            raise ValueError(f"Invalid lr: {lr}")
+        if not (0.0 <= betas[0] < 1.0):
+            raise ValueError(f"Invalid beta1: {betas[0]}")
+        if not (0.0 <= betas[1] < 1.0):
+            raise ValueError(f"Invalid beta2: {betas[1]}")
+        if not (0.0 <= beta3 < 1.0):
+            raise ValueError(f"Invalid beta3: {beta3}")
+        # optimizer.py:306-314 -- the 18 per-group keys
+        defaults = dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay,
+                        precond_freq=precond_freq, epsilon_sparse=epsilon_sparse,
+                        k_min=k_min, k_max=k_max, rho=rho, tau=tau,
+                        warmup_steps=warmup_steps, blend_steps=blend_steps,
+                        min_precond_updates=min_precond_updates,
+                        max_precond_dim=max_precond_dim, use_newton_schulz=use_newton_schulz,
+                        use_int8_ema=use_int8_ema, beta3=beta3, lars_coeff=lars_coeff)
+        super().__init__(params, defaults)
+        self._precond_stream = None
+        self._callbacks: list = []
+        self._global_step = 0
+        self._noise_std = noise_std_init
+        self._noise_anneal = noise_anneal
+        self._lookahead_k = lookahead_k
+        self._lookahead_alpha = lookahead_alpha
+        self._slow_weights: dict = {}
+        self._sparsity = sparsity
+        self._dynamic_sparsity = dynamic_sparsity
+        self._sparse_filters: dict = {}
+        self._global_norm_ema = 1.0
+        self._adaptive_warmup = adaptive_warmup
+        self._warmup_scheduler = RefWarmupScheduler(
+            warmup_steps=warmup_steps, stability_threshold=warmup_stability_threshold,
+            patience=warmup_patience, min_warmup=max(20, warmup_steps // 5))
+        self._lazy_precond = lazy_precond
+        self._lazy_triggers: dict = {}
+        self._lazy_delta_threshold = lazy_delta_threshold
+        self._lazy_max_skip = lazy_max_skip
+        self._use_gsnr_clip = use_gsnr_clip
+        self._gsnr_threshold = gsnr_threshold
+        self._adaptive_rank = adaptive_rank
+        self._in_warmup_global = True
+
+    @torch.no_grad()
+    def _lookahead_sync(self) -> None:
+        """optimizer.py:356-365."""
+        for g in self.param_groups:
+            for p in g["params"]:
+                slow = self._slow_weights.setdefault(id(p), p.data.clone())
+                slow.add_(self._lookahead_alpha * (p.data - slow))
+                p.data.copy_(slow)
+
+    @staticmethod
+    def _lars_scale(p: Tensor, upd: Tensor, c: float, wd: float) -> float:
+        """optimizer.py:371-377 (norm of p taken after the decoupled decay)."""
+        pn = p.data.norm()
+        un = upd.norm()
+        if pn == 0 or un == 0:
+            return 1.0
+        return float(c * pn / (un + wd * pn + 1e-8))
+
+    def _maybe_adjust_rank(self, pre: RefPreconditioner, gn: float, group: dict) -> None:
+        """optimizer.py:383-401."""
+        if not self._adaptive_rank:
+            return
+        ratio = gn / (self._global_norm_ema + 1e-8)
+        cur = pre.k
+        if ratio > 2.0:
+            nk = min(group["k_max"], int(cur * 1.25))
+        elif ratio < 0.5:
+            nk = max(group["k_min"], int(cur * 0.8))
+        else:
+            return
+        if nk != cur:
+            pre.k = nk
+
+    def _init_state(self, p: Tensor, group: dict) -> None:
+        """optimizer.py:407-433."""
+        st = self.state[p]
+        if len(st) > 0:
+            return
+        st["step"] = 0
+        st["scao_step"] = 0
+        for key in ("exp_avg", "exp_avg_sq", "exp_avg_diff", "prev_grad"):
+            st[key] = torch.zeros_like(p, dtype=torch.float32, memory_format=torch.preserve_format)
+        st["preconditioner"] = RefPreconditioner(
+            param=p, epsilon_sparse=group["epsilon_sparse"], k_min=group["k_min"],
+            k_max=group["k_max"], rho=group["rho"], max_precond_dim=group["max_precond_dim"],
+            use_newton_schulz=group["use_newton_schulz"], use_int8_ema=group["use_int8_ema"])
+
+    def _compute_avg_grad_norm(self) -> float:
+        """optimizer.py:439-446."""
+        norms = [float(p.grad.norm()) for g in self.param_groups for p in g["params"]
+                 if p.grad is not None]
+        if not norms:
+            return 0.0
+        avg = sum(norms) / len(norms)
+        self._global_norm_ema = 0.95 * self._global_norm_ema + 0.05 * avg
+        return avg
+
+    @torch.no_grad()
+    def step(self, closure: Optional[Callable] = None):
+        """optimizer.py:452-503."""
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        self._global_step += 1
+        avg = self._compute_avg_grad_norm()
+        if self._dynamic_sparsity:
+            for f in self._sparse_filters.values():
+                if isinstance(f, RefDynamicSparseFilter):
+                    f.set_global_norm_ref(self._global_norm_ema)
+        if self._adaptive_warmup:
+            self._in_warmup_global = self._warmup_scheduler.update(self._global_step, avg)
+        else:
+            wmax = max((g.get("warmup_steps", 100) for g in self.param_groups), default=100)
+            self._in_warmup_global = self._global_step <= wmax
+        for group in self.param_groups:
+            self._step_group(group, avg)
+        self._noise_std *= self._noise_anneal
+        if self._lookahead_k > 0 and self._global_step % self._lookahead_k == 0:
+            self._lookahead_sync()
+        if self._callbacks:
+            metrics = collect_metrics(self)
+            metrics["noise_std"] = self._noise_std
+            metrics["global_norm_ema"] = self._global_norm_ema
+            metrics["warmup_active"] = self._in_warmup_global
+            for cb in self._callbacks:
+                cb(metrics)
+        return loss
+
+    def _step_group(self, group: dict, avg_norm: float) -> None:
+        """optimizer.py:509-645."""
+        lr = group["lr"]
+        beta1, beta2 = group["betas"]
+        beta3 = group["beta3"]
+        eps = group["eps"]
+        wd = group["weight_decay"]
+        freq = group["precond_freq"]
+        tau = group["tau"]
+        warm = group["warmup_steps"]
+        min_pu = group["min_precond_updates"]
+        lars = group["lars_coeff"]
+        for p in group["params"]:
+            if p.grad is None:
+                continue
+            if p.grad.is_sparse:
+                raise RuntimeError("SCAO does not support sparse gradients.")
+            self._init_state(p, group)
+            st = self.state[p]
+            st["step"] += 1
+            t = st["step"]
+            pid = id(p)
+            grad = p.grad.float()
+            gnorm = float(grad.norm())
+            if self._sparsity > 0.0:
+                if pid not in self._sparse_filters:
+                    self._sparse_filters[pid] = (RefDynamicSparseFilter(base_sparsity=self._sparsity)
+                                                 if self._dynamic_sparsity
+                                                 else RefSparseFilter(self._sparsity))
+                grad = self._sparse_filters[pid](grad)
+            if self._noise_std > 1e-9:
+                grad = grad + torch.randn_like(grad) * self._noise_std
+            if wd != 0.0:
+                p.mul_(1.0 - lr * wd)
+            m, v, d, prev = st["exp_avg"], st["exp_avg_sq"], st["exp_avg_diff"], st["prev_grad"]
+            pre: RefPreconditioner = st["preconditioner"]
+            self._maybe_adjust_rank(pre, gnorm, group)
+            in_warm = (self._in_warmup_global if self._adaptive_warmup else (t <= warm)) \
+                or (pre.precond_step < min_pu)
+            if in_warm:
+                # Phase 1: Adam(W) -- optimizer.py:567-578
+                m.mul_(beta1).add_(grad, alpha=1.0 - beta1)
+                v.mul_(beta2).addcmul_(grad, grad, value=1.0 - beta2)
+                bc1 = 1.0 - beta1 ** t
+                bc2 = 1.0 - beta2 ** t
+                den = (v.sqrt() / math.sqrt(bc2)).add_(eps)
+                if t % freq == 0:
+                    pre.update_curvature(p.grad.detach())
+                p.add_((m / den).to(p.dtype), alpha=-(lr / bc1))
+                prev.copy_(grad)
+                continue
+            # Phase 2 -- optimizer.py:584-645
+            if not st.get("scao_phase_started", False):
+                st["scao_phase_started"] = True
+                st["phase2_start_step"] = t
+                st["scao_step"] = 0
+            st["scao_step"] += 1
+            ss = st["scao_step"]
+            if self._lazy_precond:
+                if pid not in self._lazy_triggers:
+                    self._lazy_triggers[pid] = RefLazyTrigger(self._lazy_delta_threshold,
+                                                              self._lazy_max_skip)
+                refresh = self._lazy_triggers[pid].should_update(gnorm)
+            else:
+                refresh = (t % freq == 0)
+            if refresh:
+                pre.update_curvature(p.grad.detach())
+            gp = pre.precondition(p.grad)
+            if tau is not None:
+                nat = pre.natural_grad_norm(p.grad, eps=eps)
+                if nat > tau:
+                    gp = gp * (tau / nat.clamp(min=eps))
+            bsteps = group.get("blend_steps", 50)
+            b = min(1.0, ss / bsteps) if bsteps > 0 else 1.0
+            geff = b * gp.float() + (1.0 - b) * grad
+            delta = grad - prev
+            prev.copy_(grad)
+            m.mul_(beta1).add_(geff, alpha=1.0 - beta1)
+            d.mul_(beta3).add_(delta, alpha=1.0 - beta3)
+            gad = geff + (1.0 - beta3) * delta
+            v.mul_(beta2).addcmul_(gad, gad, value=1.0 - beta2)
+            bc1 = 1.0 - beta1 ** t
+            bc2 = 1.0 - beta2 ** t
+            bc3 = 1.0 - beta3 ** t
+            upd = (m / bc1 + (1.0 - beta3) * (d / bc3)) / (v / bc2).sqrt().add_(eps)
+            if self._use_gsnr_clip:
+                upd = gsnr_clip(upd, m, v, eps, self._gsnr_threshold)
+            trust = self._lars_scale(p, upd, lars, wd) if lars > 0 else 1.0
+            p.add_(upd.to(p.dtype), alpha=-(lr * trust))
+
+    def synchronize_precond(self) -> None:
+        """optimizer.py:680-684 (no side stream on the CPU)."""
+
+    def add_callback(self, cb) -> None:
+        self._callbacks.append(cb)
+
+    def remove_callback(self, cb) -> None:
+        try:
+            self._callbacks.remove(cb)
+        except ValueError:
+            pass
+
+    def clear_callbacks(self) -> None:
+        self._callbacks.clear()
+
+    def state_dict(self) -> dict:
+        """optimizer.py:732-756."""
+        self.synchronize_precond()
+        base = super().state_dict()
+        base["_scao_precond"] = {i: st["preconditioner"].state_dict()
+                                 for i, st in enumerate(self.state.values())
+                                 if "preconditioner" in st}
+        ws = self._warmup_scheduler
+        base["_scao_runtime"] = {
+            "global_step": self._global_step, "noise_std": self._noise_std,
+            "global_norm_ema": self._global_norm_ema, "warmup_prev_norm": ws._prev_norm,
+            "warmup_stable_count": ws._stable_count,
+            "warmup_early_exit_step": ws._early_exit_step}
+        return base
+
+    def load_state_dict(self, state_dict: dict) -> None:
+        """optimizer.py:758-776.  A preconditioner object that is not this
+        module's type (e.g. one written by the GPU product) is rebuilt from
+        the param and group before the portable ``_scao_precond`` entry is
+        loaded into it."""
+        sd = dict(state_dict)
+        extra = sd.pop("_scao_precond", {})
+        rt = sd.pop("_scao_runtime", {})
+        super().load_state_dict(sd)
+        owner = {id(p): g for g in self.param_groups for p in g["params"]}
+        for i, (p, st) in enumerate(self.state.items()):
+            if "preconditioner" in st and not isinstance(st["preconditioner"], RefPreconditioner):
+                g = owner[id(p)]
+                st["preconditioner"] = RefPreconditioner(
+                    param=p, epsilon_sparse=g["epsilon_sparse"], k_min=g["k_min"],
+                    k_max=g["k_max"], rho=g["rho"], max_precond_dim=g["max_precond_dim"],
+                    use_newton_schulz=g["use_newton_schulz"], use_int8_ema=g["use_int8_ema"])
+            if i in extra and "preconditioner" in st:
+                st["preconditioner"].load_state_dict(extra[i])
+        if rt:
+            self._global_step = int(rt.get("global_step", self._global_step))
+            self._noise_std = float(rt.get("noise_std", self._noise_std))
+            self._global_norm_ema = float(rt.get("global_norm_ema", self._global_norm_ema))
+            ws = self._warmup_scheduler
+            ws._prev_norm = float(rt.get("warmup_prev_norm", ws._prev_norm))
+            ws._stable_count = int(rt.get("warmup_stable_count", ws._stable_count))
+            ws._early_exit_step = rt.get("warmup_early_exit_step", ws._early_exit_step)
+
+    def current_ranks(self) -> dict:
+        """optimizer.py:782-787."""
+        return {i: st["preconditioner"].k for i, st in enumerate(self.state.values())
+                if "preconditioner" in st}
+
+
+def collect_metrics(opt) -> dict:
+    """scao/logging.py:151-219 (used by the oracle's callback path)."""
+    step = 0
+    ranks, lnorms = [], []
+    for st in opt.state.values():
+        if "step" in st:
+            step = max(step, st["step"])
+        if "preconditioner" in st:
+            pre = st["preconditioner"]
+            ranks.append(pre.k)
+            if getattr(pre, "use_block_diagonal", False):
+                bn = []
+                for b in pre._blocks:
+                    if b.use_kronecker:
+                        bn.append(b.L_ema_scale * 127.0 if getattr(b, "use_int8_ema", False)
+                                  else b.L_ema.norm(p="fro").item())
+                if bn:
+                    lnorms.append(sum(bn) / len(bn))
+            elif getattr(pre, "use_kronecker", False):
+                lnorms.append(pre.L_ema_scale * 127.0 if getattr(pre, "use_int8_ema", False)
+                              else pre.L_ema.norm(p="fro").item())
+    out = {"step": step}
+    if ranks:
+        out.update({"scao/rank_mean": sum(ranks) / len(ranks), "scao/rank_min": min(ranks),
+                    "scao/rank_max": max(ranks), "scao/layers": len(ranks)})
+    if lnorms:
+        out["scao/L_norm_mean"] = sum(lnorms) / len(lnorms)
+    out["scao/precond_freq"] = opt.param_groups[0].get("precond_freq", -1)
+    ws = getattr(opt, "_warmup_scheduler", None)
+    if ws is not None:
+        out["scao/warmup_exited_early"] = ws.exited_early
+        out["scao/actual_warmup_steps"] = ws.actual_warmup_steps
+    return out

@@ -1,0 +1,259 @@
+"""Write the golden fixtures that pin the CPU oracle (oracle/scao_ref.py).
+
+Run in the build container only:  python tests/golden/make_goldens.py
+It imports the reference package from /root/reference (read-only), runs it
+on the CPU on seeded inputs and stores inputs/outputs as data under
+tests/golden/.  Nothing else in the repository imports this script or the
+reference; the GPU box never sees either.
+
+Cases (all grads for step t come from torch.Generator().manual_seed(1000+t),
+drawn param by param in group order; params from manual_seed(0)):
+  traj_int8     -- block-diagonal (row and column splits with remainders),
+                   Kronecker, conv-shaped and 1-D params; int8 EMA; adaptive
+                   rank; tau=1, LARS on; Phase 1 -> blend -> Phase 2.
+  traj_fp32     -- fp32 EMA, tau=None, LARS off, fixed rank.
+  traj_misc     -- lookahead, blend_steps=0, strong weight decay, int8.
+  traj_bf16     -- bf16 params and grads.
+  traj_sparse   -- default sparse filter (quantile mask) on, int8.
+  ops           -- operator-level vectors (projection, int8 EMA update,
+                   low-rank mm, quantise, adaptive rank, natural norm).
+  c1_summary    -- the 768x3072 parity config, 100 steps: per-step norms,
+                   leading values, int8 code digests, scales and ranks.
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import sys
+import warnings
+
+import torch
+from safetensors.torch import save_file
+
+REF = "/root/reference"
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+PARITY = dict(sparsity=0.0, noise_std_init=0.0, async_precond=False, lookahead_k=0)
+
+SMALL_SHAPES = {
+    "w_col": (20, 80),      # D=32 -> column blocks 32, 32, 16
+    "w_row": (70, 12),      # D=32 -> row blocks 32, 32, 6
+    "w_kron": (12, 20),     # Kronecker
+    "w_conv": (4, 3, 2, 2),  # to_2d -> (4, 12), Kronecker
+    "b": (20,),             # diagonal
+}
+
+
+def make_params(shapes, dtype=torch.float32, scale=0.02):
+    g = torch.Generator().manual_seed(0)
+    return {k: torch.nn.Parameter((torch.randn(s, generator=g) * scale).to(dtype))
+            for k, s in shapes.items()}
+
+
+def grads_for_step(t, params, scale=0.02, outliers=0.0):
+    g = torch.Generator().manual_seed(1000 + t)
+    out = {}
+    for k, p in params.items():
+        x = torch.randn(p.shape, generator=g) * scale
+        if outliers > 0:
+            mask = torch.rand(p.shape, generator=g) < outliers
+            x = torch.where(mask, x * 50.0, x)
+        out[k] = x.to(p.dtype)
+    return out
+
+
+def flatten_precond(prefix, d, tensors, meta):
+    for key, val in d.items():
+        name = f"{prefix}.{key}"
+        if key == "blocks":
+            meta[name] = len(val)
+            for i, b in enumerate(val):
+                flatten_precond(f"{name}.{i}", b, tensors, meta)
+        elif isinstance(val, torch.Tensor):
+            tensors[name] = val.detach().clone().contiguous()
+        else:
+            meta[name] = val
+
+
+def run_traj(scao, name, cfg, steps, snap_steps, dtype=torch.float32, outliers=0.0):
+    params = make_params(SMALL_SHAPES, dtype)
+    opt = scao.SCAO(list(params.values()), **cfg)
+    tensors, meta = {}, {"config": {k: (list(v) if isinstance(v, tuple) else v)
+                                    for k, v in cfg.items()},
+                         "steps": steps, "dtype": str(dtype), "names": list(params),
+                         "shapes": {k: list(v) for k, v in SMALL_SHAPES.items()},
+                         "outliers": outliers}
+    for k, p in params.items():
+        tensors[f"init.{k}"] = p.detach().clone()
+    per_step = []
+    for t in range(1, steps + 1):
+        gr = grads_for_step(t, params, outliers=outliers)
+        for k, p in params.items():
+            p.grad = gr[k].clone()
+        opt.step()
+        rec = {"global_step": opt._global_step, "global_norm_ema": opt._global_norm_ema,
+               "ranks": {str(i): k for i, k in opt.current_ranks().items()}}
+        for i, (k, p) in enumerate(params.items()):
+            st = opt.state[p]
+            tensors[f"step{t}.p.{k}"] = p.detach().clone()
+            rec[k] = {"step": st["step"], "scao_step": st["scao_step"],
+                      "phase2": bool(st.get("scao_phase_started", False)),
+                      "precond_step": st["preconditioner"].precond_step}
+        per_step.append(rec)
+        if t in snap_steps:
+            sd = opt.state_dict()
+            for i, (k, p) in enumerate(params.items()):
+                st = opt.state[p]
+                for key in ("exp_avg", "exp_avg_sq", "exp_avg_diff", "prev_grad"):
+                    tensors[f"snap{t}.{k}.{key}"] = st[key].detach().clone()
+            for idx, d in sd["_scao_precond"].items():
+                flatten_precond(f"snap{t}.precond{idx}", d, tensors, meta)
+            meta[f"snap{t}.runtime"] = sd["_scao_runtime"]
+            meta[f"snap{t}.state_keys"] = {str(i): sorted(v.keys()) for i, v in sd["state"].items()}
+            meta[f"snap{t}.group_keys"] = sorted(k for k in sd["param_groups"][0] if k != "params")
+    meta["per_step"] = per_step
+    meta["snap_steps"] = list(snap_steps)
+    save_file(tensors, os.path.join(HERE, f"{name}.safetensors"))
+    with open(os.path.join(HERE, f"{name}.json"), "w") as f:
+        json.dump(meta, f, indent=1, sort_keys=True, default=str)
+    print(f"{name}: {len(tensors)} tensors")
+
+
+def run_ops(scao):
+    from scao import utils as U
+    from scao.cuda import _fused_kronecker_precond_pytorch, _low_rank_precond_mm_pytorch, \
+        _int8_ema_update_pytorch
+    from scao.preconditioner import SparsePreconditioner
+    g = torch.Generator().manual_seed(7)
+    T, M = {}, {}
+    for i, (m, n, k) in enumerate([(48, 64, 8), (33, 70, 5), (64, 40, 16)]):
+        G = torch.randn(m, n, generator=g)
+        Ul, _ = torch.linalg.qr(torch.randn(m, k, generator=g))
+        Ur, _ = torch.linalg.qr(torch.randn(n, k, generator=g))
+        sl = torch.rand(k, generator=g) + 0.2
+        sr = torch.rand(k, generator=g) + 0.2
+        T.update({f"fkp{i}.G": G, f"fkp{i}.Ul": Ul.contiguous(), f"fkp{i}.Ur": Ur.contiguous(),
+                  f"fkp{i}.sl": sl, f"fkp{i}.sr": sr,
+                  f"fkp{i}.out": _fused_kronecker_precond_pytorch(Ul, sl, Ur, sr, G)})
+        T[f"lrmm{i}.left"] = _low_rank_precond_mm_pytorch(Ul, sl, G, True)
+        T[f"lrmm{i}.right"] = _low_rank_precond_mm_pytorch(Ur, sr, G, False)
+    for i, (nel, sc) in enumerate([(4096, 1e-3), (1000, 3.0), (257, 1e-20)]):
+        x = torch.randn(nel, generator=g) * sc
+        q, s = U.quantize_sym_int8(x)
+        T[f"quant{i}.x"], T[f"quant{i}.q"] = x, q
+        M[f"quant{i}.scale"] = s
+        T[f"quant{i}.deq"] = U.dequantize_sym_int8(q, s)
+        nv = torch.randn(nel, generator=g) * sc * 0.1
+        q2, s2 = _int8_ema_update_pytorch(q.clone(), s, nv, 0.99)
+        T[f"ema{i}.new"], T[f"ema{i}.q"] = nv, q2
+        M[f"ema{i}.scale"] = s2
+    x = torch.tensor([0.5, 1.5, 2.5, -0.5, -1.5, 126.5, -126.5, 127.0]) * (1.0 / 127.0)
+    q, s = U.quantize_sym_int8(x)
+    T["ties.x"], T["ties.q"] = x, q
+    M["ties.scale"] = s
+    eye = torch.eye(16) * 1e-4
+    q, s = U.quantize_sym_int8(eye)
+    T["eye.q"] = q
+    M["eye.scale"] = s
+    spectra = [torch.linspace(10, 0, 50), torch.logspace(0, -6, 64), torch.zeros(10),
+               torch.ones(32), torch.tensor([5.0, 1e-9, 1e-9, 0.0])]
+    for i, sp in enumerate(spectra):
+        T[f"rank{i}.s"] = sp
+        M[f"rank{i}.k"] = [U.adaptive_rank(sp, e, kmin, kmax)
+                           for e, kmin, kmax in [(0.05, 4, 128), (0.2, 1, 8), (0.0, 2, 1000)]]
+    # standalone preconditioner: precondition + natural norm after refreshes
+    for i, (shape, D, int8) in enumerate([((40, 24), 64, True), ((96, 20), 32, True),
+                                          ((18, 50), 32, False), ((30,), 64, True)]):
+        p = torch.zeros(shape)
+        pre = SparsePreconditioner(p, k_min=3, k_max=12, rho=0.9, max_precond_dim=D,
+                                   use_int8_ema=int8)
+        for r in range(3):
+            gr = torch.randn(shape, generator=g)
+            T[f"pre{i}.g{r}"] = gr
+            pre.update_curvature(gr)
+        gq = torch.randn(shape, generator=g)
+        T[f"pre{i}.gq"] = gq
+        T[f"pre{i}.out"] = pre.precondition(gq)
+        T[f"pre{i}.nat"] = pre.natural_grad_norm(gq, eps=1e-8).reshape(1)
+        M[f"pre{i}"] = {"shape": list(shape), "D": D, "int8": int8, "k": pre.k,
+                        "memory_bytes": pre.memory_bytes()}
+    save_file({k: v.contiguous() for k, v in T.items()}, os.path.join(HERE, "ops.safetensors"))
+    with open(os.path.join(HERE, "ops.json"), "w") as f:
+        json.dump(M, f, indent=1, sort_keys=True)
+    print(f"ops: {len(T)} tensors")
+
+
+def run_c1(scao, steps=100):
+    """one 768x3072 fp32 Linear weight."""
+    g0 = torch.Generator().manual_seed(0)
+    p = torch.nn.Parameter(torch.randn(768, 3072, generator=g0) * 0.02)
+    cfg = dict(lr=1e-3, use_int8_ema=True, k_min=32, k_max=32, max_precond_dim=1024,
+               warmup_steps=20, blend_steps=50, precond_freq=10, min_precond_updates=2,
+               **PARITY)
+    opt = scao.SCAO([p], **cfg)
+    rows = []
+    for t in range(1, steps + 1):
+        gg = torch.Generator().manual_seed(1000 + t)
+        p.grad = torch.randn(p.shape, generator=gg) * 0.02
+        opt.step()
+        st = opt.state[p]
+        pre = st["preconditioner"]
+        rec = {"t": t, "p_norm": float(p.detach().double().norm()),
+               "p_sum": float(p.detach().double().sum()),
+               "p_head": [float(v) for v in p.detach().flatten()[:16]],
+               "m_norm": float(st["exp_avg"].double().norm()),
+               "v_sum": float(st["exp_avg_sq"].double().sum()),
+               "precond_step": pre.precond_step, "k": pre.k, "blocks": []}
+        for b in pre._blocks:
+            rec["blocks"].append({
+                "L_scale": b.L_ema_scale, "R_scale": b.R_ema_scale, "k": b.k,
+                "L_sha": hashlib.sha256(b.L_ema_q.numpy().tobytes()).hexdigest()[:16],
+                "R_sha": hashlib.sha256(b.R_ema_q.numpy().tobytes()).hexdigest()[:16],
+                "L_code_sum": int(b.L_ema_q.to(torch.int64).sum()),
+                "S_l_head": [float(v) for v in b.S_l[:4]]})
+        rows.append(rec)
+    # full end state of block 0 for tolerance checks
+    b0 = pre._blocks[0]
+    save_file({"L_q": b0.L_ema_q[:32].clone(), "R_q": b0.R_ema_q[:32].clone(),
+               "p_final_rows": p.detach()[:2].clone()},
+              os.path.join(HERE, "c1_summary.safetensors"))
+    with open(os.path.join(HERE, "c1_summary.json"), "w") as f:
+        json.dump({"config": cfg, "rows": rows}, f, indent=0, sort_keys=True)
+    print("c1_summary done")
+
+
+def main():
+    sys.path.insert(0, REF)
+    warnings.simplefilter("ignore")
+    torch.set_num_threads(8)
+    import scao  # the reference package
+    base = dict(lr=1e-2, weight_decay=0.01, max_precond_dim=32, rho=0.99, **PARITY)
+    run_traj(scao, "traj_int8", dict(base, use_int8_ema=True, k_min=2, k_max=8,
+                                     warmup_steps=6, blend_steps=5, precond_freq=3,
+                                     min_precond_updates=2, tau=1.0, lars_coeff=1e-3),
+             steps=24, snap_steps=(6, 9, 24))
+    run_traj(scao, "traj_fp32", dict(base, use_int8_ema=False, k_min=4, k_max=4,
+                                     warmup_steps=4, blend_steps=4, precond_freq=2,
+                                     min_precond_updates=1, tau=None, lars_coeff=0.0),
+             steps=16, snap_steps=(16,))
+    run_traj(scao, "traj_misc", dict(base, use_int8_ema=True, k_min=3, k_max=6,
+                                     warmup_steps=3, blend_steps=0, precond_freq=2,
+                                     min_precond_updates=1, tau=0.05, lars_coeff=1e-3,
+                                     weight_decay=0.1, lookahead_k=3, lookahead_alpha=0.5),
+             steps=14, snap_steps=(14,))
+    run_traj(scao, "traj_bf16", dict(base, use_int8_ema=True, k_min=2, k_max=4,
+                                     warmup_steps=3, blend_steps=3, precond_freq=2,
+                                     min_precond_updates=1),
+             steps=10, snap_steps=(10,), dtype=torch.bfloat16)
+    run_traj(scao, "traj_sparse", dict(base, use_int8_ema=True, k_min=2, k_max=6,
+                                       warmup_steps=3, blend_steps=3, precond_freq=2,
+                                       min_precond_updates=1, sparsity=0.7),
+             steps=10, snap_steps=(10,), outliers=0.01)
+    run_ops(scao)
+    run_c1(scao)
+
+
+if __name__ == "__main__":
+    main()

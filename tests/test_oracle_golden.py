@@ -1,0 +1,175 @@
+"""Pin the CPU oracle (oracle/scao_ref.py) to the reference's own outputs.
+
+The fixtures under tests/golden/ were written by tests/golden/make_goldens.py
+from the reference package itself on seeded inputs.  These tests replay the
+same inputs through the oracle and require the same outputs.  On the torch
+build the fixtures were made with, the oracle reproduces them bit for bit;
+the tolerances below are far tighter than any algorithmic slip (a dropped
+term, a wrong sign, a swapped operand changes results at the 1e-2 level).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+
+import pytest
+import torch
+
+from oracle import scao_ref as R
+from scao_inputs import GOLDEN, config_from_meta, grads_for_step, load_golden
+
+RTOL, ATOL = 2e-6, 1e-9
+
+
+def _close(a, b, rtol=RTOL, atol=ATOL):
+    torch.testing.assert_close(a.float() if a.dtype == torch.bfloat16 else a,
+                               b.float() if b.dtype == torch.bfloat16 else b,
+                               rtol=rtol, atol=atol)
+
+
+def _replay(name):
+    T, meta = load_golden(name)
+    cfg = config_from_meta(meta)
+    names = meta["names"]
+    shapes = {k: tuple(meta["shapes"][k]) for k in names}
+    dtype = {"torch.float32": torch.float32, "torch.bfloat16": torch.bfloat16}[meta["dtype"]]
+    params = {k: torch.nn.Parameter(T[f"init.{k}"].clone()) for k in names}
+    opt = R.RefSCAO(list(params.values()), **cfg)
+    return T, meta, shapes, dtype, params, opt
+
+
+TRAJS = ["traj_int8", "traj_fp32", "traj_misc", "traj_bf16", "traj_sparse"]
+
+
+@pytest.mark.parametrize("name", TRAJS)
+def test_trajectory_matches_reference(name):
+    T, meta, shapes, dtype, params, opt = _replay(name)
+    snaps = set(meta["snap_steps"])
+    for t in range(1, meta["steps"] + 1):
+        gr = grads_for_step(t, shapes, dtype=dtype, outliers=meta.get("outliers", 0.0))
+        for k, p in params.items():
+            p.grad = gr[k].clone()
+        opt.step()
+        rec = meta["per_step"][t - 1]
+        assert opt._global_step == rec["global_step"]
+        assert opt._global_norm_ema == pytest.approx(rec["global_norm_ema"], rel=1e-12)
+        assert {str(i): k for i, k in opt.current_ranks().items()} == rec["ranks"]
+        for k, p in params.items():
+            st = opt.state[p]
+            exp = rec[k]
+            assert st["step"] == exp["step"] and st["scao_step"] == exp["scao_step"]
+            assert bool(st.get("scao_phase_started", False)) == exp["phase2"], (t, k)
+            assert st["preconditioner"].precond_step == exp["precond_step"]
+            _close(p.detach(), T[f"step{t}.p.{k}"])
+        if t in snaps:
+            sd = opt.state_dict()
+            for k, p in params.items():
+                for key in ("exp_avg", "exp_avg_sq", "exp_avg_diff", "prev_grad"):
+                    _close(opt.state[p][key], T[f"snap{t}.{k}.{key}"])
+            _check_precond_tree(sd["_scao_precond"], T, meta, f"snap{t}")
+            rt = meta[f"snap{t}.runtime"]
+            for key, val in sd["_scao_runtime"].items():
+                assert str(val) == str(rt[key]) or val == pytest.approx(rt[key], rel=1e-12)
+            assert {str(i): sorted(v.keys()) for i, v in sd["state"].items()} == \
+                meta[f"snap{t}.state_keys"]
+            assert sorted(k for k in sd["param_groups"][0] if k != "params") == \
+                meta[f"snap{t}.group_keys"]
+
+
+def _check_precond_tree(tree, T, meta, prefix):
+    for idx, d in tree.items():
+        _check_precond(d, T, meta, f"{prefix}.precond{idx}")
+
+
+def _check_precond(d, T, meta, name):
+    for key, val in d.items():
+        full = f"{name}.{key}"
+        if key == "blocks":
+            assert meta[full] == len(val)
+            for i, b in enumerate(val):
+                _check_precond(b, T, meta, f"{full}.{i}")
+        elif isinstance(val, torch.Tensor):
+            if val.dtype == torch.int8:
+                assert torch.equal(val, T[full]), full
+            elif key in ("U_l", "U_r"):
+                # eigenvector signs are LAPACK's choice; compare the projector
+                _close(val @ val.T, T[full] @ T[full].T, rtol=1e-4, atol=1e-6)
+            else:
+                _close(val, T[full])
+        elif isinstance(val, float):
+            assert val == pytest.approx(meta[full], rel=1e-12), full
+        else:
+            assert val == meta[full], full
+
+
+def test_ops_vectors():
+    from safetensors.torch import load_file
+    T = load_file(os.path.join(GOLDEN, "ops.safetensors"))
+    with open(os.path.join(GOLDEN, "ops.json")) as f:
+        M = json.load(f)
+    for i in range(3):
+        a = [T[f"fkp{i}.{x}"] for x in ("Ul", "sl", "Ur", "sr", "G")]
+        _close(R.fused_kronecker_precond(*a), T[f"fkp{i}.out"])
+        _close(R.low_rank_precond_mm(T[f"fkp{i}.Ul"], T[f"fkp{i}.sl"], T[f"fkp{i}.G"], True),
+               T[f"lrmm{i}.left"])
+        _close(R.low_rank_precond_mm(T[f"fkp{i}.Ur"], T[f"fkp{i}.sr"], T[f"fkp{i}.G"], False),
+               T[f"lrmm{i}.right"])
+    for i in range(3):
+        q, s = R.quantize_sym_int8(T[f"quant{i}.x"])
+        assert torch.equal(q, T[f"quant{i}.q"]) and s == M[f"quant{i}.scale"]
+        assert torch.equal(R.dequantize_sym_int8(q, s), T[f"quant{i}.deq"])
+        q2, s2 = R.int8_ema_update(q.clone(), s, T[f"ema{i}.new"], 0.99)
+        assert torch.equal(q2, T[f"ema{i}.q"]) and s2 == M[f"ema{i}.scale"]
+    q, s = R.quantize_sym_int8(T["ties.x"])
+    assert torch.equal(q, T["ties.q"]) and s == M["ties.scale"]
+    q, s = R.quantize_sym_int8(torch.eye(16) * 1e-4)
+    assert torch.equal(q, T["eye.q"]) and s == M["eye.scale"]
+    for i in range(5):
+        got = [R.adaptive_rank(T[f"rank{i}.s"], e, kmin, kmax)
+               for e, kmin, kmax in [(0.05, 4, 128), (0.2, 1, 8), (0.0, 2, 1000)]]
+        assert got == M[f"rank{i}.k"]
+    g = torch.Generator().manual_seed(7)
+    for i, (shape, D, int8) in enumerate([((40, 24), 64, True), ((96, 20), 32, True),
+                                          ((18, 50), 32, False), ((30,), 64, True)]):
+        pre = R.RefPreconditioner(torch.zeros(shape), k_min=3, k_max=12, rho=0.9,
+                                  max_precond_dim=D, use_int8_ema=int8)
+        for r in range(3):
+            pre.update_curvature(T[f"pre{i}.g{r}"])
+        gq = T[f"pre{i}.gq"]
+        _close(pre.precondition(gq), T[f"pre{i}.out"], rtol=1e-5, atol=1e-7)
+        _close(pre.natural_grad_norm(gq, eps=1e-8).reshape(1), T[f"pre{i}.nat"], rtol=1e-5)
+        assert pre.k == M[f"pre{i}"]["k"]
+        assert pre.memory_bytes() == M[f"pre{i}"]["memory_bytes"]
+
+
+def test_c1_summary():
+    """BASELINE config 1 (768x3072, 100 steps) against the reference's run."""
+    from safetensors.torch import load_file
+    with open(os.path.join(GOLDEN, "c1_summary.json")) as f:
+        ref = json.load(f)
+    cfg = dict(ref["config"])
+    g0 = torch.Generator().manual_seed(0)
+    p = torch.nn.Parameter(torch.randn(768, 3072, generator=g0) * 0.02)
+    opt = R.RefSCAO([p], **cfg)
+    for row in ref["rows"]:
+        t = row["t"]
+        gg = torch.Generator().manual_seed(1000 + t)
+        p.grad = torch.randn(p.shape, generator=gg) * 0.02
+        opt.step()
+        pre = opt.state[p]["preconditioner"]
+        assert pre.precond_step == row["precond_step"] and pre.k == row["k"]
+        assert float(p.detach().double().norm()) == pytest.approx(row["p_norm"], rel=1e-6)
+        head = p.detach().flatten()[:16]
+        torch.testing.assert_close(head, torch.tensor(row["p_head"]), rtol=1e-5, atol=1e-8)
+        for b, rb in zip(pre._blocks, row["blocks"]):
+            assert b.L_ema_scale == pytest.approx(rb["L_scale"], rel=1e-6)
+            assert b.R_ema_scale == pytest.approx(rb["R_scale"], rel=1e-6)
+            assert b.k == rb["k"]
+            # code sums move by at most a handful of 1-LSB flips off this build
+            assert abs(int(b.L_ema_q.to(torch.int64).sum()) - rb["L_code_sum"]) <= 64
+    T = load_file(os.path.join(GOLDEN, "c1_summary.safetensors"))
+    b0 = opt.state[p]["preconditioner"]._blocks[0]
+    assert (b0.L_ema_q[:32].int() - T["L_q"].int()).abs().max() <= 1
+    assert (b0.R_ema_q[:32].int() - T["R_q"].int()).abs().max() <= 1
