@@ -1,0 +1,272 @@
+"""SCAO.step on one MI355X at the Llama-3.2-1B shape.
+
+Workload: the 16-layer Llama-3.2-1B parameter set (q/o 2048x2048, k/v
+512x2048, gate/up 8192x2048, down 2048x8192 preconditioned: 224 blocks of
+2048x2048 + 32 of 512x2048) plus the 128256x2048 embedding and the norm
+vectors in an Adam group (warmup_steps=1e9), fp32 master params, synthetic
+N(0, 0.02^2) params and N(0, 1e-3^2) grads generated on the device.  Profile:
+int8 EMA, k_min=k_max=64, max_precond_dim=2048, sparsity=0, no noise, no
+lookahead, synchronous refresh, reference defaults otherwise (tau=1,
+lars_coeff=1e-3, betas (0.9, 0.999), beta3=0.99, wd=0.01, rho=0.999).
+
+A "step" is one optimizer.step() over all 1235.81M parameters.  The timed
+region is K consecutive steady Phase-2 steps with no curvature refresh (the
+reference refreshes only when step % precond_freq == 0); two gradient sets
+rotate so consecutive steps see different gradients.  The Phase-1 (Adam)
+step and the refresh (Gram/EMA/requantise on the GPU, eigh + rank in
+PyTorch-ROCm) are timed separately and reported in "details".
+
+Prints one JSON line.  --gpus N>1 exits: this build runs on one GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK = 8.0e12          # B/s, MI355X HBM3E
+FP32_MFMA_PEAK = 157.3e12  # flop/s, MI355X dense fp32 MFMA
+
+CONFIGS = {
+    # name: (layers, [(name, shape)] per layer precond, per-layer adam vectors, extra adam, k, D)
+    "gpt2s": dict(layers=12, mats=[("attn.c_attn", (768, 2304)), ("attn.c_proj", (768, 768)),
+                                   ("mlp.c_fc", (768, 3072)), ("mlp.c_proj", (3072, 768))],
+                  vecs=[("ln_1.w", 768), ("ln_1.b", 768), ("ln_2.w", 768), ("ln_2.b", 768)],
+                  extra=[], k=64, D=1024),
+    "llama1b": dict(layers=16, mats=[("q", (2048, 2048)), ("k", (512, 2048)), ("v", (512, 2048)),
+                                     ("o", (2048, 2048)), ("gate", (8192, 2048)),
+                                     ("up", (8192, 2048)), ("down", (2048, 8192))],
+                    vecs=[("in_norm", 2048), ("post_norm", 2048)],
+                    extra=[("embed", (128256, 2048)), ("final_norm", (2048,))], k=64, D=2048),
+    "qwen3b": dict(layers=36, mats=[("q", (2048, 2048)), ("k", (256, 2048)), ("v", (256, 2048)),
+                                    ("o", (2048, 2048)), ("gate", (11008, 2048)),
+                                    ("up", (11008, 2048)), ("down", (2048, 11008))],
+                   vecs=[("in_norm", 2048), ("post_norm", 2048)], extra=[("final_norm", (2048,))],
+                   k=128, D=2048),
+    "llama8b": dict(layers=32, mats=[("q", (4096, 4096)), ("k", (1024, 4096)),
+                                     ("v", (1024, 4096)), ("o", (4096, 4096)),
+                                     ("gate", (14336, 4096)), ("up", (14336, 4096)),
+                                     ("down", (4096, 14336))],
+                    vecs=[("in_norm", 4096), ("post_norm", 4096)], extra=[], k=256, D=4096),
+}
+
+PROFILE = dict(use_int8_ema=True, sparsity=0.0, noise_std_init=0.0, async_precond=False,
+               lookahead_k=0)
+
+
+def shapes_of(cfg):
+    pre, adam = [], []
+    for layer in range(cfg["layers"]):
+        pre += [(f"l{layer}.{n}", s) for n, s in cfg["mats"]]
+        adam += [(f"l{layer}.{n}", (d,)) for n, d in cfg["vecs"]]
+    adam += [(n, tuple(s)) for n, s in cfg["extra"]]
+    return pre, adam
+
+
+def proj_flops(m, n, k):
+    return 4 * m * n * k + 2 * (m + n) * k * k
+
+
+def leaves_of(shape, D):
+    m, n = shape
+    if max(m, n) <= D:
+        return [(m, n)]
+    big, small = (m, n) if m >= n else (n, m)
+    sizes = [D] * (big // D) + ([big % D] if big % D else [])
+    out = []
+    for b in sizes:
+        out += leaves_of((b, small) if m >= n else (small, b), D)
+    return out
+
+
+def cpu_baseline(cfg, args):
+    """The oracle (torch on the host CPU) on a bounded sample: one layer's
+    preconditioned matrices, steady Phase-2 steps (eye-initialised factors,
+    no refresh -- the same kernels' worth of work per step)."""
+    import torch
+    from oracle import scao_ref as R
+    cores = min(len(os.sched_getaffinity(0)), args.cpu_threads)
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    params = [torch.nn.Parameter(torch.randn(s, generator=g) * 0.02) for _, s in cfg["mats"]]
+    nparam = sum(p.numel() for p in params)
+    opt = R.RefSCAO(params, k_min=cfg["k"], k_max=cfg["k"], max_precond_dim=cfg["D"],
+                    warmup_steps=0, min_precond_updates=0, precond_freq=10 ** 9, **PROFILE)
+    grads = [torch.randn(p.shape, generator=g) * 1e-3 for p in params]
+    for p, gr in zip(params, grads):
+        p.grad = gr
+    opt.step()                                   # state allocation, first step
+    t0 = time.perf_counter()
+    n = 0
+    while n < args.cpu_steps or (time.perf_counter() - t0 < 5.0 and n < 10):
+        opt.step()
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    return {"value": nparam / dt, "unit": "params/s", "cores": cores, "kind": "port",
+            "sample": f"oracle (torch {torch.__version__} CPU fp32) steady Phase-2 step on one "
+                      f"layer's {len(params)} preconditioned matrices ({nparam / 1e6:.2f}M "
+                      f"params), {n} steps, {dt * 1e3:.0f} ms/step, "
+                      f"cpu={platform.processor() or platform.machine()}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", default="llama1b", choices=list(CONFIGS))
+    ap.add_argument("--cpu-baseline", type=int, default=1)
+    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--details", default=None, help="write the full report JSON here")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build runs the SCAO step on one GPU; --gpus {args.gpus} "
+              f"(WORLD_SIZE={world}) is not supported", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import scao_amd
+    from scao_amd import engine, _lib
+
+    _lib.lib()
+    dev = torch.device("cuda:0")
+    cfg = CONFIGS[args.config]
+    pre_shapes, adam_shapes = shapes_of(cfg)
+    gen = torch.Generator(device=dev).manual_seed(0)
+
+    def make(shape, scale):
+        return torch.randn(shape, generator=gen, device=dev) * scale
+
+    pre_p = [torch.nn.Parameter(make(s, 0.02)) for _, s in pre_shapes]
+    adam_p = [torch.nn.Parameter(make(s, 0.02)) for _, s in adam_shapes]
+    allp = pre_p + adam_p
+    nparams = sum(p.numel() for p in allp)
+    n_pre = sum(p.numel() for p in pre_p)
+    grad_sets = [[make(p.shape, 1e-3) for p in allp] for _ in range(2)]
+
+    def set_grads(i):
+        for p, gr in zip(allp, grad_sets[i % 2]):
+            p.grad = gr
+
+    opt = scao_amd.SCAO([{"params": pre_p}, {"params": adam_p, "warmup_steps": 10 ** 9}],
+                        k_min=cfg["k"], k_max=cfg["k"], max_precond_dim=cfg["D"],
+                        warmup_steps=3, precond_freq=3, min_precond_updates=1, **PROFILE)
+    torch.cuda.synchronize()
+
+    def timed(fn):
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3
+
+    step = [0]
+
+    def one():
+        set_grads(step[0])
+        opt.step()
+        step[0] += 1
+
+    t_first = timed(one)                      # step 1: state allocation + Phase 1
+    t_phase1 = timed(one)                     # step 2: Phase 1 (Adam) everywhere
+    engine.TIMING = {}
+    t_refresh = timed(one)                    # step 3: Phase 1 + curvature refresh
+    refresh_parts = engine.timing_summary()
+    engine.TIMING = None
+    for g in opt.param_groups:
+        g["precond_freq"] = 10 ** 9           # steady state: no refresh in the timed region
+    for _ in range(args.warmup):
+        one()
+    torch.cuda.synchronize()
+    engine.TIMING = {}
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        one()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_kernel = engine.timing_summary()
+    engine.TIMING = None
+    ms = wall * 1e3 / args.steps
+    assert all(opt.state[p].get("scao_phase_started") for p in pre_p), "not in Phase 2"
+
+    # ---- roofline of the dominant kernel --------------------------------
+    dom = max(per_kernel, key=lambda k: per_kernel[k][2])
+    n_leaf = [lf for s in (s for _, s in pre_shapes) for lf in leaves_of(s, cfg["D"])]
+    k = cfg["k"]
+    flops_proj = sum(2 * m * n * k for m, n in n_leaf)          # T = U_l^T G per step
+    alg = {
+        # bytes that the algorithm itself must move through this kernel per launch
+        "scao_kron_apply": ("hbm", 36.0 * n_pre),   # read g,m,v,d,prev; write m,v,d,prev
+        "scao_lars_write": ("hbm", 8.0 * n_pre),    # read p, write p (the 44 B/elem rest)
+        "scao_adam_step": ("hbm", 32.0 * (nparams - n_pre)),
+        "scao_kron_project": ("mfma", float(flops_proj)),
+    }
+    bound, work = alg.get(dom, ("hbm", 0.0))
+    avg_s = per_kernel[dom][1] / 1e3
+    achieved = work / avg_s if avg_s > 0 else 0.0
+    peak = HBM_PEAK if bound == "hbm" else FP32_MFMA_PEAK
+    roof = {"kernel": dom, "bound": bound,
+            "achieved": achieved / (1e9 if bound == "hbm" else 1e12),
+            "peak": peak / (1e9 if bound == "hbm" else 1e12),
+            "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
+            "frac": achieved / peak, "traffic": None,
+            "avg_ms": per_kernel[dom][1]}
+    step_bytes = 44.0 * n_pre + 32.0 * (nparams - n_pre)
+    step_flops = sum(proj_flops(m, n, k) for m, n in n_leaf)
+
+    details = {
+        "per_kernel_ms": {k: {"count": c, "mean": m_, "total_per_step": t / args.steps}
+                          for k, (c, m_, t) in per_kernel.items()},
+        "steady_step_ms": ms,
+        "phase1_step_ms": t_phase1,
+        "refresh_step_ms": t_refresh,
+        "refresh_parts_ms": {k: {"count": c, "mean": m_, "total": t}
+                             for k, (c, m_, t) in refresh_parts.items()},
+        "first_step_ms": t_first,
+        "step_roofline": {"alg_bytes": step_bytes, "alg_flops": step_flops,
+                          "hbm_frac": step_bytes / (ms / 1e3) / HBM_PEAK,
+                          "hbm_floor_ms": step_bytes / HBM_PEAK * 1e3,
+                          "mfma_floor_ms": step_flops / FP32_MFMA_PEAK * 1e3},
+        "params": nparams, "precond_params": n_pre, "blocks": len(n_leaf),
+        "device": torch.cuda.get_device_name(0),
+    }
+    cpu = cpu_baseline(cfg, args) if args.cpu_baseline else None
+    out = {
+        "metric": "SCAO.step ms + params/sec at Llama-1B shape; % of MFMA / HBM roofline",
+        "value": nparams / (ms / 1e3),
+        "unit": "params/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": f"{args.config}: SCAO steady Phase-2 step (no refresh), "
+                               f"{nparams / 1e6:.2f}M fp32 params, {len(n_leaf)} Kronecker "
+                               f"blocks, int8 EMA, k={k}, max_precond_dim={cfg['D']}",
+                   "global_batch": None, "seq_len": None, "parallelism": "single-gpu"},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "details": {"phase1_step_ms": t_phase1, "refresh_step_ms": t_refresh,
+                    "step_hbm_frac": details["step_roofline"]["hbm_frac"]},
+    }
+    if args.details:
+        with open(args.details, "w") as f:
+            json.dump({"summary": out, "details": details}, f, indent=1)
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

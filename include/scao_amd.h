@@ -1,0 +1,232 @@
+/*
+ * scao_amd.h -- C ABI of the MI355X (gfx950) SCAO optimizer-step library.
+ *
+ * Plain C: device pointers, sizes and a hipStream_t passed as void*.  No
+ * torch types cross this boundary.  Every entry point launches on the stream
+ * it is given, allocates nothing, never synchronises the host, and returns
+ * SCAO_OK or an error code; scao_last_error() gives the message of the last
+ * failure on the calling thread.  Callers own every buffer (inputs, outputs,
+ * scratch).  All floating-point state is float32 unless noted.
+ *
+ * Reference interfaces replaced (whispering3/scao):
+ *   scao_fused_kronecker_precond  <- scao.cuda.fused_kronecker_precond
+ *                                    (scao/cuda/__init__.py:149-187; fallback :78-99;
+ *                                     pybind scao/cuda/low_rank_ops.cu:388-398)
+ *   scao_int8_ema_update          <- scao.cuda.int8_ema_update
+ *                                    (scao/cuda/__init__.py:231-266; fallback :122-142)
+ *   scao_kron_project/delta/lift/apply, scao_step_finalize, scao_lars_write,
+ *   scao_adam_step, scao_diag_reduce/apply
+ *                                 <- the per-parameter Python loop of
+ *                                    SCAO._step_group (scao/optimizer.py:509-645)
+ *                                    with SparsePreconditioner.precondition and
+ *                                    natural_grad_norm (scao/preconditioner.py:457-564)
+ *                                    and SCAO._lars_scale/_curvature_clip
+ *                                    (scao/optimizer.py:371-377, 667-678), batched
+ *                                    over every parameter and Kronecker block
+ *   scao_gram_ema / scao_requant / scao_eig_prep / scao_diag_ema
+ *                                 <- SparsePreconditioner.update_curvature
+ *                                    (scao/preconditioner.py:297-361, int8 core :342-350)
+ *                                    and the dequantise/debias/Tikhonov part of
+ *                                    _update_eigenfactors (:381-406)
+ */
+#ifndef SCAO_AMD_H
+#define SCAO_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SCAO_ABI_VERSION 1
+
+enum scao_status { SCAO_OK = 0, SCAO_ERR_INVALID = 1, SCAO_ERR_HIP = 2 };
+enum scao_dtype { SCAO_F32 = 0, SCAO_BF16 = 1, SCAO_F16 = 2 };
+
+/* scao_param_desc.flags */
+#define SCAO_PF_DECAY 1  /* multiply the parameter by `decay` (weight_decay != 0)   */
+#define SCAO_PF_LARS  2  /* LARS trust ratio (lars_coeff > 0): stage the update     */
+#define SCAO_PF_CLIP  4  /* curvature clip against `tau` (tau is not None)          */
+#define SCAO_PF_GSNR  8  /* gSNR mask on the update                                 */
+#define SCAO_PF_DIAG  16 /* diagonal-mode preconditioner (1-D or degenerate 2-D)    */
+#define SCAO_PF_NORM  32 /* accumulate ||g||^2 for the global grad-norm EMA         */
+#define SCAO_PF_GF32  64 /* `g` is a float32 buffer (filtered/noised gradient)     */
+
+/* One parameter of a batched step.  Scalars arrive already rounded the way
+ * the reference rounds a Python float meeting a float32 tensor. */
+typedef struct scao_param_desc {
+  void* p;                  /* parameter storage (dtype), contiguous             */
+  const void* g;            /* gradient for the moments (dtype, or fp32 with      */
+                            /* SCAO_PF_GF32), contiguous                         */
+  const void* graw;         /* raw p.grad (dtype): preconditioner, norms         */
+  float* exp_avg;           /* numel                                             */
+  float* exp_avg_sq;
+  float* exp_avg_diff;
+  float* prev_grad;
+  float* upd;               /* LARS staging of the update (numel) or NULL        */
+  const float* diag_ema;    /* diagonal-mode curvature (numel) or NULL           */
+  int64_t numel;
+  int64_t cols;             /* row stride of the 2-D view                        */
+  double lr;
+  float decay;              /* fp32(1 - lr*weight_decay)                         */
+  float beta1, omb1;        /* fp32(beta1), fp32(1 - beta1)                      */
+  float beta2, omb2;
+  float beta3, omb3;
+  float bc1, bc2, bc3;      /* fp32(1 - beta_i ** step)                          */
+  float blend, omblend;     /* fp32(b), fp32(1 - b)                              */
+  float eps, tau, lars, wd, gsnr;
+  float diag_bias;          /* fp32(diagonal EMA bias factor)                    */
+  float adam_sqrt_bc2;      /* fp32(sqrt(1 - beta2 ** step))                     */
+  float adam_alpha;         /* fp32(-(lr / (1 - beta1 ** step)))                 */
+  int32_t dtype;            /* enum scao_dtype                                   */
+  int32_t flags;            /* SCAO_PF_*                                         */
+  int32_t pre_begin, pre_end;   /* reduction slots written before finalize 0     */
+  int32_t post_begin, post_end; /* reduction slots written before finalize 1     */
+  int32_t norm_index;       /* position in the global grad-norm average, or -1   */
+  int32_t pad0;
+} scao_param_desc;
+
+/* One Kronecker block (a whole 2-D parameter or one block-diagonal piece). */
+typedef struct scao_leaf_desc {
+  const float* Ul;          /* m x k row-major (left eigenvectors)               */
+  const float* Ur;          /* n x k row-major                                   */
+  const float* Sl;          /* k: eigenvalues, or s^-1/4 with SCAO_LF_SINV4      */
+  const float* Sr;
+  float* T;                 /* scratch k x n  : U_l^T G                          */
+  float* Delta;             /* scratch k x k  : (s_l s_r^T - 1) * (U_l^T G U_r)  */
+  float* W;                 /* scratch m x k  : U_l Delta                        */
+  int64_t off;              /* element offset of the block origin in the param   */
+  int64_t ld;               /* row stride of the parameter's 2-D view            */
+  int32_t param;            /* index into the scao_param_desc table              */
+  int32_t m, n, k;
+  int32_t flags;            /* SCAO_LF_*                                         */
+  int32_t pad0;
+} scao_leaf_desc;
+
+#define SCAO_LF_SINV4 1     /* Sl/Sr already hold clamp(S,1e-8)^-1/4             */
+#define SCAO_LF_VEC4  2     /* off, ld, n multiples of 4 and 16-byte aligned     */
+
+/* A unit of work: (leaf or param, two tile coordinates, reduction slot). */
+typedef struct scao_task {
+  int32_t idx;              /* leaf index (tile kernels) or param index (flat)   */
+  int32_t a, b;             /* tile origin (rows/cols) or chunk number           */
+  int32_t slot;             /* reduction slot, or -1                             */
+} scao_task;
+
+/* Per-parameter results of the step's reductions (written by the library). */
+typedef struct scao_param_stat {
+  double g2, p2, nu2, u2;   /* ||g||^2, ||p_decayed||^2, natural-norm^2, ||u||^2 */
+  float gnorm, pnorm, nu, clip;
+  float unorm, trust, alpha, pad0;
+} scao_param_stat;
+
+/* Number of doubles per reduction slot: [||g||^2, ||p||^2, nu^2 or ||u||^2]. */
+#define SCAO_SLOT_WIDTH 3
+/* Elements per flat task (chunk of one parameter). */
+#define SCAO_FLAT_CHUNK 4096
+/* Tile sizes of the Kronecker kernels. */
+#define SCAO_PROJ_COLS 256   /* columns of G per projection task (c-chunk of 64) */
+#define SCAO_APPLY_TILE 64   /* rows x cols per apply task                        */
+#define SCAO_GRAM_TILE 128   /* Gram output tile                                  */
+
+/* ---- library --------------------------------------------------------- */
+int scao_abi_version(void);
+const char* scao_last_error(void);
+/* sizeof and field offsets of the descriptor structs, for binding checks:
+ * which = 0 param_desc, 1 leaf_desc, 2 task, 3 param_stat; out[0]=sizeof,
+ * out[1..] = offsets in declaration order.  Returns the number written. */
+int scao_struct_layout(int which, int64_t* out, int cap);
+
+/* ---- reference operator surface ------------------------------------- */
+/* out = G + U_l ((s_l s_r^T - 1) * (U_l^T G U_r)) U_r^T   (m x n, k <= 256).
+ * G has row stride ldG; out is dense m x n.  workspace: k*n + k*k + m*k
+ * floats + 4 leaf/task descriptors worth of bytes given by
+ * scao_fused_kronecker_workspace(). */
+int64_t scao_fused_kronecker_workspace(int64_t m, int64_t n, int64_t k);
+int scao_fused_kronecker_precond(const float* U_l, const float* s_l_inv4, const float* U_r,
+                                 const float* s_r_inv4, const float* G, int64_t ldG, float* out,
+                                 int64_t m, int64_t n, int64_t k, void* workspace,
+                                 void* stream);
+/* x = fp32(q)*fp32(scale) * fp32(rho) + new_val; scale' = max|x|/127 (double)
+ * or 1.0; q' = clamp(rint(x * fp32(1/scale')), +-127).  Updates q in place,
+ * writes scale' to *scale_out (device double).  scratch: n floats +
+ * scao_reduce_scratch_bytes(n). */
+int64_t scao_int8_ema_scratch_bytes(int64_t n);
+int scao_int8_ema_update(int8_t* q, double scale_in, const float* new_val, double rho,
+                         int64_t n, double* scale_out, void* scratch, void* stream);
+
+/* ---- batched step: Phase 2 (preconditioned Adan) ---------------------- */
+/* A1  T = U_l^T G for (leaf, 256-column strip, 64-row chunk of T); also
+ *     ||g||^2 and ||p*decay||^2 partials into slots (chunk 0 only). */
+int scao_kron_project(const scao_task* tasks, int ntasks, const scao_leaf_desc* leaves,
+                      const scao_param_desc* params, double* slots, void* stream);
+/* A2  P = T U_r, Delta = (s_l s_r^T - 1) P and nu^2 partial per 64x64 tile of P. */
+int scao_kron_delta(const scao_task* tasks, int ntasks, const scao_leaf_desc* leaves,
+                    const scao_param_desc* params, double* slots, void* stream);
+/* A3  W = U_l Delta per 64-row strip. */
+int scao_kron_lift(const scao_task* tasks, int ntasks, const scao_leaf_desc* leaves,
+                   void* stream);
+/* Diagonal-mode params: ||g||^2, ||p*decay||^2 and sum g^2/(sqrt(diag)+eps). */
+int scao_diag_reduce(const scao_task* tasks, int ntasks, const scao_param_desc* params,
+                     double* slots, void* stream);
+/* phase 0: per param ||g||, ||p||, nu, clip; global grad-norm EMA in runtime[0]
+ *          (runtime[1] receives the average) when update_norm_ema != 0.
+ * phase 1: per param ||u||, LARS trust and the fp32 step multiplier. */
+int scao_step_finalize(const scao_param_desc* params, int nparams, const double* slots,
+                       scao_param_stat* stat, double* runtime, int phase,
+                       int update_norm_ema, int norm_count, void* stream);
+/* B   G + W U_r^T -> clip -> blend -> Adan moments -> update; writes the
+ *     update to upd (LARS params, ||u||^2 into slots) or the parameter. */
+int scao_kron_apply(const scao_task* tasks, int ntasks, const scao_leaf_desc* leaves,
+                    const scao_param_desc* params, const scao_param_stat* stat,
+                    double* slots, void* stream);
+int scao_diag_apply(const scao_task* tasks, int ntasks, const scao_param_desc* params,
+                    const scao_param_stat* stat, double* slots, void* stream);
+/* C   p = fma(upd, alpha, p*decay) for LARS params. */
+int scao_lars_write(const scao_task* tasks, int ntasks, const scao_param_desc* params,
+                    const scao_param_stat* stat, void* stream);
+
+/* ---- batched step: Phase 1 (Adam(W)) --------------------------------- */
+int scao_adam_step(const scao_task* tasks, int ntasks, const scao_param_desc* params,
+                   double* slots, void* stream);
+
+/* ---- curvature refresh ------------------------------------------------ */
+typedef struct scao_gram_desc {
+  const void* g;            /* gradient storage of the param (dtype)             */
+  int64_t off, ld;          /* block origin and row stride                       */
+  int8_t* q;                /* int8 EMA codes (dim x dim), or NULL for fp32 EMA  */
+  const double* scale;      /* current dequantisation scale (device double)      */
+  float* ema;               /* fp32 EMA: updated in place; int8: dim x dim scratch */
+  float* amax;              /* per-tile |EMA| maxima (int8 mode)                 */
+  int32_t rows, cols;       /* block shape m x n                                 */
+  int32_t side;             /* 0: L = G G^T (dim m), 1: R = G^T G (dim n)        */
+  int32_t dtype;
+  int32_t ntiles;           /* tiles per side (for amax)                         */
+  int32_t pad0;
+  float rho, alpha;         /* fp32(rho), fp32(1 - rho)                          */
+} scao_gram_desc;
+int scao_gram_ema(const scao_task* tasks, int ntasks, const scao_gram_desc* descs,
+                  void* stream);
+/* requantise every int8 factor of a gram_ema launch; writes the new scale to
+ * scale_out[i] (device doubles, may alias the scale inputs). */
+int scao_requant(const scao_task* tasks, int ntasks, const scao_gram_desc* descs,
+                 double* const* scale_out, void* stream);
+/* eigh input: X = (deq or ema) / fp32(bias); X_ii += fp32(max(1e-8, 1e-4*tr(X)/dim)). */
+typedef struct scao_prep_desc {
+  const int8_t* q;          /* codes or NULL                                     */
+  const double* scale;      /* device scale (int8)                               */
+  const float* ema;         /* fp32 EMA (when q is NULL)                         */
+  float* out;               /* dim x dim                                         */
+  int32_t dim;
+  float bias;               /* fp32(max(bias_factor, 1e-8))                      */
+} scao_prep_desc;
+int scao_eig_prep(const scao_task* tasks, int ntasks, const scao_prep_desc* descs,
+                  void* stream);
+/* diag_ema = fp32(diag*rho) + fp32(alpha * g*g)  (1-D preconditioners). */
+int scao_diag_ema(const scao_task* tasks, int ntasks, const scao_param_desc* params,
+                  const float* rho_alpha, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SCAO_AMD_H */

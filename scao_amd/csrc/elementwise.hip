@@ -1,0 +1,356 @@
+// Bandwidth-bound kernels of the SCAO step on gfx950: every parameter of a
+// launch is cut into SCAO_FLAT_CHUNK-element chunks, one 256-thread block per
+// chunk, float4 accesses (4 x 1024 contiguous elements per block).
+//
+//   adam_step     Phase 1 (scao/optimizer.py:567-578): decay, Adam moments,
+//                 bias-corrected step, prev_grad copy, ||g||^2   -- 32 B/elem
+//   diag_reduce   Phase 2 diagonal preconditioner reductions
+//                 (scao/preconditioner.py:554-556, optimizer.py:534, 371-377)
+//   diag_apply    Phase 2 diagonal precondition (preconditioner.py:506-510)
+//                 + the shared Adan tail
+//   lars_write    p = fma(u, -(lr*trust), p*decay) (optimizer.py:642-645)
+//   diag_ema      1-D curvature EMA (preconditioner.py:332-339)
+//   step_finalize per-parameter norms, clip factor, LARS trust, and the
+//                 global grad-norm EMA (optimizer.py:439-446, 667-678, 371-377)
+#include "scao_common.hpp"
+
+using namespace scao;
+
+namespace {
+
+__device__ __forceinline__ bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+__device__ __forceinline__ bool al_dt(const void* p, int dt) {
+  return dt == SCAO_F32 ? al16(p) : (((uintptr_t)p & 7u) == 0);
+}
+
+// element range of a flat task and this thread's 4 groups of 4 elements
+struct Chunk {
+  int64_t base, end;
+  __device__ Chunk(const scao_task& tk, int64_t numel) {
+    base = (int64_t)tk.a * SCAO_FLAT_CHUNK;
+    end = base + SCAO_FLAT_CHUNK < numel ? base + SCAO_FLAT_CHUNK : numel;
+  }
+  __device__ int64_t elem(int grp) const { return base + grp * 1024 + threadIdx.x * 4; }
+  __device__ int mask(int64_t e) const {
+    int mk = 0;
+    for (int t = 0; t < 4; ++t) mk |= (e + t < end) ? (1 << t) : 0;
+    return mk;
+  }
+};
+
+__device__ __forceinline__ void write_slot(double* slots, int slot, double a, double b, double c) {
+  if (slot < 0) return;
+  slots[(int64_t)slot * SCAO_SLOT_WIDTH + 0] = a;
+  slots[(int64_t)slot * SCAO_SLOT_WIDTH + 1] = b;
+  slots[(int64_t)slot * SCAO_SLOT_WIDTH + 2] = c;
+}
+
+// --------------------------------------------------------------- adam ---
+__global__ __launch_bounds__(256) void k_adam(const scao_task* __restrict__ tasks,
+                                              const scao_param_desc* __restrict__ params,
+                                              double* slots) {
+  __shared__ double red[16];
+  const scao_task tk = tasks[blockIdx.x];
+  const scao_param_desc& P = params[tk.idx];
+  const int dt = P.dtype;
+  const Chunk ch(tk, P.numel);
+  const bool gf32 = P.flags & SCAO_PF_GF32;
+  const bool aligned = al_dt(P.p, dt) && al16(P.g) && al_dt(P.graw, dt) && al16(P.exp_avg) &&
+                       al16(P.exp_avg_sq) && al16(P.prev_grad);
+  const bool decay = P.flags & SCAO_PF_DECAY;
+  double g2 = 0.0;
+#pragma unroll
+  for (int grp = 0; grp < 4; ++grp) {
+    const int64_t e = ch.elem(grp);
+    const int mk = ch.mask(e);
+    if (!mk) continue;
+    const bool vec = aligned && mk == 15;
+    const v4f g = ld_mgrad(P, e, vec, mk);
+    const v4f gr = gf32 ? ld4(P.graw, dt, e, vec, mk) : g;
+    v4f p = ld4(P.p, dt, e, vec, mk);
+    v4f m = ldf4(P.exp_avg, e, vec, mk);
+    v4f v = ldf4(P.exp_avg_sq, e, vec, mk);
+    float part = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      part = fmaf(gr[t], gr[t], part);
+      const float pd = decay ? round_to(dt, p[t] * P.decay) : p[t];
+      m[t] = fmaf(g[t], P.omb1, m[t] * P.beta1);
+      v[t] = fmaf(P.omb2 * g[t], g[t], v[t] * P.beta2);
+      const float den = sqrtf(v[t]) / P.adam_sqrt_bc2 + P.eps;
+      const float u = round_to(dt, m[t] / den);
+      p[t] = round_to(dt, fmaf(u, P.adam_alpha, pd));
+    }
+    g2 += (double)part;
+    stf4(P.exp_avg, e, m, vec, mk);
+    stf4(P.exp_avg_sq, e, v, vec, mk);
+    stf4(P.prev_grad, e, g, vec, mk);
+    st4(P.p, dt, e, p, vec, mk);
+  }
+  double x[1] = {g2};
+  block_sum<1>(x, red);
+  if (threadIdx.x == 0) write_slot(slots, tk.slot, x[0], 0.0, 0.0);
+}
+
+// ------------------------------------------------------- diag reduce ---
+__global__ __launch_bounds__(256) void k_diag_reduce(const scao_task* __restrict__ tasks,
+                                                     const scao_param_desc* __restrict__ params,
+                                                     double* slots) {
+  __shared__ double red[16];
+  const scao_task tk = tasks[blockIdx.x];
+  const scao_param_desc& P = params[tk.idx];
+  const int dt = P.dtype;
+  const Chunk ch(tk, P.numel);
+  const bool aligned = al_dt(P.p, dt) && al_dt(P.graw, dt) && al16(P.diag_ema);
+  const bool decay = P.flags & SCAO_PF_DECAY;
+  const bool lars = P.flags & SCAO_PF_LARS;
+  double acc[3] = {0.0, 0.0, 0.0};
+#pragma unroll
+  for (int grp = 0; grp < 4; ++grp) {
+    const int64_t e = ch.elem(grp);
+    const int mk = ch.mask(e);
+    if (!mk) continue;
+    const bool vec = aligned && mk == 15;
+    const v4f g = ld4(P.graw, dt, e, vec, mk);
+    const v4f dg = ldf4(P.diag_ema, e, vec, mk);
+    v4f p = {0.f, 0.f, 0.f, 0.f};
+    if (lars) p = ld4(P.p, dt, e, vec, mk);
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      if (!(mk & (1 << t))) continue;
+      a0 = fmaf(g[t], g[t], a0);
+      const float pd = decay ? round_to(dt, p[t] * P.decay) : p[t];
+      a1 = fmaf(pd, pd, a1);
+      a2 += (g[t] * g[t]) / (sqrtf(dg[t]) + P.eps);
+    }
+    acc[0] += a0;
+    acc[1] += a1;
+    acc[2] += a2;
+  }
+  block_sum<3>(acc, red);
+  if (threadIdx.x == 0) write_slot(slots, tk.slot, acc[0], acc[1], acc[2]);
+}
+
+// -------------------------------------------------------- diag apply ---
+__global__ __launch_bounds__(256) void k_diag_apply(const scao_task* __restrict__ tasks,
+                                                    const scao_param_desc* __restrict__ params,
+                                                    const scao_param_stat* __restrict__ stat,
+                                                    double* slots) {
+  __shared__ double red[16];
+  const scao_task tk = tasks[blockIdx.x];
+  const scao_param_desc& P = params[tk.idx];
+  const scao_param_stat S = stat[tk.idx];
+  const int dt = P.dtype;
+  const Chunk ch(tk, P.numel);
+  const bool aligned = al_dt(P.p, dt) && al16(P.g) && al_dt(P.graw, dt) && al16(P.diag_ema) &&
+                       al16(P.exp_avg) && al16(P.exp_avg_sq) && al16(P.exp_avg_diff) &&
+                       al16(P.prev_grad) && (P.upd == nullptr || al16(P.upd));
+  double u2 = 0.0;
+#pragma unroll
+  for (int grp = 0; grp < 4; ++grp) {
+    const int64_t e = ch.elem(grp);
+    const int mk = ch.mask(e);
+    if (!mk) continue;
+    const bool vec = aligned && mk == 15;
+    const v4f graw = ld4(P.graw, dt, e, vec, mk);
+    const v4f g = (P.flags & SCAO_PF_GF32) ? ld_mgrad(P, e, vec, mk) : graw;
+    const v4f dg = ldf4(P.diag_ema, e, vec, mk);
+    v4f gp;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float x = dg[t] / P.diag_bias;
+      const float den = (float)pow((double)x, 0.25) + 1e-8f;
+      gp[t] = round_to(dt, graw[t] / den);
+    }
+    const v4f u = adan_tail(P, S, e, g, gp, vec, mk);
+    u2 += (double)write_update(P, e, u, vec, mk);
+  }
+  double x[1] = {u2};
+  block_sum<1>(x, red);
+  if (threadIdx.x == 0) write_slot(slots, tk.slot, 0.0, 0.0, x[0]);
+}
+
+// -------------------------------------------------------- lars write ---
+__global__ __launch_bounds__(256) void k_lars_write(const scao_task* __restrict__ tasks,
+                                                    const scao_param_desc* __restrict__ params,
+                                                    const scao_param_stat* __restrict__ stat) {
+  const scao_task tk = tasks[blockIdx.x];
+  const scao_param_desc& P = params[tk.idx];
+  const float alpha = stat[tk.idx].alpha;
+  const int dt = P.dtype;
+  const Chunk ch(tk, P.numel);
+  const bool aligned = al_dt(P.p, dt) && al16(P.upd);
+  const bool decay = P.flags & SCAO_PF_DECAY;
+#pragma unroll
+  for (int grp = 0; grp < 4; ++grp) {
+    const int64_t e = ch.elem(grp);
+    const int mk = ch.mask(e);
+    if (!mk) continue;
+    const bool vec = aligned && mk == 15;
+    const v4f u = ldf4(P.upd, e, vec, mk);
+    v4f p = ld4(P.p, dt, e, vec, mk);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float pd = decay ? round_to(dt, p[t] * P.decay) : p[t];
+      p[t] = round_to(dt, fmaf(round_to(dt, u[t]), alpha, pd));
+    }
+    st4(P.p, dt, e, p, vec, mk);
+  }
+}
+
+// ---------------------------------------------------------- diag ema ---
+__global__ __launch_bounds__(256) void k_diag_ema(const scao_task* __restrict__ tasks,
+                                                  const scao_param_desc* __restrict__ params,
+                                                  const float* __restrict__ rho_alpha) {
+  const scao_task tk = tasks[blockIdx.x];
+  const scao_param_desc& P = params[tk.idx];
+  const float rho = rho_alpha[2 * tk.idx], alpha = rho_alpha[2 * tk.idx + 1];
+  const int dt = P.dtype;
+  float* dg = const_cast<float*>(P.diag_ema);
+  const Chunk ch(tk, P.numel);
+  const bool aligned = al_dt(P.graw, dt) && al16(dg);
+#pragma unroll
+  for (int grp = 0; grp < 4; ++grp) {
+    const int64_t e = ch.elem(grp);
+    const int mk = ch.mask(e);
+    if (!mk) continue;
+    const bool vec = aligned && mk == 15;
+    const v4f g = ld4(P.graw, dt, e, vec, mk);
+    v4f d = ldf4(dg, e, vec, mk);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) d[t] = d[t] * rho + alpha * (g[t] * g[t]);
+    stf4(dg, e, d, vec, mk);
+  }
+}
+
+// ---------------------------------------------------------- finalize ---
+__global__ __launch_bounds__(64) void k_finalize_params(const scao_param_desc* __restrict__ params,
+                                                        const double* __restrict__ slots,
+                                                        scao_param_stat* stat, int phase) {
+  const scao_param_desc& P = params[blockIdx.x];
+  scao_param_stat& S = stat[blockIdx.x];
+  const int l = threadIdx.x;
+  const int dt = P.dtype;
+  if (phase == 0) {
+    double a[3] = {0.0, 0.0, 0.0};
+    for (int s = P.pre_begin + l; s < P.pre_end; s += 64)
+      for (int q = 0; q < 3; ++q) a[q] += slots[(int64_t)s * SCAO_SLOT_WIDTH + q];
+    for (int q = 0; q < 3; ++q) a[q] = wave_sum(a[q]);
+    if (l == 0) {
+      S.g2 = a[0];
+      S.p2 = a[1];
+      S.nu2 = a[2];
+      S.gnorm = round_to(dt, (float)sqrt(a[0]));
+      S.pnorm = round_to(dt, (float)sqrt(a[1]));
+      const float nu = (float)sqrt(a[2]);
+      S.nu = nu;
+      float clip = 1.0f;
+      if ((P.flags & SCAO_PF_CLIP) && nu > P.tau) clip = (1.0f / fmaxf(nu, P.eps)) * P.tau;
+      S.clip = clip;
+      S.u2 = 0.0;
+      S.unorm = 0.f;
+      S.trust = 1.0f;
+      S.alpha = (float)(-P.lr);
+    }
+  } else {
+    double a = 0.0;
+    for (int s = P.post_begin + l; s < P.post_end; s += 64)
+      a += slots[(int64_t)s * SCAO_SLOT_WIDTH + 2];
+    a = wave_sum(a);
+    if (l == 0) {
+      S.u2 = a;
+      const float un = (float)sqrt(a);
+      S.unorm = un;
+      float trust = 1.0f;
+      if ((P.flags & SCAO_PF_LARS) && !(S.pnorm == 0.f || un == 0.f)) {
+        const float num = round_to(dt, P.lars * S.pnorm);
+        const float wdp = round_to(dt, P.wd * S.pnorm);
+        trust = num / ((un + wdp) + 1e-8f);
+      }
+      S.trust = trust;
+      S.alpha = (float)(-(P.lr * (double)trust));
+    }
+  }
+}
+
+__global__ __launch_bounds__(64) void k_finalize_global(const scao_param_desc* __restrict__ params,
+                                                        int nparams, const scao_param_stat* stat,
+                                                        double* runtime, int norm_count) {
+  if (threadIdx.x != 0) return;
+  double sum = 0.0;
+  int cnt = 0;
+  for (int i = 0; i < nparams; ++i) {
+    if (params[i].norm_index < 0) continue;
+    sum += (double)stat[i].gnorm;
+    ++cnt;
+  }
+  if (cnt == 0 || cnt != norm_count) {
+    runtime[1] = 0.0;
+    return;
+  }
+  const double avg = sum / (double)cnt;
+  runtime[1] = avg;
+  runtime[0] = 0.95 * runtime[0] + 0.05 * avg;
+}
+
+}  // namespace
+
+// ------------------------------------------------------------- C ABI ---
+#define FLAT_LAUNCH(name, kernel, ...)                                                        \
+  do {                                                                                        \
+    SCAO_CHECK_ARG(ntasks >= 0, name ": ntasks < 0");                                        \
+    if (ntasks == 0) return SCAO_OK;                                                          \
+    SCAO_CHECK_ARG(tasks && params, name ": null pointer");                                  \
+    hipLaunchKernelGGL(kernel, dim3(ntasks), dim3(256), 0, (hipStream_t)stream, __VA_ARGS__); \
+    SCAO_LAUNCH_CHECK(name);                                                                  \
+    return SCAO_OK;                                                                           \
+  } while (0)
+
+extern "C" int scao_adam_step(const scao_task* tasks, int ntasks, const scao_param_desc* params,
+                              double* slots, void* stream) {
+  SCAO_CHECK_ARG(slots || ntasks == 0, "scao_adam_step: null slots");
+  FLAT_LAUNCH("scao_adam_step", k_adam, tasks, params, slots);
+}
+
+extern "C" int scao_diag_reduce(const scao_task* tasks, int ntasks, const scao_param_desc* params,
+                                double* slots, void* stream) {
+  SCAO_CHECK_ARG(slots || ntasks == 0, "scao_diag_reduce: null slots");
+  FLAT_LAUNCH("scao_diag_reduce", k_diag_reduce, tasks, params, slots);
+}
+
+extern "C" int scao_diag_apply(const scao_task* tasks, int ntasks, const scao_param_desc* params,
+                               const scao_param_stat* stat, double* slots, void* stream) {
+  SCAO_CHECK_ARG((slots && stat) || ntasks == 0, "scao_diag_apply: null pointer");
+  FLAT_LAUNCH("scao_diag_apply", k_diag_apply, tasks, params, stat, slots);
+}
+
+extern "C" int scao_lars_write(const scao_task* tasks, int ntasks, const scao_param_desc* params,
+                               const scao_param_stat* stat, void* stream) {
+  SCAO_CHECK_ARG(stat || ntasks == 0, "scao_lars_write: null stat");
+  FLAT_LAUNCH("scao_lars_write", k_lars_write, tasks, params, stat);
+}
+
+extern "C" int scao_diag_ema(const scao_task* tasks, int ntasks, const scao_param_desc* params,
+                             const float* rho_alpha, void* stream) {
+  SCAO_CHECK_ARG(rho_alpha || ntasks == 0, "scao_diag_ema: null rho_alpha");
+  FLAT_LAUNCH("scao_diag_ema", k_diag_ema, tasks, params, rho_alpha);
+}
+
+extern "C" int scao_step_finalize(const scao_param_desc* params, int nparams, const double* slots,
+                                  scao_param_stat* stat, double* runtime, int phase,
+                                  int update_norm_ema, int norm_count, void* stream) {
+  SCAO_CHECK_ARG(nparams >= 0 && (phase == 0 || phase == 1), "scao_step_finalize: bad args");
+  if (nparams == 0) return SCAO_OK;
+  SCAO_CHECK_ARG(params && slots && stat, "scao_step_finalize: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_finalize_params, dim3(nparams), dim3(64), 0, s, params, slots, stat, phase);
+  SCAO_LAUNCH_CHECK("scao_step_finalize");
+  if (phase == 0 && update_norm_ema) {
+    SCAO_CHECK_ARG(runtime != nullptr, "scao_step_finalize: null runtime");
+    hipLaunchKernelGGL(k_finalize_global, dim3(1), dim3(64), 0, s, params, nparams, stat, runtime,
+                       norm_count);
+    SCAO_LAUNCH_CHECK("scao_step_finalize/global");
+  }
+  return SCAO_OK;
+}

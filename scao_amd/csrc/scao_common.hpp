@@ -1,0 +1,251 @@
+// Shared device helpers for the gfx950 SCAO kernels.
+//
+// Arithmetic is compiled with -ffp-contract=off: every fused multiply-add in
+// these kernels is an explicit fmaf() placed where the reference's CPU path
+// (ATen vectorised kernels) rounds once, and everything else rounds per op.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/scao_amd.h"
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+#define SCAO_WAVE 64
+
+namespace scao {
+
+// ---------------------------------------------------------------- MFMA ---
+// v_mfma_f32_16x16x4_f32.  Lane l supplies A[l%16][l/16] and B[l/16][l%16];
+// the accumulator holds D[4*(l/16)+r][l%16] in element r (checked on gfx950).
+__device__ __forceinline__ v4f mfma16(float a, float b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// ------------------------------------------------------------- dtypes ---
+__device__ __forceinline__ float bf16_to_f(uint16_t h) {
+  return __uint_as_float(((uint32_t)h) << 16);
+}
+__device__ __forceinline__ uint16_t f_to_bf16(float f) {  // round to nearest even
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float f16_to_f(uint16_t h) {
+  _Float16 x = __builtin_bit_cast(_Float16, h);
+  return (float)x;
+}
+__device__ __forceinline__ uint16_t f_to_f16(float f) {
+  _Float16 x = (_Float16)f;
+  return __builtin_bit_cast(uint16_t, x);
+}
+
+// round a float to the storage dtype and back (the reference's .to(dtype))
+__device__ __forceinline__ float round_to(int dt, float x) {
+  if (dt == SCAO_BF16) return bf16_to_f(f_to_bf16(x));
+  if (dt == SCAO_F16) return f16_to_f(f_to_f16(x));
+  return x;
+}
+
+__device__ __forceinline__ float ld1(const void* base, int dt, int64_t i) {
+  if (dt == SCAO_F32) return ((const float*)base)[i];
+  uint16_t h = ((const uint16_t*)base)[i];
+  return dt == SCAO_BF16 ? bf16_to_f(h) : f16_to_f(h);
+}
+__device__ __forceinline__ void st1(void* base, int dt, int64_t i, float x) {
+  if (dt == SCAO_F32) {
+    ((float*)base)[i] = x;
+  } else {
+    ((uint16_t*)base)[i] = dt == SCAO_BF16 ? f_to_bf16(x) : f_to_f16(x);
+  }
+}
+
+// Four consecutive elements starting at element i.  `vec` promises 16-byte
+// (fp32) / 8-byte (16-bit) alignment and that all four are in bounds; else
+// element t is loaded only when mask bit t is set (zero otherwise).
+__device__ __forceinline__ v4f ld4(const void* base, int dt, int64_t i, bool vec, int mask) {
+  v4f r = {0.f, 0.f, 0.f, 0.f};
+  if (vec) {
+    if (dt == SCAO_F32) {
+      float4 x = *(const float4*)((const float*)base + i);
+      r = v4f{x.x, x.y, x.z, x.w};
+    } else {
+      uint2 x = *(const uint2*)((const uint16_t*)base + i);
+      uint16_t h[4] = {(uint16_t)(x.x & 0xffff), (uint16_t)(x.x >> 16), (uint16_t)(x.y & 0xffff),
+                       (uint16_t)(x.y >> 16)};
+      for (int t = 0; t < 4; ++t) r[t] = dt == SCAO_BF16 ? bf16_to_f(h[t]) : f16_to_f(h[t]);
+    }
+  } else {
+    for (int t = 0; t < 4; ++t)
+      if (mask & (1 << t)) r[t] = ld1(base, dt, i + t);
+  }
+  return r;
+}
+__device__ __forceinline__ void st4(void* base, int dt, int64_t i, v4f x, bool vec, int mask) {
+  if (vec) {
+    if (dt == SCAO_F32) {
+      *(float4*)((float*)base + i) = make_float4(x[0], x[1], x[2], x[3]);
+    } else {
+      uint16_t h[4];
+      for (int t = 0; t < 4; ++t) h[t] = dt == SCAO_BF16 ? f_to_bf16(x[t]) : f_to_f16(x[t]);
+      *(uint2*)((uint16_t*)base + i) =
+          make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+    }
+  } else {
+    for (int t = 0; t < 4; ++t)
+      if (mask & (1 << t)) st1(base, dt, i + t, x[t]);
+  }
+}
+// fp32-only variants (optimizer state is always float32)
+__device__ __forceinline__ v4f ldf4(const float* base, int64_t i, bool vec, int mask) {
+  if (vec) {
+    float4 x = *(const float4*)(base + i);
+    return v4f{x.x, x.y, x.z, x.w};
+  }
+  v4f r = {0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < 4; ++t)
+    if (mask & (1 << t)) r[t] = base[i + t];
+  return r;
+}
+__device__ __forceinline__ void stf4(float* base, int64_t i, v4f x, bool vec, int mask) {
+  if (vec) {
+    *(float4*)(base + i) = make_float4(x[0], x[1], x[2], x[3]);
+    return;
+  }
+  for (int t = 0; t < 4; ++t)
+    if (mask & (1 << t)) base[i + t] = x[t];
+}
+
+// the gradient the moments use: raw p.grad in its dtype, or a float32 buffer
+__device__ __forceinline__ v4f ld_mgrad(const scao_param_desc& P, int64_t i, bool vec, int mask) {
+  if (P.flags & SCAO_PF_GF32) return ldf4((const float*)P.g, i, vec, mask);
+  return ld4(P.g, P.dtype, i, vec, mask);
+}
+
+// ---------------------------------------------------------- reductions ---
+__device__ __forceinline__ double wave_sum(double x) {
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o, SCAO_WAVE);
+  return x;
+}
+__device__ __forceinline__ float wave_max(float x) {
+  for (int o = 32; o > 0; o >>= 1) x = fmaxf(x, __shfl_xor(x, o, SCAO_WAVE));
+  return x;
+}
+// Sum over a 256-thread block, deterministic order; result valid in thread 0.
+template <int NQ>
+__device__ __forceinline__ void block_sum(double (&x)[NQ], double* lds /* >= 4*NQ */) {
+  const int w = threadIdx.x / SCAO_WAVE, l = threadIdx.x % SCAO_WAVE;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) x[q] = wave_sum(x[q]);
+  __syncthreads();
+  if (l == 0)
+    for (int q = 0; q < NQ; ++q) lds[w * NQ + q] = x[q];
+  __syncthreads();
+  if (threadIdx.x == 0)
+    for (int q = 0; q < NQ; ++q) x[q] = ((lds[q] + lds[NQ + q]) + lds[2 * NQ + q]) + lds[3 * NQ + q];
+}
+__device__ __forceinline__ float block_max(float x, float* lds) {
+  const int w = threadIdx.x / SCAO_WAVE, l = threadIdx.x % SCAO_WAVE;
+  x = wave_max(x);
+  __syncthreads();
+  if (l == 0) lds[w] = x;
+  __syncthreads();
+  float r = fmaxf(fmaxf(lds[0], lds[1]), fmaxf(lds[2], lds[3]));
+  return r;
+}
+
+// clamp(S, 1e-8)^(-1/4) for the eigenvalue scaling (torch: pow(-0.25)); the
+// double evaluation is correctly rounded, torch's CPU path is within 1 ulp.
+__device__ __forceinline__ float inv4(float s) {
+  float c = fmaxf(s, 1e-8f);
+  return (float)pow((double)c, -0.25);
+}
+// clamp(S, eps)^(-1/2) = 1/sqrt (torch lowers pow(-0.5) to a reciprocal sqrt)
+__device__ __forceinline__ float inv2(float s, float eps) {
+  float c = fmaxf(s, eps);
+  return 1.0f / sqrtf(c);
+}
+
+// The optimizer's elementwise tail for four elements (scao/optimizer.py:606-645):
+// clip -> blend -> Adan moments -> bias-corrected update (-> gSNR mask).
+// Writes m, v, d, prev; returns the fp32 update u.
+__device__ __forceinline__ v4f adan_tail(const scao_param_desc& P, const scao_param_stat& S,
+                                         int64_t e, v4f g, v4f gp, bool vec, int mask) {
+  const int dt = P.dtype;
+  if (P.flags & SCAO_PF_CLIP) {
+    for (int t = 0; t < 4; ++t) gp[t] = round_to(dt, gp[t] * S.clip);
+  }
+  v4f m = ldf4(P.exp_avg, e, vec, mask);
+  v4f v = ldf4(P.exp_avg_sq, e, vec, mask);
+  v4f d = ldf4(P.exp_avg_diff, e, vec, mask);
+  v4f pv = ldf4(P.prev_grad, e, vec, mask);
+  v4f u;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const float geff = P.blend * gp[t] + P.omblend * g[t];
+    const float delta = g[t] - pv[t];
+    m[t] = fmaf(geff, P.omb1, m[t] * P.beta1);
+    d[t] = fmaf(delta, P.omb3, d[t] * P.beta3);
+    const float gad = geff + P.omb3 * delta;
+    v[t] = fmaf(P.omb2 * gad, gad, v[t] * P.beta2);
+    const float mh = m[t] / P.bc1;
+    const float dh = d[t] / P.bc3;
+    const float vh = v[t] / P.bc2;
+    float x = (mh + P.omb3 * dh) / (sqrtf(vh) + P.eps);
+    if (P.flags & SCAO_PF_GSNR) {
+      const float snr = fabsf(m[t]) / (sqrtf(v[t]) + P.eps);
+      x = x * (snr >= P.gsnr ? 1.0f : 0.0f);
+    }
+    u[t] = x;
+  }
+  stf4(P.exp_avg, e, m, vec, mask);
+  stf4(P.exp_avg_sq, e, v, vec, mask);
+  stf4(P.exp_avg_diff, e, d, vec, mask);
+  stf4(P.prev_grad, e, g, vec, mask);
+  return u;
+}
+
+// Final write of four elements: LARS params stage u, others update p at once.
+__device__ __forceinline__ float write_update(const scao_param_desc& P, int64_t e, v4f u,
+                                              bool vec, int mask) {
+  const int dt = P.dtype;
+  float u2 = 0.f;
+  if (P.flags & SCAO_PF_LARS) {
+    stf4(P.upd, e, u, vec, mask);
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      if (mask & (1 << t)) u2 = fmaf(u[t], u[t], u2);
+  } else {
+    const float alpha = (float)(-P.lr);
+    v4f p = ld4(P.p, dt, e, vec, mask);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float pd = (P.flags & SCAO_PF_DECAY) ? round_to(dt, p[t] * P.decay) : p[t];
+      p[t] = round_to(dt, fmaf(round_to(dt, u[t]), alpha, pd));
+    }
+    st4(P.p, dt, e, p, vec, mask);
+  }
+  return u2;
+}
+
+}  // namespace scao
+
+// ------------------------------------------------------------- errors ---
+void scao_set_error(const char* fmt, ...);
+#define SCAO_CHECK_ARG(cond, ...)         \
+  do {                                    \
+    if (!(cond)) {                        \
+      scao_set_error(__VA_ARGS__);        \
+      return SCAO_ERR_INVALID;            \
+    }                                     \
+  } while (0)
+#define SCAO_LAUNCH_CHECK(name)                                                     \
+  do {                                                                              \
+    hipError_t e_ = hipGetLastError();                                              \
+    if (e_ != hipSuccess) {                                                         \
+      scao_set_error("%s: launch failed: %s", name, hipGetErrorString(e_));        \
+      return SCAO_ERR_HIP;                                                          \
+    }                                                                               \
+  } while (0)

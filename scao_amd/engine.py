@@ -1,0 +1,686 @@
+"""Batched execution of the SCAO step on one ROCm device.
+
+The reference walks parameters and Kronecker blocks one at a time in Python
+(scao/optimizer.py:509-645 -> scao/preconditioner.py:457-564), issuing ~10
+small ATen calls per block and ~20 full-size elementwise passes per
+parameter with several host synchronisations.  Here one step is a fixed
+sequence of launches over *all* parameters and blocks at once:
+
+    adam_step          Phase-1 parameters                      (flat chunks)
+    kron_project       T = U_l^T G       for every Phase-2 block (256-col strips)
+    kron_delta         P = T U_r -> Delta, nu^2                  (k x k tiles)
+    kron_lift          W = U_l Delta                             (64-row strips)
+    diag_reduce        diagonal-mode Phase-2 parameters
+    step_finalize(0)   per-param norms, clip factor, global grad-norm EMA
+    kron_apply         G + W U_r^T -> clip -> blend -> Adan -> update
+    diag_apply
+    step_finalize(1)   LARS trust ratio
+    lars_write         p = fma(u, -(lr*trust), p*decay)
+
+No host synchronisation happens inside a non-refresh step.  Descriptor
+tables are numpy record arrays uploaded through pinned memory; the task
+lists (which depend only on shapes and phases) are cached on the device.
+
+The curvature refresh (``refresh``) batches every block due for an update:
+Gram -> EMA -> requantise on the GPU (no host round trip for the int8
+scale), then the eigendecomposition in PyTorch-ROCm (``torch.linalg.eigh``
+on stacked equal-size matrices) and the adaptive-rank choice with one host
+read of all ranks.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+from torch import Tensor
+
+from . import _lib as L
+from .preconditioner import SparsePreconditioner, leaf_epoch
+from .utils import batched_adaptive_rank, to_2d
+
+F32 = np.float32
+
+
+def _f32(x: float) -> float:
+    """A Python float rounded the way ATen rounds a scalar operand of an fp32 op."""
+    return float(F32(x))
+
+
+def _align4(n: int) -> int:
+    return (n + 3) & ~3
+
+
+def _aligned16(*ptrs) -> bool:
+    return all(p % 16 == 0 for p in ptrs if p)
+
+
+def require_hip(t: Tensor, what: str) -> None:
+    if t.device.type != "cuda":
+        raise RuntimeError(
+            f"scao_amd runs on ROCm devices only: {what} is on '{t.device}'. "
+            "Move the model to the GPU (there is no CPU path).")
+
+
+# --------------------------------------------------------------------------
+# per-step parameter record
+# --------------------------------------------------------------------------
+
+@dataclass
+class PItem:
+    """One parameter taking part in a step (host-side bookkeeping)."""
+    p: Tensor
+    graw: Tensor                 # p.grad (contiguous view)
+    gmom: Tensor | None          # filtered/noised fp32 grad for the moments, or None
+    st: dict
+    group: dict
+    pre: SparsePreconditioner
+    phase2: bool
+    step: int
+    scao_step: int = 0
+    lars: bool = False
+    diag: bool = False           # diagonal-mode preconditioner in Phase 2
+    leaves: list = field(default_factory=list)  # [(leaf, r0, c0)]
+
+
+class Workspace:
+    """Device buffers reused across steps (one per optimizer)."""
+
+    def __init__(self, device: torch.device):
+        self.device = device
+        self.runtime = torch.tensor([1.0, 0.0], dtype=torch.float64, device=device)
+        self._bufs: dict[str, Tensor] = {}
+        self.struct_key = None
+        self.leaf_epoch = -1
+        self.tasks: dict[str, Tensor] = {}
+        self.ntasks: dict[str, int] = {}
+        self.slot_ranges = None
+        self.nslots = 0
+        self.leaf_dev = None
+        self.leaf_index = {}
+        self.upd_offsets = {}
+
+    def buf(self, name: str, nbytes: int) -> Tensor:
+        b = self._bufs.get(name)
+        if b is None or b.numel() < nbytes:
+            b = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+            self._bufs[name] = b
+        return b
+
+
+# --------------------------------------------------------------------------
+# task lists
+# --------------------------------------------------------------------------
+
+# Optional per-launch timing: when ``TIMING`` is a dict, every launch of the
+# step and of the refresh is bracketed by a pair of events on the launch
+# stream and appended under its entry-point name (used by bench.py).
+TIMING = None
+
+
+def _call(name: str, *args) -> None:
+    if TIMING is None:
+        L.call(name, *args)
+        return
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    L.call(name, *args)
+    b.record()
+    TIMING.setdefault(name, []).append((a, b))
+
+
+def _mark(name: str):
+    """Context manager timing a host-driven stage (e.g. torch eigh) on the stream."""
+    class _M:
+        def __enter__(self):
+            if TIMING is not None:
+                self.a = torch.cuda.Event(enable_timing=True)
+                self.a.record()
+
+        def __exit__(self, *exc):
+            if TIMING is not None:
+                b = torch.cuda.Event(enable_timing=True)
+                b.record()
+                TIMING.setdefault(name, []).append((self.a, b))
+    return _M()
+
+
+def timing_summary() -> dict:
+    """{name: (count, mean ms, total ms)} of the recorded events (synchronises)."""
+    torch.cuda.synchronize()
+    out = {}
+    for name, ev in (TIMING or {}).items():
+        ms = [a.elapsed_time(b) for a, b in ev]
+        out[name] = (len(ms), sum(ms) / len(ms), sum(ms))
+    return out
+
+
+def _flat_chunks(numel: int) -> int:
+    return (numel + L.FLAT_CHUNK - 1) // L.FLAT_CHUNK
+
+
+def _build_structure(items: list[PItem]):
+    """Slots, task lists and the Phase-2 leaf list for a step structure.
+
+    Every reduction slot is written by exactly one task; each parameter's
+    pre-finalize slots and post-finalize slots are contiguous ranges."""
+    tasks = {k: [] for k in ("adam", "proj", "delta", "lift", "dred", "apply", "dapply", "lars")}
+    ranges = []
+    leaves = []          # (leaf, r0, c0, param index)
+    slot = 0
+    for pi, it in enumerate(items):
+        pre_begin = slot
+        if not it.phase2:
+            for c in range(_flat_chunks(it.p.numel())):
+                tasks["adam"].append((pi, c, 0, slot))
+                slot += 1
+            ranges.append((pre_begin, slot, slot, slot))
+            continue
+        if it.diag:
+            for c in range(_flat_chunks(it.p.numel())):
+                tasks["dred"].append((pi, c, 0, slot))
+                slot += 1
+            pre_end = slot
+            for c in range(_flat_chunks(it.p.numel())):
+                tasks["dapply"].append((pi, c, 0, slot))
+                slot += 1
+            ranges.append((pre_begin, pre_end, pre_end, slot))
+        else:
+            first = len(leaves)
+            for (leaf, r0, c0) in it.leaves:
+                leaves.append((leaf, r0, c0, pi))
+            # projection (chunk 0 owns the norm slots)
+            for li in range(first, len(leaves)):
+                leaf = leaves[li][0]
+                m, n = leaf.m, leaf.n
+                k = leaf.U_l.shape[1]
+                for j0 in range(0, n, L.PROJ_COLS):
+                    for c0 in range(0, k, 64):
+                        if c0 == 0:
+                            tasks["proj"].append((li, j0, c0, slot))
+                            slot += 1
+                        else:
+                            tasks["proj"].append((li, j0, c0, -1))
+            for li in range(first, len(leaves)):
+                k = leaves[li][0].U_l.shape[1]
+                for a in range(0, k, 64):
+                    for b in range(0, k, 64):
+                        tasks["delta"].append((li, a, b, slot))
+                        slot += 1
+            pre_end = slot
+            for li in range(first, len(leaves)):
+                leaf = leaves[li][0]
+                k = leaf.U_l.shape[1]
+                for i0 in range(0, leaf.m, 64):
+                    for d0 in range(0, k, 64):
+                        tasks["lift"].append((li, i0, d0, -1))
+                for i0 in range(0, leaf.m, L.APPLY_TILE):
+                    for j0 in range(0, leaf.n, L.APPLY_TILE):
+                        tasks["apply"].append((li, i0, j0, slot))
+                        slot += 1
+            ranges.append((pre_begin, pre_end, pre_end, slot))
+        if it.lars:
+            for c in range(_flat_chunks(it.p.numel())):
+                tasks["lars"].append((pi, c, 0, -1))
+    arrays = {k: np.array(v, dtype=np.int32).reshape(-1, 4).copy().view(L.TASK).reshape(-1)
+              for k, v in tasks.items()}
+    return arrays, ranges, slot, leaves
+
+
+def _leaf_table(leaves, items: list[PItem], ws: Workspace):
+    """Block descriptors plus T/Delta/W scratch for every Phase-2 block."""
+    sizes = []
+    for (leaf, r0, c0, pi) in leaves:
+        k = leaf.U_l.shape[1]
+        sizes.append((_align4(k * leaf.n), _align4(k * k), _align4(leaf.m * k)))
+    total = sum(a + b + c for a, b, c in sizes)
+    scratch = ws.buf("leaf_scratch", max(total, 1) * 4)
+    base = scratch.data_ptr()
+    tab = np.zeros(len(leaves), dtype=L.LEAF_DESC)
+    off = 0
+    for i, ((leaf, r0, c0, pi), (st, sd, sw)) in enumerate(zip(leaves, sizes)):
+        it = items[pi]
+        cols = it.graw.shape[-1] if it.graw.ndim == 2 else to_2d(it.graw)[0].shape[1]
+        e = tab[i]
+        e["Ul"], e["Ur"] = leaf.U_l.data_ptr(), leaf.U_r.data_ptr()
+        e["Sl"], e["Sr"] = leaf.S_l.data_ptr(), leaf.S_r.data_ptr()
+        e["T"] = base + 4 * off
+        e["Delta"] = base + 4 * (off + st)
+        e["W"] = base + 4 * (off + st + sd)
+        off += st + sd + sw
+        e["off"] = r0 * cols + c0
+        e["ld"] = cols
+        e["param"] = pi
+        e["m"], e["n"], e["k"] = leaf.m, leaf.n, leaf.U_l.shape[1]
+        vec = (e["off"] % 4 == 0 and cols % 4 == 0 and leaf.n % 4 == 0 and
+               _aligned16(it.p.data_ptr(), it.graw.data_ptr(), int(e["T"])) and
+               (it.gmom is None or _aligned16(it.gmom.data_ptr())))
+        e["flags"] = L.LF_VEC4 if vec else 0
+    return tab
+
+
+# --------------------------------------------------------------------------
+# the step
+# --------------------------------------------------------------------------
+
+def _param_table(items: list[PItem], ranges, ws: Workspace, gsnr: float | None):
+    tab = np.zeros(len(items), dtype=L.PARAM_DESC)
+    for i, it in enumerate(items):
+        g = it.group
+        st = it.st
+        e = tab[i]
+        lr = g["lr"]
+        beta1, beta2 = g["betas"]
+        beta3 = g["beta3"]
+        wd = g["weight_decay"]
+        t = it.step
+        e["p"] = it.p.data_ptr()
+        e["graw"] = it.graw.data_ptr()
+        e["g"] = it.gmom.data_ptr() if it.gmom is not None else it.graw.data_ptr()
+        e["exp_avg"] = st["exp_avg"].data_ptr()
+        e["exp_avg_sq"] = st["exp_avg_sq"].data_ptr()
+        e["exp_avg_diff"] = st["exp_avg_diff"].data_ptr()
+        e["prev_grad"] = st["prev_grad"].data_ptr()
+        e["numel"] = it.p.numel()
+        e["cols"] = to_2d(it.p)[0].shape[1] if it.p.ndim != 2 else it.p.shape[1]
+        e["lr"] = lr
+        e["beta1"], e["omb1"] = beta1, 1.0 - beta1
+        e["beta2"], e["omb2"] = beta2, 1.0 - beta2
+        e["beta3"], e["omb3"] = beta3, 1.0 - beta3
+        e["eps"] = g["eps"]
+        flags = L.PF_NORM
+        if wd != 0.0:
+            flags |= L.PF_DECAY
+            e["decay"] = 1.0 - lr * wd
+        else:
+            e["decay"] = 1.0
+        if it.gmom is not None:
+            flags |= L.PF_GF32
+        bc1 = 1.0 - beta1 ** t
+        bc2 = 1.0 - beta2 ** t
+        if not it.phase2:
+            e["adam_sqrt_bc2"] = math.sqrt(bc2)
+            e["adam_alpha"] = -(lr / bc1)
+        else:
+            e["bc1"], e["bc2"] = bc1, bc2
+            e["bc3"] = 1.0 - beta3 ** t
+            bsteps = g.get("blend_steps", 50)
+            blend = min(1.0, it.scao_step / bsteps) if bsteps > 0 else 1.0
+            e["blend"], e["omblend"] = blend, 1.0 - blend
+            tau = g["tau"]
+            if tau is not None:
+                flags |= L.PF_CLIP
+                e["tau"] = tau
+            if it.lars:
+                flags |= L.PF_LARS
+                e["lars"] = g["lars_coeff"]
+                e["wd"] = wd
+                e["upd"] = ws.buf("upd", 4).data_ptr() + 4 * ws.upd_offsets[i]
+            if gsnr is not None:
+                flags |= L.PF_GSNR
+                e["gsnr"] = gsnr
+            if it.diag:
+                flags |= L.PF_DIAG
+                e["diag_ema"] = it.pre.diag_ema.data_ptr()
+                e["diag_bias"] = getattr(it.pre, "_diag_bias_factor", 1.0)
+        e["dtype"] = L.DTYPE_CODE[it.p.dtype]
+        e["flags"] = flags
+        e["pre_begin"], e["pre_end"], e["post_begin"], e["post_end"] = ranges[i]
+        e["norm_index"] = i
+    return tab
+
+
+def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
+             gsnr: float | None = None) -> None:
+    """Launch one optimizer step for ``items`` (all on ws.device)."""
+    if not items:
+        return
+    dev = ws.device
+    skey = tuple((id(it.p), it.phase2, it.diag, it.lars, it.p.numel(),
+                  tuple((id(lf), r0, c0, lf.U_l.shape[1]) for lf, r0, c0 in it.leaves))
+                 for it in items)
+    if skey != ws.struct_key:
+        arrays, ranges, nslots, leaves = _build_structure(items)
+        ws.tasks = {k: (L.upload(v, dev) if len(v) else None) for k, v in arrays.items()}
+        ws.ntasks = {k: len(v) for k, v in arrays.items()}
+        ws.slot_ranges, ws.nslots, ws.leaves = ranges, nslots, leaves
+        off = 0
+        ws.upd_offsets = {}
+        for i, it in enumerate(items):
+            if it.phase2 and it.lars:
+                ws.upd_offsets[i] = off
+                off += _align4(it.p.numel())
+        ws.upd_total = off
+        ws.struct_key = skey
+        ws.leaf_epoch = -1
+    if ws.upd_total:
+        ws.buf("upd", ws.upd_total * 4)
+    if ws.leaf_epoch != leaf_epoch() or ws.leaf_dev is None or _grads_moved(items, ws):
+        tab = _leaf_table(ws.leaves, items, ws)
+        ws.leaf_dev = L.upload(tab, dev) if len(tab) else None
+        ws.leaf_epoch = leaf_epoch()
+        ws.grad_ptrs = [it.graw.data_ptr() for it in items]
+    ptab = _param_table(items, ws.slot_ranges, ws, gsnr)
+    params = L.upload(ptab, dev)
+    slots = ws.buf("slots", max(ws.nslots, 1) * 8 * L.SLOT_WIDTH)
+    stat = ws.buf("stat", len(items) * L.PARAM_STAT.itemsize)
+    s = L.stream_ptr(dev)
+    T, N = ws.tasks, ws.ntasks
+    P, S, SL = params.data_ptr(), stat.data_ptr(), slots.data_ptr()
+    LF = ws.leaf_dev.data_ptr() if ws.leaf_dev is not None else 0
+
+    def tp(name):
+        return T[name].data_ptr() if T[name] is not None else 0
+
+    if N["adam"]:
+        _call("scao_adam_step", tp("adam"), N["adam"], P, SL, s)
+    if N["proj"]:
+        _call("scao_kron_project", tp("proj"), N["proj"], LF, P, SL, s)
+        _call("scao_kron_delta", tp("delta"), N["delta"], LF, P, SL, s)
+        _call("scao_kron_lift", tp("lift"), N["lift"], LF, s)
+    if N["dred"]:
+        _call("scao_diag_reduce", tp("dred"), N["dred"], P, SL, s)
+    _call("scao_step_finalize", P, len(items), SL, S, ws.runtime.data_ptr(), 0,
+           1 if update_norm_ema else 0, len(items), s)
+    if N["apply"]:
+        _call("scao_kron_apply", tp("apply"), N["apply"], LF, P, S, SL, s)
+    if N["dapply"]:
+        _call("scao_diag_apply", tp("dapply"), N["dapply"], P, S, SL, s)
+    if N["lars"]:
+        _call("scao_step_finalize", P, len(items), SL, S, 0, 1, 0, len(items), s)
+        _call("scao_lars_write", tp("lars"), N["lars"], P, S, s)
+    ws.last_params = params   # keep descriptors alive until the next step
+
+
+def _grads_moved(items, ws) -> bool:
+    ptrs = getattr(ws, "grad_ptrs", None)
+    return ptrs is None or len(ptrs) != len(items) or any(
+        p != it.graw.data_ptr() for p, it in zip(ptrs, items))
+
+
+def read_stats(ws: Workspace, n: int) -> np.ndarray:
+    """Per-parameter statistics of the last step (host copy; synchronises)."""
+    raw = ws.buf("stat", n * L.PARAM_STAT.itemsize)[: n * L.PARAM_STAT.itemsize].cpu().numpy()
+    return raw.view(L.PARAM_STAT)
+
+
+# --------------------------------------------------------------------------
+# curvature refresh
+# --------------------------------------------------------------------------
+
+REFRESH_SCRATCH_BYTES = 2 << 30   # fp32 EMA staging per refresh chunk (int8 mode)
+EIGH_BATCH_BYTES = 1 << 30        # stacked eigh inputs per launch
+
+
+def refresh(entries, eigen_only: bool = False) -> None:
+    """update_curvature for several preconditioners at once.
+
+    ``entries``: list of (SparsePreconditioner, grad tensor).  Follows
+    scao/preconditioner.py:297-451: precond_step bookkeeping, the EMA update
+    (Gram on MFMA, int8 requantisation on the device), bias correction,
+    Tikhonov shift, eigh, flip/clamp, adaptive rank with rank momentum.
+    ``eigen_only`` skips the EMA update (the curvature factors are taken as
+    they are) -- used to check the eigendecomposition stage in isolation."""
+    if not entries:
+        return
+    dev = entries[0][1].device
+    kron, diag = [], []
+    for pre, grad in entries:
+        require_hip(grad, "gradient")
+        if grad.is_sparse:
+            raise RuntimeError("SCAO does not support sparse gradients.")
+        g = grad.detach()
+        if not g.is_contiguous():
+            g = g.contiguous()
+        pre._bump_steps()
+        if pre.use_block_diagonal or pre.use_kronecker:
+            cols = to_2d(g)[0].shape[1]
+            for leaf, r0, c0 in pre.leaves():
+                kron.append((leaf, g, r0 * cols + c0, cols))
+            for sub in _diag_subblocks(pre):
+                raise NotImplementedError(
+                    "block-diagonal parameter with a 1-row/1-column remainder block "
+                    f"(shape {tuple(pre.original_shape)}) is not supported by scao_amd")
+        else:
+            diag.append((pre, g))
+    s = L.stream_ptr(dev)
+    if diag and not eigen_only:
+        _refresh_diag(diag, dev, s)
+    if kron:
+        _refresh_kron(kron, dev, s, eigen_only)
+    for pre, _ in entries:
+        pre._sync_k()
+
+
+def _diag_subblocks(pre):
+    if pre.use_block_diagonal:
+        for b in pre._blocks:
+            if not (b.use_block_diagonal or b.use_kronecker):
+                yield b
+            else:
+                yield from _diag_subblocks(b)
+
+
+def _refresh_diag(diag, dev, s):
+    tab = np.zeros(len(diag), dtype=L.PARAM_DESC)
+    ra = np.zeros(2 * len(diag), dtype=np.float32)
+    tasks = []
+    for i, (pre, g) in enumerate(diag):
+        e = tab[i]
+        e["graw"] = e["g"] = g.data_ptr()
+        e["diag_ema"] = pre.diag_ema.data_ptr()
+        e["numel"] = g.numel()
+        e["dtype"] = L.DTYPE_CODE[g.dtype]
+        ra[2 * i], ra[2 * i + 1] = pre.rho, 1.0 - pre.rho
+        tasks += [(i, c, 0, -1) for c in range(_flat_chunks(g.numel()))]
+    tt = np.array(tasks, dtype=np.int32).reshape(-1, 4).copy().view(L.TASK).reshape(-1)
+    td, pd = L.upload(tt, dev), L.upload(tab, dev)
+    rd = L.upload(ra, dev)
+    _call("scao_diag_ema", td.data_ptr(), len(tt), pd.data_ptr(), rd.data_ptr(), s)
+    for pre, _ in diag:
+        pre._diag_bias_factor = max(1.0 - pre.rho ** pre.precond_step, 1e-8)
+
+
+def _refresh_kron(kron, dev, s, eigen_only=False):
+    # 1) Gram -> EMA (-> requantise), chunked by staging memory
+    todo = [] if eigen_only else list(kron)
+    while todo:
+        chunk, used = [], 0
+        while todo:
+            leaf = todo[0][0]
+            need = 4 * (leaf.m * leaf.m + leaf.n * leaf.n) if leaf.use_int8_ema else 0
+            if chunk and used + need > REFRESH_SCRATCH_BYTES:
+                break
+            chunk.append(todo.pop(0))
+            used += need
+        _gram_chunk(chunk, dev, s)
+    # 2) eigendecomposition inputs, batched by dimension
+    jobs = {}   # dim -> list of (leaf, side)
+    for leaf, *_ in kron:
+        jobs.setdefault(leaf.m, []).append((leaf, 0))
+        jobs.setdefault(leaf.n, []).append((leaf, 1))
+    spectra = {}   # (id(leaf), side) -> (S_desc, U_desc)
+    eig_timer = _mark("refresh:eigh+rank")
+    eig_timer.__enter__()
+    for dim, lst in jobs.items():
+        per = max(1, EIGH_BATCH_BYTES // (4 * dim * dim))
+        for b0 in range(0, len(lst), per):
+            part = lst[b0:b0 + per]
+            X = _eig_inputs(part, dim, dev, s)
+            w, V = _eigh_batched(X)
+            S_desc = w.flip(-1).clamp(min=0.0)
+            U_desc = V.flip(-1)
+            for (leaf, side), Sd, Ud in zip(part, S_desc, U_desc):
+                spectra[(id(leaf), side)] = (Sd, Ud)
+            del X
+    # 3) adaptive rank for every (leaf, side) in one device pass + one read
+    keys = [(leaf, side) for leaf, *_ in kron for side in (0, 1)]
+    ranks = {}
+    by_dim = {}
+    for leaf, side in keys:
+        dim = leaf.m if side == 0 else leaf.n
+        by_dim.setdefault(dim, []).append((leaf, side))
+    dev_ranks = []
+    for dim, lst in by_dim.items():
+        S = torch.stack([spectra[(id(lf), sd)][0] for lf, sd in lst])
+        eps = torch.tensor([lf.epsilon_sparse for lf, _ in lst], device=dev, dtype=torch.float64)
+        kmin = torch.tensor([lf.k_min for lf, _ in lst], device=dev, dtype=torch.int64)
+        kmax = torch.tensor([lf.k_max for lf, _ in lst], device=dev, dtype=torch.int64)
+        dev_ranks.append((lst, batched_adaptive_rank(S, eps, kmin, kmax)))
+    host = torch.cat([r for _, r in dev_ranks]).cpu().tolist() if dev_ranks else []
+    i = 0
+    for lst, _ in dev_ranks:
+        for key in lst:
+            ranks[(id(key[0]), key[1])] = int(host[i])
+            i += 1
+    eig_timer.__exit__(None, None, None)
+    # 4) rank momentum and truncation (reference :437-451)
+    for leaf, *_ in kron:
+        k = min(ranks[(id(leaf), 0)], ranks[(id(leaf), 1)])
+        k = max(k, leaf._k - 1)
+        k = min(k, leaf._k + 4)
+        k = int(min(leaf.k_max, max(leaf.k_min, k)))
+        leaf._k = k
+        Sl, Ul = spectra[(id(leaf), 0)]
+        Sr, Ur = spectra[(id(leaf), 1)]
+        leaf.U_l = Ul[:, :k].contiguous()
+        leaf.S_l = Sl[:k].contiguous()
+        leaf.U_r = Ur[:, :k].contiguous()
+        leaf.S_r = Sr[:k].contiguous()
+        leaf._touch()
+
+
+def _gram_chunk(chunk, dev, s):
+    descs, tasks, req_tasks, scale_ptrs = [], [], [], []
+    staging = []
+    for leaf, g, off, ld in chunk:
+        for side in (0, 1):
+            dim = leaf.m if side == 0 else leaf.n
+            nt = (dim + L.GRAM_TILE - 1) // L.GRAM_TILE
+            e = np.zeros(1, dtype=L.GRAM_DESC)[0]
+            e["g"], e["off"], e["ld"] = g.data_ptr(), off, ld
+            e["rows"], e["cols"], e["side"] = leaf.m, leaf.n, side
+            e["dtype"] = L.DTYPE_CODE[g.dtype]
+            e["ntiles"] = nt * nt
+            e["rho"], e["alpha"] = leaf.rho, 1.0 - leaf.rho
+            di = len(descs)
+            if leaf.use_int8_ema:
+                q = leaf.L_ema_q if side == 0 else leaf.R_ema_q
+                x = torch.empty(dim * dim + nt * nt, dtype=torch.float32, device=dev)
+                staging.append(x)
+                e["q"] = q.data_ptr()
+                e["scale"] = leaf._scale.data_ptr() + 8 * side
+                e["ema"] = x.data_ptr()
+                e["amax"] = x.data_ptr() + 4 * dim * dim
+                scale_ptrs.append(leaf._scale.data_ptr() + 8 * side)
+                for c in range(_flat_chunks(dim * dim)):
+                    req_tasks.append((di, c, 0, -1))
+            else:
+                e["ema"] = (leaf.L_ema if side == 0 else leaf.R_ema).data_ptr()
+                scale_ptrs.append(0)
+            for a in range(nt):
+                for b in range(nt):
+                    tasks.append((di, a, b, a * nt + b))
+            descs.append(e)
+    dtab = np.array(descs, dtype=L.GRAM_DESC)
+    dd = L.upload(dtab, dev)
+    tt = np.array(tasks, dtype=np.int32).reshape(-1, 4).copy().view(L.TASK).reshape(-1)
+    td = L.upload(tt, dev)
+    _call("scao_gram_ema", td.data_ptr(), len(tt), dd.data_ptr(), s)
+    if req_tasks:
+        rt = np.array(req_tasks, dtype=np.int32).reshape(-1, 4).copy().view(L.TASK).reshape(-1)
+        rd = L.upload(rt, dev)
+        sp = L.upload(np.array(scale_ptrs, dtype=np.uint64), dev)
+        _call("scao_requant", rd.data_ptr(), len(rt), dd.data_ptr(), sp.data_ptr(), s)
+    del staging   # stream-ordered reuse by the caching allocator is safe
+
+
+def _eig_inputs(part, dim, dev, s) -> Tensor:
+    X = torch.empty(len(part), dim, dim, dtype=torch.float32, device=dev)
+    descs, tasks = [], []
+    nchunk = _flat_chunks(dim * dim)
+    for i, (leaf, side) in enumerate(part):
+        e = np.zeros(1, dtype=L.PREP_DESC)[0]
+        bias = 1.0 - leaf.rho ** leaf.precond_step
+        e["bias"] = max(bias, 1e-8)
+        e["dim"] = dim
+        e["out"] = X[i].data_ptr()
+        if leaf.use_int8_ema:
+            e["q"] = (leaf.L_ema_q if side == 0 else leaf.R_ema_q).data_ptr()
+            e["scale"] = leaf._scale.data_ptr() + 8 * side
+        else:
+            e["ema"] = (leaf.L_ema if side == 0 else leaf.R_ema).data_ptr()
+        descs.append(e)
+        tasks += [(i, c, 0, -1) for c in range(nchunk)]
+    dd = L.upload(np.array(descs, dtype=L.PREP_DESC), dev)
+    tt = np.array(tasks, dtype=np.int32).reshape(-1, 4).copy().view(L.TASK).reshape(-1)
+    td = L.upload(tt, dev)
+    _call("scao_eig_prep", td.data_ptr(), len(tt), dd.data_ptr(), s)
+    return X
+
+
+def _eigh_batched(X: Tensor):
+    """torch.linalg.eigh on a stack; on LinAlgError retry each matrix, adding
+    1e-8 to its diagonal when it fails again (reference :413-428)."""
+    try:
+        return torch.linalg.eigh(X)
+    except torch.linalg.LinAlgError:
+        ws, vs = [], []
+        for A in X:
+            try:
+                w, V = torch.linalg.eigh(A)
+            except torch.linalg.LinAlgError:
+                A = A.clone()
+                A.diagonal().add_(1e-8)
+                w, V = torch.linalg.eigh(A)
+            ws.append(w)
+            vs.append(V)
+        return torch.stack(ws), torch.stack(vs)
+
+
+# --------------------------------------------------------------------------
+# standalone preconditioner methods
+# --------------------------------------------------------------------------
+
+def precondition_one(pre: SparsePreconditioner, grad: Tensor) -> Tensor:
+    """SparsePreconditioner.precondition through the HIP fused operator."""
+    require_hip(grad, "gradient")
+    dt = grad.dtype
+    g2, shape = to_2d(grad.to(torch.float32))
+    g2 = g2.contiguous()
+    if pre.use_block_diagonal or pre.use_kronecker:
+        out = torch.zeros_like(g2) if pre.use_block_diagonal else None
+        for leaf, r0, c0 in pre.leaves():
+            gb = g2[r0:r0 + leaf.m, c0:c0 + leaf.n]
+            from .hip import fused_kronecker_precond
+            _, sl = leaf.U_l, leaf.S_l.clamp(min=1e-8).pow(-0.25)
+            sr = leaf.S_r.clamp(min=1e-8).pow(-0.25)
+            res = fused_kronecker_precond(leaf.U_l, sl, leaf.U_r, sr, gb)
+            if out is None:
+                out = res
+            else:
+                out[r0:r0 + leaf.m, c0:c0 + leaf.n] = res
+        return out.reshape(shape).to(dt)
+    bias = getattr(pre, "_diag_bias_factor", 1.0)
+    den = (pre.diag_ema / bias).reshape_as(g2).pow(0.25).add_(1e-8)
+    return (g2 / den).reshape(shape).to(dt)
+
+
+def natural_norm_one(pre: SparsePreconditioner, grad: Tensor, eps: float) -> Tensor:
+    """SparsePreconditioner.natural_grad_norm (small-matrix torch ops on device)."""
+    require_hip(grad, "gradient")
+    g2, _ = to_2d(grad.to(torch.float32))
+    if pre.use_block_diagonal:
+        parts = []
+        for leaf, r0, c0 in pre.leaves():
+            parts.append(natural_norm_one(leaf, g2[r0:r0 + leaf.m, c0:c0 + leaf.n], eps).pow(2))
+        return torch.stack(parts).sum().sqrt()
+    if not pre.use_kronecker:
+        den = pre.diag_ema.reshape_as(g2).pow(0.5).add_(eps)
+        return (g2.pow(2) / den).sum().sqrt()
+    il = pre.S_l.clamp(min=eps).pow(-0.5)
+    ir = pre.S_r.clamp(min=eps).pow(-0.5)
+    proj = (pre.U_l.T @ g2) @ pre.U_r
+    return (il.unsqueeze(1) * proj * ir.unsqueeze(0)).norm(p="fro")

@@ -1,0 +1,112 @@
+"""Callback metrics and loggers (reference: scao/logging.py:61-219).
+
+Plain Python over the optimizer's host state; computed only when a callback
+is registered.  ``scao/L_norm_mean`` for int8 EMAs uses ``scale * 127`` as
+the reference does, which reads each block's scale back from the device.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Callable
+
+MetricsDict = dict
+Callback = Callable[[MetricsDict], None]
+
+
+class ConsoleLogger:
+    """reference :61-86."""
+
+    def __init__(self, log_every: int = 100, prefix: str = "[SCAO]") -> None:
+        self.log_every = log_every
+        self.prefix = prefix
+
+    def __call__(self, metrics: MetricsDict) -> None:
+        step = metrics.get("step", 0)
+        if isinstance(step, int) and step % self.log_every != 0:
+            return
+        parts = [f"step={step}"]
+        for k, v in metrics.items():
+            if k == "step":
+                continue
+            parts.append(f"{k}={v:.4f}" if isinstance(v, float) else f"{k}={v}")
+        print(f"{self.prefix} " + "  ".join(parts))
+
+
+class TensorBoardLogger:
+    """reference :89-121."""
+
+    def __init__(self, writer, log_every: int = 50, tag_prefix: str = "") -> None:
+        self.writer = writer
+        self.log_every = log_every
+        self.tag_prefix = tag_prefix
+
+    def __call__(self, metrics: MetricsDict) -> None:
+        step = metrics.get("step", 0)
+        if isinstance(step, int) and step % self.log_every != 0:
+            return
+        for k, v in metrics.items():
+            if k == "step":
+                continue
+            if isinstance(v, (bool, int, float)):
+                x = float(v)
+            else:
+                continue
+            if math.isnan(x):
+                continue
+            self.writer.add_scalar(f"{self.tag_prefix}{k}" if self.tag_prefix else k, x,
+                                   global_step=step)
+
+
+class WandbLogger:
+    """reference :124-144 (no-op when wandb is not importable)."""
+
+    def __init__(self, log_every: int = 50) -> None:
+        self.log_every = log_every
+
+    def __call__(self, metrics: MetricsDict) -> None:
+        step = metrics.get("step", 0)
+        if isinstance(step, int) and step % self.log_every != 0:
+            return
+        try:
+            import wandb  # type: ignore[import]
+            wandb.log({k: v for k, v in metrics.items() if k != "step"}, step=step)
+        except ImportError:
+            pass
+
+
+def collect_metrics(optimizer) -> MetricsDict:
+    """reference :151-219."""
+    step = 0
+    ranks, lnorms = [], []
+    for st in optimizer.state.values():
+        if "step" in st:
+            step = max(step, st["step"])
+        if "preconditioner" in st:
+            pre = st["preconditioner"]
+            ranks.append(pre.k)
+            if getattr(pre, "use_block_diagonal", False):
+                bn = []
+                for b in pre._blocks:
+                    if b.use_kronecker:
+                        bn.append(b.L_ema_scale * 127.0 if getattr(b, "use_int8_ema", False)
+                                  else b.L_ema.norm(p="fro").item())
+                if bn:
+                    lnorms.append(sum(bn) / len(bn))
+            elif getattr(pre, "use_kronecker", False):
+                lnorms.append(pre.L_ema_scale * 127.0 if getattr(pre, "use_int8_ema", False)
+                              else pre.L_ema.norm(p="fro").item())
+    metrics: MetricsDict = {"step": step}
+    if ranks:
+        metrics["scao/rank_mean"] = sum(ranks) / len(ranks)
+        metrics["scao/rank_min"] = min(ranks)
+        metrics["scao/rank_max"] = max(ranks)
+        metrics["scao/layers"] = len(ranks)
+    if lnorms:
+        metrics["scao/L_norm_mean"] = sum(lnorms) / len(lnorms)
+    metrics["scao/precond_freq"] = optimizer.param_groups[0].get("precond_freq", -1)
+    ws = getattr(optimizer, "_warmup_scheduler", None)
+    if ws is not None:
+        metrics["scao/warmup_exited_early"] = ws.exited_early
+        metrics["scao/actual_warmup_steps"] = ws.actual_warmup_steps
+    return metrics

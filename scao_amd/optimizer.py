@@ -1,0 +1,500 @@
+"""Drop-in ``SCAO`` optimizer (reference: scao/optimizer.py:221-1002).
+
+Constructor arguments, the 18 per-group ``defaults`` keys, per-parameter
+state keys, the Phase 1 (Adam(W)) -> Phase 2 (blended, preconditioned Adan)
+state machine, the refresh schedule, ``state_dict`` layout, callbacks and
+presets follow the reference.  The per-parameter Python loop survives only
+as host bookkeeping (integer counters and phase flags); every tensor update
+of a step is launched by ``scao_amd.engine`` as a few batched HIP kernels
+on the current stream, with no host synchronisation in a non-refresh step.
+
+Differences a caller can observe:
+  * parameters must be on a ROCm device (``step`` raises otherwise);
+  * ``async_precond`` is accepted and ignored: the refresh runs in stream
+    order on the current stream, before the update that uses it (the
+    reference's side stream has no synchronisation, scao/optimizer.py:651-665);
+  * ``_global_norm_ema`` is kept on the device and read back on access.
+"""
+
+from __future__ import annotations
+
+import warnings
+from typing import Callable, Iterable, Optional
+
+import torch
+from torch import Tensor
+from torch.optim import Optimizer
+
+from . import engine
+from .engine import PItem, Workspace, require_hip
+from .preconditioner import SparsePreconditioner
+
+
+# --------------------------------------------------------------------------
+# v3 helpers (reference scao/optimizer.py:42-214), device tensors
+# --------------------------------------------------------------------------
+
+class _SparseGradFilter:
+    """reference :42-57.  Note torch.quantile's 2**24-element limit applies,
+    as in the reference."""
+
+    def __init__(self, sparsity: float = 0.7, ema: float = 0.99):
+        self.sparsity, self.ema, self.mag_ema = sparsity, ema, None
+
+    def __call__(self, grad: Tensor) -> Tensor:
+        mag = grad.abs().detach()
+        if self.mag_ema is None:
+            self.mag_ema = mag.clone()
+        else:
+            self.mag_ema.mul_(self.ema).add_((1.0 - self.ema) * mag)
+        thr = torch.quantile(self.mag_ema.float(), self.sparsity)
+        return grad * (self.mag_ema >= thr).to(grad.dtype)
+
+
+class _DynamicSparseFilter(_SparseGradFilter):
+    """reference :60-99."""
+
+    def __init__(self, base_sparsity=0.7, min_sparsity=0.3, max_sparsity=0.9, ema=0.99,
+                 norm_ema=0.95):
+        super().__init__(sparsity=base_sparsity, ema=ema)
+        self.base_sparsity, self.min_sparsity, self.max_sparsity = base_sparsity, min_sparsity, max_sparsity
+        self.norm_ema_coeff = norm_ema
+        self._norm_ema = 1.0
+        self._global_norm_ema = 1.0
+
+    def set_global_norm_ref(self, v: float) -> None:
+        self._global_norm_ema = max(v, 1e-8)
+
+    def __call__(self, grad: Tensor) -> Tensor:
+        ln = float(grad.norm())
+        self._norm_ema = self.norm_ema_coeff * self._norm_ema + (1.0 - self.norm_ema_coeff) * ln
+        ratio = self._norm_ema / self._global_norm_ema
+        margin = 0.2 * (1.0 - min(ratio, 2.0) / 2.0)
+        self.sparsity = float(max(self.min_sparsity, min(self.max_sparsity, self.base_sparsity + margin)))
+        return super().__call__(grad)
+
+
+class _AdaptiveWarmupScheduler:
+    """reference :106-154."""
+
+    def __init__(self, warmup_steps=100, stability_threshold=0.05, patience=5, min_warmup=20):
+        self.warmup_steps, self.stability_threshold = warmup_steps, stability_threshold
+        self.patience, self.min_warmup = patience, min_warmup
+        self._prev_norm = float("inf")
+        self._stable_count = 0
+        self._early_exit_step: Optional[int] = None
+
+    def update(self, step: int, avg_grad_norm: float) -> bool:
+        if step < self.min_warmup:
+            return True
+        if self._prev_norm > 0:
+            rel = abs(avg_grad_norm - self._prev_norm) / (self._prev_norm + 1e-8)
+            self._stable_count = self._stable_count + 1 if rel < self.stability_threshold else 0
+        self._prev_norm = avg_grad_norm
+        if self._stable_count >= self.patience:
+            self._early_exit_step = self._early_exit_step or step
+            return False
+        return step < self.warmup_steps
+
+    @property
+    def exited_early(self) -> bool:
+        return self._early_exit_step is not None
+
+    @property
+    def actual_warmup_steps(self) -> int:
+        return self._early_exit_step or self.warmup_steps
+
+
+class _LazyPrecondTrigger:
+    """reference :182-214."""
+
+    def __init__(self, delta_threshold: float = 0.1, max_skip: int = 50):
+        self.delta_threshold, self.max_skip = delta_threshold, max_skip
+        self._prev_grad_norm = 0.0
+        self._steps_since_update = 0
+
+    def should_update(self, grad_norm: float) -> bool:
+        self._steps_since_update += 1
+        if self._steps_since_update >= self.max_skip:
+            self._steps_since_update = 0
+            self._prev_grad_norm = grad_norm
+            return True
+        if self._prev_grad_norm > 0:
+            rel = abs(grad_norm - self._prev_grad_norm) / (self._prev_grad_norm + 1e-8)
+            if rel > self.delta_threshold:
+                self._steps_since_update = 0
+                self._prev_grad_norm = grad_norm
+                return True
+        self._prev_grad_norm = grad_norm
+        return False
+
+
+# --------------------------------------------------------------------------
+# SCAO
+# --------------------------------------------------------------------------
+
+class SCAO(Optimizer):
+    """Sparse Curvature-Aware Adaptive Optimizer on MI355X (drop-in for scao.SCAO)."""
+
+    def __init__(self, params: Iterable, lr: float = 1e-3, betas: tuple = (0.9, 0.999),
+                 eps: float = 1e-8, weight_decay: float = 0.01, precond_freq: int = 20,
+                 epsilon_sparse: float = 0.05, k_min: int = 8, k_max: int = 128,
+                 rho: float = 0.999, tau: float | None = 1.0, warmup_steps: int = 100,
+                 blend_steps: int = 50, min_precond_updates: int = 10,
+                 max_precond_dim: int = 4096, use_newton_schulz: bool = False,
+                 use_int8_ema: bool = False, async_precond: bool = True, beta3: float = 0.99,
+                 sparsity: float = 0.7, noise_std_init: float = 0.01,
+                 noise_anneal: float = 0.998, lars_coeff: float = 1e-3, lookahead_k: int = 5,
+                 lookahead_alpha: float = 0.5, dynamic_sparsity: bool = False,
+                 adaptive_warmup: bool = False, warmup_stability_threshold: float = 0.05,
+                 warmup_patience: int = 5, lazy_precond: bool = False,
+                 lazy_delta_threshold: float = 0.1, lazy_max_skip: int = 50,
+                 use_gsnr_clip: bool = False, gsnr_threshold: float = 0.5,
+                 adaptive_rank: bool = False) -> None:
+        # reference :297-304
+        if lr < 0:
+            raise ValueError(f"Invalid lr: {lr}")
+        if not (0.0 <= betas[0] < 1.0):
+            raise ValueError(f"Invalid beta1: {betas[0]}")
+        if not (0.0 <= betas[1] < 1.0):
+            raise ValueError(f"Invalid beta2: {betas[1]}")
+        if not (0.0 <= beta3 < 1.0):
+            raise ValueError(f"Invalid beta3: {beta3}")
+        defaults = dict(lr=lr, betas=betas, eps=eps, weight_decay=weight_decay,
+                        precond_freq=precond_freq, epsilon_sparse=epsilon_sparse,
+                        k_min=k_min, k_max=k_max, rho=rho, tau=tau,
+                        warmup_steps=warmup_steps, blend_steps=blend_steps,
+                        min_precond_updates=min_precond_updates,
+                        max_precond_dim=max_precond_dim, use_newton_schulz=use_newton_schulz,
+                        use_int8_ema=use_int8_ema, beta3=beta3, lars_coeff=lars_coeff)
+        super().__init__(params, defaults)
+        self._precond_stream = None
+        self._async_precond = async_precond
+        self._callbacks: list = []
+        self._global_step = 0
+        self._noise_std = noise_std_init
+        self._noise_anneal = noise_anneal
+        self._lookahead_k = lookahead_k
+        self._lookahead_alpha = lookahead_alpha
+        self._slow_weights: dict = {}
+        self._sparsity = sparsity
+        self._dynamic_sparsity = dynamic_sparsity
+        self._sparse_filters: dict = {}
+        self._norm_ema_host = 1.0
+        self._adaptive_warmup = adaptive_warmup
+        self._warmup_scheduler = _AdaptiveWarmupScheduler(
+            warmup_steps=warmup_steps, stability_threshold=warmup_stability_threshold,
+            patience=warmup_patience, min_warmup=max(20, warmup_steps // 5))
+        self._lazy_precond = lazy_precond
+        self._lazy_triggers: dict = {}
+        self._lazy_delta_threshold = lazy_delta_threshold
+        self._lazy_max_skip = lazy_max_skip
+        self._use_gsnr_clip = use_gsnr_clip
+        self._gsnr_threshold = gsnr_threshold
+        self._adaptive_rank = adaptive_rank
+        self._in_warmup_global = True
+        self._ws: Optional[Workspace] = None
+
+    # ---------------------------------------------------------- runtime --
+    @property
+    def _global_norm_ema(self) -> float:
+        if self._ws is not None:
+            return float(self._ws.runtime[0])
+        return self._norm_ema_host
+
+    @_global_norm_ema.setter
+    def _global_norm_ema(self, v: float) -> None:
+        self._norm_ema_host = float(v)
+        if self._ws is not None:
+            self._ws.runtime[0] = float(v)
+
+    def _workspace(self, device: torch.device) -> Workspace:
+        if self._ws is None:
+            self._ws = Workspace(device)
+            self._ws.runtime[0] = self._norm_ema_host
+        elif self._ws.device != device:
+            raise RuntimeError("scao_amd.SCAO: all parameters must be on one device "
+                               f"({self._ws.device} vs {device})")
+        return self._ws
+
+    # ------------------------------------------------------- lookahead ---
+    @torch.no_grad()
+    def _lookahead_sync(self) -> None:
+        """reference :356-365."""
+        for g in self.param_groups:
+            for p in g["params"]:
+                pid = id(p)
+                if pid not in self._slow_weights:
+                    self._slow_weights[pid] = p.data.clone()
+                slow = self._slow_weights[pid]
+                slow.add_(self._lookahead_alpha * (p.data - slow))
+                p.data.copy_(slow)
+
+    # ------------------------------------------------------------ rank ---
+    def _maybe_adjust_rank(self, pre: SparsePreconditioner, grad_norm: float, group: dict) -> None:
+        """reference :383-401."""
+        if not self._adaptive_rank:
+            return
+        ratio = grad_norm / (self._global_norm_ema + 1e-8)
+        cur = pre.k
+        if ratio > 2.0:
+            nk = min(group["k_max"], int(cur * 1.25))
+        elif ratio < 0.5:
+            nk = max(group["k_min"], int(cur * 0.8))
+        else:
+            return
+        if nk != cur:
+            pre.k = nk
+
+    # ------------------------------------------------------------ state --
+    def _init_state(self, p: Tensor, group: dict) -> None:
+        """reference :407-433."""
+        st = self.state[p]
+        if len(st) > 0:
+            return
+        st["step"] = 0
+        st["scao_step"] = 0
+        for key in ("exp_avg", "exp_avg_sq", "exp_avg_diff", "prev_grad"):
+            st[key] = torch.zeros_like(p, dtype=torch.float32, memory_format=torch.contiguous_format)
+        st["preconditioner"] = self._make_precond(p, group)
+
+    @staticmethod
+    def _make_precond(p: Tensor, group: dict) -> SparsePreconditioner:
+        return SparsePreconditioner(
+            param=p, epsilon_sparse=group["epsilon_sparse"], k_min=group["k_min"],
+            k_max=group["k_max"], rho=group["rho"], max_precond_dim=group["max_precond_dim"],
+            use_newton_schulz=group["use_newton_schulz"], use_int8_ema=group["use_int8_ema"])
+
+    # ------------------------------------------------------------- step --
+    @torch.no_grad()
+    def step(self, closure: Callable | None = None) -> Tensor | None:
+        """reference :452-503 (host bookkeeping) + one batched engine launch."""
+        loss = None
+        if closure is not None:
+            with torch.enable_grad():
+                loss = closure()
+        self._global_step += 1
+        active = [(g, p) for g in self.param_groups for p in g["params"] if p.grad is not None]
+        for _, p in active:
+            require_hip(p, "parameter")
+        device = active[0][1].device if active else None
+        ws = self._workspace(device) if device is not None else self._ws
+        host_norms = (self._dynamic_sparsity or self._adaptive_warmup or self._adaptive_rank
+                      or self._lazy_precond)
+        avg = 0.0
+        if host_norms and active:
+            norms = [float(p.grad.norm()) for _, p in active]
+            avg = sum(norms) / len(norms)
+            self._global_norm_ema = 0.95 * self._global_norm_ema + 0.05 * avg
+        if self._dynamic_sparsity:
+            ref = self._global_norm_ema
+            for f in self._sparse_filters.values():
+                if isinstance(f, _DynamicSparseFilter):
+                    f.set_global_norm_ref(ref)
+        if self._adaptive_warmup:
+            self._in_warmup_global = self._warmup_scheduler.update(self._global_step, avg)
+        else:
+            wmax = max((g.get("warmup_steps", 100) for g in self.param_groups), default=100)
+            self._in_warmup_global = self._global_step <= wmax
+
+        items, refresh = [], []
+        for group, p in active:
+            it = self._plan_param(group, p, refresh)
+            items.append(it)
+        engine.refresh(refresh)
+        gsnr = self._gsnr_threshold if self._use_gsnr_clip else None
+        if ws is not None:
+            engine.run_step(items, ws, update_norm_ema=not host_norms, gsnr=gsnr)
+
+        self._noise_std *= self._noise_anneal
+        if self._lookahead_k > 0 and self._global_step % self._lookahead_k == 0:
+            self._lookahead_sync()
+        if self._callbacks:
+            from .logging import collect_metrics
+            metrics = collect_metrics(self)
+            metrics["noise_std"] = self._noise_std
+            metrics["global_norm_ema"] = self._global_norm_ema
+            metrics["warmup_active"] = self._in_warmup_global
+            for cb in self._callbacks:
+                cb(metrics)
+        return loss
+
+    def _plan_param(self, group: dict, p: Tensor, refresh: list) -> PItem:
+        """Host half of reference _step_group (:521-605) for one parameter."""
+        if p.grad.is_sparse:
+            raise RuntimeError("SCAO does not support sparse gradients.")
+        if not p.is_contiguous():
+            raise RuntimeError("scao_amd.SCAO needs contiguous parameters")
+        self._init_state(p, group)
+        st = self.state[p]
+        st["step"] += 1
+        t = st["step"]
+        pid = id(p)
+        graw = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
+        need_gnorm = self._lazy_precond or self._adaptive_rank
+        gnorm = float(graw.float().norm()) if need_gnorm else 0.0
+        gmom = None
+        if self._sparsity > 0.0 or self._noise_std > 1e-9:
+            grad = graw.float()
+            if self._sparsity > 0.0:
+                if pid not in self._sparse_filters:
+                    self._sparse_filters[pid] = (_DynamicSparseFilter(base_sparsity=self._sparsity)
+                                                 if self._dynamic_sparsity
+                                                 else _SparseGradFilter(self._sparsity))
+                grad = self._sparse_filters[pid](grad)
+            if self._noise_std > 1e-9:
+                grad = grad + torch.randn_like(grad) * self._noise_std
+            gmom = grad.contiguous()
+        pre: SparsePreconditioner = st["preconditioner"]
+        self._maybe_adjust_rank(pre, gnorm, group)
+        in_warmup = (self._in_warmup_global if self._adaptive_warmup
+                     else (t <= group["warmup_steps"])) or \
+            (pre.precond_step < group["min_precond_updates"])
+        if in_warmup:
+            if t % group["precond_freq"] == 0:
+                refresh.append((pre, p.grad))
+            return PItem(p=p, graw=graw, gmom=gmom, st=st, group=group, pre=pre,
+                         phase2=False, step=t)
+        if not st.get("scao_phase_started", False):
+            st["scao_phase_started"] = True
+            st["phase2_start_step"] = t
+            st["scao_step"] = 0
+        st["scao_step"] += 1
+        if self._lazy_precond:
+            if pid not in self._lazy_triggers:
+                self._lazy_triggers[pid] = _LazyPrecondTrigger(self._lazy_delta_threshold,
+                                                               self._lazy_max_skip)
+            should = self._lazy_triggers[pid].should_update(gnorm)
+        else:
+            should = t % group["precond_freq"] == 0
+        if should:
+            refresh.append((pre, p.grad))
+        diag = not (pre.use_block_diagonal or pre.use_kronecker)
+        return PItem(p=p, graw=graw, gmom=gmom, st=st, group=group, pre=pre, phase2=True,
+                     step=t, scao_step=st["scao_step"], lars=group["lars_coeff"] > 0,
+                     diag=diag, leaves=[] if diag else list(pre.leaves()))
+
+    # ------------------------------------------------------------ misc ---
+    def synchronize_precond(self) -> None:
+        """reference :680-684.  The refresh runs on the current stream, in
+        order; there is no side stream to wait for."""
+
+    def sync_preconditioner(self, process_group=None) -> None:
+        """reference :686-710 (broadcast from rank 0).  Single-GPU build:
+        a no-op with a warning when torch.distributed is not initialised."""
+        import torch.distributed as dist
+        if not dist.is_available() or not dist.is_initialized():
+            warnings.warn("sync_preconditioner() called but distributed is not initialised.",
+                          RuntimeWarning, stacklevel=2)
+            return
+        if dist.get_world_size(group=process_group) == 1:
+            return
+        raise NotImplementedError("scao_amd is a single-GPU build: multi-rank preconditioner "
+                                  "broadcast is not provided")
+
+    def add_callback(self, callback) -> None:
+        self._callbacks.append(callback)
+
+    def remove_callback(self, callback) -> None:
+        try:
+            self._callbacks.remove(callback)
+        except ValueError:
+            pass
+
+    def clear_callbacks(self) -> None:
+        self._callbacks.clear()
+
+    def state_dict(self) -> dict:
+        """reference :732-756."""
+        self.synchronize_precond()
+        base = super().state_dict()
+        base["_scao_precond"] = {idx: st["preconditioner"].state_dict()
+                                 for idx, st in enumerate(self.state.values())
+                                 if "preconditioner" in st}
+        ws = self._warmup_scheduler
+        base["_scao_runtime"] = {
+            "global_step": self._global_step, "noise_std": self._noise_std,
+            "global_norm_ema": self._global_norm_ema, "warmup_prev_norm": ws._prev_norm,
+            "warmup_stable_count": ws._stable_count,
+            "warmup_early_exit_step": ws._early_exit_step}
+        return base
+
+    def load_state_dict(self, state_dict: dict) -> None:
+        """reference :758-776.  Preconditioner objects of another type (the
+        reference's, or the CPU oracle's) are rebuilt from the parameter and
+        its group before the portable ``_scao_precond`` entry is loaded."""
+        sd = dict(state_dict)
+        extra = sd.pop("_scao_precond", {})
+        rt = sd.pop("_scao_runtime", {})
+        super().load_state_dict(sd)
+        owner = {id(p): g for g in self.param_groups for p in g["params"]}
+        for idx, (p, st) in enumerate(self.state.items()):
+            if "preconditioner" in st and not isinstance(st["preconditioner"], SparsePreconditioner):
+                st["preconditioner"] = self._make_precond(p, owner[id(p)])
+            elif "preconditioner" in st and st["preconditioner"].device != p.device:
+                st["preconditioner"] = self._make_precond(p, owner[id(p)])
+            if idx in extra and "preconditioner" in st:
+                st["preconditioner"].load_state_dict(extra[idx])
+        if rt:
+            self._global_step = int(rt.get("global_step", self._global_step))
+            self._noise_std = float(rt.get("noise_std", self._noise_std))
+            self._global_norm_ema = float(rt.get("global_norm_ema", self._global_norm_ema))
+            ws = self._warmup_scheduler
+            ws._prev_norm = float(rt.get("warmup_prev_norm", ws._prev_norm))
+            ws._stable_count = int(rt.get("warmup_stable_count", ws._stable_count))
+            ws._early_exit_step = rt.get("warmup_early_exit_step", ws._early_exit_step)
+        if self._ws is not None:
+            self._ws.struct_key = None
+
+    def current_ranks(self) -> dict:
+        """reference :782-787."""
+        return {idx: st["preconditioner"].k for idx, st in enumerate(self.state.values())
+                if "preconditioner" in st}
+
+    def precond_stats(self) -> dict:
+        """reference :789-801."""
+        ks = list(self.current_ranks().values())
+        if not ks:
+            return {}
+        return {"num_precond_layers": len(ks), "rank_min": min(ks), "rank_max": max(ks),
+                "rank_mean": sum(ks) / len(ks), "global_norm_ema": self._global_norm_ema,
+                "warmup_exited_early": self._warmup_scheduler.exited_early,
+                "actual_warmup_steps": self._warmup_scheduler.actual_warmup_steps}
+
+
+# --------------------------------------------------------------------------
+# presets (the definitions in effect in the reference, scao/optimizer.py:958-1002)
+# --------------------------------------------------------------------------
+
+def _params_of(x):
+    return x.parameters() if hasattr(x, "parameters") else x
+
+
+def scao_sub1b(model_or_params, lr=1e-3, **kwargs):
+    return SCAO(_params_of(model_or_params), lr=lr, k_max=64, use_int8_ema=False, **kwargs)
+
+
+def scao_1b(model_or_params, lr=1e-3, **kwargs):
+    return SCAO(_params_of(model_or_params), lr=lr, k_max=48, use_int8_ema=True,
+                async_precond=True, **kwargs)
+
+
+def scao_3b(model_or_params, lr=3e-4, **kwargs):
+    return SCAO(_params_of(model_or_params), lr=lr, k_max=32, use_int8_ema=True,
+                async_precond=True, warmup_steps=20, blend_steps=10, **kwargs)
+
+
+def scao_7b(model_or_params, lr=1e-4, **kwargs):
+    return SCAO(_params_of(model_or_params), lr=lr, k_max=24, use_int8_ema=True,
+                async_precond=False, dynamic_sparsity=False, **kwargs)
+
+
+def scao_40b(model_or_params, lr=1e-4, **kwargs):
+    return SCAO(_params_of(model_or_params), lr=lr, k_max=16, use_int8_ema=True,
+                async_precond=True, lazy_precond=True, use_gsnr_clip=True, **kwargs)
+
+
+def scao_125b(model_or_params, lr=5e-5, **kwargs):
+    return SCAO(_params_of(model_or_params), lr=lr, k_max=8, use_int8_ema=True,
+                async_precond=True, lazy_precond=True, lazy_max_skip=100, use_gsnr_clip=True,
+                adaptive_rank=True, **kwargs)

@@ -1,0 +1,59 @@
+"""The C-ABI library: builds, loads without a GPU, exports every symbol the
+header declares, and its struct layouts match the Python mirrors."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "scao_amd.h")
+
+
+def _declared():
+    txt = open(HEADER).read()
+    txt = re.sub(r"/\*.*?\*/", "", txt, flags=re.S)
+    return sorted(set(re.findall(r"\b(scao_[a-z0-9_]+)\s*\(", txt)))
+
+
+def test_library_exports_every_declared_symbol():
+    from scao_amd import _lib as L
+    lib = L.lib()
+    names = _declared()
+    assert len(names) >= 15
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in scao_amd.h but not exported"
+        assert n in L.SIGNATURES, f"{n} has no ctypes signature"
+    assert sorted(L.SIGNATURES) == names
+
+
+def test_abi_version_and_layouts():
+    from scao_amd import _lib as L
+    lib = L.lib()
+    assert lib.scao_abi_version() == L.ABI_VERSION
+    L.check_layout(lib)
+
+
+def test_error_path_without_gpu():
+    """Argument validation runs on the host: bad shapes are rejected with a
+    message before anything touches a device."""
+    from scao_amd import _lib as L
+    lib = L.lib()
+    rc = lib.scao_fused_kronecker_precond(None, None, None, None, None, 0, None, 0, 0, 0, None, None)
+    assert rc == 1
+    assert b"null pointer" in lib.scao_last_error()
+    assert lib.scao_fused_kronecker_workspace(10, 20, 4) == (4 * 20 + 16 + 10 * 4) * 4
+    assert lib.scao_int8_ema_scratch_bytes(5000) == (5000 + 2) * 4
+    with pytest.raises(L.ScaoLibError):
+        L.call("scao_kron_project", None, -1, None, None, None, None)
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    from scao_amd import _lib as L
+    monkeypatch.setattr(L, "LIB_PATH", str(tmp_path / "nope.so"))
+    monkeypatch.setattr(L, "_lib", None)
+    with pytest.raises(L.ScaoLibError, match="no CPU or torch fallback"):
+        L.lib()

@@ -1,0 +1,175 @@
+"""Host logic that needs no GPU: preconditioner construction and state layout
+against the oracle, constructor validation, the no-CPU-path guard, task
+and slot bookkeeping of the batched engine, and a planted-mistake check that
+the golden fixtures would catch an oracle slip."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import scao_amd
+from oracle import scao_ref as R
+from scao_amd import SparsePreconditioner
+from scao_amd import engine as E
+
+SHAPES = [(64, 64), (128, 16), (16, 128), (300, 64), (64, 300), (5000, 4100), (4, 3, 2, 2),
+          (20,), (1, 50), (50, 1), (2049, 700), (3, 3)]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+@pytest.mark.parametrize("int8", [False, True])
+def test_precond_construction_matches_oracle(shape, int8):
+    kw = dict(k_min=8, k_max=128, max_precond_dim=64 if max(shape) < 1000 else 4096,
+              use_int8_ema=int8)
+    p = torch.zeros(shape)
+    a, b = R.RefPreconditioner(p, **kw), SparsePreconditioner(p, **kw)
+    _same_tree(a, b)
+
+
+def _same_tree(a, b):
+    for attr in ("m", "n", "k_min", "k_max", "use_block_diagonal", "use_kronecker",
+                 "precond_step", "_k", "use_int8_ema"):
+        assert getattr(a, attr) == getattr(b, attr), attr
+    if a.use_block_diagonal:
+        assert a._block_sizes == b._block_sizes and a._block_dim == b._block_dim
+        for x, y in zip(a._blocks, b._blocks):
+            _same_tree(x, y)
+    elif a.use_kronecker:
+        for t in ("U_l", "S_l", "U_r", "S_r"):
+            assert torch.equal(getattr(a, t), getattr(b, t)), t
+        if a.use_int8_ema:
+            assert torch.equal(a.L_ema_q, b.L_ema_q) and torch.equal(a.R_ema_q, b.R_ema_q)
+            assert a.L_ema_scale == b.L_ema_scale and a.R_ema_scale == b.R_ema_scale
+        else:
+            assert torch.equal(a.L_ema, b.L_ema) and torch.equal(a.R_ema, b.R_ema)
+    else:
+        assert torch.equal(a.diag_ema, b.diag_ema)
+        assert a._diag_bias_factor == b._diag_bias_factor
+    assert a.memory_bytes() == b.memory_bytes()
+    sa, sb = a.state_dict(), b.state_dict()
+    assert _skeleton(sa) == _skeleton(sb)
+
+
+def _skeleton(d):
+    return {k: ([_skeleton(x) for x in v] if k == "blocks" else
+                (tuple(v.shape), str(v.dtype)) if isinstance(v, torch.Tensor) else v)
+            for k, v in d.items()}
+
+
+def test_leaves_tile_the_parameter():
+    """Block-diagonal leaves cover the 2-D view exactly once (recursive split)."""
+    for shape, D in [((5000, 4100), 4096), ((2048, 8192), 2048), ((128256, 2048), 2048),
+                     ((11008, 2048), 2048), ((300, 64), 64)]:
+        pre = SparsePreconditioner(torch.zeros(shape), max_precond_dim=D)
+        cover = np.zeros(shape, dtype=np.int32)
+        for leaf, r0, c0 in pre.leaves():
+            assert leaf.use_kronecker and max(leaf.m, leaf.n) <= D
+            cover[r0:r0 + leaf.m, c0:c0 + leaf.n] += 1
+        assert (cover == 1).all(), shape
+
+
+def test_precond_k_setter_matches_oracle():
+    p = torch.zeros(96, 80)
+    a = R.RefPreconditioner(p, k_min=4, k_max=32, max_precond_dim=64)
+    b = SparsePreconditioner(p, k_min=4, k_max=32, max_precond_dim=64)
+    for k in (2, 40, 6, 3, 100):
+        a.k, b.k = k, k
+        _same_tree(a, b)
+
+
+def test_constructor_validation_and_defaults():
+    m = torch.nn.Linear(8, 4)
+    with pytest.raises(ValueError):
+        scao_amd.SCAO(m.parameters(), lr=-1e-3)
+    with pytest.raises(ValueError):
+        scao_amd.SCAO(m.parameters(), betas=(1.0, 0.999))
+    with pytest.raises(ValueError):
+        scao_amd.SCAO(m.parameters(), betas=(0.9, 1.0))
+    with pytest.raises(ValueError):
+        scao_amd.SCAO(m.parameters(), beta3=1.0)
+    a = scao_amd.SCAO(m.parameters())
+    b = R.RefSCAO(torch.nn.Linear(8, 4).parameters())
+    assert a.defaults == b.defaults
+    assert len(a.defaults) == 18
+    assert a._callbacks == []
+
+
+def test_step_on_cpu_raises():
+    m = torch.nn.Linear(8, 4)
+    opt = scao_amd.SCAO(m.parameters(), warmup_steps=0)
+    m(torch.randn(2, 8)).sum().backward()
+    with pytest.raises(RuntimeError, match="ROCm"):
+        opt.step()
+
+
+def test_presets_construct():
+    m = torch.nn.Linear(16, 8)
+    for f in (scao_amd.scao_sub1b, scao_amd.scao_1b, scao_amd.scao_3b, scao_amd.scao_7b,
+              scao_amd.scao_40b, scao_amd.scao_125b):
+        opt = f(m)
+        assert isinstance(opt, scao_amd.SCAO)
+    assert scao_amd.scao_1b(m).defaults["k_max"] == 48
+    assert scao_amd.scao_125b(m)._adaptive_rank
+
+
+def test_engine_slots_cover_each_once():
+    from scao_amd.engine import PItem
+    items = []
+    for i, shp in enumerate([(2048, 8192), (512, 2048), (2048,), (100, 37), (130, 70)]):
+        p = torch.zeros(shp)
+        pre = SparsePreconditioner(p, k_min=16, k_max=80, max_precond_dim=2048,
+                                   use_int8_ema=True)
+        diag = not (pre.use_block_diagonal or pre.use_kronecker)
+        items.append(PItem(p=p, graw=p, gmom=None, st={}, group={}, pre=pre, phase2=i != 3,
+                           step=3, lars=i % 2 == 0, diag=diag,
+                           leaves=[] if diag else list(pre.leaves())))
+    arrays, ranges, nslots, leaves = E._build_structure(items)
+    writes = np.zeros(nslots, int)
+    for a in arrays.values():
+        for t in a:
+            if t["slot"] >= 0:
+                writes[t["slot"]] += 1
+    assert (writes == 1).all()
+    prev_end = 0
+    for (pb, pe, qb, qe) in ranges:
+        assert pb == prev_end and pb <= pe == qb <= qe
+        prev_end = qe
+    assert prev_end == nslots
+    # every Phase-2 LARS param gets write-back tasks covering its numel
+    for i, it in enumerate(items):
+        n = sum(1 for t in arrays["lars"] if t["idx"] == i)
+        assert n == (E._flat_chunks(it.p.numel()) if it.phase2 and it.lars else 0)
+
+
+def test_golden_catches_planted_oracle_mistake(monkeypatch):
+    """Drop the '-1' of the projection correction in the oracle: the golden
+    trajectory must then fail."""
+    from scao_inputs import config_from_meta, grads_for_step, load_golden
+    T, meta = load_golden("traj_int8")
+
+    def wrong(U_l, s_l, U_r, s_r, G):
+        P = (U_l.T @ G) @ U_r
+        return G + U_l @ ((s_l[:, None] * s_r[None, :]) * P) @ U_r.T
+
+    monkeypatch.setattr(R, "fused_kronecker_precond", wrong)
+    names = meta["names"]
+    shapes = {k: tuple(meta["shapes"][k]) for k in names}
+    params = {k: torch.nn.Parameter(T[f"init.{k}"].clone()) for k in names}
+    opt = R.RefSCAO(list(params.values()), **config_from_meta(meta))
+    from test_oracle_golden import UPD_TOL, update_err
+    worst = 0.0
+    for t in range(1, meta["steps"] + 1):
+        gr = grads_for_step(t, shapes)
+        for k, p in params.items():
+            p.grad = gr[k].clone()
+        before = {k: p.detach().clone() for k, p in params.items()}
+        opt.step()
+        for k, p in params.items():
+            prev = T[f"step{t - 1}.p.{k}"] if t > 1 else T[f"init.{k}"]
+            ref = T[f"step{t}.p.{k}"] - prev
+            worst = max(worst, update_err(p.detach() - before[k], ref))
+        for k, p in params.items():   # replay from the golden state, as the gate does
+            p.data.copy_(T[f"step{t}.p.{k}"])
+    assert worst > 10 * UPD_TOL, worst
