@@ -127,6 +127,8 @@ def main():
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--details", default=None, help="write the full report JSON here")
+    ap.add_argument("--dominant", default="scao_kron_apply",
+                    help="entry point timed with HIP events inside the timed region")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -187,21 +189,33 @@ def main():
         g["precond_freq"] = 10 ** 9           # steady state: no refresh in the timed region
     for _ in range(args.warmup):
         one()
-    torch.cuda.synchronize()
-    engine.TIMING = {}
+    # timed region: HIP events only around the dominant kernel's launches
+    engine.TIMING, engine.TIMING_ONLY = {}, {args.dominant}
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
         one()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    dom_timing = engine.timing_summary()
+    ms = wall * 1e3 / args.steps
+    # diagnostic pass (not the headline): events around every launch
+    engine.TIMING, engine.TIMING_ONLY = {}, None
+    diag_steps = max(2, min(5, args.steps))
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    for _ in range(diag_steps):
+        one()
+    torch.cuda.synchronize()
+    ms_instrumented = (time.perf_counter() - t1) * 1e3 / diag_steps
     per_kernel = engine.timing_summary()
     engine.TIMING = None
-    ms = wall * 1e3 / args.steps
     assert all(opt.state[p].get("scao_phase_started") for p in pre_p), "not in Phase 2"
 
     # ---- roofline of the dominant kernel --------------------------------
-    dom = max(per_kernel, key=lambda k: per_kernel[k][2])
+    dom = args.dominant
+    if dom not in dom_timing:
+        raise SystemExit(f"bench.py: {dom} was not launched in the timed region")
     n_leaf = [lf for s in (s for _, s in pre_shapes) for lf in leaves_of(s, cfg["D"])]
     k = cfg["k"]
     flops_proj = sum(2 * m * n * k for m, n in n_leaf)          # T = U_l^T G per step
@@ -213,7 +227,7 @@ def main():
         "scao_kron_project": ("mfma", float(flops_proj)),
     }
     bound, work = alg.get(dom, ("hbm", 0.0))
-    avg_s = per_kernel[dom][1] / 1e3
+    avg_s = dom_timing[dom][1] / 1e3
     achieved = work / avg_s if avg_s > 0 else 0.0
     peak = HBM_PEAK if bound == "hbm" else FP32_MFMA_PEAK
     roof = {"kernel": dom, "bound": bound,
@@ -221,14 +235,15 @@ def main():
             "peak": peak / (1e9 if bound == "hbm" else 1e12),
             "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
             "frac": achieved / peak, "traffic": None,
-            "avg_ms": per_kernel[dom][1]}
+            "avg_ms": dom_timing[dom][1]}
     step_bytes = 44.0 * n_pre + 32.0 * (nparams - n_pre)
     step_flops = sum(proj_flops(m, n, k) for m, n in n_leaf)
 
     details = {
-        "per_kernel_ms": {k: {"count": c, "mean": m_, "total_per_step": t / args.steps}
+        "per_kernel_ms": {k: {"count": c, "mean": m_, "total_per_step": t / diag_steps}
                           for k, (c, m_, t) in per_kernel.items()},
         "steady_step_ms": ms,
+        "instrumented_step_ms": ms_instrumented,
         "phase1_step_ms": t_phase1,
         "refresh_step_ms": t_refresh,
         "refresh_parts_ms": {k: {"count": c, "mean": m_, "total": t}

@@ -51,6 +51,7 @@ enum scao_dtype { SCAO_F32 = 0, SCAO_BF16 = 1, SCAO_F16 = 2 };
 #define SCAO_PF_DIAG  16 /* diagonal-mode preconditioner (1-D or degenerate 2-D)    */
 #define SCAO_PF_NORM  32 /* accumulate ||g||^2 for the global grad-norm EMA         */
 #define SCAO_PF_GF32  64 /* `g` is a float32 buffer (filtered/noised gradient)     */
+#define SCAO_PF_ALIGNED 128 /* every pointer of the param is 16-byte aligned       */
 
 /* One parameter of a batched step.  Scalars arrive already rounded the way
  * the reference rounds a Python float meeting a float32 tensor. */
@@ -157,9 +158,12 @@ int scao_int8_ema_update(int8_t* q, double scale_in, const float* new_val, doubl
 
 /* ---- batched step: Phase 2 (preconditioned Adan) ---------------------- */
 /* A1  T = U_l^T G for (leaf, 256-column strip, 64-row chunk of T); also
- *     ||g||^2 and ||p*decay||^2 partials into slots (chunk 0 only). */
+ *     ||g||^2 (chunk 0) and ||p*decay||^2 (chunk 0 of LARS params) into slots.
+ *     variant = (fast ? 1 : 0) | (p norm ? 2 : 0): "fast" tasks promise fp32
+ *     data, SCAO_LF_VEC4, a full 256-column strip, a full 64-row chunk of T
+ *     and m % 32 == 0; "p norm" tasks are the chunk-0 tasks of LARS params. */
 int scao_kron_project(const scao_task* tasks, int ntasks, const scao_leaf_desc* leaves,
-                      const scao_param_desc* params, double* slots, void* stream);
+                      const scao_param_desc* params, double* slots, int variant, void* stream);
 /* A2  P = T U_r, Delta = (s_l s_r^T - 1) P and nu^2 partial per 64x64 tile of P. */
 int scao_kron_delta(const scao_task* tasks, int ntasks, const scao_leaf_desc* leaves,
                     const scao_param_desc* params, double* slots, void* stream);
@@ -176,10 +180,14 @@ int scao_step_finalize(const scao_param_desc* params, int nparams, const double*
                        scao_param_stat* stat, double* runtime, int phase,
                        int update_norm_ema, int norm_count, void* stream);
 /* B   G + W U_r^T -> clip -> blend -> Adan moments -> update; writes the
- *     update to upd (LARS params, ||u||^2 into slots) or the parameter. */
+ *     update to upd (LARS params, ||u||^2 into slots) or the parameter.
+ *     variant = (SCAO_PF_GF32 set ? 1 : 0) | (SCAO_PF_LARS set ? 2 : 0) |
+ *     (fast ? 4 : 0); every task of a launch must belong to a parameter of
+ *     that variant.  "fast" tasks promise fp32 data, SCAO_LF_VEC4,
+ *     SCAO_PF_ALIGNED, a full 64x64 tile and k % 16 == 0. */
 int scao_kron_apply(const scao_task* tasks, int ntasks, const scao_leaf_desc* leaves,
                     const scao_param_desc* params, const scao_param_stat* stat,
-                    double* slots, void* stream);
+                    double* slots, int variant, void* stream);
 int scao_diag_apply(const scao_task* tasks, int ntasks, const scao_param_desc* params,
                     const scao_param_stat* stat, double* slots, void* stream);
 /* C   p = fma(upd, alpha, p*decay) for LARS params. */

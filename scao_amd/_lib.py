@@ -29,7 +29,8 @@ APPLY_TILE = 64
 GRAM_TILE = 128
 
 F32, BF16, F16 = 0, 1, 2
-PF_DECAY, PF_LARS, PF_CLIP, PF_GSNR, PF_DIAG, PF_NORM, PF_GF32 = 1, 2, 4, 8, 16, 32, 64
+PF_DECAY, PF_LARS, PF_CLIP, PF_GSNR, PF_DIAG, PF_NORM, PF_GF32, PF_ALIGNED = (
+    1, 2, 4, 8, 16, 32, 64, 128)
 LF_SINV4, LF_VEC4 = 1, 2
 
 DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
@@ -89,12 +90,12 @@ SIGNATURES = {
                                           _VP, _VP]),
     "scao_int8_ema_scratch_bytes": (_I64, [_I64]),
     "scao_int8_ema_update": (_I, [_VP, _D, _VP, _D, _I64, _VP, _VP, _VP]),
-    "scao_kron_project": (_I, [_VP, _I, _VP, _VP, _VP, _VP]),
+    "scao_kron_project": (_I, [_VP, _I, _VP, _VP, _VP, _I, _VP]),
     "scao_kron_delta": (_I, [_VP, _I, _VP, _VP, _VP, _VP]),
     "scao_kron_lift": (_I, [_VP, _I, _VP, _VP]),
     "scao_diag_reduce": (_I, [_VP, _I, _VP, _VP, _VP]),
     "scao_step_finalize": (_I, [_VP, _I, _VP, _VP, _VP, _I, _I, _I, _VP]),
-    "scao_kron_apply": (_I, [_VP, _I, _VP, _VP, _VP, _VP, _VP]),
+    "scao_kron_apply": (_I, [_VP, _I, _VP, _VP, _VP, _VP, _I, _VP]),
     "scao_diag_apply": (_I, [_VP, _I, _VP, _VP, _VP, _VP]),
     "scao_lars_write": (_I, [_VP, _I, _VP, _VP, _VP]),
     "scao_adam_step": (_I, [_VP, _I, _VP, _VP, _VP]),

@@ -27,24 +27,45 @@ namespace {
 
 // ----------------------------------------------------------- project ---
 // T[c0:c0+64, j0:j0+256] = U_l^T G over all m rows.  Wave w owns 64 columns.
-// Chunk 0 tasks also reduce ||g||^2 and ||p*decay||^2 over their columns.
-__device__ __forceinline__ void project_tile(const scao_leaf_desc& L, const scao_param_desc& P, int j0,
-                             int c0, int slot, double* slots) {
+// Rows are consumed in chunks of PR=32: each chunk of G (32 x 256) and U_l
+// (32 x 64) is loaded into registers one chunk ahead (coalesced float4: one
+// wave reads one 1 KB row of G), written to LDS, and all four waves run 128
+// MFMAs on it.  Chunk-0 tasks also reduce ||g||^2 and ||p*decay||^2 from the
+// staged registers (every element of the strip passes through exactly one
+// thread).
+constexpr int PR = 32;           // rows per chunk
+constexpr int GP = SCAO_PROJ_COLS + 4;  // LDS pitch of the G chunk
+constexpr int UP = 64 + 4;       // LDS pitch of the U_l chunk
+
+template <bool FAST, bool DO_P>
+__device__ __forceinline__ void project_tile(const scao_leaf_desc& L, const scao_param_desc& P,
+                                             int j0, int c0, int slot, double* slots) {
+  __shared__ __attribute__((aligned(16))) float Gs[PR][GP];
+  __shared__ __attribute__((aligned(16))) float Us[PR][UP];
   __shared__ double red[16];
-  const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+  const int tid = threadIdx.x;
+  const int w = tid / 64, l = tid % 64;
   const int m = L.m, n = L.n, k = L.k;
   const int64_t ld = L.ld;
-  const int dt = P.dtype;
-  const int jl = j0 + 64 * w + 4 * (l % 16);
+  const int dt = FAST ? SCAO_F32 : P.dtype;
   const int kk = l / 16;
-  const int cl = c0 + (l % 16);
-  int cmask = 0;
-  for (int t = 0; t < 4; ++t) cmask |= (jl + t < n) ? (1 << t) : 0;
-  const bool vec = (L.flags & SCAO_LF_VEC4) && cmask == 15;
   const bool do_norms = (c0 == 0) && slot >= 0;
-  const bool do_p = do_norms && (P.flags & SCAO_PF_LARS);
+  constexpr bool do_p = DO_P;
   const bool decay = P.flags & SCAO_PF_DECAY;
-  const float* Ul = L.Ul;
+  const bool gvec_leaf = FAST || (L.flags & SCAO_LF_VEC4) != 0;
+  const bool kvec = FAST || (k % 4) == 0;
+
+  // loader geometry (fixed per thread): G row gr_h = idx/64, 4 columns at gc
+  const int gc = (tid % 64) * 4;         // column offset inside the strip
+  int gmask = 15;
+  if (!FAST)
+    for (int t = 0; t < 4; ++t) gmask = (j0 + gc + t < n) ? gmask : (gmask & ~(1 << t));
+  const bool gvec = gvec_leaf && gmask == 15;
+  const int uc = (tid % 16) * 4;         // c offset inside the 64-wide chunk
+  int umask = 15;
+  if (!FAST)
+    for (int t = 0; t < 4; ++t) umask = (c0 + uc + t < k) ? umask : (umask & ~(1 << t));
+  const bool uvec = kvec && umask == 15;
 
   v4f acc[4][4];
 #pragma unroll
@@ -53,77 +74,83 @@ __device__ __forceinline__ void project_tile(const scao_leaf_desc& L, const scao
     for (int t = 0; t < 4; ++t) acc[q][t] = v4f{0.f, 0.f, 0.f, 0.f};
   double g2 = 0.0, p2 = 0.0;
 
-  // two-stage register pipeline over 16-row groups
-  v4f bq[4], bn[4];
-  float aq[4][4], an[4][4];
+  v4f rg[8], ru[2], rp[8];
+  auto load_chunk = [&](int i0) {
 #pragma unroll
-  for (int s = 0; s < 4; ++s) {
-    bn[s] = v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int q = 0; q < 4; ++q) an[s][q] = 0.f;
-  }
-  auto load_stage = [&](int i0, v4f (&b)[4], float (&a)[4][4]) {
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int i = i0 + 4 * s + kk;
-      const bool rok = i < m;
-      b[s] = rok && cmask ? ld4(P.graw, dt, L.off + (int64_t)i * ld + jl, vec, cmask)
-                          : v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int c = cl + 16 * q;
-        a[s][q] = (rok && c < k) ? Ul[(int64_t)i * k + c] : 0.f;
+    for (int h = 0; h < 8; ++h) {
+      const int i = i0 + tid / 64 + 4 * h;     // rows i0 + (0..31)
+      const int64_t e = L.off + (int64_t)i * ld + j0 + gc;
+      if (FAST) {
+        rg[h] = gld4_nt((const float*)P.graw + e);
+        if (do_p) rp[h] = gld4_nt((const float*)P.p + e);
+      } else {
+        const bool ok = i < m && gmask;
+        rg[h] = ok ? ld4(P.graw, dt, e, gvec, gmask) : v4f{0.f, 0.f, 0.f, 0.f};
+        if (do_p) rp[h] = ok ? ld4(P.p, dt, e, gvec, gmask) : v4f{0.f, 0.f, 0.f, 0.f};
       }
     }
-  };
-  load_stage(0, bq, aq);
-  for (int i0 = 0; i0 < m; i0 += 16) {
-    if (i0 + 16 < m) load_stage(i0 + 16, bn, an);
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int h = 0; h < 2; ++h) {
+      const int i = i0 + tid / 16 + 16 * h;
+      if (FAST)
+        ru[h] = gld4(L.Ul + (int64_t)i * k + c0 + uc);
+      else
+        ru[h] = (i < m && umask) ? ldf4(L.Ul, (int64_t)i * k + c0 + uc, uvec, umask)
+                                 : v4f{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  auto store_chunk = [&]() {
+#pragma unroll
+    for (int h = 0; h < 8; ++h) *(v4f*)&Gs[tid / 64 + 4 * h][gc] = rg[h];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) *(v4f*)&Us[tid / 16 + 16 * h][uc] = ru[h];
+    if (do_norms) {
+      float a = 0.f, b = 0.f;
+#pragma unroll
+      for (int h = 0; h < 8; ++h)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          a = fmaf(rg[h][t], rg[h][t], a);
+          if (do_p) {
+            const float x = decay ? round_to(dt, rp[h][t] * P.decay) : rp[h][t];
+            b = fmaf(x, x, b);
+          }
+        }
+      g2 += (double)a;
+      p2 += (double)b;
+    }
+  };
+
+  load_chunk(0);
+  for (int i0 = 0; i0 < m; i0 += PR) {
+    if (i0) __syncthreads();              // previous chunk fully consumed
+    store_chunk();
+    __syncthreads();
+    if (i0 + PR < m) load_chunk(i0 + PR); // in flight during the MFMAs below
+#pragma unroll
+    for (int s = 0; s < PR / 4; ++s) {
+      const v4f b = *(const v4f*)&Gs[4 * s + kk][64 * w + 4 * (l % 16)];
+      float a[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) a[q] = Us[4 * s + kk][16 * q + (l % 16)];
 #pragma unroll
       for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[q][t] = mfma16(aq[s][q], bq[s][t], acc[q][t]);
-    if (do_norms) {
-      float part = 0.f;
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) part = fmaf(bq[s][t], bq[s][t], part);
-      g2 += (double)part;
-      if (do_p) {
-        float pp = 0.f;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int i = i0 + 4 * s + kk;
-          if (i < m && cmask) {
-            v4f pv = ld4(P.p, dt, L.off + (int64_t)i * ld + jl, vec, cmask);
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-              float x = decay ? round_to(dt, pv[t] * P.decay) : pv[t];
-              pp = fmaf(x, x, pp);
-            }
-          }
-        }
-        p2 += (double)pp;
-      }
-    }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      bq[s] = bn[s];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) aq[s][q] = an[s][q];
+        for (int t = 0; t < 4; ++t) acc[q][t] = mfma16(a[q], b[t], acc[q][t]);
     }
   }
   // T[c][j] for c = c0 + 16q + 4*(l/16) + r, j = jl + t
-  const bool tvec = (L.flags & SCAO_LF_VEC4) && cmask == 15;
+  const int jl = j0 + 64 * w + 4 * (l % 16);
+  int cmask = 15;
+  if (!FAST)
+    for (int t = 0; t < 4; ++t) cmask = (jl + t < n) ? cmask : (cmask & ~(1 << t));
+  const bool tvec = gvec_leaf && cmask == 15;
 #pragma unroll
   for (int q = 0; q < 4; ++q)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int c = c0 + 16 * q + 4 * kk + r;
-      if (c < k && cmask) {
+      if (FAST || (c < k && cmask)) {
         v4f o = {acc[q][0][r], acc[q][1][r], acc[q][2][r], acc[q][3][r]};
         stf4(L.T, (int64_t)c * n + jl, o, tvec, cmask);
       }
@@ -277,34 +304,169 @@ __device__ __forceinline__ void corr_tile(const scao_leaf_desc& L, int i0, int j
 
 namespace {
 
+// One 64x64 tile of a block: the optimizer's whole Phase-2 elementwise tail
+// fused behind the back-projection.  Order of work per wave (16 rows x 64
+// columns, 16 elements per lane):
+//   1. issue every elementwise load of the tile (g, m, v, d, prev [, p]) --
+//      they do not depend on the correction, so HBM latency overlaps step 2;
+//   2. corr = W[rows, :] U_r[cols, :]^T on MFMA, with the U_r tile (shared by
+//      the four waves) staged once per block through LDS, 64 columns of k at
+//      a time;
+//   3. gp = G + corr -> clip -> blend -> Adan -> update -> stores.
+constexpr int UPAD = 68;   // LDS row pitch (floats) of the staged U_r tile
+
+template <bool GF32, bool LARS, bool FAST>
 __device__ __forceinline__ void apply_tile(const scao_leaf_desc& L, const scao_param_desc& P,
-                           const scao_param_stat& S, int i0, int j0, int slot, double* slots) {
+                                           const scao_param_stat& S, int i0, int j0, int slot,
+                                           double* slots) {
+  __shared__ __attribute__((aligned(16))) float Us[64][UPAD];
   __shared__ double red[16];
   const int w = threadIdx.x / 64, l = threadIdx.x % 64;
-  const int m = L.m, n = L.n;
-  const int dt = P.dtype;
+  const int m = L.m, n = L.n, k = L.k;
+  const int dt = FAST ? SCAO_F32 : P.dtype;
+  const int kk = l / 16;
   const int jl = j0 + 4 * (l % 16);
-  v4f acc[4];
-  corr_tile(L, i0, jl, acc);
-  int cmask = 0;
-  for (int t = 0; t < 4; ++t) cmask |= (jl + t < n) ? (1 << t) : 0;
-  const bool vec = (L.flags & SCAO_LF_VEC4) && cmask == 15;
-  double u2 = 0.0;
+  int cmask = 15;
+  if (!FAST)
+    for (int t = 0; t < 4; ++t) cmask = (jl + t < n) ? cmask : (cmask & ~(1 << t));
+  const bool vec = FAST || ((L.flags & SCAO_LF_VEC4) && cmask == 15);
+  constexpr bool gf32 = GF32;
+  constexpr bool lars = LARS;
+  const float* __restrict__ mA = P.exp_avg;
+  const float* __restrict__ vA = P.exp_avg_sq;
+  const float* __restrict__ dA = P.exp_avg_diff;
+  const float* __restrict__ pA = P.prev_grad;
+
+  // 1) prefetch
+  v4f gr[4], gm[4], mm[4], vv[4], dd[4], pp[4], par[4];
+  int64_t e[4];
+  bool rok[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    const int i = i0 + 16 * w + 4 * (l / 16) + r;
-    if (i >= m || !cmask) continue;
-    const int64_t e = L.off + (int64_t)i * L.ld + jl;
-    const v4f graw = ld4(P.graw, dt, e, vec, cmask);
-    const v4f g = (P.flags & SCAO_PF_GF32) ? ld_mgrad(P, e, vec, cmask) : graw;
-    v4f gp;
+    const int i = i0 + 16 * w + 4 * kk + r;
+    e[r] = L.off + (int64_t)i * L.ld + jl;
+    if (FAST) {
+      rok[r] = true;
+      gr[r] = gld4_nt((const float*)P.graw + e[r]);
+      if (gf32) gm[r] = gld4_nt((const float*)P.g + e[r]);
+      mm[r] = gld4_nt(mA + e[r]);
+      vv[r] = gld4_nt(vA + e[r]);
+      dd[r] = gld4_nt(dA + e[r]);
+      pp[r] = gld4_nt(pA + e[r]);
+      if (!lars) par[r] = gld4_nt((const float*)P.p + e[r]);
+    } else {
+      rok[r] = i < m && cmask;
+      const v4f z = {0.f, 0.f, 0.f, 0.f};
+      gr[r] = rok[r] ? ld4(P.graw, dt, e[r], vec, cmask) : z;
+      if (gf32) gm[r] = rok[r] ? ldf4((const float*)P.g, e[r], vec, cmask) : z;
+      mm[r] = rok[r] ? ldf4(mA, e[r], vec, cmask) : z;
+      vv[r] = rok[r] ? ldf4(vA, e[r], vec, cmask) : z;
+      dd[r] = rok[r] ? ldf4(dA, e[r], vec, cmask) : z;
+      pp[r] = rok[r] ? ldf4(pA, e[r], vec, cmask) : z;
+      if (!lars) par[r] = rok[r] ? ld4(P.p, dt, e[r], vec, cmask) : z;
+    }
+  }
+
+  // 2) corr = W U_r^T
+  v4f acc[4];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) gp[t] = round_to(dt, graw[t] + acc[t][r]);
-    const v4f u = adan_tail(P, S, e, g, gp, vec, cmask);
-    u2 += (double)write_update(P, e, u, vec, cmask);
+  for (int t = 0; t < 4; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+  const int irow = i0 + 16 * w + (l % 16);
+  const bool kvec = FAST || (k % 4) == 0;
+  for (int cb0 = 0; cb0 < k; cb0 += 64) {
+    if (cb0) __syncthreads();
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int idx = threadIdx.x + 256 * h;
+      const int row = idx / 16, c4 = (idx % 16) * 4;
+      const int j = j0 + row, c = cb0 + c4;
+      v4f x;
+      if (FAST && c + 3 < k) {
+        x = gld4(L.Ur + (int64_t)j * k + c);
+      } else {
+        int mk = 0;
+        for (int t = 0; t < 4; ++t) mk |= (j < n && c + t < k) ? (1 << t) : 0;
+        x = mk ? ldf4(L.Ur, (int64_t)j * k + c, kvec && mk == 15, mk) : v4f{0.f, 0.f, 0.f, 0.f};
+      }
+      *(v4f*)&Us[row][c4] = x;
+    }
+    __syncthreads();
+    const int cend = k - cb0 < 64 ? k - cb0 : 64;
+    for (int cb = 0; cb < cend; cb += 16) {
+      const int c = cb0 + cb + 4 * kk;
+      int cm = 15;
+      if (!FAST)
+        for (int s = 0; s < 4; ++s) cm = (c + s < k) ? cm : (cm & ~(1 << s));
+      const v4f a = FAST ? gld4(L.W + (int64_t)irow * k + c)
+                         : ((irow < m && cm) ? ldf4(L.W, (int64_t)irow * k + c, kvec && cm == 15, cm)
+                                             : v4f{0.f, 0.f, 0.f, 0.f});
+      v4f b[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) b[t] = *(const v4f*)&Us[jl - j0 + t][cb + 4 * kk];
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = mfma16(a[s], b[t][s], acc[t]);
+    }
+  }
+
+  // 3) elementwise tail
+  const bool clip = P.flags & SCAO_PF_CLIP;
+  const bool gsnr = P.flags & SCAO_PF_GSNR;
+  const bool decay = P.flags & SCAO_PF_DECAY;
+  const float alpha_nolars = (float)(-P.lr);
+  float u2 = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if (!rok[r]) continue;
+    v4f u, pn;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      float gp = round_to(dt, gr[r][t] + acc[t][r]);
+      if (clip) gp = round_to(dt, gp * S.clip);
+      const float g = gf32 ? gm[r][t] : gr[r][t];
+      const float geff = P.blend * gp + P.omblend * g;
+      const float delta = g - pp[r][t];
+      const float m1 = fmaf(geff, P.omb1, mm[r][t] * P.beta1);
+      const float d1 = fmaf(delta, P.omb3, dd[r][t] * P.beta3);
+      const float gad = geff + P.omb3 * delta;
+      const float v1 = fmaf(P.omb2 * gad, gad, vv[r][t] * P.beta2);
+      float x = (m1 / P.bc1 + P.omb3 * (d1 / P.bc3)) / (sqrtf(v1 / P.bc2) + P.eps);
+      if (gsnr) x = x * ((fabsf(m1) / (sqrtf(v1) + P.eps)) >= P.gsnr ? 1.0f : 0.0f);
+      mm[r][t] = m1;
+      dd[r][t] = d1;
+      vv[r][t] = v1;
+      u[t] = x;
+      if (lars) {
+        if (cmask & (1 << t)) u2 = fmaf(x, x, u2);
+      } else {
+        const float pd = decay ? round_to(dt, par[r][t] * P.decay) : par[r][t];
+        pn[t] = round_to(dt, fmaf(round_to(dt, x), alpha_nolars, pd));
+      }
+    }
+    if (FAST) {
+      gst4_nt(P.exp_avg + e[r], mm[r]);
+      gst4_nt(P.exp_avg_sq + e[r], vv[r]);
+      gst4_nt(P.exp_avg_diff + e[r], dd[r]);
+      gst4_nt(P.prev_grad + e[r], gf32 ? gm[r] : gr[r]);
+      if (lars)
+        gst4(P.upd + e[r], u);
+      else
+        gst4_nt((float*)P.p + e[r], pn);
+      continue;
+    }
+    stf4(P.exp_avg, e[r], mm[r], vec, cmask);
+    stf4(P.exp_avg_sq, e[r], vv[r], vec, cmask);
+    stf4(P.exp_avg_diff, e[r], dd[r], vec, cmask);
+    stf4(P.prev_grad, e[r], gf32 ? gm[r] : gr[r], vec, cmask);
+    if (lars) {
+      stf4(P.upd, e[r], u, vec, cmask);
+    } else {
+      st4(P.p, dt, e[r], pn, vec, cmask);
+    }
   }
   if (slot >= 0) {
-    double x[1] = {u2};
+    double x[1] = {(double)u2};
     block_sum<1>(x, red);
     if (threadIdx.x == 0) {
       slots[(int64_t)slot * SCAO_SLOT_WIDTH + 0] = 0.0;
@@ -339,13 +501,14 @@ __device__ __forceinline__ void apply_out_tile(const scao_leaf_desc& L, const fl
 }
 
 // ---------------------------------------------------------- kernels ---
+template <bool FAST, bool DO_P>
 __global__ __launch_bounds__(256) void k_project(const scao_task* __restrict__ tasks,
                                                  const scao_leaf_desc* __restrict__ leaves,
                                                  const scao_param_desc* __restrict__ params,
                                                  double* slots) {
   const scao_task tk = tasks[blockIdx.x];
   const scao_leaf_desc L = leaves[tk.idx];
-  project_tile(L, params[L.param], tk.a, tk.b, tk.slot, slots);
+  project_tile<FAST, DO_P>(L, params[L.param], tk.a, tk.b, tk.slot, slots);
 }
 __global__ __launch_bounds__(256) void k_delta(const scao_task* __restrict__ tasks,
                                                const scao_leaf_desc* __restrict__ leaves,
@@ -361,6 +524,7 @@ __global__ __launch_bounds__(256) void k_lift(const scao_task* __restrict__ task
   const scao_leaf_desc L = leaves[tk.idx];
   lift_tile(L, tk.a, tk.b);
 }
+template <bool GF32, bool LARS, bool FAST>
 __global__ __launch_bounds__(256) void k_apply(const scao_task* __restrict__ tasks,
                                                const scao_leaf_desc* __restrict__ leaves,
                                                const scao_param_desc* __restrict__ params,
@@ -368,14 +532,14 @@ __global__ __launch_bounds__(256) void k_apply(const scao_task* __restrict__ tas
                                                double* slots) {
   const scao_task tk = tasks[blockIdx.x];
   const scao_leaf_desc L = leaves[tk.idx];
-  apply_tile(L, params[L.param], stat[L.param], tk.a, tk.b, tk.slot, slots);
+  apply_tile<GF32, LARS, FAST>(L, params[L.param], stat[L.param], tk.a, tk.b, tk.slot, slots);
 }
 
 // single-block reference operator (descriptors by value, tiles from blockIdx)
 __global__ __launch_bounds__(256) void k_project_one(scao_leaf_desc L, scao_param_desc P) {
   const int strips = (L.n + SCAO_PROJ_COLS - 1) / SCAO_PROJ_COLS;
-  project_tile(L, P, (blockIdx.x % strips) * SCAO_PROJ_COLS, (blockIdx.x / strips) * 64, -1,
-               nullptr);
+  project_tile<false, false>(L, P, (blockIdx.x % strips) * SCAO_PROJ_COLS,
+                             (blockIdx.x / strips) * 64, -1, nullptr);
 }
 __global__ __launch_bounds__(256) void k_delta_one(scao_leaf_desc L) {
   const int tiles = (L.k + 63) / 64;
@@ -397,12 +561,20 @@ bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 // ------------------------------------------------------------- C ABI ---
 extern "C" int scao_kron_project(const scao_task* tasks, int ntasks, const scao_leaf_desc* leaves,
-                                 const scao_param_desc* params, double* slots, void* stream) {
+                                 const scao_param_desc* params, double* slots, int variant,
+                                 void* stream) {
   SCAO_CHECK_ARG(ntasks >= 0, "scao_kron_project: ntasks < 0");
   if (ntasks == 0) return SCAO_OK;
   SCAO_CHECK_ARG(tasks && leaves && params && slots, "scao_kron_project: null pointer");
-  hipLaunchKernelGGL(k_project, dim3(ntasks), dim3(256), 0, (hipStream_t)stream, tasks, leaves,
-                     params, slots);
+  SCAO_CHECK_ARG(variant >= 0 && variant < 4, "scao_kron_project: bad variant %d", variant);
+  hipStream_t s = (hipStream_t)stream;
+  dim3 g(ntasks), b(256);
+  switch (variant) {
+    case 0: hipLaunchKernelGGL((k_project<false, false>), g, b, 0, s, tasks, leaves, params, slots); break;
+    case 1: hipLaunchKernelGGL((k_project<true, false>), g, b, 0, s, tasks, leaves, params, slots); break;
+    case 2: hipLaunchKernelGGL((k_project<false, true>), g, b, 0, s, tasks, leaves, params, slots); break;
+    default: hipLaunchKernelGGL((k_project<true, true>), g, b, 0, s, tasks, leaves, params, slots); break;
+  }
   SCAO_LAUNCH_CHECK("scao_kron_project");
   return SCAO_OK;
 }
@@ -430,12 +602,26 @@ extern "C" int scao_kron_lift(const scao_task* tasks, int ntasks, const scao_lea
 
 extern "C" int scao_kron_apply(const scao_task* tasks, int ntasks, const scao_leaf_desc* leaves,
                                const scao_param_desc* params, const scao_param_stat* stat,
-                               double* slots, void* stream) {
+                               double* slots, int variant, void* stream) {
   SCAO_CHECK_ARG(ntasks >= 0, "scao_kron_apply: ntasks < 0");
   if (ntasks == 0) return SCAO_OK;
   SCAO_CHECK_ARG(tasks && leaves && params && stat && slots, "scao_kron_apply: null pointer");
-  hipLaunchKernelGGL(k_apply, dim3(ntasks), dim3(256), 0, (hipStream_t)stream, tasks, leaves,
-                     params, stat, slots);
+  SCAO_CHECK_ARG(variant >= 0 && variant < 8, "scao_kron_apply: bad variant %d", variant);
+  hipStream_t s = (hipStream_t)stream;
+  dim3 g(ntasks), b(256);
+#define SCAO_APPLY(GF, LA, FA) \
+  hipLaunchKernelGGL((k_apply<GF, LA, FA>), g, b, 0, s, tasks, leaves, params, stat, slots)
+  switch (variant) {
+    case 0: SCAO_APPLY(false, false, false); break;
+    case 1: SCAO_APPLY(true, false, false); break;
+    case 2: SCAO_APPLY(false, true, false); break;
+    case 3: SCAO_APPLY(true, true, false); break;
+    case 4: SCAO_APPLY(false, false, true); break;
+    case 5: SCAO_APPLY(true, false, true); break;
+    case 6: SCAO_APPLY(false, true, true); break;
+    default: SCAO_APPLY(true, true, true); break;
+  }
+#undef SCAO_APPLY
   SCAO_LAUNCH_CHECK("scao_kron_apply");
   return SCAO_OK;
 }

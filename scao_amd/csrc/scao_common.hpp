@@ -49,16 +49,38 @@ __device__ __forceinline__ float round_to(int dt, float x) {
   return x;
 }
 
+// All tensors these kernels touch live in device global memory; loads and
+// stores go through address-space-1 pointers so the compiler emits global_*
+// instructions (pointers read from descriptor tables are otherwise generic
+// and become flat_* accesses).
+typedef __attribute__((address_space(1))) float gfloat;
+typedef __attribute__((address_space(1))) uint16_t gu16;
+typedef __attribute__((address_space(1))) v4f gv4f;
+typedef unsigned int v2u __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(1))) v2u gv2u;
+
+__device__ __forceinline__ v4f gld4(const float* p) { return *(const gv4f*)p; }
+__device__ __forceinline__ void gst4(float* p, v4f x) { *(gv4f*)p = x; }
+// streaming (read or written once per step): non-temporal cache policy
+__device__ __forceinline__ v4f gld4_nt(const float* p) {
+  return __builtin_nontemporal_load((const gv4f*)p);
+}
+__device__ __forceinline__ void gst4_nt(float* p, v4f x) {
+  __builtin_nontemporal_store(x, (gv4f*)p);
+}
+__device__ __forceinline__ float gld1(const float* p) { return *(const gfloat*)p; }
+__device__ __forceinline__ void gst1(float* p, float x) { *(gfloat*)p = x; }
+
 __device__ __forceinline__ float ld1(const void* base, int dt, int64_t i) {
-  if (dt == SCAO_F32) return ((const float*)base)[i];
-  uint16_t h = ((const uint16_t*)base)[i];
+  if (dt == SCAO_F32) return gld1((const float*)base + i);
+  uint16_t h = ((const gu16*)base)[i];
   return dt == SCAO_BF16 ? bf16_to_f(h) : f16_to_f(h);
 }
 __device__ __forceinline__ void st1(void* base, int dt, int64_t i, float x) {
   if (dt == SCAO_F32) {
-    ((float*)base)[i] = x;
+    gst1((float*)base + i, x);
   } else {
-    ((uint16_t*)base)[i] = dt == SCAO_BF16 ? f_to_bf16(x) : f_to_f16(x);
+    ((gu16*)base)[i] = dt == SCAO_BF16 ? f_to_bf16(x) : f_to_f16(x);
   }
 }
 
@@ -69,12 +91,11 @@ __device__ __forceinline__ v4f ld4(const void* base, int dt, int64_t i, bool vec
   v4f r = {0.f, 0.f, 0.f, 0.f};
   if (vec) {
     if (dt == SCAO_F32) {
-      float4 x = *(const float4*)((const float*)base + i);
-      r = v4f{x.x, x.y, x.z, x.w};
+      r = gld4((const float*)base + i);
     } else {
-      uint2 x = *(const uint2*)((const uint16_t*)base + i);
-      uint16_t h[4] = {(uint16_t)(x.x & 0xffff), (uint16_t)(x.x >> 16), (uint16_t)(x.y & 0xffff),
-                       (uint16_t)(x.y >> 16)};
+      const v2u x = *(const gv2u*)((const uint16_t*)base + i);
+      uint16_t h[4] = {(uint16_t)(x[0] & 0xffff), (uint16_t)(x[0] >> 16), (uint16_t)(x[1] & 0xffff),
+                       (uint16_t)(x[1] >> 16)};
       for (int t = 0; t < 4; ++t) r[t] = dt == SCAO_BF16 ? bf16_to_f(h[t]) : f16_to_f(h[t]);
     }
   } else {
@@ -86,12 +107,12 @@ __device__ __forceinline__ v4f ld4(const void* base, int dt, int64_t i, bool vec
 __device__ __forceinline__ void st4(void* base, int dt, int64_t i, v4f x, bool vec, int mask) {
   if (vec) {
     if (dt == SCAO_F32) {
-      *(float4*)((float*)base + i) = make_float4(x[0], x[1], x[2], x[3]);
+      gst4((float*)base + i, x);
     } else {
       uint16_t h[4];
       for (int t = 0; t < 4; ++t) h[t] = dt == SCAO_BF16 ? f_to_bf16(x[t]) : f_to_f16(x[t]);
-      *(uint2*)((uint16_t*)base + i) =
-          make_uint2((uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16));
+      const v2u y = {(uint32_t)h[0] | ((uint32_t)h[1] << 16), (uint32_t)h[2] | ((uint32_t)h[3] << 16)};
+      *(gv2u*)((uint16_t*)base + i) = y;
     }
   } else {
     for (int t = 0; t < 4; ++t)
@@ -100,22 +121,19 @@ __device__ __forceinline__ void st4(void* base, int dt, int64_t i, v4f x, bool v
 }
 // fp32-only variants (optimizer state is always float32)
 __device__ __forceinline__ v4f ldf4(const float* base, int64_t i, bool vec, int mask) {
-  if (vec) {
-    float4 x = *(const float4*)(base + i);
-    return v4f{x.x, x.y, x.z, x.w};
-  }
+  if (vec) return gld4(base + i);
   v4f r = {0.f, 0.f, 0.f, 0.f};
   for (int t = 0; t < 4; ++t)
-    if (mask & (1 << t)) r[t] = base[i + t];
+    if (mask & (1 << t)) r[t] = gld1(base + i + t);
   return r;
 }
 __device__ __forceinline__ void stf4(float* base, int64_t i, v4f x, bool vec, int mask) {
   if (vec) {
-    *(float4*)(base + i) = make_float4(x[0], x[1], x[2], x[3]);
+    gst4(base + i, x);
     return;
   }
   for (int t = 0; t < 4; ++t)
-    if (mask & (1 << t)) base[i + t] = x[t];
+    if (mask & (1 << t)) gst1(base + i + t, x[t]);
 }
 
 // the gradient the moments use: raw p.grad in its dtype, or a float32 buffer

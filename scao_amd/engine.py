@@ -83,6 +83,8 @@ class PItem:
     lars: bool = False
     diag: bool = False           # diagonal-mode preconditioner in Phase 2
     leaves: list = field(default_factory=list)  # [(leaf, r0, c0)]
+    fp32: bool = True            # param and gradient are float32
+    aligned: bool = True         # every pointer of the param is 16-byte aligned
 
 
 class Workspace:
@@ -118,10 +120,11 @@ class Workspace:
 # step and of the refresh is bracketed by a pair of events on the launch
 # stream and appended under its entry-point name (used by bench.py).
 TIMING = None
+TIMING_ONLY = None   # optional set of entry-point names to time (None: all)
 
 
 def _call(name: str, *args) -> None:
-    if TIMING is None:
+    if TIMING is None or (TIMING_ONLY is not None and name not in TIMING_ONLY):
         L.call(name, *args)
         return
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -166,7 +169,8 @@ def _build_structure(items: list[PItem]):
 
     Every reduction slot is written by exactly one task; each parameter's
     pre-finalize slots and post-finalize slots are contiguous ranges."""
-    tasks = {k: [] for k in ("adam", "proj", "delta", "lift", "dred", "apply", "dapply", "lars")}
+    tasks = {k: [] for k in ["adam", "delta", "lift", "dred", "dapply", "lars"] +
+             [f"proj{v}" for v in range(4)] + [f"apply{v}" for v in range(8)]}
     ranges = []
     leaves = []          # (leaf, r0, c0, param index)
     slot = 0
@@ -193,16 +197,21 @@ def _build_structure(items: list[PItem]):
                 leaves.append((leaf, r0, c0, pi))
             # projection (chunk 0 owns the norm slots)
             for li in range(first, len(leaves)):
-                leaf = leaves[li][0]
+                leaf, r0, c0l, _ = leaves[li]
                 m, n = leaf.m, leaf.n
                 k = leaf.U_l.shape[1]
+                vec = _leaf_vec(it, leaf, r0, c0l)
                 for j0 in range(0, n, L.PROJ_COLS):
                     for c0 in range(0, k, 64):
+                        fast = (vec and it.fp32 and j0 + L.PROJ_COLS <= n and c0 + 64 <= k
+                                and m % 32 == 0)
+                        do_p = c0 == 0 and it.lars
+                        var = (1 if fast else 0) | (2 if do_p else 0)
                         if c0 == 0:
-                            tasks["proj"].append((li, j0, c0, slot))
+                            tasks[f"proj{var}"].append((li, j0, c0, slot))
                             slot += 1
                         else:
-                            tasks["proj"].append((li, j0, c0, -1))
+                            tasks[f"proj{var}"].append((li, j0, c0, -1))
             for li in range(first, len(leaves)):
                 k = leaves[li][0].U_l.shape[1]
                 for a in range(0, k, 64):
@@ -211,14 +220,18 @@ def _build_structure(items: list[PItem]):
                         slot += 1
             pre_end = slot
             for li in range(first, len(leaves)):
-                leaf = leaves[li][0]
+                leaf, r0, c0l, _ = leaves[li]
                 k = leaf.U_l.shape[1]
                 for i0 in range(0, leaf.m, 64):
                     for d0 in range(0, k, 64):
                         tasks["lift"].append((li, i0, d0, -1))
-                for i0 in range(0, leaf.m, L.APPLY_TILE):
-                    for j0 in range(0, leaf.n, L.APPLY_TILE):
-                        tasks["apply"].append((li, i0, j0, slot))
+                var = (1 if it.gmom is not None else 0) | (2 if it.lars else 0)
+                ok = _leaf_vec(it, leaf, r0, c0l) and it.fp32 and it.aligned and k % 16 == 0
+                T = L.APPLY_TILE
+                for i0 in range(0, leaf.m, T):
+                    for j0 in range(0, leaf.n, T):
+                        fast = ok and i0 + T <= leaf.m and j0 + T <= leaf.n
+                        tasks[f"apply{var | (4 if fast else 0)}"].append((li, i0, j0, slot))
                         slot += 1
             ranges.append((pre_begin, pre_end, pre_end, slot))
         if it.lars:
@@ -227,6 +240,17 @@ def _build_structure(items: list[PItem]):
     arrays = {k: np.array(v, dtype=np.int32).reshape(-1, 4).copy().view(L.TASK).reshape(-1)
               for k, v in tasks.items()}
     return arrays, ranges, slot, leaves
+
+
+def _cols(t: Tensor) -> int:
+    return t.shape[1] if t.ndim == 2 else to_2d(t)[0].shape[1]
+
+
+def _leaf_vec(it: PItem, leaf, r0: int, c0: int) -> bool:
+    """float4 access is legal for the block: 4-aligned origin, row stride and width."""
+    cols = _cols(it.p)
+    return ((r0 * cols + c0) % 4 == 0 and cols % 4 == 0 and leaf.n % 4 == 0
+            and it.aligned)
 
 
 def _leaf_table(leaves, items: list[PItem], ws: Workspace):
@@ -254,9 +278,7 @@ def _leaf_table(leaves, items: list[PItem], ws: Workspace):
         e["ld"] = cols
         e["param"] = pi
         e["m"], e["n"], e["k"] = leaf.m, leaf.n, leaf.U_l.shape[1]
-        vec = (e["off"] % 4 == 0 and cols % 4 == 0 and leaf.n % 4 == 0 and
-               _aligned16(it.p.data_ptr(), it.graw.data_ptr(), int(e["T"])) and
-               (it.gmom is None or _aligned16(it.gmom.data_ptr())))
+        vec = _leaf_vec(it, leaf, r0, c0) and _aligned16(int(e["T"]))
         e["flags"] = L.LF_VEC4 if vec else 0
     return tab
 
@@ -326,6 +348,8 @@ def _param_table(items: list[PItem], ranges, ws: Workspace, gsnr: float | None):
                 e["diag_ema"] = it.pre.diag_ema.data_ptr()
                 e["diag_bias"] = getattr(it.pre, "_diag_bias_factor", 1.0)
         e["dtype"] = L.DTYPE_CODE[it.p.dtype]
+        if it.aligned:
+            flags |= L.PF_ALIGNED
         e["flags"] = flags
         e["pre_begin"], e["pre_end"], e["post_begin"], e["post_end"] = ranges[i]
         e["norm_index"] = i
@@ -338,7 +362,15 @@ def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
     if not items:
         return
     dev = ws.device
-    skey = tuple((id(it.p), it.phase2, it.diag, it.lars, it.p.numel(),
+    for it in items:
+        st = it.st
+        it.fp32 = it.p.dtype == torch.float32 and it.graw.dtype == torch.float32
+        it.aligned = _aligned16(it.p.data_ptr(), it.graw.data_ptr(),
+                                it.gmom.data_ptr() if it.gmom is not None else 0,
+                                st["exp_avg"].data_ptr(), st["exp_avg_sq"].data_ptr(),
+                                st["exp_avg_diff"].data_ptr(), st["prev_grad"].data_ptr())
+    skey = tuple((id(it.p), it.phase2, it.diag, it.lars, it.gmom is not None, it.p.numel(),
+                  it.fp32, it.aligned,
                   tuple((id(lf), r0, c0, lf.U_l.shape[1]) for lf, r0, c0 in it.leaves))
                  for it in items)
     if skey != ws.struct_key:
@@ -376,16 +408,19 @@ def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
 
     if N["adam"]:
         _call("scao_adam_step", tp("adam"), N["adam"], P, SL, s)
-    if N["proj"]:
-        _call("scao_kron_project", tp("proj"), N["proj"], LF, P, SL, s)
+    for var in range(4):
+        if N[f"proj{var}"]:
+            _call("scao_kron_project", tp(f"proj{var}"), N[f"proj{var}"], LF, P, SL, var, s)
+    if N["delta"]:
         _call("scao_kron_delta", tp("delta"), N["delta"], LF, P, SL, s)
         _call("scao_kron_lift", tp("lift"), N["lift"], LF, s)
     if N["dred"]:
         _call("scao_diag_reduce", tp("dred"), N["dred"], P, SL, s)
     _call("scao_step_finalize", P, len(items), SL, S, ws.runtime.data_ptr(), 0,
            1 if update_norm_ema else 0, len(items), s)
-    if N["apply"]:
-        _call("scao_kron_apply", tp("apply"), N["apply"], LF, P, S, SL, s)
+    for var in range(8):
+        if N[f"apply{var}"]:
+            _call("scao_kron_apply", tp(f"apply{var}"), N[f"apply{var}"], LF, P, S, SL, var, s)
     if N["dapply"]:
         _call("scao_diag_apply", tp("dapply"), N["dapply"], P, S, SL, s)
     if N["lars"]:

@@ -48,7 +48,7 @@ def test_error_path_without_gpu():
     assert lib.scao_fused_kronecker_workspace(10, 20, 4) == (4 * 20 + 16 + 10 * 4) * 4
     assert lib.scao_int8_ema_scratch_bytes(5000) == (5000 + 2) * 4
     with pytest.raises(L.ScaoLibError):
-        L.call("scao_kron_project", None, -1, None, None, None, None)
+        L.call("scao_kron_project", None, -1, None, None, None, 0, None)
 
 
 def test_missing_library_raises(monkeypatch, tmp_path):

@@ -124,6 +124,8 @@ def test_int8_ema_update(n, sc):
 SHAPES = {"w_col": (20, 80), "w_row": (70, 12), "w_kron": (12, 20), "w_conv": (4, 3, 2, 2),
           "b": (20,)}
 BIG = {"wq": (256, 256), "wk": (64, 256), "wup": (512, 256), "wdown": (256, 512), "ln": (256,)}
+FAST = {"sq": (512, 512), "wide": (256, 1024), "tall": (1024, 256), "odd": (320, 448),
+        "ln": (512,)}
 
 CASES = {
     "int8_small": (SHAPES, dict(lr=1e-2, weight_decay=0.01, max_precond_dim=32, rho=0.99,
@@ -142,6 +144,15 @@ CASES = {
                            use_int8_ema=True, k_min=32, k_max=32, warmup_steps=4,
                            blend_steps=4, precond_freq=3, min_precond_updates=1, tau=1.0,
                            lars_coeff=1e-3), 10),
+    # k=64 and whole 64x64 / 256-column tiles: the fast (unmasked fp32) kernel paths
+    "fast_k64": (FAST, dict(lr=1e-3, weight_decay=0.01, max_precond_dim=512, rho=0.999,
+                            use_int8_ema=True, k_min=64, k_max=64, warmup_steps=2,
+                            blend_steps=3, precond_freq=4, min_precond_updates=1, tau=1.0,
+                            lars_coeff=1e-3), 7),
+    "fast_k128_nolars": (FAST, dict(lr=1e-3, weight_decay=0.0, max_precond_dim=512, rho=0.999,
+                                    use_int8_ema=False, k_min=128, k_max=128, warmup_steps=2,
+                                    blend_steps=2, precond_freq=4, min_precond_updates=1,
+                                    tau=None, lars_coeff=0.0), 6),
 }
 
 
