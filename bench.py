@@ -87,6 +87,19 @@ def leaves_of(shape, D):
     return out
 
 
+def _profiled_traffic(kernel: str, config: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (calibrated against a 1 GiB copy), or None."""
+    name = kernel.replace("scao_", "")
+    path = os.path.join(ROOT, "profiles", f"{name}_{config}_traffic.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith(f"traffic_bytes_per_launch {name} {config}:"):
+            return float(line.split(":")[1])
+    return None
+
+
 def cpu_baseline(cfg, args):
     """The oracle (torch on the host CPU) on a bounded sample: one layer's
     preconditioned matrices, steady Phase-2 steps (eye-initialised factors,
@@ -129,6 +142,12 @@ def main():
     ap.add_argument("--details", default=None, help="write the full report JSON here")
     ap.add_argument("--dominant", default="scao_kron_apply",
                     help="entry point timed with HIP events inside the timed region")
+    ap.add_argument("--no-refresh", action="store_true",
+                    help="reach Phase 2 without a curvature refresh (eye-initialised "
+                         "factors; same per-step work) -- for short profiler passes")
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="before timing, copy a buffer of this size once (a plain copy "
+                         "kernel of known size to calibrate traffic counters)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -160,9 +179,20 @@ def main():
         for p, gr in zip(allp, grad_sets[i % 2]):
             p.grad = gr
 
+    if args.no_refresh:
+        sched = dict(warmup_steps=2, precond_freq=10 ** 9, min_precond_updates=0)
+    else:
+        sched = dict(warmup_steps=3, precond_freq=3, min_precond_updates=1)
     opt = scao_amd.SCAO([{"params": pre_p}, {"params": adam_p, "warmup_steps": 10 ** 9}],
-                        k_min=cfg["k"], k_max=cfg["k"], max_precond_dim=cfg["D"],
-                        warmup_steps=3, precond_freq=3, min_precond_updates=1, **PROFILE)
+                        k_min=cfg["k"], k_max=cfg["k"], max_precond_dim=cfg["D"], **sched,
+                        **PROFILE)
+    if args.copy_probe_mib:
+        src = torch.ones(args.copy_probe_mib << 18, device=dev)
+        dst = torch.empty_like(src)
+        torch.cuda.synchronize()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     torch.cuda.synchronize()
 
     def timed(fn):
@@ -184,6 +214,8 @@ def main():
     engine.TIMING = {}
     t_refresh = timed(one)                    # step 3: Phase 1 + curvature refresh
     refresh_parts = engine.timing_summary()
+    if args.no_refresh:                       # step 3 was a plain Phase-2 step
+        t_refresh, refresh_parts = None, {}
     engine.TIMING = None
     for g in opt.param_groups:
         g["precond_freq"] = 10 ** 9           # steady state: no refresh in the timed region
@@ -234,7 +266,7 @@ def main():
             "achieved": achieved / (1e9 if bound == "hbm" else 1e12),
             "peak": peak / (1e9 if bound == "hbm" else 1e12),
             "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
-            "frac": achieved / peak, "traffic": None,
+            "frac": achieved / peak, "traffic": _profiled_traffic(dom, args.config),
             "avg_ms": dom_timing[dom][1]}
     step_bytes = 44.0 * n_pre + 32.0 * (nparams - n_pre)
     step_flops = sum(proj_flops(m, n, k) for m, n in n_leaf)

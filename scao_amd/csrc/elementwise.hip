@@ -46,50 +46,87 @@ __device__ __forceinline__ void write_slot(double* slots, int slot, double a, do
 }
 
 // --------------------------------------------------------------- adam ---
-__global__ __launch_bounds__(256) void k_adam(const scao_task* __restrict__ tasks,
-                                              const scao_param_desc* __restrict__ params,
-                                              double* slots) {
+// FAST: fp32 data, 16-byte aligned, a full 4096-element chunk -- straight-line
+// non-temporal float4 traffic with every load of the thread issued first.
+template <bool FAST>
+__device__ __forceinline__ void adam_chunk(const scao_task& tk, const scao_param_desc& P,
+                                           double* slots) {
   __shared__ double red[16];
-  const scao_task tk = tasks[blockIdx.x];
-  const scao_param_desc& P = params[tk.idx];
-  const int dt = P.dtype;
+  const int dt = FAST ? SCAO_F32 : P.dtype;
   const Chunk ch(tk, P.numel);
   const bool gf32 = P.flags & SCAO_PF_GF32;
-  const bool aligned = al_dt(P.p, dt) && al16(P.g) && al_dt(P.graw, dt) && al16(P.exp_avg) &&
-                       al16(P.exp_avg_sq) && al16(P.prev_grad);
+  const bool aligned = FAST || (al_dt(P.p, dt) && al16(P.g) && al_dt(P.graw, dt) &&
+                                al16(P.exp_avg) && al16(P.exp_avg_sq) && al16(P.prev_grad));
   const bool decay = P.flags & SCAO_PF_DECAY;
-  double g2 = 0.0;
+  v4f g[4], gr[4], p[4], m[4], v[4];
+  int mk[4];
 #pragma unroll
   for (int grp = 0; grp < 4; ++grp) {
     const int64_t e = ch.elem(grp);
-    const int mk = ch.mask(e);
-    if (!mk) continue;
-    const bool vec = aligned && mk == 15;
-    const v4f g = ld_mgrad(P, e, vec, mk);
-    const v4f gr = gf32 ? ld4(P.graw, dt, e, vec, mk) : g;
-    v4f p = ld4(P.p, dt, e, vec, mk);
-    v4f m = ldf4(P.exp_avg, e, vec, mk);
-    v4f v = ldf4(P.exp_avg_sq, e, vec, mk);
-    float part = 0.f;
+    if (FAST) {
+      mk[grp] = 15;
+      g[grp] = gld4_nt((const float*)P.g + e);
+      gr[grp] = gf32 ? gld4_nt((const float*)P.graw + e) : g[grp];
+      p[grp] = gld4_nt((const float*)P.p + e);
+      m[grp] = gld4_nt(P.exp_avg + e);
+      v[grp] = gld4_nt(P.exp_avg_sq + e);
+    } else {
+      mk[grp] = ch.mask(e);
+      const bool vec = aligned && mk[grp] == 15;
+      const v4f z = {0.f, 0.f, 0.f, 0.f};
+      g[grp] = mk[grp] ? ld_mgrad(P, e, vec, mk[grp]) : z;
+      gr[grp] = (mk[grp] && gf32) ? ld4(P.graw, dt, e, vec, mk[grp]) : g[grp];
+      p[grp] = mk[grp] ? ld4(P.p, dt, e, vec, mk[grp]) : z;
+      m[grp] = mk[grp] ? ldf4(P.exp_avg, e, vec, mk[grp]) : z;
+      v[grp] = mk[grp] ? ldf4(P.exp_avg_sq, e, vec, mk[grp]) : z;
+    }
+  }
+  float part = 0.f;
+#pragma unroll
+  for (int grp = 0; grp < 4; ++grp) {
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      part = fmaf(gr[t], gr[t], part);
-      const float pd = decay ? round_to(dt, p[t] * P.decay) : p[t];
-      m[t] = fmaf(g[t], P.omb1, m[t] * P.beta1);
-      v[t] = fmaf(P.omb2 * g[t], g[t], v[t] * P.beta2);
-      const float den = sqrtf(v[t]) / P.adam_sqrt_bc2 + P.eps;
-      const float u = round_to(dt, m[t] / den);
-      p[t] = round_to(dt, fmaf(u, P.adam_alpha, pd));
+      part = fmaf(gr[grp][t], gr[grp][t], part);
+      const float pd = decay ? round_to(dt, p[grp][t] * P.decay) : p[grp][t];
+      m[grp][t] = fmaf(g[grp][t], P.omb1, m[grp][t] * P.beta1);
+      v[grp][t] = fmaf(P.omb2 * g[grp][t], g[grp][t], v[grp][t] * P.beta2);
+      const float den = sqrtf(v[grp][t]) / P.adam_sqrt_bc2 + P.eps;
+      const float u = round_to(dt, m[grp][t] / den);
+      p[grp][t] = round_to(dt, fmaf(u, P.adam_alpha, pd));
     }
-    g2 += (double)part;
-    stf4(P.exp_avg, e, m, vec, mk);
-    stf4(P.exp_avg_sq, e, v, vec, mk);
-    stf4(P.prev_grad, e, g, vec, mk);
-    st4(P.p, dt, e, p, vec, mk);
+    const int64_t e = ch.elem(grp);
+    if (FAST) {
+      gst4_nt(P.exp_avg + e, m[grp]);
+      gst4_nt(P.exp_avg_sq + e, v[grp]);
+      gst4_nt(P.prev_grad + e, g[grp]);
+      gst4_nt((float*)P.p + e, p[grp]);
+    } else if (mk[grp]) {
+      const bool vec = aligned && mk[grp] == 15;
+      stf4(P.exp_avg, e, m[grp], vec, mk[grp]);
+      stf4(P.exp_avg_sq, e, v[grp], vec, mk[grp]);
+      stf4(P.prev_grad, e, g[grp], vec, mk[grp]);
+      st4(P.p, dt, e, p[grp], vec, mk[grp]);
+    }
   }
-  double x[1] = {g2};
+  double x[1] = {(double)part};
   block_sum<1>(x, red);
   if (threadIdx.x == 0) write_slot(slots, tk.slot, x[0], 0.0, 0.0);
+}
+
+__device__ __forceinline__ bool flat_fast(const scao_task& tk, const scao_param_desc& P) {
+  return P.dtype == SCAO_F32 && (P.flags & SCAO_PF_ALIGNED) &&
+         (int64_t)(tk.a + 1) * SCAO_FLAT_CHUNK <= P.numel;
+}
+
+__global__ __launch_bounds__(256) void k_adam(const scao_task* __restrict__ tasks,
+                                              const scao_param_desc* __restrict__ params,
+                                              double* slots) {
+  const scao_task tk = tasks[blockIdx.x];
+  const scao_param_desc& P = params[tk.idx];
+  if (flat_fast(tk, P))
+    adam_chunk<true>(tk, P, slots);
+  else
+    adam_chunk<false>(tk, P, slots);
 }
 
 // ------------------------------------------------------- diag reduce ---
@@ -172,31 +209,56 @@ __global__ __launch_bounds__(256) void k_diag_apply(const scao_task* __restrict_
 }
 
 // -------------------------------------------------------- lars write ---
+template <bool FAST>
+__device__ __forceinline__ void lars_chunk(const scao_task& tk, const scao_param_desc& P,
+                                           float alpha) {
+  const int dt = FAST ? SCAO_F32 : P.dtype;
+  const Chunk ch(tk, P.numel);
+  const bool aligned = FAST || (al_dt(P.p, dt) && al16(P.upd));
+  const bool decay = P.flags & SCAO_PF_DECAY;
+  v4f u[4], p[4];
+  int mk[4];
+#pragma unroll
+  for (int grp = 0; grp < 4; ++grp) {
+    const int64_t e = ch.elem(grp);
+    if (FAST) {
+      mk[grp] = 15;
+      u[grp] = gld4(P.upd + e);
+      p[grp] = gld4_nt((const float*)P.p + e);
+    } else {
+      mk[grp] = ch.mask(e);
+      const bool vec = aligned && mk[grp] == 15;
+      const v4f z = {0.f, 0.f, 0.f, 0.f};
+      u[grp] = mk[grp] ? ldf4(P.upd, e, vec, mk[grp]) : z;
+      p[grp] = mk[grp] ? ld4(P.p, dt, e, vec, mk[grp]) : z;
+    }
+  }
+#pragma unroll
+  for (int grp = 0; grp < 4; ++grp) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float pd = decay ? round_to(dt, p[grp][t] * P.decay) : p[grp][t];
+      p[grp][t] = round_to(dt, fmaf(round_to(dt, u[grp][t]), alpha, pd));
+    }
+    const int64_t e = ch.elem(grp);
+    if (FAST) {
+      gst4_nt((float*)P.p + e, p[grp]);
+    } else if (mk[grp]) {
+      st4(P.p, dt, e, p[grp], aligned && mk[grp] == 15, mk[grp]);
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void k_lars_write(const scao_task* __restrict__ tasks,
                                                     const scao_param_desc* __restrict__ params,
                                                     const scao_param_stat* __restrict__ stat) {
   const scao_task tk = tasks[blockIdx.x];
   const scao_param_desc& P = params[tk.idx];
   const float alpha = stat[tk.idx].alpha;
-  const int dt = P.dtype;
-  const Chunk ch(tk, P.numel);
-  const bool aligned = al_dt(P.p, dt) && al16(P.upd);
-  const bool decay = P.flags & SCAO_PF_DECAY;
-#pragma unroll
-  for (int grp = 0; grp < 4; ++grp) {
-    const int64_t e = ch.elem(grp);
-    const int mk = ch.mask(e);
-    if (!mk) continue;
-    const bool vec = aligned && mk == 15;
-    const v4f u = ldf4(P.upd, e, vec, mk);
-    v4f p = ld4(P.p, dt, e, vec, mk);
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const float pd = decay ? round_to(dt, p[t] * P.decay) : p[t];
-      p[t] = round_to(dt, fmaf(round_to(dt, u[t]), alpha, pd));
-    }
-    st4(P.p, dt, e, p, vec, mk);
-  }
+  if (flat_fast(tk, P))
+    lars_chunk<true>(tk, P, alpha);
+  else
+    lars_chunk<false>(tk, P, alpha);
 }
 
 // ---------------------------------------------------------- diag ema ---
@@ -225,18 +287,20 @@ __global__ __launch_bounds__(256) void k_diag_ema(const scao_task* __restrict__ 
 }
 
 // ---------------------------------------------------------- finalize ---
-__global__ __launch_bounds__(64) void k_finalize_params(const scao_param_desc* __restrict__ params,
-                                                        const double* __restrict__ slots,
-                                                        scao_param_stat* stat, int phase) {
+__global__ __launch_bounds__(256) void k_finalize_params(const scao_param_desc* __restrict__ params,
+                                                         const double* __restrict__ slots,
+                                                         scao_param_stat* stat, int phase) {
+  __shared__ double red[16];
   const scao_param_desc& P = params[blockIdx.x];
   scao_param_stat& S = stat[blockIdx.x];
   const int l = threadIdx.x;
   const int dt = P.dtype;
+  const double* __restrict__ sl = slots;
   if (phase == 0) {
     double a[3] = {0.0, 0.0, 0.0};
-    for (int s = P.pre_begin + l; s < P.pre_end; s += 64)
-      for (int q = 0; q < 3; ++q) a[q] += slots[(int64_t)s * SCAO_SLOT_WIDTH + q];
-    for (int q = 0; q < 3; ++q) a[q] = wave_sum(a[q]);
+    for (int s = P.pre_begin + l; s < P.pre_end; s += 256)
+      for (int q = 0; q < 3; ++q) a[q] += sl[(int64_t)s * SCAO_SLOT_WIDTH + q];
+    block_sum<3>(a, red);
     if (l == 0) {
       S.g2 = a[0];
       S.p2 = a[1];
@@ -254,10 +318,11 @@ __global__ __launch_bounds__(64) void k_finalize_params(const scao_param_desc* _
       S.alpha = (float)(-P.lr);
     }
   } else {
-    double a = 0.0;
-    for (int s = P.post_begin + l; s < P.post_end; s += 64)
-      a += slots[(int64_t)s * SCAO_SLOT_WIDTH + 2];
-    a = wave_sum(a);
+    double ax[1] = {0.0};
+    for (int s = P.post_begin + l; s < P.post_end; s += 256)
+      ax[0] += sl[(int64_t)s * SCAO_SLOT_WIDTH + 2];
+    block_sum<1>(ax, red);
+    const double a = ax[0];
     if (l == 0) {
       S.u2 = a;
       const float un = (float)sqrt(a);
@@ -344,7 +409,7 @@ extern "C" int scao_step_finalize(const scao_param_desc* params, int nparams, co
   if (nparams == 0) return SCAO_OK;
   SCAO_CHECK_ARG(params && slots && stat, "scao_step_finalize: null pointer");
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(k_finalize_params, dim3(nparams), dim3(64), 0, s, params, slots, stat, phase);
+  hipLaunchKernelGGL(k_finalize_params, dim3(nparams), dim3(256), 0, s, params, slots, stat, phase);
   SCAO_LAUNCH_CHECK("scao_step_finalize");
   if (phase == 0 && update_norm_ema) {
     SCAO_CHECK_ARG(runtime != nullptr, "scao_step_finalize: null runtime");

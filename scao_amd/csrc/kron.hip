@@ -168,65 +168,133 @@ __device__ __forceinline__ void project_tile(const scao_leaf_desc& L, const scao
 
 // ------------------------------------------------------------- delta ---
 // P[c0:c0+64, d0:d0+64] = T U_r; Delta and the natural-norm partial.
-__device__ __forceinline__ void delta_tile(const scao_leaf_desc& L, float eps, int c0, int d0, int slot,
-                           double* slots) {
+// The four waves split the n-reduction (one quarter each, 16-column chunks,
+// one chunk prefetched); every wave accumulates the whole 64x64 tile
+// (16 MFMA tiles) and the four partial tiles are added in LDS in a fixed
+// order.  P column d of tile t sits at lane column jj with d = d0 + 4*jj + t,
+// so one float4 of a U_r row feeds all four tiles.
+constexpr int DP = 64 + 4;   // LDS pitch of a partial tile
+
+template <bool FAST>
+__device__ __forceinline__ void delta_tile(const scao_leaf_desc& L, float eps, int c0, int d0,
+                                           int slot, double* slots) {
+  __shared__ __attribute__((aligned(16))) float Ps[3][64][DP];
   __shared__ double red[16];
   const int w = threadIdx.x / 64, l = threadIdx.x % 64;
   const int n = L.n, k = L.k;
   const int kk = l / 16;
-  const int crow = c0 + 16 * w + (l % 16);  // A row supplied by this lane
-  const bool tvec = (L.flags & SCAO_LF_VEC4) != 0;
   const float* T = L.T;
   const float* Ur = L.Ur;
-  v4f acc[4];
+  const int dl = d0 + 4 * (l % 16);      // this lane's 4 P columns
+  int dmask = 15;
+  if (!FAST)
+    for (int t = 0; t < 4; ++t) dmask = (dl + t < k) ? dmask : (dmask & ~(1 << t));
+  const bool uvec = FAST || ((k % 4) == 0 && dmask == 15);
+  const bool tvec_leaf = FAST || (L.flags & SCAO_LF_VEC4) != 0;
+  const int nq = ((n + 63) / 64) * 16;    // per-wave share of n, multiple of 16
+  const int jbeg = w * nq, jend = min(n, jbeg + nq);
+
+  v4f acc[4][4];
 #pragma unroll
-  for (int t = 0; t < 4; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-  for (int jb = 0; jb < n; jb += 16) {
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[q][t] = v4f{0.f, 0.f, 0.f, 0.f};
+
+  v4f ra[4], rb[4], na[4], nb[4];
+  auto load = [&](int jb, v4f (&a)[4], v4f (&b)[4]) {
     const int j = jb + 4 * kk;
-    int jm = 0;
-    for (int s = 0; s < 4; ++s) jm |= (j + s < n) ? (1 << s) : 0;
-    v4f a = (crow < k && jm) ? ldf4(T, (int64_t)crow * n + j, tvec && jm == 15, jm)
+    int jm = 15;
+    if (!FAST)
+      for (int s2 = 0; s2 < 4; ++s2) jm = (j + s2 < jend) ? jm : (jm & ~(1 << s2));
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int c = c0 + 16 * q + (l % 16);
+      if (FAST)
+        a[q] = gld4(T + (int64_t)c * n + j);
+      else
+        a[q] = (c < k && jm) ? ldf4(T, (int64_t)c * n + j, tvec_leaf && jm == 15, jm)
                              : v4f{0.f, 0.f, 0.f, 0.f};
+    }
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    for (int s2 = 0; s2 < 4; ++s2) {
+      if (FAST)
+        b[s2] = gld4(Ur + (int64_t)(j + s2) * k + dl);
+      else
+        b[s2] = (((jm >> s2) & 1) && dmask) ? ldf4(Ur, (int64_t)(j + s2) * k + dl, uvec, dmask)
+                                            : v4f{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+  if (jbeg < jend) load(jbeg, ra, rb);
+  for (int jb = jbeg; jb < jend; jb += 16) {
+    if (jb + 16 < jend) load(jb + 16, na, nb);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int d = d0 + 16 * t + (l % 16);
-        const float b = ((jm >> s) & 1) && d < k ? Ur[(int64_t)(j + s) * k + d] : 0.f;
-        acc[t] = mfma16(a[s], b, acc[t]);
-      }
+    for (int s2 = 0; s2 < 4; ++s2)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[q][t] = mfma16(ra[q][s2], rb[s2][t], acc[q][t]);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      ra[q] = na[q];
+      rb[q] = nb[q];
     }
   }
+  // partial tiles of waves 1..3 go through LDS; wave 0 adds them in order
+  // (((w0 + w1) + w2) + w3) and finishes its 64 elements per lane:
+  // element (16q + 4*kk + r, 4*(l%16) + t)
+  if (w > 0) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        *(v4f*)&Ps[w - 1][16 * q + 4 * kk + r][4 * (l % 16)] =
+            v4f{acc[q][0][r], acc[q][1][r], acc[q][2][r], acc[q][3][r]};
+  }
+  __syncthreads();
   const bool sinv4 = L.flags & SCAO_LF_SINV4;
   double nu2 = 0.0;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int c = c0 + 16 * w + 4 * kk + r;
-    if (c >= k) continue;
-    const float sl = L.Sl[c];
-    const float sl4 = sinv4 ? sl : inv4(sl);
-    const float il2 = sinv4 ? 0.f : inv2(sl, eps);
+  if (w == 0) {
+    float sr4[4], ir2[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      const int d = d0 + 16 * t + (l % 16);
-      if (d >= k) continue;
-      const float sr = L.Sr[d];
-      const float sr4 = sinv4 ? sr : inv4(sr);
-      const float pv = acc[t][r];
-      L.Delta[(int64_t)c * k + d] = (sl4 * sr4 - 1.0f) * pv;
-      if (!sinv4) {
-        const float x = (il2 * pv) * inv2(sr, eps);
-        nu2 += (double)x * (double)x;
-      }
+      const int d = dl + t;
+      const float sr = d < k ? gld1(L.Sr + d) : 1.f;
+      sr4[t] = sinv4 ? sr : inv4(sr);
+      ir2[t] = sinv4 ? 0.f : inv2(sr, eps);
     }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * q + 4 * kk + r;
+        const int c = c0 + row;
+        if (c >= k) continue;
+        const float sl = gld1(L.Sl + c);
+        const float sl4 = sinv4 ? sl : inv4(sl);
+        const float il2 = sinv4 ? 0.f : inv2(sl, eps);
+        const v4f p1 = *(const v4f*)&Ps[0][row][4 * (l % 16)];
+        const v4f p2 = *(const v4f*)&Ps[1][row][4 * (l % 16)];
+        const v4f p3 = *(const v4f*)&Ps[2][row][4 * (l % 16)];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int d = dl + t;
+          if (d >= k) continue;
+          const float pv = ((acc[q][t][r] + p1[t]) + p2[t]) + p3[t];
+          gst1(L.Delta + (int64_t)c * k + d, (sl4 * sr4[t] - 1.0f) * pv);
+          if (!sinv4) {
+            const float y = (il2 * pv) * ir2[t];
+            nu2 += (double)y * (double)y;
+          }
+        }
+      }
   }
   if (slot >= 0) {
-    double x[1] = {nu2};
-    block_sum<1>(x, red);
+    double xs[1] = {nu2};
+    block_sum<1>(xs, red);
     if (threadIdx.x == 0) {
       slots[(int64_t)slot * SCAO_SLOT_WIDTH + 0] = 0.0;
       slots[(int64_t)slot * SCAO_SLOT_WIDTH + 1] = 0.0;
-      slots[(int64_t)slot * SCAO_SLOT_WIDTH + 2] = x[0];
+      slots[(int64_t)slot * SCAO_SLOT_WIDTH + 2] = xs[0];
     }
   }
 }
@@ -516,7 +584,12 @@ __global__ __launch_bounds__(256) void k_delta(const scao_task* __restrict__ tas
                                                double* slots) {
   const scao_task tk = tasks[blockIdx.x];
   const scao_leaf_desc L = leaves[tk.idx];
-  delta_tile(L, params[L.param].eps, tk.a, tk.b, tk.slot, slots);
+  const bool fast = (L.flags & SCAO_LF_VEC4) && (L.k % 4 == 0) && tk.a + 64 <= L.k &&
+                    tk.b + 64 <= L.k && (L.n % 64 == 0);
+  if (fast)
+    delta_tile<true>(L, params[L.param].eps, tk.a, tk.b, tk.slot, slots);
+  else
+    delta_tile<false>(L, params[L.param].eps, tk.a, tk.b, tk.slot, slots);
 }
 __global__ __launch_bounds__(256) void k_lift(const scao_task* __restrict__ tasks,
                                               const scao_leaf_desc* __restrict__ leaves) {
@@ -543,7 +616,7 @@ __global__ __launch_bounds__(256) void k_project_one(scao_leaf_desc L, scao_para
 }
 __global__ __launch_bounds__(256) void k_delta_one(scao_leaf_desc L) {
   const int tiles = (L.k + 63) / 64;
-  delta_tile(L, 1e-8f, (blockIdx.x / tiles) * 64, (blockIdx.x % tiles) * 64, -1, nullptr);
+  delta_tile<false>(L, 1e-8f, (blockIdx.x / tiles) * 64, (blockIdx.x % tiles) * 64, -1, nullptr);
 }
 __global__ __launch_bounds__(256) void k_lift_one(scao_leaf_desc L) {
   const int tiles = (L.k + 63) / 64;

@@ -345,3 +345,61 @@ def a_leaves(pre, r0=0, c0=0):
             off += bs
     elif pre.use_kronecker:
         yield pre, r0, c0
+
+
+def test_bf16_params_from_shared_state():
+    """bf16 parameters and gradients (the reference casts to fp32 for the
+    statistics and back for the writes): updates within bf16 rounding."""
+    dev = _dev()
+    shapes, cfg, steps = SHAPES, dict(CASES["int8_small"][1]), 12
+    rp = make_params(shapes, dtype=torch.bfloat16)
+    ref = R.RefSCAO(list(rp.values()), **cfg, **PARITY)
+    worst = 0.0
+    for t in range(1, steps + 1):
+        gp, gopt = _gpu_from_oracle(ref, rp, cfg, dev)
+        grads = grads_for_step(t, shapes, dtype=torch.bfloat16)
+        before = {k: v.detach().clone() for k, v in rp.items()}
+        for k in shapes:
+            rp[k].grad = grads[k].clone()
+            gp[k].grad = grads[k].to(dev)
+        ref.step()
+        gopt.step()
+        torch.cuda.synchronize()
+        for k in shapes:
+            assert gp[k].dtype == torch.bfloat16
+            a, b = rp[k].detach().float(), gp[k].detach().cpu().float()
+            # one bf16 ulp of the parameter is the resolution of the write
+            ulp = (a.abs() * 2.0 ** -7).clamp(min=1e-30)
+            frac = ((a - b).abs() > ulp).float().mean().item()
+            worst = max(worst, frac)
+            assert frac < 0.02, (t, k, frac)
+    report("bf16_params_from_shared_state", "int8_small", {"frac_beyond_1ulp": worst})
+
+
+def test_sparse_filter_trajectory():
+    """Default sparse gradient filter (quantile mask on the magnitude EMA),
+    identical starts, 8 steps; the filter state is not checkpointed by the
+    reference, so this is a trajectory check."""
+    dev = _dev()
+    import scao_amd
+    shapes = SHAPES
+    cfg = dict(CASES["int8_small"][1], sparsity=0.7)
+    rp = make_params(shapes)
+    gp = {k: torch.nn.Parameter(v.detach().clone().to(dev)) for k, v in rp.items()}
+    kw = dict(noise_std_init=0.0, async_precond=False, lookahead_k=0)
+    ref = R.RefSCAO(list(rp.values()), **cfg, **kw)
+    gopt = scao_amd.SCAO(list(gp.values()), **cfg, **kw)
+    init = {k: v.detach().clone() for k, v in rp.items()}
+    errs = []
+    for t in range(1, 9):
+        grads = grads_for_step(t, shapes, outliers=0.01)
+        for k in shapes:
+            rp[k].grad = grads[k].clone()
+            gp[k].grad = grads[k].to(dev)
+        ref.step()
+        gopt.step()
+        torch.cuda.synchronize()
+        for k in shapes:
+            errs.append(_rel(gp[k].detach() - init[k].to(dev), rp[k].detach() - init[k]))
+    report("sparse_filter_trajectory", "int8_small", {"max_cumulative_update_rel_err": max(errs)})
+    assert max(errs) < 1e-3
