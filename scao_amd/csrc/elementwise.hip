@@ -58,6 +58,7 @@ __device__ __forceinline__ void adam_chunk(const scao_task& tk, const scao_param
   const bool aligned = FAST || (al_dt(P.p, dt) && al16(P.g) && al_dt(P.graw, dt) &&
                                 al16(P.exp_avg) && al16(P.exp_avg_sq) && al16(P.prev_grad));
   const bool decay = P.flags & SCAO_PF_DECAY;
+  const float alpha = round_to(dt, P.adam_alpha);
   v4f g[4], gr[4], p[4], m[4], v[4];
   int mk[4];
 #pragma unroll
@@ -92,7 +93,7 @@ __device__ __forceinline__ void adam_chunk(const scao_task& tk, const scao_param
       v[grp][t] = fmaf(P.omb2 * g[grp][t], g[grp][t], v[grp][t] * P.beta2);
       const float den = sqrtf(v[grp][t]) / P.adam_sqrt_bc2 + P.eps;
       const float u = round_to(dt, m[grp][t] / den);
-      p[grp][t] = round_to(dt, fmaf(u, P.adam_alpha, pd));
+      p[grp][t] = round_to(dt, fmaf(u, alpha, pd));
     }
     const int64_t e = ch.elem(grp);
     if (FAST) {
@@ -315,7 +316,7 @@ __global__ __launch_bounds__(256) void k_finalize_params(const scao_param_desc* 
       S.u2 = 0.0;
       S.unorm = 0.f;
       S.trust = 1.0f;
-      S.alpha = (float)(-P.lr);
+      S.alpha = round_to(dt, (float)(-P.lr));
     }
   } else {
     double ax[1] = {0.0};
@@ -334,7 +335,7 @@ __global__ __launch_bounds__(256) void k_finalize_params(const scao_param_desc* 
         trust = num / ((un + wdp) + 1e-8f);
       }
       S.trust = trust;
-      S.alpha = (float)(-(P.lr * (double)trust));
+      S.alpha = round_to(dt, (float)(-(P.lr * (double)trust)));
     }
   }
 }

@@ -482,7 +482,7 @@ __device__ __forceinline__ void apply_tile(const scao_leaf_desc& L, const scao_p
   const bool clip = P.flags & SCAO_PF_CLIP;
   const bool gsnr = P.flags & SCAO_PF_GSNR;
   const bool decay = P.flags & SCAO_PF_DECAY;
-  const float alpha_nolars = (float)(-P.lr);
+  const float alpha_nolars = round_to(dt, (float)(-P.lr));
   float u2 = 0.f;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {

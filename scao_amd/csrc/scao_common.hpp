@@ -236,7 +236,7 @@ __device__ __forceinline__ float write_update(const scao_param_desc& P, int64_t 
     for (int t = 0; t < 4; ++t)
       if (mask & (1 << t)) u2 = fmaf(u[t], u[t], u2);
   } else {
-    const float alpha = (float)(-P.lr);
+    const float alpha = round_to(dt, (float)(-P.lr));
     v4f p = ld4(P.p, dt, e, vec, mask);
 #pragma unroll
     for (int t = 0; t < 4; ++t) {

@@ -287,72 +287,105 @@ def _leaf_table(leaves, items: list[PItem], ws: Workspace):
 # the step
 # --------------------------------------------------------------------------
 
+_MOMENTS = ("exp_avg", "exp_avg_sq", "exp_avg_diff", "prev_grad")
+
+
 def _param_table(items: list[PItem], ranges, ws: Workspace, gsnr: float | None):
-    tab = np.zeros(len(items), dtype=L.PARAM_DESC)
+    """The per-step parameter descriptors, built column by column.
+
+    Scalars are Python floats rounded to fp32 by the record's f4 fields (the
+    same round-to-nearest ATen applies to a scalar operand of an fp32 op)."""
+    n = len(items)
+    tab = np.zeros(n, dtype=L.PARAM_DESC)
+    cols = {k: [] for k in ("p", "g", "graw", "exp_avg", "exp_avg_sq", "exp_avg_diff",
+                            "prev_grad", "upd", "diag_ema", "numel", "cols", "lr", "decay",
+                            "beta1", "omb1", "beta2", "omb2", "beta3", "omb3", "bc1", "bc2",
+                            "bc3", "blend", "omblend", "eps", "tau", "lars", "wd", "gsnr",
+                            "diag_bias", "adam_sqrt_bc2", "adam_alpha", "dtype", "flags")}
+    upd_base = ws.buf("upd", 4).data_ptr() if ws.upd_total else 0
     for i, it in enumerate(items):
-        g = it.group
-        st = it.st
-        e = tab[i]
+        g, st = it.group, it.st
         lr = g["lr"]
         beta1, beta2 = g["betas"]
         beta3 = g["beta3"]
         wd = g["weight_decay"]
         t = it.step
-        e["p"] = it.p.data_ptr()
-        e["graw"] = it.graw.data_ptr()
-        e["g"] = it.gmom.data_ptr() if it.gmom is not None else it.graw.data_ptr()
-        e["exp_avg"] = st["exp_avg"].data_ptr()
-        e["exp_avg_sq"] = st["exp_avg_sq"].data_ptr()
-        e["exp_avg_diff"] = st["exp_avg_diff"].data_ptr()
-        e["prev_grad"] = st["prev_grad"].data_ptr()
-        e["numel"] = it.p.numel()
-        e["cols"] = to_2d(it.p)[0].shape[1] if it.p.ndim != 2 else it.p.shape[1]
-        e["lr"] = lr
-        e["beta1"], e["omb1"] = beta1, 1.0 - beta1
-        e["beta2"], e["omb2"] = beta2, 1.0 - beta2
-        e["beta3"], e["omb3"] = beta3, 1.0 - beta3
-        e["eps"] = g["eps"]
+        graw = it.graw.data_ptr()
+        cols["p"].append(it.p.data_ptr())
+        cols["graw"].append(graw)
+        cols["g"].append(it.gmom.data_ptr() if it.gmom is not None else graw)
+        for key in _MOMENTS:
+            m = st[key]
+            if m.dtype != torch.float32 or not m.is_contiguous() or m.device != it.p.device:
+                raise ValueError(f"state[{key!r}] must be a contiguous float32 tensor on "
+                                 f"{it.p.device}; got {m.dtype} on {m.device}")
+            cols[key].append(m.data_ptr())
+        cols["numel"].append(it.p.numel())
+        cols["cols"].append(_cols(it.p))
+        cols["lr"].append(lr)
+        cols["beta1"].append(beta1)
+        cols["omb1"].append(1.0 - beta1)
+        cols["beta2"].append(beta2)
+        cols["omb2"].append(1.0 - beta2)
+        cols["beta3"].append(beta3)
+        cols["omb3"].append(1.0 - beta3)
+        cols["eps"].append(g["eps"])
         flags = L.PF_NORM
         if wd != 0.0:
             flags |= L.PF_DECAY
-            e["decay"] = 1.0 - lr * wd
-        else:
-            e["decay"] = 1.0
+        cols["decay"].append(1.0 - lr * wd if wd != 0.0 else 1.0)
         if it.gmom is not None:
             flags |= L.PF_GF32
         bc1 = 1.0 - beta1 ** t
         bc2 = 1.0 - beta2 ** t
+        upd = diag = 0
+        tau = lars = wdv = gs = dbias = 0.0
+        blend = omb = bc3 = sq = alpha = 0.0
         if not it.phase2:
-            e["adam_sqrt_bc2"] = math.sqrt(bc2)
-            e["adam_alpha"] = -(lr / bc1)
+            sq, alpha = math.sqrt(bc2), -(lr / bc1)
         else:
-            e["bc1"], e["bc2"] = bc1, bc2
-            e["bc3"] = 1.0 - beta3 ** t
+            bc3 = 1.0 - beta3 ** t
             bsteps = g.get("blend_steps", 50)
             blend = min(1.0, it.scao_step / bsteps) if bsteps > 0 else 1.0
-            e["blend"], e["omblend"] = blend, 1.0 - blend
-            tau = g["tau"]
-            if tau is not None:
+            omb = 1.0 - blend
+            if g["tau"] is not None:
                 flags |= L.PF_CLIP
-                e["tau"] = tau
+                tau = g["tau"]
             if it.lars:
                 flags |= L.PF_LARS
-                e["lars"] = g["lars_coeff"]
-                e["wd"] = wd
-                e["upd"] = ws.buf("upd", 4).data_ptr() + 4 * ws.upd_offsets[i]
+                lars, wdv = g["lars_coeff"], wd
+                upd = upd_base + 4 * ws.upd_offsets[i]
             if gsnr is not None:
                 flags |= L.PF_GSNR
-                e["gsnr"] = gsnr
+                gs = gsnr
             if it.diag:
                 flags |= L.PF_DIAG
-                e["diag_ema"] = it.pre.diag_ema.data_ptr()
-                e["diag_bias"] = getattr(it.pre, "_diag_bias_factor", 1.0)
-        e["dtype"] = L.DTYPE_CODE[it.p.dtype]
+                diag = it.pre.diag_ema.data_ptr()
+                dbias = getattr(it.pre, "_diag_bias_factor", 1.0)
         if it.aligned:
             flags |= L.PF_ALIGNED
-        e["flags"] = flags
-        e["pre_begin"], e["pre_end"], e["post_begin"], e["post_end"] = ranges[i]
-        e["norm_index"] = i
+        cols["bc1"].append(bc1 if it.phase2 else 0.0)
+        cols["bc2"].append(bc2 if it.phase2 else 0.0)
+        cols["bc3"].append(bc3)
+        cols["blend"].append(blend)
+        cols["omblend"].append(omb)
+        cols["tau"].append(tau)
+        cols["lars"].append(lars)
+        cols["wd"].append(wdv)
+        cols["gsnr"].append(gs)
+        cols["diag_bias"].append(dbias)
+        cols["adam_sqrt_bc2"].append(sq)
+        cols["adam_alpha"].append(alpha)
+        cols["upd"].append(upd)
+        cols["diag_ema"].append(diag)
+        cols["dtype"].append(L.DTYPE_CODE[it.p.dtype])
+        cols["flags"].append(flags)
+    for k, v in cols.items():
+        tab[k] = np.asarray(v, dtype=tab.dtype.fields[k][0])
+    r = np.asarray(ranges, dtype=np.int32).reshape(n, 4)
+    tab["pre_begin"], tab["pre_end"] = r[:, 0], r[:, 1]
+    tab["post_begin"], tab["post_end"] = r[:, 2], r[:, 3]
+    tab["norm_index"] = np.arange(n, dtype=np.int32)
     return tab
 
 

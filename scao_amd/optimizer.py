@@ -427,6 +427,7 @@ class SCAO(Optimizer):
         extra = sd.pop("_scao_precond", {})
         rt = sd.pop("_scao_runtime", {})
         super().load_state_dict(sd)
+        self._restore_fp32_moments(sd)
         owner = {id(p): g for g in self.param_groups for p in g["params"]}
         for idx, (p, st) in enumerate(self.state.items()):
             if "preconditioner" in st and not isinstance(st["preconditioner"], SparsePreconditioner):
@@ -445,6 +446,29 @@ class SCAO(Optimizer):
             ws._early_exit_step = rt.get("warmup_early_exit_step", ws._early_exit_step)
         if self._ws is not None:
             self._ws.struct_key = None
+
+    def _restore_fp32_moments(self, sd: dict) -> None:
+        """``torch.optim.Optimizer.load_state_dict`` casts every floating state
+        tensor to its parameter's dtype.  The reference inherits that, so after
+        a resume its bf16/fp16 parameters carry reduced-precision moments,
+        although it creates them in fp32 (scao/optimizer.py:407-433).  The
+        step kernels keep fp32 statistics, so the moments are taken again from
+        the checkpoint at full precision, contiguous, on the parameter's
+        device."""
+        saved = [i for g in sd.get("param_groups", []) for i in g["params"]]
+        current = [p for g in self.param_groups for p in g["params"]]
+        for i, p in zip(saved, current):
+            src = sd.get("state", {}).get(i)
+            if not src or p not in self.state:
+                continue
+            st = self.state[p]
+            for key in ("exp_avg", "exp_avg_sq", "exp_avg_diff", "prev_grad"):
+                v, cur = src.get(key), st.get(key)
+                if not isinstance(v, Tensor) or not isinstance(cur, Tensor):
+                    continue
+                if cur.dtype != torch.float32:
+                    cur = v.to(device=p.device, dtype=torch.float32, copy=True)
+                st[key] = cur.contiguous()
 
     def current_ranks(self) -> dict:
         """reference :782-787."""

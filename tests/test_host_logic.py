@@ -104,6 +104,38 @@ def test_step_on_cpu_raises():
         opt.step()
 
 
+def test_load_state_dict_keeps_fp32_moments_for_bf16():
+    """torch's Optimizer.load_state_dict casts state to the parameter dtype, so
+    the reference (and the oracle, which inherits the same base) comes back
+    from a checkpoint with bf16 moments.  This build restores them as
+    bit-identical fp32 copies of the checkpoint's tensors."""
+    g = torch.Generator().manual_seed(5)
+    shapes = [(12, 20), (20,)]
+    rp = [torch.nn.Parameter(torch.randn(s, generator=g).bfloat16()) for s in shapes]
+    cfg = dict(lr=1e-2, warmup_steps=10, sparsity=0.0, noise_std_init=0.0,
+               async_precond=False, lookahead_k=0)
+    ref = R.RefSCAO(rp, **cfg)
+    for _ in range(2):
+        for p in rp:
+            p.grad = torch.randn(p.shape, generator=g).bfloat16()
+        ref.step()
+    sd = ref.state_dict()
+    assert sd["state"][0]["exp_avg"].dtype == torch.float32
+    mp = [torch.nn.Parameter(p.detach().clone()) for p in rp]
+    opt = scao_amd.SCAO(mp, **cfg)
+    opt.load_state_dict(sd)
+    for i, p in enumerate(mp):
+        for key in ("exp_avg", "exp_avg_sq", "exp_avg_diff", "prev_grad"):
+            got = opt.state[p][key]
+            assert got.dtype == torch.float32 and got.is_contiguous()
+            assert torch.equal(got, sd["state"][i][key])
+            assert got.data_ptr() != sd["state"][i][key].data_ptr()
+    # what the inherited base does (the reference's behaviour after a resume)
+    again = R.RefSCAO([torch.nn.Parameter(p.detach().clone()) for p in rp], **cfg)
+    again.load_state_dict(sd)
+    assert next(iter(again.state.values()))["exp_avg"].dtype == torch.bfloat16
+
+
 def test_presets_construct():
     m = torch.nn.Linear(16, 8)
     for f in (scao_amd.scao_sub1b, scao_amd.scao_1b, scao_amd.scao_3b, scao_amd.scao_7b,
