@@ -127,7 +127,9 @@ typedef struct scao_param_stat {
 #define SCAO_FLAT_CHUNK 4096
 /* Tile sizes of the Kronecker kernels. */
 #define SCAO_PROJ_COLS 256   /* columns of G per projection task (c-chunk of 64) */
-#define SCAO_APPLY_TILE 64   /* rows x cols per apply task                        */
+#define SCAO_APPLY_TILE 64   /* rows x cols per masked apply task                 */
+#define SCAO_APPLY_WIDE_ROWS 16   /* rows of a fast (variant bit 4) apply task    */
+#define SCAO_APPLY_WIDE_COLS 256  /* columns of a fast apply task                  */
 #define SCAO_GRAM_TILE 128   /* Gram output tile                                  */
 
 /* ---- library --------------------------------------------------------- */
@@ -184,7 +186,9 @@ int scao_step_finalize(const scao_param_desc* params, int nparams, const double*
  *     variant = (SCAO_PF_GF32 set ? 1 : 0) | (SCAO_PF_LARS set ? 2 : 0) |
  *     (fast ? 4 : 0); every task of a launch must belong to a parameter of
  *     that variant.  "fast" tasks promise fp32 data, SCAO_LF_VEC4,
- *     SCAO_PF_ALIGNED, a full 64x64 tile and k % 16 == 0. */
+ *     SCAO_PF_ALIGNED, k % 16 == 0 and a whole 16x256 tile at (a, b)
+ *     (SCAO_APPLY_WIDE_ROWS x SCAO_APPLY_WIDE_COLS); other tasks are masked
+ *     64x64 tiles (SCAO_APPLY_TILE) at (a, b), clipped to the block. */
 int scao_kron_apply(const scao_task* tasks, int ntasks, const scao_leaf_desc* leaves,
                     const scao_param_desc* params, const scao_param_stat* stat,
                     double* slots, int variant, void* stream);

@@ -372,18 +372,69 @@ __device__ __forceinline__ void corr_tile(const scao_leaf_desc& L, int i0, int j
 
 namespace {
 
-// One 64x64 tile of a block: the optimizer's whole Phase-2 elementwise tail
-// fused behind the back-projection.  Order of work per wave (16 rows x 64
-// columns, 16 elements per lane):
+// The Phase-2 elementwise tail for one row of four columns (t = 0..3):
+// gp = G + corr -> clip -> blend -> Adan moments -> update.  With LARS the
+// update itself is returned in `out` (the write waits for the trust ratio);
+// otherwise `out` is the new parameter value.  u2 accumulates u^2 over the
+// columns in `cmask`.  Operation order and roundings follow
+// scao/optimizer.py:584-645 (see the rounding notes on each line).
+template <bool GF32, bool LARS>
+__device__ __forceinline__ void adan4(const scao_param_desc& P, const scao_param_stat& S, int dt,
+                                      const v4f& gr, const v4f& gm, const v4f& corr, v4f& mm,
+                                      v4f& vv, v4f& dd, const v4f& pp, const v4f& par, v4f& out,
+                                      float& u2, int cmask) {
+  const bool clip = P.flags & SCAO_PF_CLIP;
+  const bool gsnr = P.flags & SCAO_PF_GSNR;
+  const bool decay = P.flags & SCAO_PF_DECAY;
+  const float alpha_nolars = round_to(dt, (float)(-P.lr));
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    float gp = round_to(dt, gr[t] + corr[t]);           // precondition() output in p.dtype
+    if (clip) gp = round_to(dt, gp * S.clip);           // gp * (tau / nu)
+    const float g = GF32 ? gm[t] : gr[t];
+    const float geff = P.blend * gp + P.omblend * g;    // b*gp.float() + (1-b)*grad
+    const float delta = g - pp[t];
+    const float m1 = fmaf(geff, P.omb1, mm[t] * P.beta1);
+    const float d1 = fmaf(delta, P.omb3, dd[t] * P.beta3);
+    const float gad = geff + P.omb3 * delta;
+    const float v1 = fmaf(P.omb2 * gad, gad, vv[t] * P.beta2);
+    float x = (m1 / P.bc1 + P.omb3 * (d1 / P.bc3)) / (sqrtf(v1 / P.bc2) + P.eps);
+    if (gsnr) x = x * ((fabsf(m1) / (sqrtf(v1) + P.eps)) >= P.gsnr ? 1.0f : 0.0f);
+    mm[t] = m1;
+    dd[t] = d1;
+    vv[t] = v1;
+    if (LARS) {
+      out[t] = x;
+      if (cmask & (1 << t)) u2 = fmaf(x, x, u2);
+    } else {
+      const float pd = decay ? round_to(dt, par[t] * P.decay) : par[t];
+      out[t] = round_to(dt, fmaf(round_to(dt, x), alpha_nolars, pd));
+    }
+  }
+}
+
+__device__ __forceinline__ void write_u2_slot(double* slots, int slot, float u2, double* red) {
+  if (slot < 0) return;
+  double x[1] = {(double)u2};
+  block_sum<1>(x, red);
+  if (threadIdx.x == 0) {
+    slots[(int64_t)slot * SCAO_SLOT_WIDTH + 0] = 0.0;
+    slots[(int64_t)slot * SCAO_SLOT_WIDTH + 1] = 0.0;
+    slots[(int64_t)slot * SCAO_SLOT_WIDTH + 2] = x[0];
+  }
+}
+
+// One 64x64 tile of a block, any shape, dtype or alignment (masked).  Per wave
+// 16 rows x 64 columns, 16 elements per lane:
 //   1. issue every elementwise load of the tile (g, m, v, d, prev [, p]) --
 //      they do not depend on the correction, so HBM latency overlaps step 2;
 //   2. corr = W[rows, :] U_r[cols, :]^T on MFMA, with the U_r tile (shared by
 //      the four waves) staged once per block through LDS, 64 columns of k at
 //      a time;
-//   3. gp = G + corr -> clip -> blend -> Adan -> update -> stores.
+//   3. the elementwise tail, then the stores.
 constexpr int UPAD = 68;   // LDS row pitch (floats) of the staged U_r tile
 
-template <bool GF32, bool LARS, bool FAST>
+template <bool GF32, bool LARS>
 __device__ __forceinline__ void apply_tile(const scao_leaf_desc& L, const scao_param_desc& P,
                                            const scao_param_stat& S, int i0, int j0, int slot,
                                            double* slots) {
@@ -391,19 +442,12 @@ __device__ __forceinline__ void apply_tile(const scao_leaf_desc& L, const scao_p
   __shared__ double red[16];
   const int w = threadIdx.x / 64, l = threadIdx.x % 64;
   const int m = L.m, n = L.n, k = L.k;
-  const int dt = FAST ? SCAO_F32 : P.dtype;
+  const int dt = P.dtype;
   const int kk = l / 16;
   const int jl = j0 + 4 * (l % 16);
   int cmask = 15;
-  if (!FAST)
-    for (int t = 0; t < 4; ++t) cmask = (jl + t < n) ? cmask : (cmask & ~(1 << t));
-  const bool vec = FAST || ((L.flags & SCAO_LF_VEC4) && cmask == 15);
-  constexpr bool gf32 = GF32;
-  constexpr bool lars = LARS;
-  const float* __restrict__ mA = P.exp_avg;
-  const float* __restrict__ vA = P.exp_avg_sq;
-  const float* __restrict__ dA = P.exp_avg_diff;
-  const float* __restrict__ pA = P.prev_grad;
+  for (int t = 0; t < 4; ++t) cmask = (jl + t < n) ? cmask : (cmask & ~(1 << t));
+  const bool vec = (L.flags & SCAO_LF_VEC4) && cmask == 15;
 
   // 1) prefetch
   v4f gr[4], gm[4], mm[4], vv[4], dd[4], pp[4], par[4];
@@ -413,26 +457,15 @@ __device__ __forceinline__ void apply_tile(const scao_leaf_desc& L, const scao_p
   for (int r = 0; r < 4; ++r) {
     const int i = i0 + 16 * w + 4 * kk + r;
     e[r] = L.off + (int64_t)i * L.ld + jl;
-    if (FAST) {
-      rok[r] = true;
-      gr[r] = gld4_nt((const float*)P.graw + e[r]);
-      if (gf32) gm[r] = gld4_nt((const float*)P.g + e[r]);
-      mm[r] = gld4_nt(mA + e[r]);
-      vv[r] = gld4_nt(vA + e[r]);
-      dd[r] = gld4_nt(dA + e[r]);
-      pp[r] = gld4_nt(pA + e[r]);
-      if (!lars) par[r] = gld4_nt((const float*)P.p + e[r]);
-    } else {
-      rok[r] = i < m && cmask;
-      const v4f z = {0.f, 0.f, 0.f, 0.f};
-      gr[r] = rok[r] ? ld4(P.graw, dt, e[r], vec, cmask) : z;
-      if (gf32) gm[r] = rok[r] ? ldf4((const float*)P.g, e[r], vec, cmask) : z;
-      mm[r] = rok[r] ? ldf4(mA, e[r], vec, cmask) : z;
-      vv[r] = rok[r] ? ldf4(vA, e[r], vec, cmask) : z;
-      dd[r] = rok[r] ? ldf4(dA, e[r], vec, cmask) : z;
-      pp[r] = rok[r] ? ldf4(pA, e[r], vec, cmask) : z;
-      if (!lars) par[r] = rok[r] ? ld4(P.p, dt, e[r], vec, cmask) : z;
-    }
+    rok[r] = i < m && cmask;
+    const v4f z = {0.f, 0.f, 0.f, 0.f};
+    gr[r] = rok[r] ? ld4(P.graw, dt, e[r], vec, cmask) : z;
+    gm[r] = (GF32 && rok[r]) ? ldf4((const float*)P.g, e[r], vec, cmask) : z;
+    mm[r] = rok[r] ? ldf4(P.exp_avg, e[r], vec, cmask) : z;
+    vv[r] = rok[r] ? ldf4(P.exp_avg_sq, e[r], vec, cmask) : z;
+    dd[r] = rok[r] ? ldf4(P.exp_avg_diff, e[r], vec, cmask) : z;
+    pp[r] = rok[r] ? ldf4(P.prev_grad, e[r], vec, cmask) : z;
+    par[r] = (!LARS && rok[r]) ? ld4(P.p, dt, e[r], vec, cmask) : z;
   }
 
   // 2) corr = W U_r^T
@@ -440,7 +473,7 @@ __device__ __forceinline__ void apply_tile(const scao_leaf_desc& L, const scao_p
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
   const int irow = i0 + 16 * w + (l % 16);
-  const bool kvec = FAST || (k % 4) == 0;
+  const bool kvec = (k % 4) == 0;
   for (int cb0 = 0; cb0 < k; cb0 += 64) {
     if (cb0) __syncthreads();
 #pragma unroll
@@ -448,14 +481,10 @@ __device__ __forceinline__ void apply_tile(const scao_leaf_desc& L, const scao_p
       const int idx = threadIdx.x + 256 * h;
       const int row = idx / 16, c4 = (idx % 16) * 4;
       const int j = j0 + row, c = cb0 + c4;
-      v4f x;
-      if (FAST && c + 3 < k) {
-        x = gld4(L.Ur + (int64_t)j * k + c);
-      } else {
-        int mk = 0;
-        for (int t = 0; t < 4; ++t) mk |= (j < n && c + t < k) ? (1 << t) : 0;
-        x = mk ? ldf4(L.Ur, (int64_t)j * k + c, kvec && mk == 15, mk) : v4f{0.f, 0.f, 0.f, 0.f};
-      }
+      int mk = 0;
+      for (int t = 0; t < 4; ++t) mk |= (j < n && c + t < k) ? (1 << t) : 0;
+      const v4f x = mk ? ldf4(L.Ur, (int64_t)j * k + c, kvec && mk == 15, mk)
+                       : v4f{0.f, 0.f, 0.f, 0.f};
       *(v4f*)&Us[row][c4] = x;
     }
     __syncthreads();
@@ -463,11 +492,9 @@ __device__ __forceinline__ void apply_tile(const scao_leaf_desc& L, const scao_p
     for (int cb = 0; cb < cend; cb += 16) {
       const int c = cb0 + cb + 4 * kk;
       int cm = 15;
-      if (!FAST)
-        for (int s = 0; s < 4; ++s) cm = (c + s < k) ? cm : (cm & ~(1 << s));
-      const v4f a = FAST ? gld4(L.W + (int64_t)irow * k + c)
-                         : ((irow < m && cm) ? ldf4(L.W, (int64_t)irow * k + c, kvec && cm == 15, cm)
-                                             : v4f{0.f, 0.f, 0.f, 0.f});
+      for (int s = 0; s < 4; ++s) cm = (c + s < k) ? cm : (cm & ~(1 << s));
+      const v4f a = (irow < m && cm) ? ldf4(L.W, (int64_t)irow * k + c, kvec && cm == 15, cm)
+                                     : v4f{0.f, 0.f, 0.f, 0.f};
       v4f b[4];
 #pragma unroll
       for (int t = 0; t < 4; ++t) b[t] = *(const v4f*)&Us[jl - j0 + t][cb + 4 * kk];
@@ -479,69 +506,103 @@ __device__ __forceinline__ void apply_tile(const scao_leaf_desc& L, const scao_p
   }
 
   // 3) elementwise tail
-  const bool clip = P.flags & SCAO_PF_CLIP;
-  const bool gsnr = P.flags & SCAO_PF_GSNR;
-  const bool decay = P.flags & SCAO_PF_DECAY;
-  const float alpha_nolars = round_to(dt, (float)(-P.lr));
   float u2 = 0.f;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     if (!rok[r]) continue;
-    v4f u, pn;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      float gp = round_to(dt, gr[r][t] + acc[t][r]);
-      if (clip) gp = round_to(dt, gp * S.clip);
-      const float g = gf32 ? gm[r][t] : gr[r][t];
-      const float geff = P.blend * gp + P.omblend * g;
-      const float delta = g - pp[r][t];
-      const float m1 = fmaf(geff, P.omb1, mm[r][t] * P.beta1);
-      const float d1 = fmaf(delta, P.omb3, dd[r][t] * P.beta3);
-      const float gad = geff + P.omb3 * delta;
-      const float v1 = fmaf(P.omb2 * gad, gad, vv[r][t] * P.beta2);
-      float x = (m1 / P.bc1 + P.omb3 * (d1 / P.bc3)) / (sqrtf(v1 / P.bc2) + P.eps);
-      if (gsnr) x = x * ((fabsf(m1) / (sqrtf(v1) + P.eps)) >= P.gsnr ? 1.0f : 0.0f);
-      mm[r][t] = m1;
-      dd[r][t] = d1;
-      vv[r][t] = v1;
-      u[t] = x;
-      if (lars) {
-        if (cmask & (1 << t)) u2 = fmaf(x, x, u2);
-      } else {
-        const float pd = decay ? round_to(dt, par[r][t] * P.decay) : par[r][t];
-        pn[t] = round_to(dt, fmaf(round_to(dt, x), alpha_nolars, pd));
-      }
-    }
-    if (FAST) {
-      gst4_nt(P.exp_avg + e[r], mm[r]);
-      gst4_nt(P.exp_avg_sq + e[r], vv[r]);
-      gst4_nt(P.exp_avg_diff + e[r], dd[r]);
-      gst4_nt(P.prev_grad + e[r], gf32 ? gm[r] : gr[r]);
-      if (lars)
-        gst4(P.upd + e[r], u);
-      else
-        gst4_nt((float*)P.p + e[r], pn);
-      continue;
-    }
+    const v4f corr = {acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+    v4f out;
+    adan4<GF32, LARS>(P, S, dt, gr[r], gm[r], corr, mm[r], vv[r], dd[r], pp[r], par[r], out, u2,
+                      cmask);
     stf4(P.exp_avg, e[r], mm[r], vec, cmask);
     stf4(P.exp_avg_sq, e[r], vv[r], vec, cmask);
     stf4(P.exp_avg_diff, e[r], dd[r], vec, cmask);
-    stf4(P.prev_grad, e[r], gf32 ? gm[r] : gr[r], vec, cmask);
-    if (lars) {
-      stf4(P.upd, e[r], u, vec, cmask);
-    } else {
-      st4(P.p, dt, e[r], pn, vec, cmask);
-    }
+    stf4(P.prev_grad, e[r], GF32 ? gm[r] : gr[r], vec, cmask);
+    if (LARS)
+      stf4(P.upd, e[r], out, vec, cmask);
+    else
+      st4(P.p, dt, e[r], out, vec, cmask);
   }
-  if (slot >= 0) {
-    double x[1] = {(double)u2};
-    block_sum<1>(x, red);
-    if (threadIdx.x == 0) {
-      slots[(int64_t)slot * SCAO_SLOT_WIDTH + 0] = 0.0;
-      slots[(int64_t)slot * SCAO_SLOT_WIDTH + 1] = 0.0;
-      slots[(int64_t)slot * SCAO_SLOT_WIDTH + 2] = x[0];
-    }
+  write_u2_slot(slots, slot, u2, red);
+}
+
+// One 16x256 tile, wholly inside an fp32 block whose rows are 16-byte
+// aligned, k % 16 == 0.  A 16-row x 1 KB footprint per block streams
+// measurably faster than 64 rows x 256 B.  Wave w owns columns
+// j0+64w .. j0+64w+63 of all 16 rows; lane l holds rows i0+4*(l/16)+r and
+// columns jl..jl+3, jl = j0+64w+4*(l%16).  The correction for those columns
+// needs U_r rows private to the wave, so they are read straight from L2 in
+// the MFMA B layout; the 16 rows of W are common to the four waves.
+template <bool GF32, bool LARS>
+__device__ __forceinline__ void apply_wide(const scao_leaf_desc& L, const scao_param_desc& P,
+                                           const scao_param_stat& S, int i0, int j0, int slot,
+                                           double* slots) {
+  __shared__ double red[16];
+  const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+  const int k = L.k;
+  const int kk = l / 16;
+  const int jl = j0 + 64 * w + 4 * (l % 16);
+
+  // 1) prefetch
+  v4f gr[4], gm[4], mm[4], vv[4], dd[4], pp[4], par[4];
+  int64_t e[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    e[r] = L.off + (int64_t)(i0 + 4 * kk + r) * L.ld + jl;
+    gr[r] = gld4_nt((const float*)P.graw + e[r]);
+    if (GF32) gm[r] = gld4_nt((const float*)P.g + e[r]);
+    mm[r] = gld4_nt(P.exp_avg + e[r]);
+    vv[r] = gld4_nt(P.exp_avg_sq + e[r]);
+    dd[r] = gld4_nt(P.exp_avg_diff + e[r]);
+    pp[r] = gld4_nt(P.prev_grad + e[r]);
+    if (!LARS) par[r] = gld4_nt((const float*)P.p + e[r]);
   }
+
+  // 2) corr = W U_r^T; reduction index c + 4*(l/16) + s for both operands
+  v4f acc[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+  const float* __restrict__ wrow = L.W + (int64_t)(i0 + l % 16) * k + 4 * kk;
+  const float* __restrict__ urow = L.Ur + (int64_t)jl * k + 4 * kk;
+  // operands of chunk c+16 are loaded while chunk c runs on MFMA
+  v4f a = gld4(wrow), b[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) b[t] = gld4(urow + (int64_t)t * k);
+  for (int c = 0; c < k; c += 16) {
+    const bool more = c + 16 < k;
+    v4f an = a, bn[4] = {b[0], b[1], b[2], b[3]};
+    if (more) {
+      an = gld4(wrow + c + 16);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) bn[t] = gld4(urow + (int64_t)t * k + c + 16);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[t] = mfma16(a[s], b[t][s], acc[t]);
+    a = an;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) b[t] = bn[t];
+  }
+
+  // 3) elementwise tail
+  float u2 = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const v4f corr = {acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+    v4f out;
+    adan4<GF32, LARS>(P, S, SCAO_F32, gr[r], gm[r], corr, mm[r], vv[r], dd[r], pp[r], par[r], out,
+                      u2, 15);
+    gst4_nt(P.exp_avg + e[r], mm[r]);
+    gst4_nt(P.exp_avg_sq + e[r], vv[r]);
+    gst4_nt(P.exp_avg_diff + e[r], dd[r]);
+    gst4_nt(P.prev_grad + e[r], GF32 ? gm[r] : gr[r]);
+    if (LARS)
+      gst4(P.upd + e[r], out);
+    else
+      gst4_nt((float*)P.p + e[r], out);
+  }
+  write_u2_slot(slots, slot, u2, red);
 }
 
 // Reference operator: out = G + W U_r^T (dense m x n output).
@@ -605,7 +666,10 @@ __global__ __launch_bounds__(256) void k_apply(const scao_task* __restrict__ tas
                                                double* slots) {
   const scao_task tk = tasks[blockIdx.x];
   const scao_leaf_desc L = leaves[tk.idx];
-  apply_tile<GF32, LARS, FAST>(L, params[L.param], stat[L.param], tk.a, tk.b, tk.slot, slots);
+  if (FAST)
+    apply_wide<GF32, LARS>(L, params[L.param], stat[L.param], tk.a, tk.b, tk.slot, slots);
+  else
+    apply_tile<GF32, LARS>(L, params[L.param], stat[L.param], tk.a, tk.b, tk.slot, slots);
 }
 
 // single-block reference operator (descriptors by value, tiles from blockIdx)

@@ -227,11 +227,25 @@ def _build_structure(items: list[PItem]):
                         tasks["lift"].append((li, i0, d0, -1))
                 var = (1 if it.gmom is not None else 0) | (2 if it.lars else 0)
                 ok = _leaf_vec(it, leaf, r0, c0l) and it.fp32 and it.aligned and k % 16 == 0
-                T = L.APPLY_TILE
-                for i0 in range(0, leaf.m, T):
-                    for j0 in range(0, leaf.n, T):
-                        fast = ok and i0 + T <= leaf.m and j0 + T <= leaf.n
-                        tasks[f"apply{var | (4 if fast else 0)}"].append((li, i0, j0, slot))
+                m, n, T = leaf.m, leaf.n, L.APPLY_TILE
+                # wide 16x256 tiles over the interior that they tile exactly,
+                # masked 64x64 tiles over the right column strip and the
+                # bottom row strip
+                mw = m - m % L.APPLY_WIDE_ROWS if ok else 0
+                nw = n - n % L.APPLY_WIDE_COLS if ok else 0
+                if not (mw and nw):
+                    mw = nw = 0
+                for i0 in range(0, mw, L.APPLY_WIDE_ROWS):
+                    for j0 in range(0, nw, L.APPLY_WIDE_COLS):
+                        tasks[f"apply{var | 4}"].append((li, i0, j0, slot))
+                        slot += 1
+                for i0 in range(0, m, T):
+                    for j0 in range(nw, n, T):
+                        tasks[f"apply{var}"].append((li, i0, j0, slot))
+                        slot += 1
+                for i0 in range(mw, m, T):
+                    for j0 in range(0, nw, T):
+                        tasks[f"apply{var}"].append((li, i0, j0, slot))
                         slot += 1
             ranges.append((pre_begin, pre_end, pre_end, slot))
         if it.lars:

@@ -124,8 +124,10 @@ def test_int8_ema_update(n, sc):
 SHAPES = {"w_col": (20, 80), "w_row": (70, 12), "w_kron": (12, 20), "w_conv": (4, 3, 2, 2),
           "b": (20,)}
 BIG = {"wq": (256, 256), "wk": (64, 256), "wup": (512, 256), "wdown": (256, 512), "ln": (256,)}
+# wide 16x256 apply tiles: whole (sq, wide, tall), with a masked right strip
+# (odd), and with right + bottom strips and their corner (ragged)
 FAST = {"sq": (512, 512), "wide": (256, 1024), "tall": (1024, 256), "odd": (320, 448),
-        "ln": (512,)}
+        "ragged": (328, 264), "ln": (512,)}
 
 CASES = {
     "int8_small": (SHAPES, dict(lr=1e-2, weight_decay=0.01, max_precond_dim=32, rho=0.99,

@@ -12,6 +12,7 @@ import torch
 import scao_amd
 from oracle import scao_ref as R
 from scao_amd import SparsePreconditioner
+from scao_amd import _lib as L
 from scao_amd import engine as E
 
 SHAPES = [(64, 64), (128, 16), (16, 128), (300, 64), (64, 300), (5000, 4100), (4, 3, 2, 2),
@@ -173,6 +174,38 @@ def test_engine_slots_cover_each_once():
     for i, it in enumerate(items):
         n = sum(1 for t in arrays["lars"] if t["idx"] == i)
         assert n == (E._flat_chunks(it.p.numel()) if it.phase2 and it.lars else 0)
+
+
+@pytest.mark.parametrize("shape,fp32", [((2048, 8192), True), ((328, 264), True),
+                                        ((320, 448), True), ((100, 37), True),
+                                        ((300, 520), True), ((512, 512), False)])
+def test_apply_tasks_tile_each_block_once(shape, fp32):
+    """Wide 16x256 tasks (variant bit 4) over the exactly tiled interior and
+    masked 64x64 tasks over the strips cover every element of every block
+    once; wide tasks lie wholly inside their block."""
+    from scao_amd.engine import PItem
+    p = torch.zeros(shape)
+    pre = SparsePreconditioner(p, k_min=16, k_max=64, max_precond_dim=2048, use_int8_ema=True)
+    it = PItem(p=p, graw=p, gmom=None, st={}, group={}, pre=pre, phase2=True, step=3,
+               lars=True, leaves=list(pre.leaves()), fp32=fp32)
+    arrays, _, _, leaves = E._build_structure([it])
+    seen_wide = False
+    for li, (leaf, r0, c0, _) in enumerate(leaves):
+        cover = np.zeros((leaf.m, leaf.n), np.int32)
+        for var in range(8):
+            for t in arrays[f"apply{var}"]:
+                if t["idx"] != li:
+                    continue
+                i0, j0 = int(t["a"]), int(t["b"])
+                if var & 4:
+                    seen_wide = True
+                    assert fp32
+                    assert i0 + L.APPLY_WIDE_ROWS <= leaf.m and j0 + L.APPLY_WIDE_COLS <= leaf.n
+                    cover[i0:i0 + L.APPLY_WIDE_ROWS, j0:j0 + L.APPLY_WIDE_COLS] += 1
+                else:
+                    cover[i0:i0 + L.APPLY_TILE, j0:j0 + L.APPLY_TILE] += 1
+        assert (cover == 1).all(), (shape, leaf.m, leaf.n)
+    assert seen_wide == (fp32 and shape[0] >= 16 and min(shape[1], 2048) >= 256)
 
 
 def test_golden_catches_planted_oracle_mistake(monkeypatch):
