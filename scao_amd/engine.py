@@ -251,9 +251,38 @@ def _build_structure(items: list[PItem]):
         if it.lars:
             for c in range(_flat_chunks(it.p.numel())):
                 tasks["lars"].append((pi, c, 0, -1))
+    for k in tasks:
+        if k.startswith("apply") or k.startswith("proj"):
+            tasks[k] = _xcd_interleave(tasks[k])
     arrays = {k: np.array(v, dtype=np.int32).reshape(-1, 4).copy().view(L.TASK).reshape(-1)
               for k, v in tasks.items()}
     return arrays, ranges, slot, leaves
+
+
+XCDS = 8   # MI355X: 8 accelerator dies, workgroup i is dispatched to die i % 8
+
+
+def _xcd_interleave(tasks: list) -> list:
+    """Order a launch's tasks so that every tile of one block runs on the same
+    die: the blocks are dealt to XCDS queues (largest first, each to the
+    least-loaded queue) and the queues are interleaved, so workgroup i comes
+    from queue i % XCDS while all queues last.  Each die's L2 then fetches a
+    block's shared operands (U_l; W and U_r) once instead of every die doing
+    so.  Only the order changes: tasks, slots and sums are the same."""
+    if len(tasks) <= XCDS:
+        return tasks
+    groups: dict = {}
+    for t in tasks:
+        groups.setdefault(t[0], []).append(t)
+    queues = [[] for _ in range(XCDS)]
+    for g in sorted(groups.values(), key=len, reverse=True):
+        min(queues, key=len).extend(g)
+    out = []
+    for i in range(max(len(q) for q in queues)):
+        for q in queues:
+            if i < len(q):
+                out.append(q[i])
+    return out
 
 
 def _cols(t: Tensor) -> int:
