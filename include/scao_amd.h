@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define SCAO_ABI_VERSION 1
+#define SCAO_ABI_VERSION 3
 
 enum scao_status { SCAO_OK = 0, SCAO_ERR_INVALID = 1, SCAO_ERR_HIP = 2 };
 enum scao_dtype { SCAO_F32 = 0, SCAO_BF16 = 1, SCAO_F16 = 2 };
@@ -229,14 +229,41 @@ typedef struct scao_prep_desc {
   const double* scale;      /* device scale (int8)                               */
   const float* ema;         /* fp32 EMA (when q is NULL)                         */
   float* out;               /* dim x dim                                         */
+  float* shift;             /* one float of device scratch: the diagonal shift   */
   int32_t dim;
   float bias;               /* fp32(max(bias_factor, 1e-8))                      */
 } scao_prep_desc;
 int scao_eig_prep(const scao_task* tasks, int ntasks, const scao_prep_desc* descs,
-                  void* stream);
+                  int ndescs, void* stream);
 /* diag_ema = fp32(diag*rho) + fp32(alpha * g*g)  (1-D preconditioners). */
 int scao_diag_ema(const scao_task* tasks, int ntasks, const scao_param_desc* params,
                   const float* rho_alpha, void* stream);
+
+/* ---- sparse gradient filter ----------------------------------------------
+ * Replaces _SparseGradFilter.__call__ (scao/optimizer.py:49-57) for a batch
+ * of parameters: ema = |g| (first) or fp32(fp32(ema*decay) + fp32(omd*|g|));
+ * t = torch.quantile(ema, q) (linear interpolation, exact order statistics by
+ * radix select); out = fp32(g) * (ema >= t).  torch.quantile refuses more than
+ * 2^24 elements; this entry point has no such limit.  Tasks are
+ * (desc index, chunk of SCAO_FLAT_CHUNK elements, 0, -1). */
+#define SCAO_FILTER_BINS 2048
+#define SCAO_FILTER_WORK_WORDS (2 * SCAO_FILTER_BINS + 8)
+typedef struct scao_filter_desc {
+  const void* g;            /* gradient (dtype), numel elements                  */
+  float* ema;               /* magnitude EMA, updated in place                   */
+  float* out;               /* filtered fp32 gradient                            */
+  uint32_t* work;           /* SCAO_FILTER_WORK_WORDS words of device scratch per
+                               desc: zero before its first call; every call
+                               leaves it ready for the next                      */
+  int64_t numel;
+  float decay, omd;         /* fp32(ema), fp32(1 - ema)                          */
+  float q;                  /* fp32(sparsity)                                    */
+  int32_t dtype;
+  int32_t first;            /* 1 on the filter's first call (ema = |g|)          */
+  int32_t pad0;
+} scao_filter_desc;
+int scao_sparse_filter(const scao_task* tasks, int ntasks, const scao_filter_desc* descs,
+                       int ndescs, void* stream);
 
 #ifdef __cplusplus
 }

@@ -21,7 +21,7 @@ import torch  # noqa: F401  -- loads torch's HIP runtime before ours
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("SCAO_AMD_LIB", os.path.join(HERE, "_lib", "libscao_amd.so"))
 
-ABI_VERSION = 1
+ABI_VERSION = 3
 SLOT_WIDTH = 3
 FLAT_CHUNK = 4096
 PROJ_COLS = 256
@@ -71,15 +71,23 @@ GRAM_DESC = np.dtype([
 ], align=True)
 
 PREP_DESC = np.dtype([
-    ("q", "u8"), ("scale", "u8"), ("ema", "u8"), ("out", "u8"), ("dim", "i4"), ("bias", "f4"),
+    ("q", "u8"), ("scale", "u8"), ("ema", "u8"), ("out", "u8"), ("shift", "u8"), ("dim", "i4"),
+    ("bias", "f4"),
 ], align=True)
+
+FILTER_DESC = np.dtype([
+    ("g", "u8"), ("ema", "u8"), ("out", "u8"), ("work", "u8"), ("numel", "i8"),
+    ("decay", "f4"), ("omd", "f4"), ("q", "f4"), ("dtype", "i4"), ("first", "i4"), ("pad0", "i4"),
+], align=True)
+FILTER_WORK_WORDS = 2 * 2048 + 8
 
 STRUCTS = {0: (PARAM_DESC, [n for n in PARAM_DESC.names if n != "pad0"]),
            1: (LEAF_DESC, [n for n in LEAF_DESC.names if n != "pad0"]),
            2: (TASK, list(TASK.names)),
            3: (PARAM_STAT, [n for n in PARAM_STAT.names if n != "pad0"]),
            4: (GRAM_DESC, [n for n in GRAM_DESC.names if n != "pad0"]),
-           5: (PREP_DESC, list(PREP_DESC.names))}
+           5: (PREP_DESC, list(PREP_DESC.names)),
+           6: (FILTER_DESC, [n for n in FILTER_DESC.names if n != "pad0"])}
 
 _VP, _I, _I64, _D = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_double
 
@@ -103,8 +111,9 @@ SIGNATURES = {
     "scao_adam_step": (_I, [_VP, _I, _VP, _VP, _VP]),
     "scao_gram_ema": (_I, [_VP, _I, _VP, _VP]),
     "scao_requant": (_I, [_VP, _I, _VP, _VP, _VP]),
-    "scao_eig_prep": (_I, [_VP, _I, _VP, _VP]),
+    "scao_eig_prep": (_I, [_VP, _I, _VP, _I, _VP]),
     "scao_diag_ema": (_I, [_VP, _I, _VP, _VP, _VP]),
+    "scao_sparse_filter": (_I, [_VP, _I, _VP, _I, _VP]),
 }
 
 

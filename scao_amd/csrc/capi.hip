@@ -85,7 +85,15 @@ extern "C" int scao_struct_layout(int which, int64_t* out, int cap) {
       typedef scao_prep_desc S;
       PUT(sizeof(S));
       PUT(offsetof(S, q)); PUT(offsetof(S, scale)); PUT(offsetof(S, ema)); PUT(offsetof(S, out));
-      PUT(offsetof(S, dim)); PUT(offsetof(S, bias));
+      PUT(offsetof(S, shift)); PUT(offsetof(S, dim)); PUT(offsetof(S, bias));
+      break;
+    }
+    case 6: {
+      typedef scao_filter_desc S;
+      PUT(sizeof(S));
+      PUT(offsetof(S, g)); PUT(offsetof(S, ema)); PUT(offsetof(S, out)); PUT(offsetof(S, work));
+      PUT(offsetof(S, numel)); PUT(offsetof(S, decay)); PUT(offsetof(S, omd));
+      PUT(offsetof(S, q)); PUT(offsetof(S, dtype)); PUT(offsetof(S, first));
       break;
     }
     default:

@@ -18,11 +18,6 @@ using namespace scao;
 
 namespace {
 
-__device__ __forceinline__ bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
-__device__ __forceinline__ bool al_dt(const void* p, int dt) {
-  return dt == SCAO_F32 ? al16(p) : (((uintptr_t)p & 7u) == 0);
-}
-
 // element range of a flat task and this thread's 4 groups of 4 elements
 struct Chunk {
   int64_t base, end;

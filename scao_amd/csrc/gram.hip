@@ -145,9 +145,29 @@ __global__ __launch_bounds__(256) void k_gram_ema(const scao_task* __restrict__ 
 
 // Requantise x[0:n) given the per-tile maxima; divide (utils.quantize_sym_int8)
 // or multiply by the fp32 reciprocal (the int8_ema_update operator).
+// Code for one value: rint(y) clamped to +-127 (rintf rounds half to even,
+// as torch.round does).
+__device__ __forceinline__ uint32_t code_of(float y) {
+  return (uint32_t)(uint8_t)(int8_t)(int)fminf(fmaxf(rintf(y), -127.f), 127.f);
+}
+
+// Requantise one SCAO_FLAT_CHUNK-element chunk of x into q.  The scale is
+// max|x| / 127 in double from the per-tile maxima amax[0..nparts); `recip`
+// selects the reference operator's reciprocal multiply
+// (scao/cuda/__init__.py:122-142) instead of quantize_sym_int8's division
+// (scao/utils.py:170-189).  Whole, aligned chunks stream 4 values per load
+// and store 4 codes per 32-bit write, each wave covering 1 KB of x per
+// instruction; other chunks go element by element.
 __device__ __forceinline__ void requant_chunk(const float* x, int64_t n, const float* amax, int nparts,
                               int8_t* q, double* scale_out, int chunk, bool recip) {
   __shared__ float red[4];
+  const int64_t base = (int64_t)chunk * SCAO_FLAT_CHUNK;
+  const bool vec = base + SCAO_FLAT_CHUNK <= n && (((uintptr_t)x | (uintptr_t)q) & 15) == 0;
+  v4f v[4];
+  if (vec) {   // the chunk's loads go out before the scale is known
+#pragma unroll
+    for (int j = 0; j < 4; ++j) v[j] = gld4_nt(x + base + 4 * (threadIdx.x + 256 * j));
+  }
   float mx = 0.f;
   for (int i = threadIdx.x; i < nparts; i += 256) mx = fmaxf(mx, amax[i]);
   mx = block_max(mx, red);
@@ -166,18 +186,23 @@ __device__ __forceinline__ void requant_chunk(const float* x, int64_t n, const f
     div = (float)scale;
   }
   if (chunk == 0 && threadIdx.x == 0) *scale_out = scale;
-  const int64_t base = (int64_t)chunk * SCAO_FLAT_CHUNK;
+  if (vec) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t w = 0;
+      if (!zero) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          w |= code_of(recip ? v[j][t] * mul : v[j][t] / div) << (8 * t);
+      }
+      gst1((uint32_t*)(q + base) + threadIdx.x + 256 * j, w);
+    }
+    return;
+  }
   for (int t = threadIdx.x; t < SCAO_FLAT_CHUNK; t += 256) {
     const int64_t e = base + t;
     if (e >= n) break;
-    float c;
-    if (zero) {
-      c = 0.f;
-    } else {
-      const float y = recip ? x[e] * mul : x[e] / div;
-      c = fminf(fmaxf(rintf(y), -127.f), 127.f);
-    }
-    q[e] = (int8_t)(int)c;
+    q[e] = zero ? (int8_t)0 : (int8_t)code_of(recip ? x[e] * mul : x[e] / div);
   }
 }
 
@@ -190,36 +215,83 @@ __global__ __launch_bounds__(256) void k_requant(const scao_task* __restrict__ t
   requant_chunk(D.ema, (int64_t)dim * dim, D.amax, D.ntiles, D.q, scale_out[tk.idx], tk.a, false);
 }
 
-__global__ __launch_bounds__(256) void k_eig_prep(const scao_task* __restrict__ tasks,
-                                                  const scao_prep_desc* __restrict__ descs) {
+// eigh input, pass 1 (one block per factor): shift = fp32(max(1e-8,
+// 1e-4 * fp32(tr X) / dim)), the trace summed in double in a fixed order.
+__device__ __forceinline__ float prep_val(const scao_prep_desc& D, float sf, int64_t e) {
+  const float x = D.q ? (float)D.q[e] * sf : D.ema[e];
+  return x / D.bias;
+}
+__global__ __launch_bounds__(256) void k_eig_trace(const scao_prep_desc* __restrict__ descs) {
   __shared__ double red[16];
-  const scao_task tk = tasks[blockIdx.x];
-  const scao_prep_desc D = descs[tk.idx];
+  const scao_prep_desc D = descs[blockIdx.x];
   const int dim = D.dim;
   const float sf = D.q ? (float)(*D.scale) : 0.f;
-  auto val = [&](int64_t e) -> float {
-    const float x = D.q ? (float)D.q[e] * sf : D.ema[e];
-    return x / D.bias;
-  };
   double tr = 0.0;
-  for (int i = threadIdx.x; i < dim; i += 256) tr += (double)val((int64_t)i * dim + i);
+  for (int i = threadIdx.x; i < dim; i += 256) tr += (double)prep_val(D, sf, (int64_t)i * dim + i);
   double x[1] = {tr};
   block_sum<1>(x, red);
-  __shared__ float eps_s;
   if (threadIdx.x == 0) {
     const float tr_f = (float)x[0];
     double eps = 1e-4 * (double)tr_f / (double)dim;
     if (eps < 1e-8) eps = 1e-8;
-    eps_s = (float)eps;
+    *D.shift = (float)eps;
   }
-  __syncthreads();
-  const float eps = eps_s;
+}
+
+// eigh input, pass 2: X = deq / fp32(bias) (+ shift on the diagonal), one
+// SCAO_FLAT_CHUNK-element chunk per block.  Whole aligned chunks of a
+// dim % 4 == 0 factor read 4 codes (or 4 fp32) per load and write a float4,
+// each wave covering a contiguous stretch per instruction.
+__global__ __launch_bounds__(256) void k_eig_prep(const scao_task* __restrict__ tasks,
+                                                  const scao_prep_desc* __restrict__ descs) {
+  const scao_task tk = tasks[blockIdx.x];
+  const scao_prep_desc D = descs[tk.idx];
+  const int dim = D.dim;
   const int64_t n = (int64_t)dim * dim;
   const int64_t base = (int64_t)tk.a * SCAO_FLAT_CHUNK;
+  const uintptr_t src = D.q ? (uintptr_t)D.q : (uintptr_t)D.ema;
+  const bool vec = dim % 4 == 0 && base + SCAO_FLAT_CHUNK <= n && n < (1LL << 31) &&
+                   ((src | (uintptr_t)D.out) & 15) == 0;
+  if (vec) {
+    // the chunk's loads go out before the scale and shift are read
+    v4f x[4];
+    uint32_t w[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t e = base + 4 * (threadIdx.x + 256 * j);
+      if (D.q)
+        w[j] = gld1((const uint32_t*)(D.q + e));
+      else
+        x[j] = gld4_nt(D.ema + e);
+    }
+    const float sf = D.q ? (float)(*D.scale) : 0.f;
+    const float eps = *D.shift;
+    if (D.q) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) x[j][t] = (float)(int8_t)(w[j] >> (8 * t)) * sf;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int e = (int)(base + 4 * (threadIdx.x + 256 * j));
+      const int row = e / dim, col = e - row * dim;
+      v4f y;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        y[t] = x[j][t] / D.bias;
+        if (col + t == row) y[t] = y[t] + eps;
+      }
+      gst4_nt(D.out + e, y);
+    }
+    return;
+  }
+  const float sf = D.q ? (float)(*D.scale) : 0.f;
+  const float eps = *D.shift;
   for (int t = threadIdx.x; t < SCAO_FLAT_CHUNK; t += 256) {
     const int64_t e = base + t;
     if (e >= n) break;
-    float y = val(e);
+    float y = prep_val(D, sf, e);
     if (e / dim == e % dim) y = y + eps;
     D.out[e] = y;
   }
@@ -275,11 +347,13 @@ extern "C" int scao_requant(const scao_task* tasks, int ntasks, const scao_gram_
 }
 
 extern "C" int scao_eig_prep(const scao_task* tasks, int ntasks, const scao_prep_desc* descs,
-                             void* stream) {
-  SCAO_CHECK_ARG(ntasks >= 0, "scao_eig_prep: ntasks < 0");
+                             int ndescs, void* stream) {
+  SCAO_CHECK_ARG(ntasks >= 0 && ndescs >= 0, "scao_eig_prep: negative count");
   if (ntasks == 0) return SCAO_OK;
-  SCAO_CHECK_ARG(tasks && descs, "scao_eig_prep: null pointer");
-  hipLaunchKernelGGL(k_eig_prep, dim3(ntasks), dim3(256), 0, (hipStream_t)stream, tasks, descs);
+  SCAO_CHECK_ARG(tasks && descs && ndescs > 0, "scao_eig_prep: null pointer");
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_eig_trace, dim3(ndescs), dim3(256), 0, s, descs);
+  hipLaunchKernelGGL(k_eig_prep, dim3(ntasks), dim3(256), 0, s, tasks, descs);
   SCAO_LAUNCH_CHECK("scao_eig_prep");
   return SCAO_OK;
 }

@@ -70,6 +70,14 @@ __device__ __forceinline__ void gst4_nt(float* p, v4f x) {
 }
 __device__ __forceinline__ float gld1(const float* p) { return *(const gfloat*)p; }
 __device__ __forceinline__ void gst1(float* p, float x) { *(gfloat*)p = x; }
+// 16-byte alignment for fp32 float4 access, 8-byte for a 16-bit dtype's 4-pack
+__device__ __forceinline__ bool al16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+__device__ __forceinline__ bool al_dt(const void* p, int dt) {
+  return dt == SCAO_F32 ? al16(p) : (((uintptr_t)p & 7u) == 0);
+}
+typedef __attribute__((address_space(1))) uint32_t gu32;
+__device__ __forceinline__ uint32_t gld1(const uint32_t* p) { return *(const gu32*)p; }
+__device__ __forceinline__ void gst1(uint32_t* p, uint32_t x) { *(gu32*)p = x; }
 
 __device__ __forceinline__ float ld1(const void* base, int dt, int64_t i) {
   if (dt == SCAO_F32) return gld1((const float*)base + i);

@@ -505,6 +505,66 @@ def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
     ws.last_params = params   # keep descriptors alive until the next step
 
 
+# --------------------------------------------------------------------------
+# sparse gradient filter (reference scao/optimizer.py:42-57)
+# --------------------------------------------------------------------------
+
+_FILTER_TASKS: dict = {}
+
+
+def _filter_tasks(numels: tuple, dev) -> Tensor:
+    """Device task list (desc, chunk) for a tuple of element counts, cached."""
+    key = (numels, str(dev))
+    t = _FILTER_TASKS.get(key)
+    if t is None:
+        counts = np.array([_flat_chunks(n) for n in numels], dtype=np.int64)
+        arr = np.zeros((int(counts.sum()), 4), dtype=np.int32)
+        arr[:, 0] = np.repeat(np.arange(len(numels), dtype=np.int32), counts)
+        starts = np.repeat(np.cumsum(counts) - counts, counts)
+        arr[:, 1] = np.arange(int(counts.sum()), dtype=np.int64) - starts
+        arr[:, 3] = -1
+        t = L.upload(arr.view(L.TASK).reshape(-1), dev)
+        if len(_FILTER_TASKS) > 16:
+            _FILTER_TASKS.clear()
+        _FILTER_TASKS[key] = t
+    return t
+
+
+def sparse_filter(entries) -> list:
+    """Run the filter for [(filter, grad)] in one batched launch sequence and
+    return each filtered fp32 gradient.  ``filter`` carries ``mag_ema`` (None
+    before its first call), ``work`` (zeroed device scratch, allocated here)
+    and ``sparsity``; gradients must be contiguous, on one device."""
+    entries = [(f, g) for f, g in entries if g.numel() > 0]
+    if not entries:
+        return []
+    dev = entries[0][1].device
+    descs = np.zeros(len(entries), dtype=L.FILTER_DESC)
+    outs = []
+    for i, (f, g) in enumerate(entries):
+        require_hip(g, "sparse filter gradient")
+        first = f.mag_ema is None
+        if first:
+            f.mag_ema = torch.empty(g.shape, dtype=torch.float32, device=dev)
+        if getattr(f, "work", None) is None or f.work.device != dev:
+            f.work = torch.zeros(L.FILTER_WORK_WORDS, dtype=torch.int32, device=dev)
+        out = torch.empty(g.shape, dtype=torch.float32, device=dev)
+        outs.append(out)
+        e = descs[i]
+        e["g"], e["ema"], e["out"] = g.data_ptr(), f.mag_ema.data_ptr(), out.data_ptr()
+        e["work"] = f.work.data_ptr()
+        e["numel"] = g.numel()
+        e["decay"], e["omd"], e["q"] = f.ema, 1.0 - f.ema, f.sparsity
+        e["dtype"] = L.DTYPE_CODE[g.dtype]
+        e["first"] = 1 if first else 0
+    tasks = _filter_tasks(tuple(int(g.numel()) for _, g in entries), dev)
+    dd = L.upload(descs, dev)
+    _call("scao_sparse_filter", tasks.data_ptr(), tasks.numel() // L.TASK.itemsize,
+          dd.data_ptr(), len(entries), L.stream_ptr(dev))
+    it = iter(outs)
+    return [next(it) for _ in entries]
+
+
 def _grads_moved(items, ws) -> bool:
     ptrs = getattr(ws, "grad_ptrs", None)
     return ptrs is None or len(ptrs) != len(items) or any(
@@ -710,6 +770,7 @@ def _gram_chunk(chunk, dev, s):
 
 def _eig_inputs(part, dim, dev, s) -> Tensor:
     X = torch.empty(len(part), dim, dim, dtype=torch.float32, device=dev)
+    shift = torch.empty(len(part), dtype=torch.float32, device=dev)
     descs, tasks = [], []
     nchunk = _flat_chunks(dim * dim)
     for i, (leaf, side) in enumerate(part):
@@ -718,6 +779,7 @@ def _eig_inputs(part, dim, dev, s) -> Tensor:
         e["bias"] = max(bias, 1e-8)
         e["dim"] = dim
         e["out"] = X[i].data_ptr()
+        e["shift"] = shift.data_ptr() + 4 * i
         if leaf.use_int8_ema:
             e["q"] = (leaf.L_ema_q if side == 0 else leaf.R_ema_q).data_ptr()
             e["scale"] = leaf._scale.data_ptr() + 8 * side
@@ -728,7 +790,7 @@ def _eig_inputs(part, dim, dev, s) -> Tensor:
     dd = L.upload(np.array(descs, dtype=L.PREP_DESC), dev)
     tt = np.array(tasks, dtype=np.int32).reshape(-1, 4).copy().view(L.TASK).reshape(-1)
     td = L.upload(tt, dev)
-    _call("scao_eig_prep", td.data_ptr(), len(tt), dd.data_ptr(), s)
+    _call("scao_eig_prep", td.data_ptr(), len(tt), dd.data_ptr(), len(descs), s)
     return X
 
 

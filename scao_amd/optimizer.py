@@ -35,20 +35,23 @@ from .preconditioner import SparsePreconditioner
 # --------------------------------------------------------------------------
 
 class _SparseGradFilter:
-    """reference :42-57.  Note torch.quantile's 2**24-element limit applies,
-    as in the reference."""
+    """reference :42-57: EMA of |g| and the mask ``ema >= quantile(ema, q)``.
+    The work runs in ``scao_sparse_filter`` (one batched launch sequence per
+    step, exact order statistics by radix select); ``__call__`` filters one
+    gradient through the same entry point.  torch.quantile refuses more than
+    2**24 elements, so the reference raises for such a parameter; this filter
+    computes the same statistic for any size."""
 
     def __init__(self, sparsity: float = 0.7, ema: float = 0.99):
         self.sparsity, self.ema, self.mag_ema = sparsity, ema, None
+        self.work = None          # device scratch of the batched kernel
+
+    def prepare(self, grad: Tensor) -> None:
+        """Host-side update before the batched launch (dynamic sparsity)."""
 
     def __call__(self, grad: Tensor) -> Tensor:
-        mag = grad.abs().detach()
-        if self.mag_ema is None:
-            self.mag_ema = mag.clone()
-        else:
-            self.mag_ema.mul_(self.ema).add_((1.0 - self.ema) * mag)
-        thr = torch.quantile(self.mag_ema.float(), self.sparsity)
-        return grad * (self.mag_ema >= thr).to(grad.dtype)
+        self.prepare(grad)
+        return engine.sparse_filter([(self, grad.contiguous())])[0]
 
 
 class _DynamicSparseFilter(_SparseGradFilter):
@@ -65,13 +68,13 @@ class _DynamicSparseFilter(_SparseGradFilter):
     def set_global_norm_ref(self, v: float) -> None:
         self._global_norm_ema = max(v, 1e-8)
 
-    def __call__(self, grad: Tensor) -> Tensor:
-        ln = float(grad.norm())
+    def prepare(self, grad: Tensor) -> None:
+        """reference :88-99: the sparsity for this call from the layer norm."""
+        ln = float(grad.float().norm())
         self._norm_ema = self.norm_ema_coeff * self._norm_ema + (1.0 - self.norm_ema_coeff) * ln
         ratio = self._norm_ema / self._global_norm_ema
         margin = 0.2 * (1.0 - min(ratio, 2.0) / 2.0)
         self.sparsity = float(max(self.min_sparsity, min(self.max_sparsity, self.base_sparsity + margin)))
-        return super().__call__(grad)
 
 
 class _AdaptiveWarmupScheduler:
@@ -297,10 +300,11 @@ class SCAO(Optimizer):
             wmax = max((g.get("warmup_steps", 100) for g in self.param_groups), default=100)
             self._in_warmup_global = self._global_step <= wmax
 
-        items, refresh = [], []
+        items, refresh, filtered = [], [], []
         for group, p in active:
-            it = self._plan_param(group, p, refresh)
+            it = self._plan_param(group, p, refresh, filtered)
             items.append(it)
+        self._filter_and_noise(items, filtered)
         engine.refresh(refresh)
         gsnr = self._gsnr_threshold if self._use_gsnr_clip else None
         if ws is not None:
@@ -319,7 +323,22 @@ class SCAO(Optimizer):
                 cb(metrics)
         return loss
 
-    def _plan_param(self, group: dict, p: Tensor, refresh: list) -> PItem:
+    def _filter_and_noise(self, items: list, filtered: list) -> None:
+        """The gradient the moments see (reference :533-545): every filtered
+        parameter of the step goes through one batched filter launch
+        sequence, then noise is added in parameter order."""
+        outs = engine.sparse_filter([(f, g) for _, f, g in filtered]) if filtered else []
+        by_item = {id(it): out for (it, _, _), out in zip(filtered, outs)}
+        for it in items:
+            grad = by_item.get(id(it))
+            if self._noise_std > 1e-9:
+                if grad is None:
+                    grad = it.graw.float()
+                grad = grad + torch.randn_like(grad) * self._noise_std
+            if grad is not None:
+                it.gmom = grad.contiguous()
+
+    def _plan_param(self, group: dict, p: Tensor, refresh: list, filtered: list) -> PItem:
         """Host half of reference _step_group (:521-605) for one parameter."""
         if p.grad.is_sparse:
             raise RuntimeError("SCAO does not support sparse gradients.")
@@ -333,18 +352,15 @@ class SCAO(Optimizer):
         graw = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
         need_gnorm = self._lazy_precond or self._adaptive_rank
         gnorm = float(graw.float().norm()) if need_gnorm else 0.0
-        gmom = None
-        if self._sparsity > 0.0 or self._noise_std > 1e-9:
-            grad = graw.float()
-            if self._sparsity > 0.0:
-                if pid not in self._sparse_filters:
-                    self._sparse_filters[pid] = (_DynamicSparseFilter(base_sparsity=self._sparsity)
-                                                 if self._dynamic_sparsity
-                                                 else _SparseGradFilter(self._sparsity))
-                grad = self._sparse_filters[pid](grad)
-            if self._noise_std > 1e-9:
-                grad = grad + torch.randn_like(grad) * self._noise_std
-            gmom = grad.contiguous()
+        gmom = None   # set by _filter_and_noise when filtered or noised
+        filt = None
+        if self._sparsity > 0.0:
+            if pid not in self._sparse_filters:
+                self._sparse_filters[pid] = (_DynamicSparseFilter(base_sparsity=self._sparsity)
+                                             if self._dynamic_sparsity
+                                             else _SparseGradFilter(self._sparsity))
+            filt = self._sparse_filters[pid]
+            filt.prepare(graw)
         pre: SparsePreconditioner = st["preconditioner"]
         self._maybe_adjust_rank(pre, gnorm, group)
         in_warmup = (self._in_warmup_global if self._adaptive_warmup
@@ -353,8 +369,11 @@ class SCAO(Optimizer):
         if in_warmup:
             if t % group["precond_freq"] == 0:
                 refresh.append((pre, p.grad))
-            return PItem(p=p, graw=graw, gmom=gmom, st=st, group=group, pre=pre,
-                         phase2=False, step=t)
+            it = PItem(p=p, graw=graw, gmom=gmom, st=st, group=group, pre=pre,
+                       phase2=False, step=t)
+            if filt is not None:
+                filtered.append((it, filt, graw))
+            return it
         if not st.get("scao_phase_started", False):
             st["scao_phase_started"] = True
             st["phase2_start_step"] = t
@@ -370,9 +389,12 @@ class SCAO(Optimizer):
         if should:
             refresh.append((pre, p.grad))
         diag = not (pre.use_block_diagonal or pre.use_kronecker)
-        return PItem(p=p, graw=graw, gmom=gmom, st=st, group=group, pre=pre, phase2=True,
-                     step=t, scao_step=st["scao_step"], lars=group["lars_coeff"] > 0,
-                     diag=diag, leaves=[] if diag else list(pre.leaves()))
+        it = PItem(p=p, graw=graw, gmom=gmom, st=st, group=group, pre=pre, phase2=True,
+                   step=t, scao_step=st["scao_step"], lars=group["lars_coeff"] > 0,
+                   diag=diag, leaves=[] if diag else list(pre.leaves()))
+        if filt is not None:
+            filtered.append((it, filt, graw))
+        return it
 
     # ------------------------------------------------------------ misc ---
     def synchronize_precond(self) -> None:
