@@ -148,6 +148,9 @@ def main():
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="before timing, copy a buffer of this size once (a plain copy "
                          "kernel of known size to calibrate traffic counters)")
+    ap.add_argument("--sparse-steps", type=int, default=3,
+                    help="steady steps timed afterwards with the reference's default sparse "
+                         "gradient filter (sparsity=0.7), reported in details (0: skip)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -244,6 +247,29 @@ def main():
     engine.TIMING = None
     assert all(opt.state[p].get("scao_phase_started") for p in pre_p), "not in Phase 2"
 
+    # diagnostic (not the headline): the reference's default sparse gradient
+    # filter (sparsity=0.7) switched on for a few steady steps
+    sparse = None
+    if args.sparse_steps > 0:
+        opt._sparsity = 0.7
+        one()                                 # first filter call: EMA = |g|
+        engine.TIMING, engine.TIMING_ONLY = {}, {"scao_sparse_filter"}
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        for _ in range(args.sparse_steps):
+            one()
+        torch.cuda.synchronize()
+        sp_ms = (time.perf_counter() - t2) * 1e3 / args.sparse_steps
+        filt = engine.timing_summary().get("scao_sparse_filter")
+        engine.TIMING, engine.TIMING_ONLY = None, None
+        opt._sparsity = PROFILE["sparsity"]
+        f_ms = filt[1] if filt else None
+        sparse = {"sparsity": 0.7, "steady_step_ms": sp_ms, "filter_ms": f_ms,
+                  "filter_elements": nparams,
+                  # EMA pass 12 B, two radix passes 4 B each, mask pass 12 B
+                  "filter_GBps_at_32B_per_elem": (32.0 * nparams / (f_ms / 1e3) / 1e9
+                                                  if f_ms else None)}
+
     # ---- roofline of the dominant kernel --------------------------------
     dom = args.dominant
     if dom not in dom_timing:
@@ -281,6 +307,7 @@ def main():
         "refresh_parts_ms": {k: {"count": c, "mean": m_, "total": t}
                              for k, (c, m_, t) in refresh_parts.items()},
         "first_step_ms": t_first,
+        "default_sparse_filter": sparse,
         "step_roofline": {"alg_bytes": step_bytes, "alg_flops": step_flops,
                           "hbm_frac": step_bytes / (ms / 1e3) / HBM_PEAK,
                           "hbm_floor_ms": step_bytes / HBM_PEAK * 1e3,
@@ -307,7 +334,8 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "details": {"phase1_step_ms": t_phase1, "refresh_step_ms": t_refresh,
-                    "step_hbm_frac": details["step_roofline"]["hbm_frac"]},
+                    "step_hbm_frac": details["step_roofline"]["hbm_frac"],
+                    "steady_step_sparsity07_ms": sparse["steady_step_ms"] if sparse else None},
     }
     if args.details:
         with open(args.details, "w") as f:

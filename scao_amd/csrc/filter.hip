@@ -125,44 +125,81 @@ __global__ __launch_bounds__(256) void k_filter_ema(const scao_task* __restrict_
 }
 
 // -------------------------------------------- passes 1, 2: digits 1, 2 ---
+// A block takes FH consecutive tasks.  All their loads go out first (nothing
+// they read depends on the selection state); the LDS histograms are flushed
+// to the parameter's global ones whenever the next task belongs to another
+// parameter, and at the end.
+constexpr int FH = 4;
+
 __global__ __launch_bounds__(256) void k_filter_hist(const scao_task* __restrict__ tasks,
+                                                     int ntasks,
                                                      const scao_filter_desc* __restrict__ descs,
                                                      int pass) {
   __shared__ uint32_t h[2][NB];
-  const scao_task tk = tasks[blockIdx.x];
-  const scao_filter_desc& D = descs[tk.idx];
-  const FState* S = state_of(D);
-  const FChunk ch(tk, D.numel);
+  const int t0 = blockIdx.x * FH;
+  const int nt = ntasks - t0 < FH ? ntasks - t0 : FH;
+  v4f e[FH][4];
+  int mk[FH][4];
+#pragma unroll
+  for (int c = 0; c < FH; ++c) {
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp) mk[c][grp] = 0;
+    if (c >= nt) continue;
+    const scao_task tk = tasks[t0 + c];
+    const scao_filter_desc& D = descs[tk.idx];
+    const FChunk ch(tk, D.numel);
+    const bool vec = ((uintptr_t)D.ema & 15) == 0;
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp) {
+      const int64_t i = ch.elem(grp);
+      mk[c][grp] = ch.mask(i);
+      e[c][grp] = mk[c][grp] ? ldf4(D.ema, i, vec && mk[c][grp] == 15, mk[c][grp])
+                             : v4f{0.f, 0.f, 0.f, 0.f};
+    }
+  }
   const int sh_prev = SHIFT[pass - 1], sh = SHIFT[pass];
   const uint32_t dm = DMASK[pass];
-  const uint32_t p0 = S->prefix[0], p1 = S->prefix[1];
-  const bool split = S->split != 0u;
   const int nb = (int)dm + 1;
-  zero_lds(&h[0][0], split ? 2 * NB : NB);
-  const bool vec = ((uintptr_t)D.ema & 15) == 0;
-  v4f e[4];
-  int mk[4];
+  zero_lds(&h[0][0], 2 * NB);
+  int cur = -1;
+  uint32_t p0 = 0, p1 = 0;
+  bool split = false;
 #pragma unroll
-  for (int grp = 0; grp < 4; ++grp) {
-    const int64_t i = ch.elem(grp);
-    mk[grp] = ch.mask(i);
-    e[grp] = mk[grp] ? ldf4(D.ema, i, vec && mk[grp] == 15, mk[grp]) : v4f{0.f, 0.f, 0.f, 0.f};
-  }
-  __syncthreads();
+  for (int c = 0; c < FH; ++c) {
+    if (c >= nt) break;
+    const int idx = tasks[t0 + c].idx;
+    if (idx != cur) {
+      if (cur >= 0) {
+        __syncthreads();
+        flush(&h[0][0], hist_of(descs[cur], 0), nb);
+        if (split) flush(&h[1][0], hist_of(descs[cur], 1), nb);
+        __syncthreads();
+        zero_lds(&h[0][0], 2 * NB);
+      }
+      cur = idx;
+      const FState* S = state_of(descs[cur]);
+      p0 = S->prefix[0];
+      p1 = S->prefix[1];
+      split = S->split != 0u;
+      __syncthreads();
+    }
 #pragma unroll
-  for (int grp = 0; grp < 4; ++grp) {
+    for (int grp = 0; grp < 4; ++grp) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      if (!(mk[grp] & (1 << t))) continue;
-      const uint32_t key = __float_as_uint(e[grp][t]);
-      const uint32_t top = key >> sh_prev;
-      if (top == p0) atomicAdd(&h[0][(key >> sh) & dm], 1u);
-      if (split && top == p1) atomicAdd(&h[1][(key >> sh) & dm], 1u);
+      for (int t = 0; t < 4; ++t) {
+        if (!(mk[c][grp] & (1 << t))) continue;
+        const uint32_t key = __float_as_uint(e[c][grp][t]);
+        const uint32_t top = key >> sh_prev;
+        if (top == p0) atomicAdd(&h[0][(key >> sh) & dm], 1u);
+        if (split && top == p1) atomicAdd(&h[1][(key >> sh) & dm], 1u);
+      }
     }
   }
   __syncthreads();
-  flush(&h[0][0], hist_of(D, 0), nb);
-  if (split) flush(&h[1][0], hist_of(D, 1), nb);
+  if (cur >= 0) {
+    flush(&h[0][0], hist_of(descs[cur], 0), nb);
+    if (split) flush(&h[1][0], hist_of(descs[cur], 1), nb);
+  }
 }
 
 // Inclusive prefix sums of NB counts held 8 per thread (256 threads); finds,
@@ -305,9 +342,10 @@ extern "C" int scao_sparse_filter(const scao_task* tasks, int ntasks,
   hipStream_t s = (hipStream_t)stream;
   hipLaunchKernelGGL(k_filter_ema, dim3(ntasks), dim3(256), 0, s, tasks, descs);
   hipLaunchKernelGGL(k_filter_select, dim3(ndescs), dim3(256), 0, s, descs, 0);
-  hipLaunchKernelGGL(k_filter_hist, dim3(ntasks), dim3(256), 0, s, tasks, descs, 1);
+  const int hblocks = (ntasks + FH - 1) / FH;
+  hipLaunchKernelGGL(k_filter_hist, dim3(hblocks), dim3(256), 0, s, tasks, ntasks, descs, 1);
   hipLaunchKernelGGL(k_filter_select, dim3(ndescs), dim3(256), 0, s, descs, 1);
-  hipLaunchKernelGGL(k_filter_hist, dim3(ntasks), dim3(256), 0, s, tasks, descs, 2);
+  hipLaunchKernelGGL(k_filter_hist, dim3(hblocks), dim3(256), 0, s, tasks, ntasks, descs, 2);
   hipLaunchKernelGGL(k_filter_select, dim3(ndescs), dim3(256), 0, s, descs, 2);
   hipLaunchKernelGGL(k_filter_mask, dim3(ntasks), dim3(256), 0, s, tasks, descs);
   SCAO_LAUNCH_CHECK("scao_sparse_filter");
