@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define SCAO_ABI_VERSION 3
+#define SCAO_ABI_VERSION 4
 
 enum scao_status { SCAO_OK = 0, SCAO_ERR_INVALID = 1, SCAO_ERR_HIP = 2 };
 enum scao_dtype { SCAO_F32 = 0, SCAO_BF16 = 1, SCAO_F16 = 2 };
@@ -239,28 +239,34 @@ int scao_eig_prep(const scao_task* tasks, int ntasks, const scao_prep_desc* desc
 int scao_diag_ema(const scao_task* tasks, int ntasks, const scao_param_desc* params,
                   const float* rho_alpha, void* stream);
 
-/* ---- sparse gradient filter ----------------------------------------------
- * Replaces _SparseGradFilter.__call__ (scao/optimizer.py:49-57) for a batch
- * of parameters: ema = |g| (first) or fp32(fp32(ema*decay) + fp32(omd*|g|));
- * t = torch.quantile(ema, q) (linear interpolation, exact order statistics by
- * radix select); out = fp32(g) * (ema >= t).  torch.quantile refuses more than
- * 2^24 elements; this entry point has no such limit.  Tasks are
- * (desc index, chunk of SCAO_FLAT_CHUNK elements, 0, -1). */
+/* ---- the gradient the moments see -----------------------------------------
+ * Replaces the prologue of SCAO._step_group (scao/optimizer.py:533-545) for a
+ * batch of parameters: with SCAO_FILTER_MASK, _SparseGradFilter.__call__
+ * (:49-57): ema = |g| (SCAO_FILTER_FIRST) or fp32(fp32(ema*decay) +
+ * fp32(omd*|g|)); t = torch.quantile(ema, q) (linear interpolation, exact
+ * order statistics by radix select); out = fp32(g) * (ema >= t).  Without it
+ * out = fp32(g).  With noise > 0, out += fp32(noise * z), z ~ N(0,1) from
+ * Philox4x32-10 keyed by *seed, counter = element index / 4 (Box-Muller).
+ * torch.quantile refuses more than 2^24 elements; this entry point has no such
+ * limit.  Tasks are (desc index, chunk of SCAO_FLAT_CHUNK elements, 0, -1). */
 #define SCAO_FILTER_BINS 2048
 #define SCAO_FILTER_WORK_WORDS (2 * SCAO_FILTER_BINS + 8)
+#define SCAO_FILTER_MASK 1
+#define SCAO_FILTER_FIRST 2
 typedef struct scao_filter_desc {
   const void* g;            /* gradient (dtype), numel elements                  */
-  float* ema;               /* magnitude EMA, updated in place                   */
-  float* out;               /* filtered fp32 gradient                            */
+  float* ema;               /* magnitude EMA, updated in place (MASK)            */
+  float* out;               /* the moment gradient, fp32                         */
   uint32_t* work;           /* SCAO_FILTER_WORK_WORDS words of device scratch per
-                               desc: zero before its first call; every call
-                               leaves it ready for the next                      */
+                               desc (MASK): zero before its first call; every
+                               call leaves it ready for the next                 */
+  const uint64_t* seed;     /* device noise key (noise > 0)                      */
   int64_t numel;
   float decay, omd;         /* fp32(ema), fp32(1 - ema)                          */
   float q;                  /* fp32(sparsity)                                    */
+  float noise;              /* fp32(noise_std), 0 for none                       */
   int32_t dtype;
-  int32_t first;            /* 1 on the filter's first call (ema = |g|)          */
-  int32_t pad0;
+  int32_t flags;            /* SCAO_FILTER_MASK | SCAO_FILTER_FIRST              */
 } scao_filter_desc;
 int scao_sparse_filter(const scao_task* tasks, int ntasks, const scao_filter_desc* descs,
                        int ndescs, void* stream);

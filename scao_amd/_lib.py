@@ -21,7 +21,7 @@ import torch  # noqa: F401  -- loads torch's HIP runtime before ours
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("SCAO_AMD_LIB", os.path.join(HERE, "_lib", "libscao_amd.so"))
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 SLOT_WIDTH = 3
 FLAT_CHUNK = 4096
 PROJ_COLS = 256
@@ -76,9 +76,11 @@ PREP_DESC = np.dtype([
 ], align=True)
 
 FILTER_DESC = np.dtype([
-    ("g", "u8"), ("ema", "u8"), ("out", "u8"), ("work", "u8"), ("numel", "i8"),
-    ("decay", "f4"), ("omd", "f4"), ("q", "f4"), ("dtype", "i4"), ("first", "i4"), ("pad0", "i4"),
+    ("g", "u8"), ("ema", "u8"), ("out", "u8"), ("work", "u8"), ("seed", "u8"), ("numel", "i8"),
+    ("decay", "f4"), ("omd", "f4"), ("q", "f4"), ("noise", "f4"), ("dtype", "i4"),
+    ("flags", "i4"),
 ], align=True)
+FILTER_MASK, FILTER_FIRST = 1, 2
 FILTER_WORK_WORDS = 2 * 2048 + 8
 
 STRUCTS = {0: (PARAM_DESC, [n for n in PARAM_DESC.names if n != "pad0"]),
@@ -87,7 +89,7 @@ STRUCTS = {0: (PARAM_DESC, [n for n in PARAM_DESC.names if n != "pad0"]),
            3: (PARAM_STAT, [n for n in PARAM_STAT.names if n != "pad0"]),
            4: (GRAM_DESC, [n for n in GRAM_DESC.names if n != "pad0"]),
            5: (PREP_DESC, list(PREP_DESC.names)),
-           6: (FILTER_DESC, [n for n in FILTER_DESC.names if n != "pad0"])}
+           6: (FILTER_DESC, list(FILTER_DESC.names))}
 
 _VP, _I, _I64, _D = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_double
 

@@ -92,8 +92,9 @@ extern "C" int scao_struct_layout(int which, int64_t* out, int cap) {
       typedef scao_filter_desc S;
       PUT(sizeof(S));
       PUT(offsetof(S, g)); PUT(offsetof(S, ema)); PUT(offsetof(S, out)); PUT(offsetof(S, work));
-      PUT(offsetof(S, numel)); PUT(offsetof(S, decay)); PUT(offsetof(S, omd));
-      PUT(offsetof(S, q)); PUT(offsetof(S, dtype)); PUT(offsetof(S, first));
+      PUT(offsetof(S, seed)); PUT(offsetof(S, numel)); PUT(offsetof(S, decay));
+      PUT(offsetof(S, omd)); PUT(offsetof(S, q)); PUT(offsetof(S, noise));
+      PUT(offsetof(S, dtype)); PUT(offsetof(S, flags));
       break;
     }
     default:

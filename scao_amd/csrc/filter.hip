@@ -10,7 +10,11 @@
 //         fma(-(v_hi - v_lo), 1 - w, v_hi); NaN when any e is NaN (the
 //         reference's rank then points at the sorted NaN)
 //   out   g * (e >= t ? 1 : 0) in fp32 (NaN/inf gradients propagate as in
-//         the reference's multiply)
+//         the reference's multiply); descs without SCAO_FILTER_MASK pass g
+//         through.  With noise > 0, out + fp32(noise * z) (grad +
+//         randn_like(grad) * noise_std, :544-545), z from Philox4x32-10
+//         (Salmon et al., SC'11) keyed by the desc's seed with the element
+//         index / 4 as counter, turned into normals by Box-Muller.
 //
 // The two order statistics come from an exact radix select on the bit
 // patterns of e (e >= 0, so unsigned order is float order): digits of 11, 11
@@ -83,6 +87,8 @@ __global__ __launch_bounds__(256) void k_filter_ema(const scao_task* __restrict_
   __shared__ uint32_t nan_s;
   const scao_task tk = tasks[blockIdx.x];
   const scao_filter_desc& D = descs[tk.idx];
+  if (!(D.flags & SCAO_FILTER_MASK)) return;
+  const bool first = D.flags & SCAO_FILTER_FIRST;
   const FChunk ch(tk, D.numel);
   zero_lds(h, NB);
   if (threadIdx.x == 0) nan_s = 0u;
@@ -96,7 +102,7 @@ __global__ __launch_bounds__(256) void k_filter_ema(const scao_task* __restrict_
     const bool v = vec && mk[grp] == 15;
     const v4f z = {0.f, 0.f, 0.f, 0.f};
     g[grp] = mk[grp] ? ld4(D.g, D.dtype, i, v, mk[grp]) : z;
-    e[grp] = (mk[grp] && !D.first) ? ldf4(D.ema, i, v, mk[grp]) : z;
+    e[grp] = (mk[grp] && !first) ? ldf4(D.ema, i, v, mk[grp]) : z;
   }
   __syncthreads();
   uint32_t nans = 0;
@@ -106,7 +112,7 @@ __global__ __launch_bounds__(256) void k_filter_ema(const scao_task* __restrict_
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const float mag = fabsf(g[grp][t]);
-      const float x = D.first ? mag : (e[grp][t] * D.decay) + (D.omd * mag);
+      const float x = first ? mag : (e[grp][t] * D.decay) + (D.omd * mag);
       e[grp][t] = x;
       if (mk[grp] & (1 << t)) {
         const uint32_t key = __float_as_uint(x);
@@ -147,6 +153,7 @@ __global__ __launch_bounds__(256) void k_filter_hist(const scao_task* __restrict
     if (c >= nt) continue;
     const scao_task tk = tasks[t0 + c];
     const scao_filter_desc& D = descs[tk.idx];
+    if (!(D.flags & SCAO_FILTER_MASK)) continue;
     const FChunk ch(tk, D.numel);
     const bool vec = ((uintptr_t)D.ema & 15) == 0;
 #pragma unroll
@@ -168,6 +175,7 @@ __global__ __launch_bounds__(256) void k_filter_hist(const scao_task* __restrict
   for (int c = 0; c < FH; ++c) {
     if (c >= nt) break;
     const int idx = tasks[t0 + c].idx;
+    if (!(descs[idx].flags & SCAO_FILTER_MASK)) continue;
     if (idx != cur) {
       if (cur >= 0) {
         __syncthreads();
@@ -243,6 +251,7 @@ __global__ __launch_bounds__(256) void k_filter_select(const scao_filter_desc* _
   __shared__ uint32_t scan[256];
   __shared__ uint32_t bin[2], before[2];
   const scao_filter_desc& D = descs[blockIdx.x];
+  if (!(D.flags & SCAO_FILTER_MASK)) return;
   FState* S = state_of(D);
   uint32_t r[2], pre[2];
   bool split;
@@ -302,13 +311,51 @@ __global__ __launch_bounds__(256) void k_filter_select(const scao_filter_desc* _
   }
 }
 
-// --------------------------------------------------------------- mask ---
-__global__ __launch_bounds__(256) void k_filter_mask(const scao_task* __restrict__ tasks,
-                                                     const scao_filter_desc* __restrict__ descs) {
+// ---------------------------------------------------------------- out ---
+// Philox4x32-10: ten rounds of the published multiply/xor network with the
+// Weyl key schedule (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
+// easy as 1, 2, 3", SC'11).
+__device__ __forceinline__ void philox(uint32_t (&c)[4], uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t lo0 = 0xD2511F53u * c[0], hi0 = __umulhi(0xD2511F53u, c[0]);
+    const uint32_t lo1 = 0xCD9E8D57u * c[2], hi1 = __umulhi(0xCD9E8D57u, c[2]);
+    const uint32_t n0 = hi1 ^ c[1] ^ k0, n2 = hi0 ^ c[3] ^ k1;
+    c[0] = n0;
+    c[1] = lo1;
+    c[2] = n2;
+    c[3] = lo0;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+}
+
+// four N(0,1) values for the 4-element group starting at element e
+__device__ __forceinline__ v4f normals4(uint64_t key, int64_t e) {
+  const uint64_t ctr = (uint64_t)e >> 2;
+  uint32_t c[4] = {(uint32_t)ctr, (uint32_t)(ctr >> 32), 0u, 0u};
+  philox(c, (uint32_t)key, (uint32_t)(key >> 32));
+  v4f z;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    // uniforms in (0, 1): 24 bits plus half a step
+    const float u1 = ((float)(c[2 * j] >> 8) + 0.5f) * 5.9604645e-8f;
+    const float u2 = ((float)(c[2 * j + 1] >> 8) + 0.5f) * 5.9604645e-8f;
+    const float rad = sqrtf(-2.0f * logf(u1));
+    float sn, cs;
+    sincosf(6.2831853f * u2, &sn, &cs);
+    z[2 * j] = rad * cs;
+    z[2 * j + 1] = rad * sn;
+  }
+  return z;
+}
+
+__global__ __launch_bounds__(256) void k_filter_out(const scao_task* __restrict__ tasks,
+                                                    const scao_filter_desc* __restrict__ descs) {
   const scao_task tk = tasks[blockIdx.x];
   const scao_filter_desc& D = descs[tk.idx];
   const FChunk ch(tk, D.numel);
-  const float thr = state_of(D)->thr;
+  const bool masked = D.flags & SCAO_FILTER_MASK;
   const bool vec = ((((uintptr_t)D.ema) | (uintptr_t)D.out) & 15) == 0 && al_dt(D.g, D.dtype);
   v4f g[4], e[4];
   int mk[4];
@@ -319,15 +366,25 @@ __global__ __launch_bounds__(256) void k_filter_mask(const scao_task* __restrict
     const v4f z = {0.f, 0.f, 0.f, 0.f};
     const bool v = vec && mk[grp] == 15;
     g[grp] = mk[grp] ? ld4(D.g, D.dtype, i, v, mk[grp]) : z;
-    e[grp] = mk[grp] ? ldf4(D.ema, i, v, mk[grp]) : z;
+    e[grp] = (masked && mk[grp]) ? ldf4(D.ema, i, v, mk[grp]) : z;
   }
+  const float thr = masked ? state_of(D)->thr : 0.f;
+  const bool noisy = D.noise > 0.f;
+  const uint64_t key = noisy ? *D.seed : 0ull;
 #pragma unroll
   for (int grp = 0; grp < 4; ++grp) {
     if (!mk[grp]) continue;
+    const int64_t i = ch.elem(grp);
     v4f o;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) o[t] = g[grp][t] * (e[grp][t] >= thr ? 1.0f : 0.0f);
-    stf4(D.out, ch.elem(grp), o, vec && mk[grp] == 15, mk[grp]);
+    for (int t = 0; t < 4; ++t)
+      o[t] = masked ? g[grp][t] * (e[grp][t] >= thr ? 1.0f : 0.0f) : g[grp][t];
+    if (noisy) {
+      const v4f z = normals4(key, i);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) o[t] = o[t] + z[t] * D.noise;
+    }
+    stf4(D.out, i, o, vec && mk[grp] == 15, mk[grp]);
   }
 }
 
@@ -347,7 +404,7 @@ extern "C" int scao_sparse_filter(const scao_task* tasks, int ntasks,
   hipLaunchKernelGGL(k_filter_select, dim3(ndescs), dim3(256), 0, s, descs, 1);
   hipLaunchKernelGGL(k_filter_hist, dim3(hblocks), dim3(256), 0, s, tasks, ntasks, descs, 2);
   hipLaunchKernelGGL(k_filter_select, dim3(ndescs), dim3(256), 0, s, descs, 2);
-  hipLaunchKernelGGL(k_filter_mask, dim3(ntasks), dim3(256), 0, s, tasks, descs);
+  hipLaunchKernelGGL(k_filter_out, dim3(ntasks), dim3(256), 0, s, tasks, descs);
   SCAO_LAUNCH_CHECK("scao_sparse_filter");
   return SCAO_OK;
 }

@@ -530,39 +530,65 @@ def _filter_tasks(numels: tuple, dev) -> Tensor:
     return t
 
 
-def sparse_filter(entries) -> list:
-    """Run the filter for [(filter, grad)] in one batched launch sequence and
-    return each filtered fp32 gradient.  ``filter`` carries ``mag_ema`` (None
-    before its first call), ``work`` (zeroed device scratch, allocated here)
-    and ``sparsity``; gradients must be contiguous, on one device."""
-    entries = [(f, g) for f, g in entries if g.numel() > 0]
-    if not entries:
-        return []
-    dev = entries[0][1].device
-    descs = np.zeros(len(entries), dtype=L.FILTER_DESC)
+def moment_grads(entries, noise_std: float = 0.0) -> list:
+    """The gradient the moments see, for [(filter or None, grad)], in one
+    batched launch sequence (reference scao/optimizer.py:533-545): the sparse
+    filter where a filter is given, then ``noise_std * N(0, 1)`` when
+    noise_std > 0.  A filter carries ``mag_ema`` (None before its first call),
+    ``work`` (zeroed device scratch, allocated here), ``ema`` and
+    ``sparsity``.  Gradients must be contiguous and on one ROCm device; each
+    result is a new fp32 tensor of the gradient's shape."""
+    keep = [(f, g) for f, g in entries if g.numel() > 0]
+    if not keep:
+        return [torch.empty(g.shape, dtype=torch.float32, device=g.device) for _, g in entries]
+    dev = keep[0][1].device
+    n = len(keep)
     outs = []
-    for i, (f, g) in enumerate(entries):
-        require_hip(g, "sparse filter gradient")
-        first = f.mag_ema is None
-        if first:
-            f.mag_ema = torch.empty(g.shape, dtype=torch.float32, device=dev)
-        if getattr(f, "work", None) is None or f.work.device != dev:
-            f.work = torch.zeros(L.FILTER_WORK_WORDS, dtype=torch.int32, device=dev)
+    cols = {k: [] for k in ("g", "ema", "out", "work", "seed", "numel", "decay", "omd", "q",
+                            "dtype", "flags")}
+    noisy = noise_std > 0.0
+    seeds = (torch.randint(0, 2 ** 62, (n,), dtype=torch.int64, device=dev) if noisy else None)
+    for i, (f, g) in enumerate(keep):
+        require_hip(g, "moment gradient")
         out = torch.empty(g.shape, dtype=torch.float32, device=dev)
         outs.append(out)
-        e = descs[i]
-        e["g"], e["ema"], e["out"] = g.data_ptr(), f.mag_ema.data_ptr(), out.data_ptr()
-        e["work"] = f.work.data_ptr()
-        e["numel"] = g.numel()
-        e["decay"], e["omd"], e["q"] = f.ema, 1.0 - f.ema, f.sparsity
-        e["dtype"] = L.DTYPE_CODE[g.dtype]
-        e["first"] = 1 if first else 0
-    tasks = _filter_tasks(tuple(int(g.numel()) for _, g in entries), dev)
+        flags, ema, work, decay, omd, q = 0, 0, 0, 0.0, 0.0, 0.0
+        if f is not None:
+            flags = L.FILTER_MASK
+            if f.mag_ema is None:
+                f.mag_ema = torch.empty(g.shape, dtype=torch.float32, device=dev)
+                flags |= L.FILTER_FIRST
+            if getattr(f, "work", None) is None or f.work.device != dev:
+                f.work = torch.zeros(L.FILTER_WORK_WORDS, dtype=torch.int32, device=dev)
+            ema, work = f.mag_ema.data_ptr(), f.work.data_ptr()
+            decay, omd, q = f.ema, 1.0 - f.ema, f.sparsity
+        cols["g"].append(g.data_ptr())
+        cols["ema"].append(ema)
+        cols["out"].append(out.data_ptr())
+        cols["work"].append(work)
+        cols["seed"].append(seeds.data_ptr() + 8 * i if noisy else 0)
+        cols["numel"].append(g.numel())
+        cols["decay"].append(decay)
+        cols["omd"].append(omd)
+        cols["q"].append(q)
+        cols["dtype"].append(L.DTYPE_CODE[g.dtype])
+        cols["flags"].append(flags)
+    descs = np.zeros(n, dtype=L.FILTER_DESC)
+    for k, v in cols.items():
+        descs[k] = np.asarray(v, dtype=descs.dtype.fields[k][0])
+    descs["noise"] = noise_std if noisy else 0.0
+    tasks = _filter_tasks(tuple(int(g.numel()) for _, g in keep), dev)
     dd = L.upload(descs, dev)
     _call("scao_sparse_filter", tasks.data_ptr(), tasks.numel() // L.TASK.itemsize,
-          dd.data_ptr(), len(entries), L.stream_ptr(dev))
+          dd.data_ptr(), n, L.stream_ptr(dev))
     it = iter(outs)
-    return [next(it) for _ in entries]
+    return [next(it) if g.numel() > 0 else torch.empty(g.shape, dtype=torch.float32, device=g.device)
+            for _, g in entries]
+
+
+def sparse_filter(entries) -> list:
+    """The sparse filter alone for [(filter, grad)] (no noise)."""
+    return moment_grads(entries, 0.0)
 
 
 def _grads_moved(items, ws) -> bool:

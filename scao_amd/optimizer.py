@@ -51,7 +51,7 @@ class _SparseGradFilter:
 
     def __call__(self, grad: Tensor) -> Tensor:
         self.prepare(grad)
-        return engine.sparse_filter([(self, grad.contiguous())])[0]
+        return engine.moment_grads([(self, grad.contiguous())])[0]
 
 
 class _DynamicSparseFilter(_SparseGradFilter):
@@ -324,19 +324,18 @@ class SCAO(Optimizer):
         return loss
 
     def _filter_and_noise(self, items: list, filtered: list) -> None:
-        """The gradient the moments see (reference :533-545): every filtered
-        parameter of the step goes through one batched filter launch
-        sequence, then noise is added in parameter order."""
-        outs = engine.sparse_filter([(f, g) for _, f, g in filtered]) if filtered else []
-        by_item = {id(it): out for (it, _, _), out in zip(filtered, outs)}
-        for it in items:
-            grad = by_item.get(id(it))
-            if self._noise_std > 1e-9:
-                if grad is None:
-                    grad = it.graw.float()
-                grad = grad + torch.randn_like(grad) * self._noise_std
-            if grad is not None:
-                it.gmom = grad.contiguous()
+        """The gradient the moments see (reference :533-545): the filtered
+        parameters, and with noise every parameter, go through one batched
+        launch sequence (scao_sparse_filter: filter, then noise_std * N(0,1)
+        from a counter-based generator keyed per parameter and step)."""
+        noise = self._noise_std if self._noise_std > 1e-9 else 0.0
+        filt = {id(it): f for it, f, _ in filtered}
+        todo = [it for it in items if id(it) in filt or noise > 0.0]
+        if not todo:
+            return
+        outs = engine.moment_grads([(filt.get(id(it)), it.graw) for it in todo], noise)
+        for it, out in zip(todo, outs):
+            it.gmom = out
 
     def _plan_param(self, group: dict, p: Tensor, refresh: list, filtered: list) -> PItem:
         """Host half of reference _step_group (:521-605) for one parameter."""

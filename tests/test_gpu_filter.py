@@ -148,3 +148,78 @@ def test_filter_at_and_beyond_quantile_limit(n):
         assert torch.equal(e, ref.mag_ema), t
         thr = _aten_quantile(e.numpy(), 0.7)
         assert torch.equal(o, g * (e >= float(thr)).float()), t
+
+
+# ----------------------------------------------------------------- noise ---
+# grad + randn_like(grad) * noise_std (scao/optimizer.py:544-545).  The
+# reference's draws come from torch's generator and cannot be reproduced on
+# another device, so the noise is checked for its distribution.
+
+def _ks_normal(x: np.ndarray) -> float:
+    from scipy import stats
+    return stats.kstest(x, "norm").pvalue
+
+
+def test_noise_distribution_and_independence():
+    from scao_amd import engine
+    dev = _dev()
+    n, std = 1 << 22, 0.01
+    g = torch.randn(n, generator=torch.Generator().manual_seed(2)) * 1e-3
+    gd = g.to(dev)
+    torch.manual_seed(123)
+    a, b = engine.moment_grads([(None, gd), (None, gd)], std)
+    c, = engine.moment_grads([(None, gd)], std)
+    za = ((a.cpu().double() - g.double()) / std).numpy()
+    zb = ((b.cpu().double() - g.double()) / std).numpy()
+    zc = ((c.cpu().double() - g.double()) / std).numpy()
+    for z in (za, zb, zc):
+        assert abs(z.mean()) < 5.0 / np.sqrt(n)
+        assert abs(z.std() - 1.0) < 5e-3
+        assert _ks_normal(z) > 1e-4
+    # separate parameters and separate calls draw separate streams
+    assert abs(np.corrcoef(za, zb)[0, 1]) < 5.0 / np.sqrt(n)
+    assert abs(np.corrcoef(za, zc)[0, 1]) < 5.0 / np.sqrt(n)
+    # consecutive 4-element groups are not correlated either
+    assert abs(np.corrcoef(za[:-4], za[4:])[0, 1]) < 5.0 / np.sqrt(n)
+    # the same seed gives the same draws
+    torch.manual_seed(123)
+    a2, _ = engine.moment_grads([(None, gd), (None, gd)], std)
+    assert torch.equal(a, a2)
+
+
+def test_filter_then_noise():
+    """Noise goes on top of the filtered gradient, everywhere (masked-out
+    elements included); the filter part is still bit-exact."""
+    from scao_amd import engine
+    from scao_amd.optimizer import _SparseGradFilter
+    dev = _dev()
+    ref, gpu = R.RefSparseFilter(0.7), _SparseGradFilter(0.7)
+    std = 0.005
+    for t, g in enumerate(_grads(1 << 20, 2, 21)):
+        r = ref(g.clone())
+        o, = engine.moment_grads([(gpu, g.to(dev))], std)
+        assert _same(gpu.mag_ema, ref.mag_ema), t
+        z = ((o.cpu().double() - r.double()) / std).numpy()
+        assert abs(z.mean()) < 5.0 / np.sqrt(z.size) and abs(z.std() - 1.0) < 1e-2
+        assert _ks_normal(z) > 1e-4
+        masked_out = (r == 0).numpy()
+        assert masked_out.mean() > 0.6 and np.abs(z[masked_out]).max() > 0
+
+
+def test_optimizer_noise_anneals_and_is_applied():
+    """SCAO with noise only: the moment gradient differs from the raw one by
+    noise of the current (annealed) scale."""
+    import scao_amd
+    dev = _dev()
+    p = torch.nn.Parameter(torch.zeros(512, 256, device=dev))
+    opt = scao_amd.SCAO([p], lr=1e-3, sparsity=0.0, noise_std_init=0.02, noise_anneal=0.5,
+                        lookahead_k=0, async_precond=False)
+    for step, std in enumerate([0.02, 0.01]):
+        p.grad = torch.zeros_like(p)
+        opt.step()
+        # Phase 1 with g = noise only: m = (1 - beta1) * noise
+        m = opt.state[p]["exp_avg"] if step == 0 else None
+        if m is not None:
+            z = (m.double().cpu() / (0.1 * std)).numpy().ravel()
+            assert abs(z.std() - 1.0) < 2e-2 and _ks_normal(z) > 1e-4
+    assert opt._noise_std == pytest.approx(0.005)
