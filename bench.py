@@ -150,7 +150,8 @@ def main():
                          "kernel of known size to calibrate traffic counters)")
     ap.add_argument("--sparse-steps", type=int, default=3,
                     help="steady steps timed afterwards with the reference's default sparse "
-                         "gradient filter (sparsity=0.7), reported in details (0: skip)")
+                         "gradient filter and noise (sparsity=0.7, noise_std=0.01), reported "
+                         "in details (0: skip)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -247,11 +248,12 @@ def main():
     engine.TIMING = None
     assert all(opt.state[p].get("scao_phase_started") for p in pre_p), "not in Phase 2"
 
-    # diagnostic (not the headline): the reference's default sparse gradient
-    # filter (sparsity=0.7) switched on for a few steady steps
+    # diagnostic (not the headline): the reference's default moment gradient
+    # (sparse filter at sparsity=0.7, noise_std 0.01) for a few steady steps
     sparse = None
     if args.sparse_steps > 0:
         opt._sparsity = 0.7
+        opt._noise_std, noise0 = 0.01, opt._noise_std
         one()                                 # first filter call: EMA = |g|
         engine.TIMING, engine.TIMING_ONLY = {}, {"scao_sparse_filter"}
         torch.cuda.synchronize()
@@ -262,11 +264,11 @@ def main():
         sp_ms = (time.perf_counter() - t2) * 1e3 / args.sparse_steps
         filt = engine.timing_summary().get("scao_sparse_filter")
         engine.TIMING, engine.TIMING_ONLY = None, None
-        opt._sparsity = PROFILE["sparsity"]
+        opt._sparsity, opt._noise_std = PROFILE["sparsity"], noise0
         f_ms = filt[1] if filt else None
-        sparse = {"sparsity": 0.7, "steady_step_ms": sp_ms, "filter_ms": f_ms,
+        sparse = {"sparsity": 0.7, "noise_std": 0.01, "steady_step_ms": sp_ms, "filter_ms": f_ms,
                   "filter_elements": nparams,
-                  # EMA pass 12 B, two radix passes 4 B each, mask pass 12 B
+                  # EMA pass 12 B, two radix passes 4 B each, output pass 12 B
                   "filter_GBps_at_32B_per_elem": (32.0 * nparams / (f_ms / 1e3) / 1e9
                                                   if f_ms else None)}
 
@@ -335,7 +337,8 @@ def main():
         "cpu_baseline": cpu,
         "details": {"phase1_step_ms": t_phase1, "refresh_step_ms": t_refresh,
                     "step_hbm_frac": details["step_roofline"]["hbm_frac"],
-                    "steady_step_sparsity07_ms": sparse["steady_step_ms"] if sparse else None},
+                    "steady_step_default_filter_noise_ms": (sparse["steady_step_ms"]
+                                                            if sparse else None)},
     }
     if args.details:
         with open(args.details, "w") as f:
