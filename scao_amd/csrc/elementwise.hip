@@ -293,9 +293,22 @@ __global__ __launch_bounds__(256) void k_finalize_params(const scao_param_desc* 
   const int dt = P.dtype;
   const double* __restrict__ sl = slots;
   if (phase == 0) {
-    double a[3] = {0.0, 0.0, 0.0};
-    for (int s = P.pre_begin + l; s < P.pre_end; s += 256)
-      for (int q = 0; q < 3; ++q) a[q] += sl[(int64_t)s * SCAO_SLOT_WIDTH + q];
+    // four independent partial sums per thread keep four slot loads in
+    // flight (an Adam-path embedding has tens of thousands of slots); they
+    // are combined in a fixed order
+    double a4[3][4] = {};
+    int s = P.pre_begin + l;
+    for (; s + 768 < P.pre_end; s += 1024)
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+#pragma unroll
+        for (int q = 0; q < 3; ++q) a4[q][u] += sl[(int64_t)(s + 256 * u) * SCAO_SLOT_WIDTH + q];
+    for (; s < P.pre_end; s += 256)
+#pragma unroll
+      for (int q = 0; q < 3; ++q) a4[q][0] += sl[(int64_t)s * SCAO_SLOT_WIDTH + q];
+    double a[3];
+#pragma unroll
+    for (int q = 0; q < 3; ++q) a[q] = (a4[q][0] + a4[q][1]) + (a4[q][2] + a4[q][3]);
     block_sum<3>(a, red);
     if (l == 0) {
       S.g2 = a[0];
@@ -314,9 +327,13 @@ __global__ __launch_bounds__(256) void k_finalize_params(const scao_param_desc* 
       S.alpha = round_to(dt, (float)(-P.lr));
     }
   } else {
-    double ax[1] = {0.0};
-    for (int s = P.post_begin + l; s < P.post_end; s += 256)
-      ax[0] += sl[(int64_t)s * SCAO_SLOT_WIDTH + 2];
+    double a4[4] = {0.0, 0.0, 0.0, 0.0};
+    int s = P.post_begin + l;
+    for (; s + 768 < P.post_end; s += 1024)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) a4[u] += sl[(int64_t)(s + 256 * u) * SCAO_SLOT_WIDTH + 2];
+    for (; s < P.post_end; s += 256) a4[0] += sl[(int64_t)s * SCAO_SLOT_WIDTH + 2];
+    double ax[1] = {(a4[0] + a4[1]) + (a4[2] + a4[3])};
     block_sum<1>(ax, red);
     const double a = ax[0];
     if (l == 0) {
@@ -335,17 +352,33 @@ __global__ __launch_bounds__(256) void k_finalize_params(const scao_param_desc* 
   }
 }
 
-__global__ __launch_bounds__(64) void k_finalize_global(const scao_param_desc* __restrict__ params,
-                                                        int nparams, const scao_param_stat* stat,
-                                                        double* runtime, int norm_count) {
-  if (threadIdx.x != 0) return;
+// The average of the per-parameter gradient norms, summed in parameter order
+// as the reference's Python sum does; 256 threads stage each batch of norms in
+// LDS so that the ordered sum does not wait on one global load per term.
+__global__ __launch_bounds__(256) void k_finalize_global(const scao_param_desc* __restrict__ params,
+                                                         int nparams, const scao_param_stat* stat,
+                                                         double* runtime, int norm_count) {
+  constexpr int B = 1024;
+  __shared__ double v[B];
+  __shared__ int use[B];
   double sum = 0.0;
   int cnt = 0;
-  for (int i = 0; i < nparams; ++i) {
-    if (params[i].norm_index < 0) continue;
-    sum += (double)stat[i].gnorm;
-    ++cnt;
+  for (int b0 = 0; b0 < nparams; b0 += B) {
+    const int nb = nparams - b0 < B ? nparams - b0 : B;
+    for (int i = threadIdx.x; i < nb; i += 256) {
+      use[i] = params[b0 + i].norm_index >= 0;
+      v[i] = (double)stat[b0 + i].gnorm;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+      for (int i = 0; i < nb; ++i)
+        if (use[i]) {
+          sum += v[i];
+          ++cnt;
+        }
+    __syncthreads();
   }
+  if (threadIdx.x != 0) return;
   if (cnt == 0 || cnt != norm_count) {
     runtime[1] = 0.0;
     return;
@@ -409,7 +442,7 @@ extern "C" int scao_step_finalize(const scao_param_desc* params, int nparams, co
   SCAO_LAUNCH_CHECK("scao_step_finalize");
   if (phase == 0 && update_norm_ema) {
     SCAO_CHECK_ARG(runtime != nullptr, "scao_step_finalize: null runtime");
-    hipLaunchKernelGGL(k_finalize_global, dim3(1), dim3(64), 0, s, params, nparams, stat, runtime,
+    hipLaunchKernelGGL(k_finalize_global, dim3(1), dim3(256), 0, s, params, nparams, stat, runtime,
                        norm_count);
     SCAO_LAUNCH_CHECK("scao_step_finalize/global");
   }
