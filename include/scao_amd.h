@@ -130,6 +130,8 @@ typedef struct scao_param_stat {
 #define SCAO_APPLY_TILE 64   /* rows x cols per masked apply task                 */
 #define SCAO_APPLY_WIDE_ROWS 16   /* rows of a fast (variant bit 4) apply task    */
 #define SCAO_APPLY_WIDE_COLS 256  /* columns of a fast apply task                  */
+#define SCAO_APPLY_GROUP 8    /* consecutive fast tasks per block of the pipelined
+                                 variant (bit 8)                                 */
 #define SCAO_GRAM_TILE 128   /* Gram output tile                                  */
 
 /* ---- library --------------------------------------------------------- */
@@ -188,7 +190,10 @@ int scao_step_finalize(const scao_param_desc* params, int nparams, const double*
  *     that variant.  "fast" tasks promise fp32 data, SCAO_LF_VEC4,
  *     SCAO_PF_ALIGNED, k % 16 == 0 and a whole 16x256 tile at (a, b)
  *     (SCAO_APPLY_WIDE_ROWS x SCAO_APPLY_WIDE_COLS); other tasks are masked
- *     64x64 tiles (SCAO_APPLY_TILE) at (a, b), clipped to the block. */
+ *     64x64 tiles (SCAO_APPLY_TILE) at (a, b), clipped to the block.
+ *     variant | 8 (with 4): the same fast tasks through a two-role pipeline,
+ *     SCAO_APPLY_GROUP consecutive tasks per block (the engine's choice for
+ *     k >= 128). */
 int scao_kron_apply(const scao_task* tasks, int ntasks, const scao_leaf_desc* leaves,
                     const scao_param_desc* params, const scao_param_stat* stat,
                     double* slots, int variant, void* stream);

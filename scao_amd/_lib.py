@@ -28,6 +28,7 @@ PROJ_COLS = 256
 APPLY_TILE = 64
 APPLY_WIDE_ROWS = 16
 APPLY_WIDE_COLS = 256
+APPLY_GROUP = 8
 GRAM_TILE = 128
 
 F32, BF16, F16 = 0, 1, 2

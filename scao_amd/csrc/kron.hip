@@ -605,6 +605,135 @@ __device__ __forceinline__ void apply_wide(const scao_leaf_desc& L, const scao_p
   write_u2_slot(slots, slot, u2, red);
 }
 
+// Wide tiles through a two-role pipeline, for ranks where the back-projection
+// no longer hides under the streaming of one-tile blocks (k >= 128; at k = 64
+// both kernels measure the same).  A block of eight waves
+// takes SCAO_APPLY_GROUP consecutive wide tasks.  Waves 4..7 compute
+// corr = W U_r^T of tile s into one of two LDS buffers while waves 0..3
+// stream tile s-1 (loads, Adan tail, stores) and then issue tile s+1's loads;
+// one block barrier per tile hands a buffer over.  Each role waits only on
+// its own memory operations (the vector-memory counter is in order within a
+// wave, so an operand load queued behind the streaming loads would wait for
+// them too).  Both roles use apply_wide's lane <-> element mapping, so a
+// streaming wave reads exactly the 16x64 slice its partner wrote.  u^2 per
+// tile: four wave partials through LDS, summed in a fixed order.
+constexpr int CP = SCAO_APPLY_WIDE_COLS + 4;   // LDS pitch of a correction row
+
+template <bool GF32, bool LARS>
+__global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict__ tasks, int ntasks,
+                                                    const scao_leaf_desc* __restrict__ leaves,
+                                                    const scao_param_desc* __restrict__ params,
+                                                    const scao_param_stat* __restrict__ stat,
+                                                    double* slots) {
+  __shared__ __attribute__((aligned(16))) float cbuf[2][16][CP];
+  __shared__ double part[2][4];
+  const int wv = threadIdx.x / 64, l = threadIdx.x % 64;
+  const int w = wv & 3;
+  const int kk = l / 16;
+  const int t0 = blockIdx.x * SCAO_APPLY_GROUP;
+  const int nt = ntasks - t0 < SCAO_APPLY_GROUP ? ntasks - t0 : SCAO_APPLY_GROUP;
+
+  if (wv >= 4) {
+    // ---- MFMA role ----
+    for (int s = 0; s < nt; ++s) {
+      const scao_task tk = tasks[t0 + s];
+      const scao_leaf_desc& L = leaves[tk.idx];
+      const int k = L.k;
+      const int jl = tk.b + 64 * w + 4 * (l % 16);
+      v4f acc[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+      const float* __restrict__ wrow = L.W + (int64_t)(tk.a + l % 16) * k + 4 * kk;
+      const float* __restrict__ urow = L.Ur + (int64_t)jl * k + 4 * kk;
+      v4f a = gld4(wrow), b[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) b[t] = gld4(urow + (int64_t)t * k);
+      for (int c = 0; c < k; c += 16) {
+        const bool more = c + 16 < k;
+        v4f an = a, bn[4] = {b[0], b[1], b[2], b[3]};
+        if (more) {
+          an = gld4(wrow + c + 16);
+#pragma unroll
+          for (int t = 0; t < 4; ++t) bn[t] = gld4(urow + (int64_t)t * k + c + 16);
+        }
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) acc[t] = mfma16(a[s4], b[t][s4], acc[t]);
+        a = an;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) b[t] = bn[t];
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        *(v4f*)&cbuf[s & 1][4 * kk + r][64 * w + 4 * (l % 16)] =
+            v4f{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+      __syncthreads();   // corr(s) ready
+    }
+    __syncthreads();     // the streaming role's last barrier
+    return;
+  }
+
+  // ---- streaming role ----
+  v4f gr[4], gm[4], mm[4], vv[4], dd[4], pp[4], par[4];
+  int64_t e[4];
+  auto prefetch = [&](int s) {
+    const scao_task tk = tasks[t0 + s];
+    const scao_leaf_desc& L = leaves[tk.idx];
+    const scao_param_desc& P = params[L.param];
+    const int jl = tk.b + 64 * w + 4 * (l % 16);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      e[r] = L.off + (int64_t)(tk.a + 4 * kk + r) * L.ld + jl;
+      gr[r] = gld4_nt((const float*)P.graw + e[r]);
+      if (GF32) gm[r] = gld4_nt((const float*)P.g + e[r]);
+      mm[r] = gld4_nt(P.exp_avg + e[r]);
+      vv[r] = gld4_nt(P.exp_avg_sq + e[r]);
+      dd[r] = gld4_nt(P.exp_avg_diff + e[r]);
+      pp[r] = gld4_nt(P.prev_grad + e[r]);
+      if (!LARS) par[r] = gld4_nt((const float*)P.p + e[r]);
+    }
+  };
+  auto put_slot = [&](int s) {
+    const int slot = tasks[t0 + s].slot;
+    if (slot < 0) return;
+    const double u2 = ((part[s & 1][0] + part[s & 1][1]) + part[s & 1][2]) + part[s & 1][3];
+    slots[(int64_t)slot * SCAO_SLOT_WIDTH + 0] = 0.0;
+    slots[(int64_t)slot * SCAO_SLOT_WIDTH + 1] = 0.0;
+    slots[(int64_t)slot * SCAO_SLOT_WIDTH + 2] = u2;
+  };
+  if (nt > 0) prefetch(0);
+  for (int s = 0; s < nt; ++s) {
+    __syncthreads();     // corr(s) in cbuf[s & 1]; tile s-1's partials in part
+    if (s > 0 && w == 0 && l == 0) put_slot(s - 1);
+    const scao_task tk = tasks[t0 + s];
+    const scao_leaf_desc& L = leaves[tk.idx];
+    const scao_param_desc& P = params[L.param];
+    const scao_param_stat& S = stat[L.param];
+    float u2 = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const v4f corr = *(const v4f*)&cbuf[s & 1][4 * kk + r][64 * w + 4 * (l % 16)];
+      v4f out;
+      adan4<GF32, LARS>(P, S, SCAO_F32, gr[r], gm[r], corr, mm[r], vv[r], dd[r], pp[r], par[r],
+                        out, u2, 15);
+      gst4_nt(P.exp_avg + e[r], mm[r]);
+      gst4_nt(P.exp_avg_sq + e[r], vv[r]);
+      gst4_nt(P.exp_avg_diff + e[r], dd[r]);
+      gst4_nt(P.prev_grad + e[r], GF32 ? gm[r] : gr[r]);
+      if (LARS)
+        gst4(P.upd + e[r], out);
+      else
+        gst4_nt((float*)P.p + e[r], out);
+    }
+    const double wsum = wave_sum((double)u2);
+    if (l == 0) part[s & 1][w] = wsum;
+    if (s + 1 < nt) prefetch(s + 1);
+  }
+  __syncthreads();       // the last tile's partials
+  if (nt > 0 && w == 0 && l == 0) put_slot(nt - 1);
+}
+
 // Reference operator: out = G + W U_r^T (dense m x n output).
 __device__ __forceinline__ void apply_out_tile(const scao_leaf_desc& L, const float* G, float* out, int i0,
                                int j0) {
@@ -743,8 +872,23 @@ extern "C" int scao_kron_apply(const scao_task* tasks, int ntasks, const scao_le
   SCAO_CHECK_ARG(ntasks >= 0, "scao_kron_apply: ntasks < 0");
   if (ntasks == 0) return SCAO_OK;
   SCAO_CHECK_ARG(tasks && leaves && params && stat && slots, "scao_kron_apply: null pointer");
-  SCAO_CHECK_ARG(variant >= 0 && variant < 8, "scao_kron_apply: bad variant %d", variant);
+  SCAO_CHECK_ARG(variant >= 0 && variant < 16 && (variant < 8 || (variant & 4)),
+                 "scao_kron_apply: bad variant %d", variant);
   hipStream_t s = (hipStream_t)stream;
+  if (variant & 8) {
+    const dim3 gp((ntasks + SCAO_APPLY_GROUP - 1) / SCAO_APPLY_GROUP), bp(512);
+#define SCAO_APPLY_PIPE(GF, LA) \
+  hipLaunchKernelGGL((k_apply_pipe<GF, LA>), gp, bp, 0, s, tasks, ntasks, leaves, params, stat, slots)
+    switch (variant & 3) {
+      case 0: SCAO_APPLY_PIPE(false, false); break;
+      case 1: SCAO_APPLY_PIPE(true, false); break;
+      case 2: SCAO_APPLY_PIPE(false, true); break;
+      default: SCAO_APPLY_PIPE(true, true); break;
+    }
+#undef SCAO_APPLY_PIPE
+    SCAO_LAUNCH_CHECK("scao_kron_apply");
+    return SCAO_OK;
+  }
   dim3 g(ntasks), b(256);
 #define SCAO_APPLY(GF, LA, FA) \
   hipLaunchKernelGGL((k_apply<GF, LA, FA>), g, b, 0, s, tasks, leaves, params, stat, slots)

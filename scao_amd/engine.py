@@ -170,7 +170,7 @@ def _build_structure(items: list[PItem]):
     Every reduction slot is written by exactly one task; each parameter's
     pre-finalize slots and post-finalize slots are contiguous ranges."""
     tasks = {k: [] for k in ["adam", "delta", "lift", "dred", "dapply", "lars"] +
-             [f"proj{v}" for v in range(4)] + [f"apply{v}" for v in range(8)]}
+             [f"proj{v}" for v in range(4)] + [f"apply{v}" for v in range(16)]}
     ranges = []
     leaves = []          # (leaf, r0, c0, param index)
     slot = 0
@@ -235,9 +235,10 @@ def _build_structure(items: list[PItem]):
                 nw = n - n % L.APPLY_WIDE_COLS if ok else 0
                 if not (mw and nw):
                     mw = nw = 0
+                wide = var | 4 | (8 if k >= PIPE_MIN_RANK else 0)
                 for i0 in range(0, mw, L.APPLY_WIDE_ROWS):
                     for j0 in range(0, nw, L.APPLY_WIDE_COLS):
-                        tasks[f"apply{var | 4}"].append((li, i0, j0, slot))
+                        tasks[f"apply{wide}"].append((li, i0, j0, slot))
                         slot += 1
                 for i0 in range(0, m, T):
                     for j0 in range(nw, n, T):
@@ -253,35 +254,40 @@ def _build_structure(items: list[PItem]):
                 tasks["lars"].append((pi, c, 0, -1))
     for k in tasks:
         if k.startswith("apply") or k.startswith("proj"):
-            tasks[k] = _xcd_interleave(tasks[k])
+            grp = L.APPLY_GROUP if k.startswith("apply") and int(k[5:]) & 8 else 1
+            tasks[k] = _xcd_interleave(tasks[k], grp)
     arrays = {k: np.array(v, dtype=np.int32).reshape(-1, 4).copy().view(L.TASK).reshape(-1)
               for k, v in tasks.items()}
     return arrays, ranges, slot, leaves
 
 
 XCDS = 8   # MI355X: 8 accelerator dies, workgroup i is dispatched to die i % 8
+PIPE_MIN_RANK = 128   # wide apply tiles of blocks with k >= this use the pipelined kernel
 
 
-def _xcd_interleave(tasks: list) -> list:
+def _xcd_interleave(tasks: list, group: int = 1) -> list:
     """Order a launch's tasks so that every tile of one block runs on the same
     die: the blocks are dealt to XCDS queues (largest first, each to the
-    least-loaded queue) and the queues are interleaved, so workgroup i comes
-    from queue i % XCDS while all queues last.  Each die's L2 then fetches a
-    block's shared operands (U_l; W and U_r) once instead of every die doing
-    so.  Only the order changes: tasks, slots and sums are the same."""
-    if len(tasks) <= XCDS:
+    least-loaded queue), each queue is cut into runs of `group` tasks (the
+    tasks one workgroup takes) and the runs are interleaved, so workgroup i
+    takes its run from queue i % XCDS while all queues last.  Each die's L2
+    then fetches a block's shared operands (U_l; W and U_r) once instead of
+    every die doing so.  Only the order changes: tasks, slots and sums are
+    the same."""
+    if len(tasks) <= XCDS * group:
         return tasks
-    groups: dict = {}
+    by_leaf: dict = {}
     for t in tasks:
-        groups.setdefault(t[0], []).append(t)
+        by_leaf.setdefault(t[0], []).append(t)
     queues = [[] for _ in range(XCDS)]
-    for g in sorted(groups.values(), key=len, reverse=True):
+    for g in sorted(by_leaf.values(), key=len, reverse=True):
         min(queues, key=len).extend(g)
+    runs = [[q[i:i + group] for i in range(0, len(q), group)] for q in queues]
     out = []
-    for i in range(max(len(q) for q in queues)):
-        for q in queues:
-            if i < len(q):
-                out.append(q[i])
+    for i in range(max(len(r) for r in runs)):
+        for r in runs:
+            if i < len(r):
+                out.extend(r[i])
     return out
 
 
@@ -494,7 +500,7 @@ def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
         _call("scao_diag_reduce", tp("dred"), N["dred"], P, SL, s)
     _call("scao_step_finalize", P, len(items), SL, S, ws.runtime.data_ptr(), 0,
            1 if update_norm_ema else 0, len(items), s)
-    for var in range(8):
+    for var in range(16):
         if N[f"apply{var}"]:
             _call("scao_kron_apply", tp(f"apply{var}"), N[f"apply{var}"], LF, P, S, SL, var, s)
     if N["dapply"]:

@@ -155,6 +155,11 @@ CASES = {
                                     use_int8_ema=False, k_min=128, k_max=128, warmup_steps=2,
                                     blend_steps=2, precond_freq=4, min_precond_updates=1,
                                     tau=None, lars_coeff=0.0), 6),
+    # k >= 128: the pipelined (two-role) apply kernel, with LARS staging and clip
+    "pipe_k128_lars": (FAST, dict(lr=1e-3, weight_decay=0.01, max_precond_dim=512, rho=0.999,
+                                  use_int8_ema=True, k_min=128, k_max=128, warmup_steps=2,
+                                  blend_steps=3, precond_freq=4, min_precond_updates=1, tau=1.0,
+                                  lars_coeff=1e-3), 7),
 }
 
 
@@ -392,14 +397,22 @@ def test_bf16_params_from_shared_state():
            {"max_err_over_bound": worst, "adam_phase_exact_fraction_min": exact_min})
 
 
-def test_sparse_filter_trajectory():
+SPARSE_CASES = {
+    "int8_small": (SHAPES, dict(CASES["int8_small"][1], sparsity=0.7)),
+    # filtered moments (GF32) through the fast and the pipelined apply kernels
+    "fast_k128": (FAST, dict(CASES["fast_k128_nolars"][1], sparsity=0.7, lars_coeff=1e-3,
+                             tau=1.0, weight_decay=0.01)),
+}
+
+
+@pytest.mark.parametrize("case", list(SPARSE_CASES))
+def test_sparse_filter_trajectory(case):
     """Default sparse gradient filter (quantile mask on the magnitude EMA),
     identical starts, 8 steps; the filter state is not checkpointed by the
     reference, so this is a trajectory check."""
     dev = _dev()
     import scao_amd
-    shapes = SHAPES
-    cfg = dict(CASES["int8_small"][1], sparsity=0.7)
+    shapes, cfg = SPARSE_CASES[case]
     rp = make_params(shapes)
     gp = {k: torch.nn.Parameter(v.detach().clone().to(dev)) for k, v in rp.items()}
     kw = dict(noise_std_init=0.0, async_precond=False, lookahead_k=0)
@@ -417,5 +430,5 @@ def test_sparse_filter_trajectory():
         torch.cuda.synchronize()
         for k in shapes:
             errs.append(_rel(gp[k].detach() - init[k].to(dev), rp[k].detach() - init[k]))
-    report("sparse_filter_trajectory", "int8_small", {"max_cumulative_update_rel_err": max(errs)})
+    report("sparse_filter_trajectory", case, {"max_cumulative_update_rel_err": max(errs)})
     assert max(errs) < 1e-3

@@ -176,6 +176,30 @@ def test_engine_slots_cover_each_once():
         assert n == (E._flat_chunks(it.p.numel()) if it.phase2 and it.lars else 0)
 
 
+def test_pipelined_apply_tasks():
+    """Wide tasks of blocks with k >= PIPE_MIN_RANK carry variant bit 8 and are
+    ordered in runs of APPLY_GROUP tasks of one die's queue."""
+    from scao_amd.engine import PItem
+    items = []
+    for shp in [(1024, 2048)] * 8 + [(512, 1536)]:
+        p = torch.zeros(shp)
+        pre = SparsePreconditioner(p, k_min=128, k_max=128, max_precond_dim=2048)
+        items.append(PItem(p=p, graw=p, gmom=None, st={}, group={}, pre=pre, phase2=True,
+                           step=3, lars=True, leaves=list(pre.leaves())))
+    arrays, _, _, leaves = E._build_structure(items)
+    pipe = arrays["apply14"]
+    assert len(pipe) == sum(lf.m // 16 * (lf.n // 256) for lf, *_ in leaves)
+    assert len(arrays["apply6"]) == 0
+    runs = [pipe[i:i + L.APPLY_GROUP] for i in range(0, len(pipe), L.APPLY_GROUP)]
+    # eight equal blocks, one per die queue: workgroup b takes its run from
+    # queue b % XCDS, and a block's tiles never change queue
+    queue_of = {}
+    for b, run in enumerate(runs[:E.XCDS * 32]):
+        for t in run:
+            queue_of.setdefault(int(t["idx"]), b % E.XCDS)
+            assert queue_of[int(t["idx"])] == b % E.XCDS
+
+
 @pytest.mark.parametrize("shape,fp32", [((2048, 8192), True), ((328, 264), True),
                                         ((320, 448), True), ((100, 37), True),
                                         ((300, 520), True), ((512, 512), False)])
@@ -192,7 +216,7 @@ def test_apply_tasks_tile_each_block_once(shape, fp32):
     seen_wide = False
     for li, (leaf, r0, c0, _) in enumerate(leaves):
         cover = np.zeros((leaf.m, leaf.n), np.int32)
-        for var in range(8):
+        for var in range(16):
             for t in arrays[f"apply{var}"]:
                 if t["idx"] != li:
                     continue
