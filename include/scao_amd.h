@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define SCAO_ABI_VERSION 4
+#define SCAO_ABI_VERSION 5
 
 enum scao_status { SCAO_OK = 0, SCAO_ERR_INVALID = 1, SCAO_ERR_HIP = 2 };
 enum scao_dtype { SCAO_F32 = 0, SCAO_BF16 = 1, SCAO_F16 = 2 };
@@ -275,6 +275,21 @@ typedef struct scao_filter_desc {
 } scao_filter_desc;
 int scao_sparse_filter(const scao_task* tasks, int ntasks, const scao_filter_desc* descs,
                        int ndescs, void* stream);
+
+/* ---- lookahead ------------------------------------------------------------
+ * Replaces SCAO._lookahead_sync (scao/optimizer.py:356-365) for a batch of
+ * parameters: slow = slow + fp32(alpha * (p - slow)); p = slow, with the
+ * reference's three roundings in the parameter dtype.  Tasks are (desc index,
+ * chunk of SCAO_FLAT_CHUNK elements, 0, -1). */
+typedef struct scao_lookahead_desc {
+  void* p;                  /* parameter (dtype)                                 */
+  void* slow;               /* slow weights, same dtype and layout               */
+  int64_t numel;
+  int32_t dtype;
+  int32_t pad0;
+} scao_lookahead_desc;
+int scao_lookahead(const scao_task* tasks, int ntasks, const scao_lookahead_desc* descs,
+                   float alpha, void* stream);
 
 #ifdef __cplusplus
 }

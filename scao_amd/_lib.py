@@ -21,7 +21,7 @@ import torch  # noqa: F401  -- loads torch's HIP runtime before ours
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("SCAO_AMD_LIB", os.path.join(HERE, "_lib", "libscao_amd.so"))
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 SLOT_WIDTH = 3
 FLAT_CHUNK = 4096
 PROJ_COLS = 256
@@ -82,6 +82,10 @@ FILTER_DESC = np.dtype([
     ("flags", "i4"),
 ], align=True)
 FILTER_MASK, FILTER_FIRST = 1, 2
+
+LOOKAHEAD_DESC = np.dtype([
+    ("p", "u8"), ("slow", "u8"), ("numel", "i8"), ("dtype", "i4"), ("pad0", "i4"),
+], align=True)
 FILTER_WORK_WORDS = 2 * 2048 + 8
 
 STRUCTS = {0: (PARAM_DESC, [n for n in PARAM_DESC.names if n != "pad0"]),
@@ -90,7 +94,8 @@ STRUCTS = {0: (PARAM_DESC, [n for n in PARAM_DESC.names if n != "pad0"]),
            3: (PARAM_STAT, [n for n in PARAM_STAT.names if n != "pad0"]),
            4: (GRAM_DESC, [n for n in GRAM_DESC.names if n != "pad0"]),
            5: (PREP_DESC, list(PREP_DESC.names)),
-           6: (FILTER_DESC, list(FILTER_DESC.names))}
+           6: (FILTER_DESC, list(FILTER_DESC.names)),
+           7: (LOOKAHEAD_DESC, [n for n in LOOKAHEAD_DESC.names if n != "pad0"])}
 
 _VP, _I, _I64, _D = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_double
 
@@ -117,6 +122,7 @@ SIGNATURES = {
     "scao_eig_prep": (_I, [_VP, _I, _VP, _I, _VP]),
     "scao_diag_ema": (_I, [_VP, _I, _VP, _VP, _VP]),
     "scao_sparse_filter": (_I, [_VP, _I, _VP, _I, _VP]),
+    "scao_lookahead": (_I, [_VP, _I, _VP, ctypes.c_float, _VP]),
 }
 
 

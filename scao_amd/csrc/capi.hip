@@ -97,6 +97,12 @@ extern "C" int scao_struct_layout(int which, int64_t* out, int cap) {
       PUT(offsetof(S, dtype)); PUT(offsetof(S, flags));
       break;
     }
+    case 7: {
+      typedef scao_lookahead_desc S;
+      PUT(sizeof(S));
+      PUT(offsetof(S, p)); PUT(offsetof(S, slow)); PUT(offsetof(S, numel)); PUT(offsetof(S, dtype));
+      break;
+    }
     default:
       return 0;
   }

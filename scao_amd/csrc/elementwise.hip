@@ -282,6 +282,44 @@ __global__ __launch_bounds__(256) void k_diag_ema(const scao_task* __restrict__ 
   }
 }
 
+// ---------------------------------------------------------- lookahead ---
+// slow = slow + fp32(alpha * (p - slow)); p = slow (three roundings in the
+// parameter dtype, scao/optimizer.py:363-364).  16 B/elem for fp32.
+__global__ __launch_bounds__(256) void k_lookahead(const scao_task* __restrict__ tasks,
+                                                   const scao_lookahead_desc* __restrict__ descs,
+                                                   float alpha) {
+  const scao_task tk = tasks[blockIdx.x];
+  const scao_lookahead_desc& D = descs[tk.idx];
+  const int dt = D.dtype;
+  const Chunk ch(tk, D.numel);
+  const bool aligned = al_dt(D.p, dt) && al_dt(D.slow, dt);
+  v4f p[4], w[4];
+  int mk[4];
+#pragma unroll
+  for (int grp = 0; grp < 4; ++grp) {
+    const int64_t e = ch.elem(grp);
+    mk[grp] = ch.mask(e);
+    const bool vec = aligned && mk[grp] == 15;
+    const v4f z = {0.f, 0.f, 0.f, 0.f};
+    p[grp] = mk[grp] ? ld4(D.p, dt, e, vec, mk[grp]) : z;
+    w[grp] = mk[grp] ? ld4(D.slow, dt, e, vec, mk[grp]) : z;
+  }
+#pragma unroll
+  for (int grp = 0; grp < 4; ++grp) {
+    if (!mk[grp]) continue;
+    const int64_t e = ch.elem(grp);
+    const bool vec = aligned && mk[grp] == 15;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const float d = round_to(dt, p[grp][t] - w[grp][t]);
+      const float a = round_to(dt, alpha * d);
+      w[grp][t] = round_to(dt, w[grp][t] + a);
+    }
+    st4(D.slow, dt, e, w[grp], vec, mk[grp]);
+    st4(D.p, dt, e, w[grp], vec, mk[grp]);
+  }
+}
+
 // ---------------------------------------------------------- finalize ---
 __global__ __launch_bounds__(256) void k_finalize_params(const scao_param_desc* __restrict__ params,
                                                          const double* __restrict__ slots,
@@ -423,6 +461,17 @@ extern "C" int scao_lars_write(const scao_task* tasks, int ntasks, const scao_pa
                                const scao_param_stat* stat, void* stream) {
   SCAO_CHECK_ARG(stat || ntasks == 0, "scao_lars_write: null stat");
   FLAT_LAUNCH("scao_lars_write", k_lars_write, tasks, params, stat);
+}
+
+extern "C" int scao_lookahead(const scao_task* tasks, int ntasks,
+                              const scao_lookahead_desc* descs, float alpha, void* stream) {
+  SCAO_CHECK_ARG(ntasks >= 0, "scao_lookahead: ntasks < 0");
+  if (ntasks == 0) return SCAO_OK;
+  SCAO_CHECK_ARG(tasks && descs, "scao_lookahead: null pointer");
+  hipLaunchKernelGGL(k_lookahead, dim3(ntasks), dim3(256), 0, (hipStream_t)stream, tasks, descs,
+                     alpha);
+  SCAO_LAUNCH_CHECK("scao_lookahead");
+  return SCAO_OK;
 }
 
 extern "C" int scao_diag_ema(const scao_task* tasks, int ntasks, const scao_param_desc* params,

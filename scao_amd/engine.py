@@ -592,6 +592,27 @@ def moment_grads(entries, noise_std: float = 0.0) -> list:
             for _, g in entries]
 
 
+def lookahead(pairs, alpha: float) -> None:
+    """slow = slow + alpha * (p - slow); p = slow for [(p, slow)] in one launch
+    (reference scao/optimizer.py:356-365).  Tensors contiguous, same dtype,
+    on one ROCm device."""
+    pairs = [(p, w) for p, w in pairs if p.numel() > 0]
+    if not pairs:
+        return
+    dev = pairs[0][0].device
+    descs = np.zeros(len(pairs), dtype=L.LOOKAHEAD_DESC)
+    for i, (p, w) in enumerate(pairs):
+        require_hip(p, "lookahead parameter")
+        if w.dtype != p.dtype or w.shape != p.shape or not (p.is_contiguous() and w.is_contiguous()):
+            raise ValueError("lookahead: slow weights must match the parameter")
+        descs[i]["p"], descs[i]["slow"] = p.data_ptr(), w.data_ptr()
+        descs[i]["numel"], descs[i]["dtype"] = p.numel(), L.DTYPE_CODE[p.dtype]
+    tasks = _filter_tasks(tuple(int(p.numel()) for p, _ in pairs), dev)
+    dd = L.upload(descs, dev)
+    _call("scao_lookahead", tasks.data_ptr(), tasks.numel() // L.TASK.itemsize, dd.data_ptr(),
+          alpha, L.stream_ptr(dev))
+
+
 def sparse_filter(entries) -> list:
     """The sparse filter alone for [(filter, grad)] (no noise)."""
     return moment_grads(entries, 0.0)

@@ -223,15 +223,16 @@ class SCAO(Optimizer):
     # ------------------------------------------------------- lookahead ---
     @torch.no_grad()
     def _lookahead_sync(self) -> None:
-        """reference :356-365."""
+        """reference :356-365, every parameter in one batched launch
+        (``scao_lookahead``): slow += alpha * (p - slow); p = slow."""
+        pairs = []
         for g in self.param_groups:
             for p in g["params"]:
                 pid = id(p)
                 if pid not in self._slow_weights:
-                    self._slow_weights[pid] = p.data.clone()
-                slow = self._slow_weights[pid]
-                slow.add_(self._lookahead_alpha * (p.data - slow))
-                p.data.copy_(slow)
+                    self._slow_weights[pid] = p.data.clone(memory_format=torch.contiguous_format)
+                pairs.append((p.data, self._slow_weights[pid]))
+        engine.lookahead(pairs, self._lookahead_alpha)
 
     # ------------------------------------------------------------ rank ---
     def _maybe_adjust_rank(self, pre: SparsePreconditioner, grad_norm: float, group: dict) -> None:

@@ -432,3 +432,53 @@ def test_sparse_filter_trajectory(case):
             errs.append(_rel(gp[k].detach() - init[k].to(dev), rp[k].detach() - init[k]))
     report("sparse_filter_trajectory", case, {"max_cumulative_update_rel_err": max(errs)})
     assert max(errs) < 1e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_lookahead_matches_oracle(dtype):
+    """scao_lookahead (one launch for every parameter) against the oracle's
+    _lookahead_sync on identical parameters and slow weights: bit-identical."""
+    dev = _dev()
+    from scao_amd import engine
+    g = torch.Generator().manual_seed(9)
+    shapes = [(37,), (96, 160), (4, 3, 5, 5), (1000, 1003)]
+    params = [torch.nn.Parameter((torch.randn(s, generator=g) * 0.02).to(dtype)) for s in shapes]
+    slows = [(p.detach() + torch.randn(p.shape, generator=g).to(dtype) * 0.01).clone() for p in params]
+    ref = R.RefSCAO(params, lookahead_k=5, lookahead_alpha=0.5, **PARITY_LA)
+    for p, w in zip(params, slows):
+        ref._slow_weights[id(p)] = w.clone()
+    gp = [p.detach().to(dev).clone() for p in params]
+    gw = [w.to(dev).clone() for w in slows]
+    ref._lookahead_sync()
+    engine.lookahead(list(zip(gp, gw)), 0.5)
+    torch.cuda.synchronize()
+    for p, a, b in zip(params, gp, gw):
+        assert torch.equal(a.cpu(), p.detach()) and torch.equal(b.cpu(), ref._slow_weights[id(p)])
+
+
+PARITY_LA = dict(sparsity=0.0, noise_std_init=0.0, async_precond=False)
+
+
+def test_lookahead_trajectory():
+    """SCAO with lookahead every 2 steps, identical starts, 7 steps."""
+    dev = _dev()
+    import scao_amd
+    cfg = dict(CASES["fp32_small"][1], lookahead_k=2, lookahead_alpha=0.5)
+    rp = make_params(SHAPES)
+    gp = {k: torch.nn.Parameter(v.detach().clone().to(dev)) for k, v in rp.items()}
+    ref = R.RefSCAO(list(rp.values()), **cfg, **PARITY_LA)
+    gopt = scao_amd.SCAO(list(gp.values()), **cfg, **PARITY_LA)
+    init = {k: v.detach().clone() for k, v in rp.items()}
+    worst = 0.0
+    for t in range(1, 8):
+        grads = grads_for_step(t, SHAPES)
+        for k in SHAPES:
+            rp[k].grad = grads[k].clone()
+            gp[k].grad = grads[k].to(dev)
+        ref.step()
+        gopt.step()
+        torch.cuda.synchronize()
+        for k in SHAPES:
+            worst = max(worst, _rel(gp[k].detach() - init[k].to(dev), rp[k].detach() - init[k]))
+    report("lookahead_trajectory", "fp32_small", {"max_cumulative_update_rel_err": worst})
+    assert worst < 1e-4
