@@ -34,6 +34,19 @@ from .preconditioner import SparsePreconditioner
 # v3 helpers (reference scao/optimizer.py:42-214), device tensors
 # --------------------------------------------------------------------------
 
+def _carry_diag_bias(src, dst) -> None:
+    """A diagonal preconditioner's bias factor is not part of the portable
+    ``_scao_precond`` state (scao/preconditioner.py:570-600); the object in
+    the per-parameter state carries it.  Take it over when a preconditioner
+    is rebuilt from another object (the reference's, a checkpoint record or
+    one on another device)."""
+    bias = getattr(src, "_diag_bias_factor", None)
+    if bias is not None and hasattr(dst, "_diag_bias_factor"):
+        dst._diag_bias_factor = float(bias)
+    for a, b in zip(getattr(src, "_blocks", None) or [], getattr(dst, "_blocks", None) or []):
+        _carry_diag_bias(a, b)
+
+
 class _SparseGradFilter:
     """reference :42-57: EMA of |g| and the mask ``ema >= quantile(ema, q)``.
     The work runs in ``scao_sparse_filter`` (one batched launch sequence per
@@ -452,10 +465,11 @@ class SCAO(Optimizer):
         self._restore_fp32_moments(sd)
         owner = {id(p): g for g in self.param_groups for p in g["params"]}
         for idx, (p, st) in enumerate(self.state.items()):
-            if "preconditioner" in st and not isinstance(st["preconditioner"], SparsePreconditioner):
+            old = st.get("preconditioner")
+            if old is not None and (not isinstance(old, SparsePreconditioner)
+                                    or old.device != p.device):
                 st["preconditioner"] = self._make_precond(p, owner[id(p)])
-            elif "preconditioner" in st and st["preconditioner"].device != p.device:
-                st["preconditioner"] = self._make_precond(p, owner[id(p)])
+                _carry_diag_bias(old, st["preconditioner"])
             if idx in extra and "preconditioner" in st:
                 st["preconditioner"].load_state_dict(extra[idx])
         if rt:

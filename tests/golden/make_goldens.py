@@ -19,6 +19,9 @@ drawn param by param in group order; params from manual_seed(0)):
                    low-rank mm, quantise, adaptive rank, natural norm).
   c1_summary    -- the 768x3072 parity config, 100 steps: per-step norms,
                    leading values, int8 code digests, scales and ranks.
+  ref_checkpoint.pt + ckpt_resume -- a checkpoint file written by the
+                   reference's state_dict() after 5 steps, and the parameters
+                   of a fresh reference optimizer resumed from it for 2 steps.
 """
 
 from __future__ import annotations
@@ -224,6 +227,47 @@ def run_c1(scao, steps=100):
     print("c1_summary done")
 
 
+def run_ckpt(scao):
+    """A reference checkpoint file and what the reference does after resuming
+    from it: 5 steps (Phase 1, a refresh, Phase 2), torch.save of
+    state_dict(); a fresh reference optimizer loads the file and takes two
+    more Phase-2 steps.  Stored: the file, the parameters at the save and
+    after each resumed step."""
+    import io
+    cfg = dict(lr=1e-2, weight_decay=0.01, max_precond_dim=32, rho=0.99, use_int8_ema=True,
+               k_min=2, k_max=6, warmup_steps=2, blend_steps=3, precond_freq=4,
+               min_precond_updates=1, tau=1.0, lars_coeff=1e-3, **PARITY)
+    params = make_params(SMALL_SHAPES)
+    opt = scao.SCAO(list(params.values()), **cfg)
+    for t in range(1, 6):
+        grads = grads_for_step(t, params)
+        for k, p in params.items():
+            p.grad = grads[k]
+        opt.step()
+    buf = io.BytesIO()
+    torch.save(opt.state_dict(), buf)
+    with open(os.path.join(HERE, "ref_checkpoint.pt"), "wb") as f:
+        f.write(buf.getvalue())
+    out = {f"ckpt/{k}": p.detach().clone() for k, p in params.items()}
+    resumed = {k: torch.nn.Parameter(p.detach().clone()) for k, p in params.items()}
+    opt2 = scao.SCAO(list(resumed.values()), **cfg)
+    buf.seek(0)
+    opt2.load_state_dict(torch.load(buf, weights_only=False))   # written above
+    for t in (6, 7):
+        grads = grads_for_step(t, resumed)
+        for k, p in resumed.items():
+            p.grad = grads[k]
+        opt2.step()
+        for k, p in resumed.items():
+            out[f"step{t}/{k}"] = p.detach().clone()
+    save_file({k: v.contiguous() for k, v in out.items()},
+              os.path.join(HERE, "ckpt_resume.safetensors"))
+    meta = {"config": cfg, "names": list(SMALL_SHAPES), "saved_after_step": 5,
+            "resumed_steps": [6, 7]}
+    with open(os.path.join(HERE, "ckpt_resume.json"), "w") as f:
+        json.dump(meta, f, indent=1, sort_keys=True)
+
+
 def main():
     sys.path.insert(0, REF)
     warnings.simplefilter("ignore")
@@ -253,6 +297,7 @@ def main():
              steps=10, snap_steps=(10,), outliers=0.01)
     run_ops(scao)
     run_c1(scao)
+    run_ckpt(scao)
 
 
 if __name__ == "__main__":

@@ -167,20 +167,12 @@ def _gpu_from_oracle(ref_opt, ref_params, cfg, dev):
     import scao_amd
     params = {k: torch.nn.Parameter(v.detach().clone().to(dev)) for k, v in ref_params.items()}
     opt = scao_amd.SCAO(list(params.values()), **cfg, **PARITY)
+    # the portable _scao_precond entry lacks a diagonal preconditioner's bias
+    # factor (scao/preconditioner.py:570-600); load_state_dict takes it from
+    # the preconditioner object in the per-parameter state, as the reference's
+    # own resume does
     opt.load_state_dict(copy.deepcopy(ref_opt.state_dict()))
-    # the reference's state_dict does not carry a diagonal preconditioner's
-    # bias factor (scao/preconditioner.py:570-600); hand it over explicitly
-    for a, b in zip(ref_opt.state.values(), opt.state.values()):
-        _copy_bias(a["preconditioner"], b["preconditioner"])
     return params, opt
-
-
-def _copy_bias(a, b):
-    if a.use_block_diagonal:
-        for x, y in zip(a._blocks, b._blocks):
-            _copy_bias(x, y)
-    elif not a.use_kronecker:
-        b._diag_bias_factor = a._diag_bias_factor
 
 
 @pytest.mark.parametrize("case", list(CASES))
@@ -482,3 +474,39 @@ def test_lookahead_trajectory():
             worst = max(worst, _rel(gp[k].detach() - init[k].to(dev), rp[k].detach() - init[k]))
     report("lookahead_trajectory", "fp32_small", {"max_cumulative_update_rel_err": worst})
     assert worst < 1e-4
+
+
+def test_resume_from_reference_checkpoint_file():
+    """A checkpoint file written by the reference (golden fixture), loaded
+    with scao_amd.checkpoint.load (safe loader) onto the GPU, then two
+    Phase-2 steps: each step's update matches what a fresh reference
+    optimizer did after loading the same file (reference's own resume)."""
+    import json
+    import os
+    from safetensors.torch import load_file
+    from scao_amd import checkpoint
+    import scao_amd
+    dev = _dev()
+    gdir = os.path.join(os.path.dirname(__file__), "golden")
+    meta = json.load(open(os.path.join(gdir, "ckpt_resume.json")))
+    vals = load_file(os.path.join(gdir, "ckpt_resume.safetensors"))
+    names = meta["names"]
+    shapes = {k: tuple(vals[f"ckpt/{k}"].shape) for k in names}
+    gp = {k: torch.nn.Parameter(vals[f"ckpt/{k}"].clone().to(dev)) for k in names}
+    opt = scao_amd.SCAO(list(gp.values()), **meta["config"])
+    opt.load_state_dict(checkpoint.load(os.path.join(gdir, "ref_checkpoint.pt"), map_location=dev))
+    prev = {k: vals[f"ckpt/{k}"] for k in names}
+    worst = 0.0
+    for t in meta["resumed_steps"]:
+        grads = grads_for_step(t, shapes)
+        for k in names:
+            gp[k].grad = grads[k].to(dev)
+        opt.step()
+        torch.cuda.synchronize()
+        for k in names:
+            want = vals[f"step{t}/{k}"]
+            err = _rel(gp[k].detach().cpu() - prev[k], want - prev[k])
+            worst = max(worst, err)
+            assert err < 1e-4, (t, k, err)
+            prev[k] = want
+    report("resume_from_reference_checkpoint", "small", {"max_update_rel_err": worst})

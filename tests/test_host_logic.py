@@ -262,3 +262,50 @@ def test_golden_catches_planted_oracle_mistake(monkeypatch):
         for k, p in params.items():   # replay from the golden state, as the gate does
             p.data.copy_(T[f"step{t}.p.{k}"])
     assert worst > 10 * UPD_TOL, worst
+
+
+def test_reference_checkpoint_through_safe_torch_load():
+    """A checkpoint file written by the reference's state_dict() (golden
+    fixture) loads through scao_amd.checkpoint.load (torch.load with
+    weights_only=True; plain weights_only refuses the reference's pickled
+    preconditioner class) into scao_amd.SCAO with every tensor, counter and
+    the diagonal bias factor intact, and this package's own checkpoints go
+    through the same safe loader."""
+    import io
+    import json
+    import os
+    from safetensors.torch import load_file
+    from scao_amd import checkpoint
+    gdir = os.path.join(os.path.dirname(__file__), "golden")
+    meta = json.load(open(os.path.join(gdir, "ckpt_resume.json")))
+    vals = load_file(os.path.join(gdir, "ckpt_resume.safetensors"))
+    path = os.path.join(gdir, "ref_checkpoint.pt")
+    with pytest.raises(Exception, match="scao.preconditioner.SparsePreconditioner"):
+        torch.load(path, weights_only=True)
+    sd = checkpoint.load(path)
+    cfg = meta["config"]
+    mp = [torch.nn.Parameter(vals[f"ckpt/{k}"].clone()) for k in meta["names"]]
+    opt = scao_amd.SCAO(mp, **cfg)
+    opt.load_state_dict(sd)
+    assert opt._global_step == sd["_scao_runtime"]["global_step"] == 5
+    assert opt._global_norm_ema == sd["_scao_runtime"]["global_norm_ema"]
+    for i, (p, st) in enumerate(opt.state.items()):
+        src = sd["state"][i]
+        for key in ("exp_avg", "exp_avg_sq", "exp_avg_diff", "prev_grad"):
+            assert torch.equal(st[key], src[key])
+        assert st["step"] == src["step"] and st["scao_step"] == src["scao_step"]
+        pre = st["preconditioner"]
+        assert isinstance(pre, SparsePreconditioner)
+        assert pre.state_dict().keys() == sd["_scao_precond"][i].keys()
+        for k, v in sd["_scao_precond"][i].items():
+            if isinstance(v, torch.Tensor):
+                assert torch.equal(pre.state_dict()[k], v), (i, k)
+        bias = getattr(src["preconditioner"], "_diag_bias_factor", None)
+        if bias is not None:
+            assert pre._diag_bias_factor == bias
+    buf = io.BytesIO()
+    torch.save(opt.state_dict(), buf)
+    buf.seek(0)
+    again = checkpoint.load(buf)
+    assert again["_scao_runtime"] == sd["_scao_runtime"]
+    assert isinstance(again["state"][0]["preconditioner"], SparsePreconditioner)
