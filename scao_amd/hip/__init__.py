@@ -1,7 +1,8 @@
 """Operator surface of the reference's native layer, on gfx950.
 
 Mirrors ``scao.cuda`` (scao/cuda/__init__.py:149-266): the same function
-names, argument meaning and return values.  Unlike the reference there is
+names (fused_kronecker_precond, low_rank_precond_mm, int8_ema_update),
+argument meaning and return values.  Unlike the reference there is
 no silent fallback: inputs must be float32 tensors on a ROCm device and the
 HIP library must be built; otherwise these raise.  (The reference falls back
 to PyTorch when its extension is missing -- scao/cuda/__init__.py:56-71,
@@ -55,6 +56,25 @@ def fused_kronecker_precond(U_l: Tensor, s_l_inv4: Tensor, U_r: Tensor, s_r_inv4
            s_r_inv4.data_ptr(), G.data_ptr(), G.stride(0), out.data_ptr(), m, n, k,
            ws.data_ptr(), L.stream_ptr(G.device))
     return out
+
+
+def low_rank_precond_mm(U: Tensor, s: Tensor, G: Tensor, left: bool = True) -> Tensor:
+    """left=True: U diag(s) U^T G;  left=False: G U diag(s) U^T
+    (reference :190-228, whose kernel path and fallback :100-117 both compute
+    (U*s) @ (U^T @ G) and (G @ (U*s)) @ U^T).  Not on the optimizer step:
+    two plain GEMMs, run by rocBLAS on the device in that order."""
+    for t, nm in ((U, "U"), (s, "s"), (G, "G")):
+        _check(t, nm)
+    if G.ndim != 2 or U.ndim != 2 or s.numel() != U.shape[1]:
+        raise ValueError(f"shape mismatch: U {tuple(U.shape)}, s {tuple(s.shape)}, "
+                         f"G {tuple(G.shape)}")
+    d = G.shape[0] if left else G.shape[1]
+    if U.shape[0] != d:
+        raise ValueError(f"U has {U.shape[0]} rows, G's {'rows' if left else 'columns'} are {d}")
+    Us = U * s.reshape(1, -1)
+    if left:
+        return Us @ (U.T @ G)
+    return (G @ Us) @ U.T
 
 
 def int8_ema_update(ema_q: Tensor, ema_scale: float, new_val: Tensor, rho: float):

@@ -510,3 +510,21 @@ def test_resume_from_reference_checkpoint_file():
             assert err < 1e-4, (t, k, err)
             prev[k] = want
     report("resume_from_reference_checkpoint", "small", {"max_update_rel_err": worst})
+
+
+def test_low_rank_precond_mm_golden_vectors():
+    """scao_amd.hip.low_rank_precond_mm against the reference's own outputs
+    (golden operator vectors), both sides."""
+    import os
+    from safetensors.torch import load_file
+    from scao_amd.hip import low_rank_precond_mm
+    dev = _dev()
+    T = load_file(os.path.join(os.path.dirname(__file__), "golden", "ops.safetensors"))
+    for i in range(3):
+        G = T[f"fkp{i}.G"].to(dev)
+        for side, U, sv in (("left", T[f"fkp{i}.Ul"], T[f"fkp{i}.sl"]),
+                            ("right", T[f"fkp{i}.Ur"], T[f"fkp{i}.sr"])):
+            out = low_rank_precond_mm(U.to(dev), sv.to(dev), G, side == "left").cpu()
+            want = T[f"lrmm{i}.{side}"]
+            assert out.shape == want.shape
+            assert _rel(out, want) < 1e-5, (i, side)
