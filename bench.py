@@ -248,6 +248,21 @@ def main():
     engine.TIMING = None
     assert all(opt.state[p].get("scao_phase_started") for p in pre_p), "not in Phase 2"
 
+    # per-step distribution (the survey's definition of the metric): an event
+    # before step(), an event and a synchronisation after it, for each step
+    per_step = []
+    for _ in range(max(20, args.steps)):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        one()
+        e1.record()
+        torch.cuda.synchronize()
+        per_step.append(e0.elapsed_time(e1))
+    per_step.sort()
+    step_dist = {"steps": len(per_step), "median_ms": per_step[len(per_step) // 2],
+                 "p90_ms": per_step[min(len(per_step) - 1, int(0.9 * len(per_step)))],
+                 "min_ms": per_step[0], "max_ms": per_step[-1]}
+
     # diagnostic (not the headline): the reference's default moment gradient
     # (sparse filter at sparsity=0.7, noise_std 0.01) for a few steady steps
     sparse = None
@@ -303,6 +318,7 @@ def main():
         "per_kernel_ms": {k: {"count": c, "mean": m_, "total_per_step": t / diag_steps}
                           for k, (c, m_, t) in per_kernel.items()},
         "steady_step_ms": ms,
+        "steady_step_distribution": step_dist,
         "instrumented_step_ms": ms_instrumented,
         "phase1_step_ms": t_phase1,
         "refresh_step_ms": t_refresh,
@@ -336,6 +352,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "details": {"phase1_step_ms": t_phase1, "refresh_step_ms": t_refresh,
+                    "step_median_ms": step_dist["median_ms"], "step_p90_ms": step_dist["p90_ms"],
                     "step_hbm_frac": details["step_roofline"]["hbm_frac"],
                     "steady_step_default_filter_noise_ms": (sparse["steady_step_ms"]
                                                             if sparse else None)},

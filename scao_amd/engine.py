@@ -95,6 +95,7 @@ class Workspace:
         self.runtime = torch.tensor([1.0, 0.0], dtype=torch.float64, device=device)
         self._bufs: dict[str, Tensor] = {}
         self.struct_key = None
+        self.cheap_key = None
         self.leaf_epoch = -1
         self.tasks: dict[str, Tensor] = {}
         self.ntasks: dict[str, int] = {}
@@ -103,6 +104,11 @@ class Workspace:
         self.leaf_dev = None
         self.leaf_index = {}
         self.upd_offsets = {}
+
+    def invalidate(self) -> None:
+        """Forget the cached step structure (rebuilt on the next step)."""
+        self.struct_key = None
+        self.cheap_key = None
 
     def buf(self, name: str, nbytes: int) -> Tensor:
         b = self._bufs.get(name)
@@ -451,10 +457,17 @@ def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
                                 it.gmom.data_ptr() if it.gmom is not None else 0,
                                 st["exp_avg"].data_ptr(), st["exp_avg_sq"].data_ptr(),
                                 st["exp_avg_diff"].data_ptr(), st["prev_grad"].data_ptr())
-    skey = tuple((id(it.p), it.phase2, it.diag, it.lars, it.gmom is not None, it.p.numel(),
-                  it.fp32, it.aligned,
-                  tuple((id(lf), r0, c0, lf.U_l.shape[1]) for lf, r0, c0 in it.leaves))
-                 for it in items)
+    # the full structure key (with every block's rank) is only rebuilt when
+    # the cheap one or the global factor epoch says something may have changed
+    ckey = (tuple((id(it.p), it.phase2, it.diag, it.lars, it.gmom is not None, it.p.numel(),
+                   it.fp32, it.aligned, len(it.leaves)) for it in items), leaf_epoch())
+    skey = ws.struct_key
+    if ckey != ws.cheap_key:
+        skey = tuple((id(it.p), it.phase2, it.diag, it.lars, it.gmom is not None, it.p.numel(),
+                      it.fp32, it.aligned,
+                      tuple((id(lf), r0, c0, lf.U_l.shape[1]) for lf, r0, c0 in it.leaves))
+                     for it in items)
+        ws.cheap_key = ckey
     if skey != ws.struct_key:
         arrays, ranges, nslots, leaves = _build_structure(items)
         ws.tasks = {k: (L.upload(v, dev) if len(v) else None) for k, v in arrays.items()}

@@ -1,14 +1,16 @@
 """Callback metrics and loggers (reference: scao/logging.py:61-219).
 
-Plain Python over the optimizer's host state; computed only when a callback
-is registered.  ``scao/L_norm_mean`` for int8 EMAs uses ``scale * 127`` as
-the reference does, which reads each block's scale back from the device.
+Computed only when a callback is registered.  ``scao/L_norm_mean`` for int8
+EMAs uses ``scale * 127`` as the reference does; the per-block values are
+gathered on the device and read back in one transfer.
 """
 
 from __future__ import annotations
 
 import math
 from typing import Callable
+
+import torch
 
 MetricsDict = dict
 Callback = Callable[[MetricsDict], None]
@@ -75,10 +77,23 @@ class WandbLogger:
             pass
 
 
+def _l_norm_device(pre):
+    """max|L_ema| (int8: scale * 127, in double as the reference's Python
+    float) or ||L_ema||_F, as a device scalar."""
+    scale = getattr(pre, "_scale", None)
+    if getattr(pre, "use_int8_ema", False) and isinstance(scale, torch.Tensor):
+        return scale[0] * 127.0
+    if getattr(pre, "use_int8_ema", False):
+        return torch.tensor(pre.L_ema_scale * 127.0, dtype=torch.float64)
+    return pre.L_ema.norm(p="fro").double()
+
+
 def collect_metrics(optimizer) -> MetricsDict:
-    """reference :151-219."""
+    """reference :151-219.  The per-block EMA norms are gathered on the
+    device and read back in one transfer (the reference reads one Python
+    scalar per block)."""
     step = 0
-    ranks, lnorms = [], []
+    ranks, groups, vals = [], [], []
     for st in optimizer.state.values():
         if "step" in st:
             step = max(step, st["step"])
@@ -86,16 +101,22 @@ def collect_metrics(optimizer) -> MetricsDict:
             pre = st["preconditioner"]
             ranks.append(pre.k)
             if getattr(pre, "use_block_diagonal", False):
-                bn = []
-                for b in pre._blocks:
-                    if b.use_kronecker:
-                        bn.append(b.L_ema_scale * 127.0 if getattr(b, "use_int8_ema", False)
-                                  else b.L_ema.norm(p="fro").item())
-                if bn:
-                    lnorms.append(sum(bn) / len(bn))
+                bl = [b for b in pre._blocks if b.use_kronecker]
+                if bl:
+                    groups.append(len(bl))
+                    vals += [_l_norm_device(b) for b in bl]
             elif getattr(pre, "use_kronecker", False):
-                lnorms.append(pre.L_ema_scale * 127.0 if getattr(pre, "use_int8_ema", False)
-                              else pre.L_ema.norm(p="fro").item())
+                groups.append(1)
+                vals.append(_l_norm_device(pre))
+    host = []
+    if vals:
+        dev = next((v.device for v in vals if v.device.type != "cpu"), torch.device("cpu"))
+        host = torch.stack([v.to(dev) for v in vals]).cpu().tolist()
+    lnorms, i = [], 0
+    for n in groups:
+        bn = host[i:i + n]
+        i += n
+        lnorms.append(bn[0] if n == 1 else sum(bn) / len(bn))
     metrics: MetricsDict = {"step": step}
     if ranks:
         metrics["scao/rank_mean"] = sum(ranks) / len(ranks)

@@ -404,7 +404,7 @@ class SCAO(Optimizer):
         diag = not (pre.use_block_diagonal or pre.use_kronecker)
         it = PItem(p=p, graw=graw, gmom=gmom, st=st, group=group, pre=pre, phase2=True,
                    step=t, scao_step=st["scao_step"], lars=group["lars_coeff"] > 0,
-                   diag=diag, leaves=[] if diag else list(pre.leaves()))
+                   diag=diag, leaves=[] if diag else pre.leaf_list())
         if filt is not None:
             filtered.append((it, filt, graw))
         return it
@@ -481,7 +481,7 @@ class SCAO(Optimizer):
             ws._stable_count = int(rt.get("warmup_stable_count", ws._stable_count))
             ws._early_exit_step = rt.get("warmup_early_exit_step", ws._early_exit_step)
         if self._ws is not None:
-            self._ws.struct_key = None
+            self._ws.invalidate()
 
     def _restore_fp32_moments(self, sd: dict) -> None:
         """``torch.optim.Optimizer.load_state_dict`` casts every floating state

@@ -158,6 +158,19 @@ class SparsePreconditioner:
         self._k = new_k
 
     # ------------------------------------------------------------ leaves --
+    def leaf_list(self) -> list:
+        """``list(self.leaves())``, kept: the block split is fixed at
+        construction (rank changes do not alter it)."""
+        cached = self.__dict__.get("_leaves_cache")
+        if cached is None:
+            cached = self.__dict__["_leaves_cache"] = list(self.leaves())
+        return cached
+
+    def __getstate__(self) -> dict:
+        state = dict(self.__dict__)
+        state.pop("_leaves_cache", None)
+        return state
+
     def leaves(self, r0: int = 0, c0: int = 0):
         """Kronecker blocks as (block, row offset, col offset) in the 2-D view."""
         if self.use_block_diagonal:
