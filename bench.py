@@ -119,7 +119,7 @@ def cpu_baseline(cfg, args):
     opt.step()                                   # state allocation, first step
     t0 = time.perf_counter()
     n = 0
-    while n < args.cpu_steps or (time.perf_counter() - t0 < 5.0 and n < 10):
+    while n < args.cpu_steps or (time.perf_counter() - t0 < args.cpu_seconds and n < 1000):
         opt.step()
         n += 1
     dt = (time.perf_counter() - t0) / n
@@ -139,6 +139,8 @@ def main():
     ap.add_argument("--cpu-baseline", type=int, default=1)
     ap.add_argument("--cpu-threads", type=int, default=16)
     ap.add_argument("--cpu-steps", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0,
+                    help="time the CPU baseline for at least this long (bounded sample)")
     ap.add_argument("--details", default=None, help="write the full report JSON here")
     ap.add_argument("--dominant", default="scao_kron_apply",
                     help="entry point timed with HIP events inside the timed region")
