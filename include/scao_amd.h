@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define SCAO_ABI_VERSION 5
+#define SCAO_ABI_VERSION 6
 
 enum scao_status { SCAO_OK = 0, SCAO_ERR_INVALID = 1, SCAO_ERR_HIP = 2 };
 enum scao_dtype { SCAO_F32 = 0, SCAO_BF16 = 1, SCAO_F16 = 2 };
@@ -50,8 +50,13 @@ enum scao_dtype { SCAO_F32 = 0, SCAO_BF16 = 1, SCAO_F16 = 2 };
 #define SCAO_PF_GSNR  8  /* gSNR mask on the update                                 */
 #define SCAO_PF_DIAG  16 /* diagonal-mode preconditioner (1-D or degenerate 2-D)    */
 #define SCAO_PF_NORM  32 /* accumulate ||g||^2 for the global grad-norm EMA         */
-#define SCAO_PF_GF32  64 /* `g` is a float32 buffer (filtered/noised gradient)     */
+#define SCAO_PF_GF32  64 /* the moments see another gradient than `graw`: the fp32
+                            buffer `g`, or with FMASK/FNOISE one formed in-kernel   */
 #define SCAO_PF_ALIGNED 128 /* every pointer of the param is 16-byte aligned       */
+#define SCAO_PF_FMASK 256   /* moment grad = fp32(graw) * (fema >= *fthr): the sparse
+                               filter's mask (scao_sparse_filter with out == NULL)  */
+#define SCAO_PF_FNOISE 512  /* moment grad += fp32(fnoise * z), z ~ N(0,1) drawn as
+                               scao_sparse_filter draws it from *fseed              */
 
 /* One parameter of a batched step.  Scalars arrive already rounded the way
  * the reference rounds a Python float meeting a float32 tensor. */
@@ -66,6 +71,9 @@ typedef struct scao_param_desc {
   float* prev_grad;
   float* upd;               /* LARS staging of the update (numel) or NULL        */
   const float* diag_ema;    /* diagonal-mode curvature (numel) or NULL           */
+  const float* fema;        /* SCAO_PF_FMASK: the filter's magnitude EMA (numel) */
+  const float* fthr;        /* SCAO_PF_FMASK: device threshold of this step      */
+  const uint64_t* fseed;    /* SCAO_PF_FNOISE: device noise key of this step     */
   int64_t numel;
   int64_t cols;             /* row stride of the 2-D view                        */
   double lr;
@@ -84,7 +92,7 @@ typedef struct scao_param_desc {
   int32_t pre_begin, pre_end;   /* reduction slots written before finalize 0     */
   int32_t post_begin, post_end; /* reduction slots written before finalize 1     */
   int32_t norm_index;       /* position in the global grad-norm average, or -1   */
-  int32_t pad0;
+  float fnoise;             /* SCAO_PF_FNOISE: fp32(noise_std)                   */
 } scao_param_desc;
 
 /* One Kronecker block (a whole 2-D parameter or one block-diagonal piece). */
@@ -252,10 +260,14 @@ int scao_diag_ema(const scao_task* tasks, int ntasks, const scao_param_desc* par
  * order statistics by radix select); out = fp32(g) * (ema >= t).  Without it
  * out = fp32(g).  With noise > 0, out += fp32(noise * z), z ~ N(0,1) from
  * Philox4x32-10 keyed by *seed, counter = element index / 4 (Box-Muller).
+ * With out == NULL the last pass is skipped: the step kernels form the same
+ * values themselves (SCAO_PF_FMASK / SCAO_PF_FNOISE; the threshold is the
+ * float at work + SCAO_FILTER_THR_WORD).
  * torch.quantile refuses more than 2^24 elements; this entry point has no such
  * limit.  Tasks are (desc index, chunk of SCAO_FLAT_CHUNK elements, 0, -1). */
 #define SCAO_FILTER_BINS 2048
 #define SCAO_FILTER_WORK_WORDS (2 * SCAO_FILTER_BINS + 8)
+#define SCAO_FILTER_THR_WORD (2 * SCAO_FILTER_BINS + 7)
 #define SCAO_FILTER_MASK 1
 #define SCAO_FILTER_FIRST 2
 typedef struct scao_filter_desc {

@@ -21,7 +21,7 @@ import torch  # noqa: F401  -- loads torch's HIP runtime before ours
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("SCAO_AMD_LIB", os.path.join(HERE, "_lib", "libscao_amd.so"))
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 SLOT_WIDTH = 3
 FLAT_CHUNK = 4096
 PROJ_COLS = 256
@@ -34,6 +34,8 @@ GRAM_TILE = 128
 F32, BF16, F16 = 0, 1, 2
 PF_DECAY, PF_LARS, PF_CLIP, PF_GSNR, PF_DIAG, PF_NORM, PF_GF32, PF_ALIGNED = (
     1, 2, 4, 8, 16, 32, 64, 128)
+PF_FMASK, PF_FNOISE = 256, 512
+FILTER_THR_WORD = 2 * 2048 + 7
 LF_SINV4, LF_VEC4 = 1, 2
 
 DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
@@ -42,13 +44,14 @@ DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 PARAM_DESC = np.dtype([
     ("p", "u8"), ("g", "u8"), ("graw", "u8"), ("exp_avg", "u8"), ("exp_avg_sq", "u8"),
     ("exp_avg_diff", "u8"), ("prev_grad", "u8"), ("upd", "u8"), ("diag_ema", "u8"),
+    ("fema", "u8"), ("fthr", "u8"), ("fseed", "u8"),
     ("numel", "i8"), ("cols", "i8"), ("lr", "f8"), ("decay", "f4"),
     ("beta1", "f4"), ("omb1", "f4"), ("beta2", "f4"), ("omb2", "f4"), ("beta3", "f4"),
     ("omb3", "f4"), ("bc1", "f4"), ("bc2", "f4"), ("bc3", "f4"), ("blend", "f4"),
     ("omblend", "f4"), ("eps", "f4"), ("tau", "f4"), ("lars", "f4"), ("wd", "f4"),
     ("gsnr", "f4"), ("diag_bias", "f4"), ("adam_sqrt_bc2", "f4"), ("adam_alpha", "f4"),
     ("dtype", "i4"), ("flags", "i4"), ("pre_begin", "i4"), ("pre_end", "i4"),
-    ("post_begin", "i4"), ("post_end", "i4"), ("norm_index", "i4"), ("pad0", "i4"),
+    ("post_begin", "i4"), ("post_end", "i4"), ("norm_index", "i4"), ("fnoise", "f4"),
 ], align=True)
 
 LEAF_DESC = np.dtype([

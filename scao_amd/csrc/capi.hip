@@ -34,7 +34,8 @@ extern "C" int scao_struct_layout(int which, int64_t* out, int cap) {
       PUT(sizeof(S));
       PUT(offsetof(S, p)); PUT(offsetof(S, g)); PUT(offsetof(S, graw)); PUT(offsetof(S, exp_avg));
       PUT(offsetof(S, exp_avg_sq)); PUT(offsetof(S, exp_avg_diff)); PUT(offsetof(S, prev_grad));
-      PUT(offsetof(S, upd)); PUT(offsetof(S, diag_ema)); PUT(offsetof(S, numel));
+      PUT(offsetof(S, upd)); PUT(offsetof(S, diag_ema)); PUT(offsetof(S, fema));
+      PUT(offsetof(S, fthr)); PUT(offsetof(S, fseed)); PUT(offsetof(S, numel));
       PUT(offsetof(S, cols)); PUT(offsetof(S, lr)); PUT(offsetof(S, decay));
       PUT(offsetof(S, beta1)); PUT(offsetof(S, omb1)); PUT(offsetof(S, beta2));
       PUT(offsetof(S, omb2)); PUT(offsetof(S, beta3)); PUT(offsetof(S, omb3));
@@ -44,7 +45,7 @@ extern "C" int scao_struct_layout(int which, int64_t* out, int cap) {
       PUT(offsetof(S, gsnr)); PUT(offsetof(S, diag_bias)); PUT(offsetof(S, adam_sqrt_bc2));
       PUT(offsetof(S, adam_alpha)); PUT(offsetof(S, dtype)); PUT(offsetof(S, flags));
       PUT(offsetof(S, pre_begin)); PUT(offsetof(S, pre_end)); PUT(offsetof(S, post_begin));
-      PUT(offsetof(S, post_end)); PUT(offsetof(S, norm_index));
+      PUT(offsetof(S, post_end)); PUT(offsetof(S, norm_index)); PUT(offsetof(S, fnoise));
       break;
     }
     case 1: {

@@ -50,8 +50,11 @@ __device__ __forceinline__ void adam_chunk(const scao_task& tk, const scao_param
   const int dt = FAST ? SCAO_F32 : P.dtype;
   const Chunk ch(tk, P.numel);
   const bool gf32 = P.flags & SCAO_PF_GF32;
+  const bool fused = fused_mgrad(P);
+  const bool fmask = P.flags & SCAO_PF_FMASK;
   const bool aligned = FAST || (al_dt(P.p, dt) && al16(P.g) && al_dt(P.graw, dt) &&
-                                al16(P.exp_avg) && al16(P.exp_avg_sq) && al16(P.prev_grad));
+                                al16(P.exp_avg) && al16(P.exp_avg_sq) && al16(P.prev_grad) &&
+                                (!fmask || al16(P.fema)));
   const bool decay = P.flags & SCAO_PF_DECAY;
   const float alpha = round_to(dt, P.adam_alpha);
   v4f g[4], gr[4], p[4], m[4], v[4];
@@ -61,8 +64,13 @@ __device__ __forceinline__ void adam_chunk(const scao_task& tk, const scao_param
     const int64_t e = ch.elem(grp);
     if (FAST) {
       mk[grp] = 15;
-      g[grp] = gld4_nt((const float*)P.g + e);
-      gr[grp] = gf32 ? gld4_nt((const float*)P.graw + e) : g[grp];
+      if (fused) {   // g holds the filter's EMA until finish_mgrad below
+        gr[grp] = gld4_nt((const float*)P.graw + e);
+        g[grp] = fmask ? gld4_nt(P.fema + e) : gr[grp];
+      } else {
+        g[grp] = gld4_nt((const float*)P.g + e);
+        gr[grp] = gf32 ? gld4_nt((const float*)P.graw + e) : g[grp];
+      }
       p[grp] = gld4_nt((const float*)P.p + e);
       m[grp] = gld4_nt(P.exp_avg + e);
       v[grp] = gld4_nt(P.exp_avg_sq + e);
@@ -70,12 +78,22 @@ __device__ __forceinline__ void adam_chunk(const scao_task& tk, const scao_param
       mk[grp] = ch.mask(e);
       const bool vec = aligned && mk[grp] == 15;
       const v4f z = {0.f, 0.f, 0.f, 0.f};
-      g[grp] = mk[grp] ? ld_mgrad(P, e, vec, mk[grp]) : z;
-      gr[grp] = (mk[grp] && gf32) ? ld4(P.graw, dt, e, vec, mk[grp]) : g[grp];
+      if (fused) {
+        gr[grp] = mk[grp] ? ld4(P.graw, dt, e, vec, mk[grp]) : z;
+        g[grp] = (mk[grp] && fmask) ? ldf4(P.fema, e, vec, mk[grp]) : gr[grp];
+      } else {
+        g[grp] = mk[grp] ? ld_mgrad(P, e, vec, mk[grp]) : z;
+        gr[grp] = (mk[grp] && gf32) ? ld4(P.graw, dt, e, vec, mk[grp]) : g[grp];
+      }
       p[grp] = mk[grp] ? ld4(P.p, dt, e, vec, mk[grp]) : z;
       m[grp] = mk[grp] ? ldf4(P.exp_avg, e, vec, mk[grp]) : z;
       v[grp] = mk[grp] ? ldf4(P.exp_avg_sq, e, vec, mk[grp]) : z;
     }
+  }
+  if (fused) {
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp)
+      if (mk[grp]) g[grp] = finish_mgrad(P, ch.elem(grp), gr[grp], g[grp], mk[grp]);
   }
   float part = 0.f;
 #pragma unroll
@@ -178,7 +196,8 @@ __global__ __launch_bounds__(256) void k_diag_apply(const scao_task* __restrict_
   const Chunk ch(tk, P.numel);
   const bool aligned = al_dt(P.p, dt) && al16(P.g) && al_dt(P.graw, dt) && al16(P.diag_ema) &&
                        al16(P.exp_avg) && al16(P.exp_avg_sq) && al16(P.exp_avg_diff) &&
-                       al16(P.prev_grad) && (P.upd == nullptr || al16(P.upd));
+                       al16(P.prev_grad) && (P.upd == nullptr || al16(P.upd)) &&
+                       (!(P.flags & SCAO_PF_FMASK) || al16(P.fema));
   double u2 = 0.0;
 #pragma unroll
   for (int grp = 0; grp < 4; ++grp) {
@@ -187,7 +206,10 @@ __global__ __launch_bounds__(256) void k_diag_apply(const scao_task* __restrict_
     if (!mk) continue;
     const bool vec = aligned && mk == 15;
     const v4f graw = ld4(P.graw, dt, e, vec, mk);
-    const v4f g = (P.flags & SCAO_PF_GF32) ? ld_mgrad(P, e, vec, mk) : graw;
+    const v4f g = fused_mgrad(P)
+                      ? finish_mgrad(P, e, graw,
+                                     (P.flags & SCAO_PF_FMASK) ? ldf4(P.fema, e, vec, mk) : graw, mk)
+                      : ((P.flags & SCAO_PF_GF32) ? ld_mgrad(P, e, vec, mk) : graw);
     const v4f dg = ldf4(P.diag_ema, e, vec, mk);
     v4f gp;
 #pragma unroll

@@ -312,48 +312,11 @@ __global__ __launch_bounds__(256) void k_filter_select(const scao_filter_desc* _
 }
 
 // ---------------------------------------------------------------- out ---
-// Philox4x32-10: ten rounds of the published multiply/xor network with the
-// Weyl key schedule (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as
-// easy as 1, 2, 3", SC'11).
-__device__ __forceinline__ void philox(uint32_t (&c)[4], uint32_t k0, uint32_t k1) {
-#pragma unroll
-  for (int r = 0; r < 10; ++r) {
-    const uint32_t lo0 = 0xD2511F53u * c[0], hi0 = __umulhi(0xD2511F53u, c[0]);
-    const uint32_t lo1 = 0xCD9E8D57u * c[2], hi1 = __umulhi(0xCD9E8D57u, c[2]);
-    const uint32_t n0 = hi1 ^ c[1] ^ k0, n2 = hi0 ^ c[3] ^ k1;
-    c[0] = n0;
-    c[1] = lo1;
-    c[2] = n2;
-    c[3] = lo0;
-    k0 += 0x9E3779B9u;
-    k1 += 0xBB67AE85u;
-  }
-}
-
-// four N(0,1) values for the 4-element group starting at element e
-__device__ __forceinline__ v4f normals4(uint64_t key, int64_t e) {
-  const uint64_t ctr = (uint64_t)e >> 2;
-  uint32_t c[4] = {(uint32_t)ctr, (uint32_t)(ctr >> 32), 0u, 0u};
-  philox(c, (uint32_t)key, (uint32_t)(key >> 32));
-  v4f z;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    // uniforms in (0, 1): 24 bits plus half a step
-    const float u1 = ((float)(c[2 * j] >> 8) + 0.5f) * 5.9604645e-8f;
-    const float u2 = ((float)(c[2 * j + 1] >> 8) + 0.5f) * 5.9604645e-8f;
-    const float rad = sqrtf(-2.0f * logf(u1));
-    float sn, cs;
-    sincosf(6.2831853f * u2, &sn, &cs);
-    z[2 * j] = rad * cs;
-    z[2 * j + 1] = rad * sn;
-  }
-  return z;
-}
-
 __global__ __launch_bounds__(256) void k_filter_out(const scao_task* __restrict__ tasks,
                                                     const scao_filter_desc* __restrict__ descs) {
   const scao_task tk = tasks[blockIdx.x];
   const scao_filter_desc& D = descs[tk.idx];
+  if (D.out == nullptr) return;   // the step kernels form the values themselves
   const FChunk ch(tk, D.numel);
   const bool masked = D.flags & SCAO_FILTER_MASK;
   const bool vec = ((((uintptr_t)D.ema) | (uintptr_t)D.out) & 15) == 0 && al_dt(D.g, D.dtype);

@@ -460,7 +460,11 @@ __device__ __forceinline__ void apply_tile(const scao_leaf_desc& L, const scao_p
     rok[r] = i < m && cmask;
     const v4f z = {0.f, 0.f, 0.f, 0.f};
     gr[r] = rok[r] ? ld4(P.graw, dt, e[r], vec, cmask) : z;
-    gm[r] = (GF32 && rok[r]) ? ldf4((const float*)P.g, e[r], vec, cmask) : z;
+    // GF32: the fp32 moment buffer, or (fused) the filter's EMA until finish_mgrad
+    gm[r] = (GF32 && rok[r])
+                ? (fused_mgrad(P) ? ((P.flags & SCAO_PF_FMASK) ? ldf4(P.fema, e[r], vec, cmask) : gr[r])
+                                  : ldf4((const float*)P.g, e[r], vec, cmask))
+                : z;
     mm[r] = rok[r] ? ldf4(P.exp_avg, e[r], vec, cmask) : z;
     vv[r] = rok[r] ? ldf4(P.exp_avg_sq, e[r], vec, cmask) : z;
     dd[r] = rok[r] ? ldf4(P.exp_avg_diff, e[r], vec, cmask) : z;
@@ -511,6 +515,7 @@ __device__ __forceinline__ void apply_tile(const scao_leaf_desc& L, const scao_p
   for (int r = 0; r < 4; ++r) {
     if (!rok[r]) continue;
     const v4f corr = {acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+    if (GF32 && fused_mgrad(P)) gm[r] = finish_mgrad(P, e[r], gr[r], gm[r], cmask);
     v4f out;
     adan4<GF32, LARS>(P, S, dt, gr[r], gm[r], corr, mm[r], vv[r], dd[r], pp[r], par[r], out, u2,
                       cmask);
@@ -550,7 +555,12 @@ __device__ __forceinline__ void apply_wide(const scao_leaf_desc& L, const scao_p
   for (int r = 0; r < 4; ++r) {
     e[r] = L.off + (int64_t)(i0 + 4 * kk + r) * L.ld + jl;
     gr[r] = gld4_nt((const float*)P.graw + e[r]);
-    if (GF32) gm[r] = gld4_nt((const float*)P.g + e[r]);
+    if (GF32) {   // the fp32 moment buffer, or (fused) the filter's EMA
+      if (!fused_mgrad(P))
+        gm[r] = gld4_nt((const float*)P.g + e[r]);
+      else
+        gm[r] = (P.flags & SCAO_PF_FMASK) ? gld4_nt(P.fema + e[r]) : gr[r];
+    }
     mm[r] = gld4_nt(P.exp_avg + e[r]);
     vv[r] = gld4_nt(P.exp_avg_sq + e[r]);
     dd[r] = gld4_nt(P.exp_avg_diff + e[r]);
@@ -590,6 +600,7 @@ __device__ __forceinline__ void apply_wide(const scao_leaf_desc& L, const scao_p
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const v4f corr = {acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+    if (GF32 && fused_mgrad(P)) gm[r] = finish_mgrad(P, e[r], gr[r], gm[r], 15);
     v4f out;
     adan4<GF32, LARS>(P, S, SCAO_F32, gr[r], gm[r], corr, mm[r], vv[r], dd[r], pp[r], par[r], out,
                       u2, 15);
@@ -686,7 +697,12 @@ __global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict_
     for (int r = 0; r < 4; ++r) {
       e[r] = L.off + (int64_t)(tk.a + 4 * kk + r) * L.ld + jl;
       gr[r] = gld4_nt((const float*)P.graw + e[r]);
-      if (GF32) gm[r] = gld4_nt((const float*)P.g + e[r]);
+      if (GF32) {
+        if (!fused_mgrad(P))
+          gm[r] = gld4_nt((const float*)P.g + e[r]);
+        else
+          gm[r] = (P.flags & SCAO_PF_FMASK) ? gld4_nt(P.fema + e[r]) : gr[r];
+      }
       mm[r] = gld4_nt(P.exp_avg + e[r]);
       vv[r] = gld4_nt(P.exp_avg_sq + e[r]);
       dd[r] = gld4_nt(P.exp_avg_diff + e[r]);
@@ -714,6 +730,7 @@ __global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict_
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const v4f corr = *(const v4f*)&cbuf[s & 1][4 * kk + r][64 * w + 4 * (l % 16)];
+      if (GF32 && fused_mgrad(P)) gm[r] = finish_mgrad(P, e[r], gr[r], gm[r], 15);
       v4f out;
       adan4<GF32, LARS>(P, S, SCAO_F32, gr[r], gm[r], corr, mm[r], vv[r], dd[r], pp[r], par[r],
                         out, u2, 15);

@@ -145,6 +145,82 @@ __device__ __forceinline__ void stf4(float* base, int64_t i, v4f x, bool vec, in
 }
 
 // the gradient the moments use: raw p.grad in its dtype, or a float32 buffer
+// ---- gradient noise: Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel
+// random numbers: as easy as 1, 2, 3", SC'11): ten rounds of the published
+// multiply/xor network with the Weyl key schedule; Box-Muller turns the four
+// words of counter (element index / 4) into four N(0,1) values.
+__device__ __forceinline__ void philox(uint32_t (&c)[4], uint32_t k0, uint32_t k1) {
+#pragma unroll
+  for (int r = 0; r < 10; ++r) {
+    const uint32_t lo0 = 0xD2511F53u * c[0], hi0 = __umulhi(0xD2511F53u, c[0]);
+    const uint32_t lo1 = 0xCD9E8D57u * c[2], hi1 = __umulhi(0xCD9E8D57u, c[2]);
+    const uint32_t n0 = hi1 ^ c[1] ^ k0, n2 = hi0 ^ c[3] ^ k1;
+    c[0] = n0;
+    c[1] = lo1;
+    c[2] = n2;
+    c[3] = lo0;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+}
+
+// N(0,1) values of elements e .. e+3 for e a multiple of 4
+__device__ __forceinline__ v4f normals4(uint64_t key, int64_t e) {
+  const uint64_t ctr = (uint64_t)e >> 2;
+  uint32_t c[4] = {(uint32_t)ctr, (uint32_t)(ctr >> 32), 0u, 0u};
+  philox(c, (uint32_t)key, (uint32_t)(key >> 32));
+  v4f z;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    // uniforms in (0, 1): 24 bits plus half a step
+    const float u1 = ((float)(c[2 * j] >> 8) + 0.5f) * 5.9604645e-8f;
+    const float u2 = ((float)(c[2 * j + 1] >> 8) + 0.5f) * 5.9604645e-8f;
+    const float rad = sqrtf(-2.0f * logf(u1));
+    float sn, cs;
+    sincosf(6.2831853f * u2, &sn, &cs);
+    z[2 * j] = rad * cs;
+    z[2 * j + 1] = rad * sn;
+  }
+  return z;
+}
+
+// The moment gradient of elements e .. e+3 from their raw values and, with
+// SCAO_PF_FMASK, the filter's EMA values `em` (loaded by the caller with its
+// other streams): fp32(g) * (em >= t), then + fp32(fnoise * z) with
+// SCAO_PF_FNOISE -- the values scao_sparse_filter's output pass would write.
+// Lanes outside `mask` are left as they are.
+__device__ __forceinline__ v4f finish_mgrad(const scao_param_desc& P, int64_t e, const v4f& gr,
+                                            const v4f& em, int mask) {
+  v4f o = gr;
+  if (P.flags & SCAO_PF_FMASK) {
+    const float thr = *P.fthr;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) o[t] = gr[t] * (em[t] >= thr ? 1.0f : 0.0f);
+  }
+  if (P.flags & SCAO_PF_FNOISE) {
+    const uint64_t key = *P.fseed;
+    if ((e & 3) == 0) {
+      const v4f z = normals4(key, e);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) o[t] = o[t] + z[t] * P.fnoise;
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (!(mask & (1 << t))) continue;
+        const int64_t i = e + t;
+        const v4f z = normals4(key, i & ~(int64_t)3);
+        o[t] = o[t] + z[(int)(i & 3)] * P.fnoise;
+      }
+    }
+  }
+  return o;
+}
+
+// true when the moment gradient is formed in-kernel from graw (+ the EMA)
+__device__ __forceinline__ bool fused_mgrad(const scao_param_desc& P) {
+  return (P.flags & (SCAO_PF_FMASK | SCAO_PF_FNOISE)) != 0;
+}
+
 __device__ __forceinline__ v4f ld_mgrad(const scao_param_desc& P, int64_t i, bool vec, int mask) {
   if (P.flags & SCAO_PF_GF32) return ldf4((const float*)P.g, i, vec, mask);
   return ld4(P.g, P.dtype, i, vec, mask);

@@ -32,6 +32,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass, field
+from typing import NamedTuple
 
 import numpy as np
 import torch
@@ -85,6 +86,12 @@ class PItem:
     leaves: list = field(default_factory=list)  # [(leaf, r0, c0)]
     fp32: bool = True            # param and gradient are float32
     aligned: bool = True         # every pointer of the param is 16-byte aligned
+    msrc: "MomentSource | None" = None   # filter/noise formed inside the step kernels
+
+    @property
+    def mgrad(self) -> bool:
+        """The moments see another gradient than p.grad."""
+        return self.gmom is not None or self.msrc is not None
 
 
 class Workspace:
@@ -231,7 +238,7 @@ def _build_structure(items: list[PItem]):
                 for i0 in range(0, leaf.m, 64):
                     for d0 in range(0, k, 64):
                         tasks["lift"].append((li, i0, d0, -1))
-                var = (1 if it.gmom is not None else 0) | (2 if it.lars else 0)
+                var = (1 if it.mgrad else 0) | (2 if it.lars else 0)
                 ok = _leaf_vec(it, leaf, r0, c0l) and it.fp32 and it.aligned and k % 16 == 0
                 m, n, T = leaf.m, leaf.n, L.APPLY_TILE
                 # wide 16x256 tiles over the interior that they tile exactly,
@@ -356,7 +363,8 @@ def _param_table(items: list[PItem], ranges, ws: Workspace, gsnr: float | None):
                             "prev_grad", "upd", "diag_ema", "numel", "cols", "lr", "decay",
                             "beta1", "omb1", "beta2", "omb2", "beta3", "omb3", "bc1", "bc2",
                             "bc3", "blend", "omblend", "eps", "tau", "lars", "wd", "gsnr",
-                            "diag_bias", "adam_sqrt_bc2", "adam_alpha", "dtype", "flags")}
+                            "diag_bias", "adam_sqrt_bc2", "adam_alpha", "dtype", "flags",
+                            "fema", "fthr", "fseed", "fnoise")}
     upd_base = ws.buf("upd", 4).data_ptr() if ws.upd_total else 0
     for i, it in enumerate(items):
         g, st = it.group, it.st
@@ -391,6 +399,21 @@ def _param_table(items: list[PItem], ranges, ws: Workspace, gsnr: float | None):
         cols["decay"].append(1.0 - lr * wd if wd != 0.0 else 1.0)
         if it.gmom is not None:
             flags |= L.PF_GF32
+        ms = it.msrc
+        fema = fthr = fseed = 0
+        fnoise = 0.0
+        if ms is not None:
+            flags |= L.PF_GF32
+            if ms.ema is not None:
+                flags |= L.PF_FMASK
+                fema, fthr = ms.ema.data_ptr(), ms.thr
+            if ms.noise > 0.0:
+                flags |= L.PF_FNOISE
+                fseed, fnoise = ms.seed, ms.noise
+        cols["fema"].append(fema)
+        cols["fthr"].append(fthr)
+        cols["fseed"].append(fseed)
+        cols["fnoise"].append(fnoise)
         bc1 = 1.0 - beta1 ** t
         bc2 = 1.0 - beta2 ** t
         upd = diag = 0
@@ -455,15 +478,17 @@ def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
         it.fp32 = it.p.dtype == torch.float32 and it.graw.dtype == torch.float32
         it.aligned = _aligned16(it.p.data_ptr(), it.graw.data_ptr(),
                                 it.gmom.data_ptr() if it.gmom is not None else 0,
+                                it.msrc.ema.data_ptr() if it.msrc is not None and
+                                it.msrc.ema is not None else 0,
                                 st["exp_avg"].data_ptr(), st["exp_avg_sq"].data_ptr(),
                                 st["exp_avg_diff"].data_ptr(), st["prev_grad"].data_ptr())
     # the full structure key (with every block's rank) is only rebuilt when
     # the cheap one or the global factor epoch says something may have changed
-    ckey = (tuple((id(it.p), it.phase2, it.diag, it.lars, it.gmom is not None, it.p.numel(),
+    ckey = (tuple((id(it.p), it.phase2, it.diag, it.lars, it.mgrad, it.p.numel(),
                    it.fp32, it.aligned, len(it.leaves)) for it in items), leaf_epoch())
     skey = ws.struct_key
     if ckey != ws.cheap_key:
-        skey = tuple((id(it.p), it.phase2, it.diag, it.lars, it.gmom is not None, it.p.numel(),
+        skey = tuple((id(it.p), it.phase2, it.diag, it.lars, it.mgrad, it.p.numel(),
                       it.fp32, it.aligned,
                       tuple((id(lf), r0, c0, lf.U_l.shape[1]) for lf, r0, c0 in it.leaves))
                      for it in items)
@@ -624,6 +649,64 @@ def lookahead(pairs, alpha: float) -> None:
     dd = L.upload(descs, dev)
     _call("scao_lookahead", tasks.data_ptr(), tasks.numel() // L.TASK.itemsize, dd.data_ptr(),
           alpha, L.stream_ptr(dev))
+
+
+class MomentSource(NamedTuple):
+    """Where the step kernels find the moment gradient's ingredients: the
+    filter's EMA (or None) and the device addresses of its threshold and of
+    the noise key.  ``keep`` holds the tensors those addresses point into."""
+    ema: Tensor | None
+    thr: int
+    seed: int
+    noise: float
+    keep: tuple
+
+
+def moment_sources(entries, noise_std: float = 0.0) -> list:
+    """Like ``moment_grads`` but without writing the moment gradients: the
+    filter's EMA and threshold are computed (one batched launch, output pass
+    skipped) and the step kernels form fp32(g) * (ema >= t) + noise
+    themselves from them (SCAO_PF_FMASK / SCAO_PF_FNOISE).  Returns one
+    MomentSource per entry."""
+    entries = list(entries)
+    if not entries:
+        return []
+    dev = entries[0][1].device
+    noisy = noise_std > 0.0
+    seeds = (torch.randint(0, 2 ** 62, (len(entries),), dtype=torch.int64, device=dev)
+             if noisy else None)
+    launch = [(i, f, g) for i, (f, g) in enumerate(entries) if f is not None and g.numel() > 0]
+    if launch:
+        n = len(launch)
+        descs = np.zeros(n, dtype=L.FILTER_DESC)
+        for j, (_, f, g) in enumerate(launch):
+            require_hip(g, "moment gradient")
+            flags = L.FILTER_MASK
+            if f.mag_ema is None:
+                f.mag_ema = torch.empty(g.shape, dtype=torch.float32, device=dev)
+                flags |= L.FILTER_FIRST
+            if getattr(f, "work", None) is None or f.work.device != dev:
+                f.work = torch.zeros(L.FILTER_WORK_WORDS, dtype=torch.int32, device=dev)
+            e = descs[j]
+            e["g"], e["ema"], e["out"] = g.data_ptr(), f.mag_ema.data_ptr(), 0
+            e["work"] = f.work.data_ptr()
+            e["numel"] = g.numel()
+            e["decay"], e["omd"], e["q"] = f.ema, 1.0 - f.ema, f.sparsity
+            e["dtype"] = L.DTYPE_CODE[g.dtype]
+            e["flags"] = flags
+        tasks = _filter_tasks(tuple(int(g.numel()) for _, _, g in launch), dev)
+        dd = L.upload(descs, dev)
+        _call("scao_sparse_filter", tasks.data_ptr(), tasks.numel() // L.TASK.itemsize,
+              dd.data_ptr(), n, L.stream_ptr(dev))
+    out = []
+    for i, (f, g) in enumerate(entries):
+        ema = f.mag_ema if f is not None and g.numel() > 0 else None
+        thr = f.work.data_ptr() + 4 * L.FILTER_THR_WORD if ema is not None else 0
+        seed = seeds.data_ptr() + 8 * i if noisy else 0
+        keep = tuple(x for x in (ema, f.work if ema is not None else None, seeds)
+                     if x is not None)
+        out.append(MomentSource(ema, thr, seed, noise_std if noisy else 0.0, keep))
+    return out
 
 
 def sparse_filter(entries) -> list:

@@ -339,17 +339,18 @@ class SCAO(Optimizer):
 
     def _filter_and_noise(self, items: list, filtered: list) -> None:
         """The gradient the moments see (reference :533-545): the filtered
-        parameters, and with noise every parameter, go through one batched
-        launch sequence (scao_sparse_filter: filter, then noise_std * N(0,1)
-        from a counter-based generator keyed per parameter and step)."""
+        parameters go through one batched launch (scao_sparse_filter: EMA and
+        threshold); the step kernels then form fp32(g) * mask + noise_std *
+        N(0, 1) themselves (counter-based generator keyed per parameter and
+        step), so the moment gradient is never written out."""
         noise = self._noise_std if self._noise_std > 1e-9 else 0.0
         filt = {id(it): f for it, f, _ in filtered}
         todo = [it for it in items if id(it) in filt or noise > 0.0]
         if not todo:
             return
-        outs = engine.moment_grads([(filt.get(id(it)), it.graw) for it in todo], noise)
-        for it, out in zip(todo, outs):
-            it.gmom = out
+        srcs = engine.moment_sources([(filt.get(id(it)), it.graw) for it in todo], noise)
+        for it, src in zip(todo, srcs):
+            it.msrc = src
 
     def _plan_param(self, group: dict, p: Tensor, refresh: list, filtered: list) -> PItem:
         """Host half of reference _step_group (:521-605) for one parameter."""

@@ -223,3 +223,38 @@ def test_optimizer_noise_anneals_and_is_applied():
             z = (m.double().cpu() / (0.1 * std)).numpy().ravel()
             assert abs(z.std() - 1.0) < 2e-2 and _ks_normal(z) > 1e-4
     assert opt._noise_std == pytest.approx(0.005)
+
+
+@pytest.mark.parametrize("phase2", [False, True])
+def test_step_kernels_form_the_filter_output(phase2):
+    """In a step the filter's output pass is skipped and the step kernels form
+    fp32(g) * (ema >= t) + noise themselves.  The moment gradient they used
+    (stored as prev_grad) equals, bit for bit, what the output pass writes for
+    the same filter state and noise key: Phase 1 through the Adam kernel,
+    Phase 2 through the wide, masked and diagonal apply paths."""
+    import scao_amd
+    from scao_amd import engine
+    from scao_amd.optimizer import _SparseGradFilter
+    dev = _dev()
+    shapes = [(512, 512), (100, 37), (300,), (96, 160)]
+    g = torch.Generator().manual_seed(17)
+    params = [torch.nn.Parameter((torch.randn(s, generator=g) * 0.02).to(dev)) for s in shapes]
+    grads = [(torch.randn(s, generator=g) * 1e-3).to(dev) for s in shapes]
+    sched = (dict(warmup_steps=0, min_precond_updates=0, precond_freq=10 ** 9) if phase2
+             else dict(warmup_steps=10))
+    opt = scao_amd.SCAO(params, lr=1e-3, sparsity=0.7, noise_std_init=0.01, lookahead_k=0,
+                        async_precond=False, k_min=64, k_max=64, max_precond_dim=512, **sched)
+    for p, gr in zip(params, grads):
+        p.grad = gr.clone()
+    torch.manual_seed(7)
+    opt.step()
+    filters = [_SparseGradFilter(0.7) for _ in shapes]
+    torch.manual_seed(7)
+    want = engine.moment_grads(list(zip(filters, grads)), 0.01)
+    torch.cuda.synchronize()
+    for p, w, f in zip(params, want, filters):
+        st = opt.state[p]
+        assert torch.equal(st["prev_grad"], w), tuple(p.shape)
+        assert torch.equal(opt._sparse_filters[id(p)].mag_ema, f.mag_ema)
+    if phase2:
+        assert all(opt.state[p].get("scao_phase_started") for p in params)

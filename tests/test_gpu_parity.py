@@ -392,6 +392,7 @@ def test_bf16_params_from_shared_state():
 SPARSE_CASES = {
     "int8_small": (SHAPES, dict(CASES["int8_small"][1], sparsity=0.7)),
     # filtered moments (GF32) through the fast and the pipelined apply kernels
+    "fast_k64": (FAST, dict(CASES["fast_k64"][1], sparsity=0.7)),
     "fast_k128": (FAST, dict(CASES["fast_k128_nolars"][1], sparsity=0.7, lars_coeff=1e-3,
                              tau=1.0, weight_decay=0.01)),
 }
