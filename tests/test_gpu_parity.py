@@ -529,3 +529,52 @@ def test_low_rank_precond_mm_golden_vectors():
             want = T[f"lrmm{i}.{side}"]
             assert out.shape == want.shape
             assert _rel(out, want) < 1e-5, (i, side)
+
+
+FEATURES = {
+    # gSNR mask on the update (reference scao/optimizer.py:160-181)
+    "gsnr": (dict(CASES["fp32_small"][1], use_gsnr_clip=True, gsnr_threshold=0.5), 12),
+    # refresh triggered by the gradient-norm change (:187-214)
+    "lazy_precond": (dict(CASES["int8_small"][1], lazy_precond=True, lazy_delta_threshold=0.05,
+                          lazy_max_skip=3), 14),
+    # warm-up that ends when the gradient norm settles (:106-154)
+    "adaptive_warmup": (dict(CASES["fp32_small"][1], adaptive_warmup=True, warmup_steps=30,
+                             warmup_stability_threshold=0.5, warmup_patience=2), 26),
+    # sparsity from the layer's norm against the global EMA (:60-99)
+    "dynamic_sparsity": (dict(CASES["int8_small"][1], sparsity=0.7, dynamic_sparsity=True), 12),
+    # rank moved by the gradient-norm ratio (:383-401)
+    "adaptive_rank": (dict(CASES["fp32_small"][1], adaptive_rank=True, k_min=2, k_max=8), 12),
+}
+
+
+@pytest.mark.parametrize("feature", list(FEATURES))
+def test_feature_trajectory(feature):
+    """The reference's optional features, identical starts, against the
+    oracle: cumulative update per parameter, ranks and runtime state."""
+    dev = _dev()
+    import scao_amd
+    cfg, steps = FEATURES[feature]
+    kw = dict(noise_std_init=0.0, async_precond=False, lookahead_k=0)
+    cfg = {**cfg, **{k: v for k, v in kw.items()}}
+    cfg.setdefault("sparsity", 0.0)
+    rp = make_params(SHAPES)
+    gp = {k: torch.nn.Parameter(v.detach().clone().to(dev)) for k, v in rp.items()}
+    ref = R.RefSCAO(list(rp.values()), **cfg)
+    gopt = scao_amd.SCAO(list(gp.values()), **cfg)
+    init = {k: v.detach().clone() for k, v in rp.items()}
+    worst = 0.0
+    for t in range(1, steps + 1):
+        grads = grads_for_step(t, SHAPES)
+        for k in SHAPES:
+            rp[k].grad = grads[k].clone()
+            gp[k].grad = grads[k].to(dev)
+        ref.step()
+        gopt.step()
+        torch.cuda.synchronize()
+        for k in SHAPES:
+            worst = max(worst, _rel(gp[k].detach() - init[k].to(dev), rp[k].detach() - init[k]))
+        assert gopt.current_ranks() == ref.current_ranks(), (t, feature)
+        assert gopt._in_warmup_global == ref._in_warmup_global, t
+    assert gopt._global_norm_ema == pytest.approx(ref._global_norm_ema, rel=1e-5)
+    report("feature_trajectory", feature, {"max_cumulative_update_rel_err": worst})
+    assert worst < 1e-3, worst
