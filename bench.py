@@ -1,4 +1,4 @@
-"""SCAO.step on one MI355X at the Llama-3.2-1B shape.
+"""SCAO.step on one MI355X at the Llama-3.2-1B shape (16 layers, hidden 2048, FFN 8192).
 
 Workload: the 16-layer Llama-3.2-1B parameter set (q/o 2048x2048, k/v
 512x2048, gate/up 8192x2048, down 2048x8192 preconditioned: 224 blocks of

@@ -30,7 +30,6 @@ adaptive rank are restated from ``scao/optimizer.py:106-214, 383-401``.
 from __future__ import annotations
 
 import math
-import warnings
 from typing import Callable, Iterable, Optional
 
 import torch

@@ -194,7 +194,3 @@ def upload(arr: np.ndarray, device: torch.device) -> torch.Tensor:
     host = torch.empty(raw.size, dtype=torch.uint8, pin_memory=True)
     host.numpy()[:] = raw
     return host.to(device, non_blocking=True)
-
-
-def ptr(t) -> int:
-    return 0 if t is None else t.data_ptr()

@@ -42,12 +42,6 @@ from . import _lib as L
 from .preconditioner import SparsePreconditioner, leaf_epoch
 from .utils import batched_adaptive_rank, to_2d
 
-F32 = np.float32
-
-
-def _f32(x: float) -> float:
-    """A Python float rounded the way ATen rounds a scalar operand of an fp32 op."""
-    return float(F32(x))
 
 
 def _align4(n: int) -> int:
@@ -718,12 +712,6 @@ def _grads_moved(items, ws) -> bool:
     ptrs = getattr(ws, "grad_ptrs", None)
     return ptrs is None or len(ptrs) != len(items) or any(
         p != it.graw.data_ptr() for p, it in zip(ptrs, items))
-
-
-def read_stats(ws: Workspace, n: int) -> np.ndarray:
-    """Per-parameter statistics of the last step (host copy; synchronises)."""
-    raw = ws.buf("stat", n * L.PARAM_STAT.itemsize)[: n * L.PARAM_STAT.itemsize].cpu().numpy()
-    return raw.view(L.PARAM_STAT)
 
 
 # --------------------------------------------------------------------------

@@ -189,7 +189,7 @@ def run_ops(scao):
 
 
 def run_c1(scao, steps=100):
-    """one 768x3072 fp32 Linear weight."""
+    """The 768x3072 parity configuration: one fp32 Linear weight."""
     g0 = torch.Generator().manual_seed(0)
     p = torch.nn.Parameter(torch.randn(768, 3072, generator=g0) * 0.02)
     cfg = dict(lr=1e-3, use_int8_ema=True, k_min=32, k_max=32, max_precond_dim=1024,

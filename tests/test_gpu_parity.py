@@ -273,7 +273,7 @@ def test_state_dict_layout_matches_oracle():
 
 
 def test_trajectory_c1_shape():
-    """BASELINE config 1 shape (768x3072, k=32, D=1024, int8) for 40 steps
+    """The 768x3072 parity configuration (k=32, D=1024, int8) for 40 steps
     (Phase 1, refreshes, blend); drift reported, loose gate."""
     dev = _dev()
     import scao_amd

@@ -10,7 +10,6 @@ term, a wrong sign, a swapped operand changes results at the 1e-2 level).
 
 from __future__ import annotations
 
-import hashlib
 import json
 import os
 
@@ -159,7 +158,7 @@ def test_ops_vectors():
 
 
 def test_c1_summary():
-    """BASELINE config 1 (768x3072, 100 steps) against the reference's run."""
+    """The 768x3072 parity configuration (100 steps) against the reference's run."""
     from safetensors.torch import load_file
     with open(os.path.join(GOLDEN, "c1_summary.json")) as f:
         ref = json.load(f)
