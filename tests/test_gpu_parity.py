@@ -346,25 +346,27 @@ def a_leaves(pre, r0=0, c0=0):
         yield pre, r0, c0
 
 
-def test_bf16_params_from_shared_state():
-    """bf16 parameters and gradients (the reference keeps fp32 statistics and
-    writes ``p.add_(u.to(bf16), alpha=a)``).  ATen's CPU kernel for that write
-    rounds ``a`` to bf16 and fuses the multiply-add in fp32 over whole vectors
-    (32 lanes with AVX-512, 16 with AVX2); the last ``numel % vec`` elements go
-    through a scalar loop that also rounds ``a*u`` to bf16 first.  The HIP
-    write follows the vector form, so over the first ``32*floor(n/32)``
-    elements of each parameter the Adam-phase steps (bit-exact fp32
-    arithmetic) must agree exactly; every element must agree to within one
-    bf16 ulp of the result plus one of the step, which covers the scalar tail
-    and a one-ulp difference of the bf16-rounded update in the SCAO phase."""
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_half_params_from_shared_state(dtype):
+    """bf16 and fp16 parameters and gradients (the reference keeps fp32
+    statistics and writes ``p.add_(u.to(dtype), alpha=a)``).  ATen's CPU
+    kernel for that write rounds ``a`` to the parameter dtype and fuses the
+    multiply-add in fp32 over whole vectors (32 lanes with AVX-512, 16 with
+    AVX2); the last ``numel % vec`` elements go through a scalar loop that also
+    rounds ``a*u`` first.  The HIP write follows the vector form, so over the
+    first ``32*floor(n/32)`` elements of each parameter the Adam-phase steps
+    (bit-exact fp32 arithmetic) must agree exactly; every element must agree
+    to within one ulp of the result (2^-7 for bf16, 2^-10 for fp16) plus one
+    of the step, which covers the scalar tail and a one-ulp difference of the
+    rounded update in the SCAO phase."""
     dev = _dev()
     shapes, cfg, steps = SHAPES, dict(CASES["int8_small"][1]), 12
-    rp = make_params(shapes, dtype=torch.bfloat16)
+    rp = make_params(shapes, dtype=dtype)
     ref = R.RefSCAO(list(rp.values()), **cfg, **PARITY)
     worst, exact_min = 0.0, 1.0
     for t in range(1, steps + 1):
         gp, gopt = _gpu_from_oracle(ref, rp, cfg, dev)
-        grads = grads_for_step(t, shapes, dtype=torch.bfloat16)
+        grads = grads_for_step(t, shapes, dtype=dtype)
         before = {k: v.detach().float().clone() for k, v in rp.items()}
         for k in shapes:
             rp[k].grad = grads[k].clone()
@@ -373,10 +375,11 @@ def test_bf16_params_from_shared_state():
         gopt.step()
         torch.cuda.synchronize()
         for k in shapes:
-            assert gp[k].dtype == torch.bfloat16
+            assert gp[k].dtype == dtype
             a, b = rp[k].detach().float().flatten(), gp[k].detach().cpu().float().flatten()
             step = (a - before[k].flatten()).abs()
-            tol = (a.abs() + step) * 2.0 ** -7 + 1e-30
+            ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+            tol = (a.abs() + step) * ulp + 1e-30
             ratio = ((a - b).abs() / tol).max().item()
             worst = max(worst, ratio)
             assert ratio <= 1.0, (t, k, ratio)
@@ -385,7 +388,7 @@ def test_bf16_params_from_shared_state():
                 exact = (a[:nv] == b[:nv]).float().mean().item()
                 exact_min = min(exact_min, exact)
                 assert exact >= 0.99, (t, k, exact)
-    report("bf16_params_from_shared_state", "int8_small",
+    report("half_params_from_shared_state", str(dtype),
            {"max_err_over_bound": worst, "adam_phase_exact_fraction_min": exact_min})
 
 
