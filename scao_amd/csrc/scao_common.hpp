@@ -164,7 +164,10 @@ __device__ __forceinline__ void philox(uint32_t (&c)[4], uint32_t k0, uint32_t k
   }
 }
 
-// N(0,1) values of elements e .. e+3 for e a multiple of 4
+// N(0,1) values of elements e .. e+3 for e a multiple of 4.  Box-Muller on
+// the hardware transcendentals: -2 ln u = -2 ln2 * v_log_f32(u) (log2),
+// v_sqrt_f32, and v_sin_f32 / v_cos_f32, which take the angle in
+// revolutions -- u2 in (0, 1] already is one.
 __device__ __forceinline__ v4f normals4(uint64_t key, int64_t e) {
   const uint64_t ctr = (uint64_t)e >> 2;
   uint32_t c[4] = {(uint32_t)ctr, (uint32_t)(ctr >> 32), 0u, 0u};
@@ -175,11 +178,9 @@ __device__ __forceinline__ v4f normals4(uint64_t key, int64_t e) {
     // uniforms in (0, 1): 24 bits plus half a step
     const float u1 = ((float)(c[2 * j] >> 8) + 0.5f) * 5.9604645e-8f;
     const float u2 = ((float)(c[2 * j + 1] >> 8) + 0.5f) * 5.9604645e-8f;
-    const float rad = sqrtf(-2.0f * logf(u1));
-    float sn, cs;
-    sincosf(6.2831853f * u2, &sn, &cs);
-    z[2 * j] = rad * cs;
-    z[2 * j + 1] = rad * sn;
+    const float rad = __builtin_amdgcn_sqrtf(-1.3862944f * __builtin_amdgcn_logf(u1));
+    z[2 * j] = rad * __builtin_amdgcn_cosf(u2);
+    z[2 * j + 1] = rad * __builtin_amdgcn_sinf(u2);
   }
   return z;
 }

@@ -13,6 +13,7 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import noise as NZ
 from oracle import scao_ref as R
 
 pytestmark = pytest.mark.gpu
@@ -185,6 +186,32 @@ def test_noise_distribution_and_independence():
     torch.manual_seed(123)
     a2, _ = engine.moment_grads([(None, gd), (None, gd)], std)
     assert torch.equal(a, a2)
+
+
+# Box-Muller on the device uses the hardware log2, sqrt, sin and cos; the
+# draws must match the float64 restatement to this absolute tolerance.  A
+# mistake in the Philox stage (multiplier, key schedule, counter layout)
+# changes the draws completely, so it shows at any tolerance.
+NOISE_ATOL = 5e-5
+
+
+@pytest.mark.parametrize("n", [1, 7, 4096 + 3, 1 << 20])
+def test_noise_matches_philox_box_muller(n):
+    """Noise on a zero gradient is fp32(z * std): z against the oracle's
+    Philox4x32-10 + Box-Muller stream under the seed the call drew (torch's
+    generator, randint(0, 2^62) per parameter)."""
+    from scao_amd import engine
+    dev = _dev()
+    std = 0.25
+    g = torch.zeros(n, device=dev)
+    torch.manual_seed(77)
+    o, = engine.moment_grads([(None, g)], std)
+    torch.manual_seed(77)
+    seed = int(torch.randint(0, 2 ** 62, (1,), dtype=torch.int64, device=dev).item())
+    z = o.cpu().double().numpy() / np.float32(std)
+    want = NZ.normals(seed, n)
+    err = np.abs(z - want).max()
+    assert err <= NOISE_ATOL, (n, err)
 
 
 def test_filter_then_noise():
