@@ -285,8 +285,9 @@ def main():
         f_ms = filt[1] if filt else None
         sparse = {"sparsity": 0.7, "noise_std": 0.01, "steady_step_ms": sp_ms, "filter_ms": f_ms,
                   "filter_elements": nparams,
-                  # EMA pass 12 B, two radix passes 4 B each, output pass 12 B
-                  "filter_GBps_at_32B_per_elem": (32.0 * nparams / (f_ms / 1e3) / 1e9
+                  # EMA pass 12 B, two radix passes 4 B each (the step kernels
+                  # form the filtered, noisy gradient, so no output pass)
+                  "filter_GBps_at_20B_per_elem": (20.0 * nparams / (f_ms / 1e3) / 1e9
                                                   if f_ms else None)}
 
     # ---- roofline of the dominant kernel --------------------------------
