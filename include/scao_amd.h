@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define SCAO_ABI_VERSION 6
+#define SCAO_ABI_VERSION 7
 
 enum scao_status { SCAO_OK = 0, SCAO_ERR_INVALID = 1, SCAO_ERR_HIP = 2 };
 enum scao_dtype { SCAO_F32 = 0, SCAO_BF16 = 1, SCAO_F16 = 2 };
@@ -264,9 +264,17 @@ int scao_diag_ema(const scao_task* tasks, int ntasks, const scao_param_desc* par
  * values themselves (SCAO_PF_FMASK / SCAO_PF_FNOISE; the threshold is the
  * float at work + SCAO_FILTER_THR_WORD).
  * torch.quantile refuses more than 2^24 elements; this entry point has no such
- * limit.  Tasks are (desc index, chunk of SCAO_FLAT_CHUNK elements, 0, -1). */
+ * limit.  Tasks are (desc index, chunk of SCAO_FLAT_CHUNK elements, 0, -1).
+ * After its first call a desc's EMA pass assumes the threshold stays in the
+ * previous call's top-digit bin; when it does, one select resolves two
+ * digits, and with a candidate buffer (cand, cap >= ceil(numel /
+ * SCAO_FLAT_CHUNK) * (SCAO_FILTER_REGION + 4) floats) that receives the
+ * bin's values, the last refinement pass reads only those.  Tasks must list
+ * each desc's chunks in order for the buffer to be used.  Results do not
+ * depend on either. */
 #define SCAO_FILTER_BINS 2048
-#define SCAO_FILTER_WORK_WORDS (2 * SCAO_FILTER_BINS + 8)
+#define SCAO_FILTER_REGION (SCAO_FLAT_CHUNK / 2)
+#define SCAO_FILTER_WORK_WORDS (2 * SCAO_FILTER_BINS + 16)
 #define SCAO_FILTER_THR_WORD (2 * SCAO_FILTER_BINS + 7)
 #define SCAO_FILTER_MASK 1
 #define SCAO_FILTER_FIRST 2
@@ -284,6 +292,10 @@ typedef struct scao_filter_desc {
   float noise;              /* fp32(noise_std), 0 for none                       */
   int32_t dtype;
   int32_t flags;            /* SCAO_FILTER_MASK | SCAO_FILTER_FIRST              */
+  float* cand;              /* optional candidate buffer of cap floats (MASK),
+                               NULL for none; kept with work between calls, no
+                               initial contents needed                          */
+  int64_t cap;
 } scao_filter_desc;
 int scao_sparse_filter(const scao_task* tasks, int ntasks, const scao_filter_desc* descs,
                        int ndescs, void* stream);

@@ -21,7 +21,7 @@ import torch  # noqa: F401  -- loads torch's HIP runtime before ours
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("SCAO_AMD_LIB", os.path.join(HERE, "_lib", "libscao_amd.so"))
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 SLOT_WIDTH = 3
 FLAT_CHUNK = 4096
 PROJ_COLS = 256
@@ -82,14 +82,16 @@ PREP_DESC = np.dtype([
 FILTER_DESC = np.dtype([
     ("g", "u8"), ("ema", "u8"), ("out", "u8"), ("work", "u8"), ("seed", "u8"), ("numel", "i8"),
     ("decay", "f4"), ("omd", "f4"), ("q", "f4"), ("noise", "f4"), ("dtype", "i4"),
-    ("flags", "i4"),
+    ("flags", "i4"), ("cand", "u8"), ("cap", "i8"),
 ], align=True)
 FILTER_MASK, FILTER_FIRST = 1, 2
 
 LOOKAHEAD_DESC = np.dtype([
     ("p", "u8"), ("slow", "u8"), ("numel", "i8"), ("dtype", "i4"), ("pad0", "i4"),
 ], align=True)
-FILTER_WORK_WORDS = 2 * 2048 + 8
+FILTER_WORK_WORDS = 2 * 2048 + 16
+FILTER_COMPACT_WORD = 2 * 2048 + 11   # 1 when the refinement passes read the candidates
+FILTER_REGION = 2048                  # candidate slots per chunk (SCAO_FLAT_CHUNK / 2)
 
 STRUCTS = {0: (PARAM_DESC, [n for n in PARAM_DESC.names if n != "pad0"]),
            1: (LEAF_DESC, [n for n in LEAF_DESC.names if n != "pad0"]),

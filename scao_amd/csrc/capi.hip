@@ -95,7 +95,8 @@ extern "C" int scao_struct_layout(int which, int64_t* out, int cap) {
       PUT(offsetof(S, g)); PUT(offsetof(S, ema)); PUT(offsetof(S, out)); PUT(offsetof(S, work));
       PUT(offsetof(S, seed)); PUT(offsetof(S, numel)); PUT(offsetof(S, decay));
       PUT(offsetof(S, omd)); PUT(offsetof(S, q)); PUT(offsetof(S, noise));
-      PUT(offsetof(S, dtype)); PUT(offsetof(S, flags));
+      PUT(offsetof(S, dtype)); PUT(offsetof(S, flags)); PUT(offsetof(S, cand));
+      PUT(offsetof(S, cap));
       break;
     }
     case 7: {

@@ -568,6 +568,27 @@ def _filter_tasks(numels: tuple, dev) -> Tensor:
     return t
 
 
+# The candidate buffer (half a float per element, plus four counts per
+# chunk) holds the keys of the top-digit bin (a quarter octave) the previous
+# threshold fell in; with it the last refinement pass of a steady filter
+# reads about a tenth of the EMA.  False saves the memory and runs that pass
+# over the EMA; results are the same either way.
+FILTER_CANDIDATES = True
+
+
+def _filter_scratch(f, numel: int, dev) -> None:
+    """The filter's device scratch on ``dev``: ``work`` (selection state,
+    zero before the first call) and ``cand`` (candidate keys, or None)."""
+    if getattr(f, "work", None) is None or f.work.device != dev:
+        f.work = torch.zeros(L.FILTER_WORK_WORDS, dtype=torch.int32, device=dev)
+        f.cand = None
+    cap = _flat_chunks(numel) * (L.FILTER_REGION + 4) if FILTER_CANDIDATES else 0
+    if cap == 0:
+        f.cand = None
+    elif getattr(f, "cand", None) is None or f.cand.numel() != cap:
+        f.cand = torch.empty(cap, dtype=torch.float32, device=dev)
+
+
 def moment_grads(entries, noise_std: float = 0.0) -> list:
     """The gradient the moments see, for [(filter or None, grad)], in one
     batched launch sequence (reference scao/optimizer.py:533-545): the sparse
@@ -583,7 +604,7 @@ def moment_grads(entries, noise_std: float = 0.0) -> list:
     n = len(keep)
     outs = []
     cols = {k: [] for k in ("g", "ema", "out", "work", "seed", "numel", "decay", "omd", "q",
-                            "dtype", "flags")}
+                            "dtype", "flags", "cand", "cap")}
     noisy = noise_std > 0.0
     seeds = (torch.randint(0, 2 ** 62, (n,), dtype=torch.int64, device=dev) if noisy else None)
     for i, (f, g) in enumerate(keep):
@@ -596,8 +617,7 @@ def moment_grads(entries, noise_std: float = 0.0) -> list:
             if f.mag_ema is None:
                 f.mag_ema = torch.empty(g.shape, dtype=torch.float32, device=dev)
                 flags |= L.FILTER_FIRST
-            if getattr(f, "work", None) is None or f.work.device != dev:
-                f.work = torch.zeros(L.FILTER_WORK_WORDS, dtype=torch.int32, device=dev)
+            _filter_scratch(f, g.numel(), dev)
             ema, work = f.mag_ema.data_ptr(), f.work.data_ptr()
             decay, omd, q = f.ema, 1.0 - f.ema, f.sparsity
         cols["g"].append(g.data_ptr())
@@ -611,6 +631,9 @@ def moment_grads(entries, noise_std: float = 0.0) -> list:
         cols["q"].append(q)
         cols["dtype"].append(L.DTYPE_CODE[g.dtype])
         cols["flags"].append(flags)
+        cand = f.cand if f is not None else None
+        cols["cand"].append(cand.data_ptr() if cand is not None else 0)
+        cols["cap"].append(cand.numel() if cand is not None else 0)
     descs = np.zeros(n, dtype=L.FILTER_DESC)
     for k, v in cols.items():
         descs[k] = np.asarray(v, dtype=descs.dtype.fields[k][0])
@@ -679,8 +702,7 @@ def moment_sources(entries, noise_std: float = 0.0) -> list:
             if f.mag_ema is None:
                 f.mag_ema = torch.empty(g.shape, dtype=torch.float32, device=dev)
                 flags |= L.FILTER_FIRST
-            if getattr(f, "work", None) is None or f.work.device != dev:
-                f.work = torch.zeros(L.FILTER_WORK_WORDS, dtype=torch.int32, device=dev)
+            _filter_scratch(f, g.numel(), dev)
             e = descs[j]
             e["g"], e["ema"], e["out"] = g.data_ptr(), f.mag_ema.data_ptr(), 0
             e["work"] = f.work.data_ptr()
@@ -688,6 +710,8 @@ def moment_sources(entries, noise_std: float = 0.0) -> list:
             e["decay"], e["omd"], e["q"] = f.ema, 1.0 - f.ema, f.sparsity
             e["dtype"] = L.DTYPE_CODE[g.dtype]
             e["flags"] = flags
+            if f.cand is not None:
+                e["cand"], e["cap"] = f.cand.data_ptr(), f.cand.numel()
         tasks = _filter_tasks(tuple(int(g.numel()) for _, _, g in launch), dev)
         dd = L.upload(descs, dev)
         _call("scao_sparse_filter", tasks.data_ptr(), tasks.numel() // L.TASK.itemsize,

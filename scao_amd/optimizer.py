@@ -57,7 +57,8 @@ class _SparseGradFilter:
 
     def __init__(self, sparsity: float = 0.7, ema: float = 0.99):
         self.sparsity, self.ema, self.mag_ema = sparsity, ema, None
-        self.work = None          # device scratch of the batched kernel
+        self.work = None          # device scratch of the batched kernel: selection
+        self.cand = None          # state, and the candidate keys of one bin
 
     def prepare(self, grad: Tensor) -> None:
         """Host-side update before the batched launch (dynamic sparsity)."""

@@ -112,6 +112,55 @@ def test_filter_batched_launch_matches_single():
             assert _same(f.mag_ema, rf.mag_ema) and _same(o, r), (t, tuple(x.shape))
 
 
+def _compact(f) -> int:
+    """1 when the filter's last call histogrammed the candidate keys instead
+    of the whole EMA in its refinement passes."""
+    from scao_amd import _lib as L
+    return int(f.work[L.FILTER_COMPACT_WORD].item())
+
+
+@pytest.mark.parametrize("case", ["steady", "jump", "crowded", "q_change", "no_buffer",
+                                  "long_segments"])
+def test_filter_candidate_passes(case, monkeypatch):
+    """The refinement passes read the candidates of the previous call's bin
+    only when the threshold stays in that bin and every chunk's region held
+    all of its keys of that bin ("crowded": over half of each chunk is in
+    it); either way the EMA, threshold and mask match the oracle bit for
+    bit."""
+    from scao_amd import engine
+    from scao_amd.optimizer import _SparseGradFilter
+    dev = _dev()
+    # 300_007 elements give one chunk per block; 2**24 give segments of several
+    # chunks whose candidates are streamed as one array
+    n, calls = (1 << 24, 3) if case == "long_segments" else (300_007, 5)
+    kind = "ulps" if case == "crowded" else "normal"
+    grads = _grads(n, calls, 41, kind)
+    qs = [0.7] * calls
+    if case == "jump":
+        grads[3] = grads[3] * 64.0          # the EMA moves up by more than a bin
+    if case == "q_change":
+        qs[2] = 0.2
+    if case == "no_buffer":
+        monkeypatch.setattr(engine, "FILTER_CANDIDATES", False)
+    ref, gpu = R.RefSparseFilter(0.7), _SparseGradFilter(0.7)
+    modes = []
+    for t, g in enumerate(grads):
+        print(f"filter candidates case={case} call={t}", flush=True)
+        ref.sparsity = gpu.sparsity = qs[t]
+        r = ref(g.clone())
+        o = gpu(g.to(dev))
+        torch.cuda.synchronize()
+        modes.append(_compact(gpu))
+        from scao_amd import _lib as L
+        assert int(gpu.work[L.FILTER_COMPACT_WORD + 1].item()) == 3   # all digits selected
+        assert _same(gpu.mag_ema, ref.mag_ema), (t, "mag_ema")
+        assert _same(o, r), (t, "filtered gradient")
+    assert modes[0] == 0                     # nothing predicted on the first call
+    want = {"steady": [0, 1, 1, 1, 1], "jump": [0, 1, 1, 0, 1], "crowded": [0] * calls,
+            "q_change": [0, 1, 0, 0, 1], "no_buffer": [0] * calls, "long_segments": [0, 1, 1]}
+    assert modes == want[case], modes
+
+
 def _aten_quantile(e: np.ndarray, q: float) -> np.float32:
     n = e.size
     ranks = np.float32(np.float32(q) * np.float32(n - 1))
