@@ -117,7 +117,8 @@ __device__ __forceinline__ void flush(const uint32_t* h, uint32_t* g, int n) {
 // once per segment.  The candidates of a segment of L chunks go to its
 // L * RG slots from the first chunk's on, a quarter for each wave: wave w
 // appends its keys (wave-level prefix sums, no block barrier) to sub-stream
-// w and leaves their count in the first chunk's count word w.  The last
+// w, through a buffer in LDS so that they are stored in whole 2 KB blocks,
+// and leaves their count in the first chunk's count word w.  The last
 // refinement pass sees the same segments and streams each sub-stream.
 
 // One past the last task of the segment that starts at task t: the desc's
@@ -175,6 +176,7 @@ __global__ __launch_bounds__(256) void k_filter_ema(const scao_task* __restrict_
   __shared__ uint32_t h[1][NB];
   __shared__ uint32_t nan_s;
   __shared__ unsigned long long below_s;
+  __shared__ __attribute__((aligned(16))) float stage[4][1536];
   const int tb = blockIdx.x * per;
   const int te = ntasks - tb < per ? ntasks : tb + per;
   const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
@@ -202,6 +204,11 @@ __global__ __launch_bounds__(256) void k_filter_ema(const scao_task* __restrict_
     float* slots = D.cand + (int64_t)tk0.a * RG + (int64_t)w * sub;
     const bool vec = ((uintptr_t)D.ema & 15) == 0 && al_dt(D.g, D.dtype);
     uint32_t run = 0;      // this wave's candidates of the segment so far
+    // keys wait in the wave's LDS buffer and go out in whole, aligned blocks
+    // of 512 (2 KB): a partly written line evicted before the rest of it
+    // arrives costs a read-modify-write in HBM
+    uint32_t pend = 0, written = 0;
+    float* st = &stage[w][0];
     uint32_t nbelow = 0;   // this thread's keys below bin pred
     for (int c = t; c < se; ++c) {
       const scao_task tk = tasks[c];
@@ -246,17 +253,34 @@ __global__ __launch_bounds__(256) void k_filter_ema(const scao_task* __restrict_
       if (nans) atomicAdd(&nan_s, nans);
       if (gather) {
         uint32_t total;
-        uint32_t at = run + wave_offset(__popc(cmask), &total);
+        uint32_t at = pend + wave_offset(__popc(cmask), &total);   // < 512 + 1024
 #pragma unroll
         for (int grp = 0; grp < 4; ++grp)
 #pragma unroll
           for (int k = 0; k < 4; ++k)
-            if (cmask & (1u << (4 * grp + k))) {
-              if (at < sub) slots[at] = e[grp][k];
-              ++at;
-            }
+            if (cmask & (1u << (4 * grp + k))) st[at++] = e[grp][k];
+        pend += total;
         run += total;
+        __syncwarp();
+        while (pend >= 512u) {
+          if (written + 512u <= sub) {
+            const v4f a0 = *(const v4f*)&st[4 * l];
+            const v4f a1 = *(const v4f*)&st[256 + 4 * l];
+            *(v4f*)&slots[written + 4 * l] = a0;
+            *(v4f*)&slots[written + 256 + 4 * l] = a1;
+          }
+          __syncwarp();
+          for (uint32_t i = l; i + 512u < pend; i += 64) st[i] = st[i + 512];
+          __syncwarp();
+          written += 512u;
+          pend -= 512u;
+        }
       }
+    }
+    if (gather) {
+      for (uint32_t i = l; i < pend; i += 64)
+        if (written + i < sub) slots[written + i] = st[i];
+      __syncwarp();
     }
     if (gather && l == 0) {
       *cand_count(D, tk0.a, w) = run;
