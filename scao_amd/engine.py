@@ -243,10 +243,9 @@ def _build_structure(items: list[PItem]):
                 if not (mw and nw):
                     mw = nw = 0
                 wide = var | 4 | (8 if k >= PIPE_MIN_RANK else 0)
-                for i0 in range(0, mw, L.APPLY_WIDE_ROWS):
-                    for j0 in range(0, nw, L.APPLY_WIDE_COLS):
-                        tasks[f"apply{wide}"].append((li, i0, j0, slot))
-                        slot += 1
+                for i0, j0 in _wide_tiles(mw, nw, k):
+                    tasks[f"apply{wide}"].append((li, i0, j0, slot))
+                    slot += 1
                 for i0 in range(0, m, T):
                     for j0 in range(nw, n, T):
                         tasks[f"apply{var}"].append((li, i0, j0, slot))
@@ -270,6 +269,34 @@ def _build_structure(items: list[PItem]):
 
 XCDS = 8   # MI355X: 8 accelerator dies, workgroup i is dispatched to die i % 8
 PIPE_MIN_RANK = 128   # wide apply tiles of blocks with k >= this use the pipelined kernel
+L2_OPERANDS = 2 << 20   # bytes of W / U_r rows a die's L2 (4 MB) keeps beside the streams
+
+
+def _wide_tiles(mw: int, nw: int, k: int) -> list:
+    """(i0, j0) of a leaf's wide apply tiles in the order their blocks run.
+
+    A tile reads the W rows of its row band (16 x k) and the U_r rows of its
+    column strip (256 x k) from L2.  While a leaf's whole W and U_r fit in
+    L2_OPERANDS the tiles go row by row (a block's run of APPLY_GROUP tiles
+    crosses the strips of one band, which streams best).  Beyond that (k=256
+    at 4096 x 4096: 4 MB each) row-major order makes a die's resident blocks
+    cycle through every strip's U_r, and the misses refetch it from HBM.
+    Then the tiles go in super-tiles of R bands x S strips, strip by strip,
+    with R and S sized so that one super-tile's operands take L2_OPERANDS:
+    a block's run stays in one strip and the die shares a few strips."""
+    rows, cols = L.APPLY_WIDE_ROWS, L.APPLY_WIDE_COLS
+    if (mw + nw) * k * 4 <= L2_OPERANDS:
+        return [(i0, j0) for i0 in range(0, mw, rows) for j0 in range(0, nw, cols)]
+    half = L2_OPERANDS // 2
+    s = max(1, half // (cols * k * 4))
+    r = max(L.APPLY_GROUP, half // (rows * k * 4) // L.APPLY_GROUP * L.APPLY_GROUP)
+    out = []
+    for ib in range(0, mw, r * rows):
+        for jb in range(0, nw, s * cols):
+            for j0 in range(jb, min(nw, jb + s * cols), cols):
+                for i0 in range(ib, min(mw, ib + r * rows), rows):
+                    out.append((i0, j0))
+    return out
 
 
 def _xcd_interleave(tasks: list, group: int = 1) -> list:

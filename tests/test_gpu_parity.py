@@ -160,6 +160,13 @@ CASES = {
                                   use_int8_ema=True, k_min=128, k_max=128, warmup_steps=2,
                                   blend_steps=3, precond_freq=4, min_precond_updates=1, tau=1.0,
                                   lars_coeff=1e-3), 7),
+    # k = 256 on a 2048 x 1024 block: W and U_r (3 MB) exceed what the wide
+    # tiles' row-major order keeps in L2, so they run in super-tiles
+    "pipe_k256_supertile": ({"big": (2048, 1024), "ln": (1024,)},
+                            dict(lr=1e-3, weight_decay=0.01, max_precond_dim=2048, rho=0.999,
+                                 use_int8_ema=True, k_min=256, k_max=256, warmup_steps=2,
+                                 blend_steps=2, precond_freq=4, min_precond_updates=1, tau=1.0,
+                                 lars_coeff=1e-3), 6),
 }
 
 
@@ -206,7 +213,12 @@ def test_step_from_shared_state(case):
             assert st_g.get("scao_phase_started") == st_r.get("scao_phase_started")
             tol = 1e-4 if not refreshed else 2e-3
             assert r < tol, f"step {t} param {k}: update rel err {r:.3e} (refresh={refreshed})"
-        assert gopt._global_norm_ema == pytest.approx(ref._global_norm_ema, rel=1e-6)
+        # the oracle's norms are the reference's fp32 CPU reductions; over n
+        # squares their rounding walks like sqrt(n / lanes) * eps (1.5e-5 at
+        # 2M elements), the kernels add fp32 partials in fp64
+        big = max(int(torch.tensor(s).prod()) for s in shapes.values())
+        gn_tol = 1e-6 if big <= 1 << 18 else 5e-5
+        assert gopt._global_norm_ema == pytest.approx(ref._global_norm_ema, rel=gn_tol)
         # preconditioner state after refresh: codes within 1 LSB, scales 1e-6
         for (kr, pr), (kg, pg) in zip(ref.state.items(), gopt.state.items()):
             _cmp_precond(pr["preconditioner"], pg["preconditioner"], t, refreshed)

@@ -200,6 +200,32 @@ def test_pipelined_apply_tasks():
             assert queue_of[int(t["idx"])] == b % E.XCDS
 
 
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 256), (1024, 4096, 256), (2048, 2048, 128),
+                                   (2048, 2048, 64), (4096, 2048, 256)])
+def test_wide_tile_order(m, n, k):
+    """Every wide tile once; leaves whose W and U_r exceed L2_OPERANDS go in
+    super-tiles whose operands fit it, each run of APPLY_GROUP tiles inside
+    one column strip; smaller leaves keep row-major order."""
+    rows, cols = L.APPLY_WIDE_ROWS, L.APPLY_WIDE_COLS
+    order = E._wide_tiles(m, n, k)
+    assert sorted(order) == [(i, j) for i in range(0, m, rows) for j in range(0, n, cols)]
+    if (m + n) * k * 4 <= E.L2_OPERANDS:
+        assert order == [(i, j) for i in range(0, m, rows) for j in range(0, n, cols)]
+        return
+    for b in range(0, len(order), L.APPLY_GROUP):
+        assert len({j for _, j in order[b:b + L.APPLY_GROUP]}) == 1
+    # a window of tiles the size of one super-tile touches at most
+    # L2_OPERANDS of W rows and U_r rows
+    half = E.L2_OPERANDS // 2
+    s = max(1, half // (cols * k * 4))
+    r = max(L.APPLY_GROUP, half // (rows * k * 4) // L.APPLY_GROUP * L.APPLY_GROUP)
+    for b in range(0, len(order), r * s):
+        win = order[b:b + r * s]
+        strips = {j for _, j in win}
+        bands = {i for i, _ in win}
+        assert len(strips) * cols * k * 4 + len(bands) * rows * k * 4 <= E.L2_OPERANDS
+
+
 @pytest.mark.parametrize("shape,fp32", [((2048, 8192), True), ((328, 264), True),
                                         ((320, 448), True), ((100, 37), True),
                                         ((300, 520), True), ((512, 512), False)])
