@@ -630,6 +630,60 @@ __device__ __forceinline__ void apply_wide(const scao_leaf_desc& L, const scao_p
 // tile: four wave partials through LDS, summed in a fixed order.
 constexpr int CP = SCAO_APPLY_WIDE_COLS + 4;   // LDS pitch of a correction row
 
+// One MFMA wave's 16x64 share of corr = W U_r^T: rows of W from wrow, its 64
+// U_r rows from urow (lane layout as in apply_wide).  With NC > 0 (k = 16 NC)
+// the reduction is fully unrolled with PD chunks of operands in flight, so
+// every wait is for one chunk's loads (a loop's back edge makes the compiler
+// wait for all of them); NC = 0 takes any multiple of 16 with one chunk of
+// lookahead.
+template <int NC>
+__device__ __forceinline__ void pipe_corr(const float* __restrict__ wrow,
+                                          const float* __restrict__ urow, int k, v4f (&acc)[4]) {
+  if constexpr (NC > 0) {
+    constexpr int PD = 4;
+    v4f A[PD], B[PD][4];
+#pragma unroll
+    for (int d = 0; d < PD && d < NC; ++d) {
+      A[d] = gld4(wrow + 16 * d);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) B[d][t] = gld4(urow + (int64_t)t * (16 * NC) + 16 * d);
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = c % PD;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = mfma16(A[d][s4], B[d][t][s4], acc[t]);
+      if (c + PD < NC) {
+        A[d] = gld4(wrow + 16 * (c + PD));
+#pragma unroll
+        for (int t = 0; t < 4; ++t) B[d][t] = gld4(urow + (int64_t)t * (16 * NC) + 16 * (c + PD));
+      }
+    }
+  } else {
+    v4f a = gld4(wrow), b[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) b[t] = gld4(urow + (int64_t)t * k);
+    for (int c = 0; c < k; c += 16) {
+      const bool more = c + 16 < k;
+      v4f an = a, bn[4] = {b[0], b[1], b[2], b[3]};
+      if (more) {
+        an = gld4(wrow + c + 16);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) bn[t] = gld4(urow + (int64_t)t * k + c + 16);
+      }
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = mfma16(a[s4], b[t][s4], acc[t]);
+      a = an;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) b[t] = bn[t];
+    }
+  }
+}
+
 template <bool GF32, bool LARS>
 __global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict__ tasks, int ntasks,
                                                     const scao_leaf_desc* __restrict__ leaves,
@@ -656,25 +710,12 @@ __global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict_
       for (int t = 0; t < 4; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
       const float* __restrict__ wrow = L.W + (int64_t)(tk.a + l % 16) * k + 4 * kk;
       const float* __restrict__ urow = L.Ur + (int64_t)jl * k + 4 * kk;
-      v4f a = gld4(wrow), b[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) b[t] = gld4(urow + (int64_t)t * k);
-      for (int c = 0; c < k; c += 16) {
-        const bool more = c + 16 < k;
-        v4f an = a, bn[4] = {b[0], b[1], b[2], b[3]};
-        if (more) {
-          an = gld4(wrow + c + 16);
-#pragma unroll
-          for (int t = 0; t < 4; ++t) bn[t] = gld4(urow + (int64_t)t * k + c + 16);
-        }
-#pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4)
-#pragma unroll
-          for (int t = 0; t < 4; ++t) acc[t] = mfma16(a[s4], b[t][s4], acc[t]);
-        a = an;
-#pragma unroll
-        for (int t = 0; t < 4; ++t) b[t] = bn[t];
-      }
+      if (k == 256)
+        pipe_corr<16>(wrow, urow, k, acc);
+      else if (k == 128)
+        pipe_corr<8>(wrow, urow, k, acc);
+      else
+        pipe_corr<0>(wrow, urow, k, acc);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
         *(v4f*)&cbuf[s & 1][4 * kk + r][64 * w + 4 * (l % 16)] =
