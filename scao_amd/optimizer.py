@@ -417,17 +417,16 @@ class SCAO(Optimizer):
         order; there is no side stream to wait for."""
 
     def sync_preconditioner(self, process_group=None) -> None:
-        """reference :686-710 (broadcast from rank 0).  Single-GPU build:
-        a no-op with a warning when torch.distributed is not initialised."""
+        """reference :686-710: rank 0's moments, step counters and
+        preconditioner state on every rank (``distributed.broadcast_state``);
+        a warning and nothing else when torch.distributed is not initialised."""
         import torch.distributed as dist
         if not dist.is_available() or not dist.is_initialized():
             warnings.warn("sync_preconditioner() called but distributed is not initialised.",
                           RuntimeWarning, stacklevel=2)
             return
-        if dist.get_world_size(group=process_group) == 1:
-            return
-        raise NotImplementedError("scao_amd is a single-GPU build: multi-rank preconditioner "
-                                  "broadcast is not provided")
+        from .distributed import broadcast_state
+        broadcast_state(self, process_group)
 
     def add_callback(self, callback) -> None:
         self._callbacks.append(callback)
