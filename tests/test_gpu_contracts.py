@@ -404,6 +404,68 @@ def test_distributed_noops(dev):
     sync_preconditioners(opt)
 
 
+def _same_precond(a, b) -> None:
+    """Portable preconditioner states equal, int8 scales up to fp32 rounding."""
+    assert a.keys() == b.keys()
+    for name, v in a.items():
+        w = b[name]
+        if isinstance(v, torch.Tensor):
+            assert torch.equal(v, w), name
+        elif isinstance(v, list):
+            assert len(v) == len(w)
+            for x, y in zip(v, w):
+                _same_precond(x, y)
+        elif name.endswith("_scale"):
+            assert w == torch.tensor(v, dtype=torch.float32).item(), name
+        else:
+            assert v == w, name
+
+
+def test_sync_preconditioner_single_rank_gloo(dev):
+    """The broadcast and the averaging over a one-rank gloo group: device
+    state goes through host buckets and comes back unchanged (the int8 scales
+    rounded to fp32, as the reference's broadcast leaves them), and the next
+    step runs on the rebuilt step structure."""
+    import socket
+
+    import torch.distributed as dist
+    from scao_amd.distributed import sync_preconditioners
+    with socket.socket() as sk:
+        sk.bind(("127.0.0.1", 0))
+        port = sk.getsockname()[1]
+    dist.init_process_group("gloo", init_method=f"tcp://127.0.0.1:{port}", rank=0,
+                            world_size=1)
+    try:
+        torch.manual_seed(0)
+        m = nn.Sequential(nn.Linear(48, 40), nn.Linear(40, 96)).to(dev)
+        opt = SCAO(m.parameters(), lr=1e-3, warmup_steps=1, blend_steps=1, precond_freq=2,
+                   min_precond_updates=1, use_int8_ema=True, max_precond_dim=64,
+                   sparsity=0.0, noise_std_init=0.0, lookahead_k=0)
+        x = torch.randn(8, 48, device=dev)
+        for _ in range(4):
+            opt.zero_grad()
+            m(x).sum().backward()
+            opt.step()
+        before = copy.deepcopy(opt.state_dict())
+        opt.sync_preconditioner()
+        sync_preconditioners(opt)         # one rank: a no-op
+        after = opt.state_dict()
+        for i, st in before["state"].items():
+            for key in ("exp_avg", "exp_avg_sq", "exp_avg_diff", "prev_grad"):
+                assert torch.equal(st[key], after["state"][i][key]), key
+            assert st["step"] == after["state"][i]["step"]
+        assert before["_scao_precond"].keys() == after["_scao_precond"].keys()
+        for i, pc in before["_scao_precond"].items():
+            _same_precond(pc, after["_scao_precond"][i])
+        opt.zero_grad()
+        m(x).sum().backward()
+        opt.step()
+        torch.cuda.synchronize()
+        assert all(torch.isfinite(p).all() for p in m.parameters())
+    finally:
+        dist.destroy_process_group()
+
+
 def test_resume_from_saved_checkpoint_is_bit_identical(dev):
     """Save after 6 steps (int8 EMA, refreshes, Phase 2), reload through the
     safe loader (scao_amd.checkpoint.load) into a fresh optimizer and
