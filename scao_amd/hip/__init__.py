@@ -97,7 +97,3 @@ def int8_ema_update(ema_q: Tensor, ema_scale: float, new_val: Tensor, rho: float
     L.call("scao_int8_ema_update", q.data_ptr(), float(ema_scale), v.data_ptr(), float(rho), n,
            scale.data_ptr(), scratch.data_ptr(), L.stream_ptr(q.device))
     return q.view(ema_q.shape), float(scale.item())
-
-
-def library_path() -> str:
-    return L.LIB_PATH
