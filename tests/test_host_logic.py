@@ -365,3 +365,15 @@ def test_wandb_logger_without_wandb():
     if importlib.util.find_spec("wandb") is not None:
         pytest.skip("wandb is installed")
     WandbLogger(log_every=1)({"step": 1, "a": 1.0})
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py --gpus N > 1 exits with a message, before touching a GPU."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=300)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr and r.stdout == ""
