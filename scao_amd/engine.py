@@ -31,6 +31,7 @@ read of all ranks.
 from __future__ import annotations
 
 import math
+import weakref
 from dataclasses import dataclass, field
 from typing import NamedTuple
 
@@ -95,6 +96,9 @@ class Workspace:
         self.device = device
         self.runtime = torch.tensor([1.0, 0.0], dtype=torch.float64, device=device)
         self._bufs: dict[str, Tensor] = {}
+        # moment tensors already checked (contiguous fp32 on the device), per
+        # parameter state: weak references, so a replaced tensor is checked again
+        self.checked: dict = {}
         self.struct_key = None
         self.cheap_key = None
         self.leaf_epoch = -1
@@ -326,7 +330,13 @@ def _xcd_interleave(tasks: list, group: int = 1) -> list:
 
 
 def _cols(t: Tensor) -> int:
-    return t.shape[1] if t.ndim == 2 else to_2d(t)[0].shape[1]
+    """Columns of to_2d(t) (1-D: n; N-D: prod(shape[1:])), without a view."""
+    shape = t.shape
+    if len(shape) == 1:
+        return shape[0]
+    if len(shape) == 2 or shape[0] == 0:
+        return shape[1] if len(shape) == 2 else to_2d(t)[0].shape[1]
+    return math.prod(shape[1:])
 
 
 def _leaf_vec(it: PItem, leaf, r0: int, c0: int) -> bool:
@@ -373,56 +383,76 @@ def _leaf_table(leaves, items: list[PItem], ws: Workspace):
 _MOMENTS = ("exp_avg", "exp_avg_sq", "exp_avg_diff", "prev_grad")
 
 
+def _group_scalars(g: dict, t: int, phase2: bool, scao_step: int, lars: bool,
+                   gsnr: float | None) -> tuple:
+    """The descriptor fields every parameter of a group shares at one step:
+    (lr .. gsnr), (adam_sqrt_bc2, adam_alpha) and the group's flags."""
+    lr = g["lr"]
+    beta1, beta2 = g["betas"]
+    beta3 = g["beta3"]
+    wd = g["weight_decay"]
+    flags = L.PF_NORM
+    decay = 1.0
+    if wd != 0.0:
+        flags |= L.PF_DECAY
+        decay = 1.0 - lr * wd
+    bc1 = bc2 = bc3 = blend = omb = tau = lv = wdv = gs = sq = alpha = 0.0
+    if not phase2:
+        sq, alpha = math.sqrt(1.0 - beta2 ** t), -(lr / (1.0 - beta1 ** t))
+    else:
+        bc1, bc2, bc3 = 1.0 - beta1 ** t, 1.0 - beta2 ** t, 1.0 - beta3 ** t
+        bsteps = g.get("blend_steps", 50)
+        blend = min(1.0, scao_step / bsteps) if bsteps > 0 else 1.0
+        omb = 1.0 - blend
+        if g["tau"] is not None:
+            flags |= L.PF_CLIP
+            tau = g["tau"]
+        if lars:
+            flags |= L.PF_LARS
+            lv, wdv = g["lars_coeff"], wd
+        if gsnr is not None:
+            flags |= L.PF_GSNR
+            gs = gsnr
+    head = (lr, decay, beta1, 1.0 - beta1, beta2, 1.0 - beta2, beta3, 1.0 - beta3, bc1, bc2,
+            bc3, blend, omb, g["eps"], tau, lv, wdv, gs)
+    return head, (sq, alpha), flags
+
+
 def _param_table(items: list[PItem], ranges, ws: Workspace, gsnr: float | None):
-    """The per-step parameter descriptors, built column by column.
+    """The per-step parameter descriptors, one record per parameter in the
+    field order of scao_param_desc.  Scalars shared by a group at one step
+    are computed once.
 
     Scalars are Python floats rounded to fp32 by the record's f4 fields (the
     same round-to-nearest ATen applies to a scalar operand of an fp32 op)."""
-    n = len(items)
-    tab = np.zeros(n, dtype=L.PARAM_DESC)
-    cols = {k: [] for k in ("p", "g", "graw", "exp_avg", "exp_avg_sq", "exp_avg_diff",
-                            "prev_grad", "upd", "diag_ema", "numel", "cols", "lr", "decay",
-                            "beta1", "omb1", "beta2", "omb2", "beta3", "omb3", "bc1", "bc2",
-                            "bc3", "blend", "omblend", "eps", "tau", "lars", "wd", "gsnr",
-                            "diag_bias", "adam_sqrt_bc2", "adam_alpha", "dtype", "flags",
-                            "fema", "fthr", "fseed", "fnoise")}
     upd_base = ws.buf("upd", 4).data_ptr() if ws.upd_total else 0
+    f32 = torch.float32
+    shared: dict = {}
+    rows = []
     for i, it in enumerate(items):
-        g, st = it.group, it.st
-        lr = g["lr"]
-        beta1, beta2 = g["betas"]
-        beta3 = g["beta3"]
-        wd = g["weight_decay"]
-        t = it.step
+        st = it.st
+        dev = it.p.device
+        moms = [st[key] for key in _MOMENTS]
+        seen = ws.checked.get(id(st))
+        if seen is None or any(r() is not m for r, m in zip(seen, moms)):
+            for key, m in zip(_MOMENTS, moms):
+                if m.dtype != f32 or not m.is_contiguous() or m.device != dev:
+                    raise ValueError(f"state[{key!r}] must be a contiguous float32 tensor on "
+                                     f"{dev}; got {m.dtype} on {m.device}")
+            ws.checked[id(st)] = tuple(weakref.ref(m) for m in moms)
+        lars = it.phase2 and it.lars
+        skey = (id(it.group), it.step, it.phase2, it.scao_step if it.phase2 else 0, lars)
+        sc = shared.get(skey)
+        if sc is None:
+            sc = shared[skey] = _group_scalars(it.group, it.step, it.phase2, it.scao_step,
+                                               lars, gsnr)
+        head, tail, flags = sc
         graw = it.graw.data_ptr()
-        cols["p"].append(it.p.data_ptr())
-        cols["graw"].append(graw)
-        cols["g"].append(it.gmom.data_ptr() if it.gmom is not None else graw)
-        for key in _MOMENTS:
-            m = st[key]
-            if m.dtype != torch.float32 or not m.is_contiguous() or m.device != it.p.device:
-                raise ValueError(f"state[{key!r}] must be a contiguous float32 tensor on "
-                                 f"{it.p.device}; got {m.dtype} on {m.device}")
-            cols[key].append(m.data_ptr())
-        cols["numel"].append(it.p.numel())
-        cols["cols"].append(_cols(it.p))
-        cols["lr"].append(lr)
-        cols["beta1"].append(beta1)
-        cols["omb1"].append(1.0 - beta1)
-        cols["beta2"].append(beta2)
-        cols["omb2"].append(1.0 - beta2)
-        cols["beta3"].append(beta3)
-        cols["omb3"].append(1.0 - beta3)
-        cols["eps"].append(g["eps"])
-        flags = L.PF_NORM
-        if wd != 0.0:
-            flags |= L.PF_DECAY
-        cols["decay"].append(1.0 - lr * wd if wd != 0.0 else 1.0)
         if it.gmom is not None:
             flags |= L.PF_GF32
-        ms = it.msrc
         fema = fthr = fseed = 0
         fnoise = 0.0
+        ms = it.msrc
         if ms is not None:
             flags |= L.PF_GF32
             if ms.ema is not None:
@@ -431,61 +461,22 @@ def _param_table(items: list[PItem], ranges, ws: Workspace, gsnr: float | None):
             if ms.noise > 0.0:
                 flags |= L.PF_FNOISE
                 fseed, fnoise = ms.seed, ms.noise
-        cols["fema"].append(fema)
-        cols["fthr"].append(fthr)
-        cols["fseed"].append(fseed)
-        cols["fnoise"].append(fnoise)
-        bc1 = 1.0 - beta1 ** t
-        bc2 = 1.0 - beta2 ** t
         upd = diag = 0
-        tau = lars = wdv = gs = dbias = 0.0
-        blend = omb = bc3 = sq = alpha = 0.0
-        if not it.phase2:
-            sq, alpha = math.sqrt(bc2), -(lr / bc1)
-        else:
-            bc3 = 1.0 - beta3 ** t
-            bsteps = g.get("blend_steps", 50)
-            blend = min(1.0, it.scao_step / bsteps) if bsteps > 0 else 1.0
-            omb = 1.0 - blend
-            if g["tau"] is not None:
-                flags |= L.PF_CLIP
-                tau = g["tau"]
-            if it.lars:
-                flags |= L.PF_LARS
-                lars, wdv = g["lars_coeff"], wd
-                upd = upd_base + 4 * ws.upd_offsets[i]
-            if gsnr is not None:
-                flags |= L.PF_GSNR
-                gs = gsnr
-            if it.diag:
-                flags |= L.PF_DIAG
-                diag = it.pre.diag_ema.data_ptr()
-                dbias = getattr(it.pre, "_diag_bias_factor", 1.0)
+        dbias = 0.0
+        if lars:
+            upd = upd_base + 4 * ws.upd_offsets[i]
+        if it.phase2 and it.diag:
+            flags |= L.PF_DIAG
+            diag = it.pre.diag_ema.data_ptr()
+            dbias = getattr(it.pre, "_diag_bias_factor", 1.0)
         if it.aligned:
             flags |= L.PF_ALIGNED
-        cols["bc1"].append(bc1 if it.phase2 else 0.0)
-        cols["bc2"].append(bc2 if it.phase2 else 0.0)
-        cols["bc3"].append(bc3)
-        cols["blend"].append(blend)
-        cols["omblend"].append(omb)
-        cols["tau"].append(tau)
-        cols["lars"].append(lars)
-        cols["wd"].append(wdv)
-        cols["gsnr"].append(gs)
-        cols["diag_bias"].append(dbias)
-        cols["adam_sqrt_bc2"].append(sq)
-        cols["adam_alpha"].append(alpha)
-        cols["upd"].append(upd)
-        cols["diag_ema"].append(diag)
-        cols["dtype"].append(L.DTYPE_CODE[it.p.dtype])
-        cols["flags"].append(flags)
-    for k, v in cols.items():
-        tab[k] = np.asarray(v, dtype=tab.dtype.fields[k][0])
-    r = np.asarray(ranges, dtype=np.int32).reshape(n, 4)
-    tab["pre_begin"], tab["pre_end"] = r[:, 0], r[:, 1]
-    tab["post_begin"], tab["post_end"] = r[:, 2], r[:, 3]
-    tab["norm_index"] = np.arange(n, dtype=np.int32)
-    return tab
+        rows.append((it.p.data_ptr(), it.gmom.data_ptr() if it.gmom is not None else graw, graw,
+                     moms[0].data_ptr(), moms[1].data_ptr(), moms[2].data_ptr(),
+                     moms[3].data_ptr(), upd, diag, fema, fthr, fseed, it.p.numel(),
+                     _cols(it.p)) + head + (dbias,) + tail +
+                    (L.DTYPE_CODE[it.p.dtype], flags) + tuple(ranges[i]) + (i, fnoise))
+    return np.array(rows, dtype=L.PARAM_DESC)
 
 
 def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
@@ -530,11 +521,12 @@ def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
         ws.leaf_epoch = -1
     if ws.upd_total:
         ws.buf("upd", ws.upd_total * 4)
-    if ws.leaf_epoch != leaf_epoch() or ws.leaf_dev is None or _grads_moved(items, ws):
+    # the block table holds no gradient pointer: a gradient that moves keeps
+    # it valid (its alignment is part of the structure key)
+    if ws.leaf_epoch != leaf_epoch() or ws.leaf_dev is None:
         tab = _leaf_table(ws.leaves, items, ws)
         ws.leaf_dev = L.upload(tab, dev) if len(tab) else None
         ws.leaf_epoch = leaf_epoch()
-        ws.grad_ptrs = [it.graw.data_ptr() for it in items]
     ptab = _param_table(items, ws.slot_ranges, ws, gsnr)
     params = L.upload(ptab, dev)
     slots = ws.buf("slots", max(ws.nslots, 1) * 8 * L.SLOT_WIDTH)
@@ -757,12 +749,6 @@ def moment_sources(entries, noise_std: float = 0.0) -> list:
 def sparse_filter(entries) -> list:
     """The sparse filter alone for [(filter, grad)] (no noise)."""
     return moment_grads(entries, 0.0)
-
-
-def _grads_moved(items, ws) -> bool:
-    ptrs = getattr(ws, "grad_ptrs", None)
-    return ptrs is None or len(ptrs) != len(items) or any(
-        p != it.graw.data_ptr() for p, it in zip(ptrs, items))
 
 
 # --------------------------------------------------------------------------

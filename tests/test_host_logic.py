@@ -176,6 +176,46 @@ def test_engine_slots_cover_each_once():
         assert n == (E._flat_chunks(it.p.numel()) if it.phase2 and it.lars else 0)
 
 
+def test_param_table_fields_and_state_checks():
+    """Per-step descriptors: group scalars at known steps, per-parameter
+    pointers and flags, and the moment checks (again after a tensor is
+    replaced)."""
+    from scao_amd.engine import PItem
+    g = {"lr": 0.1, "betas": (0.9, 0.999), "beta3": 0.99, "weight_decay": 0.01, "eps": 1e-8,
+         "tau": 1.0, "lars_coeff": 1e-3, "blend_steps": 50}
+    ws = E.Workspace(torch.device("cpu"))
+    items = []
+    for i, (shape, phase2) in enumerate([((8, 12), True), ((16,), False), ((4, 3, 5), True)]):
+        p = torch.zeros(shape)
+        st = {k: torch.zeros(shape) for k in E._MOMENTS}
+        items.append(PItem(p=p, graw=torch.zeros(shape), gmom=None, st=st, group=g, pre=None,
+                           phase2=phase2, step=1 if not phase2 else 30, scao_step=25,
+                           lars=True))
+    ws.upd_offsets, ws.upd_total = {0: 0, 2: 96}, 156
+    ranges = [(0, 1, 1, 2), (2, 2, 2, 2), (2, 3, 3, 4)]
+    tab = E._param_table(items, ranges, ws, None)
+    f4 = np.float32
+    assert tab["bc1"][0] == f4(1 - 0.9 ** 30) and tab["bc1"][1] == 0.0
+    assert tab["blend"][0] == f4(0.5) and tab["omblend"][2] == f4(0.5)
+    assert tab["decay"][1] == f4(1 - 0.1 * 0.01)
+    assert tab["adam_alpha"][1] == f4(-0.1 / (1 - 0.9)) and tab["adam_sqrt_bc2"][0] == 0.0
+    assert list(tab["cols"]) == [12, 16, 15] and list(tab["numel"]) == [96, 16, 60]
+    for i in (0, 2):
+        assert tab["flags"][i] & L.PF_LARS and tab["flags"][i] & L.PF_CLIP
+    assert not tab["flags"][1] & (L.PF_LARS | L.PF_CLIP)
+    upd = ws.buf("upd", 4).data_ptr()
+    assert list(tab["upd"]) == [upd, 0, upd + 4 * 96]
+    assert tab["exp_avg_sq"][2] == items[2].st["exp_avg_sq"].data_ptr()
+    assert [tuple(r) for r in tab[["pre_begin", "pre_end", "post_begin", "post_end"]]] == ranges
+    assert list(tab["norm_index"]) == [0, 1, 2]
+    items[1].st["exp_avg"] = torch.zeros(16, dtype=torch.bfloat16)   # replaced after a check
+    with pytest.raises(ValueError, match="contiguous float32"):
+        E._param_table(items, ranges, ws, None)
+    items[1].st["exp_avg"] = torch.zeros(32)[::2]
+    with pytest.raises(ValueError, match="contiguous float32"):
+        E._param_table(items, ranges, ws, None)
+
+
 def test_pipelined_apply_tasks():
     """Wide tasks of blocks with k >= PIPE_MIN_RANK carry variant bit 8 and are
     ordered in runs of APPLY_GROUP tasks of one die's queue."""
