@@ -50,11 +50,24 @@ def _align4(n: int) -> int:
 
 
 def _aligned16(*ptrs) -> bool:
-    return all(p % 16 == 0 for p in ptrs if p)
+    x = 0
+    for p in ptrs:
+        x |= p
+    return x & 15 == 0
+
+
+def _item_ptrs(it: "PItem") -> tuple:
+    """PItem.ptrs: the device addresses a step reads, once per step."""
+    st, ms = it.st, it.msrc
+    return (it.p.data_ptr(), it.graw.data_ptr(),
+            it.gmom.data_ptr() if it.gmom is not None else 0,
+            ms.ema.data_ptr() if ms is not None and ms.ema is not None else 0,
+            st["exp_avg"].data_ptr(), st["exp_avg_sq"].data_ptr(),
+            st["exp_avg_diff"].data_ptr(), st["prev_grad"].data_ptr())
 
 
 def require_hip(t: Tensor, what: str) -> None:
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         raise RuntimeError(
             f"scao_amd runs on ROCm devices only: {what} is on '{t.device}'. "
             "Move the model to the GPU (there is no CPU path).")
@@ -64,7 +77,7 @@ def require_hip(t: Tensor, what: str) -> None:
 # per-step parameter record
 # --------------------------------------------------------------------------
 
-@dataclass
+@dataclass(slots=True)
 class PItem:
     """One parameter taking part in a step (host-side bookkeeping)."""
     p: Tensor
@@ -82,6 +95,9 @@ class PItem:
     fp32: bool = True            # param and gradient are float32
     aligned: bool = True         # every pointer of the param is 16-byte aligned
     msrc: "MomentSource | None" = None   # filter/noise formed inside the step kernels
+    # device addresses, read once per step: p, graw, gmom, filter EMA (0 when
+    # absent) and the four moments in _MOMENTS order
+    ptrs: tuple = ()
 
     @property
     def mgrad(self) -> bool:
@@ -418,23 +434,52 @@ def _group_scalars(g: dict, t: int, phase2: bool, scao_step: int, lars: bool,
     return head, (sq, alpha), flags
 
 
-def _param_table(items: list[PItem], ranges, ws: Workspace, gsnr: float | None):
-    """The per-step parameter descriptors, one record per parameter in the
-    field order of scao_param_desc.  Scalars shared by a group at one step
-    are computed once.
+def _desc_blocks():
+    """Byte ranges of scao_param_desc's runs of same-typed fields: 64-bit
+    addresses and sizes (p .. cols), lr (double), the fp32 scalars (decay ..
+    adam_alpha), the int32 fields (dtype .. norm_index) and fnoise."""
+    f = L.PARAM_DESC.fields
+    names = list(L.PARAM_DESC.names)
 
-    Scalars are Python floats rounded to fp32 by the record's f4 fields (the
+    def run(first, last, size):
+        i, j = names.index(first), names.index(last)
+        for a, b in zip(names[i:j], names[i + 1:j + 1]):
+            assert f[b][1] == f[a][1] + size, (a, b)
+        return f[first][1], f[last][1] + size, j - i + 1
+
+    blocks = {"u8": run("p", "cols", 8), "f8": run("lr", "lr", 8),
+              "f4": run("decay", "adam_alpha", 4), "i4": run("dtype", "norm_index", 4),
+              "fnoise": run("fnoise", "fnoise", 4)}
+    assert names[-1] == "fnoise" and blocks["fnoise"][1] <= L.PARAM_DESC.itemsize
+    assert names.index("decay") == names.index("lr") + 1
+    assert names.index("dtype") == names.index("adam_alpha") + 1
+    return blocks
+
+
+_BLOCKS = _desc_blocks()
+_DBIAS = list(L.PARAM_DESC.names).index("diag_bias") - list(L.PARAM_DESC.names).index("decay")
+
+
+def _param_table(items: list[PItem], ranges, ws: Workspace, gsnr: float | None):
+    """The per-step parameter descriptors (scao_param_desc records).  The
+    device addresses come from ``it.ptrs``; scalars shared by a group at one
+    step are computed once and written to all its rows together.
+
+    Scalars are Python floats rounded to fp32 by the float32 columns (the
     same round-to-nearest ATen applies to a scalar operand of an fp32 op)."""
+    n = len(items)
     upd_base = ws.buf("upd", 4).data_ptr() if ws.upd_total else 0
     f32 = torch.float32
     shared: dict = {}
-    rows = []
+    u8rows, i4rows, fnoise, dbias = [], [], [], []
     for i, it in enumerate(items):
         st = it.st
         dev = it.p.device
-        moms = [st[key] for key in _MOMENTS]
+        pp, graw, gmom, fema, m0, m1, m2, m3 = it.ptrs
         seen = ws.checked.get(id(st))
-        if seen is None or any(r() is not m for r, m in zip(seen, moms)):
+        if (seen is None or seen[0]() is not st["exp_avg"] or seen[1]() is not st["exp_avg_sq"]
+                or seen[2]() is not st["exp_avg_diff"] or seen[3]() is not st["prev_grad"]):
+            moms = [st[key] for key in _MOMENTS]
             for key, m in zip(_MOMENTS, moms):
                 if m.dtype != f32 or not m.is_contiguous() or m.device != dev:
                     raise ValueError(f"state[{key!r}] must be a contiguous float32 tensor on "
@@ -444,39 +489,53 @@ def _param_table(items: list[PItem], ranges, ws: Workspace, gsnr: float | None):
         skey = (id(it.group), it.step, it.phase2, it.scao_step if it.phase2 else 0, lars)
         sc = shared.get(skey)
         if sc is None:
-            sc = shared[skey] = _group_scalars(it.group, it.step, it.phase2, it.scao_step,
-                                               lars, gsnr)
-        head, tail, flags = sc
-        graw = it.graw.data_ptr()
-        if it.gmom is not None:
+            sc = shared[skey] = list(_group_scalars(it.group, it.step, it.phase2, it.scao_step,
+                                                    lars, gsnr)) + [[]]
+        sc[3].append(i)
+        flags = sc[2]
+        if gmom:
             flags |= L.PF_GF32
-        fema = fthr = fseed = 0
-        fnoise = 0.0
+        fthr = fseed = 0
+        fn = 0.0
         ms = it.msrc
         if ms is not None:
             flags |= L.PF_GF32
             if ms.ema is not None:
                 flags |= L.PF_FMASK
-                fema, fthr = ms.ema.data_ptr(), ms.thr
+                fthr = ms.thr
             if ms.noise > 0.0:
                 flags |= L.PF_FNOISE
-                fseed, fnoise = ms.seed, ms.noise
+                fseed, fn = ms.seed, ms.noise
         upd = diag = 0
-        dbias = 0.0
         if lars:
             upd = upd_base + 4 * ws.upd_offsets[i]
         if it.phase2 and it.diag:
             flags |= L.PF_DIAG
             diag = it.pre.diag_ema.data_ptr()
-            dbias = getattr(it.pre, "_diag_bias_factor", 1.0)
+            dbias.append((i, getattr(it.pre, "_diag_bias_factor", 1.0)))
         if it.aligned:
             flags |= L.PF_ALIGNED
-        rows.append((it.p.data_ptr(), it.gmom.data_ptr() if it.gmom is not None else graw, graw,
-                     moms[0].data_ptr(), moms[1].data_ptr(), moms[2].data_ptr(),
-                     moms[3].data_ptr(), upd, diag, fema, fthr, fseed, it.p.numel(),
-                     _cols(it.p)) + head + (dbias,) + tail +
-                    (L.DTYPE_CODE[it.p.dtype], flags) + tuple(ranges[i]) + (i, fnoise))
-    return np.array(rows, dtype=L.PARAM_DESC)
+        u8rows.append((pp, gmom or graw, graw, m0, m1, m2, m3, upd, diag, fema, fthr, fseed,
+                       it.p.numel(), _cols(it.p)))
+        r = ranges[i]
+        i4rows.append((L.DTYPE_CODE[it.p.dtype], flags, r[0], r[1], r[2], r[3], i))
+        fnoise.append(fn)
+    raw = np.zeros((n, L.PARAM_DESC.itemsize), dtype=np.uint8)
+
+    def cols(block, dt):
+        a, b, _ = _BLOCKS[block]
+        return raw[:, a:b].view(dt)
+
+    cols("u8", np.uint64)[:] = np.array(u8rows, dtype=np.uint64)
+    cols("i4", np.int32)[:] = np.array(i4rows, dtype=np.int32)
+    cols("fnoise", np.float32)[:, 0] = np.array(fnoise, dtype=np.float32)
+    f8, f4 = cols("f8", np.float64), cols("f4", np.float32)
+    for head, tail, _, rows in shared.values():
+        f8[rows, 0] = head[0]
+        f4[rows] = np.array(head[1:] + (0.0,) + tail, dtype=np.float32)
+    for i, v in dbias:
+        f4[i, _DBIAS] = v
+    return raw.view(L.PARAM_DESC).reshape(n)
 
 
 def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
@@ -485,15 +544,11 @@ def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
     if not items:
         return
     dev = ws.device
+    f32 = torch.float32
     for it in items:
-        st = it.st
-        it.fp32 = it.p.dtype == torch.float32 and it.graw.dtype == torch.float32
-        it.aligned = _aligned16(it.p.data_ptr(), it.graw.data_ptr(),
-                                it.gmom.data_ptr() if it.gmom is not None else 0,
-                                it.msrc.ema.data_ptr() if it.msrc is not None and
-                                it.msrc.ema is not None else 0,
-                                st["exp_avg"].data_ptr(), st["exp_avg_sq"].data_ptr(),
-                                st["exp_avg_diff"].data_ptr(), st["prev_grad"].data_ptr())
+        it.fp32 = it.p.dtype == f32 and it.graw.dtype == f32
+        it.ptrs = _item_ptrs(it)
+        it.aligned = _aligned16(*it.ptrs)
     # the full structure key (with every block's rank) is only rebuilt when
     # the cheap one or the global factor epoch says something may have changed
     ckey = (tuple((id(it.p), it.phase2, it.diag, it.lars, it.mgrad, it.p.numel(),

@@ -355,16 +355,18 @@ class SCAO(Optimizer):
 
     def _plan_param(self, group: dict, p: Tensor, refresh: list, filtered: list) -> PItem:
         """Host half of reference _step_group (:521-605) for one parameter."""
-        if p.grad.is_sparse:
+        grad = p.grad
+        if grad.is_sparse:
             raise RuntimeError("SCAO does not support sparse gradients.")
         if not p.is_contiguous():
             raise RuntimeError("scao_amd.SCAO needs contiguous parameters")
-        self._init_state(p, group)
         st = self.state[p]
+        if not st:
+            self._init_state(p, group)
         st["step"] += 1
         t = st["step"]
         pid = id(p)
-        graw = p.grad if p.grad.is_contiguous() else p.grad.contiguous()
+        graw = grad if grad.is_contiguous() else grad.contiguous()
         need_gnorm = self._lazy_precond or self._adaptive_rank
         gnorm = float(graw.float().norm()) if need_gnorm else 0.0
         gmom = None   # set by _filter_and_noise when filtered or noised
@@ -383,7 +385,7 @@ class SCAO(Optimizer):
             (pre.precond_step < group["min_precond_updates"])
         if in_warmup:
             if t % group["precond_freq"] == 0:
-                refresh.append((pre, p.grad))
+                refresh.append((pre, grad))
             it = PItem(p=p, graw=graw, gmom=gmom, st=st, group=group, pre=pre,
                        phase2=False, step=t)
             if filt is not None:
@@ -402,7 +404,7 @@ class SCAO(Optimizer):
         else:
             should = t % group["precond_freq"] == 0
         if should:
-            refresh.append((pre, p.grad))
+            refresh.append((pre, grad))
         diag = not (pre.use_block_diagonal or pre.use_kronecker)
         it = PItem(p=p, graw=graw, gmom=gmom, st=st, group=group, pre=pre, phase2=True,
                    step=t, scao_step=st["scao_step"], lars=group["lars_coeff"] > 0,

@@ -191,6 +191,8 @@ def test_param_table_fields_and_state_checks():
         items.append(PItem(p=p, graw=torch.zeros(shape), gmom=None, st=st, group=g, pre=None,
                            phase2=phase2, step=1 if not phase2 else 30, scao_step=25,
                            lars=True))
+    for it in items:
+        it.ptrs = E._item_ptrs(it)
     ws.upd_offsets, ws.upd_total = {0: 0, 2: 96}, 156
     ranges = [(0, 1, 1, 2), (2, 2, 2, 2), (2, 3, 3, 4)]
     tab = E._param_table(items, ranges, ws, None)
