@@ -618,16 +618,22 @@ __device__ __forceinline__ void apply_wide(const scao_leaf_desc& L, const scao_p
 
 // Wide tiles through a two-role pipeline, for ranks where the back-projection
 // no longer hides under the streaming of one-tile blocks (k >= 128; at k = 64
-// both kernels measure the same).  A block of eight waves
-// takes SCAO_APPLY_GROUP consecutive wide tasks.  Waves 4..7 compute
-// corr = W U_r^T of tile s into one of two LDS buffers while waves 0..3
-// stream tile s-1 (loads, Adan tail, stores) and then issue tile s+1's loads;
-// one block barrier per tile hands a buffer over.  Each role waits only on
-// its own memory operations (the vector-memory counter is in order within a
-// wave, so an operand load queued behind the streaming loads would wait for
-// them too).  Both roles use apply_wide's lane <-> element mapping, so a
-// streaming wave reads exactly the 16x64 slice its partner wrote.  u^2 per
-// tile: four wave partials through LDS, summed in a fixed order.
+// both kernels measure the same).  A block of eight waves takes
+// SCAO_APPLY_GROUP consecutive wide tasks.  Waves 0..3 stream tile s (loads,
+// Adan tail, stores) between block barriers s and s+1, then issue tile s+1's
+// loads.  Waves 4..7 compute corr = W U_r^T into four LDS tile buffers, two
+// tiles at a time: tiles 2q and 2q+1 of one column strip share their U_r
+// rows, so one pass over them serves both (the operand loads from L2, not
+// the MFMAs, bound this role).  Pair q's reduction is split in two halves,
+// computed between barriers 2q-2, 2q-1 and 2q, so each barrier interval holds
+// one tile's worth of MFMA work; pair 0 is done before barrier 0.  Tiles of
+// different blocks or strips are computed one per half instead.  Each role
+// waits only on its own memory operations (the vector-memory counter is in
+// order within a wave, so an operand load queued behind the streaming loads
+// would wait for them too).  Both roles use apply_wide's lane <-> element
+// mapping, so a streaming wave reads exactly the 16x64 slice its partner
+// wrote.  u^2 per tile: four wave partials through LDS, summed in a fixed
+// order.
 constexpr int CP = SCAO_APPLY_WIDE_COLS + 4;   // LDS pitch of a correction row
 
 // One MFMA wave's 16x64 share of corr = W U_r^T: rows of W from wrow, its 64
@@ -684,13 +690,49 @@ __device__ __forceinline__ void pipe_corr(const float* __restrict__ wrow,
   }
 }
 
+// The same for two row tiles of one strip (W rows from wa and wb, one U_r
+// row set), over NH chunks of a reduction of length K: every U_r load feeds
+// both tiles.  Used for k = 256 (k = 128 measures no gain from it, and the
+// other instantiations would raise the kernel's register count past the 128
+// that keep two blocks on a CU).
+template <int K, int NH, int PD>
+__device__ __forceinline__ void pipe_corr2(const float* __restrict__ wa,
+                                           const float* __restrict__ wb,
+                                           const float* __restrict__ urow, v4f (&acc)[2][4]) {
+  v4f A[PD][2], B[PD][4];
+#pragma unroll
+  for (int d = 0; d < PD && d < NH; ++d) {
+    A[d][0] = gld4(wa + 16 * d);
+    A[d][1] = gld4(wb + 16 * d);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) B[d][t] = gld4(urow + (int64_t)t * K + 16 * d);
+  }
+#pragma unroll
+  for (int c = 0; c < NH; ++c) {
+    const int d = c % PD;
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        acc[0][t] = mfma16(A[d][0][s4], B[d][t][s4], acc[0][t]);
+        acc[1][t] = mfma16(A[d][1][s4], B[d][t][s4], acc[1][t]);
+      }
+    if (c + PD < NH) {
+      A[d][0] = gld4(wa + 16 * (c + PD));
+      A[d][1] = gld4(wb + 16 * (c + PD));
+#pragma unroll
+      for (int t = 0; t < 4; ++t) B[d][t] = gld4(urow + (int64_t)t * K + 16 * (c + PD));
+    }
+  }
+}
+
 template <bool GF32, bool LARS>
 __global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict__ tasks, int ntasks,
                                                     const scao_leaf_desc* __restrict__ leaves,
                                                     const scao_param_desc* __restrict__ params,
                                                     const scao_param_stat* __restrict__ stat,
                                                     double* slots) {
-  __shared__ __attribute__((aligned(16))) float cbuf[2][16][CP];
+  __shared__ __attribute__((aligned(16))) float cbuf[4][16][CP];
   __shared__ double part[2][4];
   const int wv = threadIdx.x / 64, l = threadIdx.x % 64;
   const int w = wv & 3;
@@ -699,30 +741,71 @@ __global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict_
   const int nt = ntasks - t0 < SCAO_APPLY_GROUP ? ntasks - t0 : SCAO_APPLY_GROUP;
 
   if (wv >= 4) {
-    // ---- MFMA role ----
-    for (int s = 0; s < nt; ++s) {
-      const scao_task tk = tasks[t0 + s];
-      const scao_leaf_desc& L = leaves[tk.idx];
-      const int k = L.k;
-      const int jl = tk.b + 64 * w + 4 * (l % 16);
-      v4f acc[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
-      const float* __restrict__ wrow = L.W + (int64_t)(tk.a + l % 16) * k + 4 * kk;
-      const float* __restrict__ urow = L.Ur + (int64_t)jl * k + 4 * kk;
-      if (k == 256)
-        pipe_corr<16>(wrow, urow, k, acc);
-      else if (k == 128)
-        pipe_corr<8>(wrow, urow, k, acc);
-      else
-        pipe_corr<0>(wrow, urow, k, acc);
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        *(v4f*)&cbuf[s & 1][4 * kk + r][64 * w + 4 * (l % 16)] =
-            v4f{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
-      __syncthreads();   // corr(s) ready
+    // ---- MFMA role: nt + 1 barriers, as the streaming role ----
+    if (nt <= 0) {
+      __syncthreads();
+      return;
     }
-    __syncthreads();     // the streaming role's last barrier
+    v4f acc[2][4];
+    // half h of pair q (tiles 2q and 2q+1; the second may be absent)
+    auto work = [&](int q, int h) {
+      const scao_task ta = tasks[t0 + 2 * q];
+      const bool hasb = 2 * q + 1 < nt;
+      const scao_task tb = hasb ? tasks[t0 + 2 * q + 1] : ta;
+      if (h == 0) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int t = 0; t < 4; ++t) acc[i][t] = v4f{0.f, 0.f, 0.f, 0.f};
+      }
+      if (hasb && tb.idx == ta.idx && tb.b == ta.b && leaves[ta.idx].k == 256) {
+        // chunks [8h, 8h + 8) of both tiles
+        const scao_leaf_desc& L = leaves[ta.idx];
+        const int jl = ta.b + 64 * w + 4 * (l % 16);
+        const int c0 = 4 * kk + 128 * h;
+        pipe_corr2<256, 8, 4>(L.W + (int64_t)(ta.a + l % 16) * 256 + c0,
+                              L.W + (int64_t)(tb.a + l % 16) * 256 + c0,
+                              L.Ur + (int64_t)jl * 256 + c0, acc);
+      } else if (h == 0 || hasb) {
+        const scao_task tk = h ? tb : ta;
+        const scao_leaf_desc& L = leaves[tk.idx];
+        const int k = L.k;
+        const int jl = tk.b + 64 * w + 4 * (l % 16);
+        const float* __restrict__ wrow = L.W + (int64_t)(tk.a + l % 16) * k + 4 * kk;
+        const float* __restrict__ urow = L.Ur + (int64_t)jl * k + 4 * kk;
+        if (k == 256)
+          pipe_corr<16>(wrow, urow, k, acc[h]);
+        else if (k == 128)
+          pipe_corr<8>(wrow, urow, k, acc[h]);
+        else
+          pipe_corr<0>(wrow, urow, k, acc[h]);
+      }
+    };
+    auto put = [&](int q) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const int s = 2 * q + i;
+        if (s < nt) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            *(v4f*)&cbuf[s & 3][4 * kk + r][64 * w + 4 * (l % 16)] =
+                v4f{acc[i][0][r], acc[i][1][r], acc[i][2][r], acc[i][3][r]};
+        }
+      }
+    };
+    work(0, 0);
+    work(0, 1);
+    put(0);
+    __syncthreads();                       // barrier 0: tiles 0 and 1 ready
+    const int np = (nt + 1) / 2;
+    for (int q = 1; q < np; ++q) {
+      work(q, 0);
+      __syncthreads();                     // barrier 2q-1
+      work(q, 1);
+      put(q);                              // buffers of tiles 2q-4, 2q-3: consumed
+      __syncthreads();                     // barrier 2q: tiles 2q, 2q+1 ready
+    }
+    for (int b = 2 * np - 1; b < nt + 1; ++b) __syncthreads();
     return;
   }
 
@@ -761,7 +844,7 @@ __global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict_
   };
   if (nt > 0) prefetch(0);
   for (int s = 0; s < nt; ++s) {
-    __syncthreads();     // corr(s) in cbuf[s & 1]; tile s-1's partials in part
+    __syncthreads();     // corr(s) in cbuf[s & 3]; tile s-1's partials in part
     if (s > 0 && w == 0 && l == 0) put_slot(s - 1);
     const scao_task tk = tasks[t0 + s];
     const scao_leaf_desc& L = leaves[tk.idx];
@@ -770,7 +853,7 @@ __global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict_
     float u2 = 0.f;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const v4f corr = *(const v4f*)&cbuf[s & 1][4 * kk + r][64 * w + 4 * (l % 16)];
+      const v4f corr = *(const v4f*)&cbuf[s & 3][4 * kk + r][64 * w + 4 * (l % 16)];
       if (GF32 && fused_mgrad(P)) gm[r] = finish_mgrad(P, e[r], gr[r], gm[r], 15);
       v4f out;
       adan4<GF32, LARS>(P, S, SCAO_F32, gr[r], gm[r], corr, mm[r], vv[r], dd[r], pp[r], par[r],

@@ -167,6 +167,14 @@ CASES = {
                                  use_int8_ema=True, k_min=256, k_max=256, warmup_steps=2,
                                  blend_steps=2, precond_freq=4, min_precond_updates=1, tau=1.0,
                                  lars_coeff=1e-3), 6),
+    # k = 256 where a block's run of wide tiles is short (17 bands: runs of
+    # 8, 8, 1) or crosses strips (two strips, row-major): the back-projection
+    # pairs tiles of one strip and computes the others one at a time
+    "pipe_k256_ragged_runs": ({"a": (272, 256), "b": (256, 512), "ln": (256,)},
+                              dict(lr=1e-3, weight_decay=0.01, max_precond_dim=2048, rho=0.999,
+                                   use_int8_ema=True, k_min=256, k_max=256, warmup_steps=2,
+                                   blend_steps=2, precond_freq=4, min_precond_updates=1,
+                                   tau=1.0, lars_coeff=1e-3), 6),
 }
 
 
