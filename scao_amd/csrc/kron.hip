@@ -692,9 +692,8 @@ __device__ __forceinline__ void pipe_corr(const float* __restrict__ wrow,
 
 // The same for two row tiles of one strip (W rows from wa and wb, one U_r
 // row set), over NH chunks of a reduction of length K: every U_r load feeds
-// both tiles.  Used for k = 256 (k = 128 measures no gain from it, and the
-// other instantiations would raise the kernel's register count past the 128
-// that keep two blocks on a CU).
+// both tiles.  Instantiated for k = 256 only: a second instantiation raises
+// the kernel's register count past the 128 that keep two blocks on a CU.
 template <int K, int NH, int PD>
 __device__ __forceinline__ void pipe_corr2(const float* __restrict__ wa,
                                            const float* __restrict__ wb,
