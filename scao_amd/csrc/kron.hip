@@ -300,16 +300,94 @@ __device__ __forceinline__ void delta_tile(const scao_leaf_desc& L, float eps, i
 }
 
 // -------------------------------------------------------------- lift ---
-// W[i0:i0+64, d0:d0+64] = U_l Delta.
+// W[i0:i0+64, d0:d0+64] = U_l Delta.  Wave w computes rows i0+16w .. +15.
+// On whole tiles (k % 16 == 0, 16-byte aligned factors) lane column jj holds
+// W columns d0 + 4*jj + t of MFMA tile t, so one float4 of a Delta row feeds
+// all four tiles and each row of the result leaves as one float4; the
+// reduction runs with NH chunks of operands in flight (fully unrolled for
+// k = 16 NC, NC > 0; any multiple of 16 with one chunk of lookahead for
+// NC = 0).  Other tiles take the element-wise path.
+template <int NC>
+__device__ __forceinline__ void lift_chunks(const float* __restrict__ urow,
+                                            const float* __restrict__ drow, int k,
+                                            v4f (&acc)[4]) {
+  // urow: U_l row + 4*kk; drow: Delta row 4*kk, columns dl..dl+3
+  if constexpr (NC > 0) {
+    constexpr int PD = NC < 4 ? NC : 4;
+    v4f A[PD], B[PD][4];
+#pragma unroll
+    for (int d = 0; d < PD; ++d) {
+      A[d] = gld4(urow + 16 * d);
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) B[d][s4] = gld4(drow + (int64_t)(16 * d + s4) * (16 * NC));
+    }
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = c % PD;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = mfma16(A[d][s4], B[d][s4][t], acc[t]);
+      if (c + PD < NC) {
+        A[d] = gld4(urow + 16 * (c + PD));
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4)
+          B[d][s4] = gld4(drow + (int64_t)(16 * (c + PD) + s4) * (16 * NC));
+      }
+    }
+  } else {
+    v4f a = gld4(urow), b[4];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) b[s4] = gld4(drow + (int64_t)s4 * k);
+    for (int cb = 0; cb < k; cb += 16) {
+      const bool more = cb + 16 < k;
+      v4f an = a, bn[4] = {b[0], b[1], b[2], b[3]};
+      if (more) {
+        an = gld4(urow + cb + 16);
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) bn[s4] = gld4(drow + (int64_t)(cb + 16 + s4) * k);
+      }
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = mfma16(a[s4], b[s4][t], acc[t]);
+      a = an;
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) b[s4] = bn[s4];
+    }
+  }
+}
+
 __device__ __forceinline__ void lift_tile(const scao_leaf_desc& L, int i0, int d0) {
   const int w = threadIdx.x / 64, l = threadIdx.x % 64;
   const int m = L.m, k = L.k;
   const int kk = l / 16;
-  const int irow = i0 + 16 * w + (l % 16);
-  const bool kvec = (k % 4) == 0;
   v4f acc[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+  const bool whole = k % 16 == 0 && i0 + 64 <= m && d0 + 64 <= k &&
+                     (((uintptr_t)L.Ul | (uintptr_t)L.Delta | (uintptr_t)L.W) & 15) == 0;
+  if (whole) {
+    const int irow = i0 + 16 * w + (l % 16);
+    const int dl = d0 + 4 * (l % 16);
+    const float* __restrict__ urow = L.Ul + (int64_t)irow * k + 4 * kk;
+    const float* __restrict__ drow = L.Delta + (int64_t)(4 * kk) * k + dl;
+    if (k == 256)
+      lift_chunks<16>(urow, drow, k, acc);
+    else if (k == 128)
+      lift_chunks<8>(urow, drow, k, acc);
+    else if (k == 64)
+      lift_chunks<4>(urow, drow, k, acc);
+    else
+      lift_chunks<0>(urow, drow, k, acc);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      gst4(L.W + (int64_t)(i0 + 16 * w + 4 * kk + r) * k + dl,
+           v4f{acc[0][r], acc[1][r], acc[2][r], acc[3][r]});
+    return;
+  }
+  const int irow = i0 + 16 * w + (l % 16);
+  const bool kvec = (k % 4) == 0;
   for (int cb = 0; cb < k; cb += 16) {
     const int c = cb + 4 * kk;
     int cm = 0;
