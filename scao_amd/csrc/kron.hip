@@ -26,20 +26,25 @@ using namespace scao;
 namespace {
 
 // ----------------------------------------------------------- project ---
-// T[c0:c0+64, j0:j0+256] = U_l^T G over all m rows.  Wave w owns 64 columns.
+// T[c0:c0+CR, j0:j0+256] = U_l^T G over all m rows.  Wave w owns 64 columns.
 // Rows are consumed in chunks of PR=32: each chunk of G (32 x 256) and U_l
-// (32 x 64) is loaded into registers one chunk ahead (coalesced float4: one
-// wave reads one 1 KB row of G), written to LDS, and all four waves run 128
-// MFMAs on it.  Chunk-0 tasks also reduce ||g||^2 and ||p*decay||^2 from the
-// staged registers (every element of the strip passes through exactly one
-// thread).
+// (32 x CR) is loaded into registers one chunk ahead (coalesced float4: one
+// wave reads one 1 KB row of G), written to LDS, and all four waves run
+// 2*CR MFMAs on it.  CR = 64, or 128 for whole tiles of k % 128 == 0 blocks
+// (every G chunk staged then feeds twice the MFMAs, and each strip of G is
+// read by half as many blocks).  Chunk-0 tasks also reduce ||g||^2 and
+// ||p*decay||^2 from the staged registers (every element of the strip passes
+// through exactly one thread).
 constexpr int PR = 32;           // rows per chunk
 constexpr int GP = SCAO_PROJ_COLS + 4;  // LDS pitch of the G chunk
-constexpr int UP = 64 + 4;       // LDS pitch of the U_l chunk
 
-template <bool FAST, bool DO_P>
+template <bool FAST, bool DO_P, int CR = 64>
 __device__ __forceinline__ void project_tile(const scao_leaf_desc& L, const scao_param_desc& P,
                                              int j0, int c0, int slot, double* slots) {
+  static_assert(CR == 64 || (CR == 128 && FAST), "CR");
+  constexpr int UP = CR + 4;       // LDS pitch of the U_l chunk
+  constexpr int NQ = CR / 16;      // MFMA tiles down T
+  constexpr int NU = CR / 32;      // float4 of U_l per thread and chunk
   __shared__ __attribute__((aligned(16))) float Gs[PR][GP];
   __shared__ __attribute__((aligned(16))) float Us[PR][UP];
   __shared__ double red[16];
@@ -61,20 +66,20 @@ __device__ __forceinline__ void project_tile(const scao_leaf_desc& L, const scao
   if (!FAST)
     for (int t = 0; t < 4; ++t) gmask = (j0 + gc + t < n) ? gmask : (gmask & ~(1 << t));
   const bool gvec = gvec_leaf && gmask == 15;
-  const int uc = (tid % 16) * 4;         // c offset inside the 64-wide chunk
+  const int uc = (tid % (CR / 4)) * 4;   // c offset inside the CR-wide chunk
   int umask = 15;
   if (!FAST)
     for (int t = 0; t < 4; ++t) umask = (c0 + uc + t < k) ? umask : (umask & ~(1 << t));
   const bool uvec = kvec && umask == 15;
 
-  v4f acc[4][4];
+  v4f acc[NQ][4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
+  for (int q = 0; q < NQ; ++q)
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[q][t] = v4f{0.f, 0.f, 0.f, 0.f};
   double g2 = 0.0, p2 = 0.0;
 
-  v4f rg[8], ru[2], rp[8];
+  v4f rg[8], ru[NU], rp[8];
   auto load_chunk = [&](int i0) {
 #pragma unroll
     for (int h = 0; h < 8; ++h) {
@@ -90,8 +95,8 @@ __device__ __forceinline__ void project_tile(const scao_leaf_desc& L, const scao
       }
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int i = i0 + tid / 16 + 16 * h;
+    for (int h = 0; h < NU; ++h) {
+      const int i = i0 + tid / (CR / 4) + (1024 / CR) * h;
       if (FAST)
         ru[h] = gld4(L.Ul + (int64_t)i * k + c0 + uc);
       else
@@ -103,7 +108,7 @@ __device__ __forceinline__ void project_tile(const scao_leaf_desc& L, const scao
 #pragma unroll
     for (int h = 0; h < 8; ++h) *(v4f*)&Gs[tid / 64 + 4 * h][gc] = rg[h];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) *(v4f*)&Us[tid / 16 + 16 * h][uc] = ru[h];
+    for (int h = 0; h < NU; ++h) *(v4f*)&Us[tid / (CR / 4) + (1024 / CR) * h][uc] = ru[h];
     if (do_norms) {
       float a = 0.f, b = 0.f;
 #pragma unroll
@@ -130,11 +135,11 @@ __device__ __forceinline__ void project_tile(const scao_leaf_desc& L, const scao
 #pragma unroll
     for (int s = 0; s < PR / 4; ++s) {
       const v4f b = *(const v4f*)&Gs[4 * s + kk][64 * w + 4 * (l % 16)];
-      float a[4];
+      float a[NQ];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) a[q] = Us[4 * s + kk][16 * q + (l % 16)];
+      for (int q = 0; q < NQ; ++q) a[q] = Us[4 * s + kk][16 * q + (l % 16)];
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
+      for (int q = 0; q < NQ; ++q)
 #pragma unroll
         for (int t = 0; t < 4; ++t) acc[q][t] = mfma16(a[q], b[t], acc[q][t]);
     }
@@ -146,7 +151,7 @@ __device__ __forceinline__ void project_tile(const scao_leaf_desc& L, const scao
     for (int t = 0; t < 4; ++t) cmask = (jl + t < n) ? cmask : (cmask & ~(1 << t));
   const bool tvec = gvec_leaf && cmask == 15;
 #pragma unroll
-  for (int q = 0; q < 4; ++q)
+  for (int q = 0; q < NQ; ++q)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int c = c0 + 16 * q + 4 * kk + r;
@@ -977,14 +982,14 @@ __device__ __forceinline__ void apply_out_tile(const scao_leaf_desc& L, const fl
 }
 
 // ---------------------------------------------------------- kernels ---
-template <bool FAST, bool DO_P>
+template <bool FAST, bool DO_P, int CR = 64>
 __global__ __launch_bounds__(256) void k_project(const scao_task* __restrict__ tasks,
                                                  const scao_leaf_desc* __restrict__ leaves,
                                                  const scao_param_desc* __restrict__ params,
                                                  double* slots) {
   const scao_task tk = tasks[blockIdx.x];
   const scao_leaf_desc L = leaves[tk.idx];
-  project_tile<FAST, DO_P>(L, params[L.param], tk.a, tk.b, tk.slot, slots);
+  project_tile<FAST, DO_P, CR>(L, params[L.param], tk.a, tk.b, tk.slot, slots);
 }
 __global__ __launch_bounds__(256) void k_delta(const scao_task* __restrict__ tasks,
                                                const scao_leaf_desc* __restrict__ leaves,
@@ -1050,14 +1055,17 @@ extern "C" int scao_kron_project(const scao_task* tasks, int ntasks, const scao_
   SCAO_CHECK_ARG(ntasks >= 0, "scao_kron_project: ntasks < 0");
   if (ntasks == 0) return SCAO_OK;
   SCAO_CHECK_ARG(tasks && leaves && params && slots, "scao_kron_project: null pointer");
-  SCAO_CHECK_ARG(variant >= 0 && variant < 4, "scao_kron_project: bad variant %d", variant);
+  SCAO_CHECK_ARG(variant >= 0 && variant < 8 && (variant < 4 || (variant & 1)),
+                 "scao_kron_project: bad variant %d", variant);
   hipStream_t s = (hipStream_t)stream;
   dim3 g(ntasks), b(256);
   switch (variant) {
     case 0: hipLaunchKernelGGL((k_project<false, false>), g, b, 0, s, tasks, leaves, params, slots); break;
     case 1: hipLaunchKernelGGL((k_project<true, false>), g, b, 0, s, tasks, leaves, params, slots); break;
     case 2: hipLaunchKernelGGL((k_project<false, true>), g, b, 0, s, tasks, leaves, params, slots); break;
-    default: hipLaunchKernelGGL((k_project<true, true>), g, b, 0, s, tasks, leaves, params, slots); break;
+    case 3: hipLaunchKernelGGL((k_project<true, true>), g, b, 0, s, tasks, leaves, params, slots); break;
+    case 5: hipLaunchKernelGGL((k_project<true, false, 128>), g, b, 0, s, tasks, leaves, params, slots); break;
+    default: hipLaunchKernelGGL((k_project<true, true, 128>), g, b, 0, s, tasks, leaves, params, slots); break;
   }
   SCAO_LAUNCH_CHECK("scao_kron_project");
   return SCAO_OK;

@@ -197,7 +197,7 @@ def _build_structure(items: list[PItem]):
     Every reduction slot is written by exactly one task; each parameter's
     pre-finalize slots and post-finalize slots are contiguous ranges."""
     tasks = {k: [] for k in ["adam", "delta", "lift", "dred", "dapply", "lars"] +
-             [f"proj{v}" for v in range(4)] + [f"apply{v}" for v in range(16)]}
+             [f"proj{v}" for v in range(8)] + [f"apply{v}" for v in range(16)]}
     ranges = []
     leaves = []          # (leaf, r0, c0, param index)
     slot = 0
@@ -229,11 +229,13 @@ def _build_structure(items: list[PItem]):
                 k = leaf.U_l.shape[1]
                 vec = _leaf_vec(it, leaf, r0, c0l)
                 for j0 in range(0, n, L.PROJ_COLS):
-                    for c0 in range(0, k, 64):
-                        fast = (vec and it.fp32 and j0 + L.PROJ_COLS <= n and c0 + 64 <= k
-                                and m % 32 == 0)
+                    whole = vec and it.fp32 and j0 + L.PROJ_COLS <= n and m % 32 == 0
+                    # 128 rows of T per task where k allows (variant bit 4)
+                    cr = 128 if TALL_PROJECT and whole and k % 128 == 0 else 64
+                    for c0 in range(0, k, cr):
+                        fast = whole and c0 + 64 <= k
                         do_p = c0 == 0 and it.lars
-                        var = (1 if fast else 0) | (2 if do_p else 0)
+                        var = (1 if fast else 0) | (2 if do_p else 0) | (4 if cr == 128 else 0)
                         if c0 == 0:
                             tasks[f"proj{var}"].append((li, j0, c0, slot))
                             slot += 1
@@ -289,6 +291,7 @@ def _build_structure(items: list[PItem]):
 
 XCDS = 8   # MI355X: 8 accelerator dies, workgroup i is dispatched to die i % 8
 PIPE_MIN_RANK = 128   # wide apply tiles of blocks with k >= this use the pipelined kernel
+TALL_PROJECT = True   # projection tasks of 128 rows of T where k % 128 == 0
 L2_OPERANDS = 2 << 20   # bytes of W / U_r rows a die's L2 (4 MB) keeps beside the streams
 
 
@@ -596,7 +599,7 @@ def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
 
     if N["adam"]:
         _call("scao_adam_step", tp("adam"), N["adam"], P, SL, s)
-    for var in range(4):
+    for var in range(8):
         if N[f"proj{var}"]:
             _call("scao_kron_project", tp(f"proj{var}"), N[f"proj{var}"], LF, P, SL, var, s)
     if N["delta"]:
