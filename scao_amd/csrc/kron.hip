@@ -631,19 +631,18 @@ __device__ __forceinline__ void apply_wide(const scao_leaf_desc& L, const scao_p
   const int kk = l / 16;
   const int jl = j0 + 64 * w + 4 * (l % 16);
 
-  // 1) prefetch
+  // 1) prefetch.  A fused filter's EMA goes first: its keep bits are taken
+  // as soon as it lands (before the back-projection), which frees its
+  // registers for the rest of the tile.
   v4f gr[4], gm[4], mm[4], vv[4], dd[4], pp[4], par[4];
   int64_t e[4];
+  const bool fmask = GF32 && (P.flags & SCAO_PF_FMASK);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     e[r] = L.off + (int64_t)(i0 + 4 * kk + r) * L.ld + jl;
+    if (fmask) gm[r] = gld4_nt(P.fema + e[r]);
     gr[r] = gld4_nt((const float*)P.graw + e[r]);
-    if (GF32) {   // the fp32 moment buffer, or (fused) the filter's EMA
-      if (!fused_mgrad(P))
-        gm[r] = gld4_nt((const float*)P.g + e[r]);
-      else
-        gm[r] = (P.flags & SCAO_PF_FMASK) ? gld4_nt(P.fema + e[r]) : gr[r];
-    }
+    if (GF32 && !fused_mgrad(P)) gm[r] = gld4_nt((const float*)P.g + e[r]);
     mm[r] = gld4_nt(P.exp_avg + e[r]);
     vv[r] = gld4_nt(P.exp_avg_sq + e[r]);
     dd[r] = gld4_nt(P.exp_avg_diff + e[r]);
@@ -661,6 +660,15 @@ __device__ __forceinline__ void apply_wide(const scao_leaf_desc& L, const scao_p
   v4f a = gld4(wrow), b[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) b[t] = gld4(urow + (int64_t)t * k);
+  uint32_t keep = 0xffffu;   // bit 4r+t: the filter keeps element (r, t)
+  if (fmask) {
+    const float thr = *P.fthr;
+    keep = 0u;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int t = 0; t < 4; ++t) keep |= (gm[r][t] >= thr ? 1u : 0u) << (4 * r + t);
+  }
   for (int c = 0; c < k; c += 16) {
     const bool more = c + 16 < k;
     v4f an = a, bn[4] = {b[0], b[1], b[2], b[3]};
@@ -683,7 +691,7 @@ __device__ __forceinline__ void apply_wide(const scao_leaf_desc& L, const scao_p
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const v4f corr = {acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
-    if (GF32 && fused_mgrad(P)) gm[r] = finish_mgrad(P, e[r], gr[r], gm[r], 15);
+    if (GF32 && fused_mgrad(P)) gm[r] = finish_mgrad_bits(P, e[r], gr[r], (keep >> (4 * r)) & 15u, 15);
     v4f out;
     adan4<GF32, LARS>(P, S, SCAO_F32, gr[r], gm[r], corr, mm[r], vv[r], dd[r], pp[r], par[r], out,
                       u2, 15);

@@ -190,13 +190,14 @@ __device__ __forceinline__ v4f normals4(uint64_t key, int64_t e) {
 // other streams): fp32(g) * (em >= t), then + fp32(fnoise * z) with
 // SCAO_PF_FNOISE -- the values scao_sparse_filter's output pass would write.
 // Lanes outside `mask` are left as they are.
-__device__ __forceinline__ v4f finish_mgrad(const scao_param_desc& P, int64_t e, const v4f& gr,
-                                            const v4f& em, int mask) {
+// keep: bit t set when the filter keeps element t (EMA >= threshold); all
+// set when the parameter has no filter mask.
+__device__ __forceinline__ v4f finish_mgrad_bits(const scao_param_desc& P, int64_t e,
+                                                 const v4f& gr, uint32_t keep, int mask) {
   v4f o = gr;
   if (P.flags & SCAO_PF_FMASK) {
-    const float thr = *P.fthr;
 #pragma unroll
-    for (int t = 0; t < 4; ++t) o[t] = gr[t] * (em[t] >= thr ? 1.0f : 0.0f);
+    for (int t = 0; t < 4; ++t) o[t] = gr[t] * (((keep >> t) & 1u) ? 1.0f : 0.0f);
   }
   if (P.flags & SCAO_PF_FNOISE) {
     const uint64_t key = *P.fseed;
@@ -215,6 +216,18 @@ __device__ __forceinline__ v4f finish_mgrad(const scao_param_desc& P, int64_t e,
     }
   }
   return o;
+}
+
+__device__ __forceinline__ v4f finish_mgrad(const scao_param_desc& P, int64_t e, const v4f& gr,
+                                            const v4f& em, int mask) {
+  uint32_t keep = 15u;
+  if (P.flags & SCAO_PF_FMASK) {
+    const float thr = *P.fthr;
+    keep = 0u;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) keep |= (em[t] >= thr ? 1u : 0u) << t;
+  }
+  return finish_mgrad_bits(P, e, gr, keep, mask);
 }
 
 // true when the moment gradient is formed in-kernel from graw (+ the EMA)
