@@ -785,7 +785,11 @@ __device__ __forceinline__ void pipe_corr(const float* __restrict__ wrow,
 // row set), over NH chunks of a reduction of length K: every U_r load feeds
 // both tiles.  Instantiated for k = 256 only: a second instantiation raises
 // the kernel's register count past the 128 that keep two blocks on a CU.
-template <int K, int NH, int PD>
+// With MID >= 0 a block barrier follows chunk MID's products: the loads of
+// the chunks after it are already in flight across the barrier (a block
+// barrier waits for LDS operations only), so the second half of a pair starts
+// without an operand-latency bubble.
+template <int K, int NH, int PD, int MID = -1>
 __device__ __forceinline__ void pipe_corr2(const float* __restrict__ wa,
                                            const float* __restrict__ wb,
                                            const float* __restrict__ urow, v4f (&acc)[2][4]) {
@@ -813,6 +817,7 @@ __device__ __forceinline__ void pipe_corr2(const float* __restrict__ wa,
 #pragma unroll
       for (int t = 0; t < 4; ++t) B[d][t] = gld4(urow + (int64_t)t * K + 16 * (c + PD));
     }
+    if (c == MID) __syncthreads();
   }
 }
 
@@ -837,39 +842,44 @@ __global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict_
       return;
     }
     v4f acc[2][4];
-    // half h of pair q (tiles 2q and 2q+1; the second may be absent)
-    auto work = [&](int q, int h) {
-      const scao_task ta = tasks[t0 + 2 * q];
-      const bool hasb = 2 * q + 1 < nt;
-      const scao_task tb = hasb ? tasks[t0 + 2 * q + 1] : ta;
-      if (h == 0) {
+    auto zero = [&]() {
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < 2; ++i)
 #pragma unroll
-          for (int t = 0; t < 4; ++t) acc[i][t] = v4f{0.f, 0.f, 0.f, 0.f};
-      }
-      if (hasb && tb.idx == ta.idx && tb.b == ta.b && leaves[ta.idx].k == 256) {
-        // chunks [8h, 8h + 8) of both tiles
-        const scao_leaf_desc& L = leaves[ta.idx];
-        const int jl = ta.b + 64 * w + 4 * (l % 16);
-        const int c0 = 4 * kk + 128 * h;
-        pipe_corr2<256, 8, 4>(L.W + (int64_t)(ta.a + l % 16) * 256 + c0,
-                              L.W + (int64_t)(tb.a + l % 16) * 256 + c0,
-                              L.Ur + (int64_t)jl * 256 + c0, acc);
-      } else if (h == 0 || hasb) {
-        const scao_task tk = h ? tb : ta;
-        const scao_leaf_desc& L = leaves[tk.idx];
-        const int k = L.k;
-        const int jl = tk.b + 64 * w + 4 * (l % 16);
-        const float* __restrict__ wrow = L.W + (int64_t)(tk.a + l % 16) * k + 4 * kk;
-        const float* __restrict__ urow = L.Ur + (int64_t)jl * k + 4 * kk;
-        if (k == 256)
-          pipe_corr<16>(wrow, urow, k, acc[h]);
-        else if (k == 128)
-          pipe_corr<8>(wrow, urow, k, acc[h]);
-        else
-          pipe_corr<0>(wrow, urow, k, acc[h]);
-      }
+        for (int t = 0; t < 4; ++t) acc[i][t] = v4f{0.f, 0.f, 0.f, 0.f};
+    };
+    // tiles 2q and 2q+1 share one pass over their U_r rows
+    auto paired = [&](int q) {
+      if (2 * q + 1 >= nt) return false;
+      const scao_task ta = tasks[t0 + 2 * q], tb = tasks[t0 + 2 * q + 1];
+      return tb.idx == ta.idx && tb.b == ta.b && leaves[ta.idx].k == 256;
+    };
+    // a pair's 16 chunks, with barrier 2q-1 after the first 8 when MID
+    auto pair = [&](int q, auto mid) {
+      const scao_task ta = tasks[t0 + 2 * q], tb = tasks[t0 + 2 * q + 1];
+      const scao_leaf_desc& L = leaves[ta.idx];
+      const int jl = ta.b + 64 * w + 4 * (l % 16);
+      zero();
+      pipe_corr2<256, 16, 4, decltype(mid)::value>(
+          L.W + (int64_t)(ta.a + l % 16) * 256 + 4 * kk,
+          L.W + (int64_t)(tb.a + l % 16) * 256 + 4 * kk, L.Ur + (int64_t)jl * 256 + 4 * kk, acc);
+    };
+    // otherwise tile 2q in the first half and tile 2q+1 (if any) in the second
+    auto single = [&](int q, int h) {
+      if (h == 0) zero();
+      if (h == 1 && 2 * q + 1 >= nt) return;
+      const scao_task tk = tasks[t0 + 2 * q + h];
+      const scao_leaf_desc& L = leaves[tk.idx];
+      const int k = L.k;
+      const int jl = tk.b + 64 * w + 4 * (l % 16);
+      const float* __restrict__ wrow = L.W + (int64_t)(tk.a + l % 16) * k + 4 * kk;
+      const float* __restrict__ urow = L.Ur + (int64_t)jl * k + 4 * kk;
+      if (k == 256)
+        pipe_corr<16>(wrow, urow, k, acc[h]);
+      else if (k == 128)
+        pipe_corr<8>(wrow, urow, k, acc[h]);
+      else
+        pipe_corr<0>(wrow, urow, k, acc[h]);
     };
     auto put = [&](int q) {
 #pragma unroll
@@ -883,15 +893,25 @@ __global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict_
         }
       }
     };
-    work(0, 0);
-    work(0, 1);
+    using NoMid = std::integral_constant<int, -1>;
+    using Mid = std::integral_constant<int, 7>;
+    if (paired(0)) {
+      pair(0, NoMid{});
+    } else {
+      single(0, 0);
+      single(0, 1);
+    }
     put(0);
     __syncthreads();                       // barrier 0: tiles 0 and 1 ready
     const int np = (nt + 1) / 2;
     for (int q = 1; q < np; ++q) {
-      work(q, 0);
-      __syncthreads();                     // barrier 2q-1
-      work(q, 1);
+      if (paired(q)) {
+        pair(q, Mid{});                    // barrier 2q-1 inside
+      } else {
+        single(q, 0);
+        __syncthreads();                   // barrier 2q-1
+        single(q, 1);
+      }
       put(q);                              // buffers of tiles 2q-4, 2q-3: consumed
       __syncthreads();                     // barrier 2q: tiles 2q, 2q+1 ready
     }
