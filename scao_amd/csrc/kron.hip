@@ -180,11 +180,12 @@ __device__ __forceinline__ void project_tile(const scao_leaf_desc& L, const scao
 // so one float4 of a U_r row feeds all four tiles.
 constexpr int DP = 64 + 4;   // LDS pitch of a partial tile
 
+// Ps (three partial tiles) and red live in the caller's LDS, so a kernel
+// holding both instantiations allocates them once.
 template <bool FAST>
 __device__ __forceinline__ void delta_tile(const scao_leaf_desc& L, float eps, int c0, int d0,
-                                           int slot, double* slots) {
-  __shared__ __attribute__((aligned(16))) float Ps[3][64][DP];
-  __shared__ double red[16];
+                                           int slot, double* slots, float (*Ps)[64][DP],
+                                           double* red) {
   const int w = threadIdx.x / 64, l = threadIdx.x % 64;
   const int n = L.n, k = L.k;
   const int kk = l / 16;
@@ -1025,12 +1026,14 @@ __global__ __launch_bounds__(256) void k_delta(const scao_task* __restrict__ tas
                                                double* slots) {
   const scao_task tk = tasks[blockIdx.x];
   const scao_leaf_desc L = leaves[tk.idx];
+  __shared__ __attribute__((aligned(16))) float Ps[3][64][DP];
+  __shared__ double red[16];
   const bool fast = (L.flags & SCAO_LF_VEC4) && (L.k % 4 == 0) && tk.a + 64 <= L.k &&
                     tk.b + 64 <= L.k && (L.n % 64 == 0);
   if (fast)
-    delta_tile<true>(L, params[L.param].eps, tk.a, tk.b, tk.slot, slots);
+    delta_tile<true>(L, params[L.param].eps, tk.a, tk.b, tk.slot, slots, Ps, red);
   else
-    delta_tile<false>(L, params[L.param].eps, tk.a, tk.b, tk.slot, slots);
+    delta_tile<false>(L, params[L.param].eps, tk.a, tk.b, tk.slot, slots, Ps, red);
 }
 __global__ __launch_bounds__(256) void k_lift(const scao_task* __restrict__ tasks,
                                               const scao_leaf_desc* __restrict__ leaves) {
@@ -1059,8 +1062,11 @@ __global__ __launch_bounds__(256) void k_project_one(scao_leaf_desc L, scao_para
                              (blockIdx.x / strips) * 64, -1, nullptr);
 }
 __global__ __launch_bounds__(256) void k_delta_one(scao_leaf_desc L) {
+  __shared__ __attribute__((aligned(16))) float Ps[3][64][DP];
+  __shared__ double red[16];
   const int tiles = (L.k + 63) / 64;
-  delta_tile<false>(L, 1e-8f, (blockIdx.x / tiles) * 64, (blockIdx.x % tiles) * 64, -1, nullptr);
+  delta_tile<false>(L, 1e-8f, (blockIdx.x / tiles) * 64, (blockIdx.x % tiles) * 64, -1, nullptr,
+                    Ps, red);
 }
 __global__ __launch_bounds__(256) void k_lift_one(scao_leaf_desc L) {
   const int tiles = (L.k + 63) / 64;
