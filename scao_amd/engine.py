@@ -476,18 +476,22 @@ def _param_table(items: list[PItem], ranges, ws: Workspace, gsnr: float | None):
     shared: dict = {}
     u8rows, i4rows, fnoise, dbias = [], [], [], []
     for i, it in enumerate(items):
-        st = it.st
-        dev = it.p.device
+        st, p = it.st, it.p
         pp, graw, gmom, fema, m0, m1, m2, m3 = it.ptrs
+        # per parameter, kept while the parameter and its moment tensors are
+        # the same objects: the moments' check, numel, columns, dtype code
         seen = ws.checked.get(id(st))
         if (seen is None or seen[0]() is not st["exp_avg"] or seen[1]() is not st["exp_avg_sq"]
-                or seen[2]() is not st["exp_avg_diff"] or seen[3]() is not st["prev_grad"]):
+                or seen[2]() is not st["exp_avg_diff"] or seen[3]() is not st["prev_grad"]
+                or seen[4]() is not p):
+            dev = p.device
             moms = [st[key] for key in _MOMENTS]
             for key, m in zip(_MOMENTS, moms):
                 if m.dtype != f32 or not m.is_contiguous() or m.device != dev:
                     raise ValueError(f"state[{key!r}] must be a contiguous float32 tensor on "
                                      f"{dev}; got {m.dtype} on {m.device}")
-            ws.checked[id(st)] = tuple(weakref.ref(m) for m in moms)
+            seen = ws.checked[id(st)] = (*(weakref.ref(m) for m in moms), weakref.ref(p),
+                                         p.numel(), _cols(p), L.DTYPE_CODE[p.dtype])
         lars = it.phase2 and it.lars
         skey = (id(it.group), it.step, it.phase2, it.scao_step if it.phase2 else 0, lars)
         sc = shared.get(skey)
@@ -519,9 +523,9 @@ def _param_table(items: list[PItem], ranges, ws: Workspace, gsnr: float | None):
         if it.aligned:
             flags |= L.PF_ALIGNED
         u8rows.append((pp, gmom or graw, graw, m0, m1, m2, m3, upd, diag, fema, fthr, fseed,
-                       it.p.numel(), _cols(it.p)))
+                       seen[5], seen[6]))
         r = ranges[i]
-        i4rows.append((L.DTYPE_CODE[it.p.dtype], flags, r[0], r[1], r[2], r[3], i))
+        i4rows.append((seen[7], flags, r[0], r[1], r[2], r[3], i))
         fnoise.append(fn)
     raw = np.zeros((n, L.PARAM_DESC.itemsize), dtype=np.uint8)
 
