@@ -784,8 +784,7 @@ __device__ __forceinline__ void pipe_corr(const float* __restrict__ wrow,
 
 // The same for two row tiles of one strip (W rows from wa and wb, one U_r
 // row set), over NH chunks of a reduction of length K: every U_r load feeds
-// both tiles.  Instantiated for k = 256 only: a second instantiation raises
-// the kernel's register count past the 128 that keep two blocks on a CU.
+// both tiles (k = 128 and 256).
 // With MID >= 0 a block barrier follows chunk MID's products: the loads of
 // the chunks after it are already in flight across the barrier (a block
 // barrier waits for LDS operations only), so the second half of a pair starts
@@ -853,7 +852,7 @@ __global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict_
     auto paired = [&](int q) {
       if (2 * q + 1 >= nt) return false;
       const scao_task ta = tasks[t0 + 2 * q], tb = tasks[t0 + 2 * q + 1];
-      return tb.idx == ta.idx && tb.b == ta.b && leaves[ta.idx].k == 256;
+      return tb.idx == ta.idx && tb.b == ta.b && (leaves[ta.idx].k == 256 || leaves[ta.idx].k == 128);
     };
     // a pair's 16 chunks, with barrier 2q-1 after the first 8 when MID
     auto pair = [&](int q, auto mid) {
@@ -861,9 +860,14 @@ __global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict_
       const scao_leaf_desc& L = leaves[ta.idx];
       const int jl = ta.b + 64 * w + 4 * (l % 16);
       zero();
-      pipe_corr2<256, 16, 4, decltype(mid)::value>(
-          L.W + (int64_t)(ta.a + l % 16) * 256 + 4 * kk,
-          L.W + (int64_t)(tb.a + l % 16) * 256 + 4 * kk, L.Ur + (int64_t)jl * 256 + 4 * kk, acc);
+      if (L.k == 256)
+        pipe_corr2<256, 16, 4, decltype(mid)::value>(
+            L.W + (int64_t)(ta.a + l % 16) * 256 + 4 * kk,
+            L.W + (int64_t)(tb.a + l % 16) * 256 + 4 * kk, L.Ur + (int64_t)jl * 256 + 4 * kk, acc);
+      else
+        pipe_corr2<128, 8, 4, (decltype(mid)::value < 0 ? -1 : 3)>(
+            L.W + (int64_t)(ta.a + l % 16) * 128 + 4 * kk,
+            L.W + (int64_t)(tb.a + l % 16) * 128 + 4 * kk, L.Ur + (int64_t)jl * 128 + 4 * kk, acc);
     };
     // otherwise tile 2q in the first half and tile 2q+1 (if any) in the second
     auto single = [&](int q, int h) {

@@ -265,7 +265,7 @@ def _build_structure(items: list[PItem]):
                 if not (mw and nw):
                     mw = nw = 0
                 wide = var | 4 | (8 if k >= PIPE_MIN_RANK else 0)
-                for i0, j0 in _wide_tiles(mw, nw, k):
+                for i0, j0 in _wide_tiles(mw, nw, k, k >= PIPE_MIN_RANK):
                     tasks[f"apply{wide}"].append((li, i0, j0, slot))
                     slot += 1
                 for i0 in range(0, m, T):
@@ -292,10 +292,11 @@ def _build_structure(items: list[PItem]):
 XCDS = 8   # MI355X: 8 accelerator dies, workgroup i is dispatched to die i % 8
 PIPE_MIN_RANK = 128   # wide apply tiles of blocks with k >= this use the pipelined kernel
 TALL_PROJECT = True   # projection tasks of 128 rows of T where k % 128 == 0
+PIPE_STRIP_ORDER = True   # pipelined leaves always take the strip-major (super-tile) order
 L2_OPERANDS = 2 << 20   # bytes of W / U_r rows a die's L2 (4 MB) keeps beside the streams
 
 
-def _wide_tiles(mw: int, nw: int, k: int) -> list:
+def _wide_tiles(mw: int, nw: int, k: int, pipelined: bool = False) -> list:
     """(i0, j0) of a leaf's wide apply tiles in the order their blocks run.
 
     A tile reads the W rows of its row band (16 x k) and the U_r rows of its
@@ -306,9 +307,11 @@ def _wide_tiles(mw: int, nw: int, k: int) -> list:
     cycle through every strip's U_r, and the misses refetch it from HBM.
     Then the tiles go in super-tiles of R bands x S strips, strip by strip,
     with R and S sized so that one super-tile's operands take L2_OPERANDS:
-    a block's run stays in one strip and the die shares a few strips."""
+    a block's run stays in one strip and the die shares a few strips.  The
+    pipelined kernel's leaves always take that order: it computes two tiles
+    of one strip per pass over their U_r rows."""
     rows, cols = L.APPLY_WIDE_ROWS, L.APPLY_WIDE_COLS
-    if (mw + nw) * k * 4 <= L2_OPERANDS:
+    if (mw + nw) * k * 4 <= L2_OPERANDS and not (pipelined and PIPE_STRIP_ORDER):
         return [(i0, j0) for i0 in range(0, mw, rows) for j0 in range(0, nw, cols)]
     half = L2_OPERANDS // 2
     s = max(1, half // (cols * k * 4))

@@ -242,16 +242,18 @@ def test_pipelined_apply_tasks():
             assert queue_of[int(t["idx"])] == b % E.XCDS
 
 
-@pytest.mark.parametrize("m,n,k", [(4096, 4096, 256), (1024, 4096, 256), (2048, 2048, 128),
-                                   (2048, 2048, 64), (4096, 2048, 256)])
-def test_wide_tile_order(m, n, k):
-    """Every wide tile once; leaves whose W and U_r exceed L2_OPERANDS go in
-    super-tiles whose operands fit it, each run of APPLY_GROUP tiles inside
-    one column strip; smaller leaves keep row-major order."""
+@pytest.mark.parametrize("m,n,k,pipelined", [(4096, 4096, 256, True), (1024, 4096, 256, True),
+                                             (2048, 2048, 128, False), (2048, 2048, 128, True),
+                                             (2048, 2048, 64, False), (4096, 2048, 256, True)])
+def test_wide_tile_order(m, n, k, pipelined):
+    """Every wide tile once; leaves whose W and U_r exceed L2_OPERANDS, and
+    every leaf of the pipelined kernel, go in super-tiles whose operands fit
+    it, each run of APPLY_GROUP tiles inside one column strip (so the
+    pipelined kernel can pair them); other leaves keep row-major order."""
     rows, cols = L.APPLY_WIDE_ROWS, L.APPLY_WIDE_COLS
-    order = E._wide_tiles(m, n, k)
+    order = E._wide_tiles(m, n, k, pipelined)
     assert sorted(order) == [(i, j) for i in range(0, m, rows) for j in range(0, n, cols)]
-    if (m + n) * k * 4 <= E.L2_OPERANDS:
+    if (m + n) * k * 4 <= E.L2_OPERANDS and not pipelined:
         assert order == [(i, j) for i in range(0, m, rows) for j in range(0, n, cols)]
         return
     for b in range(0, len(order), L.APPLY_GROUP):
