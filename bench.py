@@ -219,11 +219,14 @@ def main():
 
     t_first = timed(one)                      # step 1: state allocation + Phase 1
     t_phase1 = timed(one)                     # step 2: Phase 1 (Adam) everywhere
+    t_refresh_first = timed(one)              # step 3: Phase 1 + the first curvature refresh
+    one()                                     # step 4: Phase 2 begins (task lists built)
+    one()                                     # step 5
     engine.TIMING = {}
-    t_refresh = timed(one)                    # step 3: Phase 1 + curvature refresh
+    t_refresh = timed(one)                    # step 6: Phase 2 + a refresh (steady state)
     refresh_parts = engine.timing_summary()
-    if args.no_refresh:                       # step 3 was a plain Phase-2 step
-        t_refresh, refresh_parts = None, {}
+    if args.no_refresh:                       # steps 3 and 6 were plain steps
+        t_refresh, t_refresh_first, refresh_parts = None, None, {}
     engine.TIMING = None
     for g in opt.param_groups:
         g["precond_freq"] = 10 ** 9           # steady state: no refresh in the timed region
@@ -349,6 +352,7 @@ def main():
         "phase1_step_ms": p1_ms,
         "phase1_first_step_ms": t_phase1,
         "refresh_step_ms": t_refresh,
+        "refresh_first_step_ms": t_refresh_first,
         "refresh_parts_ms": {k: {"count": c, "mean": m_, "total": t}
                              for k, (c, m_, t) in refresh_parts.items()},
         "first_step_ms": t_first,
