@@ -160,6 +160,12 @@ CASES = {
                                   use_int8_ema=True, k_min=128, k_max=128, warmup_steps=2,
                                   blend_steps=3, precond_freq=4, min_precond_updates=1, tau=1.0,
                                   lars_coeff=1e-3), 7),
+    # k = 192 (a multiple of 16, not of 128): the generic-k paths of the
+    # pipelined apply (no pairs), the lift and 64-row projection chunks
+    "pipe_k192_generic": (FAST, dict(lr=1e-3, weight_decay=0.01, max_precond_dim=512,
+                                     rho=0.999, use_int8_ema=True, k_min=192, k_max=192,
+                                     warmup_steps=2, blend_steps=2, precond_freq=4,
+                                     min_precond_updates=1, tau=1.0, lars_coeff=1e-3), 6),
     # k = 256 on a 2048 x 1024 block: W and U_r (3 MB) exceed what the wide
     # tiles' row-major order keeps in L2, so they run in super-tiles
     "pipe_k256_supertile": ({"big": (2048, 1024), "ln": (1024,)},
