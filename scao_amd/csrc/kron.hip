@@ -719,7 +719,8 @@ __device__ __forceinline__ void apply_wide(const scao_leaf_desc& L, const scao_p
 // the MFMAs, bound this role).  Pair q's reduction is split in two halves,
 // computed between barriers 2q-2, 2q-1 and 2q, so each barrier interval holds
 // one tile's worth of MFMA work; pair 0 is done before barrier 0.  Tiles of
-// different blocks or strips are computed one per half instead.  Each role
+// different blocks or strips, and ranks other than 128 and 256, are computed
+// one per half instead.  Each role
 // waits only on its own memory operations (the vector-memory counter is in
 // order within a wave, so an operand load queued behind the streaming loads
 // would wait for them too).  Both roles use apply_wide's lane <-> element
@@ -854,7 +855,8 @@ __global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict_
       const scao_task ta = tasks[t0 + 2 * q], tb = tasks[t0 + 2 * q + 1];
       return tb.idx == ta.idx && tb.b == ta.b && (leaves[ta.idx].k == 256 || leaves[ta.idx].k == 128);
     };
-    // a pair's 16 chunks, with barrier 2q-1 after the first 8 when MID
+    // a pair's chunks (16 at k = 256, 8 at k = 128), with barrier 2q-1 after
+    // the first half when MID
     auto pair = [&](int q, auto mid) {
       const scao_task ta = tasks[t0 + 2 * q], tb = tasks[t0 + 2 * q + 1];
       const scao_leaf_desc& L = leaves[ta.idx];
