@@ -506,6 +506,44 @@ def test_lookahead_trajectory():
     assert worst < 1e-4
 
 
+def test_params_without_gradient_in_some_steps():
+    """A parameter whose .grad is None in a step is skipped that step (its
+    state and counters untouched), as the reference does; the others step
+    normally.  The set of stepping parameters changes from step to step (a
+    frozen branch, a conditional layer), 9 steps through Phase 1, the blend
+    and Phase 2 with refreshes."""
+    dev = _dev()
+    import scao_amd
+    cfg = dict(CASES["int8_small"][1])
+    rp = make_params(SHAPES)
+    gp = {k: torch.nn.Parameter(v.detach().clone().to(dev)) for k, v in rp.items()}
+    ref = R.RefSCAO(list(rp.values()), **cfg, **PARITY)
+    gopt = scao_amd.SCAO(list(gp.values()), **cfg, **PARITY)
+    init = {k: v.detach().clone() for k, v in rp.items()}
+    names = list(SHAPES)
+    worst = 0.0
+    for t in range(1, 10):
+        grads = grads_for_step(t, SHAPES)
+        skip = {names[t % len(names)], names[(3 * t) % len(names)]} if t % 3 else set()
+        for k in SHAPES:
+            if k in skip:
+                rp[k].grad = gp[k].grad = None
+            else:
+                rp[k].grad = grads[k].clone()
+                gp[k].grad = grads[k].to(dev)
+        print(f"step {t}: skipping {sorted(skip)}", flush=True)
+        ref.step()
+        gopt.step()
+        torch.cuda.synchronize()
+        for k in SHAPES:
+            rs, gs = ref.state.get(rp[k], {}), gopt.state.get(gp[k], {})
+            assert rs.get("step", 0) == gs.get("step", 0), (t, k)
+            assert rs.get("scao_step", 0) == gs.get("scao_step", 0), (t, k)
+            worst = max(worst, _rel(gp[k].detach() - init[k].to(dev), rp[k].detach() - init[k]))
+    report("params_without_gradient", "int8_small", {"max_cumulative_update_rel_err": worst})
+    assert worst < 1e-3
+
+
 def test_resume_from_reference_checkpoint_file():
     """A checkpoint file written by the reference (golden fixture), loaded
     with scao_amd.checkpoint.load (safe loader) onto the GPU, then two
