@@ -544,6 +544,40 @@ def test_params_without_gradient_in_some_steps():
     assert worst < 1e-3
 
 
+def test_param_groups_with_different_settings():
+    """Three parameter groups with their own lr, betas, weight decay, clip
+    and LARS in one optimizer (the step's per-group scalars), 8 steps."""
+    dev = _dev()
+    import scao_amd
+    cfg = dict(CASES["int8_small"][1])
+    rp = make_params(SHAPES)
+    gp = {k: torch.nn.Parameter(v.detach().clone().to(dev)) for k, v in rp.items()}
+    names = list(SHAPES)
+    over = [dict(), dict(lr=3e-3, betas=(0.8, 0.99), weight_decay=0.0, tau=None,
+                         lars_coeff=0.0),
+            dict(lr=2e-2, weight_decay=0.1, tau=0.5, beta3=0.9)]
+
+    def groups(params):
+        return [dict(params=[params[k] for k in names[i::3]], **over[i]) for i in range(3)]
+
+    ref = R.RefSCAO(groups(rp), **cfg, **PARITY)
+    gopt = scao_amd.SCAO(groups(gp), **cfg, **PARITY)
+    init = {k: v.detach().clone() for k, v in rp.items()}
+    worst = 0.0
+    for t in range(1, 9):
+        grads = grads_for_step(t, SHAPES)
+        for k in SHAPES:
+            rp[k].grad = grads[k].clone()
+            gp[k].grad = grads[k].to(dev)
+        ref.step()
+        gopt.step()
+        torch.cuda.synchronize()
+        for k in SHAPES:
+            worst = max(worst, _rel(gp[k].detach() - init[k].to(dev), rp[k].detach() - init[k]))
+    report("param_groups", "int8_small", {"max_cumulative_update_rel_err": worst})
+    assert worst < 1e-3
+
+
 def test_resume_from_reference_checkpoint_file():
     """A checkpoint file written by the reference (golden fixture), loaded
     with scao_amd.checkpoint.load (safe loader) onto the GPU, then two
