@@ -115,6 +115,8 @@ class Workspace:
         # moment tensors already checked (contiguous fp32 on the device), per
         # parameter state: weak references, so a replaced tensor is checked again
         self.checked: dict = {}
+        # per-parameter shares of the step structure (engine._build_structure)
+        self.structures: dict = {}
         self.struct_key = None
         self.cheap_key = None
         self.leaf_epoch = -1
@@ -191,101 +193,150 @@ def _flat_chunks(numel: int) -> int:
     return (numel + L.FLAT_CHUNK - 1) // L.FLAT_CHUNK
 
 
-def _build_structure(items: list[PItem]):
+_LEAF_TASKS = ("delta", "lift")   # with proj* and apply*: idx is a block index
+_TASK_TYPES = (["adam", "delta", "lift", "dred", "dapply", "lars"] +
+               [f"proj{v}" for v in range(8)] + [f"apply{v}" for v in range(16)])
+
+
+def _param_tasks(it: PItem):
+    """One parameter's share of a step structure, with local indices: block
+    indices from 0 (first block of the parameter), parameter index 0, slots
+    from 0.  Returns ({type: int32 array (n, 4)}, local slot ranges, slot
+    count, [(leaf, r0, c0)])."""
+    tasks = {}
+
+    def add(kind, t):
+        tasks.setdefault(kind, []).append(t)
+
+    slot = 0
+    leaves = list(it.leaves) if it.phase2 and not it.diag else []
+    if not it.phase2:
+        for c in range(_flat_chunks(it.p.numel())):
+            add("adam", (0, c, 0, slot))
+            slot += 1
+        rng = (0, slot, slot, slot)
+    elif it.diag:
+        for c in range(_flat_chunks(it.p.numel())):
+            add("dred", (0, c, 0, slot))
+            slot += 1
+        pre_end = slot
+        for c in range(_flat_chunks(it.p.numel())):
+            add("dapply", (0, c, 0, slot))
+            slot += 1
+        rng = (0, pre_end, pre_end, slot)
+    else:
+        # projection (chunk 0 owns the norm slots)
+        for li, (leaf, r0, c0l) in enumerate(leaves):
+            m, n = leaf.m, leaf.n
+            k = leaf.U_l.shape[1]
+            vec = _leaf_vec(it, leaf, r0, c0l)
+            for j0 in range(0, n, L.PROJ_COLS):
+                whole = vec and it.fp32 and j0 + L.PROJ_COLS <= n and m % 32 == 0
+                # 128 rows of T per task where k allows (variant bit 4)
+                cr = 128 if TALL_PROJECT and whole and k % 128 == 0 else 64
+                for c0 in range(0, k, cr):
+                    fast = whole and c0 + 64 <= k
+                    do_p = c0 == 0 and it.lars
+                    var = (1 if fast else 0) | (2 if do_p else 0) | (4 if cr == 128 else 0)
+                    if c0 == 0:
+                        add(f"proj{var}", (li, j0, c0, slot))
+                        slot += 1
+                    else:
+                        add(f"proj{var}", (li, j0, c0, -1))
+        for li, (leaf, _, _) in enumerate(leaves):
+            k = leaf.U_l.shape[1]
+            for a in range(0, k, 64):
+                for b in range(0, k, 64):
+                    add("delta", (li, a, b, slot))
+                    slot += 1
+        pre_end = slot
+        for li, (leaf, r0, c0l) in enumerate(leaves):
+            k = leaf.U_l.shape[1]
+            for i0 in range(0, leaf.m, 64):
+                for d0 in range(0, k, 64):
+                    add("lift", (li, i0, d0, -1))
+            var = (1 if it.mgrad else 0) | (2 if it.lars else 0)
+            ok = _leaf_vec(it, leaf, r0, c0l) and it.fp32 and it.aligned and k % 16 == 0
+            m, n, T = leaf.m, leaf.n, L.APPLY_TILE
+            # wide 16x256 tiles over the interior that they tile exactly,
+            # masked 64x64 tiles over the right column strip and the
+            # bottom row strip
+            mw = m - m % L.APPLY_WIDE_ROWS if ok else 0
+            nw = n - n % L.APPLY_WIDE_COLS if ok else 0
+            if not (mw and nw):
+                mw = nw = 0
+            wide = var | 4 | (8 if k >= PIPE_MIN_RANK else 0)
+            for i0, j0 in _wide_tiles(mw, nw, k, k >= PIPE_MIN_RANK):
+                add(f"apply{wide}", (li, i0, j0, slot))
+                slot += 1
+            for i0 in range(0, m, T):
+                for j0 in range(nw, n, T):
+                    add(f"apply{var}", (li, i0, j0, slot))
+                    slot += 1
+            for i0 in range(mw, m, T):
+                for j0 in range(0, nw, T):
+                    add(f"apply{var}", (li, i0, j0, slot))
+                    slot += 1
+        rng = (0, pre_end, pre_end, slot)
+    if it.phase2 and it.lars:
+        for c in range(_flat_chunks(it.p.numel())):
+            add("lars", (0, c, 0, -1))
+    arrays = {k: np.array(v, dtype=np.int32).reshape(-1, 4) for k, v in tasks.items()}
+    return arrays, rng, slot, leaves
+
+
+def _item_key(it: PItem) -> tuple:
+    """Everything _param_tasks reads from an item."""
+    return (id(it.p), it.phase2, it.diag, it.lars, it.mgrad, it.p.numel(), it.fp32, it.aligned,
+            _cols(it.p), tuple((id(lf), r0, c0, lf.U_l.shape[1]) for lf, r0, c0 in it.leaves)
+            if it.phase2 and not it.diag else ())
+
+
+def _build_structure(items: list[PItem], cache: dict | None = None):
     """Slots, task lists and the Phase-2 leaf list for a step structure.
 
     Every reduction slot is written by exactly one task; each parameter's
-    pre-finalize slots and post-finalize slots are contiguous ranges."""
-    tasks = {k: [] for k in ["adam", "delta", "lift", "dred", "dapply", "lars"] +
-             [f"proj{v}" for v in range(8)] + [f"apply{v}" for v in range(16)]}
-    ranges = []
-    leaves = []          # (leaf, r0, c0, param index)
+    pre-finalize slots and post-finalize slots are contiguous ranges.  Each
+    parameter's share is built once per configuration (``cache``, keyed by
+    the item and the module's tiling settings) and placed by offsets, so a
+    step whose set of parameters changes (a parameter without a gradient,
+    a rank change) costs array arithmetic, not a rebuild of every tile."""
+    knobs = (TALL_PROJECT, PIPE_STRIP_ORDER, PIPE_MIN_RANK, L2_OPERANDS, L.APPLY_GROUP)
+    if cache is not None and len(cache) > 4 * len(items) + 64:
+        cache.clear()
+    parts = {k: [] for k in _TASK_TYPES}
+    offs = {k: [] for k in _TASK_TYPES}    # (index offset, slot offset, rows) per part
+    ranges, leaves = [], []
     slot = 0
     for pi, it in enumerate(items):
-        pre_begin = slot
-        if not it.phase2:
-            for c in range(_flat_chunks(it.p.numel())):
-                tasks["adam"].append((pi, c, 0, slot))
-                slot += 1
-            ranges.append((pre_begin, slot, slot, slot))
-            continue
-        if it.diag:
-            for c in range(_flat_chunks(it.p.numel())):
-                tasks["dred"].append((pi, c, 0, slot))
-                slot += 1
-            pre_end = slot
-            for c in range(_flat_chunks(it.p.numel())):
-                tasks["dapply"].append((pi, c, 0, slot))
-                slot += 1
-            ranges.append((pre_begin, pre_end, pre_end, slot))
+        key = (_item_key(it), knobs)
+        frag = cache.get(key) if cache is not None else None
+        if frag is None:
+            frag = _param_tasks(it)
+            if cache is not None:
+                cache[key] = frag
+        arrays, rng, nslot, lvs = frag
+        base = len(leaves)
+        for kind, arr in arrays.items():
+            parts[kind].append(arr)
+            offs[kind].append((base if (kind in _LEAF_TASKS or kind.startswith(("proj", "apply")))
+                               else pi, slot, len(arr)))
+        ranges.append(tuple(x + slot for x in rng))
+        leaves.extend((lf, r0, c0, pi) for lf, r0, c0 in lvs)
+        slot += nslot
+    arrays = {}
+    for kind in _TASK_TYPES:
+        if parts[kind]:
+            a = np.concatenate(parts[kind])
+            o = np.array(offs[kind], dtype=np.int64)
+            a[:, 0] += np.repeat(o[:, 0], o[:, 2]).astype(np.int32)
+            a[:, 3] += np.where(a[:, 3] >= 0, np.repeat(o[:, 1], o[:, 2]), 0).astype(np.int32)
         else:
-            first = len(leaves)
-            for (leaf, r0, c0) in it.leaves:
-                leaves.append((leaf, r0, c0, pi))
-            # projection (chunk 0 owns the norm slots)
-            for li in range(first, len(leaves)):
-                leaf, r0, c0l, _ = leaves[li]
-                m, n = leaf.m, leaf.n
-                k = leaf.U_l.shape[1]
-                vec = _leaf_vec(it, leaf, r0, c0l)
-                for j0 in range(0, n, L.PROJ_COLS):
-                    whole = vec and it.fp32 and j0 + L.PROJ_COLS <= n and m % 32 == 0
-                    # 128 rows of T per task where k allows (variant bit 4)
-                    cr = 128 if TALL_PROJECT and whole and k % 128 == 0 else 64
-                    for c0 in range(0, k, cr):
-                        fast = whole and c0 + 64 <= k
-                        do_p = c0 == 0 and it.lars
-                        var = (1 if fast else 0) | (2 if do_p else 0) | (4 if cr == 128 else 0)
-                        if c0 == 0:
-                            tasks[f"proj{var}"].append((li, j0, c0, slot))
-                            slot += 1
-                        else:
-                            tasks[f"proj{var}"].append((li, j0, c0, -1))
-            for li in range(first, len(leaves)):
-                k = leaves[li][0].U_l.shape[1]
-                for a in range(0, k, 64):
-                    for b in range(0, k, 64):
-                        tasks["delta"].append((li, a, b, slot))
-                        slot += 1
-            pre_end = slot
-            for li in range(first, len(leaves)):
-                leaf, r0, c0l, _ = leaves[li]
-                k = leaf.U_l.shape[1]
-                for i0 in range(0, leaf.m, 64):
-                    for d0 in range(0, k, 64):
-                        tasks["lift"].append((li, i0, d0, -1))
-                var = (1 if it.mgrad else 0) | (2 if it.lars else 0)
-                ok = _leaf_vec(it, leaf, r0, c0l) and it.fp32 and it.aligned and k % 16 == 0
-                m, n, T = leaf.m, leaf.n, L.APPLY_TILE
-                # wide 16x256 tiles over the interior that they tile exactly,
-                # masked 64x64 tiles over the right column strip and the
-                # bottom row strip
-                mw = m - m % L.APPLY_WIDE_ROWS if ok else 0
-                nw = n - n % L.APPLY_WIDE_COLS if ok else 0
-                if not (mw and nw):
-                    mw = nw = 0
-                wide = var | 4 | (8 if k >= PIPE_MIN_RANK else 0)
-                for i0, j0 in _wide_tiles(mw, nw, k, k >= PIPE_MIN_RANK):
-                    tasks[f"apply{wide}"].append((li, i0, j0, slot))
-                    slot += 1
-                for i0 in range(0, m, T):
-                    for j0 in range(nw, n, T):
-                        tasks[f"apply{var}"].append((li, i0, j0, slot))
-                        slot += 1
-                for i0 in range(mw, m, T):
-                    for j0 in range(0, nw, T):
-                        tasks[f"apply{var}"].append((li, i0, j0, slot))
-                        slot += 1
-            ranges.append((pre_begin, pre_end, pre_end, slot))
-        if it.lars:
-            for c in range(_flat_chunks(it.p.numel())):
-                tasks["lars"].append((pi, c, 0, -1))
-    for k in tasks:
-        if k.startswith("apply") or k.startswith("proj"):
-            grp = L.APPLY_GROUP if k.startswith("apply") and int(k[5:]) & 8 else 1
-            tasks[k] = _xcd_interleave(tasks[k], grp)
-    arrays = {k: np.array(v, dtype=np.int32).reshape(-1, 4).copy().view(L.TASK).reshape(-1)
-              for k, v in tasks.items()}
+            a = np.zeros((0, 4), np.int32)
+        if kind.startswith("apply") or kind.startswith("proj"):
+            grp = L.APPLY_GROUP if kind.startswith("apply") and int(kind[5:]) & 8 else 1
+            a = _xcd_interleave(a, grp)
+        arrays[kind] = np.ascontiguousarray(a, dtype=np.int32).view(L.TASK).reshape(-1)
     return arrays, ranges, slot, leaves
 
 
@@ -325,30 +376,37 @@ def _wide_tiles(mw: int, nw: int, k: int, pipelined: bool = False) -> list:
     return out
 
 
-def _xcd_interleave(tasks: list, group: int = 1) -> list:
-    """Order a launch's tasks so that every tile of one block runs on the same
-    die: the blocks are dealt to XCDS queues (largest first, each to the
+def _xcd_interleave(tasks: np.ndarray, group: int = 1) -> np.ndarray:
+    """Order a launch's tasks (int32 rows: idx, a, b, slot) so that every tile
+    of one block runs on the same die: the blocks are dealt to XCDS queues
+    (largest first, ties in order of appearance, each to the first
     least-loaded queue), each queue is cut into runs of `group` tasks (the
     tasks one workgroup takes) and the runs are interleaved, so workgroup i
     takes its run from queue i % XCDS while all queues last.  Each die's L2
     then fetches a block's shared operands (U_l; W and U_r) once instead of
     every die doing so.  Only the order changes: tasks, slots and sums are
     the same."""
-    if len(tasks) <= XCDS * group:
+    n = len(tasks)
+    if n <= XCDS * group:
         return tasks
-    by_leaf: dict = {}
-    for t in tasks:
-        by_leaf.setdefault(t[0], []).append(t)
-    queues = [[] for _ in range(XCDS)]
-    for g in sorted(by_leaf.values(), key=len, reverse=True):
-        min(queues, key=len).extend(g)
-    runs = [[q[i:i + group] for i in range(0, len(q), group)] for q in queues]
-    out = []
-    for i in range(max(len(r) for r in runs)):
-        for r in runs:
-            if i < len(r):
-                out.extend(r[i])
-    return out
+    u, first, inv, cnt = np.unique(tasks[:, 0], return_index=True, return_inverse=True,
+                                   return_counts=True)
+    app = np.argsort(first, kind="stable")                 # blocks in order of appearance
+    srt = app[np.argsort(-cnt[app], kind="stable")]        # largest first
+    queue = np.empty(len(u), dtype=np.int64)
+    rank = np.empty(len(u), dtype=np.int64)
+    qlen = [0] * XCDS
+    for r, j in enumerate(srt.tolist()):
+        q = min(range(XCDS), key=qlen.__getitem__)
+        queue[j], rank[j] = q, r
+        qlen[q] += int(cnt[j])
+    tq, tr = queue[inv], rank[inv]
+    o1 = np.lexsort((np.arange(n), tr, tq))               # each queue's tasks in order
+    q1 = tq[o1]
+    starts = np.concatenate(([0], np.cumsum(np.bincount(q1, minlength=XCDS))[:-1]))
+    pos = np.arange(n) - starts[q1]                       # position inside its queue
+    o2 = np.lexsort((pos, q1, pos // group))              # run by run, queue by queue
+    return tasks[o1][o2]
 
 
 def _cols(t: Tensor) -> int:
@@ -571,7 +629,7 @@ def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
                      for it in items)
         ws.cheap_key = ckey
     if skey != ws.struct_key:
-        arrays, ranges, nslots, leaves = _build_structure(items)
+        arrays, ranges, nslots, leaves = _build_structure(items, ws.structures)
         ws.tasks = {k: (L.upload(v, dev) if len(v) else None) for k, v in arrays.items()}
         ws.ntasks = {k: len(v) for k, v in arrays.items()}
         ws.slot_ranges, ws.nslots, ws.leaves = ranges, nslots, leaves

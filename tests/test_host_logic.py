@@ -218,6 +218,39 @@ def test_param_table_fields_and_state_checks():
         E._param_table(items, ranges, ws, None)
 
 
+def test_structure_cache_matches_fresh_builds():
+    """Per-parameter shares cached across steps give the same task lists,
+    slots and ranges as a fresh build, also when the set of parameters
+    changes from step to step; the interleave keeps every task once."""
+    from scao_amd.engine import PItem
+    items = []
+    for i, shp in enumerate([(512, 512), (256, 1024), (320, 448), (512,), (1024, 256),
+                             (100, 37)]):
+        p = torch.zeros(shp)
+        pre = SparsePreconditioner(p, k_min=128 if i % 2 else 64, k_max=128 if i % 2 else 64,
+                                   max_precond_dim=512, use_int8_ema=True)
+        diag = not (pre.use_block_diagonal or pre.use_kronecker)
+        items.append(PItem(p=p, graw=p, gmom=None, st={}, group={}, pre=pre, phase2=i != 4,
+                           step=3, lars=i % 3 != 0, diag=diag,
+                           leaves=[] if diag else list(pre.leaves())))
+    cache = {}
+
+    def same(a, b):
+        assert set(a[0]) == set(b[0])
+        for k in a[0]:
+            assert a[0][k].tobytes() == b[0][k].tobytes(), k
+        assert a[1:3] == b[1:3]
+        assert [(id(x[0]),) + x[1:] for x in a[3]] == [(id(x[0]),) + x[1:] for x in b[3]]
+
+    for sub in (items, items[1:], items[::2], items):
+        same(E._build_structure(sub), E._build_structure(sub, cache))
+        fresh = E._build_structure(sub)
+        for k, arr in fresh[0].items():
+            rows = sorted(map(tuple, arr.view(np.int32).reshape(-1, 4).tolist()))
+            assert len(rows) == len(set(rows)), k
+    assert cache
+
+
 def test_pipelined_apply_tasks():
     """Wide tasks of blocks with k >= PIPE_MIN_RANK carry variant bit 8 and are
     ordered in runs of APPLY_GROUP tasks of one die's queue."""
