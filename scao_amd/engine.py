@@ -117,6 +117,8 @@ class Workspace:
         self.checked: dict = {}
         # per-parameter shares of the step structure (engine._build_structure)
         self.structures: dict = {}
+        # the last RECENT_STRUCTURES whole structures, most recent last
+        self.recent: dict = {}
         self.struct_key = None
         self.cheap_key = None
         self.leaf_epoch = -1
@@ -129,9 +131,11 @@ class Workspace:
         self.upd_offsets = {}
 
     def invalidate(self) -> None:
-        """Forget the cached step structure (rebuilt on the next step)."""
+        """Forget the cached step structures (rebuilt on the next step)."""
         self.struct_key = None
         self.cheap_key = None
+        self.recent.clear()
+        self.structures.clear()
 
     def buf(self, name: str, nbytes: int) -> Tensor:
         b = self._bufs.get(name)
@@ -343,6 +347,7 @@ def _build_structure(items: list[PItem], cache: dict | None = None):
 XCDS = 8   # MI355X: 8 accelerator dies, workgroup i is dispatched to die i % 8
 PIPE_MIN_RANK = 128   # wide apply tiles of blocks with k >= this use the pipelined kernel
 TALL_PROJECT = True   # projection tasks of 128 rows of T where k % 128 == 0
+RECENT_STRUCTURES = 4   # whole step structures kept on the device (run_step)
 PIPE_STRIP_ORDER = True   # pipelined leaves always take the strip-major (super-tile) order
 L2_OPERANDS = 2 << 20   # bytes of W / U_r rows a die's L2 (4 MB) keeps beside the streams
 
@@ -629,17 +634,26 @@ def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
                      for it in items)
         ws.cheap_key = ckey
     if skey != ws.struct_key:
-        arrays, ranges, nslots, leaves = _build_structure(items, ws.structures)
-        ws.tasks = {k: (L.upload(v, dev) if len(v) else None) for k, v in arrays.items()}
-        ws.ntasks = {k: len(v) for k, v in arrays.items()}
-        ws.slot_ranges, ws.nslots, ws.leaves = ranges, nslots, leaves
-        off = 0
-        ws.upd_offsets = {}
-        for i, it in enumerate(items):
-            if it.phase2 and it.lars:
-                ws.upd_offsets[i] = off
-                off += _align4(it.p.numel())
-        ws.upd_total = off
+        # the last few structures stay on the device (their task lists hold
+        # indices only, and their leaf lists keep the blocks alive, so a key
+        # cannot be reused by other blocks); the block table, which holds
+        # addresses, is rebuilt on every switch
+        ent = ws.recent.pop(skey, None)
+        if ent is None:
+            arrays, ranges, nslots, leaves = _build_structure(items, ws.structures)
+            upd_offsets, off = {}, 0
+            for i, it in enumerate(items):
+                if it.phase2 and it.lars:
+                    upd_offsets[i] = off
+                    off += _align4(it.p.numel())
+            ent = ({k: (L.upload(v, dev) if len(v) else None) for k, v in arrays.items()},
+                   {k: len(v) for k, v in arrays.items()}, ranges, nslots, leaves, upd_offsets,
+                   off)
+        ws.recent[skey] = ent
+        while len(ws.recent) > RECENT_STRUCTURES:
+            ws.recent.pop(next(iter(ws.recent)))
+        (ws.tasks, ws.ntasks, ws.slot_ranges, ws.nslots, ws.leaves, ws.upd_offsets,
+         ws.upd_total) = ent
         ws.struct_key = skey
         ws.leaf_epoch = -1
     if ws.upd_total:
