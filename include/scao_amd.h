@@ -160,6 +160,21 @@ int scao_fused_kronecker_precond(const float* U_l, const float* s_l_inv4, const 
                                  const float* s_r_inv4, const float* G, int64_t ldG, float* out,
                                  int64_t m, int64_t n, int64_t k, void* workspace,
                                  void* stream);
+/* The same operator with no workspace argument and no allocation of any kind.
+ * It has no counterpart in the reference.  It exists for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Its scratch is a static device array of
+ * SCAO_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends, so
+ * k*n + k*k + m*k floats must fit in it (m = n = 4096 at k = 256 does); larger
+ * sizes are rejected with SCAO_ERR_INVALID.  Every call on one GPU shares that
+ * GPU's array: calls on one stream are ordered, but calls that overlap on one
+ * GPU (two streams, two threads) race.  Results are identical to
+ * scao_fused_kronecker_precond's. */
+#define SCAO_NOALLOC_SCRATCH_BYTES (16u << 20)
+int scao_fused_kronecker_precond_noalloc(const float* U_l, const float* s_l_inv4,
+                                         const float* U_r, const float* s_r_inv4,
+                                         const float* G, int64_t ldG, float* out, int64_t m,
+                                         int64_t n, int64_t k, void* stream);
 /* x = fp32(q)*fp32(scale) * fp32(rho) + new_val; scale' = max|x|/127 (double)
  * or 1.0; q' = clamp(rint(x * fp32(1/scale')), +-127).  Updates q in place,
  * writes scale' to *scale_out (device double).  scratch: n floats +

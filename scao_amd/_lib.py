@@ -30,6 +30,7 @@ APPLY_WIDE_ROWS = 16
 APPLY_WIDE_COLS = 256
 APPLY_GROUP = 8
 GRAM_TILE = 128
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 F32, BF16, F16 = 0, 1, 2
 PF_DECAY, PF_LARS, PF_CLIP, PF_GSNR, PF_DIAG, PF_NORM, PF_GF32, PF_ALIGNED = (
@@ -111,6 +112,8 @@ SIGNATURES = {
     "scao_fused_kronecker_workspace": (_I64, [_I64, _I64, _I64]),
     "scao_fused_kronecker_precond": (_I, [_VP, _VP, _VP, _VP, _VP, _I64, _VP, _I64, _I64, _I64,
                                           _VP, _VP]),
+    "scao_fused_kronecker_precond_noalloc": (_I, [_VP, _VP, _VP, _VP, _VP, _I64, _VP, _I64,
+                                                  _I64, _I64, _VP]),
     "scao_int8_ema_scratch_bytes": (_I64, [_I64]),
     "scao_int8_ema_update": (_I, [_VP, _D, _VP, _D, _I64, _VP, _VP, _VP]),
     "scao_kron_project": (_I, [_VP, _I, _VP, _VP, _VP, _I, _VP]),

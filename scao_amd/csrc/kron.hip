@@ -19,6 +19,8 @@
 //   * reduction index: K-step s of a 16-wide chunk uses index
 //     kb + 4*(l/16) + s, so one float4 per lane feeds four K-steps.
 // Both only reorder an exact sum, so they change rounding order, never terms.
+#include <mutex>
+
 #include "scao_common.hpp"
 
 using namespace scao;
@@ -1178,19 +1180,13 @@ extern "C" int64_t scao_fused_kronecker_workspace(int64_t m, int64_t n, int64_t 
   return (k * n + k * k + m * k) * (int64_t)sizeof(float);
 }
 
-extern "C" int scao_fused_kronecker_precond(const float* U_l, const float* s_l_inv4,
-                                            const float* U_r, const float* s_r_inv4,
-                                            const float* G, int64_t ldG, float* out, int64_t m,
-                                            int64_t n, int64_t k, void* workspace,
-                                            void* stream) {
-  SCAO_CHECK_ARG(U_l && s_l_inv4 && U_r && s_r_inv4 && G && out && workspace,
-                 "scao_fused_kronecker_precond: null pointer");
-  SCAO_CHECK_ARG(m > 0 && n > 0 && k > 0 && ldG >= n,
-                 "scao_fused_kronecker_precond: bad shape m=%lld n=%lld k=%lld ldG=%lld",
-                 (long long)m, (long long)n, (long long)k, (long long)ldG);
-  SCAO_CHECK_ARG(m < (1LL << 31) && n < (1LL << 31) && k <= 4096,
-                 "scao_fused_kronecker_precond: dimension too large");
-  float* ws = (float*)workspace;
+namespace {
+
+// The four launches of the reference operator over one block, with the
+// block's T, Delta and W in the k*n + k*k + m*k floats at ws.
+int launch_fused_kronecker(const float* U_l, const float* s_l_inv4, const float* U_r,
+                           const float* s_r_inv4, const float* G, int64_t ldG, float* out,
+                           int64_t m, int64_t n, int64_t k, float* ws, hipStream_t s) {
   scao_leaf_desc L = {};
   L.Ul = U_l;
   L.Ur = U_r;
@@ -1212,7 +1208,6 @@ extern "C" int scao_fused_kronecker_precond(const float* U_l, const float* s_l_i
   P.g = G;
   P.graw = G;
   P.dtype = SCAO_F32;
-  hipStream_t s = (hipStream_t)stream;
   const int strips = (int)((n + SCAO_PROJ_COLS - 1) / SCAO_PROJ_COLS);
   const int kt = (int)((k + 63) / 64);
   hipLaunchKernelGGL(k_project_one, dim3(strips * kt), dim3(256), 0, s, L, P);
@@ -1225,4 +1220,80 @@ extern "C" int scao_fused_kronecker_precond(const float* U_l, const float* s_l_i
                      dim3(256), 0, s, L, G, out);
   SCAO_LAUNCH_CHECK("scao_fused_kronecker_precond/apply");
   return SCAO_OK;
+}
+
+// Scratch of the no-allocation entry point: one copy per GPU, alive until the
+// process ends.  Host code never uses the array's name as an address (on the
+// host it is only a stand-in for the symbol): each device's address comes
+// from hipGetSymbolAddress, fetched once with that device current.
+static __device__ __align__(256) float scratch[SCAO_NOALLOC_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_for_current_device(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    scao_set_error("scao_fused_kronecker_precond_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+    return SCAO_ERR_HIP;
+  }
+  if (dev < 0 || dev >= kMaxDevices) {
+    scao_set_error("scao_fused_kronecker_precond_noalloc: device %d out of range", dev);
+    return SCAO_ERR_INVALID;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      scao_set_error("scao_fused_kronecker_precond_noalloc: hipGetSymbolAddress: %s",
+                     hipGetErrorString(e));
+      return SCAO_ERR_HIP;
+    }
+    g_scratch_ptr[dev] = (float*)p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SCAO_OK;
+}
+
+}  // namespace
+
+#define SCAO_FUSED_ARGS_CHECK(name)                                                          \
+  SCAO_CHECK_ARG(U_l && s_l_inv4 && U_r && s_r_inv4 && G && out, name ": null pointer");   \
+  SCAO_CHECK_ARG(m > 0 && n > 0 && k > 0 && ldG >= n,                                      \
+                 name ": bad shape m=%lld n=%lld k=%lld ldG=%lld", (long long)m,           \
+                 (long long)n, (long long)k, (long long)ldG);                              \
+  SCAO_CHECK_ARG(m < (1LL << 31) && n < (1LL << 31) && k <= 4096, name ": dimension too large")
+
+extern "C" int scao_fused_kronecker_precond(const float* U_l, const float* s_l_inv4,
+                                            const float* U_r, const float* s_r_inv4,
+                                            const float* G, int64_t ldG, float* out, int64_t m,
+                                            int64_t n, int64_t k, void* workspace,
+                                            void* stream) {
+  SCAO_CHECK_ARG(workspace, "scao_fused_kronecker_precond: null pointer");
+  SCAO_FUSED_ARGS_CHECK("scao_fused_kronecker_precond");
+  return launch_fused_kronecker(U_l, s_l_inv4, U_r, s_r_inv4, G, ldG, out, m, n, k,
+                                (float*)workspace, (hipStream_t)stream);
+}
+
+extern "C" int scao_fused_kronecker_precond_noalloc(const float* U_l, const float* s_l_inv4,
+                                                    const float* U_r, const float* s_r_inv4,
+                                                    const float* G, int64_t ldG, float* out,
+                                                    int64_t m, int64_t n, int64_t k,
+                                                    void* stream) {
+  SCAO_FUSED_ARGS_CHECK("scao_fused_kronecker_precond_noalloc");
+  const int64_t need = scao_fused_kronecker_workspace(m, n, k);
+  SCAO_CHECK_ARG(need <= (int64_t)SCAO_NOALLOC_SCRATCH_BYTES,
+                 "scao_fused_kronecker_precond_noalloc: m=%lld n=%lld k=%lld needs %lld bytes "
+                 "of scratch, above the %lld-byte maximum (use scao_fused_kronecker_precond "
+                 "with a workspace)",
+                 (long long)m, (long long)n, (long long)k, (long long)need,
+                 (long long)SCAO_NOALLOC_SCRATCH_BYTES);
+  float* ws = nullptr;
+  const int rc = scratch_for_current_device(&ws);
+  if (rc != SCAO_OK) return rc;
+  return launch_fused_kronecker(U_l, s_l_inv4, U_r, s_r_inv4, G, ldG, out, m, n, k, ws,
+                                (hipStream_t)stream);
 }

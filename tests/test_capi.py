@@ -49,6 +49,12 @@ def test_error_path_without_gpu():
     assert lib.scao_int8_ema_scratch_bytes(5000) == (5000 + 2) * 4
     with pytest.raises(L.ScaoLibError):
         L.call("scao_kron_project", None, -1, None, None, None, 0, None)
+    # the no-allocation operator rejects a block whose scratch exceeds its
+    # static array (8192 x 8192 at k = 256 needs 16.25 MiB) before any launch
+    rc = lib.scao_fused_kronecker_precond_noalloc(16, 16, 16, 16, 16, 8192, 16, 8192, 8192, 256,
+                                                  None)
+    assert rc == 1 and b"maximum" in lib.scao_last_error()
+    assert L.NOALLOC_SCRATCH_BYTES == 16 << 20
 
 
 def test_missing_library_raises(monkeypatch, tmp_path):
