@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define SCAO_ABI_VERSION 7
+#define SCAO_ABI_VERSION 8
 
 enum scao_status { SCAO_OK = 0, SCAO_ERR_INVALID = 1, SCAO_ERR_HIP = 2 };
 enum scao_dtype { SCAO_F32 = 0, SCAO_BF16 = 1, SCAO_F16 = 2 };
@@ -109,11 +109,15 @@ typedef struct scao_leaf_desc {
   int32_t param;            /* index into the scao_param_desc table              */
   int32_t m, n, k;
   int32_t flags;            /* SCAO_LF_*                                         */
-  int32_t pad0;
+  float dbias;              /* SCAO_LF_DIAG: fp32(diagonal EMA bias factor)      */
 } scao_leaf_desc;
 
 #define SCAO_LF_SINV4 1     /* Sl/Sr already hold clamp(S,1e-8)^-1/4             */
 #define SCAO_LF_VEC4  2     /* off, ld, n multiples of 4 and 16-byte aligned     */
+#define SCAO_LF_DIAG  4     /* a diagonal sub-block (1 x n or m x 1 remainder of a
+                               block-diagonal split): Sl is its m*n diag EMA, no
+                               U/S/T/Delta/W, k = 0; it takes delta tasks (its
+                               norm partials) and masked apply tasks only      */
 
 /* A unit of work: (leaf or param, two tile coordinates, reduction slot). */
 typedef struct scao_task {

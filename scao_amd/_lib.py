@@ -21,7 +21,7 @@ import torch  # noqa: F401  -- loads torch's HIP runtime before ours
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("SCAO_AMD_LIB", os.path.join(HERE, "_lib", "libscao_amd.so"))
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 SLOT_WIDTH = 3
 FLAT_CHUNK = 4096
 PROJ_COLS = 256
@@ -37,7 +37,7 @@ PF_DECAY, PF_LARS, PF_CLIP, PF_GSNR, PF_DIAG, PF_NORM, PF_GF32, PF_ALIGNED = (
     1, 2, 4, 8, 16, 32, 64, 128)
 PF_FMASK, PF_FNOISE = 256, 512
 FILTER_THR_WORD = 2 * 2048 + 7
-LF_SINV4, LF_VEC4 = 1, 2
+LF_SINV4, LF_VEC4, LF_DIAG = 1, 2, 4
 
 DTYPE_CODE = {torch.float32: F32, torch.bfloat16: BF16, torch.float16: F16}
 
@@ -58,7 +58,7 @@ PARAM_DESC = np.dtype([
 LEAF_DESC = np.dtype([
     ("Ul", "u8"), ("Ur", "u8"), ("Sl", "u8"), ("Sr", "u8"), ("T", "u8"), ("Delta", "u8"),
     ("W", "u8"), ("off", "i8"), ("ld", "i8"), ("param", "i4"), ("m", "i4"), ("n", "i4"),
-    ("k", "i4"), ("flags", "i4"), ("pad0", "i4"),
+    ("k", "i4"), ("flags", "i4"), ("dbias", "f4"),
 ], align=True)
 
 TASK = np.dtype([("idx", "i4"), ("a", "i4"), ("b", "i4"), ("slot", "i4")], align=True)
@@ -95,7 +95,7 @@ FILTER_COMPACT_WORD = 2 * 2048 + 11   # 1 when the refinement passes read the ca
 FILTER_REGION = 2048                  # candidate slots per chunk (SCAO_FLAT_CHUNK / 2)
 
 STRUCTS = {0: (PARAM_DESC, [n for n in PARAM_DESC.names if n != "pad0"]),
-           1: (LEAF_DESC, [n for n in LEAF_DESC.names if n != "pad0"]),
+           1: (LEAF_DESC, list(LEAF_DESC.names)),
            2: (TASK, list(TASK.names)),
            3: (PARAM_STAT, [n for n in PARAM_STAT.names if n != "pad0"]),
            4: (GRAM_DESC, [n for n in GRAM_DESC.names if n != "pad0"]),

@@ -64,7 +64,7 @@ __device__ __forceinline__ void stage(const scao_gram_desc& D, int dim, int K, i
   }
 }
 
-__global__ __launch_bounds__(256) void k_gram_ema(const scao_task* __restrict__ tasks,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gram_ema(const scao_task* __restrict__ tasks,
                                                   const scao_gram_desc* __restrict__ descs) {
   __shared__ __attribute__((aligned(16))) float As[2][KC][LP];
   __shared__ __attribute__((aligned(16))) float Bs[2][KC][LP];
@@ -79,11 +79,18 @@ __global__ __launch_bounds__(256) void k_gram_ema(const scao_task* __restrict__ 
   const bool vec = ((D.off | D.ld) % 4 == 0) &&
                    (((uintptr_t)D.g & (D.dtype == SCAO_F32 ? 15u : 7u)) == 0);
 
-  v4f acc[4][4];
+  // Two-level sum: the MFMAs accumulate FOLD consecutive K values in acc,
+  // which is then added to tot and cleared.  One fp32 accumulator over all
+  // of K (2048-4096 here, K/4 dependent MFMA adds) drifts by about
+  // sqrt(K/4) ulps, above the reference's own float32 GEMM; two levels of
+  // sqrt(FOLD/4) and sqrt(K/FOLD) bring that under it.  Both sums are exact
+  // sums of the same products, so only rounding changes.
+  constexpr int FOLD = 128;
+  v4f acc[4][4], tot[4][4];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int b = 0; b < 4; ++b) acc[a][b] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int b = 0; b < 4; ++b) acc[a][b] = tot[a][b] = v4f{0.f, 0.f, 0.f, 0.f};
 
   stage(D, dim, K, i0, 0, As[0], vec);
   stage(D, dim, K, j0, 0, Bs[0], vec);
@@ -109,9 +116,18 @@ __global__ __launch_bounds__(256) void k_gram_ema(const scao_task* __restrict__ 
     }
     __syncthreads();
     buf ^= 1;
+    if ((kb + KC) % FOLD == 0 || kb + KC >= K) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          tot[a][b] += acc[a][b];
+          acc[a][b] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+    }
   }
 
-  // EMA epilogue: element (i, j) = acc[a][b][r],
+  // EMA epilogue: element (i, j) = tot[a][b][r],
   // i = i0 + wr + 16a + 4*(l/16) + r, j = j0 + wc + 16b + l%16
   const float sf = D.q ? (float)(*D.scale) : 0.f;
   float amax = 0.f;
@@ -126,7 +142,7 @@ __global__ __launch_bounds__(256) void k_gram_ema(const scao_task* __restrict__ 
         const int j = j0 + wc + 16 * b + (l % 16);
         if (j >= dim) continue;
         const int64_t e = (int64_t)i * dim + j;
-        const float add = D.alpha * acc[a][b][r];
+        const float add = D.alpha * tot[a][b][r];
         if (D.q) {
           const float old = ((float)D.q[e] * sf) * D.rho;
           const float x = old + add;

@@ -307,6 +307,41 @@ __device__ __forceinline__ void delta_tile(const scao_leaf_desc& L, float eps, i
   }
 }
 
+// A diagonal sub-block of a block-diagonal parameter (SCAO_LF_DIAG: a
+// remainder block one row or one column wide, reference
+// preconditioner.py:142-153, 232-236).  Nothing is projected: one 64x64 tile
+// of it contributes ||g||^2, ||p*decay||^2 (LARS params) and the natural-norm
+// sum g^2 / (sqrt(diag) + eps) (:542-544) to the task's slot, in the place
+// the projection and delta tasks of a Kronecker block write them.
+__device__ __forceinline__ void diag_leaf_reduce(const scao_leaf_desc& L,
+                                                 const scao_param_desc& P, int i0, int j0,
+                                                 int slot, double* slots, double* red) {
+  const int dt = P.dtype;
+  const bool decay = P.flags & SCAO_PF_DECAY;
+  const bool lars = P.flags & SCAO_PF_LARS;
+  double acc[3] = {0.0, 0.0, 0.0};
+  for (int q = threadIdx.x; q < 64 * 64; q += 256) {
+    const int i = i0 + q / 64, j = j0 + q % 64;
+    if (i >= L.m || j >= L.n) continue;
+    const int64_t e = L.off + (int64_t)i * L.ld + j;
+    const float g = ld1(P.graw, dt, e);
+    const float dg = gld1(L.Sl + (int64_t)i * L.n + j);
+    acc[0] += (double)(g * g);
+    if (lars) {
+      const float p = ld1(P.p, dt, e);
+      const float pd = decay ? round_to(dt, p * P.decay) : p;
+      acc[1] += (double)(pd * pd);
+    }
+    acc[2] += (double)((g * g) / (sqrtf(dg) + P.eps));
+  }
+  block_sum<3>(acc, red);
+  if (threadIdx.x == 0 && slot >= 0) {
+    slots[(int64_t)slot * SCAO_SLOT_WIDTH + 0] = acc[0];
+    slots[(int64_t)slot * SCAO_SLOT_WIDTH + 1] = acc[1];
+    slots[(int64_t)slot * SCAO_SLOT_WIDTH + 2] = acc[2];
+  }
+}
+
 // -------------------------------------------------------------- lift ---
 // W[i0:i0+64, d0:d0+64] = U_l Delta.  Wave w computes rows i0+16w .. +15.
 // On whole tiles (k % 16 == 0, 16-byte aligned factors) lane column jj holds
@@ -468,14 +503,15 @@ template <bool GF32, bool LARS>
 __device__ __forceinline__ void adan4(const scao_param_desc& P, const scao_param_stat& S, int dt,
                                       const v4f& gr, const v4f& gm, const v4f& corr, v4f& mm,
                                       v4f& vv, v4f& dd, const v4f& pp, const v4f& par, v4f& out,
-                                      float& u2, int cmask) {
+                                      float& u2, int cmask, bool direct = false) {
   const bool clip = P.flags & SCAO_PF_CLIP;
   const bool gsnr = P.flags & SCAO_PF_GSNR;
   const bool decay = P.flags & SCAO_PF_DECAY;
   const float alpha_nolars = round_to(dt, (float)(-P.lr));
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
-    float gp = round_to(dt, gr[t] + corr[t]);           // precondition() output in p.dtype
+    // precondition() output in p.dtype; `direct`: corr already is that output
+    float gp = round_to(dt, direct ? corr[t] : gr[t] + corr[t]);
     if (clip) gp = round_to(dt, gp * S.clip);           // gp * (tau / nu)
     const float g = GF32 ? gm[t] : gr[t];
     const float geff = P.blend * gp + P.omblend * g;    // b*gp.float() + (1-b)*grad
@@ -558,13 +594,30 @@ __device__ __forceinline__ void apply_tile(const scao_leaf_desc& L, const scao_p
     par[r] = (!LARS && rok[r]) ? ld4(P.p, dt, e[r], vec, cmask) : z;
   }
 
-  // 2) corr = W U_r^T
+  // 2) corr = W U_r^T; for a diagonal sub-block the preconditioned gradient
+  //    itself, g / (clamp-free (diag / bias)^(1/4) + 1e-8) (reference
+  //    preconditioner.py:506-510), with diag element (i, j) at i*n + j
   v4f acc[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
+  const bool dleaf = L.flags & SCAO_LF_DIAG;
+  if (dleaf) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if (!rok[r]) continue;
+      const int i = i0 + 16 * w + 4 * kk + r;
+      const v4f dg = ldf4(L.Sl, (int64_t)i * n + jl, false, cmask);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const float x = dg[t] / L.dbias;
+        const float den = (float)pow((double)x, 0.25) + 1e-8f;
+        acc[t][r] = gr[r][t] / den;
+      }
+    }
+  }
   const int irow = i0 + 16 * w + (l % 16);
   const bool kvec = (k % 4) == 0;
-  for (int cb0 = 0; cb0 < k; cb0 += 64) {
+  for (int cb0 = 0; cb0 < (dleaf ? 0 : k); cb0 += 64) {
     if (cb0) __syncthreads();
 #pragma unroll
     for (int h = 0; h < 4; ++h) {
@@ -604,7 +657,7 @@ __device__ __forceinline__ void apply_tile(const scao_leaf_desc& L, const scao_p
     if (GF32 && fused_mgrad(P)) gm[r] = finish_mgrad(P, e[r], gr[r], gm[r], cmask);
     v4f out;
     adan4<GF32, LARS>(P, S, dt, gr[r], gm[r], corr, mm[r], vv[r], dd[r], pp[r], par[r], out, u2,
-                      cmask);
+                      cmask, dleaf);
     stf4(P.exp_avg, e[r], mm[r], vec, cmask);
     stf4(P.exp_avg_sq, e[r], vv[r], vec, cmask);
     stf4(P.exp_avg_diff, e[r], dd[r], vec, cmask);
@@ -1036,6 +1089,10 @@ __global__ __launch_bounds__(256) void k_delta(const scao_task* __restrict__ tas
   const scao_leaf_desc L = leaves[tk.idx];
   __shared__ __attribute__((aligned(16))) float Ps[3][64][DP];
   __shared__ double red[16];
+  if (L.flags & SCAO_LF_DIAG) {
+    diag_leaf_reduce(L, params[L.param], tk.a, tk.b, tk.slot, slots, red);
+    return;
+  }
   const bool fast = (L.flags & SCAO_LF_VEC4) && (L.k % 4 == 0) && tk.a + 64 <= L.k &&
                     tk.b + 64 <= L.k && (L.n % 64 == 0);
   if (fast)

@@ -202,6 +202,11 @@ _TASK_TYPES = (["adam", "delta", "lift", "dred", "dapply", "lars"] +
                [f"proj{v}" for v in range(8)] + [f"apply{v}" for v in range(16)])
 
 
+def _leaf_k(leaf) -> int:
+    """Rank of a step leaf: its eigenfactor width, 0 for a diagonal sub-block."""
+    return leaf.U_l.shape[1] if leaf.use_kronecker else 0
+
+
 def _param_tasks(it: PItem):
     """One parameter's share of a step structure, with local indices: block
     indices from 0 (first block of the parameter), parameter index 0, slots
@@ -231,6 +236,8 @@ def _param_tasks(it: PItem):
     else:
         # projection (chunk 0 owns the norm slots)
         for li, (leaf, r0, c0l) in enumerate(leaves):
+            if not leaf.use_kronecker:
+                continue
             m, n = leaf.m, leaf.n
             k = leaf.U_l.shape[1]
             vec = _leaf_vec(it, leaf, r0, c0l)
@@ -248,6 +255,13 @@ def _param_tasks(it: PItem):
                     else:
                         add(f"proj{var}", (li, j0, c0, -1))
         for li, (leaf, _, _) in enumerate(leaves):
+            if not leaf.use_kronecker:
+                # a diagonal sub-block: its norm partials, 64x64 tiles
+                for a in range(0, leaf.m, 64):
+                    for b in range(0, leaf.n, 64):
+                        add("delta", (li, a, b, slot))
+                        slot += 1
+                continue
             k = leaf.U_l.shape[1]
             for a in range(0, k, 64):
                 for b in range(0, k, 64):
@@ -255,12 +269,13 @@ def _param_tasks(it: PItem):
                     slot += 1
         pre_end = slot
         for li, (leaf, r0, c0l) in enumerate(leaves):
-            k = leaf.U_l.shape[1]
+            k = _leaf_k(leaf)
             for i0 in range(0, leaf.m, 64):
                 for d0 in range(0, k, 64):
                     add("lift", (li, i0, d0, -1))
             var = (1 if it.mgrad else 0) | (2 if it.lars else 0)
-            ok = _leaf_vec(it, leaf, r0, c0l) and it.fp32 and it.aligned and k % 16 == 0
+            ok = (leaf.use_kronecker and _leaf_vec(it, leaf, r0, c0l) and it.fp32 and it.aligned
+                  and k % 16 == 0)
             m, n, T = leaf.m, leaf.n, L.APPLY_TILE
             # wide 16x256 tiles over the interior that they tile exactly,
             # masked 64x64 tiles over the right column strip and the
@@ -292,7 +307,7 @@ def _param_tasks(it: PItem):
 def _item_key(it: PItem) -> tuple:
     """Everything _param_tasks reads from an item."""
     return (id(it.p), it.phase2, it.diag, it.lars, it.mgrad, it.p.numel(), it.fp32, it.aligned,
-            _cols(it.p), tuple((id(lf), r0, c0, lf.U_l.shape[1]) for lf, r0, c0 in it.leaves)
+            _cols(it.p), tuple((id(lf), r0, c0, _leaf_k(lf)) for lf, r0, c0 in it.leaves)
             if it.phase2 and not it.diag else ())
 
 
@@ -435,7 +450,7 @@ def _leaf_table(leaves, items: list[PItem], ws: Workspace):
     """Block descriptors plus T/Delta/W scratch for every Phase-2 block."""
     sizes = []
     for (leaf, r0, c0, pi) in leaves:
-        k = leaf.U_l.shape[1]
+        k = _leaf_k(leaf)
         sizes.append((_align4(k * leaf.n), _align4(k * k), _align4(leaf.m * k)))
     total = sum(a + b + c for a, b, c in sizes)
     scratch = ws.buf("leaf_scratch", max(total, 1) * 4)
@@ -446,15 +461,22 @@ def _leaf_table(leaves, items: list[PItem], ws: Workspace):
         it = items[pi]
         cols = it.graw.shape[-1] if it.graw.ndim == 2 else to_2d(it.graw)[0].shape[1]
         e = tab[i]
+        e["off"] = r0 * cols + c0
+        e["ld"] = cols
+        e["param"] = pi
+        if not leaf.use_kronecker:
+            # diagonal sub-block: its EMA in Sl, the bias factor in dbias
+            e["Sl"] = leaf.diag_ema.data_ptr()
+            e["m"], e["n"], e["k"] = leaf.m, leaf.n, 0
+            e["flags"] = L.LF_DIAG
+            e["dbias"] = getattr(leaf, "_diag_bias_factor", 1.0)
+            continue
         e["Ul"], e["Ur"] = leaf.U_l.data_ptr(), leaf.U_r.data_ptr()
         e["Sl"], e["Sr"] = leaf.S_l.data_ptr(), leaf.S_r.data_ptr()
         e["T"] = base + 4 * off
         e["Delta"] = base + 4 * (off + st)
         e["W"] = base + 4 * (off + st + sd)
         off += st + sd + sw
-        e["off"] = r0 * cols + c0
-        e["ld"] = cols
-        e["param"] = pi
         e["m"], e["n"], e["k"] = leaf.m, leaf.n, leaf.U_l.shape[1]
         vec = _leaf_vec(it, leaf, r0, c0) and _aligned16(int(e["T"]))
         e["flags"] = L.LF_VEC4 if vec else 0
@@ -630,7 +652,7 @@ def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
     if ckey != ws.cheap_key:
         skey = tuple((id(it.p), it.phase2, it.diag, it.lars, it.mgrad, it.p.numel(),
                       it.fp32, it.aligned,
-                      tuple((id(lf), r0, c0, lf.U_l.shape[1]) for lf, r0, c0 in it.leaves))
+                      tuple((id(lf), r0, c0, _leaf_k(lf)) for lf, r0, c0 in it.leaves))
                      for it in items)
         ws.cheap_key = ckey
     if skey != ws.struct_key:
@@ -893,10 +915,16 @@ def sparse_filter(entries) -> list:
 # --------------------------------------------------------------------------
 
 REFRESH_SCRATCH_BYTES = 2 << 30   # fp32 EMA staging per refresh chunk (int8 mode)
+# Optional callable run between a refresh's EMA update and its eigen stage,
+# with the list of (block, gradient, offset, row stride) being refreshed.  Used
+# by the parity tests to check the new EMA and then continue from the CPU
+# reference's own post-EMA state, so the eigen stage and the step that follows
+# are compared from identical inputs.
+AFTER_EMA_HOOK = None
 EIGH_BATCH_BYTES = 1 << 30        # stacked eigh inputs per launch
 
 
-def refresh(entries, eigen_only: bool = False) -> None:
+def refresh(entries, eigen_only: bool = False, ema_only: bool = False) -> None:
     """update_curvature for several preconditioners at once.
 
     ``entries``: list of (SparsePreconditioner, grad tensor).  Follows
@@ -904,7 +932,8 @@ def refresh(entries, eigen_only: bool = False) -> None:
     (Gram on MFMA, int8 requantisation on the device), bias correction,
     Tikhonov shift, eigh, flip/clamp, adaptive rank with rank momentum.
     ``eigen_only`` skips the EMA update (the curvature factors are taken as
-    they are) -- used to check the eigendecomposition stage in isolation."""
+    they are) and ``ema_only`` the eigen stage -- used to check each stage in
+    isolation."""
     if not entries:
         return
     dev = entries[0][1].device
@@ -918,31 +947,24 @@ def refresh(entries, eigen_only: bool = False) -> None:
             g = g.contiguous()
         pre._bump_steps()
         if pre.use_block_diagonal or pre.use_kronecker:
-            cols = to_2d(g)[0].shape[1]
-            for leaf, r0, c0 in pre.leaves():
-                kron.append((leaf, g, r0 * cols + c0, cols))
-            for sub in _diag_subblocks(pre):
-                raise NotImplementedError(
-                    "block-diagonal parameter with a 1-row/1-column remainder block "
-                    f"(shape {tuple(pre.original_shape)}) is not supported by scao_amd")
+            g2 = to_2d(g)[0]
+            cols = g2.shape[1]
+            for leaf, r0, c0 in pre.leaves(diag=True):
+                if leaf.use_kronecker:
+                    kron.append((leaf, g, r0 * cols + c0, cols))
+                else:
+                    # a diagonal sub-block (1-wide remainder): its slice of the
+                    # gradient, gathered contiguous (reference :316-339)
+                    diag.append((leaf, g2[r0:r0 + leaf.m, c0:c0 + leaf.n].contiguous()))
         else:
             diag.append((pre, g))
     s = L.stream_ptr(dev)
     if diag and not eigen_only:
         _refresh_diag(diag, dev, s)
     if kron:
-        _refresh_kron(kron, dev, s, eigen_only)
+        _refresh_kron(kron, dev, s, eigen_only, ema_only)
     for pre, _ in entries:
         pre._sync_k()
-
-
-def _diag_subblocks(pre):
-    if pre.use_block_diagonal:
-        for b in pre._blocks:
-            if not (b.use_block_diagonal or b.use_kronecker):
-                yield b
-            else:
-                yield from _diag_subblocks(b)
 
 
 def _refresh_diag(diag, dev, s):
@@ -963,9 +985,10 @@ def _refresh_diag(diag, dev, s):
     _call("scao_diag_ema", td.data_ptr(), len(tt), pd.data_ptr(), rd.data_ptr(), s)
     for pre, _ in diag:
         pre._diag_bias_factor = max(1.0 - pre.rho ** pre.precond_step, 1e-8)
+        pre._touch()   # a diagonal sub-block's bias factor sits in the block table
 
 
-def _refresh_kron(kron, dev, s, eigen_only=False):
+def _refresh_kron(kron, dev, s, eigen_only=False, ema_only=False):
     # 1) Gram -> EMA (-> requantise), chunked by staging memory
     todo = [] if eigen_only else list(kron)
     while todo:
@@ -978,6 +1001,12 @@ def _refresh_kron(kron, dev, s, eigen_only=False):
             chunk.append(todo.pop(0))
             used += need
         _gram_chunk(chunk, dev, s)
+    if AFTER_EMA_HOOK is not None and not eigen_only:
+        AFTER_EMA_HOOK(kron)
+    if ema_only:
+        for leaf, *_ in kron:
+            leaf._touch()
+        return
     # 2) eigendecomposition inputs, batched by dimension
     jobs = {}   # dim -> list of (leaf, side)
     for leaf, *_ in kron:
@@ -1136,8 +1165,11 @@ def precondition_one(pre: SparsePreconditioner, grad: Tensor) -> Tensor:
     g2 = g2.contiguous()
     if pre.use_block_diagonal or pre.use_kronecker:
         out = torch.zeros_like(g2) if pre.use_block_diagonal else None
-        for leaf, r0, c0 in pre.leaves():
+        for leaf, r0, c0 in pre.leaves(diag=True):
             gb = g2[r0:r0 + leaf.m, c0:c0 + leaf.n]
+            if not leaf.use_kronecker:
+                out[r0:r0 + leaf.m, c0:c0 + leaf.n] = precondition_one(leaf, gb)
+                continue
             from .hip import fused_kronecker_precond
             _, sl = leaf.U_l, leaf.S_l.clamp(min=1e-8).pow(-0.25)
             sr = leaf.S_r.clamp(min=1e-8).pow(-0.25)
@@ -1158,7 +1190,7 @@ def natural_norm_one(pre: SparsePreconditioner, grad: Tensor, eps: float) -> Ten
     g2, _ = to_2d(grad.to(torch.float32))
     if pre.use_block_diagonal:
         parts = []
-        for leaf, r0, c0 in pre.leaves():
+        for leaf, r0, c0 in pre.leaves(diag=True):
             parts.append(natural_norm_one(leaf, g2[r0:r0 + leaf.m, c0:c0 + leaf.n], eps).pow(2))
         return torch.stack(parts).sum().sqrt()
     if not pre.use_kronecker:

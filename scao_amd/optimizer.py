@@ -408,7 +408,7 @@ class SCAO(Optimizer):
         diag = not (pre.use_block_diagonal or pre.use_kronecker)
         it = PItem(p=p, graw=graw, gmom=gmom, st=st, group=group, pre=pre, phase2=True,
                    step=t, scao_step=st["scao_step"], lars=group["lars_coeff"] > 0,
-                   diag=diag, leaves=[] if diag else pre.leaf_list())
+                   diag=diag, leaves=[] if diag else pre.step_leaf_list())
         if filt is not None:
             filtered.append((it, filt, graw))
         return it

@@ -166,20 +166,32 @@ class SparsePreconditioner:
             cached = self.__dict__["_leaves_cache"] = list(self.leaves())
         return cached
 
+    def step_leaf_list(self) -> list:
+        """``list(self.leaves(diag=True))``, kept like ``leaf_list``."""
+        cached = self.__dict__.get("_step_leaves_cache")
+        if cached is None:
+            cached = self.__dict__["_step_leaves_cache"] = list(self.leaves(diag=True))
+        return cached
+
     def __getstate__(self) -> dict:
         state = dict(self.__dict__)
         state.pop("_leaves_cache", None)
+        state.pop("_step_leaves_cache", None)
         return state
 
-    def leaves(self, r0: int = 0, c0: int = 0):
-        """Kronecker blocks as (block, row offset, col offset) in the 2-D view."""
+    def leaves(self, r0: int = 0, c0: int = 0, diag: bool = False):
+        """Kronecker blocks as (block, row offset, col offset) in the 2-D view.
+        With ``diag``, also the diagonal sub-blocks of a block-diagonal split
+        (a remainder one row or one column wide: reference
+        preconditioner.py:142-153 gives it the diagonal mode), in block order."""
         if self.use_block_diagonal:
             off = 0
             for bs, b in zip(self._block_sizes, self._blocks):
-                if self._block_dim == 0:
-                    yield from b.leaves(r0 + off, c0)
-                else:
-                    yield from b.leaves(r0, c0 + off)
+                r, c = (r0 + off, c0) if self._block_dim == 0 else (r0, c0 + off)
+                if b.use_block_diagonal or b.use_kronecker:
+                    yield from b.leaves(r, c, diag)
+                elif diag:
+                    yield b, r, c
                 off += bs
         elif self.use_kronecker:
             yield self, r0, c0

@@ -1,0 +1,152 @@
+"""Elementwise parity gates and shared-state plumbing for the GPU tests.
+
+The north star's bar is stated per element: parameter updates within rtol
+1e-4 in fp32.  An update element that is a small difference of larger terms
+(an Adan step where m and the gradient delta nearly cancel) carries the
+absolute rounding error of its terms, so every gate is |got - want| <=
+atol + rtol * |want| with atol a stated fraction of the largest |want| of
+the tensor.  ``ratio`` is the largest |got - want| / (atol + rtol * |want|)
+over the tensor: <= 1 passes."""
+
+from __future__ import annotations
+
+import json
+import os
+
+import torch
+
+UPDATE_RTOL = 1e-4      # north star: parameter updates within rtol 1e-4 (fp32)
+UPDATE_ATOL = 1e-6      # x max |update| of the tensor
+MOMENT_RTOL = 1e-4
+MOMENT_ATOL = 1e-6      # x max |moment| of the tensor
+
+
+def ulp(x: torch.Tensor) -> torch.Tensor:
+    """Spacing of the float32 grid at |x| (float64 result)."""
+    a = x.detach().float().abs().cpu()
+    return (torch.nextafter(a, torch.full_like(a, float("inf"))) - a).double()
+
+
+def eig_input(leaf) -> torch.Tensor:
+    """The eigh input of a CPU-reference block, in float64 from its own
+    float32 arithmetic (scao/preconditioner.py:381-406): dequantised EMA
+    over the bias factor plus the Tikhonov shift on the diagonal."""
+    import oracle.scao_ref as R
+    out = []
+    bias = max(1.0 - leaf.rho ** leaf.precond_step, 1e-8)
+    for side in ("L", "R"):
+        if leaf.use_int8_ema:
+            X = R.dequantize_sym_int8(getattr(leaf, f"{side}_ema_q"),
+                                      getattr(leaf, f"{side}_ema_scale"))
+        else:
+            X = getattr(leaf, f"{side}_ema")
+        X = X / bias
+        tik = max(1e-8, 1e-4 * X.trace().item() / X.shape[0])
+        X = X.clone()
+        X.diagonal().add_(tik)
+        out.append(X.double())
+    return out
+
+
+def ratio(got, want, rtol, atol_frac, extra=None) -> float:
+    """max |got - want| / (atol_frac * max|want| + rtol * |want| + extra)."""
+    got = got.detach().double().cpu()
+    want = want.detach().double().cpu()
+    if want.numel() == 0:
+        return 0.0
+    atol = atol_frac * want.abs().max().item()
+    bound = atol + rtol * want.abs()
+    if extra is not None:
+        bound = bound + extra
+    err = (got - want).abs()
+    bound = bound.clamp(min=1e-300)
+    return (err / bound).max().item()
+
+
+def assert_close(got, want, rtol, atol_frac, what, extra=None) -> float:
+    r = ratio(got, want, rtol, atol_frac, extra)
+    assert r <= 1.0, f"{what}: worst |err| / (atol + rtol|ref|) = {r:.3g} " \
+                     f"(rtol {rtol:g}, atol {atol_frac:g} x max|ref|)"
+    return r
+
+
+def assert_update_close(p_new, p_new_ref, p_old, what, rtol=UPDATE_RTOL,
+                        atol_frac=UPDATE_ATOL) -> float:
+    """The step's update p_new - p_old against the reference's, element by
+    element.  An update is only observable through the stored parameter,
+    which is rounded to float32 once: where the reference and the kernel
+    round a new value to neighbouring floats, the two updates differ by one
+    float32 spacing of the new parameter whatever their precision (with
+    LARS the step lr * trust * u is often far below that spacing).  So the
+    bound adds ulp(p_new_ref) to atol + rtol * |update|."""
+    p_old = p_old.detach().double().cpu()
+    return assert_close(p_new.detach().double().cpu() - p_old,
+                        p_new_ref.detach().double().cpu() - p_old, rtol, atol_frac, what,
+                        extra=torch.maximum(ulp(p_new_ref), ulp(p_new)))
+
+
+def report(test, case, data):
+    """Append measured errors to $SCAO_REPORT (JSON lines) when set."""
+    path = os.environ.get("SCAO_REPORT")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps({"test": test, "case": case, "data": data}) + "\n")
+
+
+def kron_leaves(pre, r0=0, c0=0):
+    """Kronecker blocks of a CPU-reference preconditioner in block order
+    (reference preconditioner.py:163-194), as (block, row, col)."""
+    if pre.use_block_diagonal:
+        off = 0
+        for bs, blk in zip(pre._block_sizes, pre._blocks):
+            if pre._block_dim == 0:
+                yield from kron_leaves(blk, r0 + off, c0)
+            else:
+                yield from kron_leaves(blk, r0, c0 + off)
+            off += bs
+    elif pre.use_kronecker:
+        yield pre, r0, c0
+
+
+class IdenticalPostEma:
+    """engine.AFTER_EMA_HOOK for one step: checks the GPU's new EMA of every
+    refreshed block against the CPU reference's (int8 codes within 1 LSB,
+    scales within 1e-6 relative; fp32 EMAs within 1e-5 relative), then
+    replaces it by the reference's, so the eigen stage and the update that
+    follow start from identical inputs.  ``pairs``: {id(gpu block): cpu block}."""
+
+    def __init__(self, pairs: dict):
+        self.pairs = pairs
+        self.checked = 0
+        self.max_lsb = 0
+        self.max_scale_rel = 0.0
+
+    def __call__(self, kron):
+        for leaf, *_ in kron:
+            ref = self.pairs[id(leaf)]
+            dev = leaf.device
+            if leaf.use_int8_ema:
+                for side in ("L", "R"):
+                    qg = getattr(leaf, f"{side}_ema_q").cpu().int()
+                    qr = getattr(ref, f"{side}_ema_q").int()
+                    lsb = (qg - qr).abs().max().item()
+                    sg = getattr(leaf, f"{side}_ema_scale")
+                    sr = getattr(ref, f"{side}_ema_scale")
+                    rel = abs(sg - sr) / abs(sr)
+                    self.max_lsb = max(self.max_lsb, lsb)
+                    self.max_scale_rel = max(self.max_scale_rel, rel)
+                    assert lsb <= 1, (side, lsb)
+                    assert rel <= 1e-6, (side, sg, sr)
+                leaf.L_ema_q = ref.L_ema_q.to(dev).contiguous()
+                leaf.R_ema_q = ref.R_ema_q.to(dev).contiguous()
+                leaf._scale = torch.tensor([ref.L_ema_scale, ref.R_ema_scale],
+                                           dtype=torch.float64, device=dev)
+            else:
+                for side in ("L", "R"):
+                    eg = getattr(leaf, f"{side}_ema").cpu().double()
+                    er = getattr(ref, f"{side}_ema").double()
+                    rel = ((eg - er).norm() / er.norm()).item()
+                    assert rel < 1e-5, (side, rel)
+                leaf.L_ema.copy_(ref.L_ema)
+                leaf.R_ema.copy_(ref.R_ema)
+            self.checked += 1

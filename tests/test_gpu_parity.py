@@ -14,7 +14,9 @@ import copy
 import pytest
 import torch
 
+import parity as P
 from oracle import scao_ref as R
+from parity import report
 from scao_inputs import grads_for_step, make_params
 
 pytestmark = pytest.mark.gpu
@@ -26,16 +28,6 @@ def _dev():
     if not torch.cuda.is_available():
         pytest.skip("no ROCm GPU")
     return torch.device("cuda:0")
-
-
-def report(test, case, data):
-    """Append measured errors to $SCAO_REPORT (JSON lines) when set."""
-    import json
-    import os
-    path = os.environ.get("SCAO_REPORT")
-    if path:
-        with open(path, "a") as f:
-            f.write(json.dumps({"test": test, "case": case, "data": data}) + "\n")
 
 
 def _rel(a, b):
@@ -146,6 +138,21 @@ CASES = {
                            use_int8_ema=True, k_min=32, k_max=32, warmup_steps=4,
                            blend_steps=4, precond_freq=3, min_precond_updates=1, tau=1.0,
                            lars_coeff=1e-3), 10),
+    # a block-diagonal split with a remainder one row / one column wide: a
+    # diagonal sub-block (reference preconditioner.py:142-153, 232-236) beside
+    # Kronecker blocks, int8, LARS and clip
+    "diag_remainder": ({"rows": (65, 40), "cols": (40, 65), "b": (40,)},
+                       dict(lr=1e-2, weight_decay=0.01, max_precond_dim=32, rho=0.99,
+                            use_int8_ema=True, k_min=2, k_max=8, warmup_steps=4,
+                            blend_steps=3, precond_freq=3, min_precond_updates=1, tau=1.0,
+                            lars_coeff=1e-3), 10),
+    # the same shapes entering Phase 2 at step 1, before any refresh
+    # (min_precond_updates=0): the sub-block's zero EMA with bias factor 1e-8
+    "diag_remainder_early": ({"rows": (65, 40), "cols": (40, 65)},
+                             dict(lr=1e-2, weight_decay=0.01, max_precond_dim=32, rho=0.99,
+                                  use_int8_ema=False, k_min=4, k_max=4, warmup_steps=0,
+                                  blend_steps=2, precond_freq=3, min_precond_updates=0,
+                                  tau=1.0, lars_coeff=1e-3), 5),
     # k=64 and whole 64x64 / 256-column tiles: the fast (unmasked fp32) kernel paths
     "fast_k64": (FAST, dict(lr=1e-3, weight_decay=0.01, max_precond_dim=512, rho=0.999,
                             use_int8_ema=True, k_min=64, k_max=64, warmup_steps=2,
@@ -198,46 +205,70 @@ def _gpu_from_oracle(ref_opt, ref_params, cfg, dev):
 
 @pytest.mark.parametrize("case", list(CASES))
 def test_step_from_shared_state(case):
+    """Every step of a short run compared on its own: before each step the GPU
+    optimizer loads the CPU reference's state.  Updates and moments are
+    checked element by element at the north star's rtol 1e-4 (atol 1e-6 x
+    the tensor's largest element).  On refresh steps the GPU's new EMA is
+    checked (codes within 1 LSB, scales within 1e-6) and then replaced by the
+    reference's, so the eigen stage and the update start from identical
+    inputs and meet the same bar."""
+    from scao_amd import engine
     dev = _dev()
     shapes, cfg, steps = CASES[case]
     rp = make_params(shapes)
     ref = R.RefSCAO(list(rp.values()), **cfg, **PARITY)
-    worst = {}
+    worst, worst_m, emas = {}, 0.0, 0
     for t in range(1, steps + 1):
         print(f"case={case} step={t}", flush=True)
         gp, gopt = _gpu_from_oracle(ref, rp, cfg, dev)
+        pairs = {}
+        for k in shapes:
+            pa = ref.state[rp[k]].get("preconditioner")
+            if pa is not None:
+                pb = gopt.state[gp[k]]["preconditioner"]
+                for (la, *_), (lb, *_) in zip(P.kron_leaves(pa), pb.leaves()):
+                    pairs[id(lb)] = la
         grads = grads_for_step(t, shapes)
         before = {k: v.detach().clone() for k, v in rp.items()}
         for k in shapes:
             rp[k].grad = grads[k].clone()
             gp[k].grad = grads[k].to(dev)
         ref.step()
-        gopt.step()
+        hook = P.IdenticalPostEma(pairs)
+        engine.AFTER_EMA_HOOK = hook
+        try:
+            gopt.step()
+        finally:
+            engine.AFTER_EMA_HOOK = None
         torch.cuda.synchronize()
+        emas += hook.checked
         refreshed = t % cfg["precond_freq"] == 0
+        # the preconditioner state first: a refresh's eigen stage, compared
+        # from identical inputs, is checked before the update it feeds
+        for (kr, pr), (kg, pg) in zip(ref.state.items(), gopt.state.items()):
+            _cmp_precond(pr["preconditioner"], pg["preconditioner"], t, refreshed)
         for k in shapes:
-            dref = rp[k].detach() - before[k]
-            dgpu = gp[k].detach().cpu() - before[k]
-            r = _rel(dgpu, dref)
+            r = P.assert_update_close(gp[k], rp[k], before[k],
+                                      f"step {t} param {k} update (refresh={refreshed})")
             worst[(k, refreshed)] = max(worst.get((k, refreshed), 0.0), r)
             st_r, st_g = ref.state[rp[k]], gopt.state[gp[k]]
             for key in ("exp_avg", "exp_avg_sq", "exp_avg_diff", "prev_grad"):
-                assert _rel(st_g[key], st_r[key]) < (1e-4 if not refreshed else 2e-3), (t, k, key)
+                worst_m = max(worst_m, P.assert_close(st_g[key], st_r[key], P.MOMENT_RTOL,
+                                                      P.MOMENT_ATOL, f"step {t} {k} {key}"))
             assert st_g["step"] == st_r["step"] and st_g["scao_step"] == st_r["scao_step"]
             assert st_g.get("scao_phase_started") == st_r.get("scao_phase_started")
-            tol = 1e-4 if not refreshed else 2e-3
-            assert r < tol, f"step {t} param {k}: update rel err {r:.3e} (refresh={refreshed})"
         # the oracle's norms are the reference's fp32 CPU reductions; over n
         # squares their rounding walks like sqrt(n / lanes) * eps (1.5e-5 at
         # 2M elements), the kernels add fp32 partials in fp64
         big = max(int(torch.tensor(s).prod()) for s in shapes.values())
         gn_tol = 1e-6 if big <= 1 << 18 else 5e-5
         assert gopt._global_norm_ema == pytest.approx(ref._global_norm_ema, rel=gn_tol)
-        # preconditioner state after refresh: codes within 1 LSB, scales 1e-6
-        for (kr, pr), (kg, pg) in zip(ref.state.items(), gopt.state.items()):
-            _cmp_precond(pr["preconditioner"], pg["preconditioner"], t, refreshed)
     report("step_from_shared_state", case,
-           {f"{k}{'/refresh' if r else ''}": v for (k, r), v in worst.items()})
+           {**{f"{k}{'/refresh' if r else ''}": v for (k, r), v in worst.items()},
+            "moments": worst_m, "emas_checked": emas, "gate": "elementwise ratio <= 1"})
+
+
+_PROJ_ERR = [0.0]
 
 
 def _cmp_precond(a, b, t, refreshed=False):
@@ -258,13 +289,15 @@ def _cmp_precond(a, b, t, refreshed=False):
         else:
             assert _rel(b.L_ema, a.L_ema) < 1e-5 and _rel(b.R_ema, a.R_ema) < 1e-5
         assert b.U_l.shape == a.U_l.shape
-        # eigenvectors up to sign/rotation: compare U diag(S) U^T.  After a
-        # refresh the top-k subspace of a continuous spectrum moves with the
-        # permitted 1-LSB code flips (the eigen stage alone is checked from
-        # identical codes in test_eigen_stage_from_identical_codes).
-        pa = a.U_l @ torch.diag(a.S_l) @ a.U_l.T
-        pb = (b.U_l @ torch.diag(b.S_l) @ b.U_l.T).cpu()
-        assert _rel(pb, pa) < (2e-2 if refreshed else 1e-6), (t, _rel(pb, pa))
+        # eigenvectors up to sign/rotation: compare U diag(S) U^T (after a
+        # refresh, computed by both sides from identical post-EMA codes)
+        for Ua, Sa, Ub, Sb in ((a.U_l, a.S_l, b.U_l, b.S_l), (a.U_r, a.S_r, b.U_r, b.S_r)):
+            torch.testing.assert_close(Sb.cpu(), Sa, rtol=1e-4, atol=1e-9)
+            pa = Ua @ torch.diag(Sa) @ Ua.T
+            pb = (Ub @ torch.diag(Sb) @ Ub.T).cpu()
+            e = _rel(pb, pa)
+            _PROJ_ERR[0] = max(_PROJ_ERR[0], e)
+            assert e < (1e-4 if refreshed else 1e-6), (t, a.m, a.n, e)
     else:
         assert _rel(b.diag_ema, a.diag_ema) < 1e-5
         assert b._diag_bias_factor == pytest.approx(a._diag_bias_factor, rel=1e-12)

@@ -71,6 +71,65 @@ def test_leaves_tile_the_parameter():
         assert (cover == 1).all(), shape
 
 
+@pytest.mark.parametrize("shape,D", [((65, 40), 32), ((40, 65), 32), ((4097, 300), 2048),
+                                     ((300, 2049), 2048), ((65, 65), 32)])
+def test_step_leaves_cover_remainders_of_one(shape, D):
+    """A 1-wide remainder of a block-diagonal split is a diagonal sub-block
+    (reference preconditioner.py:142-153); with diag=True the leaves,
+    Kronecker and diagonal, cover the 2-D view exactly once, and their modes
+    match the oracle's blocks."""
+    pre = SparsePreconditioner(torch.zeros(shape), max_precond_dim=D, use_int8_ema=True)
+    ref = R.RefPreconditioner(torch.zeros(shape), max_precond_dim=D, use_int8_ema=True)
+    cover = np.zeros(shape, dtype=np.int32)
+    ndiag = 0
+    for leaf, r0, c0 in pre.leaves(diag=True):
+        if not leaf.use_kronecker:
+            ndiag += 1
+            assert min(leaf.m, leaf.n) == 1 and tuple(leaf.diag_ema.shape) == (leaf.m, leaf.n)
+        cover[r0:r0 + leaf.m, c0:c0 + leaf.n] += 1
+    assert (cover == 1).all(), shape
+    assert ndiag >= 1
+    assert pre.step_leaf_list() == list(pre.leaves(diag=True))
+    _same_tree(ref, pre)
+
+
+def test_diag_subblock_tasks():
+    """A parameter with a diagonal sub-block: the sub-block takes no projection
+    or lift task, its norm partials come from delta tasks with slots of their
+    own, and masked apply tasks cover it once."""
+    from scao_amd.engine import PItem
+    p = torch.zeros(65, 40)
+    pre = SparsePreconditioner(p, k_min=4, k_max=8, max_precond_dim=32, use_int8_ema=True)
+    it = PItem(p=p, graw=p, gmom=None, st={}, group={}, pre=pre, phase2=True, step=3,
+               lars=True, leaves=pre.step_leaf_list())
+    arrays, ranges, nslots, leaves = E._build_structure([it])
+    dl = [i for i, (lf, *_) in enumerate(leaves) if not lf.use_kronecker]
+    assert len(dl) == 1
+    d = dl[0]
+    for kind in [f"proj{v}" for v in range(8)] + ["lift"]:
+        assert not any(int(t["idx"]) == d for t in arrays[kind]), kind
+    dtasks = [t for t in arrays["delta"] if int(t["idx"]) == d]
+    assert len(dtasks) == 1 and dtasks[0]["slot"] >= 0
+    assert ranges[0][0] <= dtasks[0]["slot"] < ranges[0][1]
+    cover = np.zeros((1, 40), np.int32)
+    for var in range(16):
+        for t in arrays[f"apply{var}"]:
+            if int(t["idx"]) == d:
+                assert not var & 4
+                cover[t["a"]:t["a"] + 64, t["b"]:t["b"] + 64] += 1
+    assert (cover == 1).all()
+    writes = np.zeros(nslots, int)
+    for a in arrays.values():
+        for t in a:
+            if t["slot"] >= 0:
+                writes[t["slot"]] += 1
+    assert (writes == 1).all()
+    tab = E._leaf_table(leaves, [it], E.Workspace(torch.device("cpu")))
+    assert tab[d]["flags"] == L.LF_DIAG and tab[d]["k"] == 0
+    assert tab[d]["Sl"] == leaves[d][0].diag_ema.data_ptr()
+    assert tab[d]["off"] == 64 * 40 and tab[d]["ld"] == 40
+
+
 def test_precond_k_setter_matches_oracle():
     p = torch.zeros(96, 80)
     a = R.RefPreconditioner(p, k_min=4, k_max=32, max_precond_dim=64)

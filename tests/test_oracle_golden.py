@@ -186,3 +186,23 @@ def test_c1_summary():
     b0 = opt.state[p]["preconditioner"]._blocks[0]
     assert (b0.L_ema_q[:32].int() - T["L_q"].int()).abs().max() <= 1
     assert (b0.R_ema_q[:32].int() - T["R_q"].int()).abs().max() <= 1
+
+
+def test_exact_norm_mode():
+    """The reference's float32 CPU norm of a large tensor runs low (its squares
+    stop registering against a large running sum); EXACT_NORMS takes the
+    float64 norm rounded to float32 once.  Pinned against float64 on a
+    tensor the size of a Qwen2.5-3B MLP matrix, and a no-op on small ones."""
+    import oracle.scao_ref as R
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(11008, 2048, generator=g) * 1e-3
+    exact = x.double().norm().item()
+    assert abs(R._norm(x).item() / exact - 1.0) > 1e-3          # float32 CPU: ~0.45% low
+    R.EXACT_NORMS = True
+    try:
+        assert R._norm(x).item() == float(torch.tensor(exact, dtype=torch.float32))
+        small = torch.randn(64, 48, generator=g)
+        assert R._norm(small).item() == small.norm().item() or \
+            abs(R._norm(small).item() / small.norm().item() - 1) < 1e-6
+    finally:
+        R.EXACT_NORMS = False
