@@ -269,6 +269,57 @@ typedef struct scao_prep_desc {
 } scao_prep_desc;
 int scao_eig_prep(const scao_task* tasks, int ntasks, const scao_prep_desc* descs,
                   int ndescs, void* stream);
+/* ---- eigen stage: top-k eigenpairs of a batch of symmetric matrices -----
+ * Replaces the torch.linalg.eigh calls of _update_eigenfactors
+ * (scao/preconditioner.py:413-426), which need every eigenvalue (for
+ * utils.adaptive_rank, scao/utils.py:121-151) but only the top-k_max
+ * eigenvectors.  Two-stage: the dense matrix is reduced to a band of
+ * SCAO_EIG_BAND sub-diagonals by block Householder transformations (panel QR
+ * here, trailing two-sided updates as plain batched GEMMs by the caller),
+ * the band to tridiagonal by bulge chasing, eigenvalues by bisection on the
+ * tridiagonal (float64 Sturm counts), eigenvectors by float64 inverse
+ * iteration on the band matrix, back-transformed by the caller's GEMMs with
+ * the stored block reflectors.  Matrix i of a batch starts at base +
+ * i * stride (elements); every matrix of one call has the same dim n. */
+#define SCAO_EIG_BAND 16
+#define SCAO_EIG_BANDW (2 * SCAO_EIG_BAND + 1)  /* band row pitch: diagonals 0..2b */
+/* Householder QR of the panel A[c0+b:n, c0:c0+b] of every matrix (A row-major,
+ * leading dim n, float32; c0 a multiple of b, c0 + b < n <= 4096 + b),
+ * LAPACK geqr2/larft semantics.  The panel of A is overwritten by the
+ * reflectors V (explicit: unit lower trapezoidal, n-c0-b x b), the upper
+ * triangular factor T (b x b) goes to T + i*b*b and R into the band storage
+ * (rows c0+b.., band + i*bstride, pitch SCAO_EIG_BANDW). */
+int scao_eig_panel_qr(float* A, int64_t stride, int n, int c0, int batch, float* T, float* band,
+                      int64_t bstride, void* stream);
+/* The band matrix: diagonals 0..b of every row, from the final diagonal
+ * blocks of A and the R factors in band, into orig (float32, pitch b+1: kept
+ * for the eigenvector stage) and into band64 (float64, n x SCAO_EIG_BANDW per
+ * matrix, bulge diagonals b+1..2b zeroed: the bulge-chasing work array). */
+int scao_eig_band_finish(const float* A, int64_t stride, int n, int batch, const float* band,
+                         int64_t bstride, float* orig, int64_t ostride, double* band64,
+                         void* stream);
+/* Band -> tridiagonal by bulge chasing in float64 (one wavefront per
+ * matrix) on band64; writes the diagonal d (n) and sub-diagonal e (n-1) at
+ * d + i*n, e + i*n (float64). */
+int scao_eig_sb2st(double* band64, int n, int batch, double* d, double* e, void* stream);
+/* Eigenvalues of the tridiagonals by bisection: the kq largest, descending,
+ * into w + i*kq (float64), and sum over all eigenvalues of max(lambda, 0) into
+ * total[i] (float64: the trace minus the negative eigenvalues).  work:
+ * scao_eig_bisect_work(n, batch) bytes. */
+int64_t scao_eig_bisect_work(int n, int batch);
+int scao_eig_bisect(const double* d, const double* e, int n, int batch, int kq, double* w,
+                    double* total, void* work, void* stream);
+/* Eigenvectors of the band matrices (orig, pitch b+1) for the eigenvalues w
+ * (kq per matrix): float64 inverse iteration with band LU and partial
+ * pivoting (two solves from a pseudo-random start), then Gram-Schmidt inside
+ * clusters of eigenvalues closer than 1e-10 of the largest |B| entry (whose
+ * members get shifts offset by 1e-13 |B| steps).  Output Z (n x kq row-major,
+ * float32) at Z + i*zstride; w is replaced by the vectors' Rayleigh
+ * quotients.  work: scao_eig_vectors_work(n, batch, kq) bytes. */
+int64_t scao_eig_vectors_work(int n, int batch, int kq);
+int scao_eig_vectors(const float* orig, int64_t ostride, int n, int batch, int kq, double* w,
+                     float* Z, int64_t zstride, void* work, void* stream);
+
 /* diag_ema = fp32(diag*rho) + fp32(alpha * g*g)  (1-D preconditioners). */
 int scao_diag_ema(const scao_task* tasks, int ntasks, const scao_param_desc* params,
                   const float* rho_alpha, void* stream);

@@ -31,6 +31,8 @@ APPLY_WIDE_COLS = 256
 APPLY_GROUP = 8
 GRAM_TILE = 128
 NOALLOC_SCRATCH_BYTES = 16 << 20
+EIG_BAND = 16
+EIG_BANDW = 2 * EIG_BAND + 1
 
 F32, BF16, F16 = 0, 1, 2
 PF_DECAY, PF_LARS, PF_CLIP, PF_GSNR, PF_DIAG, PF_NORM, PF_GF32, PF_ALIGNED = (
@@ -130,6 +132,13 @@ SIGNATURES = {
     "scao_eig_prep": (_I, [_VP, _I, _VP, _I, _VP]),
     "scao_diag_ema": (_I, [_VP, _I, _VP, _VP, _VP]),
     "scao_sparse_filter": (_I, [_VP, _I, _VP, _I, _VP]),
+    "scao_eig_panel_qr": (_I, [_VP, _I64, _I, _I, _I, _VP, _VP, _I64, _VP]),
+    "scao_eig_band_finish": (_I, [_VP, _I64, _I, _I, _VP, _I64, _VP, _I64, _VP, _VP]),
+    "scao_eig_sb2st": (_I, [_VP, _I, _I, _VP, _VP, _VP]),
+    "scao_eig_bisect_work": (_I64, [_I, _I]),
+    "scao_eig_bisect": (_I, [_VP, _VP, _I, _I, _I, _VP, _VP, _VP, _VP]),
+    "scao_eig_vectors_work": (_I64, [_I, _I, _I]),
+    "scao_eig_vectors": (_I, [_VP, _I64, _I, _I, _I, _VP, _VP, _I64, _VP, _VP]),
     "scao_lookahead": (_I, [_VP, _I, _VP, ctypes.c_float, _VP]),
 }
 

@@ -1,0 +1,851 @@
+// Eigen stage of the curvature refresh on gfx950: the top-k eigenpairs (and
+// the sum of the clamped spectrum) of a batch of symmetric fp32 matrices --
+// what scao/preconditioner.py:413-451 obtains from torch.linalg.eigh, whose
+// LAPACK/rocSOLVER drivers tridiagonalise with Householder matrix-vector
+// products (one pass over the trailing matrix per column).  Here:
+//
+//   1. dense -> band (SCAO_EIG_BAND = b sub-diagonals): per panel of b
+//      columns a Householder QR (k_panel_qr, one workgroup per matrix, the
+//      panel in registers); the two-sided trailing update is two plain batched
+//      GEMMs issued by the caller (scao_amd/eigen.py);
+//   2. band -> tridiagonal by bulge chasing (k_sb2st): sweep s annihilates
+//      column s below the sub-diagonal with a reflector of length b and
+//      chases the bulge it creates down the band, one task per b-row block;
+//      a task touches only its own b rows of band storage (diagonals 0..2b);
+//   3. eigenvalues of the tridiagonal by bisection with float64 Sturm counts
+//      (k_bisect): the kq largest, and every negative one so that the sum of
+//      the clamped spectrum is exact (trace minus the negatives);
+//   4. eigenvectors by float64 inverse iteration on the band matrix itself
+//      (k_inviter: band LU with partial pivoting in a sliding 17 x 33 window,
+//      one wavefront per vector), two solves with a Rayleigh-quotient shift in
+//      between, then Gram-Schmidt inside clusters of (nearly) equal
+//      eigenvalues (k_cluster_orth);
+//   5. back-transformation with the stage-1 block reflectors: caller GEMMs.
+//
+// The tridiagonal's reflectors are never stored: the vectors come from the
+// band matrix, so only stage 1's reflectors (kept in the panels of A) are
+// applied to them.
+#include "scao_common.hpp"
+
+using namespace scao;
+
+namespace {
+
+constexpr int NB = SCAO_EIG_BAND;    // 16
+constexpr int BW = SCAO_EIG_BANDW;   // 33: band row pitch (diagonals 0..2b)
+constexpr int OW = NB + 1;           // 17: pitch of the original band copy
+
+// ------------------------------------------------------------ panel QR ---
+// Block reduction of NV floats over a 1024-thread workgroup: every thread
+// receives the NV sums in out[] (LDS).
+template <int NV>
+__device__ __forceinline__ void block_sum_f(float (&x)[NV], float (*red)[NV + 1], float* out) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) {
+    float y = x[v];
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) y += __shfl_xor(y, o);
+    x[v] = y;
+  }
+  if (lane == 0)
+#pragma unroll
+    for (int v = 0; v < NV; ++v) red[wid][v] = x[v];
+  __syncthreads();
+  if (threadIdx.x < NV) {
+    float s = 0.f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) s += red[w][threadIdx.x];
+    out[threadIdx.x] = s;
+  }
+  __syncthreads();
+}
+
+// Householder QR of the panel A[r0:n, c0:c0+NB], r0 = c0 + NB, m = n - r0
+// rows (LAPACK geqr2 + larft, forward columnwise).  Thread t holds rows
+// t + 1024 h (h < RPT) of the panel.  Outputs: V (explicit, unit lower
+// trapezoidal) over the panel of A, T (NB x NB upper), R into the band.
+template <int RPT>
+__global__ __launch_bounds__(1024) void k_panel_qr(float* A, int64_t stride, int n, int c0,
+                                                   float* Tout, float* band, int64_t bstride) {
+  __shared__ float red[16][NB + 1];
+  __shared__ float bc[NB + 2];
+  __shared__ float Ts[NB][NB];
+  __shared__ float betas[NB];
+  const int tid = threadIdx.x;
+  float* Am = A + (int64_t)blockIdx.x * stride;
+  const int r0 = c0 + NB, m = n - r0;
+  const int kk = m < NB ? m : NB;
+  float P[RPT][NB];
+#pragma unroll
+  for (int h = 0; h < RPT; ++h) {
+    const int row = tid + 1024 * h;
+#pragma unroll
+    for (int c = 0; c < NB; ++c)
+      P[h][c] = row < m ? Am[(int64_t)(r0 + row) * n + c0 + c] : 0.f;
+  }
+  if (tid < NB * NB) Ts[tid / NB][tid % NB] = 0.f;
+  __syncthreads();
+  for (int j = 0; j < kk; ++j) {
+    // alpha = P[row j][j] (thread j, h = 0); sigma^2 over rows below j
+    if (tid == j) bc[NB] = P[0][j];
+    float s2[1] = {0.f};
+#pragma unroll
+    for (int h = 0; h < RPT; ++h) {
+      const int row = tid + 1024 * h;
+      if (row > j && row < m) s2[0] = fmaf(P[h][j], P[h][j], s2[0]);
+    }
+    block_sum_f<1>(s2, (float(*)[2])red, bc + NB + 1);
+    const float alpha = bc[NB], sig2 = bc[NB + 1];
+    float tau = 0.f, beta = alpha, scale = 0.f;
+    if (sig2 > 0.f) {
+      beta = -copysignf(sqrtf(alpha * alpha + sig2), alpha);
+      tau = (beta - alpha) / beta;
+      scale = 1.f / (alpha - beta);
+    }
+    // v (rows > j) replaces column j; dots with the other columns:
+    // c > j: w_c = v^T P[:, c];  c < j: d_c = V_c^T v
+    float acc[NB];
+#pragma unroll
+    for (int c = 0; c < NB; ++c) acc[c] = 0.f;
+#pragma unroll
+    for (int h = 0; h < RPT; ++h) {
+      const int row = tid + 1024 * h;
+      if (row >= j && row < m) {
+        float v = 1.f;
+        if (row > j) {
+          v = P[h][j] * scale;
+          P[h][j] = v;
+        }
+#pragma unroll
+        for (int c = 0; c < NB; ++c)
+          if (c != j) acc[c] = fmaf(v, P[h][c], acc[c]);
+      }
+    }
+    block_sum_f<NB>(acc, red, bc);
+#pragma unroll
+    for (int h = 0; h < RPT; ++h) {
+      const int row = tid + 1024 * h;
+      if (row >= j && row < m) {
+        const float v = row > j ? P[h][j] : 1.f;
+#pragma unroll
+        for (int c = 0; c < NB; ++c)
+          if (c > j) P[h][c] = fmaf(-tau * v, bc[c], P[h][c]);
+      }
+    }
+    if (tid == 0) {
+      // T[0:j, j] = T[0:j, 0:j] (-tau d[0:j]);  T[j][j] = tau
+      for (int i = 0; i < j; ++i) {
+        float s = 0.f;
+        for (int l = i; l < j; ++l) s = fmaf(Ts[i][l], bc[l], s);
+        Ts[i][j] = -tau * s;
+      }
+      Ts[j][j] = tau;
+      betas[j] = beta;
+    }
+    __syncthreads();
+  }
+  // outputs
+  float* Tm = Tout + (int64_t)blockIdx.x * NB * NB;
+  if (tid < NB * NB) Tm[tid] = Ts[tid / NB][tid % NB];
+  float* Bm = band + (int64_t)blockIdx.x * bstride;
+#pragma unroll
+  for (int h = 0; h < RPT; ++h) {
+    const int row = tid + 1024 * h;
+    if (row >= m) continue;
+    float* arow = Am + (int64_t)(r0 + row) * n + c0;
+#pragma unroll
+    for (int c = 0; c < NB; ++c) arow[c] = row > c ? (c < kk ? P[h][c] : 0.f) : (row == c ? (c < kk ? 1.f : 0.f) : 0.f);
+    if (row < NB) {
+      // R row `row`: columns c >= row, band diagonal d = NB + row - c
+      float* brow = Bm + (int64_t)(r0 + row) * BW;
+#pragma unroll
+      for (int c = 0; c < NB; ++c)
+        if (c >= row) brow[NB + row - c] = c == row ? (row < kk ? betas[row] : P[h][c]) : P[h][c];
+    }
+  }
+}
+
+// ---------------------------------------------------------- band finish ---
+// Row i: diagonals 0..i-bs from the final diagonal block of A (bs = start of
+// i's NB-row block), diagonals above that up to NB were written by the panel
+// QR (R), or are left of column 0 (first block: zero); bulge diagonals
+// NB+1..2NB zero.  orig keeps diagonals 0..NB.
+__global__ __launch_bounds__(256) void k_band_finish(const float* A, int64_t stride, int n,
+                                                     const float* band, int64_t bstride,
+                                                     float* orig, int64_t ostride, double* band64) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const int mat = blockIdx.y;
+  const float* Am = A + (int64_t)mat * stride;
+  const float* brow = band + (int64_t)mat * bstride + (int64_t)i * BW;
+  float* orow = orig + (int64_t)mat * ostride + (int64_t)i * OW;
+  double* wrow = band64 + (int64_t)mat * n * BW + (int64_t)i * BW;
+  const int bs = (i / NB) * NB;
+  for (int d = 0; d <= NB; ++d) {
+    float v;
+    if (d <= i - bs)
+      v = Am[(int64_t)i * n + (i - d)];
+    else if (bs == 0)
+      v = 0.f;
+    else
+      v = brow[d];
+    orow[d] = v;
+    wrow[d] = (double)v;
+  }
+  for (int d = NB + 1; d < BW; ++d) wrow[d] = 0.0;
+}
+
+// --------------------------------------------------------------- sb2st ---
+// Bulge chasing in float64, one workgroup of SB_W wavefronts per matrix.
+// Task k of sweep s owns band rows q0..q0+LM-1 (q0 = s + 1 + 16k): the block
+// E = B[rows, previous block's rows] (for task 0 the single column s) and the
+// diagonal block D.  E gets the previous reflector from the right, a new
+// reflector annihilates E's first column below its first row and is applied
+// to E from the left and to D from both sides.  A task touches only its own
+// rows, so:
+//   * wavefront w runs sweeps w, w + SB_W, ...; sweep s may run task k once
+//     sweep s-1 has finished task k+2 (their rows overlap up to there), and
+//     each wavefront publishes its progress (s * 65536 + tasks done) in LDS;
+//   * the rows of task k+1 are loaded while task k computes (they need sweep
+//     s-1 to have finished task k+3, which it almost always has).
+constexpr int SB_W = 4;
+constexpr int SB_BIG = 1 << 16;
+
+struct Sb2stLds {
+  double E[NB][NB + 1];
+  double D[NB][NB + 1];
+  double v[NB];
+  double y[NB];
+  double pv[NB];
+};
+
+__device__ __forceinline__ double sum4(double x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  return x;
+}
+__device__ __forceinline__ double sum16(double x) {
+  x += __shfl_xor(x, 1);
+  x += __shfl_xor(x, 2);
+  x += __shfl_xor(x, 4);
+  x += __shfl_xor(x, 8);
+  return x;
+}
+// LDS traffic of one wavefront is ordered; this keeps the compiler from
+// moving its accesses across the point.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+__device__ __forceinline__ int sb_ntasks(int n, int s) { return (n - 1 - s + NB - 1) / NB; }
+
+// Wait until the wavefront running sweep s-1 has finished `tasks` of its tasks.
+__device__ __forceinline__ void sb_wait(volatile int* prog, int s, int tasks) {
+  if (s == 0) return;
+  const int w = (s - 1) % SB_W;
+  const int target = (s - 1) * SB_BIG + tasks;
+  while (__hip_atomic_load(&prog[w], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target)
+    __builtin_amdgcn_s_sleep(1);
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+__global__ __launch_bounds__(SB_W * 64) void k_sb2st(double* band, int n, double* dout,
+                                                     double* eout) {
+  __shared__ Sb2stLds Sall[SB_W];
+  __shared__ int prog[SB_W];
+  const int wid = threadIdx.x >> 6, l = threadIdx.x & 63;
+  Sb2stLds& S = Sall[wid];
+  double* Bm = band + (int64_t)blockIdx.x * n * BW;
+  if (l == 0) prog[wid] = -SB_BIG;
+  __syncthreads();
+  const int r = l >> 2, q = l & 3;   // (row or column, quarter) lane roles
+  for (int s = wid; s + 2 < n; s += SB_W) {
+    const int nt = sb_ntasks(n, s);
+    const int ntp = s > 0 ? sb_ntasks(n, s - 1) : 0;
+    double cur[8], nxt[8];
+    // rows of task 0
+    sb_wait(prog, s, min(3, ntp));
+    {
+      const int q0 = s + 1, LM = min(NB, n - q0);
+      for (int t = 0; t < 8; ++t) {
+        const int idx = l + 64 * t, row = idx >> 5, d = idx & 31;
+        cur[t] = row < LM ? Bm[(int64_t)(q0 + row) * BW + d] : 0.0;
+      }
+    }
+    int q0 = s + 1, LN = 1;          // task 0: E is column s (one column)
+    double ptau = 0.0;               // previous reflector (none for task 0)
+    for (int k = 0; k < nt; ++k) {
+      const int LM = min(NB, n - q0);
+      // scatter this task's rows into E / D
+      for (int t = 0; t < 8; ++t) {
+        const int idx = l + 64 * t, row = idx >> 5, d = idx & 31;
+        if (row < LM) {
+          if (d <= row) {
+            S.D[row][row - d] = cur[t];
+            S.D[row - d][row] = cur[t];
+          } else if (d <= row + LN) {
+            S.E[row][LN + row - d] = cur[t];
+          }
+        }
+      }
+      // prefetch the next task's rows
+      if (k + 1 < nt) {
+        sb_wait(prog, s, min(k + 4, ntp));
+        const int q1 = q0 + LM, LM1 = min(NB, n - q1);
+        for (int t = 0; t < 8; ++t) {
+          const int idx = l + 64 * t, row = idx >> 5, d = idx & 31;
+          nxt[t] = row < LM1 ? Bm[(int64_t)(q1 + row) * BW + d] : 0.0;
+        }
+      }
+      wave_sync();
+      // 1. E <- E (I - ptau pv pv^T)
+      if (ptau != 0.0) {
+        double t = 0.0;
+        if (r < LM)
+          for (int c = 4 * q; c < 4 * q + 4; ++c)
+            if (c < LN) t = fma(S.E[r][c], S.pv[c], t);
+        t = sum4(t);
+        wave_sync();
+        if (r < LM)
+          for (int c = 4 * q; c < 4 * q + 4; ++c)
+            if (c < LN) S.E[r][c] = fma(-ptau * t, S.pv[c], S.E[r][c]);
+        wave_sync();
+      }
+      // 2. reflector from E[:, 0] (length LM)
+      const int rr = l & 15;
+      const double x0 = rr < LM ? S.E[rr][0] : 0.0;
+      const double alpha = S.E[0][0];
+      const double s2 = sum16(rr >= 1 ? x0 * x0 : 0.0);
+      double tau = 0.0, beta = alpha, scale = 0.0;
+      if (s2 > 0.0) {
+        beta = -copysign(sqrt(alpha * alpha + s2), alpha);
+        tau = (beta - alpha) / beta;
+        scale = 1.0 / (alpha - beta);
+      }
+      wave_sync();
+      if (l < NB) {
+        S.v[l] = l == 0 ? 1.0 : (l < LM ? x0 * scale : 0.0);
+        if (l < LM) S.E[l][0] = l == 0 ? beta : 0.0;
+      }
+      wave_sync();
+      if (tau != 0.0) {
+        // 3. E[:, 1:] <- (I - tau v v^T) E[:, 1:]   (lane: column r, rows 4q..4q+3)
+        double w = 0.0;
+        if (r >= 1 && r < LN)
+          for (int i = 4 * q; i < 4 * q + 4; ++i)
+            if (i < LM) w = fma(S.v[i], S.E[i][r], w);
+        w = sum4(w);
+        wave_sync();
+        if (r >= 1 && r < LN)
+          for (int i = 4 * q; i < 4 * q + 4; ++i)
+            if (i < LM) S.E[i][r] = fma(-tau * S.v[i], w, S.E[i][r]);
+        // 4. D <- H D H: y = tau D v; y -= (tau/2)(y^T v) v; D -= v y^T + y v^T
+        double y = 0.0;
+        if (r < LM)
+          for (int c = 4 * q; c < 4 * q + 4; ++c)
+            if (c < LM) y = fma(S.D[r][c], S.v[c], y);
+        y = tau * sum4(y);
+        double a = (q == 0 && r < LM) ? y * S.v[r] : 0.0;
+        a += __shfl_xor(a, 4);
+        a += __shfl_xor(a, 8);
+        a += __shfl_xor(a, 16);
+        a += __shfl_xor(a, 32);
+        a *= 0.5 * tau;
+        if (q == 0 && r < LM) S.y[r] = fma(-a, S.v[r], y);
+        wave_sync();
+        if (r < LM)
+          for (int c = 4 * q; c < 4 * q + 4; ++c)
+            if (c < LM) S.D[r][c] = S.D[r][c] - (S.v[r] * S.y[c] + S.y[r] * S.v[c]);
+        wave_sync();
+      }
+      // store the rows back, then publish the task
+      for (int t = 0; t < 8; ++t) {
+        const int idx = l + 64 * t, row = idx >> 5, d = idx & 31;
+        if (row < LM) {
+          if (d <= row)
+            Bm[(int64_t)(q0 + row) * BW + d] = S.D[row][row - d];
+          else if (d <= row + LN)
+            Bm[(int64_t)(q0 + row) * BW + d] = S.E[row][LN + row - d];
+        }
+      }
+      if (l < NB) S.pv[l] = S.v[l];
+      ptau = tau;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      if (l == 0)
+        __hip_atomic_store(&prog[wid], s * SB_BIG + k + 1, __ATOMIC_RELEASE,
+                           __HIP_MEMORY_SCOPE_WORKGROUP);
+      wave_sync();
+      q0 += LM;
+      LN = LM;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) cur[t] = nxt[t];
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  for (int i = threadIdx.x; i < n; i += SB_W * 64) {
+    dout[(int64_t)blockIdx.x * n + i] = Bm[(int64_t)i * BW];
+    if (i + 1 < n) eout[(int64_t)blockIdx.x * n + i] = Bm[(int64_t)(i + 1) * BW + 1];
+  }
+}
+
+// ------------------------------------------------------------- bisection ---
+// Sturm count of T - x: the number of eigenvalues below x (float64, with
+// LAPACK's pivmin guard against a zero pivot).
+__device__ __forceinline__ int sturm(const double* d, const double* e, int n, double x,
+                                     double pivmin) {
+  int c = 0;
+  double qv = d[0] - x;
+  if (fabs(qv) < pivmin) qv = -pivmin;
+  c += qv < 0.0;
+  for (int i = 1; i < n; ++i) {
+    const double ee = e[i - 1];
+    qv = (d[i] - x) - ee * ee / qv;
+    if (fabs(qv) < pivmin) qv = -pivmin;
+    c += qv < 0.0;
+  }
+  return c;
+}
+
+// Per matrix: Gershgorin bounds, pivmin, the trace (float64), the number of
+// negative eigenvalues.  info = {lo, hi, pivmin, trace}, nneg.
+__global__ __launch_bounds__(256) void k_tri_info(const double* d, const double* e, int n,
+                                                  double* info, int* nneg) {
+  __shared__ double red[16];
+  const int mat = blockIdx.x;
+  const double* dm = d + (int64_t)mat * n;
+  const double* em = e + (int64_t)mat * n;
+  double lo = 1e300, hi = -1e300, tr = 0.0, e2max = 0.0;
+  for (int i = threadIdx.x; i < n; i += 256) {
+    const double r = (i > 0 ? fabs(em[i - 1]) : 0.0) + (i + 1 < n ? fabs(em[i]) : 0.0);
+    lo = fmin(lo, dm[i] - r);
+    hi = fmax(hi, dm[i] + r);
+    tr += dm[i];
+    if (i + 1 < n) e2max = fmax(e2max, em[i] * em[i]);
+  }
+  double x[2] = {tr, 0.0};
+  block_sum<2>(x, red);
+  // min / max / max through the same LDS, one at a time
+  __shared__ double mm[3][256];
+  mm[0][threadIdx.x] = lo;
+  mm[1][threadIdx.x] = hi;
+  mm[2][threadIdx.x] = e2max;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int t = 1; t < 256; ++t) {
+      lo = fmin(lo, mm[0][t]);
+      hi = fmax(hi, mm[1][t]);
+      e2max = fmax(e2max, mm[2][t]);
+    }
+    const double tnorm = fmax(fabs(lo), fabs(hi));
+    const double pivmin = 2.2250738585072014e-308 * fmax(1.0, e2max);
+    // widen the interval so bisection brackets every eigenvalue
+    const double pad = 2.0 * 2.220446049250313e-16 * tnorm * n + 2.0 * pivmin;
+    info[4 * mat + 0] = lo - pad;
+    info[4 * mat + 1] = hi + pad;
+    info[4 * mat + 2] = pivmin;
+    info[4 * mat + 3] = x[0];
+    nneg[mat] = sturm(dm, em, n, 0.0, pivmin);
+  }
+}
+
+// One thread per (matrix, eigenvalue index); index j (0-based, ascending) is
+// computed when j >= n - kq (the kq largest) or j < nneg (negative).
+__global__ __launch_bounds__(256) void k_bisect(const double* d, const double* e, int n, int kq,
+                                                const double* info, const int* nneg,
+                                                double* wall) {
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  const int mat = blockIdx.y;
+  if (j >= n) return;
+  const int neg = nneg[mat];
+  if (!(j >= n - kq || j < neg)) return;
+  const double* dm = d + (int64_t)mat * n;
+  const double* em = e + (int64_t)mat * n;
+  double lo = info[4 * mat + 0], hi = info[4 * mat + 1];
+  const double pivmin = info[4 * mat + 2];
+  for (int it = 0; it < 80; ++it) {
+    const double mid = 0.5 * (lo + hi);
+    if (hi - lo <= 2.0 * 2.220446049250313e-16 * fmax(fabs(lo), fabs(hi)) + pivmin) break;
+    if (sturm(dm, em, n, mid, pivmin) > j)
+      hi = mid;
+    else
+      lo = mid;
+  }
+  wall[(int64_t)mat * n + j] = 0.5 * (lo + hi);
+}
+
+// The kq largest, descending, and total = trace - sum of the negative ones
+// (summed in ascending order, fixed), i.e. the sum of the clamped spectrum.
+__global__ __launch_bounds__(64) void k_bisect_finish(const double* wall, int n, int kq,
+                                                      const double* info, const int* nneg,
+                                                      double* w, double* total) {
+  const int mat = blockIdx.x;
+  const double* wm = wall + (int64_t)mat * n;
+  for (int i = threadIdx.x; i < kq; i += 64) w[(int64_t)mat * kq + i] = wm[n - 1 - i];
+  if (threadIdx.x == 0) {
+    double s = 0.0;
+    const int neg = nneg[mat];
+    for (int j = 0; j < neg; ++j) s += wm[j];
+    total[mat] = info[4 * mat + 3] - s;
+  }
+}
+
+// ------------------------------------------------------ inverse iteration ---
+constexpr int WC = 2 * NB + 1;   // 33 window columns
+constexpr int WR = NB + 1;       // 17 window rows
+
+// B[i][c] - (i == c) * sigma for the band matrix (orig: diagonals 0..NB of the
+// lower band, row pitch OW), zero outside the band or the matrix.
+__device__ __forceinline__ double mval(const float* orig, int n, int i, int c, double sigma) {
+  if (i < 0 || c < 0 || i >= n || c >= n) return 0.0;
+  const int dd = i - c;
+  if (dd > NB || dd < -NB) return 0.0;
+  double v = dd >= 0 ? (double)orig[(int64_t)i * OW + dd] : (double)orig[(int64_t)c * OW - dd];
+  if (dd == 0) v -= sigma;
+  return v;
+}
+
+__device__ __forceinline__ double wave_sum_d(double x) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
+__device__ __forceinline__ double readlane_d(double x, int lane) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, x);
+  const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)u, lane);
+  const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(u >> 32), lane);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// Deterministic start vector: a hash of (vector, row) mapped to [-1, 1].
+__device__ __forceinline__ double start_val(uint32_t vid, int row) {
+  uint32_t h = vid * 0x9E3779B9u ^ (uint32_t)row * 0x85EBCA6Bu;
+  h ^= h >> 16;
+  h *= 0x7FEB352Du;
+  h ^= h >> 15;
+  h *= 0x846CA68Bu;
+  h ^= h >> 16;
+  return (double)(h & 0xFFFFFF) / 8388608.0 - 1.0;
+}
+
+// Solve (B - sigma I) x = rhs with band LU and partial pivoting; rhs given by
+// `rhs` (NULL: start_val).  U rows (WC doubles each) and the transformed rhs
+// go to work; x (float64, normalised) to xout.  One wavefront; lanes 0..32
+// each own one window column (lane L holds column j + ((L - j) mod 33) at
+// step j), every lane holds all 17 row slots of its column.
+__device__ void band_solve(const float* orig, int n, double sigma, double bnorm, uint32_t vid,
+                           const double* rhs, double* U, double* ys, double* xout) {
+  const int L = threadIdx.x & 63;
+  const bool act = L < WC;
+  double W[WR], y[WR];
+  // initial window: rows 0..16, columns 0..32 (lane L <-> column L)
+#pragma unroll
+  for (int s = 0; s < WR; ++s) {
+    W[s] = act ? mval(orig, n, s, L, sigma) : 0.0;
+    y[s] = s < n ? (rhs ? rhs[s] : start_val(vid, s)) : 0.0;
+  }
+  const double tiny = 2.220446049250313e-16 * bnorm + 1e-300;
+  for (int j = 0; j < n; ++j) {
+    const int lj = j % WC;
+    double col[WR];
+#pragma unroll
+    for (int s = 0; s < WR; ++s) col[s] = readlane_d(W[s], lj);
+    int p = 0;
+    double best = fabs(col[0]);
+#pragma unroll
+    for (int s = 1; s < WR; ++s)
+      if (fabs(col[s]) > best) {
+        best = fabs(col[s]);
+        p = s;
+      }
+    p = __builtin_amdgcn_readfirstlane(p);
+#pragma unroll
+    for (int s = 1; s < WR; ++s)
+      if (p == s) {
+        double t = W[0]; W[0] = W[s]; W[s] = t;
+        t = y[0]; y[0] = y[s]; y[s] = t;
+        t = col[0]; col[0] = col[s]; col[s] = t;
+      }
+    double piv = col[0];
+    if (fabs(piv) < tiny) piv = piv < 0.0 ? -tiny : tiny;
+    const double inv = 1.0 / piv;
+#pragma unroll
+    for (int s = 1; s < WR; ++s) {
+      const double lm = col[s] * inv;
+      W[s] = fma(-lm, W[0], W[s]);
+      y[s] = fma(-lm, y[0], y[s]);
+    }
+    // retire the pivot row as U row j (column offset of this lane)
+    const int off = (L - lj + WC) % WC;
+    double w0 = W[0];
+    if (L == lj) w0 = piv;
+    if (act) U[(int64_t)j * WC + off] = w0;
+    if (L == 0) ys[j] = y[0];
+    // row j + 17 enters slot 0; lane lj's column becomes j + 33
+    const int i = j + WR;
+    const int colL = j + 1 + ((L - (lj + 1)) % WC + WC) % WC;
+    W[0] = act ? mval(orig, n, i, colL, sigma) : 0.0;
+    y[0] = i < n ? (rhs ? rhs[i] : start_val(vid, i)) : 0.0;
+  }
+  __threadfence_block();
+  // back substitution: x[j] = (ys[j] - sum_{c>=1} U[j][c] x[j+c]) / U[j][0];
+  // lane L keeps x[row] for the row = L (mod 33) inside the window
+  double xv = 0.0, nrm = 0.0;
+  for (int j = n - 1; j >= 0; --j) {
+    const int lj = j % WC;
+    const int off = (L - lj + WC) % WC;
+    double part = 0.0;
+    if (act && off != 0 && j + off < n) part = U[(int64_t)j * WC + off] * xv;
+    const double sm = wave_sum_d(part);
+    const double xj = (ys[j] - sm) / U[(int64_t)j * WC];
+    if (L == lj) {
+      xv = xj;
+      nrm = fma(xj, xj, nrm);
+      xout[j] = xj;
+    }
+  }
+  nrm = wave_sum_d(nrm);
+  __threadfence_block();
+  const double sc = 1.0 / sqrt(nrm);
+  for (int j = L; j < n; j += 64) xout[j] *= sc;
+  __threadfence_block();
+}
+
+// Rayleigh quotient x^T B x of a normalised float64 vector (one wavefront).
+__device__ double rayleigh(const float* orig, int n, const double* x) {
+  const int L = threadIdx.x & 63;
+  double acc = 0.0;
+  for (int i = L; i < n; i += 64) {
+    double bx = 0.0;
+    const int c0 = i - NB < 0 ? 0 : i - NB, c1 = i + NB >= n ? n - 1 : i + NB;
+    for (int c = c0; c <= c1; ++c) bx = fma(mval(orig, n, i, c, 0.0), x[c], bx);
+    acc = fma(x[i], bx, acc);
+  }
+  return wave_sum_d(acc);
+}
+
+// Clusters: consecutive eigenvalues (descending) closer than kClusterTol times
+// the largest |B| entry.  Inverse iteration cannot separate them (their
+// vectors would converge to one combination), so each member gets its own
+// shift, offset by (rank + 1/2) * kShiftStep * |B| -- no exactly singular
+// pivot, and the random start vectors stay independent -- and the members are
+// made orthonormal afterwards (LAPACK's stein perturbs and orthogonalises
+// clustered eigenvalues the same way).
+constexpr double kClusterTol = 1e-10;
+constexpr double kShiftStep = 1e-13;
+
+// One wavefront per eigenvector; vectors [v0, v0 + gridDim.x * 4) of the
+// flattened (matrix, index) list; 4 wavefronts per block.  Two solves with
+// the same shift from a pseudo-random start (the shift is a float64
+// eigenvalue of the float64 tridiagonal, so one solve already converges for
+// any gap far above 1e-15 |B|), then the Rayleigh quotient into wr.
+__global__ __launch_bounds__(256) void k_inviter(const float* orig, int64_t ostride, int n, int kq,
+                                                 int nvec, int v0, const double* w,
+                                                 const double* bnorm, double* work, double* xall,
+                                                 double* wr) {
+  const int wv = threadIdx.x >> 6;
+  const int vid = v0 + blockIdx.x * 4 + wv;
+  if (vid >= nvec) return;
+  const int mat = vid / kq, idx = vid % kq;
+  const float* om = orig + (int64_t)mat * ostride;
+  const int64_t slot = (int64_t)(vid - v0);
+  double* U = work + slot * ((int64_t)n * (WC + 1));
+  double* ys = U + (int64_t)n * WC;
+  double* x = xall + (int64_t)vid * n;
+  const double bn = bnorm[mat];
+  const double* wm = w + (int64_t)mat * kq;
+  const double tol = kClusterTol * bn;
+  int rank = 0;
+  for (int t = idx; t > 0 && fabs(wm[t - 1] - wm[t]) <= tol; --t) ++rank;
+  const bool clustered = rank > 0 || (idx + 1 < kq && fabs(wm[idx] - wm[idx + 1]) <= tol);
+  const double sigma = wm[idx] + (clustered ? (rank + 0.5) * kShiftStep * bn : 0.0);
+  band_solve(om, n, sigma, bn, (uint32_t)vid, nullptr, U, ys, x);
+  band_solve(om, n, sigma, bn, (uint32_t)vid, x, U, ys, x);
+  const double rq = rayleigh(om, n, x);
+  if ((threadIdx.x & 63) == 0) wr[vid] = rq;
+}
+
+// Sum over a 256-thread block, the result returned to every thread.
+__device__ __forceinline__ double block_sum_all(double x, double* red /* >= 5 */) {
+  double a[1] = {x};
+  block_sum<1>(a, red);
+  if (threadIdx.x == 0) red[4] = a[0];
+  __syncthreads();
+  const double r = red[4];
+  __syncthreads();
+  return r;
+}
+
+// Per matrix: Gram-Schmidt (twice) of each vector against the earlier ones of
+// its cluster -- consecutive eigenvalues whose gaps are all below tol * bnorm
+// -- then the float32 output Z (n x kq, row-major).
+__global__ __launch_bounds__(256) void k_cluster_orth(int n, int kq, double* w, const double* wr,
+                                                      const double* bnorm, double* xall,
+                                                      float* Z, int64_t zstride) {
+  __shared__ double red[16];
+  const int mat = blockIdx.x;
+  double* wm = w + (int64_t)mat * kq;
+  double* xm = xall + (int64_t)mat * kq * n;
+  const double tol = kClusterTol * bnorm[mat];
+  int cstart = 0;
+  for (int i = 0; i < kq; ++i) {
+    if (i == 0 || fabs(wm[i - 1] - wm[i]) > tol) cstart = i;
+    double* xi = xm + (int64_t)i * n;
+    if (i > cstart) {
+      for (int pass = 0; pass < 2; ++pass) {
+        for (int jv = cstart; jv < i; ++jv) {
+          const double* xj = xm + (int64_t)jv * n;
+          double x = 0.0;
+          for (int r = threadIdx.x; r < n; r += 256) x = fma(xj[r], xi[r], x);
+          x = block_sum_all(x, red);
+          for (int r = threadIdx.x; r < n; r += 256) xi[r] = fma(-x, xj[r], xi[r]);
+          __syncthreads();
+        }
+        double x = 0.0;
+        for (int r = threadIdx.x; r < n; r += 256) x = fma(xi[r], xi[r], x);
+        x = block_sum_all(x, red);
+        const double sc = 1.0 / sqrt(x);
+        for (int r = threadIdx.x; r < n; r += 256) xi[r] *= sc;
+        __syncthreads();
+      }
+    }
+    float* zm = Z + (int64_t)mat * zstride;
+    for (int r = threadIdx.x; r < n; r += 256) zm[(int64_t)r * kq + i] = (float)xi[r];
+  }
+  __syncthreads();
+  // the Rayleigh quotients replace the bisection values once the clusters
+  // (found from the latter) are done
+  for (int i = threadIdx.x; i < kq; i += 256) wm[i] = wr[(int64_t)mat * kq + i];
+}
+
+// max |B| over the band (float64) per matrix: the scale of the pivot guard
+// and of the cluster tolerance.
+__global__ __launch_bounds__(256) void k_band_norm(const float* orig, int64_t ostride, int n,
+                                                   double* bnorm) {
+  __shared__ float mx[256];
+  const float* om = orig + (int64_t)blockIdx.x * ostride;
+  float m = 0.f;
+  for (int64_t t = threadIdx.x; t < (int64_t)n * OW; t += 256) m = fmaxf(m, fabsf(om[t]));
+  mx[threadIdx.x] = m;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int t = 1; t < 256; ++t) m = fmaxf(m, mx[t]);
+    bnorm[blockIdx.x] = (double)m;
+  }
+}
+
+constexpr int kInvChunk = 2048;   // vectors per inverse-iteration launch
+
+}  // namespace
+
+// ------------------------------------------------------------- C ABI ---
+extern "C" int scao_eig_panel_qr(float* A, int64_t stride, int n, int c0, int batch, float* T,
+                                 float* band, int64_t bstride, void* stream) {
+  SCAO_CHECK_ARG(A && T && band, "scao_eig_panel_qr: null pointer");
+  SCAO_CHECK_ARG(batch >= 0 && n > 0 && n <= 4096 + NB && c0 >= 0 && c0 % NB == 0 &&
+                     c0 + NB < n && stride >= (int64_t)n * n && bstride >= (int64_t)n * BW,
+                 "scao_eig_panel_qr: bad arguments n=%d c0=%d", n, c0);
+  if (batch == 0) return SCAO_OK;
+  const int m = n - c0 - NB;
+  hipStream_t s = (hipStream_t)stream;
+  float* Am = A;
+  if (m <= 1024)
+    hipLaunchKernelGGL((k_panel_qr<1>), dim3(batch), dim3(1024), 0, s, Am, stride, n, c0, T, band, bstride);
+  else if (m <= 2048)
+    hipLaunchKernelGGL((k_panel_qr<2>), dim3(batch), dim3(1024), 0, s, Am, stride, n, c0, T, band, bstride);
+  else
+    hipLaunchKernelGGL((k_panel_qr<4>), dim3(batch), dim3(1024), 0, s, Am, stride, n, c0, T, band, bstride);
+  SCAO_LAUNCH_CHECK("scao_eig_panel_qr");
+  return SCAO_OK;
+}
+
+extern "C" int scao_eig_band_finish(const float* A, int64_t stride, int n, int batch,
+                                    const float* band, int64_t bstride, float* orig,
+                                    int64_t ostride, double* band64, void* stream) {
+  SCAO_CHECK_ARG(A && band && orig && band64, "scao_eig_band_finish: null pointer");
+  SCAO_CHECK_ARG(batch >= 0 && n > 0 && stride >= (int64_t)n * n && bstride >= (int64_t)n * BW &&
+                     ostride >= (int64_t)n * OW,
+                 "scao_eig_band_finish: bad arguments");
+  if (batch == 0) return SCAO_OK;
+  hipLaunchKernelGGL(k_band_finish, dim3((n + 255) / 256, batch), dim3(256), 0, (hipStream_t)stream,
+                     A, stride, n, band, bstride, orig, ostride, band64);
+  SCAO_LAUNCH_CHECK("scao_eig_band_finish");
+  return SCAO_OK;
+}
+
+extern "C" int scao_eig_sb2st(double* band64, int n, int batch, double* d, double* e,
+                              void* stream) {
+  SCAO_CHECK_ARG(band64 && d && e, "scao_eig_sb2st: null pointer");
+  SCAO_CHECK_ARG(batch >= 0 && n > 0, "scao_eig_sb2st: bad arguments");
+  if (batch == 0) return SCAO_OK;
+  hipLaunchKernelGGL(k_sb2st, dim3(batch), dim3(SB_W * 64), 0, (hipStream_t)stream, band64, n, d,
+                     e);
+  SCAO_LAUNCH_CHECK("scao_eig_sb2st");
+  return SCAO_OK;
+}
+
+extern "C" int64_t scao_eig_bisect_work(int n, int batch) {
+  if (n <= 0 || batch <= 0) return 0;
+  return (int64_t)batch * ((int64_t)n * 8 + 4 * 8 + 8);
+}
+
+extern "C" int scao_eig_bisect(const double* d, const double* e, int n, int batch, int kq, double* w,
+                               double* total, void* work, void* stream) {
+  SCAO_CHECK_ARG(d && e && w && total && work, "scao_eig_bisect: null pointer");
+  SCAO_CHECK_ARG(batch >= 0 && n > 0 && kq > 0 && kq <= n, "scao_eig_bisect: bad arguments");
+  if (batch == 0) return SCAO_OK;
+  hipStream_t s = (hipStream_t)stream;
+  double* wall = (double*)work;
+  double* info = wall + (int64_t)batch * n;
+  int* nneg = (int*)(info + 4 * (int64_t)batch);
+  hipLaunchKernelGGL(k_tri_info, dim3(batch), dim3(256), 0, s, d, e, n, info, nneg);
+  SCAO_LAUNCH_CHECK("scao_eig_bisect/info");
+  hipLaunchKernelGGL(k_bisect, dim3((n + 255) / 256, batch), dim3(256), 0, s, d, e, n, kq, info,
+                     nneg, wall);
+  SCAO_LAUNCH_CHECK("scao_eig_bisect/bisect");
+  hipLaunchKernelGGL(k_bisect_finish, dim3(batch), dim3(64), 0, s, wall, n, kq, info, nneg, w,
+                     total);
+  SCAO_LAUNCH_CHECK("scao_eig_bisect/finish");
+  return SCAO_OK;
+}
+
+extern "C" int64_t scao_eig_vectors_work(int n, int batch, int kq) {
+  if (n <= 0 || batch <= 0 || kq <= 0) return 0;
+  const int64_t nvec = (int64_t)batch * kq;
+  const int64_t chunk = nvec < kInvChunk ? nvec : kInvChunk;
+  // per chunk vector: U (n x 33) + ys (n); per vector: x (n) and its Rayleigh
+  // quotient; per matrix: |B|
+  return (chunk * (int64_t)n * (WC + 1) + nvec * ((int64_t)n + 1) + batch) *
+         (int64_t)sizeof(double);
+}
+
+extern "C" int scao_eig_vectors(const float* orig, int64_t ostride, int n, int batch, int kq,
+                                double* w, float* Z, int64_t zstride, void* work, void* stream) {
+  SCAO_CHECK_ARG(orig && w && Z && work, "scao_eig_vectors: null pointer");
+  SCAO_CHECK_ARG(batch >= 0 && n > 0 && kq > 0 && kq <= n && ostride >= (int64_t)n * OW &&
+                     zstride >= (int64_t)n * kq,
+                 "scao_eig_vectors: bad arguments");
+  if (batch == 0) return SCAO_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int nvec = batch * kq;
+  const int chunk = nvec < kInvChunk ? nvec : kInvChunk;
+  double* U = (double*)work;
+  double* xall = U + (int64_t)chunk * n * (WC + 1);
+  double* wr = xall + (int64_t)nvec * n;
+  double* bnorm = wr + nvec;
+  hipLaunchKernelGGL(k_band_norm, dim3(batch), dim3(256), 0, s, orig, ostride, n, bnorm);
+  SCAO_LAUNCH_CHECK("scao_eig_vectors/norm");
+  for (int v0 = 0; v0 < nvec; v0 += chunk) {
+    const int cnt = nvec - v0 < chunk ? nvec - v0 : chunk;
+    hipLaunchKernelGGL(k_inviter, dim3((cnt + 3) / 4), dim3(256), 0, s, orig, ostride, n, kq, nvec,
+                       v0, w, bnorm, U, xall, wr);
+    SCAO_LAUNCH_CHECK("scao_eig_vectors/inviter");
+  }
+  hipLaunchKernelGGL(k_cluster_orth, dim3(batch), dim3(256), 0, s, n, kq, w, wr, bnorm, xall, Z,
+                     zstride);
+  SCAO_LAUNCH_CHECK("scao_eig_vectors/orth");
+  return SCAO_OK;
+}

@@ -1,0 +1,120 @@
+"""Top-k eigenpairs of a batch of symmetric matrices on the device.
+
+The eigen stage of the curvature refresh (scao/preconditioner.py:413-451)
+needs, per factor, the k_max largest eigenpairs and the sum of the clamped
+spectrum (utils.adaptive_rank, scao/utils.py:121-151).  The reference gets
+them from a full torch.linalg.eigh.  Here the work is split between the HIP
+kernels of csrc/eig.hip and plain batched GEMMs (rocBLAS, through torch):
+
+1. dense -> band with SCAO_EIG_BAND sub-diagonals: for every panel of b
+   columns, ``scao_eig_panel_qr`` factors it (Householder, V kept in the
+   panel, T returned), then the trailing matrix gets the two-sided update
+   A22 <- Q^T A22 Q = A22 - (V W^T + W V^T), W = X - V (T^T V^T X) / 2,
+   X = A22 V T (three GEMMs);
+2. ``scao_eig_band_finish`` / ``scao_eig_sb2st``: band -> tridiagonal;
+3. ``scao_eig_bisect``: the kq largest eigenvalues and the clamped sum;
+4. ``scao_eig_vectors``: eigenvectors of the band matrix;
+5. back-transformation Z <- Q_0 (Q_1 (... Q_last Z)), two GEMMs per panel.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import Tensor
+
+from . import _lib as L
+
+NB = L.EIG_BAND
+BW = L.EIG_BANDW
+
+
+def panels(n: int) -> list:
+    """Column origins of the stage-1 panels of an n x n matrix."""
+    return list(range(0, n - NB, NB))
+
+
+def _check(X: Tensor) -> None:
+    if X.dtype != torch.float32 or X.ndim != 3 or X.shape[1] != X.shape[2]:
+        raise ValueError(f"eigen: expected (B, n, n) float32, got {tuple(X.shape)} {X.dtype}")
+    if X.device.type != "cuda":
+        raise RuntimeError("eigen: X must be on a ROCm device")
+    if not X.is_contiguous():
+        raise ValueError("eigen: X must be contiguous")
+    if X.shape[1] > 4096 + NB:
+        raise ValueError(f"eigen: n={X.shape[1]} above the supported {4096 + NB}")
+
+
+def _reduce(X: Tensor):
+    """Stages 1-2: returns (panel origins, T factors, band copy (B, n, b+1):
+    lower diagonals 0..b of the band matrix, tridiagonal d, e)."""
+    B, n, _ = X.shape
+    dev = X.device
+    f32 = torch.float32
+    s = L.stream_ptr(dev)
+    pcs = panels(n)
+    Tall = torch.empty(max(len(pcs), 1), B, NB, NB, dtype=f32, device=dev)
+    band = torch.zeros(B, n, BW, dtype=f32, device=dev)
+    nn = n * n
+    for p, c0 in enumerate(pcs):
+        L.call("scao_eig_panel_qr", X.data_ptr(), nn, n, c0, B, Tall[p].data_ptr(),
+               band.data_ptr(), n * BW, s)
+        r0 = c0 + NB
+        V = X[:, r0:, c0:c0 + NB]
+        T = Tall[p]
+        A22 = X[:, r0:, r0:]
+        Y = torch.bmm(torch.bmm(A22, V), T)                        # X = A22 V T
+        M = torch.bmm(T.transpose(1, 2), torch.bmm(V.transpose(1, 2), Y))
+        W = torch.baddbmm(Y, V, M, alpha=-0.5)                     # X - V M / 2
+        A22.baddbmm_(torch.cat([V, W], 2), torch.cat([W, V], 2).transpose(1, 2), alpha=-1.0)
+    orig = torch.empty(B, n, NB + 1, dtype=f32, device=dev)
+    band64 = torch.empty(B, n, BW, dtype=torch.float64, device=dev)
+    L.call("scao_eig_band_finish", X.data_ptr(), nn, n, B, band.data_ptr(), n * BW,
+           orig.data_ptr(), n * (NB + 1), band64.data_ptr(), s)
+    del band
+    d = torch.empty(B, n, dtype=torch.float64, device=dev)
+    e = torch.zeros(B, n, dtype=torch.float64, device=dev)
+    L.call("scao_eig_sb2st", band64.data_ptr(), n, B, d.data_ptr(), e.data_ptr(), s)
+    return pcs, Tall, orig, d, e
+
+
+def stages(X: Tensor):
+    """Stages 1-2 alone (for tests): (band copy, d, e); X is overwritten."""
+    _check(X)
+    _, _, orig, d, e = _reduce(X)
+    return orig, d, e
+
+
+def topk_eigh(X: Tensor, kq: int):
+    """The kq largest eigenpairs of each symmetric matrix of X (B, n, n).
+
+    X must be a contiguous float32 device tensor; it is overwritten (its
+    panels end up holding the stage-1 reflectors).  Returns (w, U, total):
+    w (B, kq) float64 eigenvalues in descending order (Rayleigh quotients of
+    the band matrix), U (B, n, kq) float32 orthonormal eigenvectors, total
+    (B,) float64 = sum over all eigenvalues of max(lambda, 0)."""
+    _check(X)
+    B, n, _ = X.shape
+    if not 1 <= kq <= n:
+        raise ValueError(f"topk_eigh: kq={kq} outside [1, {n}]")
+    dev = X.device
+    s = L.stream_ptr(dev)
+    pcs, Tall, orig, d, e = _reduce(X)
+    w = torch.empty(B, kq, dtype=torch.float64, device=dev)
+    total = torch.empty(B, dtype=torch.float64, device=dev)
+    work = torch.empty(max(L.lib().scao_eig_bisect_work(n, B), 8), dtype=torch.uint8, device=dev)
+    L.call("scao_eig_bisect", d.data_ptr(), e.data_ptr(), n, B, kq, w.data_ptr(),
+           total.data_ptr(), work.data_ptr(), s)
+    Z = torch.empty(B, n, kq, dtype=torch.float32, device=dev)
+    work = torch.empty(max(L.lib().scao_eig_vectors_work(n, B, kq), 8), dtype=torch.uint8,
+                       device=dev)
+    L.call("scao_eig_vectors", orig.data_ptr(), n * (NB + 1), n, B, kq, w.data_ptr(),
+           Z.data_ptr(), n * kq, work.data_ptr(), s)
+    del work
+    # Z <- Q_0 (Q_1 (... Q_last Z)),  Q_p = I - V_p T_p V_p^T
+    for p in reversed(range(len(pcs))):
+        c0 = pcs[p]
+        r0 = c0 + NB
+        V = X[:, r0:, c0:c0 + NB]
+        Zs = Z[:, r0:, :]
+        Zs.sub_(torch.bmm(V, torch.bmm(Tall[p], torch.bmm(V.transpose(1, 2), Zs))))
+    return w, Z, total

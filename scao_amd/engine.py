@@ -40,8 +40,9 @@ import torch
 from torch import Tensor
 
 from . import _lib as L
+from . import eigen
 from .preconditioner import SparsePreconditioner, leaf_epoch
-from .utils import batched_adaptive_rank, to_2d
+from .utils import batched_adaptive_rank, batched_adaptive_rank_topk, to_2d
 
 
 
@@ -915,6 +916,11 @@ def sparse_filter(entries) -> list:
 # --------------------------------------------------------------------------
 
 REFRESH_SCRATCH_BYTES = 2 << 30   # fp32 EMA staging per refresh chunk (int8 mode)
+# The eigen stage: "hip" is scao_amd.eigen.topk_eigh (two-stage reduction,
+# bisection, inverse iteration: only the k_max vectors a factor can keep);
+# "torch" is the full torch.linalg.eigh (rocSOLVER syevd), kept for A/B runs.
+EIGEN_SOLVER = "hip"
+EIGEN_BATCH_BYTES = 8 << 30       # stacked eigen-stage inputs per launch (hip)
 # Optional callable run between a refresh's EMA update and its eigen stage,
 # with the list of (block, gradient, offset, row stride) being refreshed.  Used
 # by the parity tests to check the new EMA and then continue from the CPU
@@ -1012,19 +1018,28 @@ def _refresh_kron(kron, dev, s, eigen_only=False, ema_only=False):
     for leaf, *_ in kron:
         jobs.setdefault(leaf.m, []).append((leaf, 0))
         jobs.setdefault(leaf.n, []).append((leaf, 1))
-    spectra = {}   # (id(leaf), side) -> (S_desc, U_desc)
+    spectra = {}   # (id(leaf), side) -> (S_desc, U_desc, total)
     eig_timer = _mark("refresh:eigh+rank")
     eig_timer.__enter__()
+    hip = EIGEN_SOLVER == "hip"
     for dim, lst in jobs.items():
-        per = max(1, EIGH_BATCH_BYTES // (4 * dim * dim))
+        budget = EIGEN_BATCH_BYTES if hip else EIGH_BATCH_BYTES
+        per = max(1, budget // (4 * dim * dim))
+        # vectors a factor can keep: k <= k_max (rank momentum and clamps)
+        kq = min(dim, max(leaf.k_max for leaf, _ in lst))
         for b0 in range(0, len(lst), per):
             part = lst[b0:b0 + per]
             X = _eig_inputs(part, dim, dev, s)
-            w, V = _eigh_batched(X)
-            S_desc = w.flip(-1).clamp(min=0.0)
-            U_desc = V.flip(-1)
-            for (leaf, side), Sd, Ud in zip(part, S_desc, U_desc):
-                spectra[(id(leaf), side)] = (Sd, Ud)
+            if hip:
+                w, U_desc, total = eigen.topk_eigh(X, kq)
+                S_desc = w.clamp(min=0.0).float()
+            else:
+                w, V = _eigh_batched(X)
+                S_desc = w.flip(-1).clamp(min=0.0)
+                U_desc = V.flip(-1)
+                total = S_desc.sum(dim=1).double()
+            for (leaf, side), Sd, Ud, tot in zip(part, S_desc, U_desc, total):
+                spectra[(id(leaf), side)] = (Sd, Ud, tot)
             del X
     # 3) adaptive rank for every (leaf, side) in one device pass + one read
     keys = [(leaf, side) for leaf, *_ in kron for side in (0, 1)]
@@ -1039,7 +1054,11 @@ def _refresh_kron(kron, dev, s, eigen_only=False, ema_only=False):
         eps = torch.tensor([lf.epsilon_sparse for lf, _ in lst], device=dev, dtype=torch.float64)
         kmin = torch.tensor([lf.k_min for lf, _ in lst], device=dev, dtype=torch.int64)
         kmax = torch.tensor([lf.k_max for lf, _ in lst], device=dev, dtype=torch.int64)
-        dev_ranks.append((lst, batched_adaptive_rank(S, eps, kmin, kmax)))
+        if hip:
+            tot = torch.stack([spectra[(id(lf), sd)][2] for lf, sd in lst])
+            dev_ranks.append((lst, batched_adaptive_rank_topk(S, tot, dim, eps, kmin, kmax)))
+        else:
+            dev_ranks.append((lst, batched_adaptive_rank(S, eps, kmin, kmax)))
     host = torch.cat([r for _, r in dev_ranks]).cpu().tolist() if dev_ranks else []
     i = 0
     for lst, _ in dev_ranks:
@@ -1054,8 +1073,8 @@ def _refresh_kron(kron, dev, s, eigen_only=False, ema_only=False):
         k = min(k, leaf._k + 4)
         k = int(min(leaf.k_max, max(leaf.k_min, k)))
         leaf._k = k
-        Sl, Ul = spectra[(id(leaf), 0)]
-        Sr, Ur = spectra[(id(leaf), 1)]
+        Sl, Ul, _ = spectra[(id(leaf), 0)]
+        Sr, Ur, _ = spectra[(id(leaf), 1)]
         leaf.U_l = Ul[:, :k].contiguous()
         leaf.S_l = Sl[:k].contiguous()
         leaf.U_r = Ur[:, :k].contiguous()

@@ -87,3 +87,24 @@ def batched_adaptive_rank(S_desc: Tensor, epsilon: Tensor, k_min: Tensor, k_max:
                         torch.full_like(total, d, dtype=torch.int64))
     k = torch.minimum(k_max, torch.maximum(k_min, first))
     return torch.where(total.double() < 1e-12, k_min, k)
+
+
+def batched_adaptive_rank_topk(S_top: Tensor, total: Tensor, dim: int, epsilon: Tensor,
+                               k_min: Tensor, k_max: Tensor):
+    """``adaptive_rank`` from the kq largest eigenvalues of each spectrum
+    (clamped, descending, [B, kq]) and the sum of the whole clamped spectrum
+    (float64 [B]): the reference's total is the float32 sum of the clamped
+    spectrum, threshold = fp32((1 - eps) * double(total)), k = first index
+    whose float32 cumsum reaches it, plus one; when none of the kq does, the
+    first index lies beyond them (kq + 1, or dim when kq == dim), above every
+    k_max <= kq; k_min when total < 1e-12; clamped to [k_min, k_max]."""
+    kq = S_top.shape[1]
+    tot = total.float()
+    thr = ((1.0 - epsilon.double()) * tot.double()).float()
+    csum = torch.cumsum(S_top, dim=1)
+    hit = csum >= thr.unsqueeze(1)
+    beyond = dim if kq == dim else kq + 1
+    first = torch.where(hit.any(dim=1), hit.to(torch.int8).argmax(dim=1) + 1,
+                        torch.full_like(tot, beyond, dtype=torch.int64))
+    k = torch.minimum(k_max, torch.maximum(k_min, first))
+    return torch.where(tot.double() < 1e-12, k_min, k)

@@ -513,3 +513,25 @@ def test_bench_refuses_more_than_one_gpu():
                        capture_output=True, text=True, timeout=300)
     assert r.returncode == 2
     assert "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_adaptive_rank_from_top_eigenvalues_matches_full_spectrum():
+    """batched_adaptive_rank_topk (top kq values + the clamped total) picks the
+    same rank as batched_adaptive_rank on the whole spectrum (and as the
+    reference's utils.adaptive_rank restated in the oracle)."""
+    from scao_amd.utils import batched_adaptive_rank, batched_adaptive_rank_topk
+    g = torch.Generator().manual_seed(4)
+    for dim, kq, eps in [(64, 16, 0.05), (64, 64, 0.05), (200, 24, 0.3), (200, 24, 0.001),
+                         (32, 8, 0.5)]:
+        for trial in range(20):
+            lam = torch.rand(dim, generator=g) ** (1 + trial % 5) * (trial + 1)
+            if trial % 7 == 0:
+                lam[: dim // 2] = 0.0
+            S = lam.sort(descending=True).values.clamp(min=0).unsqueeze(0)
+            e = torch.tensor([eps], dtype=torch.float64)
+            kmin = torch.tensor([min(4, kq)])
+            kmax = torch.tensor([kq])
+            want = batched_adaptive_rank(S, e, kmin, kmax)
+            got = batched_adaptive_rank_topk(S[:, :kq], S.double().sum(dim=1), dim, e, kmin, kmax)
+            ref = R.adaptive_rank(S[0], eps, int(kmin), int(kmax))
+            assert int(got) == int(want) == ref, (dim, kq, eps, trial, int(got), int(want), ref)
