@@ -3,7 +3,10 @@
 Workload: the 16-layer Llama-3.2-1B parameter set (q/o 2048x2048, k/v
 512x2048, gate/up 8192x2048, down 2048x8192 preconditioned: 224 blocks of
 2048x2048 + 32 of 512x2048) plus the 128256x2048 embedding and the norm
-vectors in an Adam group (warmup_steps=1e9), fp32 master params, synthetic
+vectors in an Adam-path group (warmup_steps=1e9 and precond_freq=1e9: the
+reference keeps accumulating curvature during warmup, scao/optimizer.py:573-574,
+so an Adam-only group also needs a refresh period that never fires), fp32
+master params, synthetic
 N(0, 0.02^2) params and N(0, 1e-3^2) grads generated on the device.  Profile:
 int8 EMA, k_min=k_max=64, max_precond_dim=2048, sparsity=0, no noise, no
 lookahead, synchronous refresh, reference defaults otherwise (tau=1,
@@ -13,8 +16,8 @@ A "step" is one optimizer.step() over all 1235.81M parameters.  The timed
 region is K consecutive steady Phase-2 steps with no curvature refresh (the
 reference refreshes only when step % precond_freq == 0); two gradient sets
 rotate so consecutive steps see different gradients.  The Phase-1 (Adam)
-step and the refresh (Gram/EMA/requantise on the GPU, eigh + rank in
-PyTorch-ROCm) are timed separately and reported in "details".
+step and the curvature refresh (Gram/EMA/requantise and the top-k eigen
+stage on the GPU) are timed separately and reported in "details".
 
 Prints one JSON line.  --gpus N>1 exits: this build runs on one GPU.
 """
@@ -191,7 +194,8 @@ def main():
         sched = dict(warmup_steps=2, precond_freq=10 ** 9, min_precond_updates=0)
     else:
         sched = dict(warmup_steps=3, precond_freq=3, min_precond_updates=1)
-    opt = scao_amd.SCAO([{"params": pre_p}, {"params": adam_p, "warmup_steps": 10 ** 9}],
+    opt = scao_amd.SCAO([{"params": pre_p},
+                         {"params": adam_p, "warmup_steps": 10 ** 9, "precond_freq": 10 ** 9}],
                         k_min=cfg["k"], k_max=cfg["k"], max_precond_dim=cfg["D"], **sched,
                         **PROFILE)
     if args.copy_probe_mib:

@@ -311,7 +311,8 @@ int scao_eig_bisect(const double* d, const double* e, int n, int batch, int kq, 
                     double* total, void* work, void* stream);
 /* Eigenvectors of the band matrices (orig, pitch b+1) for the eigenvalues w
  * (kq per matrix): float64 inverse iteration with band LU and partial
- * pivoting (two solves from a pseudo-random start), then Gram-Schmidt inside
+ * pivoting (one solve from a pseudo-random start, a second when the solution
+ * did not grow enough to have converged), then Gram-Schmidt inside
  * clusters of eigenvalues closer than 1e-10 of the largest |B| entry (whose
  * members get shifts offset by 1e-13 |B| steps).  Output Z (n x kq row-major,
  * float32) at Z + i*zstride; w is replaced by the vectors' Rayleigh

@@ -208,7 +208,7 @@ __global__ __launch_bounds__(256) void k_band_finish(const float* A, int64_t str
 //     each wavefront publishes its progress (s * 65536 + tasks done) in LDS;
 //   * the rows of task k+1 are loaded while task k computes (they need sweep
 //     s-1 to have finished task k+3, which it almost always has).
-constexpr int SB_W = 4;
+constexpr int SB_W = 8;
 constexpr int SB_BIG = 1 << 16;
 
 struct Sb2stLds {
@@ -531,13 +531,32 @@ __device__ __forceinline__ double start_val(uint32_t vid, int row) {
   return (double)(h & 0xFFFFFF) / 8388608.0 - 1.0;
 }
 
+// Prefetch distance (steps) of the band solve: the band values entering the
+// window and the U rows of the back substitution are loaded this many steps
+// before their use, so one step's work covers the memory latency of another.
+constexpr int PF = 8;
+
+// Value entering lane L's slot 0 at the end of elimination step j: row
+// j + WR, column j + 1 + ((L - (j mod WC) - 1) mod WC).
+__device__ __forceinline__ double enter_val(const float* orig, int n, int j, int L, bool act,
+                                            double sigma) {
+  const int lj = j % WC;
+  const int colL = j + 1 + ((L - (lj + 1)) % WC + WC) % WC;
+  return act ? mval(orig, n, j + WR, colL, sigma) : 0.0;
+}
+
+__device__ __forceinline__ double enter_rhs(const double* rhs, uint32_t vid, int n, int i) {
+  return i < n ? (rhs ? rhs[i] : start_val(vid, i)) : 0.0;
+}
+
 // Solve (B - sigma I) x = rhs with band LU and partial pivoting; rhs given by
 // `rhs` (NULL: start_val).  U rows (WC doubles each) and the transformed rhs
 // go to work; x (float64, normalised) to xout.  One wavefront; lanes 0..32
 // each own one window column (lane L holds column j + ((L - j) mod 33) at
-// step j), every lane holds all 17 row slots of its column.
-__device__ void band_solve(const float* orig, int n, double sigma, double bnorm, uint32_t vid,
-                           const double* rhs, double* U, double* ys, double* xout) {
+// step j), every lane holds all 17 row slots of its column.  Returns the
+// norm of the solution before normalisation.
+__device__ double band_solve(const float* orig, int n, double sigma, double bnorm, uint32_t vid,
+                             const double* rhs, double* U, double* ys, double* xout) {
   const int L = threadIdx.x & 63;
   const bool act = L < WC;
   double W[WR], y[WR];
@@ -545,66 +564,94 @@ __device__ void band_solve(const float* orig, int n, double sigma, double bnorm,
 #pragma unroll
   for (int s = 0; s < WR; ++s) {
     W[s] = act ? mval(orig, n, s, L, sigma) : 0.0;
-    y[s] = s < n ? (rhs ? rhs[s] : start_val(vid, s)) : 0.0;
+    y[s] = enter_rhs(rhs, vid, n, s);
+  }
+  double qW[PF], qY[PF];
+#pragma unroll
+  for (int t = 0; t < PF; ++t) {
+    qW[t] = enter_val(orig, n, t, L, act, sigma);
+    qY[t] = enter_rhs(rhs, vid, n, t + WR);
   }
   const double tiny = 2.220446049250313e-16 * bnorm + 1e-300;
-  for (int j = 0; j < n; ++j) {
-    const int lj = j % WC;
-    double col[WR];
+  for (int j0 = 0; j0 < n; j0 += PF) {
 #pragma unroll
-    for (int s = 0; s < WR; ++s) col[s] = readlane_d(W[s], lj);
-    int p = 0;
-    double best = fabs(col[0]);
+    for (int t = 0; t < PF; ++t) {
+      const int j = j0 + t;
+      if (j >= n) break;
+      const int lj = j % WC;
+      double col[WR];
 #pragma unroll
-    for (int s = 1; s < WR; ++s)
-      if (fabs(col[s]) > best) {
-        best = fabs(col[s]);
-        p = s;
+      for (int s = 0; s < WR; ++s) col[s] = readlane_d(W[s], lj);
+      int p = 0;
+      double best = fabs(col[0]);
+#pragma unroll
+      for (int s = 1; s < WR; ++s)
+        if (fabs(col[s]) > best) {
+          best = fabs(col[s]);
+          p = s;
+        }
+      p = __builtin_amdgcn_readfirstlane(p);
+#pragma unroll
+      for (int s = 1; s < WR; ++s)
+        if (p == s) {
+          double tt = W[0]; W[0] = W[s]; W[s] = tt;
+          tt = y[0]; y[0] = y[s]; y[s] = tt;
+          tt = col[0]; col[0] = col[s]; col[s] = tt;
+        }
+      double piv = col[0];
+      if (fabs(piv) < tiny) piv = piv < 0.0 ? -tiny : tiny;
+      const double inv = 1.0 / piv;
+#pragma unroll
+      for (int s = 1; s < WR; ++s) {
+        const double lm = col[s] * inv;
+        W[s] = fma(-lm, W[0], W[s]);
+        y[s] = fma(-lm, y[0], y[s]);
       }
-    p = __builtin_amdgcn_readfirstlane(p);
-#pragma unroll
-    for (int s = 1; s < WR; ++s)
-      if (p == s) {
-        double t = W[0]; W[0] = W[s]; W[s] = t;
-        t = y[0]; y[0] = y[s]; y[s] = t;
-        t = col[0]; col[0] = col[s]; col[s] = t;
-      }
-    double piv = col[0];
-    if (fabs(piv) < tiny) piv = piv < 0.0 ? -tiny : tiny;
-    const double inv = 1.0 / piv;
-#pragma unroll
-    for (int s = 1; s < WR; ++s) {
-      const double lm = col[s] * inv;
-      W[s] = fma(-lm, W[0], W[s]);
-      y[s] = fma(-lm, y[0], y[s]);
+      // retire the pivot row as U row j (column offset of this lane)
+      const int off = (L - lj + WC) % WC;
+      double w0 = W[0];
+      if (L == lj) w0 = piv;
+      if (act) U[(int64_t)j * WC + off] = w0;
+      if (L == 0) ys[j] = y[0];
+      // row j + 17 enters slot 0 (prefetched PF steps ago); fetch step j + PF's
+      W[0] = qW[t];
+      y[0] = qY[t];
+      qW[t] = enter_val(orig, n, j + PF, L, act, sigma);
+      qY[t] = enter_rhs(rhs, vid, n, j + PF + WR);
     }
-    // retire the pivot row as U row j (column offset of this lane)
-    const int off = (L - lj + WC) % WC;
-    double w0 = W[0];
-    if (L == lj) w0 = piv;
-    if (act) U[(int64_t)j * WC + off] = w0;
-    if (L == 0) ys[j] = y[0];
-    // row j + 17 enters slot 0; lane lj's column becomes j + 33
-    const int i = j + WR;
-    const int colL = j + 1 + ((L - (lj + 1)) % WC + WC) % WC;
-    W[0] = act ? mval(orig, n, i, colL, sigma) : 0.0;
-    y[0] = i < n ? (rhs ? rhs[i] : start_val(vid, i)) : 0.0;
   }
   __threadfence_block();
   // back substitution: x[j] = (ys[j] - sum_{c>=1} U[j][c] x[j+c]) / U[j][0];
-  // lane L keeps x[row] for the row = L (mod 33) inside the window
+  // lane L keeps x[row] for the row = L (mod 33) inside the window.  Row j's
+  // U entries, diagonal and rhs are loaded PF steps ahead (they do not depend
+  // on x).
+  double qU[PF], qD[PF], qS[PF];
+#pragma unroll
+  for (int t = 0; t < PF; ++t) {
+    const int j = n - 1 - t;
+    const int off = j >= 0 ? (L - j % WC + WC) % WC : 0;
+    qU[t] = (j >= 0 && act && off != 0 && j + off < n) ? U[(int64_t)j * WC + off] : 0.0;
+    qD[t] = j >= 0 ? U[(int64_t)j * WC] : 1.0;
+    qS[t] = j >= 0 ? ys[j] : 0.0;
+  }
   double xv = 0.0, nrm = 0.0;
-  for (int j = n - 1; j >= 0; --j) {
-    const int lj = j % WC;
-    const int off = (L - lj + WC) % WC;
-    double part = 0.0;
-    if (act && off != 0 && j + off < n) part = U[(int64_t)j * WC + off] * xv;
-    const double sm = wave_sum_d(part);
-    const double xj = (ys[j] - sm) / U[(int64_t)j * WC];
-    if (L == lj) {
-      xv = xj;
-      nrm = fma(xj, xj, nrm);
-      xout[j] = xj;
+  for (int j0 = n - 1; j0 >= 0; j0 -= PF) {
+#pragma unroll
+    for (int t = 0; t < PF; ++t) {
+      const int j = j0 - t;
+      if (j < 0) break;
+      const double sm = wave_sum_d(qU[t] * xv);
+      const double xj = (qS[t] - sm) / qD[t];
+      if (L == j % WC) {
+        xv = xj;
+        nrm = fma(xj, xj, nrm);
+        xout[j] = xj;
+      }
+      const int jn = j - PF;
+      const int off = jn >= 0 ? (L - jn % WC + WC) % WC : 0;
+      qU[t] = (jn >= 0 && act && off != 0 && jn + off < n) ? U[(int64_t)jn * WC + off] : 0.0;
+      qD[t] = jn >= 0 ? U[(int64_t)jn * WC] : 1.0;
+      qS[t] = jn >= 0 ? ys[jn] : 0.0;
     }
   }
   nrm = wave_sum_d(nrm);
@@ -612,6 +659,7 @@ __device__ void band_solve(const float* orig, int n, double sigma, double bnorm,
   const double sc = 1.0 / sqrt(nrm);
   for (int j = L; j < n; j += 64) xout[j] *= sc;
   __threadfence_block();
+  return sqrt(nrm);
 }
 
 // Rayleigh quotient x^T B x of a normalised float64 vector (one wavefront).
@@ -638,11 +686,12 @@ constexpr double kClusterTol = 1e-10;
 constexpr double kShiftStep = 1e-13;
 
 // One wavefront per eigenvector; vectors [v0, v0 + gridDim.x * 4) of the
-// flattened (matrix, index) list; 4 wavefronts per block.  Two solves with
-// the same shift from a pseudo-random start (the shift is a float64
-// eigenvalue of the float64 tridiagonal, so one solve already converges for
-// any gap far above 1e-15 |B|), then the Rayleigh quotient into wr.
-__global__ __launch_bounds__(256) void k_inviter(const float* orig, int64_t ostride, int n, int kq,
+// flattened (matrix, index) list; 4 wavefronts per block.  One solve from a
+// pseudo-random start (the shift is a float64 eigenvalue of the float64
+// tridiagonal, so one solve converges for any gap far above 1e-15 |B|; a
+// second one follows when the solution did not grow as that implies), then
+// the Rayleigh quotient into wr.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_inviter(const float* orig, int64_t ostride, int n, int kq,
                                                  int nvec, int v0, const double* w,
                                                  const double* bnorm, double* work, double* xall,
                                                  double* wr) {
@@ -662,8 +711,12 @@ __global__ __launch_bounds__(256) void k_inviter(const float* orig, int64_t ostr
   for (int t = idx; t > 0 && fabs(wm[t - 1] - wm[t]) <= tol; --t) ++rank;
   const bool clustered = rank > 0 || (idx + 1 < kq && fabs(wm[idx] - wm[idx + 1]) <= tol);
   const double sigma = wm[idx] + (clustered ? (rank + 0.5) * kShiftStep * bn : 0.0);
-  band_solve(om, n, sigma, bn, (uint32_t)vid, nullptr, U, ys, x);
-  band_solve(om, n, sigma, bn, (uint32_t)vid, x, U, ys, x);
+  // the start vector has entries uniform in [-1, 1]: norm about sqrt(n / 3);
+  // a solution that grew by less than 1e10 / |B| relative to it had a shift
+  // too far from the eigenvalue to have converged: solve once more from it
+  const double growth = band_solve(om, n, sigma, bn, (uint32_t)vid, nullptr, U, ys, x);
+  if (growth * bn < 1e10 * sqrt(n / 3.0))
+    band_solve(om, n, sigma, bn, (uint32_t)vid, x, U, ys, x);
   const double rq = rayleigh(om, n, x);
   if ((threadIdx.x & 63) == 0) wr[vid] = rq;
 }
@@ -681,44 +734,60 @@ __device__ __forceinline__ double block_sum_all(double x, double* red /* >= 5 */
 
 // Per matrix: Gram-Schmidt (twice) of each vector against the earlier ones of
 // its cluster -- consecutive eigenvalues whose gaps are all below tol * bnorm
-// -- then the float32 output Z (n x kq, row-major).
+// -- in place in xall; matrices without clusters only copy the Rayleigh
+// quotients.
 __global__ __launch_bounds__(256) void k_cluster_orth(int n, int kq, double* w, const double* wr,
-                                                      const double* bnorm, double* xall,
-                                                      float* Z, int64_t zstride) {
+                                                      const double* bnorm, double* xall) {
   __shared__ double red[16];
   const int mat = blockIdx.x;
   double* wm = w + (int64_t)mat * kq;
   double* xm = xall + (int64_t)mat * kq * n;
   const double tol = kClusterTol * bnorm[mat];
+  bool any = false;
+  for (int i = 1; i < kq; ++i) any = any || fabs(wm[i - 1] - wm[i]) <= tol;
   int cstart = 0;
-  for (int i = 0; i < kq; ++i) {
+  for (int i = 0; any && i < kq; ++i) {
     if (i == 0 || fabs(wm[i - 1] - wm[i]) > tol) cstart = i;
+    if (i == cstart) continue;
     double* xi = xm + (int64_t)i * n;
-    if (i > cstart) {
-      for (int pass = 0; pass < 2; ++pass) {
-        for (int jv = cstart; jv < i; ++jv) {
-          const double* xj = xm + (int64_t)jv * n;
-          double x = 0.0;
-          for (int r = threadIdx.x; r < n; r += 256) x = fma(xj[r], xi[r], x);
-          x = block_sum_all(x, red);
-          for (int r = threadIdx.x; r < n; r += 256) xi[r] = fma(-x, xj[r], xi[r]);
-          __syncthreads();
-        }
+    for (int pass = 0; pass < 2; ++pass) {
+      for (int jv = cstart; jv < i; ++jv) {
+        const double* xj = xm + (int64_t)jv * n;
         double x = 0.0;
-        for (int r = threadIdx.x; r < n; r += 256) x = fma(xi[r], xi[r], x);
+        for (int r = threadIdx.x; r < n; r += 256) x = fma(xj[r], xi[r], x);
         x = block_sum_all(x, red);
-        const double sc = 1.0 / sqrt(x);
-        for (int r = threadIdx.x; r < n; r += 256) xi[r] *= sc;
+        for (int r = threadIdx.x; r < n; r += 256) xi[r] = fma(-x, xj[r], xi[r]);
         __syncthreads();
       }
+      double x = 0.0;
+      for (int r = threadIdx.x; r < n; r += 256) x = fma(xi[r], xi[r], x);
+      x = block_sum_all(x, red);
+      const double sc = 1.0 / sqrt(x);
+      for (int r = threadIdx.x; r < n; r += 256) xi[r] *= sc;
+      __syncthreads();
     }
-    float* zm = Z + (int64_t)mat * zstride;
-    for (int r = threadIdx.x; r < n; r += 256) zm[(int64_t)r * kq + i] = (float)xi[r];
   }
   __syncthreads();
   // the Rayleigh quotients replace the bisection values once the clusters
   // (found from the latter) are done
   for (int i = threadIdx.x; i < kq; i += 256) wm[i] = wr[(int64_t)mat * kq + i];
+}
+
+// xall (per matrix kq vectors of n float64, vector-major) -> Z (n x kq
+// float32, row-major), through a 64 x 64 LDS tile: reads coalesced along
+// rows, writes coalesced along vectors.
+__global__ __launch_bounds__(256) void k_vec_out(int n, int kq, const double* xall, float* Z,
+                                                 int64_t zstride) {
+  __shared__ float tile[64][65];
+  const int r0 = blockIdx.x * 64, v0 = blockIdx.y * 64, mat = blockIdx.z;
+  const double* xm = xall + (int64_t)mat * kq * n;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int v = ty; v < 64; v += 4)
+    if (v0 + v < kq && r0 + tx < n) tile[v][tx] = (float)xm[(int64_t)(v0 + v) * n + r0 + tx];
+  __syncthreads();
+  float* zm = Z + (int64_t)mat * zstride;
+  for (int r = ty; r < 64; r += 4)
+    if (r0 + r < n && v0 + tx < kq) zm[(int64_t)(r0 + r) * kq + v0 + tx] = tile[tx][r];
 }
 
 // max |B| over the band (float64) per matrix: the scale of the pivot guard
@@ -737,7 +806,17 @@ __global__ __launch_bounds__(256) void k_band_norm(const float* orig, int64_t os
   }
 }
 
-constexpr int kInvChunk = 2048;   // vectors per inverse-iteration launch
+// vectors per inverse-iteration launch: enough wavefronts to fill every SIMD
+// several times over, with their U workspace (n x 34 float64 each) capped
+constexpr int kInvChunkMax = 8192;
+constexpr int64_t kInvWorkBytes = (int64_t)4 << 30;
+
+__host__ __forceinline__ int inv_chunk(int n, int64_t nvec) {
+  int64_t c = kInvWorkBytes / ((int64_t)n * (WC + 1) * (int64_t)sizeof(double));
+  c = c < kInvChunkMax ? c : kInvChunkMax;
+  c = c < 256 ? 256 : c;
+  return (int)(nvec < c ? nvec : c);
+}
 
 }  // namespace
 
@@ -815,7 +894,7 @@ extern "C" int scao_eig_bisect(const double* d, const double* e, int n, int batc
 extern "C" int64_t scao_eig_vectors_work(int n, int batch, int kq) {
   if (n <= 0 || batch <= 0 || kq <= 0) return 0;
   const int64_t nvec = (int64_t)batch * kq;
-  const int64_t chunk = nvec < kInvChunk ? nvec : kInvChunk;
+  const int64_t chunk = inv_chunk(n, nvec);
   // per chunk vector: U (n x 33) + ys (n); per vector: x (n) and its Rayleigh
   // quotient; per matrix: |B|
   return (chunk * (int64_t)n * (WC + 1) + nvec * ((int64_t)n + 1) + batch) *
@@ -831,7 +910,7 @@ extern "C" int scao_eig_vectors(const float* orig, int64_t ostride, int n, int b
   if (batch == 0) return SCAO_OK;
   hipStream_t s = (hipStream_t)stream;
   const int nvec = batch * kq;
-  const int chunk = nvec < kInvChunk ? nvec : kInvChunk;
+  const int chunk = inv_chunk(n, nvec);
   double* U = (double*)work;
   double* xall = U + (int64_t)chunk * n * (WC + 1);
   double* wr = xall + (int64_t)nvec * n;
@@ -844,8 +923,10 @@ extern "C" int scao_eig_vectors(const float* orig, int64_t ostride, int n, int b
                        v0, w, bnorm, U, xall, wr);
     SCAO_LAUNCH_CHECK("scao_eig_vectors/inviter");
   }
-  hipLaunchKernelGGL(k_cluster_orth, dim3(batch), dim3(256), 0, s, n, kq, w, wr, bnorm, xall, Z,
-                     zstride);
+  hipLaunchKernelGGL(k_cluster_orth, dim3(batch), dim3(256), 0, s, n, kq, w, wr, bnorm, xall);
   SCAO_LAUNCH_CHECK("scao_eig_vectors/orth");
+  hipLaunchKernelGGL(k_vec_out, dim3((n + 63) / 64, (kq + 63) / 64, batch), dim3(256), 0, s, n, kq,
+                     xall, Z, zstride);
+  SCAO_LAUNCH_CHECK("scao_eig_vectors/out");
   return SCAO_OK;
 }

@@ -26,6 +26,7 @@ from . import _lib as L
 
 NB = L.EIG_BAND
 BW = L.EIG_BANDW
+MAX_BATCH = 65535   # matrices per call: the batch is a grid dimension
 
 
 def panels(n: int) -> list:
@@ -42,6 +43,8 @@ def _check(X: Tensor) -> None:
         raise ValueError("eigen: X must be contiguous")
     if X.shape[1] > 4096 + NB:
         raise ValueError(f"eigen: n={X.shape[1]} above the supported {4096 + NB}")
+    if X.shape[0] > MAX_BATCH:
+        raise ValueError(f"eigen: batch {X.shape[0]} above {MAX_BATCH} (grid limit)")
 
 
 def _reduce(X: Tensor):

@@ -1024,7 +1024,7 @@ def _refresh_kron(kron, dev, s, eigen_only=False, ema_only=False):
     hip = EIGEN_SOLVER == "hip"
     for dim, lst in jobs.items():
         budget = EIGEN_BATCH_BYTES if hip else EIGH_BATCH_BYTES
-        per = max(1, budget // (4 * dim * dim))
+        per = min(max(1, budget // (4 * dim * dim)), eigen.MAX_BATCH)
         # vectors a factor can keep: k <= k_max (rank momentum and clamps)
         kq = min(dim, max(leaf.k_max for leaf, _ in lst))
         for b0 in range(0, len(lst), per):
