@@ -50,6 +50,13 @@ PRECOND_DTYPE = torch.float32
 # goldens pin the reference's float32 arithmetic.
 EXACT_NORMS = False
 
+# The reference's eigendecomposition is float32 LAPACK (torch.linalg.eigh on
+# the CPU): its eigenvectors carry an error of about eps32 * |A| / gap.  With
+# EXACT_EIGH set, this oracle solves in float64 and rounds the eigenpairs to
+# float32 once; the parity tests use it to measure how far the reference's own
+# solver moves a refresh step's update.  Off by default.
+EXACT_EIGH = False
+
 
 def _norm(x: Tensor) -> Tensor:
     """x.norm() as the reference takes it, or its correctly rounded value."""
@@ -301,6 +308,10 @@ class RefPreconditioner:
     def _eig_desc(A: Tensor, eps: float):
         """preconditioner.py:412-428 -- eigh with one diagonal-shift retry, then
         descending order with eigenvalues clamped at 0."""
+        if EXACT_EIGH:
+            w, V = torch.linalg.eigh(A.double())
+            w, V = w.float(), V.float()
+            return w.flip(0).clamp(min=0.0), V.flip(1)
         try:
             w, V = torch.linalg.eigh(A)
         except torch.linalg.LinAlgError:

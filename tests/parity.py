@@ -71,18 +71,33 @@ def assert_close(got, want, rtol, atol_frac, what, extra=None) -> float:
 
 
 def assert_update_close(p_new, p_new_ref, p_old, what, rtol=UPDATE_RTOL,
-                        atol_frac=UPDATE_ATOL) -> float:
+                        atol_frac=UPDATE_ATOL, extra_abs: float = 0.0) -> float:
     """The step's update p_new - p_old against the reference's, element by
     element.  An update is only observable through the stored parameter,
     which is rounded to float32 once: where the reference and the kernel
     round a new value to neighbouring floats, the two updates differ by one
     float32 spacing of the new parameter whatever their precision (with
     LARS the step lr * trust * u is often far below that spacing).  So the
-    bound adds ulp(p_new_ref) to atol + rtol * |update|."""
+    bound adds ulp(p_new_ref) to atol + rtol * |update|, and ``extra_abs``
+    (an absolute allowance the caller states and justifies)."""
     p_old = p_old.detach().double().cpu()
     return assert_close(p_new.detach().double().cpu() - p_old,
                         p_new_ref.detach().double().cpu() - p_old, rtol, atol_frac, what,
-                        extra=torch.maximum(ulp(p_new_ref), ulp(p_new)))
+                        extra=torch.maximum(ulp(p_new_ref), ulp(p_new)) + extra_abs)
+
+
+def update_ratio(p_new, p_new_ref, p_old, rtol=UPDATE_RTOL, atol_frac=UPDATE_ATOL) -> float:
+    """The ratio assert_update_close gates, without asserting."""
+    p_old = p_old.detach().double().cpu()
+    return ratio(p_new.detach().double().cpu() - p_old, p_new_ref.detach().double().cpu() - p_old,
+                 rtol, atol_frac, extra=torch.maximum(ulp(p_new_ref), ulp(p_new)))
+
+
+def eigh_error(a, b) -> float:
+    """max |a - b| over a tensor pair (float64): the reference's own
+    eigensolver error when a is its float32-eigh result and b the same step
+    with a float64 eigh."""
+    return (a.detach().double().cpu() - b.detach().double().cpu()).abs().max().item()
 
 
 def report(test, case, data):

@@ -211,16 +211,33 @@ def test_step_from_shared_state(case):
     the tensor's largest element).  On refresh steps the GPU's new EMA is
     checked (codes within 1 LSB, scales within 1e-6) and then replaced by the
     reference's, so the eigen stage and the update start from identical
-    inputs and meet the same bar."""
+    inputs.
+
+    A refresh step's update is a function of eigenvectors, which a float32
+    solver delivers to about eps32 * |A| / gap: the reference's float32 LAPACK
+    eigh moves the update away from the exact-eigh one (the oracle with a
+    float64 eigh, rounded once) by E_ref, measured here on every refresh step
+    and tensor (up to 2.7x the elementwise bound on the 20-32 dimensional
+    blocks of fp32_small).  No implementation can reproduce LAPACK's rounding,
+    so a refresh step's bound is the north star's plus 2 * E_ref: the
+    reference's own error, and the same budget for the GPU's solver (triangle
+    inequality through the exact update).  The GPU's distance to the exact
+    update under the plain bound is reported beside it."""
     from scao_amd import engine
     dev = _dev()
     shapes, cfg, steps = CASES[case]
     rp = make_params(shapes)
     ref = R.RefSCAO(list(rp.values()), **cfg, **PARITY)
-    worst, worst_m, emas = {}, 0.0, 0
+    worst, worst_m, emas, exact = {}, 0.0, 0, {}
     for t in range(1, steps + 1):
         print(f"case={case} step={t}", flush=True)
+        refreshed = t % cfg["precond_freq"] == 0
         gp, gopt = _gpu_from_oracle(ref, rp, cfg, dev)
+        ex_p = ex = None
+        if refreshed:
+            ex_p = {k: torch.nn.Parameter(v.detach().clone()) for k, v in rp.items()}
+            ex = R.RefSCAO(list(ex_p.values()), **cfg, **PARITY)
+            ex.load_state_dict(copy.deepcopy(ref.state_dict()))
         pairs = {}
         for k in shapes:
             pa = ref.state[rp[k]].get("preconditioner")
@@ -233,7 +250,15 @@ def test_step_from_shared_state(case):
         for k in shapes:
             rp[k].grad = grads[k].clone()
             gp[k].grad = grads[k].to(dev)
+            if ex is not None:
+                ex_p[k].grad = grads[k].clone()
         ref.step()
+        if ex is not None:
+            R.EXACT_EIGH = True
+            try:
+                ex.step()
+            finally:
+                R.EXACT_EIGH = False
         hook = P.IdenticalPostEma(pairs)
         engine.AFTER_EMA_HOOK = hook
         try:
@@ -242,19 +267,26 @@ def test_step_from_shared_state(case):
             engine.AFTER_EMA_HOOK = None
         torch.cuda.synchronize()
         emas += hook.checked
-        refreshed = t % cfg["precond_freq"] == 0
         # the preconditioner state first: a refresh's eigen stage, compared
         # from identical inputs, is checked before the update it feeds
         for (kr, pr), (kg, pg) in zip(ref.state.items(), gopt.state.items()):
             _cmp_precond(pr["preconditioner"], pg["preconditioner"], t, refreshed)
         for k in shapes:
+            e_ref = P.eigh_error(rp[k], ex_p[k]) if ex is not None else 0.0
             r = P.assert_update_close(gp[k], rp[k], before[k],
-                                      f"step {t} param {k} update (refresh={refreshed})")
+                                      f"step {t} param {k} update (refresh={refreshed}, "
+                                      f"E_ref={e_ref:.3g})", extra_abs=2.0 * e_ref)
             worst[(k, refreshed)] = max(worst.get((k, refreshed), 0.0), r)
             st_r, st_g = ref.state[rp[k]], gopt.state[gp[k]]
+            if ex is not None:
+                x = exact.setdefault(k, [0.0, 0.0])
+                x[0] = max(x[0], P.update_ratio(gp[k], ex_p[k], before[k]))
+                x[1] = max(x[1], P.update_ratio(rp[k], ex_p[k], before[k]))
             for key in ("exp_avg", "exp_avg_sq", "exp_avg_diff", "prev_grad"):
+                e_m = P.eigh_error(st_r[key], ex.state[ex_p[k]][key]) if ex is not None else 0.0
                 worst_m = max(worst_m, P.assert_close(st_g[key], st_r[key], P.MOMENT_RTOL,
-                                                      P.MOMENT_ATOL, f"step {t} {k} {key}"))
+                                                      P.MOMENT_ATOL, f"step {t} {k} {key}",
+                                                      extra=2.0 * e_m))
             assert st_g["step"] == st_r["step"] and st_g["scao_step"] == st_r["scao_step"]
             assert st_g.get("scao_phase_started") == st_r.get("scao_phase_started")
         # the oracle's norms are the reference's fp32 CPU reductions; over n
@@ -265,7 +297,10 @@ def test_step_from_shared_state(case):
         assert gopt._global_norm_ema == pytest.approx(ref._global_norm_ema, rel=gn_tol)
     report("step_from_shared_state", case,
            {**{f"{k}{'/refresh' if r else ''}": v for (k, r), v in worst.items()},
-            "moments": worst_m, "emas_checked": emas, "gate": "elementwise ratio <= 1"})
+            **{f"{k}/refresh gpu_vs_exact_eigh": v[0] for k, v in exact.items()},
+            **{f"{k}/refresh ref_vs_exact_eigh": v[1] for k, v in exact.items()},
+            "moments": worst_m, "emas_checked": emas,
+            "gate": "elementwise ratio <= 1 (refresh steps: + 2 E_ref)"})
 
 
 _PROJ_ERR = [0.0]
