@@ -53,7 +53,7 @@ CONFIGS = {
                                     ("o", (2048, 2048)), ("gate", (11008, 2048)),
                                     ("up", (11008, 2048)), ("down", (2048, 11008))],
                    vecs=[("in_norm", 2048), ("post_norm", 2048)], extra=[("final_norm", (2048,))],
-                   k=128, D=2048),
+                   k=128, D=2048, outliers=(0.01, 50.0)),
     "llama8b": dict(layers=32, mats=[("q", (4096, 4096)), ("k", (1024, 4096)),
                                      ("v", (1024, 4096)), ("o", (4096, 4096)),
                                      ("gate", (14336, 4096)), ("up", (14336, 4096)),
@@ -90,31 +90,93 @@ def leaves_of(shape, D):
     return out
 
 
+# kernel sources whose code a traffic measurement belongs to
+TRAFFIC_SOURCES = ("scao_amd/csrc/kron.hip", "scao_amd/csrc/scao_common.hpp",
+                   "scao_amd/csrc/elementwise.hip")
+
+
+def source_stamp() -> str:
+    """sha256 (first 16 hex digits) over the kernel sources of the step."""
+    import hashlib
+    h = hashlib.sha256()
+    for rel in TRAFFIC_SOURCES:
+        with open(os.path.join(ROOT, rel), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def _profiled_traffic(kernel: str, config: str):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
-    WRITE_SIZE summary (calibrated against a 1 GiB copy), or None."""
+    WRITE_SIZE summary (calibrated against a 1 GiB copy), if that summary was
+    measured on the kernel sources as they are now (its source stamp matches);
+    otherwise None: a stale measurement is not reported."""
     name = kernel.replace("scao_", "")
     path = os.path.join(ROOT, "profiles", f"{name}_{config}_traffic.md")
     if not os.path.exists(path):
         return None
+    value, stamp = None, None
     for line in open(path):
         if line.startswith(f"traffic_bytes_per_launch {name} {config}:"):
-            return float(line.split(":")[1])
-    return None
+            value = float(line.split(":")[1])
+        if line.startswith("source_stamp:"):
+            stamp = line.split(":")[1].strip()
+    return value if stamp == source_stamp() else None
+
+
+def usable_cores() -> int:
+    """Cores this process may run on: the affinity set, capped by a cgroup v2
+    CPU quota when one is set."""
+    n = len(os.sched_getaffinity(0))
+    try:
+        quota, period = open("/sys/fs/cgroup/cpu.max").read().split()
+        if quota != "max":
+            n = min(n, max(1, int(int(quota) // int(period))))
+    except (OSError, ValueError):
+        pass
+    return n
+
+
+def host_description() -> str:
+    import torch
+    model = platform.processor() or platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    blas = "unknown BLAS"
+    for line in torch.__config__.parallel_info().splitlines():
+        if "Math Kernel Library" in line:
+            blas = line.strip().split(" for ")[0]
+            break
+    return f"cpu={model}, torch {torch.__version__}, {blas}"
 
 
 def cpu_baseline(cfg, args):
-    """The oracle (torch on the host CPU) on a bounded sample: one layer's
-    preconditioned matrices, steady Phase-2 steps (eye-initialised factors,
-    no refresh -- the same kernels' worth of work per step)."""
+    """The oracle (the reference's algorithm in torch, on the host CPU) on a
+    bounded sample of the workload: one layer's preconditioned matrices plus
+    1/layers of the Adam-path group (the layer's norm vectors and that share
+    of the embedding rows), steady Phase-2 steps (eye-initialised factors, no
+    refresh -- the same kernels' worth of work per step as a refreshed one)."""
     import torch
     from oracle import scao_ref as R
-    cores = min(len(os.sched_getaffinity(0)), args.cpu_threads)
+    cores = usable_cores() if args.cpu_threads <= 0 else args.cpu_threads
     torch.set_num_threads(cores)
     g = torch.Generator().manual_seed(0)
-    params = [torch.nn.Parameter(torch.randn(s, generator=g) * 0.02) for _, s in cfg["mats"]]
+    pre_shapes = [s for _, s in cfg["mats"]]
+    adam_shapes = [(d,) for _, d in cfg["vecs"]]
+    for _, s in cfg["extra"]:
+        if len(s) == 2:   # a 1/layers share of the rows
+            adam_shapes.append((max(1, s[0] // cfg["layers"]), s[1]))
+    pre = [torch.nn.Parameter(torch.randn(s, generator=g) * 0.02) for s in pre_shapes]
+    adam = [torch.nn.Parameter(torch.randn(s, generator=g) * 0.02) for s in adam_shapes]
+    params = pre + adam
     nparam = sum(p.numel() for p in params)
-    opt = R.RefSCAO(params, k_min=cfg["k"], k_max=cfg["k"], max_precond_dim=cfg["D"],
+    opt = R.RefSCAO([{"params": pre},
+                     {"params": adam, "warmup_steps": 10 ** 9, "precond_freq": 10 ** 9}],
+                    k_min=cfg["k"], k_max=cfg["k"], max_precond_dim=cfg["D"],
                     warmup_steps=0, min_precond_updates=0, precond_freq=10 ** 9, **PROFILE)
     grads = [torch.randn(p.shape, generator=g) * 1e-3 for p in params]
     for p, gr in zip(params, grads):
@@ -126,11 +188,72 @@ def cpu_baseline(cfg, args):
         opt.step()
         n += 1
     dt = (time.perf_counter() - t0) / n
+    npre = sum(p.numel() for p in pre)
     return {"value": nparam / dt, "unit": "params/s", "cores": cores, "kind": "port",
-            "sample": f"oracle (torch {torch.__version__} CPU fp32) steady Phase-2 step on one "
-                      f"layer's {len(params)} preconditioned matrices ({nparam / 1e6:.2f}M "
-                      f"params), {n} steps, {dt * 1e3:.0f} ms/step, "
-                      f"cpu={platform.processor() or platform.machine()}"}
+            "sample": f"oracle (reference algorithm, torch CPU fp32) steady Phase-2 step on one "
+                      f"layer's {len(pre)} preconditioned matrices ({npre / 1e6:.2f}M params) "
+                      f"plus 1/{cfg['layers']} of the Adam-path group "
+                      f"({(nparam - npre) / 1e6:.2f}M params): {nparam / 1e6:.2f}M params, "
+                      f"{n} steps, {dt * 1e3:.0f} ms/step, {cores} threads, "
+                      f"{host_description()}"}
+
+
+def pmc_summary(fetch_csv: str, write_csv: str, config: str, copy_mib: int, cmd: str) -> str:
+    """Markdown traffic summary from two rocprofv3 --pmc runs (FETCH_SIZE, then
+    WRITE_SIZE; counter_collection.csv each).  Counters are KiB per dispatch;
+    each is scaled by what it reads for the run's plain copy of copy_mib MiB
+    (the largest __amd_rocclr_copyBuffer dispatch).  The dominant entry
+    point's kernel is the k_apply variant with the most traffic."""
+    import csv
+    import re
+
+    def load(path, counter):
+        per = {}
+        for row in csv.DictReader(open(path)):
+            if row.get("Counter_Name") != counter:
+                continue
+            name = re.sub(r"\(.*", "", row["Kernel_Name"].replace("(anonymous namespace)::", ""))
+            name = name.replace("void ", "").strip()
+            d = per.setdefault(name, {"n": 0, "kib": 0.0, "max": 0.0})
+            v = float(row["Counter_Value"])
+            d["n"] += 1
+            d["kib"] += v
+            d["max"] = max(d["max"], v)
+        return per
+
+    fe, wr = load(fetch_csv, "FETCH_SIZE"), load(write_csv, "WRITE_SIZE")
+    copy_kib = copy_mib * 1024.0
+    ff = copy_kib / fe["__amd_rocclr_copyBuffer"]["max"]
+    wf = copy_kib / wr["__amd_rocclr_copyBuffer"]["max"]
+    rows = []
+    for name in sorted(set(fe) | set(wr)):
+        if name == "__amd_rocclr_copyBuffer":
+            continue
+        f, w = fe.get(name, {"n": 0, "kib": 0.0}), wr.get(name, {"n": 0, "kib": 0.0})
+        n = max(f["n"], w["n"])
+        rows.append((name, n, f["kib"], w["kib"], f["kib"] * ff * 1024 / 1e9,
+                     w["kib"] * wf * 1024 / 1e9))
+    rows.sort(key=lambda r: -(r[4] + r[5]))
+    apply_rows = [r for r in rows if r[0].startswith("k_apply")]
+    dom = apply_rows[0]
+    per_launch = (dom[4] + dom[5]) * 1e9 / dom[1]
+    out = [f"# HBM traffic per dispatch (rocprofv3 PMC), {config}", "",
+           "Commands (two counter runs, then this summary; from the repository root on the box):",
+           "", "```", cmd, "```", "",
+           f"Calibration: the {copy_mib} MiB plain copy (one `__amd_rocclr_copyBuffer` dispatch) "
+           f"reads FETCH_SIZE = {fe['__amd_rocclr_copyBuffer']['max']:.0f} KiB and WRITE_SIZE = "
+           f"{wr['__amd_rocclr_copyBuffer']['max']:.0f} KiB for {copy_kib:.0f} KiB moved each way: "
+           f"fetch factor {ff:.4f}, write factor {wf:.4f} (counter KiB x factor = true KiB).", "",
+           "| kernel | dispatches | FETCH KiB (raw) | WRITE KiB (raw) | read GB (scaled) "
+           "| written GB (scaled) |", "|---|---:|---:|---:|---:|---:|"]
+    for name, n, fk, wk, rg, wg in rows:
+        out.append(f"| `{name}` | {n} | {fk:.0f} | {wk:.0f} | {rg:.2f} | {wg:.2f} |")
+    out += ["", f"Dominant kernel `{dom[0]}`: {per_launch / 1e9:.3f} GB per launch "
+                f"({dom[4] * 1e9 / dom[1] / 1e9:.3f} GB read, {dom[5] * 1e9 / dom[1] / 1e9:.3f} GB "
+                f"written).", "",
+            f"traffic_bytes_per_launch kron_apply {config}: {per_launch:.0f}",
+            f"source_stamp: {source_stamp()}", ""]
+    return "\n".join(out)
 
 
 def main():
@@ -140,11 +263,17 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", default="llama1b", choices=list(CONFIGS))
     ap.add_argument("--cpu-baseline", type=int, default=1)
-    ap.add_argument("--cpu-threads", type=int, default=16)
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="threads of the CPU baseline (0: every core this process may use)")
     ap.add_argument("--cpu-steps", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=10.0,
                     help="time the CPU baseline for at least this long (bounded sample)")
     ap.add_argument("--details", default=None, help="write the full report JSON here")
+    ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"), default=None,
+                    help="print the markdown traffic summary of two rocprofv3 --pmc runs "
+                         "(FETCH_SIZE, WRITE_SIZE) of this bench and exit (no GPU use)")
+    ap.add_argument("--pmc-command", default="",
+                    help="the commands that made the --pmc-summary inputs (recorded verbatim)")
     ap.add_argument("--dominant", default="scao_kron_apply",
                     help="entry point timed with HIP events inside the timed region")
     ap.add_argument("--no-refresh", action="store_true",
@@ -160,6 +289,10 @@ def main():
                          "gradient filter and noise (sparsity=0.7, noise_std=0.01), reported "
                          "in details (0: skip)")
     args = ap.parse_args()
+    if args.pmc_summary:
+        print(pmc_summary(*args.pmc_summary, args.config, args.copy_probe_mib or 1024,
+                          args.pmc_command))
+        return
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build runs the SCAO step on one GPU; --gpus {args.gpus} "
@@ -184,7 +317,15 @@ def main():
     allp = pre_p + adam_p
     nparams = sum(p.numel() for p in allp)
     n_pre = sum(p.numel() for p in pre_p)
-    grad_sets = [[make(p.shape, 1e-3) for p in allp] for _ in range(2)]
+    def make_grad(shape):
+        g = make(shape, 1e-3)
+        if "outliers" in cfg:           # heavy tails: a fraction of elements scaled up
+            frac, mult = cfg["outliers"]
+            hit = torch.rand(shape, generator=gen, device=dev) < frac
+            g = torch.where(hit, g * mult, g)
+        return g
+
+    grad_sets = [[make_grad(p.shape) for p in allp] for _ in range(2)]
 
     def set_grads(i):
         for p, gr in zip(allp, grad_sets[i % 2]):
@@ -343,6 +484,9 @@ def main():
             "peak": peak / (1e9 if bound == "hbm" else 1e12),
             "unit": "GB/s" if bound == "hbm" else "TFLOP/s",
             "frac": achieved / peak, "traffic": _profiled_traffic(dom, args.config),
+            "traffic_source": f"profiles/{dom.replace('scao_', '')}_{args.config}_traffic.md "
+                              f"(counters; null unless measured at source stamp "
+                              f"{source_stamp()})",
             "avg_ms": dom_timing[dom][1]}
     step_bytes = 44.0 * n_pre + 32.0 * (nparams - n_pre)
     step_flops = sum(proj_flops(m, n, k) for m, n in n_leaf)
@@ -382,7 +526,12 @@ def main():
         "data": "synthetic",
         "config": {"workload": f"{args.config}: SCAO steady Phase-2 step (no refresh), "
                                f"{nparams / 1e6:.2f}M fp32 params, {len(n_leaf)} Kronecker "
-                               f"blocks, int8 EMA, k={k}, max_precond_dim={cfg['D']}",
+                               f"blocks, int8 EMA, k={k}, max_precond_dim={cfg['D']}"
+                               + (f", grads with {cfg['outliers'][0]:.0%} outliers "
+                                  f"x{cfg['outliers'][1]:g}" if "outliers" in cfg else ""),
+                   "timing": "ms_per_step = wall time of K consecutive steps between two "
+                             "device synchronisations, / K; the median of per-step event "
+                             "pairs is details.step_median_ms",
                    "global_batch": None, "seq_len": None, "parallelism": "single-gpu"},
         "roofline": roof,
         "cpu_baseline": cpu,
