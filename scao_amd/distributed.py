@@ -1,7 +1,7 @@
-"""Distributed helpers (reference: scao/distributed.py:37-160, the broadcast
-of scao/optimizer.py:686-710 and scao/preconditioner.py:647-719).
+"""The preconditioner broadcast over torch.distributed (reference:
+scao/optimizer.py:686-710 and scao/preconditioner.py:647-719).
 
-The measured path runs on one GPU; these helpers run over any initialised
+The measured path runs on one GPU; the broadcast runs over any initialised
 torch.distributed group.  Instead of one collective per tensor they move
 flat buckets, one per dtype: first the integer metadata (step counters,
 adaptive ranks) so that every rank can size its buffers, then the payload.
@@ -12,12 +12,9 @@ they stay on the device.
 
 from __future__ import annotations
 
-import warnings
-
 import torch
 
 from .preconditioner import PRECOND_DTYPE
-from .utils import dequantize_sym_int8, quantize_sym_int8
 
 _MOMENTS = ("exp_avg", "exp_avg_sq", "exp_avg_diff")   # the keys the reference broadcasts
 
@@ -166,89 +163,3 @@ def broadcast_state(optimizer, process_group=None) -> None:
             if node.use_block_diagonal:
                 node._k = sum(b._k for b in node._blocks) // max(len(node._blocks), 1)
     _touch_all(optimizer, pres)
-
-
-# --------------------------------------------------------------------------
-# averaging across ranks (sync_preconditioners)
-# --------------------------------------------------------------------------
-
-def sync_preconditioners(optimizer, process_group=None) -> None:
-    """scao/distributed.py:60-128: every rank's preconditioners become the
-    mean over ranks of the eigenfactors (U_l, S_l, U_r, S_r), the fp32 EMAs
-    and the diagonal EMAs; int8 EMAs are dequantised, averaged and
-    requantised (scale = max|x|/127).  A no-op without an initialised group
-    or with one rank.  Every rank must hold the same shapes (same parameters,
-    same adaptive ranks): that is checked first, so that a mismatch raises
-    instead of leaving a collective waiting."""
-    import torch.distributed as dist
-    if not dist.is_available() or not dist.is_initialized():
-        return
-    world = dist.get_world_size(group=process_group)
-    if world == 1:
-        return
-    pres = [st["preconditioner"] for st in _states(optimizer)
-            if st.get("preconditioner") is not None]
-    f32, q8 = [], []
-    for pre in pres:
-        for node in _nodes(pre):
-            if node.use_block_diagonal:
-                continue
-            if node.use_kronecker:
-                f32 += [node.U_l, node.S_l, node.U_r, node.S_r]
-                if node.use_int8_ema:
-                    q8.append(node)
-                else:
-                    f32 += [node.L_ema, node.R_ema]
-            else:
-                f32.append(node.diag_ema)
-    deq = [dequantize_sym_int8(q, s) for n in q8
-           for q, s in ((n.L_ema_q, n.L_ema_scale), (n.R_ema_q, n.R_ema_scale))]
-    dev = _bucket_device(f32 + deq, process_group)
-    sizes = torch.tensor([sum(t.numel() for t in f32), sum(t.numel() for t in deq)],
-                         dtype=torch.int64, device=dev)
-    lo, hi = sizes.clone(), sizes.clone()
-    dist.all_reduce(lo, op=dist.ReduceOp.MIN, group=process_group)
-    dist.all_reduce(hi, op=dist.ReduceOp.MAX, group=process_group)
-    if not torch.equal(lo, hi):
-        raise ValueError("sync_preconditioners: ranks hold preconditioners of different "
-                         f"sizes ({lo.tolist()} vs {hi.tolist()} elements)")
-    buf = _flat(f32 + deq, torch.float32, dev)
-    if buf is None:
-        return
-    dist.all_reduce(buf, op=dist.ReduceOp.SUM, group=process_group)
-    buf.div_(world)
-    nf = sizes[0].item()
-    _unflat(buf[:nf], f32)
-    off = nf
-    for n in q8:
-        for side in ("L", "R"):
-            src = getattr(n, f"{side}_ema_q")
-            m = src.numel()
-            x = buf[off:off + m].view(src.shape).to(device=src.device)
-            off += m
-            q, s = quantize_sym_int8(x)
-            src.copy_(q)
-            setattr(n, f"{side}_ema_scale", s)
-    _touch_all(optimizer, pres)
-
-
-def wrap_scao_for_fsdp(optimizer):
-    """scao/distributed.py:131-160: ``step`` also averages the preconditioners
-    on refresh steps."""
-    try:
-        from torch.distributed.fsdp import FullyShardedDataParallel  # noqa: F401
-    except ImportError:
-        warnings.warn("torch.distributed.fsdp not available; FSDP wrapping skipped.")
-        return optimizer
-    original_step = optimizer.step
-
-    def patched_step(closure=None):
-        result = original_step(closure)
-        step = next((s.get("step", 0) for s in optimizer.state.values() if "step" in s), 0)
-        if step % optimizer.defaults["precond_freq"] == 0:
-            optimizer.synchronize_precond()
-            sync_preconditioners(optimizer)
-        return result
-
-    optimizer.step = patched_step
-    return optimizer

@@ -1,80 +1,19 @@
-"""Callback metrics and loggers (reference: scao/logging.py:61-219).
+"""Callback metrics (reference: scao/logging.py:151-219).
 
-Computed only when a callback is registered.  ``scao/L_norm_mean`` for int8
+Computed only when a callback is registered; a callback is any callable
+taking the metrics dict.  ``scao/L_norm_mean`` for int8
 EMAs uses ``scale * 127`` as the reference does; the per-block values are
 gathered on the device and read back in one transfer.
 """
 
 from __future__ import annotations
 
-import math
 from typing import Callable
 
 import torch
 
 MetricsDict = dict
 Callback = Callable[[MetricsDict], None]
-
-
-class ConsoleLogger:
-    """reference :61-86."""
-
-    def __init__(self, log_every: int = 100, prefix: str = "[SCAO]") -> None:
-        self.log_every = log_every
-        self.prefix = prefix
-
-    def __call__(self, metrics: MetricsDict) -> None:
-        step = metrics.get("step", 0)
-        if isinstance(step, int) and step % self.log_every != 0:
-            return
-        parts = [f"step={step}"]
-        for k, v in metrics.items():
-            if k == "step":
-                continue
-            parts.append(f"{k}={v:.4f}" if isinstance(v, float) else f"{k}={v}")
-        print(f"{self.prefix} " + "  ".join(parts))
-
-
-class TensorBoardLogger:
-    """reference :89-121."""
-
-    def __init__(self, writer, log_every: int = 50, tag_prefix: str = "") -> None:
-        self.writer = writer
-        self.log_every = log_every
-        self.tag_prefix = tag_prefix
-
-    def __call__(self, metrics: MetricsDict) -> None:
-        step = metrics.get("step", 0)
-        if isinstance(step, int) and step % self.log_every != 0:
-            return
-        for k, v in metrics.items():
-            if k == "step":
-                continue
-            if isinstance(v, (bool, int, float)):
-                x = float(v)
-            else:
-                continue
-            if math.isnan(x):
-                continue
-            self.writer.add_scalar(f"{self.tag_prefix}{k}" if self.tag_prefix else k, x,
-                                   global_step=step)
-
-
-class WandbLogger:
-    """reference :124-144 (no-op when wandb is not importable)."""
-
-    def __init__(self, log_every: int = 50) -> None:
-        self.log_every = log_every
-
-    def __call__(self, metrics: MetricsDict) -> None:
-        step = metrics.get("step", 0)
-        if isinstance(step, int) and step % self.log_every != 0:
-            return
-        try:
-            import wandb  # type: ignore[import]
-            wandb.log({k: v for k, v in metrics.items() if k != "step"}, step=step)
-        except ImportError:
-            pass
 
 
 def _l_norm_device(pre):

@@ -61,19 +61,6 @@ def _fake_optimizer(rank: int, int8: bool, k: int = 8, k_other=None):
     return types.SimpleNamespace(param_groups=[{"params": params}], state=state)
 
 
-def _leaf_tensors(opt):
-    out = []
-    for st in D._states(opt):
-        for node in _nodes(st["preconditioner"]):
-            if node.use_block_diagonal:
-                continue
-            if node.use_kronecker:
-                out.append((node, ("U_l", "S_l", "U_r", "S_r")))
-            else:
-                out.append((node, ("diag_ema",)))
-    return out
-
-
 def _check_broadcast(rank: int, int8: bool) -> None:
     mine = _fake_optimizer(rank, int8, k_other=6 if rank else None)
     src = _fake_optimizer(0, int8)
@@ -103,35 +90,7 @@ def _check_broadcast(rank: int, int8: bool) -> None:
                 assert torch.equal(a.diag_ema, b.diag_ema)
 
 
-def _check_average(rank: int, world: int, int8: bool) -> None:
-    mine = _fake_optimizer(rank, int8)
-    ranks = [_fake_optimizer(r, int8) for r in range(world)]
-    D.sync_preconditioners(mine)
-    per_rank = [_leaf_tensors(o) for o in ranks]
-    for j, (node, names) in enumerate(_leaf_tensors(mine)):
-        for name in names:
-            want = sum(getattr(pr[j][0], name) for pr in per_rank) / world
-            assert torch.allclose(getattr(node, name), want, rtol=1e-6, atol=1e-7), name
-        if node.use_kronecker:
-            for side in ("L", "R"):
-                if int8:
-                    deq = sum(getattr(pr[j][0], f"{side}_ema_q").float()
-                              * getattr(pr[j][0], f"{side}_ema_scale") for pr in per_rank) / world
-                    amax = deq.abs().max().item()
-                    assert getattr(node, f"{side}_ema_scale") == pytest.approx(amax / 127,
-                                                                               rel=1e-6)
-                    back = getattr(node, f"{side}_ema_q").float() * (amax / 127)
-                    assert (back - deq).abs().max().item() <= 0.5 * amax / 127 * (1 + 1e-5)
-                else:
-                    want = sum(getattr(pr[j][0], f"{side}_ema") for pr in per_rank) / world
-                    assert torch.allclose(getattr(node, f"{side}_ema"), want, rtol=1e-6)
-
-
 def _check_mismatch(rank: int) -> None:
-    # different adaptive ranks: averaging refuses on every rank
-    mine = _fake_optimizer(rank, False, k_other=6 if rank else None)
-    with pytest.raises(ValueError, match="different sizes"):
-        D.sync_preconditioners(mine)
     # a rank that has not stepped: the broadcast refuses on every rank
     mine = _fake_optimizer(rank, False)
     if rank:
@@ -147,9 +106,6 @@ def _worker(rank: int, world: int, port: int, what: str) -> None:
         if what == "broadcast":
             _check_broadcast(rank, int8=False)
             _check_broadcast(rank, int8=True)
-        elif what == "average":
-            _check_average(rank, world, int8=False)
-            _check_average(rank, world, int8=True)
         else:
             _check_mismatch(rank)
         dist.barrier()
@@ -163,19 +119,16 @@ def _port() -> int:
         return s.getsockname()[1]
 
 
-@pytest.mark.parametrize("what", ["broadcast", "average", "mismatch"])
+@pytest.mark.parametrize("what", ["broadcast", "mismatch"])
 def test_two_rank_gloo(what):
     mp.spawn(_worker, args=(2, _port(), what), nprocs=2, join=True)
 
 
 def test_without_a_process_group():
-    """Averaging is a no-op and the optimizer's broadcast only warns when
-    torch.distributed is not initialised (reference behaviour)."""
+    """The optimizer's broadcast only warns when torch.distributed is not
+    initialised (reference behaviour)."""
     assert not dist.is_initialized()
     opt = _fake_optimizer(0, True)
-    before = [t.clone() for st in D._states(opt) for t in (st["exp_avg"],)]
-    D.sync_preconditioners(opt)
-    assert all(torch.equal(a, st["exp_avg"]) for a, st in zip(before, D._states(opt)))
     from scao_amd.optimizer import SCAO
     with pytest.warns(RuntimeWarning, match="not initialised"):
         SCAO.sync_preconditioner(opt)

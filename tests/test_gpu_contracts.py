@@ -320,13 +320,12 @@ def test_callbacks(dev, capsys):
     m(x).sum().backward()
     opt.step()
     assert calls == []
-    from scao_amd.logging import ConsoleLogger
     opt = SCAO(m.parameters(), lr=1e-3, precond_freq=2)
-    opt.add_callback(ConsoleLogger(log_every=1))
+    opt.add_callback(lambda mt: print("metrics", sorted(mt)))
     opt.zero_grad()
     m(x).sum().backward()
     opt.step()
-    assert "[SCAO]" in capsys.readouterr().out
+    assert "metrics" in capsys.readouterr().out
 
 
 # -- TestTorchCompile (test_optimizer.py:587-611)
@@ -384,26 +383,6 @@ def test_block_diagonal(dev):
         assert not p.isnan().any() and not p.isinf().any()
 
 
-# -- TestDistributed (test_optimizer.py:686-721)
-def test_distributed_noops(dev):
-    from scao_amd.distributed import sync_preconditioners, wrap_scao_for_fsdp
-    m = nn.Linear(16, 8).to(dev)
-    opt = SCAO(m.parameters(), lr=1e-3, warmup_steps=0, precond_freq=1)
-    opt.zero_grad()
-    m(torch.randn(4, 16, device=dev)).sum().backward()
-    opt.step()
-    sync_preconditioners(opt)
-    with warnings.catch_warnings():
-        warnings.simplefilter("ignore")
-        assert wrap_scao_for_fsdp(SCAO(m.parameters(), lr=1e-3)) is not None
-    m = nn.Linear(256, 64).to(dev)
-    opt = SCAO(m.parameters(), lr=1e-3, warmup_steps=0, precond_freq=1, max_precond_dim=64)
-    opt.zero_grad()
-    m(torch.randn(4, 256, device=dev)).sum().backward()
-    opt.step()
-    sync_preconditioners(opt)
-
-
 def _same_precond(a, b) -> None:
     """Portable preconditioner states equal, int8 scales up to fp32 rounding."""
     assert a.keys() == b.keys()
@@ -422,14 +401,13 @@ def _same_precond(a, b) -> None:
 
 
 def test_sync_preconditioner_single_rank_gloo(dev):
-    """The broadcast and the averaging over a one-rank gloo group: device
+    """The broadcast over a one-rank gloo group: device
     state goes through host buckets and comes back unchanged (the int8 scales
     rounded to fp32, as the reference's broadcast leaves them), and the next
     step runs on the rebuilt step structure."""
     import socket
 
     import torch.distributed as dist
-    from scao_amd.distributed import sync_preconditioners
     with socket.socket() as sk:
         sk.bind(("127.0.0.1", 0))
         port = sk.getsockname()[1]
@@ -448,7 +426,6 @@ def test_sync_preconditioner_single_rank_gloo(dev):
             opt.step()
         before = copy.deepcopy(opt.state_dict())
         opt.sync_preconditioner()
-        sync_preconditioners(opt)         # one rank: a no-op
         after = opt.state_dict()
         for i, st in before["state"].items():
             for key in ("exp_avg", "exp_avg_sq", "exp_avg_diff", "prev_grad"):

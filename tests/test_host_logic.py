@@ -473,36 +473,6 @@ def test_reference_checkpoint_through_safe_torch_load():
     assert isinstance(again["state"][0]["preconditioner"], SparsePreconditioner)
 
 
-def test_tensorboard_logger_scalars():
-    """scao/logging.py:89-121: numbers and booleans as scalars under the tag
-    prefix, NaN and non-numbers skipped, only every log_every steps."""
-    from scao_amd.logging import TensorBoardLogger
-
-    class Writer:
-        def __init__(self):
-            self.calls = []
-
-        def add_scalar(self, tag, value, global_step=None):
-            self.calls.append((tag, value, global_step))
-
-    w = Writer()
-    log = TensorBoardLogger(w, log_every=10, tag_prefix="opt/")
-    log({"step": 7, "a": 1.0})
-    assert w.calls == []
-    log({"step": 20, "a": 1.5, "n": 3, "flag": True, "bad": float("nan"), "s": "text"})
-    assert w.calls == [("opt/a", 1.5, 20), ("opt/n", 3.0, 20), ("opt/flag", 1.0, 20)]
-
-
-def test_wandb_logger_without_wandb():
-    """scao/logging.py:124-144: a no-op when wandb cannot be imported."""
-    import importlib.util
-
-    from scao_amd.logging import WandbLogger
-    if importlib.util.find_spec("wandb") is not None:
-        pytest.skip("wandb is installed")
-    WandbLogger(log_every=1)({"step": 1, "a": 1.0})
-
-
 def test_bench_refuses_more_than_one_gpu():
     """bench.py --gpus N > 1 exits with a message, before touching a GPU."""
     import os
