@@ -15,6 +15,11 @@ drawn param by param in group order; params from manual_seed(0)):
   traj_misc     -- lookahead, blend_steps=0, strong weight decay, int8.
   traj_bf16     -- bf16 params and grads.
   traj_sparse   -- default sparse filter (quantile mask) on, int8.
+  traj_gsnr, traj_lazy, traj_awarmup, traj_dynsparse, traj_arank -- the
+                   optional features (gSNR update mask, lazy refresh trigger,
+                   adaptive warm-up, dynamic sparsity, adaptive rank), each on
+                   the fp32 or int8 small configuration the GPU feature tests
+                   use; the warm-up flag is recorded per step.
   ops           -- operator-level vectors (projection, int8 EMA update,
                    low-rank mm, quantise, adaptive rank, natural norm).
   c1_summary    -- the 768x3072 parity config, 100 steps: per-step norms,
@@ -97,7 +102,8 @@ def run_traj(scao, name, cfg, steps, snap_steps, dtype=torch.float32, outliers=0
             p.grad = gr[k].clone()
         opt.step()
         rec = {"global_step": opt._global_step, "global_norm_ema": opt._global_norm_ema,
-               "ranks": {str(i): k for i, k in opt.current_ranks().items()}}
+               "ranks": {str(i): k for i, k in opt.current_ranks().items()},
+               "in_warmup": bool(opt._in_warmup_global)}
         for i, (k, p) in enumerate(params.items()):
             st = opt.state[p]
             tensors[f"step{t}.p.{k}"] = p.detach().clone()
@@ -268,12 +274,42 @@ def run_ckpt(scao):
         json.dump(meta, f, indent=1, sort_keys=True)
 
 
-def main():
+def main(only=None):
+    """Write every fixture, or only those named on the command line."""
     sys.path.insert(0, REF)
     warnings.simplefilter("ignore")
     torch.set_num_threads(8)
     import scao  # the reference package
+
+    def want(name):
+        return not only or name in only
+
     base = dict(lr=1e-2, weight_decay=0.01, max_precond_dim=32, rho=0.99, **PARITY)
+    fp32_small = dict(base, use_int8_ema=False, k_min=4, k_max=4, warmup_steps=4,
+                      blend_steps=4, precond_freq=2, min_precond_updates=1, tau=None,
+                      lars_coeff=0.0)
+    int8_small = dict(base, use_int8_ema=True, k_min=2, k_max=8, warmup_steps=6,
+                      blend_steps=5, precond_freq=3, min_precond_updates=2, tau=1.0,
+                      lars_coeff=1e-3)
+    features = {
+        # gSNR mask on the update (scao/optimizer.py:160-181)
+        "traj_gsnr": (dict(fp32_small, use_gsnr_clip=True, gsnr_threshold=0.5), 12),
+        # refresh triggered by the gradient-norm change (:187-214)
+        "traj_lazy": (dict(int8_small, lazy_precond=True, lazy_delta_threshold=0.05,
+                           lazy_max_skip=3), 14),
+        # warm-up that ends when the gradient norm settles (:106-154)
+        "traj_awarmup": (dict(fp32_small, adaptive_warmup=True, warmup_steps=30,
+                              warmup_stability_threshold=0.5, warmup_patience=2), 26),
+        # sparsity from the layer's norm against the global EMA (:60-99)
+        "traj_dynsparse": (dict(int8_small, sparsity=0.7, dynamic_sparsity=True), 12),
+        # rank moved by the gradient-norm ratio (:383-401)
+        "traj_arank": (dict(fp32_small, adaptive_rank=True, k_min=2, k_max=8), 12),
+    }
+    for name, (cfg, steps) in features.items():
+        if want(name):
+            run_traj(scao, name, cfg, steps=steps, snap_steps=(steps,))
+    if not want("traj_int8"):
+        return
     run_traj(scao, "traj_int8", dict(base, use_int8_ema=True, k_min=2, k_max=8,
                                      warmup_steps=6, blend_steps=5, precond_freq=3,
                                      min_precond_updates=2, tau=1.0, lars_coeff=1e-3),
@@ -301,4 +337,4 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    main(set(sys.argv[1:]) or None)

@@ -47,7 +47,10 @@ def _replay(name):
     return T, meta, shapes, dtype, params, opt
 
 
-TRAJS = ["traj_int8", "traj_fp32", "traj_misc", "traj_bf16", "traj_sparse"]
+TRAJS = ["traj_int8", "traj_fp32", "traj_misc", "traj_bf16", "traj_sparse",
+         # the optional features: gSNR mask, lazy trigger, adaptive warm-up,
+         # dynamic sparsity, adaptive rank
+         "traj_gsnr", "traj_lazy", "traj_awarmup", "traj_dynsparse", "traj_arank"]
 
 
 @pytest.mark.parametrize("name", TRAJS)
@@ -63,6 +66,8 @@ def test_trajectory_matches_reference(name):
         assert opt._global_step == rec["global_step"]
         assert opt._global_norm_ema == pytest.approx(rec["global_norm_ema"], rel=1e-12)
         assert {str(i): k for i, k in opt.current_ranks().items()} == rec["ranks"]
+        if "in_warmup" in rec:
+            assert bool(opt._in_warmup_global) == rec["in_warmup"], t
         for k, p in params.items():
             st = opt.state[p]
             exp = rec[k]
