@@ -192,9 +192,10 @@ CASES = {
 
 
 def _gpu_from_oracle(ref_opt, ref_params, cfg, dev):
+    """cfg: the case's hyperparameters; PARITY's fill in what it leaves out."""
     import scao_amd
     params = {k: torch.nn.Parameter(v.detach().clone().to(dev)) for k, v in ref_params.items()}
-    opt = scao_amd.SCAO(list(params.values()), **cfg, **PARITY)
+    opt = scao_amd.SCAO(list(params.values()), **{**PARITY, **cfg})
     # the portable _scao_precond entry lacks a diagonal preconditioner's bias
     # factor (scao/preconditioner.py:570-600); load_state_dict takes it from
     # the preconditioner object in the per-parameter state, as the reference's
@@ -223,21 +224,57 @@ def test_step_from_shared_state(case):
     reference's own error, and the same budget for the GPU's solver (triangle
     inequality through the exact update).  The GPU's distance to the exact
     update under the plain bound is reported beside it."""
+    shapes, cfg, steps = CASES[case]
+    _shared_state_run("step_from_shared_state", case, shapes, {**PARITY, **cfg}, steps)
+
+
+def _carry_features(ref, rp, gopt, gp, dev):
+    """The optional features' per-parameter host state, which no state_dict
+    carries (the reference's neither): lazy refresh triggers and sparse
+    filters (magnitude EMA, and the dynamic filter's norm EMAs and current
+    sparsity), from the oracle's objects to fresh GPU-side ones."""
+    from scao_amd import optimizer as O
+    for k in rp:
+        rid, gid = id(rp[k]), id(gp[k])
+        trig = ref._lazy_triggers.get(rid)
+        if trig is not None:
+            t = O._LazyPrecondTrigger(trig.delta_threshold, trig.max_skip)
+            t._prev_grad_norm, t._steps_since_update = trig._prev_grad_norm, trig._steps_since_update
+            gopt._lazy_triggers[gid] = t
+        f = ref._sparse_filters.get(rid)
+        if f is not None:
+            if hasattr(f, "base_sparsity"):
+                g = O._DynamicSparseFilter(f.base_sparsity, f.min_sparsity, f.max_sparsity, f.ema,
+                                           f.norm_ema_coeff)
+                g._norm_ema, g._global_norm_ema = f._norm_ema, f._global_norm_ema
+            else:
+                g = O._SparseGradFilter(f.sparsity, f.ema)
+            g.sparsity = f.sparsity
+            if f.mag_ema is not None:
+                g.mag_ema = f.mag_ema.float().contiguous().to(dev)
+            gopt._sparse_filters[gid] = g
+
+
+def _shared_state_run(test, case, shapes, cfg, steps, carry=None):
     from scao_amd import engine
     dev = _dev()
-    shapes, cfg, steps = CASES[case]
     rp = make_params(shapes)
-    ref = R.RefSCAO(list(rp.values()), **cfg, **PARITY)
+    ref = R.RefSCAO(list(rp.values()), **cfg)
     worst, worst_m, emas, exact = {}, 0.0, 0, {}
     for t in range(1, steps + 1):
         print(f"case={case} step={t}", flush=True)
-        refreshed = t % cfg["precond_freq"] == 0
         gp, gopt = _gpu_from_oracle(ref, rp, cfg, dev)
-        ex_p = ex = None
-        if refreshed:
-            ex_p = {k: torch.nn.Parameter(v.detach().clone()) for k, v in rp.items()}
-            ex = R.RefSCAO(list(ex_p.values()), **cfg, **PARITY)
-            ex.load_state_dict(copy.deepcopy(ref.state_dict()))
+        if carry is not None:
+            carry(ref, rp, gopt, gp, dev)
+        ex_p = {k: torch.nn.Parameter(v.detach().clone()) for k, v in rp.items()}
+        ex = R.RefSCAO(list(ex_p.values()), **cfg)
+        ex.load_state_dict(copy.deepcopy(ref.state_dict()))
+        if carry is not None:   # the oracle's own feature objects, copied
+            for k in shapes:
+                for attr in ("_lazy_triggers", "_sparse_filters"):
+                    obj = getattr(ref, attr).get(id(rp[k]))
+                    if obj is not None:
+                        getattr(ex, attr)[id(ex_p[k])] = copy.deepcopy(obj)
         pairs = {}
         for k in shapes:
             pa = ref.state[rp[k]].get("preconditioner")
@@ -245,20 +282,14 @@ def test_step_from_shared_state(case):
                 pb = gopt.state[gp[k]]["preconditioner"]
                 for (la, *_), (lb, *_) in zip(P.kron_leaves(pa), pb.leaves()):
                     pairs[id(lb)] = la
+        pre_steps = {k: _precond_steps(ref.state[rp[k]]) for k in shapes}
         grads = grads_for_step(t, shapes)
         before = {k: v.detach().clone() for k, v in rp.items()}
         for k in shapes:
             rp[k].grad = grads[k].clone()
             gp[k].grad = grads[k].to(dev)
-            if ex is not None:
-                ex_p[k].grad = grads[k].clone()
+            ex_p[k].grad = grads[k].clone()
         ref.step()
-        if ex is not None:
-            R.EXACT_EIGH = True
-            try:
-                ex.step()
-            finally:
-                R.EXACT_EIGH = False
         hook = P.IdenticalPostEma(pairs)
         engine.AFTER_EMA_HOOK = hook
         try:
@@ -267,40 +298,64 @@ def test_step_from_shared_state(case):
             engine.AFTER_EMA_HOOK = None
         torch.cuda.synchronize()
         emas += hook.checked
+        # a refresh step: some preconditioner (block) advanced its precond_step
+        refreshed = any(_precond_steps(ref.state[rp[k]]) != pre_steps[k] for k in shapes)
+        if refreshed:
+            R.EXACT_EIGH = True
+            try:
+                ex.step()
+            finally:
+                R.EXACT_EIGH = False
         # the preconditioner state first: a refresh's eigen stage, compared
         # from identical inputs, is checked before the update it feeds
         for (kr, pr), (kg, pg) in zip(ref.state.items(), gopt.state.items()):
             _cmp_precond(pr["preconditioner"], pg["preconditioner"], t, refreshed)
         for k in shapes:
-            e_ref = P.eigh_error(rp[k], ex_p[k]) if ex is not None else 0.0
+            e_ref = P.eigh_error(rp[k], ex_p[k]) if refreshed else 0.0
             r = P.assert_update_close(gp[k], rp[k], before[k],
                                       f"step {t} param {k} update (refresh={refreshed}, "
                                       f"E_ref={e_ref:.3g})", extra_abs=2.0 * e_ref)
             worst[(k, refreshed)] = max(worst.get((k, refreshed), 0.0), r)
             st_r, st_g = ref.state[rp[k]], gopt.state[gp[k]]
-            if ex is not None:
+            if refreshed:
                 x = exact.setdefault(k, [0.0, 0.0])
                 x[0] = max(x[0], P.update_ratio(gp[k], ex_p[k], before[k]))
                 x[1] = max(x[1], P.update_ratio(rp[k], ex_p[k], before[k]))
             for key in ("exp_avg", "exp_avg_sq", "exp_avg_diff", "prev_grad"):
-                e_m = P.eigh_error(st_r[key], ex.state[ex_p[k]][key]) if ex is not None else 0.0
+                e_m = P.eigh_error(st_r[key], ex.state[ex_p[k]][key]) if refreshed else 0.0
                 worst_m = max(worst_m, P.assert_close(st_g[key], st_r[key], P.MOMENT_RTOL,
                                                       P.MOMENT_ATOL, f"step {t} {k} {key}",
                                                       extra=2.0 * e_m))
             assert st_g["step"] == st_r["step"] and st_g["scao_step"] == st_r["scao_step"]
             assert st_g.get("scao_phase_started") == st_r.get("scao_phase_started")
+        assert gopt.current_ranks() == ref.current_ranks(), t
+        assert gopt._in_warmup_global == ref._in_warmup_global, t
         # the oracle's norms are the reference's fp32 CPU reductions; over n
         # squares their rounding walks like sqrt(n / lanes) * eps (1.5e-5 at
         # 2M elements), the kernels add fp32 partials in fp64
         big = max(int(torch.tensor(s).prod()) for s in shapes.values())
         gn_tol = 1e-6 if big <= 1 << 18 else 5e-5
         assert gopt._global_norm_ema == pytest.approx(ref._global_norm_ema, rel=gn_tol)
-    report("step_from_shared_state", case,
+    report(test, case,
            {**{f"{k}{'/refresh' if r else ''}": v for (k, r), v in worst.items()},
             **{f"{k}/refresh gpu_vs_exact_eigh": v[0] for k, v in exact.items()},
             **{f"{k}/refresh ref_vs_exact_eigh": v[1] for k, v in exact.items()},
             "moments": worst_m, "emas_checked": emas,
             "gate": "elementwise ratio <= 1 (refresh steps: + 2 E_ref)"})
+
+
+def _precond_steps(state):
+    """precond_step of a parameter's preconditioner and of all its blocks."""
+    pre = state.get("preconditioner")
+    out = []
+
+    def walk(node):
+        out.append(node.precond_step)
+        for b in getattr(node, "_blocks", None) or []:
+            walk(b)
+    if pre is not None:
+        walk(pre)
+    return out
 
 
 _PROJ_ERR = [0.0]
@@ -717,9 +772,23 @@ FEATURES = {
 
 
 @pytest.mark.parametrize("feature", list(FEATURES))
+def test_feature_from_shared_state(feature):
+    """The optional features step by step from shared state, with the same
+    elementwise gates as test_step_from_shared_state; the features' host
+    state (lazy triggers, filters) is carried over before every step, and
+    ranks and the warm-up flag must be equal after it."""
+    cfg, steps = FEATURES[feature]
+    _shared_state_run("feature_from_shared_state", feature, SHAPES, {**PARITY, **cfg}, steps,
+                      carry=_carry_features)
+
+
+@pytest.mark.parametrize("feature", list(FEATURES))
 def test_feature_trajectory(feature):
-    """The reference's optional features, identical starts, against the
-    oracle: cumulative update per parameter, ranks and runtime state."""
+    """The reference's optional features over whole runs from identical
+    starts, against the oracle: ranks, warm-up flag and grad-norm EMA equal
+    at every step, and the cumulative update per parameter reported (a drift
+    measure: refresh steps feed each solver's eigenvector error forward; the
+    per-step bar is test_feature_from_shared_state's)."""
     dev = _dev()
     import scao_amd
     cfg, steps = FEATURES[feature]
