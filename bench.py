@@ -256,6 +256,59 @@ def pmc_summary(fetch_csv: str, write_csv: str, config: str, copy_mib: int, cmd:
     return "\n".join(out)
 
 
+def refresh_summary(trace_csv: str, config: str, cmd: str) -> str:
+    """Markdown per-kernel summary of the last curvature refresh in a
+    rocprofv3 --kernel-trace CSV of this bench: the dispatches from the
+    refresh's first k_gram_ema to the next k_apply (the update that uses
+    it), grouped by kernel."""
+    import csv
+    import re
+
+    def short(name):
+        name = name.replace("(anonymous namespace)::", "")
+        name = re.sub(r"\(.*", "", name).replace("void ", "").strip()
+        if name.startswith("Cijk_"):   # rocBLAS/Tensile GEMM kernels by macro tile
+            mt = re.search(r"_MT(\d+x\d+x\d+)_", name)
+            name = "rocBLAS GEMM " + (name[5:9] + " MT" + mt.group(1) if mt else name[:40])
+        return name[:80]
+
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    names = [r["Kernel_Name"] for r in rows]
+    grams = [i for i, n in enumerate(names) if "k_gram_ema" in n]
+    starts = [i for i in grams if i == grams[0] or "k_gram_ema" not in names[i - 1] and
+              not any("k_gram_ema" in names[j] or "k_requant" in names[j]
+                      for j in range(max(0, i - 3), i))]
+    s0 = starts[-1]
+    e0 = next(i for i in range(s0, len(rows)) if "k_apply" in names[i])
+    win = rows[s0:e0]
+    t0, t1 = int(win[0]["Start_Timestamp"]), int(win[-1]["End_Timestamp"])
+    agg = {}
+    for r in win:
+        d = agg.setdefault(short(r["Kernel_Name"]), [0, 0.0])
+        d[0] += 1
+        d[1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6
+    busy = sum(v[1] for v in agg.values())
+    out = [f"# Curvature refresh kernels (rocprofv3 kernel trace), {config}", "",
+           "Commands (from the repository root on the box):", "", "```", cmd, "```", "",
+           f"The last refresh of the run (a Phase-2 step): {len(win)} dispatches from its first "
+           f"`k_gram_ema` to the `k_apply` of the update that uses it; first dispatch start to "
+           f"last dispatch end {(t1 - t0) / 1e6:.1f} ms, of which kernels run {busy:.1f} ms.", "",
+           "| kernel | dispatches | total ms | share |", "|---|---:|---:|---:|"]
+    rest = [0, 0.0, 0]
+    for name, (n, ms) in sorted(agg.items(), key=lambda kv: -kv[1][1]):
+        if ms >= 0.5:
+            out.append(f"| `{name}` | {n} | {ms:.2f} | {ms / busy:.1%} |")
+        else:
+            rest[0] += n
+            rest[1] += ms
+            rest[2] += 1
+    out.append(f"| other ({rest[2]} kernels) | {rest[0]} | {rest[1]:.2f} | {rest[1] / busy:.1%} |")
+    gemm = [v for k, v in agg.items() if k.startswith("rocBLAS GEMM")]
+    out += ["", f"rocBLAS GEMMs together (stage-1 trailing updates and the back-transformation): "
+                f"{sum(n for n, _ in gemm)} dispatches, {sum(ms for _, ms in gemm):.1f} ms."]
+    return "\n".join(out) + "\n"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -272,8 +325,11 @@ def main():
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"), default=None,
                     help="print the markdown traffic summary of two rocprofv3 --pmc runs "
                          "(FETCH_SIZE, WRITE_SIZE) of this bench and exit (no GPU use)")
+    ap.add_argument("--refresh-summary", metavar="TRACE_CSV", default=None,
+                    help="print the markdown kernel summary of the last refresh in a "
+                         "rocprofv3 --kernel-trace CSV of this bench and exit (no GPU use)")
     ap.add_argument("--pmc-command", default="",
-                    help="the commands that made the --pmc-summary inputs (recorded verbatim)")
+                    help="the commands that made a summary's inputs (recorded verbatim)")
     ap.add_argument("--dominant", default="scao_kron_apply",
                     help="entry point timed with HIP events inside the timed region")
     ap.add_argument("--no-refresh", action="store_true",
@@ -289,6 +345,9 @@ def main():
                          "gradient filter and noise (sparsity=0.7, noise_std=0.01), reported "
                          "in details (0: skip)")
     args = ap.parse_args()
+    if args.refresh_summary:
+        print(refresh_summary(args.refresh_summary, args.config, args.pmc_command))
+        return
     if args.pmc_summary:
         print(pmc_summary(*args.pmc_summary, args.config, args.copy_probe_mib or 1024,
                           args.pmc_command))

@@ -17,9 +17,11 @@
 //      the clamped spectrum is exact (trace minus the negatives);
 //   4. eigenvectors by float64 inverse iteration on the band matrix itself
 //      (k_inviter: band LU with partial pivoting in a sliding 17 x 33 window,
-//      one wavefront per vector), two solves with a Rayleigh-quotient shift in
-//      between, then Gram-Schmidt inside clusters of (nearly) equal
-//      eigenvalues (k_cluster_orth);
+//      one wavefront per vector, shifted by the bisection eigenvalue): one
+//      solve, a second only when the solution did not grow enough to have
+//      converged, then the Rayleigh quotient as the eigenvalue; Gram-Schmidt
+//      inside clusters of (nearly) equal eigenvalues (k_cluster_orth) and a
+//      transposing float32 write of the vectors (k_vec_out);
 //   5. back-transformation with the stage-1 block reflectors: caller GEMMs.
 //
 // The tridiagonal's reflectors are never stored: the vectors come from the

@@ -23,9 +23,10 @@ lists (which depend only on shapes and phases) are cached on the device.
 
 The curvature refresh (``refresh``) batches every block due for an update:
 Gram -> EMA -> requantise on the GPU (no host round trip for the int8
-scale), then the eigendecomposition in PyTorch-ROCm (``torch.linalg.eigh``
-on stacked equal-size matrices) and the adaptive-rank choice with one host
-read of all ranks.
+scale), then the eigen stage on stacked equal-size matrices
+(``scao_amd.eigen.topk_eigh``: the k_max largest eigenpairs and the sum of
+the clamped spectrum) and the adaptive-rank choice with one host read of all
+ranks.
 """
 
 from __future__ import annotations
