@@ -63,3 +63,20 @@ def test_missing_library_raises(monkeypatch, tmp_path):
     monkeypatch.setattr(L, "_lib", None)
     with pytest.raises(L.ScaoLibError, match="no CPU or torch fallback"):
         L.lib()
+
+
+def test_header_constants_match_the_python_binding():
+    """Every integer #define SCAO_<NAME> of include/scao_amd.h that scao_amd._lib
+    mirrors as <NAME> has the same value there."""
+    import re
+
+    from scao_amd import _lib as L
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    text = open(os.path.join(root, "include", "scao_amd.h")).read()
+    seen = 0
+    for name, val in re.findall(r"^#define SCAO_([A-Z0-9_]+)[ \t]+(\d+)[ \t]*(?:/\*|$)", text,
+                                re.M):
+        if hasattr(L, name) and isinstance(getattr(L, name), int):
+            assert getattr(L, name) == int(val), name
+            seen += 1
+    assert seen >= 5
