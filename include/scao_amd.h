@@ -291,6 +291,21 @@ int scao_eig_prep(const scao_task* tasks, int ntasks, const scao_prep_desc* desc
  * (rows c0+b.., band + i*bstride, pitch SCAO_EIG_BANDW). */
 int scao_eig_panel_qr(float* A, int64_t stride, int n, int c0, int batch, float* T, float* band,
                       int64_t bstride, void* stream);
+/* One panel step of the trailing update on the lower triangle of the region
+ * R (mr x mr, at A + i*sA, leading dim ldA; every matrix): with the panel's
+ * reflectors V and correction W (mr x b rows at V + i*sV / W + i*sW, leading
+ * dims ldV / ldW), A <- A - V W^T - W V^T for the elements with row >=
+ * column (nothing above the diagonal is read or written); with Vn (the next
+ * panel's reflectors, mr x b), also Y = A_new Vn for the symmetric A_new into
+ * Y + i*sY (mr x b, row-major), using `work` (scao_eig_sy2sb_work(mr, batch)
+ * bytes) for fixed-order partial sums.  Replaces, per panel, the two-sided
+ * update A22 - V W^T - W V^T and the next panel's A22 V product of the full
+ * matrix (the reference's eigh works on the whole matrix). */
+int64_t scao_eig_sy2sb_work(int mr, int batch);
+int scao_eig_sy2sb_update(float* A, int64_t sA, int ldA, int mr, int batch, const float* V,
+                          int64_t sV, int ldV, const float* W, int64_t sW, int ldW,
+                          const float* Vn, int64_t sVn, int ldVn, float* Y, int64_t sY,
+                          void* work, void* stream);
 /* The band matrix: diagonals 0..b of every row, from the final diagonal
  * blocks of A and the R factors in band, into orig (float32, pitch b+1: kept
  * for the eigenvector stage) and into band64 (float64, n x SCAO_EIG_BANDW per

@@ -134,6 +134,9 @@ SIGNATURES = {
     "scao_sparse_filter": (_I, [_VP, _I, _VP, _I, _VP]),
     "scao_eig_panel_qr": (_I, [_VP, _I64, _I, _I, _I, _VP, _VP, _I64, _VP]),
     "scao_eig_band_finish": (_I, [_VP, _I64, _I, _I, _VP, _I64, _VP, _I64, _VP, _VP]),
+    "scao_eig_sy2sb_work": (_I64, [_I, _I]),
+    "scao_eig_sy2sb_update": (_I, [_VP, _I64, _I, _I, _I, _VP, _I64, _I, _VP, _I64, _I, _VP,
+                                   _I64, _I, _VP, _I64, _VP, _VP]),
     "scao_eig_sb2st": (_I, [_VP, _I, _I, _VP, _VP, _VP]),
     "scao_eig_bisect_work": (_I64, [_I, _I]),
     "scao_eig_bisect": (_I, [_VP, _VP, _I, _I, _I, _VP, _VP, _VP, _VP]),

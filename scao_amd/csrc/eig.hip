@@ -167,6 +167,219 @@ __global__ __launch_bounds__(1024) void k_panel_qr(float* A, int64_t stride, int
   }
 }
 
+// ------------------------------------------------------- sy2sb update ---
+// One panel step of the dense -> band reduction, on the lower triangle only.
+// Region R: rows and columns >= r1 of each matrix (mr of them).  With the
+// panel's reflector block V (mr x 16, rows from r1) and its correction W,
+//   A <- A - V W^T - W V^T        (elements with row >= column)
+// and, when Vn (the next panel's reflectors, rows from r1) is given,
+//   Y  = A_new Vn                 (the symmetric matrix A_new)
+// Nothing above the diagonal is read or written: a diagonal tile is read from
+// its lower half and mirrored.  64 x 64 tiles; the workgroup of tile-row I
+// and chunk c takes tiles (I, J), J in [UCH c, min(UCH (c+1), I+1)); it
+// writes its direct product sum_J A(I,J) Vn(J) to Pd[I][c] and, per tile
+// below the diagonal, A(I,J)^T Vn(I) to Pt[J][I]; k_sy2sb_reduce sums them
+// in a fixed order.  Each tile moves 16 KB in and 16 KB out (half of them on
+// the diagonal), against 48 KB for a full-matrix update plus a separate
+// A Vn product.
+constexpr int UT = 64;           // update tile
+constexpr int UCH = 4;           // tiles per workgroup
+constexpr int UPT = UT + 4;      // LDS pitch of the A tile
+constexpr int UPL = 33;          // LDS pitch of [V | W] rows (conflict-free MFMA reads)
+constexpr int UPV = 17;          // LDS pitch of Vn rows
+
+__device__ __forceinline__ void ut_task(int t, int& I, int& c) {
+  int before = 0;
+  I = 0;
+  for (;;) {
+    const int nc = I / UCH + 1;
+    if (t < before + nc) {
+      c = t - before;
+      return;
+    }
+    before += nc;
+    ++I;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_sy2sb_update(float* A, int64_t sA, int ldA, int mr,
+                                                      const float* V, int64_t sV, int ldV,
+                                                      const float* W, int64_t sW, int ldW,
+                                                      const float* Vn, int64_t sVn, int ldVn,
+                                                      float* Pd, float* Pt, int nt, int nch) {
+  __shared__ __attribute__((aligned(16))) float As[UT][UPT];
+  __shared__ float Ls[UT][UPL];   // [V_I | W_I]
+  __shared__ float Rs[UT][UPL];   // [W_J | V_J]
+  __shared__ float VnI[UT][UPV];
+  __shared__ float VnJ[UT][UPV];
+  int I, c;
+  ut_task(blockIdx.x, I, c);
+  const int mat = blockIdx.y;
+  float* Am = A + (int64_t)mat * sA;
+  V += (int64_t)mat * sV;
+  W += (int64_t)mat * sW;
+  const bool doY = Vn != nullptr;
+  if (doY) Vn += (int64_t)mat * sVn;
+  const int tid = threadIdx.x, w = tid / 64, l = tid % 64, kk = l / 16;
+  const bool vec = (ldA % 4) == 0;
+
+  for (int idx = tid; idx < UT * 16; idx += 256) {
+    const int row = idx / 16, q = idx % 16, gi = UT * I + row;
+    const bool ok = gi < mr;
+    Ls[row][q] = ok ? V[(int64_t)gi * ldV + q] : 0.f;
+    Ls[row][16 + q] = ok ? W[(int64_t)gi * ldW + q] : 0.f;
+    if (doY) VnI[row][q] = ok ? Vn[(int64_t)gi * ldVn + q] : 0.f;
+  }
+  // the next tile's operands, in registers: A (4 x 4 per thread) and the
+  // W_J / V_J / Vn_J rows (4 each: thread t holds row t/4, columns 4(t%4)..)
+  v4f na[4], nw, nv, nn;
+  auto fetch = [&](int J) {
+    const bool diag = J == I;
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int idx = tid + 256 * h, row = idx / 16, c4 = (idx % 16) * 4;
+      const int gi = UT * I + row, gj = UT * J + c4;
+      v4f x = {0.f, 0.f, 0.f, 0.f};
+      if (gi < mr) {
+        const float* src = Am + (int64_t)gi * ldA + gj;
+        if (vec && gj + 3 < mr && (!diag || row >= c4 + 3)) {
+          x = *(const v4f*)src;
+        } else {
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            if (gj + t < mr && (!diag || row >= c4 + t)) x[t] = src[t];
+        }
+      }
+      na[h] = x;
+    }
+    const int row = tid / 4, q4 = (tid % 4) * 4, gj = UT * J + row;
+    const bool ok = gj < mr;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      nw[t] = ok ? W[(int64_t)gj * ldW + q4 + t] : 0.f;
+      nv[t] = ok ? V[(int64_t)gj * ldV + q4 + t] : 0.f;
+      nn[t] = (ok && doY) ? Vn[(int64_t)gj * ldVn + q4 + t] : 0.f;
+    }
+  };
+  v4f ay = {0.f, 0.f, 0.f, 0.f};
+  const int j0 = UCH * c, j1 = UCH * c + UCH < I + 1 ? UCH * c + UCH : I + 1;
+  fetch(j0);
+  for (int J = j0; J < j1; ++J) {
+    const bool diag = J == I;
+    __syncthreads();                 // the previous tile's LDS reads are done
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int idx = tid + 256 * h;
+      *(v4f*)&As[idx / 16][(idx % 16) * 4] = na[h];
+    }
+    {
+      const int row = tid / 4, q4 = (tid % 4) * 4;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        Rs[row][q4 + t] = nw[t];
+        Rs[row][16 + q4 + t] = nv[t];
+        VnJ[row][q4 + t] = nn[t];
+      }
+    }
+    __syncthreads();
+    if (J + 1 < j1) fetch(J + 1);    // in flight during this tile's work
+    if (diag) {                      // mirror the lower half
+      for (int idx = tid; idx < UT * UT; idx += 256) {
+        const int row = idx / UT, col = idx % UT;
+        if (row < col) As[row][col] = As[col][row];
+      }
+      __syncthreads();
+    }
+    // A_new = A - [V_I W_I] [W_J V_J]^T: wave w rows 16w.., four 16-column tiles
+    v4f d[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) d[t] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k4 = 0; k4 < 8; ++k4) {
+      const int q = 4 * k4 + kk;
+      const float a = Ls[16 * w + l % 16][q];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) d[t] = mfma16(a, Rs[16 * t + l % 16][q], d[t]);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * w + 4 * kk + r, col = 16 * t + l % 16;
+        As[row][col] = As[row][col] - d[t][r];
+      }
+    __syncthreads();
+    if (diag) {                      // the stored (lower) half defines the matrix
+      for (int idx = tid; idx < UT * UT; idx += 256) {
+        const int row = idx / UT, col = idx % UT;
+        if (row < col) As[row][col] = As[col][row];
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int h = 0; h < 4; ++h) {
+      const int idx = tid + 256 * h, row = idx / 16, c4 = (idx % 16) * 4;
+      const int gi = UT * I + row, gj = UT * J + c4;
+      if (gi >= mr) continue;
+      float* dst = Am + (int64_t)gi * ldA + gj;
+      const v4f x = *(const v4f*)&As[row][c4];
+      if (vec && gj + 3 < mr && (!diag || row >= c4 + 3)) {
+        *(v4f*)dst = x;
+      } else {
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (gj + t < mr && (!diag || row >= c4 + t)) dst[t] = x[t];
+      }
+    }
+    if (!doY) continue;
+    // direct part: rows 16w.. of A_new(I,J) Vn(J)
+#pragma unroll
+    for (int k4 = 0; k4 < 16; ++k4) {
+      const int j = 4 * k4 + kk;
+      ay = mfma16(As[16 * w + l % 16][j], VnJ[j][l % 16], ay);
+    }
+    if (!diag) {
+      // transposed part: rows 16w.. of A_new(I,J)^T Vn(I), for tile-row J
+      v4f pt = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k4 = 0; k4 < 16; ++k4) {
+        const int i = 4 * k4 + kk;
+        pt = mfma16(As[i][16 * w + l % 16], VnI[i][l % 16], pt);
+      }
+      float* dst = Pt + (((int64_t)mat * nt + J) * nt + I) * (UT * 16);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dst[(16 * w + 4 * kk + r) * 16 + l % 16] = pt[r];
+    }
+  }
+  if (doY) {
+    float* dst = Pd + (((int64_t)mat * nt + I) * nch + c) * (UT * 16);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dst[(16 * w + 4 * kk + r) * 16 + l % 16] = ay[r];
+  }
+}
+
+// Y[J rows] = sum_c Pd[J][c] + sum_{I > J} Pt[J][I], in that order.
+__global__ __launch_bounds__(256) void k_sy2sb_reduce(const float* Pd, const float* Pt, float* Y,
+                                                      int64_t sY, int mr, int nt, int nch) {
+  const int J = blockIdx.x, mat = blockIdx.y;
+  const int e0 = threadIdx.x * 4;            // 4 of the 64 x 16 outputs
+  const int row = e0 / 16, col = e0 % 16;
+  if (UT * J + row >= mr) return;
+  v4f s = {0.f, 0.f, 0.f, 0.f};
+  const int ncj = J / UCH + 1;
+  for (int c = 0; c < ncj; ++c) {
+    const v4f x = *(const v4f*)(Pd + (((int64_t)mat * nt + J) * nch + c) * (UT * 16) + e0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) s[t] += x[t];
+  }
+  for (int I = J + 1; I < nt; ++I) {
+    const v4f x = *(const v4f*)(Pt + (((int64_t)mat * nt + J) * nt + I) * (UT * 16) + e0);
+#pragma unroll
+    for (int t = 0; t < 4; ++t) s[t] += x[t];
+  }
+  *(v4f*)(Y + (int64_t)mat * sY + (int64_t)(UT * J + row) * 16 + col) = s;
+}
+
 // ---------------------------------------------------------- band finish ---
 // Row i: diagonals 0..i-bs from the final diagonal block of A (bs = start of
 // i's NB-row block), diagonals above that up to NB were written by the panel
@@ -840,6 +1053,38 @@ extern "C" int scao_eig_panel_qr(float* A, int64_t stride, int n, int c0, int ba
   else
     hipLaunchKernelGGL((k_panel_qr<4>), dim3(batch), dim3(1024), 0, s, Am, stride, n, c0, T, band, bstride);
   SCAO_LAUNCH_CHECK("scao_eig_panel_qr");
+  return SCAO_OK;
+}
+
+extern "C" int64_t scao_eig_sy2sb_work(int mr, int batch) {
+  if (mr <= 0 || batch <= 0) return 0;
+  const int64_t nt = (mr + UT - 1) / UT, nch = (nt - 1) / UCH + 1;
+  return (int64_t)batch * nt * (nt + nch) * UT * 16 * (int64_t)sizeof(float);
+}
+
+extern "C" int scao_eig_sy2sb_update(float* A, int64_t sA, int ldA, int mr, int batch,
+                                     const float* V, int64_t sV, int ldV, const float* W,
+                                     int64_t sW, int ldW, const float* Vn, int64_t sVn, int ldVn,
+                                     float* Y, int64_t sY, void* work, void* stream) {
+  SCAO_CHECK_ARG(A && V && W, "scao_eig_sy2sb_update: null pointer");
+  SCAO_CHECK_ARG(batch >= 0 && batch <= 65535 && mr >= 0 && ldA >= mr && ldV >= 16 && ldW >= 16 &&
+                     (!Vn || (ldVn >= 16 && Y && work && sY >= (int64_t)mr * 16)),
+                 "scao_eig_sy2sb_update: bad arguments mr=%d batch=%d", mr, batch);
+  if (batch == 0 || mr == 0) return SCAO_OK;
+  const int nt = (mr + UT - 1) / UT, nch = (nt - 1) / UCH + 1;
+  int ntask = 0;
+  for (int I = 0; I < nt; ++I) ntask += I / UCH + 1;
+  float* Pd = (float*)work;
+  float* Pt = Pd + (int64_t)batch * nt * nch * UT * 16;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_sy2sb_update, dim3(ntask, batch), dim3(256), 0, s, A, sA, ldA, mr, V, sV,
+                     ldV, W, sW, ldW, Vn, sVn, ldVn, Pd, Pt, nt, nch);
+  SCAO_LAUNCH_CHECK("scao_eig_sy2sb_update");
+  if (Vn) {
+    hipLaunchKernelGGL(k_sy2sb_reduce, dim3(nt, batch), dim3(256), 0, s, Pd, Pt, Y, sY, mr, nt,
+                       nch);
+    SCAO_LAUNCH_CHECK("scao_eig_sy2sb_update/reduce");
+  }
   return SCAO_OK;
 }
 

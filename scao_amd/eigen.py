@@ -10,7 +10,11 @@ kernels of csrc/eig.hip and plain batched GEMMs (rocBLAS, through torch):
    columns, ``scao_eig_panel_qr`` factors it (Householder, V kept in the
    panel, T returned), then the trailing matrix gets the two-sided update
    A22 <- Q^T A22 Q = A22 - (V W^T + W V^T), W = X - V (T^T V^T X) / 2,
-   X = A22 V T (three GEMMs);
+   X = A22 V T.  With FUSED_STAGE1 the next panel's columns are updated
+   first (a thin product), the next panel is factored, and one
+   ``scao_eig_sy2sb_update`` pass over the lower triangle applies the update
+   and forms the next panel's A22 V, so each panel reads and writes half the
+   matrix once; otherwise three batched GEMMs per panel on the full matrix;
 2. ``scao_eig_band_finish`` / ``scao_eig_sb2st``: band -> tridiagonal;
 3. ``scao_eig_bisect``: the kq largest eigenvalues and the clamped sum;
 4. ``scao_eig_vectors``: eigenvectors of the band matrix;
@@ -27,6 +31,7 @@ from . import _lib as L
 NB = L.EIG_BAND
 BW = L.EIG_BANDW
 MAX_BATCH = 65535   # matrices per call: the batch is a grid dimension
+FUSED_STAGE1 = True  # lower-triangle panel updates (scao_eig_sy2sb_update)
 
 
 def panels(n: int) -> list:
@@ -58,7 +63,9 @@ def _reduce(X: Tensor):
     Tall = torch.empty(max(len(pcs), 1), B, NB, NB, dtype=f32, device=dev)
     band = torch.zeros(B, n, BW, dtype=f32, device=dev)
     nn = n * n
-    for p, c0 in enumerate(pcs):
+    if FUSED_STAGE1 and pcs:
+        _stage1_fused(X, pcs, Tall, band, s)
+    for p, c0 in enumerate(pcs if not FUSED_STAGE1 else []):
         L.call("scao_eig_panel_qr", X.data_ptr(), nn, n, c0, B, Tall[p].data_ptr(),
                band.data_ptr(), n * BW, s)
         r0 = c0 + NB
@@ -78,6 +85,45 @@ def _reduce(X: Tensor):
     e = torch.zeros(B, n, dtype=torch.float64, device=dev)
     L.call("scao_eig_sb2st", band64.data_ptr(), n, B, d.data_ptr(), e.data_ptr(), s)
     return pcs, Tall, orig, d, e
+
+
+def _stage1_fused(X: Tensor, pcs: list, Tall: Tensor, band: Tensor, s: int) -> None:
+    """Stage 1 on the lower triangle (module docstring, step 1).  Above the
+    diagonal X holds stale values afterwards; nothing reads them."""
+    B, n, _ = X.shape
+    nn = n * n
+    f32 = torch.float32
+    base = X.data_ptr()
+    L.call("scao_eig_panel_qr", base, nn, n, 0, B, Tall[0].data_ptr(), band.data_ptr(), n * BW, s)
+    Y = torch.bmm(X[:, NB:, NB:], X[:, NB:, 0:NB])      # X is whole and symmetric here
+    work = torch.empty(max(L.lib().scao_eig_sy2sb_work(max(n - 2 * NB, 1), B), 8),
+                       dtype=torch.uint8, device=X.device)
+    for p, c0 in enumerate(pcs):
+        r0 = c0 + NB
+        V = X[:, r0:, c0:c0 + NB]
+        T = Tall[p]
+        Yt = torch.bmm(Y, T)                                   # A22 V T
+        M = torch.bmm(T.transpose(1, 2), torch.bmm(V.transpose(1, 2), Yt))
+        W = torch.baddbmm(Yt, V, M, alpha=-0.5)                # (B, m, b), contiguous
+        if p + 1 == len(pcs):                                  # the last, in-band block
+            A22 = X[:, r0:, r0:]
+            A22.baddbmm_(torch.cat([V, W], 2), torch.cat([W, V], 2).transpose(1, 2), alpha=-1.0)
+            break
+        # the next panel's columns (rows r0..), then its factorisation
+        S = X[:, r0:, r0:r0 + NB]
+        S.sub_(torch.baddbmm(torch.bmm(V, W[:, :NB].transpose(1, 2)), W,
+                             V[:, :NB].transpose(1, 2)))
+        L.call("scao_eig_panel_qr", base, nn, n, r0, B, Tall[p + 1].data_ptr(),
+               band.data_ptr(), n * BW, s)
+        # the rest of the trailing matrix (rows and columns r1..) and the next Y
+        r1 = r0 + NB
+        mr = n - r1
+        Y = torch.empty(B, mr, NB, dtype=f32, device=X.device)
+        L.call("scao_eig_sy2sb_update", base + 4 * (r1 * n + r1), nn, n, mr, B,
+               base + 4 * (r1 * n + c0), nn, n,
+               W.data_ptr() + 4 * NB * NB, W.stride(0), NB,
+               base + 4 * (r1 * n + r0), nn, n,
+               Y.data_ptr(), mr * NB, work.data_ptr(), s)
 
 
 def stages(X: Tensor):
