@@ -302,6 +302,13 @@ int scao_eig_panel_qr(float* A, int64_t stride, int n, int c0, int batch, float*
  * update A22 - V W^T - W V^T and the next panel's A22 V product of the full
  * matrix (the reference's eigh works on the whole matrix). */
 int64_t scao_eig_sy2sb_work(int mr, int batch);
+/* The panel at column c0 (its reflectors V in A, rows c0+b.., m = n-c0-b of
+ * them): from Y = A22 V (m x b per matrix, row-major, at Y + i*m*b) and T,
+ * W = Y T - V (T^T V^T Y T) / 2 into W (m x b per matrix); with strip != 0
+ * also the next panel's columns: A[c0+b+i][c0+b+j] -= V_i.W_j + W_i.V_j for
+ * j < b (needs c0 + 2b <= n). */
+int scao_eig_sy2sb_panel_w(float* A, int64_t sA, int n, int c0, int batch, const float* Y,
+                           const float* T, float* W, int strip, void* stream);
 int scao_eig_sy2sb_update(float* A, int64_t sA, int ldA, int mr, int batch, const float* V,
                           int64_t sV, int ldV, const float* W, int64_t sW, int ldW,
                           const float* Vn, int64_t sVn, int ldVn, float* Y, int64_t sY,

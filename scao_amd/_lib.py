@@ -135,6 +135,7 @@ SIGNATURES = {
     "scao_eig_panel_qr": (_I, [_VP, _I64, _I, _I, _I, _VP, _VP, _I64, _VP]),
     "scao_eig_band_finish": (_I, [_VP, _I64, _I, _I, _VP, _I64, _VP, _I64, _VP, _VP]),
     "scao_eig_sy2sb_work": (_I64, [_I, _I]),
+    "scao_eig_sy2sb_panel_w": (_I, [_VP, _I64, _I, _I, _I, _VP, _VP, _VP, _I, _VP]),
     "scao_eig_sy2sb_update": (_I, [_VP, _I64, _I, _I, _I, _VP, _I64, _I, _VP, _I64, _I, _VP,
                                    _I64, _I, _VP, _I64, _VP, _VP]),
     "scao_eig_sb2st": (_I, [_VP, _I, _I, _VP, _VP, _VP]),

@@ -358,6 +358,81 @@ __global__ __launch_bounds__(256) void k_sy2sb_update(float* A, int64_t sA, int 
   }
 }
 
+// The panel's correction W and the next panel's columns, one workgroup per
+// matrix.  V: the panel's reflectors (m x 16, rows r0.. of A at column c0),
+// Y = A22 V (m x 16), T (16 x 16 upper):
+//   G = V^T Y (fixed-order sum over the rows), M = T^T G T,
+//   W = Y T - V M / 2                          (m x 16, to Wout),
+// and, with `strip`, the next panel's columns r0..r0+15 of rows r0..:
+//   A[r0+i][r0+j] -= V[i] . W[j] + W[i] . V[j]   (j < 16).
+__global__ __launch_bounds__(256) void k_sy2sb_panel_w(float* A, int64_t sA, int n, int r0, int c0,
+                                                       const float* Y, const float* T, float* Wout,
+                                                       int strip) {
+  __shared__ float Vs[64][17], Ys[64][17];
+  __shared__ float Ts[16][17], Gs[16][17], GTs[16][17], Ms[16][17];
+  __shared__ float Vt[16][17], Wt[16][17];
+  const int mat = blockIdx.x, tid = threadIdx.x;
+  const int m = n - r0;
+  float* Am = A + (int64_t)mat * sA;
+  const float* Ym = Y + (int64_t)mat * m * 16;
+  float* Wm = Wout + (int64_t)mat * m * 16;
+  const int a = tid / 16, b = tid % 16;
+  Ts[a][b] = T[(int64_t)mat * 256 + a * 16 + b];
+  // G[a][b] = sum_i V[i][a] Y[i][b], rows in chunks of 64
+  float g = 0.f;
+  for (int i0 = 0; i0 < m; i0 += 64) {
+    __syncthreads();
+    for (int idx = tid; idx < 64 * 16; idx += 256) {
+      const int row = idx / 16, q = idx % 16, i = i0 + row;
+      Vs[row][q] = i < m ? Am[(int64_t)(r0 + i) * n + c0 + q] : 0.f;
+      Ys[row][q] = i < m ? Ym[(int64_t)i * 16 + q] : 0.f;
+    }
+    __syncthreads();
+    const int rows = m - i0 < 64 ? m - i0 : 64;
+    for (int row = 0; row < rows; ++row) g = fmaf(Vs[row][a], Ys[row][b], g);
+  }
+  Gs[a][b] = g;
+  __syncthreads();
+  float x = 0.f;
+  for (int c = 0; c < 16; ++c) x = fmaf(Gs[a][c], Ts[c][b], x);
+  GTs[a][b] = x;
+  __syncthreads();
+  x = 0.f;
+  for (int c = 0; c < 16; ++c) x = fmaf(Ts[c][a], GTs[c][b], x);
+  Ms[a][b] = x;
+  __syncthreads();
+  // W rows: 16 rows per pass, thread (row a, column b)
+  for (int i0 = 0; i0 < m; i0 += 16) {
+    const int i = i0 + a;
+    if (i < m) {
+      const float* yr = Ym + (int64_t)i * 16;
+      const float* vr = Am + (int64_t)(r0 + i) * n + c0;
+      float yt = 0.f, vm = 0.f;
+      for (int c = 0; c < 16; ++c) {
+        yt = fmaf(yr[c], Ts[c][b], yt);
+        vm = fmaf(vr[c], Ms[c][b], vm);
+      }
+      const float wv = yt - 0.5f * vm;
+      Wm[(int64_t)i * 16 + b] = wv;
+      if (i0 == 0) {
+        Wt[a][b] = wv;
+        Vt[a][b] = vr[b];
+      }
+    }
+  }
+  if (!strip) return;
+  __syncthreads();                   // W (first rows) and the V rows in LDS; W in memory
+  for (int i0 = 0; i0 < m; i0 += 16) {
+    const int i = i0 + a;
+    if (i >= m) continue;
+    const float* vr = Am + (int64_t)(r0 + i) * n + c0;
+    const float* wr = Wm + (int64_t)i * 16;
+    float d = 0.f;
+    for (int q = 0; q < 16; ++q) d = fmaf(vr[q], Wt[b][q], fmaf(wr[q], Vt[b][q], d));
+    Am[(int64_t)(r0 + i) * n + r0 + b] -= d;
+  }
+}
+
 // Y[J rows] = sum_c Pd[J][c] + sum_{I > J} Pt[J][I], in that order.
 __global__ __launch_bounds__(256) void k_sy2sb_reduce(const float* Pd, const float* Pt, float* Y,
                                                       int64_t sY, int mr, int nt, int nch) {
@@ -1053,6 +1128,20 @@ extern "C" int scao_eig_panel_qr(float* A, int64_t stride, int n, int c0, int ba
   else
     hipLaunchKernelGGL((k_panel_qr<4>), dim3(batch), dim3(1024), 0, s, Am, stride, n, c0, T, band, bstride);
   SCAO_LAUNCH_CHECK("scao_eig_panel_qr");
+  return SCAO_OK;
+}
+
+extern "C" int scao_eig_sy2sb_panel_w(float* A, int64_t sA, int n, int c0, int batch,
+                                      const float* Y, const float* T, float* W, int strip,
+                                      void* stream) {
+  SCAO_CHECK_ARG(A && Y && T && W, "scao_eig_sy2sb_panel_w: null pointer");
+  SCAO_CHECK_ARG(batch >= 0 && n > 0 && c0 >= 0 && c0 % NB == 0 && c0 + NB < n &&
+                     sA >= (int64_t)n * n && (!strip || c0 + 2 * NB <= n),
+                 "scao_eig_sy2sb_panel_w: bad arguments n=%d c0=%d", n, c0);
+  if (batch == 0) return SCAO_OK;
+  hipLaunchKernelGGL(k_sy2sb_panel_w, dim3(batch), dim3(256), 0, (hipStream_t)stream, A, sA, n,
+                     c0 + NB, c0, Y, T, W, strip);
+  SCAO_LAUNCH_CHECK("scao_eig_sy2sb_panel_w");
   return SCAO_OK;
 }
 

@@ -100,19 +100,17 @@ def _stage1_fused(X: Tensor, pcs: list, Tall: Tensor, band: Tensor, s: int) -> N
                        dtype=torch.uint8, device=X.device)
     for p, c0 in enumerate(pcs):
         r0 = c0 + NB
-        V = X[:, r0:, c0:c0 + NB]
-        T = Tall[p]
-        Yt = torch.bmm(Y, T)                                   # A22 V T
-        M = torch.bmm(T.transpose(1, 2), torch.bmm(V.transpose(1, 2), Yt))
-        W = torch.baddbmm(Yt, V, M, alpha=-0.5)                # (B, m, b), contiguous
-        if p + 1 == len(pcs):                                  # the last, in-band block
+        last = p + 1 == len(pcs)
+        # W = Y T - V (T^T V^T Y T) / 2 and, unless last, the next panel's
+        # columns (rows r0..)
+        W = torch.empty(B, n - r0, NB, dtype=f32, device=X.device)
+        L.call("scao_eig_sy2sb_panel_w", base, nn, n, c0, B, Y.data_ptr(), Tall[p].data_ptr(),
+               W.data_ptr(), 0 if last else 1, s)
+        if last:                                               # the last, in-band block
+            V = X[:, r0:, c0:c0 + NB]
             A22 = X[:, r0:, r0:]
             A22.baddbmm_(torch.cat([V, W], 2), torch.cat([W, V], 2).transpose(1, 2), alpha=-1.0)
             break
-        # the next panel's columns (rows r0..), then its factorisation
-        S = X[:, r0:, r0:r0 + NB]
-        S.sub_(torch.baddbmm(torch.bmm(V, W[:, :NB].transpose(1, 2)), W,
-                             V[:, :NB].transpose(1, 2)))
         L.call("scao_eig_panel_qr", base, nn, n, r0, B, Tall[p + 1].data_ptr(),
                band.data_ptr(), n * BW, s)
         # the rest of the trailing matrix (rows and columns r1..) and the next Y
