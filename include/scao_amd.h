@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define SCAO_ABI_VERSION 8
+#define SCAO_ABI_VERSION 9
 
 enum scao_status { SCAO_OK = 0, SCAO_ERR_INVALID = 1, SCAO_ERR_HIP = 2 };
 enum scao_dtype { SCAO_F32 = 0, SCAO_BF16 = 1, SCAO_F16 = 2 };
@@ -247,10 +247,16 @@ typedef struct scao_gram_desc {
   int32_t rows, cols;       /* block shape m x n                                 */
   int32_t side;             /* 0: L = G G^T (dim m), 1: R = G^T G (dim n)        */
   int32_t dtype;
-  int32_t ntiles;           /* tiles per side (for amax)                         */
-  int32_t pad0;
+  int32_t ntiles;           /* amax entries: (tiles per side)^2                  */
+  int32_t flags;            /* SCAO_GRAM_SYM                                     */
   float rho, alpha;         /* fp32(rho), fp32(1 - rho)                          */
 } scao_gram_desc;
+/* The factor is symmetric: the launch's tasks for this desc cover the output
+ * tiles (a, b) with a >= b only, and a task with a > b also writes tile
+ * (b, a) (EMA update of its own old values with the transposed product) and
+ * amax entry b * nt + a.  Both tiles' products are the same sums of the same
+ * products in the same order as when computed separately. */
+#define SCAO_GRAM_SYM 1
 int scao_gram_ema(const scao_task* tasks, int ntasks, const scao_gram_desc* descs,
                   void* stream);
 /* requantise every int8 factor of a gram_ema launch; writes the new scale to

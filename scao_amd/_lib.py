@@ -21,7 +21,7 @@ import torch  # noqa: F401  -- loads torch's HIP runtime before ours
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("SCAO_AMD_LIB", os.path.join(HERE, "_lib", "libscao_amd.so"))
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 SLOT_WIDTH = 3
 FLAT_CHUNK = 4096
 PROJ_COLS = 256
@@ -74,8 +74,9 @@ PARAM_STAT = np.dtype([
 GRAM_DESC = np.dtype([
     ("g", "u8"), ("off", "i8"), ("ld", "i8"), ("q", "u8"), ("scale", "u8"), ("ema", "u8"),
     ("amax", "u8"), ("rows", "i4"), ("cols", "i4"), ("side", "i4"), ("dtype", "i4"),
-    ("ntiles", "i4"), ("pad0", "i4"), ("rho", "f4"), ("alpha", "f4"),
+    ("ntiles", "i4"), ("flags", "i4"), ("rho", "f4"), ("alpha", "f4"),
 ], align=True)
+GRAM_SYM = 1
 
 PREP_DESC = np.dtype([
     ("q", "u8"), ("scale", "u8"), ("ema", "u8"), ("out", "u8"), ("shift", "u8"), ("dim", "i4"),
@@ -100,7 +101,7 @@ STRUCTS = {0: (PARAM_DESC, [n for n in PARAM_DESC.names if n != "pad0"]),
            1: (LEAF_DESC, list(LEAF_DESC.names)),
            2: (TASK, list(TASK.names)),
            3: (PARAM_STAT, [n for n in PARAM_STAT.names if n != "pad0"]),
-           4: (GRAM_DESC, [n for n in GRAM_DESC.names if n != "pad0"]),
+           4: (GRAM_DESC, list(GRAM_DESC.names)),
            5: (PREP_DESC, list(PREP_DESC.names)),
            6: (FILTER_DESC, list(FILTER_DESC.names)),
            7: (LOOKAHEAD_DESC, [n for n in LOOKAHEAD_DESC.names if n != "pad0"])}

@@ -78,8 +78,8 @@ extern "C" int scao_struct_layout(int which, int64_t* out, int cap) {
       PUT(offsetof(S, g)); PUT(offsetof(S, off)); PUT(offsetof(S, ld)); PUT(offsetof(S, q));
       PUT(offsetof(S, scale)); PUT(offsetof(S, ema)); PUT(offsetof(S, amax));
       PUT(offsetof(S, rows)); PUT(offsetof(S, cols)); PUT(offsetof(S, side));
-      PUT(offsetof(S, dtype)); PUT(offsetof(S, ntiles)); PUT(offsetof(S, rho));
-      PUT(offsetof(S, alpha));
+      PUT(offsetof(S, dtype)); PUT(offsetof(S, ntiles)); PUT(offsetof(S, flags));
+      PUT(offsetof(S, rho)); PUT(offsetof(S, alpha));
       break;
     }
     case 5: {

@@ -153,9 +153,55 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
       }
     }
+  // the transposed tile (b, a) of a symmetric factor: element (j, i) takes
+  // the same product as (i, j).  Staged through LDS (the operand buffers are
+  // free after the K loop), one 64 x 64 wave sub-tile per buffer, two waves at
+  // a time, so the global accesses run along rows of the transposed tile.
+  const bool mirror = (D.flags & SCAO_GRAM_SYM) && tk.a != tk.b;
+  if (mirror) {
+    static_assert(sizeof(As) >= 64 * 65 * sizeof(float), "staging");
+    float* S = (w % 2 == 0) ? &As[0][0][0] : &Bs[0][0][0];
+    for (int half = 0; half < 2; ++half) {
+      const bool mine = (w / 2) == half;
+      if (mine) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+              S[(16 * b + (l % 16)) * 65 + 16 * a + 4 * (l / 16) + r] = tot[a][b][r];
+      }
+      __syncthreads();
+      if (mine) {
+        const int i = i0 + wr + l;             // column of the transposed tile
+        for (int jj = 0; jj < 64; ++jj) {
+          const int j = j0 + wc + jj;          // row of the transposed tile
+          if (i >= dim || j >= dim) continue;
+          const int64_t e = (int64_t)j * dim + i;
+          const float add = D.alpha * S[jj * 65 + l];
+          if (D.q) {
+            const float old = ((float)D.q[e] * sf) * D.rho;
+            const float x = old + add;
+            D.ema[e] = x;
+            amax = fmaxf(amax, fabsf(x));
+          } else {
+            D.ema[e] = D.ema[e] * D.rho + add;
+          }
+        }
+      }
+      __syncthreads();
+    }
+  }
   if (D.q) {
     const float mx = block_max(amax, red);
-    if (threadIdx.x == 0) D.amax[tk.slot] = mx;
+    if (threadIdx.x == 0) {
+      D.amax[tk.slot] = mx;
+      if (mirror) {
+        const int nt = (dim + GT - 1) / GT;
+        D.amax[tk.b * nt + tk.a] = mx;
+      }
+    }
   }
 }
 

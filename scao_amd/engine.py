@@ -917,6 +917,7 @@ def sparse_filter(entries) -> list:
 # --------------------------------------------------------------------------
 
 REFRESH_SCRATCH_BYTES = 2 << 30   # fp32 EMA staging per refresh chunk (int8 mode)
+SYM_GRAM = True   # compute the lower Gram tiles only, each also writing its transpose
 # The eigen stage: "hip" is scao_amd.eigen.topk_eigh (two-stage reduction,
 # bisection, inverse iteration: only the k_max vectors a factor can keep);
 # "torch" is the full torch.linalg.eigh (rocSOLVER syevd), kept for A/B runs.
@@ -1111,8 +1112,9 @@ def _gram_chunk(chunk, dev, s):
             else:
                 e["ema"] = (leaf.L_ema if side == 0 else leaf.R_ema).data_ptr()
                 scale_ptrs.append(0)
+            e["flags"] = L.GRAM_SYM if SYM_GRAM else 0
             for a in range(nt):
-                for b in range(nt):
+                for b in range(a + 1 if SYM_GRAM else nt):
                     tasks.append((di, a, b, a * nt + b))
             descs.append(e)
     dtab = np.array(descs, dtype=L.GRAM_DESC)
