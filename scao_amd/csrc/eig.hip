@@ -684,15 +684,50 @@ __global__ __launch_bounds__(SB_W * 64) void k_sb2st(double* band, int n, double
 // ------------------------------------------------------------- bisection ---
 // Sturm count of T - x: the number of eigenvalues below x (float64, with
 // LAPACK's pivmin guard against a zero pivot).
-__device__ __forceinline__ int sturm(const double* d, const double* e, int n, double x,
-                                     double pivmin) {
+// Number of eigenvalues of T below x (float64 Sturm count with dstebz's
+// pivmin guard); e2[i] = e[i]^2.  The coefficients stream in groups of SG,
+// the next group's loads issued before the current group's steps, so their
+// latency hides under the division chain (the addresses are uniform: scalar
+// loads).
+constexpr int SG = 8;
+__device__ __forceinline__ int sturm(const double* __restrict__ d, const double* __restrict__ e2,
+                                     int n, double x, double pivmin) {
   int c = 0;
   double qv = d[0] - x;
   if (fabs(qv) < pivmin) qv = -pivmin;
   c += qv < 0.0;
-  for (int i = 1; i < n; ++i) {
-    const double ee = e[i - 1];
-    qv = (d[i] - x) - ee * ee / qv;
+  int i = 1;
+  if (n - 1 >= SG) {
+    double dn[SG], en[SG];
+#pragma unroll
+    for (int t = 0; t < SG; ++t) {
+      dn[t] = d[1 + t];
+      en[t] = e2[t];
+    }
+    for (; i + SG <= n; i += SG) {
+      double dc[SG], ec[SG];
+#pragma unroll
+      for (int t = 0; t < SG; ++t) {
+        dc[t] = dn[t];
+        ec[t] = en[t];
+      }
+      if (i + 2 * SG <= n) {
+#pragma unroll
+        for (int t = 0; t < SG; ++t) {
+          dn[t] = d[i + SG + t];
+          en[t] = e2[i + SG - 1 + t];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < SG; ++t) {
+        qv = (dc[t] - x) - ec[t] / qv;
+        if (fabs(qv) < pivmin) qv = -pivmin;
+        c += qv < 0.0;
+      }
+    }
+  }
+  for (; i < n; ++i) {
+    qv = (d[i] - x) - e2[i - 1] / qv;
     if (fabs(qv) < pivmin) qv = -pivmin;
     c += qv < 0.0;
   }
@@ -702,18 +737,22 @@ __device__ __forceinline__ int sturm(const double* d, const double* e, int n, do
 // Per matrix: Gershgorin bounds, pivmin, the trace (float64), the number of
 // negative eigenvalues.  info = {lo, hi, pivmin, trace}, nneg.
 __global__ __launch_bounds__(256) void k_tri_info(const double* d, const double* e, int n,
-                                                  double* info, int* nneg) {
+                                                  double* info, int* nneg, double* e2) {
   __shared__ double red[16];
   const int mat = blockIdx.x;
   const double* dm = d + (int64_t)mat * n;
   const double* em = e + (int64_t)mat * n;
+  double* e2m = e2 + (int64_t)mat * n;
   double lo = 1e300, hi = -1e300, tr = 0.0, e2max = 0.0;
   for (int i = threadIdx.x; i < n; i += 256) {
     const double r = (i > 0 ? fabs(em[i - 1]) : 0.0) + (i + 1 < n ? fabs(em[i]) : 0.0);
     lo = fmin(lo, dm[i] - r);
     hi = fmax(hi, dm[i] + r);
     tr += dm[i];
-    if (i + 1 < n) e2max = fmax(e2max, em[i] * em[i]);
+    if (i + 1 < n) {
+      e2m[i] = em[i] * em[i];
+      e2max = fmax(e2max, e2m[i]);
+    }
   }
   double x[2] = {tr, 0.0};
   block_sum<2>(x, red);
@@ -737,13 +776,13 @@ __global__ __launch_bounds__(256) void k_tri_info(const double* d, const double*
     info[4 * mat + 1] = hi + pad;
     info[4 * mat + 2] = pivmin;
     info[4 * mat + 3] = x[0];
-    nneg[mat] = sturm(dm, em, n, 0.0, pivmin);
+    nneg[mat] = sturm(dm, e2m, n, 0.0, pivmin);
   }
 }
 
 // One thread per (matrix, eigenvalue index); index j (0-based, ascending) is
 // computed when j >= n - kq (the kq largest) or j < nneg (negative).
-__global__ __launch_bounds__(256) void k_bisect(const double* d, const double* e, int n, int kq,
+__global__ __launch_bounds__(256) void k_bisect(const double* d, const double* e2, int n, int kq,
                                                 const double* info, const int* nneg,
                                                 double* wall) {
   const int j = blockIdx.x * 256 + threadIdx.x;
@@ -752,7 +791,7 @@ __global__ __launch_bounds__(256) void k_bisect(const double* d, const double* e
   const int neg = nneg[mat];
   if (!(j >= n - kq || j < neg)) return;
   const double* dm = d + (int64_t)mat * n;
-  const double* em = e + (int64_t)mat * n;
+  const double* em = e2 + (int64_t)mat * n;
   double lo = info[4 * mat + 0], hi = info[4 * mat + 1];
   const double pivmin = info[4 * mat + 2];
   for (int it = 0; it < 80; ++it) {
@@ -1204,7 +1243,8 @@ extern "C" int scao_eig_sb2st(double* band64, int n, int batch, double* d, doubl
 
 extern "C" int64_t scao_eig_bisect_work(int n, int batch) {
   if (n <= 0 || batch <= 0) return 0;
-  return (int64_t)batch * ((int64_t)n * 8 + 4 * 8 + 8);
+  // wall (n), info (4), nneg (one 8-byte slot), e^2 (n) per matrix
+  return (int64_t)batch * ((int64_t)n * 8 + 4 * 8 + 8 + (int64_t)n * 8);
 }
 
 extern "C" int scao_eig_bisect(const double* d, const double* e, int n, int batch, int kq, double* w,
@@ -1216,9 +1256,10 @@ extern "C" int scao_eig_bisect(const double* d, const double* e, int n, int batc
   double* wall = (double*)work;
   double* info = wall + (int64_t)batch * n;
   int* nneg = (int*)(info + 4 * (int64_t)batch);
-  hipLaunchKernelGGL(k_tri_info, dim3(batch), dim3(256), 0, s, d, e, n, info, nneg);
+  double* e2 = info + 5 * (int64_t)batch;     // after nneg's batch 8-byte slots
+  hipLaunchKernelGGL(k_tri_info, dim3(batch), dim3(256), 0, s, d, e, n, info, nneg, e2);
   SCAO_LAUNCH_CHECK("scao_eig_bisect/info");
-  hipLaunchKernelGGL(k_bisect, dim3((n + 255) / 256, batch), dim3(256), 0, s, d, e, n, kq, info,
+  hipLaunchKernelGGL(k_bisect, dim3((n + 255) / 256, batch), dim3(256), 0, s, d, e2, n, kq, info,
                      nneg, wall);
   SCAO_LAUNCH_CHECK("scao_eig_bisect/bisect");
   hipLaunchKernelGGL(k_bisect_finish, dim3(batch), dim3(64), 0, s, wall, n, kq, info, nneg, w,

@@ -1084,6 +1084,14 @@ def _refresh_kron(kron, dev, s, eigen_only=False, ema_only=False):
         leaf._touch()
 
 
+def _task_rows(idx, a, b, slot) -> np.ndarray:
+    """TASK rows from equal-length integer arrays (or scalars)."""
+    n = max(np.size(x) for x in (idx, a, b, slot))
+    t = np.empty((n, 4), dtype=np.int32)
+    t[:, 0], t[:, 1], t[:, 2], t[:, 3] = idx, a, b, slot
+    return t
+
+
 def _gram_chunk(chunk, dev, s):
     descs, tasks, req_tasks, scale_ptrs = [], [], [], []
     staging = []
@@ -1107,23 +1115,24 @@ def _gram_chunk(chunk, dev, s):
                 e["ema"] = x.data_ptr()
                 e["amax"] = x.data_ptr() + 4 * dim * dim
                 scale_ptrs.append(leaf._scale.data_ptr() + 8 * side)
-                for c in range(_flat_chunks(dim * dim)):
-                    req_tasks.append((di, c, 0, -1))
+                req_tasks.append(_task_rows(di, np.arange(_flat_chunks(dim * dim)), 0, -1))
             else:
                 e["ema"] = (leaf.L_ema if side == 0 else leaf.R_ema).data_ptr()
                 scale_ptrs.append(0)
             e["flags"] = L.GRAM_SYM if SYM_GRAM else 0
-            for a in range(nt):
-                for b in range(a + 1 if SYM_GRAM else nt):
-                    tasks.append((di, a, b, a * nt + b))
+            if SYM_GRAM:
+                a, b = np.tril_indices(nt)
+            else:
+                a, b = np.divmod(np.arange(nt * nt), nt)
+            tasks.append(_task_rows(di, a, b, a * nt + b))
             descs.append(e)
     dtab = np.array(descs, dtype=L.GRAM_DESC)
     dd = L.upload(dtab, dev)
-    tt = np.array(tasks, dtype=np.int32).reshape(-1, 4).copy().view(L.TASK).reshape(-1)
+    tt = np.concatenate(tasks).view(L.TASK).reshape(-1)
     td = L.upload(tt, dev)
     _call("scao_gram_ema", td.data_ptr(), len(tt), dd.data_ptr(), s)
     if req_tasks:
-        rt = np.array(req_tasks, dtype=np.int32).reshape(-1, 4).copy().view(L.TASK).reshape(-1)
+        rt = np.concatenate(req_tasks).view(L.TASK).reshape(-1)
         rd = L.upload(rt, dev)
         sp = L.upload(np.array(scale_ptrs, dtype=np.uint64), dev)
         _call("scao_requant", rd.data_ptr(), len(rt), dd.data_ptr(), sp.data_ptr(), s)
@@ -1133,7 +1142,7 @@ def _gram_chunk(chunk, dev, s):
 def _eig_inputs(part, dim, dev, s) -> Tensor:
     X = torch.empty(len(part), dim, dim, dtype=torch.float32, device=dev)
     shift = torch.empty(len(part), dtype=torch.float32, device=dev)
-    descs, tasks = [], []
+    descs = []
     nchunk = _flat_chunks(dim * dim)
     for i, (leaf, side) in enumerate(part):
         e = np.zeros(1, dtype=L.PREP_DESC)[0]
@@ -1148,9 +1157,10 @@ def _eig_inputs(part, dim, dev, s) -> Tensor:
         else:
             e["ema"] = (leaf.L_ema if side == 0 else leaf.R_ema).data_ptr()
         descs.append(e)
-        tasks += [(i, c, 0, -1) for c in range(nchunk)]
     dd = L.upload(np.array(descs, dtype=L.PREP_DESC), dev)
-    tt = np.array(tasks, dtype=np.int32).reshape(-1, 4).copy().view(L.TASK).reshape(-1)
+    n = len(part)
+    tt = _task_rows(np.repeat(np.arange(n), nchunk), np.tile(np.arange(nchunk), n), 0,
+                    -1).view(L.TASK).reshape(-1)
     td = L.upload(tt, dev)
     _call("scao_eig_prep", td.data_ptr(), len(tt), dd.data_ptr(), len(descs), s)
     return X
