@@ -862,8 +862,9 @@ __device__ __forceinline__ double start_val(uint32_t vid, int row) {
 
 // Prefetch distance (steps) of the band solve: the band values entering the
 // window and the U rows of the back substitution are loaded this many steps
-// before their use, so one step's work covers the memory latency of another.
-constexpr int PF = 8;
+// before their use (a step takes a few thousand cycles, so 4 cover the memory
+// latency; fewer registers leave room for five waves per SIMD).
+constexpr int PF = 4;
 
 // Value entering lane L's slot 0 at the end of elimination step j: row
 // j + WR, column j + 1 + ((L - (j mod WC) - 1) mod WC).
@@ -882,25 +883,28 @@ __device__ __forceinline__ double enter_rhs(const double* rhs, uint32_t vid, int
 // `rhs` (NULL: start_val).  U rows (WC doubles each) and the transformed rhs
 // go to work; x (float64, normalised) to xout.  One wavefront; lanes 0..32
 // each own one window column (lane L holds column j + ((L - j) mod 33) at
-// step j), every lane holds all 17 row slots of its column.  Returns the
+// step j), lane 33 the right-hand side (an augmented column, so elimination
+// updates it with the same instructions); every lane holds the 17 row slots.
+// The window's rows are an unordered set: the pivot row is retired as U row
+// j and the entering band row takes its slot, so no rows move.  Returns the
 // norm of the solution before normalisation.
-__device__ double band_solve(const float* orig, int n, double sigma, double bnorm, uint32_t vid,
-                             const double* rhs, double* U, double* ys, double* xout) {
+__device__ __forceinline__ double band_solve(const float* __restrict__ orig, int n, double sigma,
+                                             double bnorm, uint32_t vid,
+                                             const double* __restrict__ rhs, double* U,
+                                             double* ys, double* xout) {
   const int L = threadIdx.x & 63;
-  const bool act = L < WC;
-  double W[WR], y[WR];
+  const bool act = L < WC;          // a matrix column
+  const bool rl = L == WC;          // the right-hand side
+  double W[WR];
   // initial window: rows 0..16, columns 0..32 (lane L <-> column L)
 #pragma unroll
-  for (int s = 0; s < WR; ++s) {
-    W[s] = act ? mval(orig, n, s, L, sigma) : 0.0;
-    y[s] = enter_rhs(rhs, vid, n, s);
-  }
-  double qW[PF], qY[PF];
+  for (int s = 0; s < WR; ++s)
+    W[s] = act ? mval(orig, n, s, L, sigma) : (rl ? enter_rhs(rhs, vid, n, s) : 0.0);
+  double qW[PF];
 #pragma unroll
-  for (int t = 0; t < PF; ++t) {
-    qW[t] = enter_val(orig, n, t, L, act, sigma);
-    qY[t] = enter_rhs(rhs, vid, n, t + WR);
-  }
+  for (int t = 0; t < PF; ++t)
+    qW[t] = act ? enter_val(orig, n, t, L, true, sigma)
+                : (rl ? enter_rhs(rhs, vid, n, t + WR) : 0.0);
   const double tiny = 2.220446049250313e-16 * bnorm + 1e-300;
   for (int j0 = 0; j0 < n; j0 += PF) {
 #pragma unroll
@@ -920,33 +924,38 @@ __device__ double band_solve(const float* orig, int n, double sigma, double bnor
           p = s;
         }
       p = __builtin_amdgcn_readfirstlane(p);
+      // p is uniform: scalar branches pick the pivot row (the empty asm keeps
+      // them branches instead of 17 per-lane selects)
+      double piv = col[0], prow = W[0];
 #pragma unroll
       for (int s = 1; s < WR; ++s)
         if (p == s) {
-          double tt = W[0]; W[0] = W[s]; W[s] = tt;
-          tt = y[0]; y[0] = y[s]; y[s] = tt;
-          tt = col[0]; col[0] = col[s]; col[s] = tt;
+          asm volatile("" ::: "memory");
+          piv = col[s];
+          prow = W[s];
         }
-      double piv = col[0];
       if (fabs(piv) < tiny) piv = piv < 0.0 ? -tiny : tiny;
-      const double inv = 1.0 / piv;
+      // every slot loses col[s] / piv times the pivot row, as col[s] * (row / piv)
+      // (the pivot's own slot is overwritten below)
+      const double q = prow / piv;
 #pragma unroll
-      for (int s = 1; s < WR; ++s) {
-        const double lm = col[s] * inv;
-        W[s] = fma(-lm, W[0], W[s]);
-        y[s] = fma(-lm, y[0], y[s]);
-      }
-      // retire the pivot row as U row j (column offset of this lane)
+      for (int s = 0; s < WR; ++s) W[s] = fma(-col[s], q, W[s]);
+      // retire the pivot row as U row j (column offset of this lane) and its
+      // right-hand side
       const int off = (L - lj + WC) % WC;
-      double w0 = W[0];
-      if (L == lj) w0 = piv;
-      if (act) U[(int64_t)j * WC + off] = w0;
-      if (L == 0) ys[j] = y[0];
-      // row j + 17 enters slot 0 (prefetched PF steps ago); fetch step j + PF's
-      W[0] = qW[t];
-      y[0] = qY[t];
-      qW[t] = enter_val(orig, n, j + PF, L, act, sigma);
-      qY[t] = enter_rhs(rhs, vid, n, j + PF + WR);
+      if (act) U[(int64_t)j * WC + off] = L == lj ? piv : prow;
+      if (rl) ys[j] = prow;
+      // row j + 17 (prefetched PF steps ago) takes the pivot's slot; fetch
+      // step j + PF's
+      const double ent = qW[t];
+#pragma unroll
+      for (int s = 0; s < WR; ++s)
+        if (p == s) {
+          asm volatile("" ::: "memory");
+          W[s] = ent;
+        }
+      qW[t] = act ? enter_val(orig, n, j + PF, L, true, sigma)
+                  : (rl ? enter_rhs(rhs, vid, n, j + PF + WR) : 0.0);
     }
   }
   __threadfence_block();
@@ -1020,7 +1029,7 @@ constexpr double kShiftStep = 1e-13;
 // tridiagonal, so one solve converges for any gap far above 1e-15 |B|; a
 // second one follows when the solution did not grow as that implies), then
 // the Rayleigh quotient into wr.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_inviter(const float* orig, int64_t ostride, int n, int kq,
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 5))) void k_inviter(const float* orig, int64_t ostride, int n, int kq,
                                                  int nvec, int v0, const double* w,
                                                  const double* bnorm, double* work, double* xall,
                                                  double* wr) {
@@ -1135,10 +1144,12 @@ __global__ __launch_bounds__(256) void k_band_norm(const float* orig, int64_t os
   }
 }
 
-// vectors per inverse-iteration launch: enough wavefronts to fill every SIMD
-// several times over, with their U workspace (n x 34 float64 each) capped
-constexpr int kInvChunkMax = 8192;
-constexpr int64_t kInvWorkBytes = (int64_t)4 << 30;
+// vectors per inverse-iteration launch: two rounds of five wavefronts on every
+// SIMD (the band solve is latency-bound: 2 -> 5 waves per SIMD took it from
+// 80 to 46 ms at 480 x 2048^2, kq = 64), their U workspace (n x 34 float64
+// each) capped
+constexpr int kInvChunkMax = 10240;
+constexpr int64_t kInvWorkBytes = (int64_t)8 << 30;
 
 __host__ __forceinline__ int inv_chunk(int n, int64_t nvec) {
   int64_t c = kInvWorkBytes / ((int64_t)n * (WC + 1) * (int64_t)sizeof(double));
