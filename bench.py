@@ -309,6 +309,30 @@ def refresh_summary(trace_csv: str, config: str, cmd: str) -> str:
     return "\n".join(out) + "\n"
 
 
+def stats_summary(stats_csv: str, config: str, cmd: str, top: int = 25) -> str:
+    """Markdown table of a rocprofv3 --stats kernel_stats.csv of this bench (the
+    kernels with the largest total time first)."""
+    import csv
+    import re
+    rows = list(csv.DictReader(open(stats_csv)))
+    out = [f"# SCAO step kernels, {config} (rocprofv3 kernel trace statistics)", "",
+           "Command (from the repository root on the box):", "", "```", cmd, "```", "",
+           "Times in ms over every dispatch of the run (warm-up, timed and diagnostic steps; "
+           "with a refresh: its kernels too).", "",
+           "| kernel | calls | avg ms | min ms | max ms | total ms |",
+           "|---|---:|---:|---:|---:|---:|"]
+    for r in rows[:top]:
+        name = r["Name"].replace("(anonymous namespace)::", "")
+        name = re.sub(r"\(.*", "", name).replace("void ", "").strip()
+        if name.startswith("Cijk_"):
+            mt = re.search(r"_MT(\d+x\d+x\d+)_", name)
+            name = "rocBLAS GEMM " + (name[5:9] + " MT" + mt.group(1) if mt else name[:40])
+        out.append(f"| `{name[:80]}` | {r['Calls']} | {float(r['AverageNs']) / 1e6:.3f} | "
+                   f"{float(r['MinNs']) / 1e6:.3f} | {float(r['MaxNs']) / 1e6:.3f} | "
+                   f"{float(r['TotalDurationNs']) / 1e6:.1f} |")
+    return "\n".join(out) + "\n"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -328,6 +352,9 @@ def main():
     ap.add_argument("--refresh-summary", metavar="TRACE_CSV", default=None,
                     help="print the markdown kernel summary of the last refresh in a "
                          "rocprofv3 --kernel-trace CSV of this bench and exit (no GPU use)")
+    ap.add_argument("--stats-summary", metavar="STATS_CSV", default=None,
+                    help="print the markdown table of a rocprofv3 --stats kernel_stats.csv "
+                         "of this bench and exit (no GPU use)")
     ap.add_argument("--pmc-command", default="",
                     help="the commands that made a summary's inputs (recorded verbatim)")
     ap.add_argument("--dominant", default="scao_kron_apply",
@@ -345,6 +372,9 @@ def main():
                          "gradient filter and noise (sparsity=0.7, noise_std=0.01), reported "
                          "in details (0: skip)")
     args = ap.parse_args()
+    if args.stats_summary:
+        print(stats_summary(args.stats_summary, args.config, args.pmc_command))
+        return
     if args.refresh_summary:
         print(refresh_summary(args.refresh_summary, args.config, args.pmc_command))
         return
