@@ -1,8 +1,9 @@
 // Curvature-refresh kernels on gfx950 (scao/preconditioner.py:297-361, 381-406).
 //
 // gram_ema   C = X X^T for X = G (L side, dim m) or X = G^T (R side, dim n) on
-//            fp32 MFMA, 128x128 output tiles staged through LDS in 16-deep
-//            K chunks, fused with the EMA
+//            fp32 MFMA, 128x128 output tiles, operands staged through LDS in
+//            32-deep K chunks (the next chunk's loads in flight under the
+//            current chunk's MFMAs), fused with the EMA
 //               int8:  x = fp32(fp32(fp32(q*s)*rho) + fp32(alpha*C))
 //               fp32:  ema = fp32(fp32(ema*rho) + fp32(alpha*C))  (in place)
 //            (reference: dequantize_sym_int8(...).mul_(rho).add_(alpha*(g@g.T)),
@@ -23,100 +24,155 @@ using namespace scao;
 namespace {
 
 constexpr int GT = SCAO_GRAM_TILE;  // 128
-constexpr int KC = 16;              // K chunk
-constexpr int LP = GT + 4;          // padded LDS row
+constexpr int KC = 32;              // K chunk
+constexpr int LP = GT + 4;          // padded LDS row of an operand chunk
+constexpr int SP = GT + 1;          // LDS row of the staged output tile
 
-__device__ __forceinline__ float gload(const scao_gram_desc& D, int i, int k) {
-  // X[i][k]
-  const int64_t e = D.side == 0 ? D.off + (int64_t)i * D.ld + k : D.off + (int64_t)k * D.ld + i;
-  return ld1(D.g, D.dtype, e);
-}
+// Operand chunks X[r0:r0+128][kb:kb+32], four 4-element loads per thread,
+// held in registers (raw, in the gradient's dtype) from chunk_load until
+// chunk_store converts them into lds[k][r] (row pitch LP).  DT >= 0: the
+// chunk lies inside the factor and is aligned, so the loads are plain vector
+// loads in straight-line code (no branch may join before the MFMAs that
+// hide them); DT = -1: any chunk, masked at the edges, any dtype.
+template <int DT> struct ChunkRaw { typedef v4f T; };
+template <> struct ChunkRaw<SCAO_BF16> { typedef v2u T; };
+template <> struct ChunkRaw<SCAO_F16> { typedef v2u T; };
 
-// Stage X[r0:r0+128][kb:kb+16] into lds[k][r] (zero outside dim x K).
-__device__ __forceinline__ void stage(const scao_gram_desc& D, int dim, int K, int r0, int kb,
-                                      float (*lds)[LP], bool vec) {
+template <int DT, int SIDE>
+__device__ __forceinline__ void chunk_load(const scao_gram_desc& D, int dim, int K, int r0, int kb,
+                                           bool vec, typename ChunkRaw<DT>::T (&x)[4]) {
   const int tid = threadIdx.x;
-  if (D.side == 0) {
-    // rows contiguous in k: thread -> (row, 4 k's)
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int r = tid / 4 + 64 * h, kq = (tid % 4) * 4;
-      const int i = r0 + r;
-      int mk = 0;
-      for (int t = 0; t < 4; ++t) mk |= (i < dim && kb + kq + t < K) ? (1 << t) : 0;
-      v4f x = mk ? ld4(D.g, D.dtype, D.off + (int64_t)i * D.ld + kb + kq, vec && mk == 15, mk)
-                 : v4f{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int t = 0; t < 4; ++t) lds[kq + t][r] = x[t];
+  for (int h = 0; h < 4; ++h) {
+    int i, k;
+    int64_t e;
+    if (SIDE == 0) {
+      // rows contiguous in k: thread -> (row, 4 k's)
+      i = r0 + tid / 8 + 32 * h;
+      k = kb + (tid % 8) * 4;
+      e = D.off + (int64_t)i * D.ld + k;
+    } else {
+      // k rows contiguous in i: thread -> (k, 4 i's)
+      k = kb + tid / 32 + 8 * h;
+      i = r0 + (tid % 32) * 4;
+      e = D.off + (int64_t)k * D.ld + i;
     }
-  } else {
-    // k rows contiguous in i: thread -> (k, 4 i's)
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int kr = tid / 32 + 8 * h, iq = (tid % 32) * 4;
-      const int kk = kb + kr;
+    if constexpr (DT == SCAO_F32) {
+      x[h] = gld4((const float*)D.g + e);
+    } else if constexpr (DT >= 0) {
+      x[h] = *(const gv2u*)((const uint16_t*)D.g + e);
+    } else {
       int mk = 0;
-      for (int t = 0; t < 4; ++t) mk |= (kk < K && r0 + iq + t < dim) ? (1 << t) : 0;
-      v4f x = mk ? ld4(D.g, D.dtype, D.off + (int64_t)kk * D.ld + r0 + iq, vec && mk == 15, mk)
-                 : v4f{0.f, 0.f, 0.f, 0.f};
-      *(v4f*)&lds[kr][iq] = x;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        mk |= (SIDE == 0 ? (i < dim && k + t < K) : (k < K && i + t < dim)) ? (1 << t) : 0;
+      x[h] = mk ? ld4(D.g, D.dtype, e, vec && mk == 15, mk) : v4f{0.f, 0.f, 0.f, 0.f};
     }
   }
 }
 
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gram_ema(const scao_task* __restrict__ tasks,
-                                                  const scao_gram_desc* __restrict__ descs) {
-  __shared__ __attribute__((aligned(16))) float As[2][KC][LP];
-  __shared__ __attribute__((aligned(16))) float Bs[2][KC][LP];
-  __shared__ float red[4];
-  const scao_task tk = tasks[blockIdx.x];
-  const scao_gram_desc D = descs[tk.idx];
-  const int dim = D.side == 0 ? D.rows : D.cols;
-  const int K = D.side == 0 ? D.cols : D.rows;
-  const int i0 = tk.a * GT, j0 = tk.b * GT;
-  const int w = threadIdx.x / 64, l = threadIdx.x % 64;
-  const int wr = (w / 2) * 64, wc = (w % 2) * 64;
-  const bool vec = ((D.off | D.ld) % 4 == 0) &&
-                   (((uintptr_t)D.g & (D.dtype == SCAO_F32 ? 15u : 7u)) == 0);
+template <int DT>
+__device__ __forceinline__ v4f chunk_f32(const typename ChunkRaw<DT>::T& x) {
+  if constexpr (DT == SCAO_BF16 || DT == SCAO_F16) {
+    const uint16_t h[4] = {(uint16_t)(x[0] & 0xffff), (uint16_t)(x[0] >> 16),
+                           (uint16_t)(x[1] & 0xffff), (uint16_t)(x[1] >> 16)};
+    v4f r;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) r[t] = DT == SCAO_BF16 ? bf16_to_f(h[t]) : f16_to_f(h[t]);
+    return r;
+  } else {
+    return x;
+  }
+}
 
-  // Two-level sum: the MFMAs accumulate FOLD consecutive K values in acc,
-  // which is then added to tot and cleared.  One fp32 accumulator over all
-  // of K (2048-4096 here, K/4 dependent MFMA adds) drifts by about
-  // sqrt(K/4) ulps, above the reference's own float32 GEMM; two levels of
-  // sqrt(FOLD/4) and sqrt(K/FOLD) bring that under it.  Both sums are exact
-  // sums of the same products, so only rounding changes.
-  constexpr int FOLD = 128;
-  v4f acc[4][4], tot[4][4];
+template <int DT, int SIDE>
+__device__ __forceinline__ void chunk_store(float* lds, const typename ChunkRaw<DT>::T (&x)[4]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const v4f v = chunk_f32<DT>(x[h]);
+    if (SIDE == 0) {
+      const int r = tid / 8 + 32 * h, kq = (tid % 8) * 4;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) lds[(kq + t) * LP + r] = v[t];
+    } else {
+      *(v4f*)&lds[(tid / 32 + 8 * h) * LP + (tid % 32) * 4] = v;
+    }
+  }
+}
+
+// Two-level sum: the MFMAs accumulate FOLD consecutive K values in acc,
+// which is then added to tot and cleared.  One fp32 accumulator over all of
+// K (2048-4096 here, K/4 dependent MFMA adds) drifts by about sqrt(K/4) ulps,
+// above the reference's own float32 GEMM; two levels of sqrt(FOLD/4) and
+// sqrt(K/FOLD) bring that under it.  Both sums are exact sums of the same
+// products, so only rounding changes.
+constexpr int FOLD = 128;
+static_assert(FOLD % KC == 0, "fold");
+
+// The K loop of one 128 x 128 tile: the next chunk's loads go out before
+// this chunk's MFMAs and land in LDS after them, so their latency hides
+// under the products.  Wave w computes rows wr.., columns wc.. (64 x 64).
+template <int DT, int SIDE>
+__device__ __forceinline__ void gram_kloop(const scao_gram_desc& D, int dim, int K, int i0, int j0,
+                                           bool diag, bool vec, float* As, float* Bs, int wr,
+                                           int wc, v4f (&tot)[4][4]) {
+  const int l = threadIdx.x % 64;
+  v4f acc[4][4];
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int b = 0; b < 4; ++b) acc[a][b] = tot[a][b] = v4f{0.f, 0.f, 0.f, 0.f};
-
-  stage(D, dim, K, i0, 0, As[0], vec);
-  stage(D, dim, K, j0, 0, Bs[0], vec);
+  typename ChunkRaw<DT>::T xa[4], xb[4];
+  chunk_load<DT, SIDE>(D, dim, K, i0, 0, vec, xa);
+  if (!diag) chunk_load<DT, SIDE>(D, dim, K, j0, 0, vec, xb);
+  chunk_store<DT, SIDE>(As, xa);
+  if (!diag) chunk_store<DT, SIDE>(Bs, xb);
   __syncthreads();
   int buf = 0;
   for (int kb = 0; kb < K; kb += KC) {
-    if (kb + KC < K) {
-      stage(D, dim, K, i0, kb + KC, As[buf ^ 1], vec);
-      stage(D, dim, K, j0, kb + KC, Bs[buf ^ 1], vec);
+    const bool more = kb + KC < K;
+    if (more) {
+      chunk_load<DT, SIDE>(D, dim, K, i0, kb + KC, vec, xa);
+      if (!diag) chunk_load<DT, SIDE>(D, dim, K, j0, kb + KC, vec, xb);
     }
+    const float* Ab = As + buf * KC * LP + (l / 16) * LP + wr + (l % 16);
+    const float* Bb = (diag ? As : Bs) + buf * KC * LP + (l / 16) * LP + wc + (l % 16);
+    // operands of step ks + 1 are read from LDS while step ks's MFMAs run
+    float af[2][4], bf[2][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) af[0][a] = Ab[16 * a];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) bf[0][b] = Bb[16 * b];
 #pragma unroll
     for (int ks = 0; ks < KC / 4; ++ks) {
-      const int kr = 4 * ks + l / 16;
-      float af[4], bf[4];
+      const int cur = ks & 1;
+      if (ks + 1 < KC / 4) {
 #pragma unroll
-      for (int a = 0; a < 4; ++a) af[a] = As[buf][kr][wr + 16 * a + (l % 16)];
+        for (int a = 0; a < 4; ++a) af[cur ^ 1][a] = Ab[4 * (ks + 1) * LP + 16 * a];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) bf[b] = Bs[buf][kr][wc + 16 * b + (l % 16)];
+        for (int b = 0; b < 4; ++b) bf[cur ^ 1][b] = Bb[4 * (ks + 1) * LP + 16 * b];
+      }
 #pragma unroll
       for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] = mfma16(af[a], bf[b], acc[a][b]);
+        for (int b = 0; b < 4; ++b) acc[a][b] = mfma16(af[cur][a], bf[cur][b], acc[a][b]);
+    }
+    // the schedule: step 0's four LDS reads, then per step the next step's
+    // four reads ahead of its sixteen MFMAs
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+#pragma unroll
+    for (int ks = 0; ks < KC / 4; ++ks) {
+      if (ks + 1 < KC / 4) __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+    }
+    if (more) {
+      chunk_store<DT, SIDE>(As + (buf ^ 1) * KC * LP, xa);
+      if (!diag) chunk_store<DT, SIDE>(Bs + (buf ^ 1) * KC * LP, xb);
     }
     __syncthreads();
     buf ^= 1;
-    if ((kb + KC) % FOLD == 0 || kb + KC >= K) {
+    if ((kb + KC) % FOLD == 0 || !more) {
 #pragma unroll
       for (int a = 0; a < 4; ++a)
 #pragma unroll
@@ -126,73 +182,140 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
         }
     }
   }
+}
 
-  // EMA epilogue: element (i, j) = tot[a][b][r],
-  // i = i0 + wr + 16a + 4*(l/16) + r, j = j0 + wc + 16b + l%16
-  const float sf = D.q ? (float)(*D.scale) : 0.f;
-  float amax = 0.f;
+// EMA update of the output tile rows r0.., columns c0.. from the product
+// tile staged in S (S[row][col], or S[col][row] when `tr`).  A tile inside
+// a factor with dim % 4 == 0 goes 4 elements per thread and pass (one 32-bit
+// load of 4 codes or a float4 of the old EMA, a float4 store), each
+// wavefront covering two rows; the old values of all 16 passes are loaded
+// before any is used.  Other tiles go element by element.
+__device__ __forceinline__ float ema_one(const scao_gram_desc& D, float old, float prod, float sf,
+                                         float& amax) {
+  const float add = D.alpha * prod;
+  if (D.q) {
+    const float x = (old * sf) * D.rho + add;
+    amax = fmaxf(amax, fabsf(x));
+    return x;
+  }
+  return old * D.rho + add;
+}
+
+__device__ __forceinline__ void ema_tile(const scao_gram_desc& D, const float* S, int dim, int r0,
+                                         int c0, bool tr, float sf, float& amax) {
+  const int tid = threadIdx.x;
+  const bool vec4 = dim % 4 == 0 && r0 + GT <= dim && c0 + GT <= dim &&
+                    (((uintptr_t)D.ema | (uintptr_t)D.q) & 15) == 0;
+  if (vec4) {
+    constexpr int NP = GT * GT / 4 / 256;   // 16 passes
+    uint32_t qv[NP];
+    v4f ov[NP];
+#pragma unroll
+    for (int t = 0; t < NP; ++t) {
+      const int idx = t * 256 + tid, row = idx / (GT / 4), col = (idx % (GT / 4)) * 4;
+      const int64_t e = (int64_t)(r0 + row) * dim + c0 + col;
+      if (D.q)
+        qv[t] = gld1((const uint32_t*)(D.q + e));
+      else
+        ov[t] = gld4(D.ema + e);
+    }
+#pragma unroll
+    for (int t = 0; t < NP; ++t) {
+      const int idx = t * 256 + tid, row = idx / (GT / 4), col = (idx % (GT / 4)) * 4;
+      const int64_t e = (int64_t)(r0 + row) * dim + c0 + col;
+      v4f x;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float prod = tr ? S[(col + u) * SP + row] : S[row * SP + col + u];
+        const float old = D.q ? (float)(int8_t)(uint8_t)(qv[t] >> (8 * u)) : ov[t][u];
+        x[u] = ema_one(D, old, prod, sf, amax);
+      }
+      gst4(D.ema + e, x);
+    }
+    return;
+  }
+  for (int p0 = 0; p0 < GT * GT / 256; p0 += 16) {
+    float old[16];
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int idx = (p0 + t) * 256 + tid, row = idx / GT, col = idx % GT;
+      const int i = r0 + row, j = c0 + col;
+      const int64_t e = (int64_t)i * dim + j;
+      old[t] = 0.f;
+      if (i < dim && j < dim) old[t] = D.q ? (float)D.q[e] : D.ema[e];
+    }
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int idx = (p0 + t) * 256 + tid, row = idx / GT, col = idx % GT;
+      const int i = r0 + row, j = c0 + col;
+      if (i >= dim || j >= dim) continue;
+      D.ema[(int64_t)i * dim + j] =
+          ema_one(D, old[t], tr ? S[col * SP + row] : S[row * SP + col], sf, amax);
+    }
+  }
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_gram_ema(const scao_task* __restrict__ tasks,
+                                                  const scao_gram_desc* __restrict__ descs) {
+  // two double-buffered operand chunks; after the K loop, the 128 x 128
+  // product tile (pitch SP)
+  __shared__ __attribute__((aligned(16))) float smem[2 * 2 * KC * LP];
+  static_assert(GT * SP <= 2 * 2 * KC * LP, "output tile staging");
+  __shared__ float red[4];
+  float* As = smem;                 // [2][KC][LP]
+  float* Bs = smem + 2 * KC * LP;   // [2][KC][LP]
+  const scao_task tk = tasks[blockIdx.x];
+  const scao_gram_desc D = descs[tk.idx];
+  const int dim = D.side == 0 ? D.rows : D.cols;
+  const int K = D.side == 0 ? D.cols : D.rows;
+  const int i0 = tk.a * GT, j0 = tk.b * GT;
+  const bool diag = tk.a == tk.b;   // both operands are the same rows
+  const int w = threadIdx.x / 64, l = threadIdx.x % 64;
+  const int wr = (w / 2) * 64, wc = (w % 2) * 64;
+  const bool vec = ((D.off | D.ld) % 4 == 0) &&
+                   (((uintptr_t)D.g & (D.dtype == SCAO_F32 ? 15u : 7u)) == 0);
+
+  v4f tot[4][4];
+  const bool whole = vec && K % KC == 0 && i0 + GT <= dim && j0 + GT <= dim;
+#define SCAO_GRAM_KLOOP(DT, SIDE) \
+  gram_kloop<DT, SIDE>(D, dim, K, i0, j0, diag, vec, As, Bs, wr, wc, tot)
+  if (whole && D.dtype == SCAO_F32 && D.side == 0)
+    SCAO_GRAM_KLOOP(SCAO_F32, 0);
+  else if (whole && D.dtype == SCAO_F32)
+    SCAO_GRAM_KLOOP(SCAO_F32, 1);
+  else if (whole && D.dtype == SCAO_BF16 && D.side == 0)
+    SCAO_GRAM_KLOOP(SCAO_BF16, 0);
+  else if (whole && D.dtype == SCAO_BF16)
+    SCAO_GRAM_KLOOP(SCAO_BF16, 1);
+  else if (whole && D.dtype == SCAO_F16 && D.side == 0)
+    SCAO_GRAM_KLOOP(SCAO_F16, 0);
+  else if (whole && D.dtype == SCAO_F16)
+    SCAO_GRAM_KLOOP(SCAO_F16, 1);
+  else if (D.side == 0)
+    SCAO_GRAM_KLOOP(-1, 0);
+  else
+    SCAO_GRAM_KLOOP(-1, 1);
+#undef SCAO_GRAM_KLOOP
+
+  // EMA epilogue.  The product tile goes to LDS (the operand buffers are free
+  // after the K loop's last barrier): element (i0 + row, j0 + col) is
+  // tot[a][b][r] with row = wr + 16a + 4*(l/16) + r, col = wc + 16b + l%16.
+  // A task with a > b of a symmetric factor also updates the transposed tile
+  // (b, a): element (j, i) takes the same product as (i, j).
+  float* S = smem;
 #pragma unroll
   for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int i = i0 + wr + 16 * a + 4 * (l / 16) + r;
-      if (i >= dim) continue;
+    for (int b = 0; b < 4; ++b)
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int j = j0 + wc + 16 * b + (l % 16);
-        if (j >= dim) continue;
-        const int64_t e = (int64_t)i * dim + j;
-        const float add = D.alpha * tot[a][b][r];
-        if (D.q) {
-          const float old = ((float)D.q[e] * sf) * D.rho;
-          const float x = old + add;
-          D.ema[e] = x;
-          amax = fmaxf(amax, fabsf(x));
-        } else {
-          D.ema[e] = D.ema[e] * D.rho + add;
-        }
-      }
-    }
-  // the transposed tile (b, a) of a symmetric factor: element (j, i) takes
-  // the same product as (i, j).  Staged through LDS (the operand buffers are
-  // free after the K loop), one 64 x 64 wave sub-tile per buffer, two waves at
-  // a time, so the global accesses run along rows of the transposed tile.
-  const bool mirror = (D.flags & SCAO_GRAM_SYM) && tk.a != tk.b;
-  if (mirror) {
-    static_assert(sizeof(As) >= 64 * 65 * sizeof(float), "staging");
-    float* S = (w % 2 == 0) ? &As[0][0][0] : &Bs[0][0][0];
-    for (int half = 0; half < 2; ++half) {
-      const bool mine = (w / 2) == half;
-      if (mine) {
-#pragma unroll
-        for (int a = 0; a < 4; ++a)
-#pragma unroll
-          for (int r = 0; r < 4; ++r)
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-              S[(16 * b + (l % 16)) * 65 + 16 * a + 4 * (l / 16) + r] = tot[a][b][r];
-      }
-      __syncthreads();
-      if (mine) {
-        const int i = i0 + wr + l;             // column of the transposed tile
-        for (int jj = 0; jj < 64; ++jj) {
-          const int j = j0 + wc + jj;          // row of the transposed tile
-          if (i >= dim || j >= dim) continue;
-          const int64_t e = (int64_t)j * dim + i;
-          const float add = D.alpha * S[jj * 65 + l];
-          if (D.q) {
-            const float old = ((float)D.q[e] * sf) * D.rho;
-            const float x = old + add;
-            D.ema[e] = x;
-            amax = fmaxf(amax, fabsf(x));
-          } else {
-            D.ema[e] = D.ema[e] * D.rho + add;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  }
+      for (int r = 0; r < 4; ++r)
+        S[(wr + 16 * a + 4 * (l / 16) + r) * SP + wc + 16 * b + (l % 16)] = tot[a][b][r];
+  __syncthreads();
+  const float sf = D.q ? (float)(*D.scale) : 0.f;
+  float amax = 0.f;
+  ema_tile(D, S, dim, i0, j0, false, sf, amax);
+  const bool mirror = (D.flags & SCAO_GRAM_SYM) && !diag;
+  if (mirror) ema_tile(D, S, dim, j0, i0, true, sf, amax);
   if (D.q) {
     const float mx = block_max(amax, red);
     if (threadIdx.x == 0) {
