@@ -134,16 +134,36 @@ __device__ __forceinline__ void project_tile(const scao_leaf_desc& L, const scao
     store_chunk();
     __syncthreads();
     if (i0 + PR < m) load_chunk(i0 + PR); // in flight during the MFMAs below
+    // operands of step s + 1 are read from LDS while step s's MFMAs run
+    v4f b[2];
+    float a[2][NQ];
+    b[0] = *(const v4f*)&Gs[kk][64 * w + 4 * (l % 16)];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) a[0][q] = Us[kk][16 * q + (l % 16)];
 #pragma unroll
     for (int s = 0; s < PR / 4; ++s) {
-      const v4f b = *(const v4f*)&Gs[4 * s + kk][64 * w + 4 * (l % 16)];
-      float a[NQ];
+      const int cur = s & 1;
+      if (s + 1 < PR / 4) {
+        b[cur ^ 1] = *(const v4f*)&Gs[4 * (s + 1) + kk][64 * w + 4 * (l % 16)];
 #pragma unroll
-      for (int q = 0; q < NQ; ++q) a[q] = Us[4 * s + kk][16 * q + (l % 16)];
+        for (int q = 0; q < NQ; ++q) a[cur ^ 1][q] = Us[4 * (s + 1) + kk][16 * q + (l % 16)];
+      }
 #pragma unroll
       for (int q = 0; q < NQ; ++q)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[q][t] = mfma16(a[q], b[t], acc[q][t]);
+        for (int t = 0; t < 4; ++t) acc[q][t] = mfma16(a[cur][q], b[cur][t], acc[q][t]);
+    }
+    if (FAST && CR == 64) {
+      // the schedule: step 0's reads, then per step the next step's reads
+      // ahead of its 16 MFMAs (a G float4 and four U_l values: three LDS
+      // instructions).  Measured faster at CR = 64 only: the 128-wide tile
+      // runs slower with it.
+      __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+#pragma unroll
+      for (int s = 0; s < PR / 4; ++s) {
+        if (s + 1 < PR / 4) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+      }
     }
   }
   // T[c][j] for c = c0 + 16q + 4*(l/16) + r, j = jl + t
