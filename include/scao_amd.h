@@ -301,7 +301,9 @@ int scao_eig_panel_qr(float* A, int64_t stride, int n, int c0, int batch, float*
  * R (mr x mr, at A + i*sA, leading dim ldA; every matrix): with the panel's
  * reflectors V and correction W (mr x b rows at V + i*sV / W + i*sW, leading
  * dims ldV / ldW), A <- A - V W^T - W V^T for the elements with row >=
- * column (nothing above the diagonal is read or written); with Vn (the next
+ * column (the elements above the diagonal are never read; those of the
+ * 64 x 64 diagonal tiles may be overwritten with meaningless values when
+ * every leading dimension and mr are multiples of 4); with Vn (the next
  * panel's reflectors, mr x b), also Y = A_new Vn for the symmetric A_new into
  * Y + i*sY (mr x b, row-major), using `work` (scao_eig_sy2sb_work(mr, batch)
  * bytes) for fixed-order partial sums.  Replaces, per panel, the two-sided

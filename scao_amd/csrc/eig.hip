@@ -27,6 +27,8 @@
 // The tridiagonal's reflectors are never stored: the vectors come from the
 // band matrix, so only stage 1's reflectors (kept in the panels of A) are
 // applied to them.
+#include <type_traits>
+
 #include "scao_common.hpp"
 
 using namespace scao;
@@ -175,7 +177,8 @@ __global__ __launch_bounds__(1024) void k_panel_qr(float* A, int64_t stride, int
 // and, when Vn (the next panel's reflectors, rows from r1) is given,
 //   Y  = A_new Vn                 (the symmetric matrix A_new)
 // Nothing above the diagonal is read or written: a diagonal tile is read from
-// its lower half and mirrored.  64 x 64 tiles; the workgroup of tile-row I
+// its lower half and mirrored (k_sy2sb_update_vec below, for aligned
+// operands, also writes the upper half of diagonal tiles; nothing reads it).  64 x 64 tiles; the workgroup of tile-row I
 // and chunk c takes tiles (I, J), J in [UCH c, min(UCH (c+1), I+1)); it
 // writes its direct product sum_J A(I,J) Vn(J) to Pd[I][c] and, per tile
 // below the diagonal, A(I,J)^T Vn(I) to Pt[J][I]; k_sy2sb_reduce sums them
@@ -355,6 +358,223 @@ __global__ __launch_bounds__(256) void k_sy2sb_update(float* A, int64_t sA, int 
     float* dst = Pd + (((int64_t)mat * nt + I) * nch + c) * (UT * 16);
 #pragma unroll
     for (int r = 0; r < 4; ++r) dst[(16 * w + 4 * kk + r) * 16 + l % 16] = ay[r];
+  }
+}
+
+// The same update for 16-byte aligned operands (every leading dimension and
+// mr a multiple of 4), with the A tile held in registers: lane l of wave w
+// keeps rows 16w + 4(l/16) + r, columns 4(l%16) .. 4(l%16)+3 of the tile,
+// which is the MFMA output layout once the update's columns are permuted
+// (MFMA tile t, lane column jj <-> tile column 4jj + t).  So the rank-32
+// update happens in registers and the tile goes back to memory as float4
+// rows; LDS holds it only for the two Y products.  The LDS operands are
+// double-buffered (the next panel's reflector rows triple-buffered), so one
+// block barrier per tile suffices: before barrier J every wave writes tile
+// J's updated values and tile J+1's W/V/Vn rows, after it the Y products of
+// tile J run while tile J+1's loads are in flight.  The arithmetic is that of
+// k_sy2sb_update term by term, so the results are bit-identical.
+constexpr int UQ = 3;   // slots of the next panel's reflector rows
+
+__global__ __launch_bounds__(256) void k_sy2sb_update_vec(float* A, int64_t sA, int ldA, int mr,
+                                                          const float* V, int64_t sV, int ldV,
+                                                          const float* W, int64_t sW, int ldW,
+                                                          const float* Vn, int64_t sVn, int ldVn,
+                                                          float* Pd, float* Pt, int nt, int nch) {
+  __shared__ __attribute__((aligned(16))) float As[2][UT][UPT];
+  __shared__ float Ls[UT][UPL];      // [V_I | W_I]
+  __shared__ float Rs[2][UT][UPL];   // [W_J | V_J]
+  __shared__ float VnI[UT][UPV];
+  __shared__ float VnJ[UQ][UT][UPV];
+  int I, c;
+  ut_task(blockIdx.x, I, c);
+  const int mat = blockIdx.y;
+  float* Am = A + (int64_t)mat * sA;
+  V += (int64_t)mat * sV;
+  W += (int64_t)mat * sW;
+  const bool doY = Vn != nullptr;
+  if (doY) Vn += (int64_t)mat * sVn;
+  const int tid = threadIdx.x, w = tid / 64, l = tid % 64, kk = l / 16, jj = l % 16;
+
+  // Tile loads: every address stays inside the region (rows and columns at or
+  // beyond mr read row / column 0); such values are replaced by zeros where
+  // they are used, not where they land, so no wait follows a load.  The
+  // block's (at most UCH) tiles are unrolled, so each prefetch buffer has a
+  // fixed register name and nothing is copied between iterations.
+  const int gr0 = UT * I + 16 * w + 4 * kk;   // the lane's first tile row
+  // Every prefetch is issued whether or not its tile exists (a tile past the
+  // block's last reads the region's first element, one line for all lanes):
+  // a load issued on one path only would make the compiler wait for all
+  // loads at the join.
+  const int j0 = UCH * c, j1 = UCH * c + UCH < I + 1 ? UCH * c + UCH : I + 1;
+  auto load_a = [&](int J, v4f (&x)[4]) {
+    const int gj = UT * J + 4 * jj;
+    const bool cok = J < j1 && gj < mr;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const bool ok = cok && gr0 + r < mr;
+      x[r] = gld4(Am + (int64_t)(ok ? gr0 + r : 0) * ldA + (ok ? gj : 0));
+    }
+  };
+  // W_J, V_J, Vn_J rows: thread -> row tid/4, columns 4(tid%4) ..
+  const int rrow = tid / 4, rq = (tid % 4) * 4;
+  auto load_rows = [&](int J, v4f (&x)[3]) {
+    const int gj = UT * J + rrow;
+    const int64_t g = J < j1 && gj < mr ? gj : 0;
+    x[0] = gld4(W + g * ldW + rq);
+    x[1] = gld4(V + g * ldV + rq);
+    x[2] = gld4(doY ? Vn + g * ldVn + rq : W + rq);
+  };
+  auto put_rows = [&](int J, int b, int slot, const v4f (&x)[3]) {
+    const bool ok = UT * J + rrow < mr;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      Rs[b][rrow][rq + t] = ok ? x[0][t] : 0.f;
+      Rs[b][rrow][16 + rq + t] = ok ? x[1][t] : 0.f;
+      VnJ[slot][rrow][rq + t] = ok && doY ? x[2][t] : 0.f;
+    }
+  };
+
+  v4f ay = {0.f, 0.f, 0.f, 0.f};
+  // EDGE: the last tile-row of a region whose size is not a multiple of 64
+  // (rows, and the diagonal tile's columns, reach past mr).  Elsewhere every
+  // element of every tile exists and the stores are four float4 rows per
+  // lane on every path; a diagonal tile then also writes its upper half,
+  // which nothing reads (the stored lower half defines the matrix), so that
+  // the number of memory operations in flight is the same on every path and
+  // each wait is for the one load it needs.
+  auto tiles = [&](auto edge_tag) {
+    constexpr bool EDGE = decltype(edge_tag)::value;
+    v4f ab[3][4], rb[2][3], li[3];
+    v4f keep[UCH][4], ptk[UCH];   // each tile's new values and transposed partial
+    // the tile-row's own V, W, Vn rows and the first two tiles, all in flight
+    // together
+    {
+      const int gi = UT * I + rrow;
+      const int64_t g = gi < mr ? gi : 0;
+      li[0] = gld4(V + g * ldV + rq);
+      li[1] = gld4(W + g * ldW + rq);
+      li[2] = gld4(doY ? Vn + g * ldVn + rq : W + rq);
+    }
+    load_a(j0, ab[0]);
+    load_a(j0 + 1, ab[1]);
+    load_rows(j0, rb[0]);
+    load_rows(j0 + 1, rb[1]);
+    {
+      const bool ok = UT * I + rrow < mr;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        Ls[rrow][rq + t] = ok ? li[0][t] : 0.f;
+        Ls[rrow][16 + rq + t] = ok ? li[1][t] : 0.f;
+        VnI[rrow][rq + t] = ok && doY ? li[2][t] : 0.f;
+      }
+    }
+    put_rows(j0, 0, 0, rb[0]);
+    __syncthreads();
+#pragma unroll
+    for (int jt = 0; jt < UCH; ++jt) {
+      const int J = j0 + jt;
+      if (J >= j1) break;
+      const int b = jt & 1, slot = jt % UQ;
+      const bool diag = J == I;
+      load_a(J + 2, ab[(jt + 2) % 3]);   // two tiles of A in flight
+      // A_new = A - [V_I W_I] [W_J V_J]^T, in the lane's own elements
+      v4f d[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) d[t] = v4f{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k4 = 0; k4 < 8; ++k4) {
+        const int q = 4 * k4 + kk;
+        const float a = Ls[16 * w + jj][q];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) d[t] = mfma16(a, Rs[b][4 * jj + t][q], d[t]);
+      }
+      // the next tile's W/V/Vn rows (loaded one tile ahead)
+      if (J + 1 < j1) put_rows(J + 1, b ^ 1, (jt + 1) % UQ, rb[(jt + 1) & 1]);
+      const int gj = UT * J + 4 * jj;
+      v4f (&an)[4] = keep[jt];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const bool ok = !EDGE || (gj < mr && gr0 + r < mr);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) an[r][t] = (ok ? ab[jt % 3][r][t] : 0.f) - d[t][r];
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) *(v4f*)&As[b][16 * w + 4 * kk + r][4 * jj] = an[r];
+      load_rows(J + 2, rb[jt & 1]);
+      __syncthreads();
+      if (diag) {                      // the stored (lower) half defines the matrix
+#pragma unroll
+        for (int h = 0; h < UT * UT / 256; ++h) {
+          const int idx = tid + 256 * h, row = idx / UT, col = idx % UT;
+          if (row < col) As[b][row][col] = As[b][col][row];
+        }
+        __syncthreads();
+      }
+      if (doY) {
+        // direct part: rows 16w.. of A_new(I,J) Vn(J); transposed part: rows
+        // 16w.. of A_new(I,J)^T Vn(I), for tile-row J
+        if (!diag) {
+          v4f pt = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int k4 = 0; k4 < 16; ++k4) {
+            const int j = 4 * k4 + kk;
+            ay = mfma16(As[b][16 * w + jj][j], VnJ[slot][j][jj], ay);
+            pt = mfma16(As[b][j][16 * w + jj], VnI[j][jj], pt);
+          }
+          ptk[jt] = pt;
+        } else {
+#pragma unroll
+          for (int k4 = 0; k4 < 16; ++k4) {
+            const int j = 4 * k4 + kk;
+            ay = mfma16(As[b][16 * w + jj][j], VnJ[slot][j][jj], ay);
+          }
+        }
+      }
+    }
+    // Every global store of the block goes out here, after the last load:
+    // with stores and loads both in flight the compiler can only wait for
+    // all of them (vmcnt(0)), which would expose each prefetch's latency.
+#pragma unroll
+    for (int jt = 0; jt < UCH; ++jt) {
+      const int J = j0 + jt;
+      if (J >= j1) break;
+      const bool diag = J == I;
+      const int gj = UT * J + 4 * jj;
+      if (!EDGE) {
+        // a diagonal tile also writes its upper half, which nothing reads
+#pragma unroll
+        for (int r = 0; r < 4; ++r) gst4(Am + (int64_t)(gr0 + r) * ldA + gj, keep[jt][r]);
+      } else {
+        // the lower triangle only, inside the region
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int gi = gr0 + r;
+          if (gi >= mr || gj >= mr) continue;
+          float* dst = Am + (int64_t)gi * ldA + gj;
+          if (!diag) {
+            gst4(dst, keep[jt][r]);
+          } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              if (gi >= gj + t) dst[t] = keep[jt][r][t];
+          }
+        }
+      }
+      if (doY && !diag) {
+        float* dst = Pt + (((int64_t)mat * nt + J) * nt + I) * (UT * 16);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dst[(16 * w + 4 * kk + r) * 16 + jj] = ptk[jt][r];
+      }
+    }
+  };
+  if (UT * I + UT <= mr)
+    tiles(std::false_type{});
+  else
+    tiles(std::true_type{});
+  if (doY) {
+    float* dst = Pd + (((int64_t)mat * nt + I) * nch + c) * (UT * 16);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dst[(16 * w + 4 * kk + r) * 16 + jj] = ay[r];
   }
 }
 
@@ -1216,8 +1436,16 @@ extern "C" int scao_eig_sy2sb_update(float* A, int64_t sA, int ldA, int mr, int 
   float* Pd = (float*)work;
   float* Pt = Pd + (int64_t)batch * nt * nch * UT * 16;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(k_sy2sb_update, dim3(ntask, batch), dim3(256), 0, s, A, sA, ldA, mr, V, sV,
-                     ldV, W, sW, ldW, Vn, sVn, ldVn, Pd, Pt, nt, nch);
+  const auto al16 = [](const void* p) { return ((uintptr_t)p & 15u) == 0; };
+  const bool vec = mr % 4 == 0 && ldA % 4 == 0 && ldV % 4 == 0 && ldW % 4 == 0 && sA % 4 == 0 &&
+                   sV % 4 == 0 && sW % 4 == 0 && al16(A) && al16(V) && al16(W) &&
+                   (!Vn || (ldVn % 4 == 0 && sVn % 4 == 0 && al16(Vn)));
+  if (vec)
+    hipLaunchKernelGGL(k_sy2sb_update_vec, dim3(ntask, batch), dim3(256), 0, s, A, sA, ldA, mr, V,
+                       sV, ldV, W, sW, ldW, Vn, sVn, ldVn, Pd, Pt, nt, nch);
+  else
+    hipLaunchKernelGGL(k_sy2sb_update, dim3(ntask, batch), dim3(256), 0, s, A, sA, ldA, mr, V, sV,
+                       ldV, W, sW, ldW, Vn, sVn, ldVn, Pd, Pt, nt, nch);
   SCAO_LAUNCH_CHECK("scao_eig_sy2sb_update");
   if (Vn) {
     hipLaunchKernelGGL(k_sy2sb_reduce, dim3(nt, batch), dim3(256), 0, s, Pd, Pt, Y, sY, mr, nt,
