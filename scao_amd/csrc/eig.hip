@@ -751,7 +751,12 @@ __device__ __forceinline__ void wave_sync() {
 __device__ __forceinline__ int sb_ntasks(int n, int s) { return (n - 1 - s + NB - 1) / NB; }
 
 // Wait until the wavefront running sweep s-1 has finished `tasks` of its tasks.
-__device__ __forceinline__ void sb_wait(volatile int* prog, int s, int tasks) {
+// The progress words live in LDS and are reached through an LDS-typed
+// pointer: a generic (flat) access would count as a vector memory operation,
+// and each poll would wait for every load and store of the wave.
+typedef __attribute__((address_space(3))) int lds_int;
+
+__device__ __forceinline__ void sb_wait(lds_int* prog, int s, int tasks) {
   if (s == 0) return;
   const int w = (s - 1) % SB_W;
   const int target = (s - 1) * SB_BIG + tasks;
@@ -763,7 +768,8 @@ __device__ __forceinline__ void sb_wait(volatile int* prog, int s, int tasks) {
 __global__ __launch_bounds__(SB_W * 64) void k_sb2st(double* band, int n, double* dout,
                                                      double* eout) {
   __shared__ Sb2stLds Sall[SB_W];
-  __shared__ int prog[SB_W];
+  __shared__ int prog_s[SB_W];
+  lds_int* prog = (lds_int*)prog_s;
   const int wid = threadIdx.x >> 6, l = threadIdx.x & 63;
   Sb2stLds& S = Sall[wid];
   double* Bm = band + (int64_t)blockIdx.x * n * BW;
