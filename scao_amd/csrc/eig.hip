@@ -41,7 +41,9 @@ constexpr int OW = NB + 1;           // 17: pitch of the original band copy
 
 // ------------------------------------------------------------ panel QR ---
 // Block reduction of NV floats over a 1024-thread workgroup: every thread
-// receives the NV sums in out[] (LDS).
+// receives the NV sums in out[] (LDS).  (A reduce-scatter across the wave's
+// lanes, 28 shuffles for 16 values instead of 96, measured slower: its
+// lane-dependent selects cost more than the shuffles they save.)
 template <int NV>
 __device__ __forceinline__ void block_sum_f(float (&x)[NV], float (*red)[NV + 1], float* out) {
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
@@ -73,6 +75,7 @@ __global__ __launch_bounds__(1024) void k_panel_qr(float* A, int64_t stride, int
                                                    float* Tout, float* band, int64_t bstride) {
   __shared__ float red[16][NB + 1];
   __shared__ float bc[NB + 2];
+  __shared__ float rowj[2][NB];
   __shared__ float Ts[NB][NB];
   __shared__ float betas[NB];
   const int tid = threadIdx.x;
@@ -89,28 +92,42 @@ __global__ __launch_bounds__(1024) void k_panel_qr(float* A, int64_t stride, int
   }
   if (tid < NB * NB) Ts[tid / NB][tid % NB] = 0.f;
   __syncthreads();
+  // Column j: one reduction gives G[c] = sum over rows i > j of P[i][j] P[i][c]
+  // for every c (G[j] = sigma^2); with v = (1, scale * P[j+1:, j]) every dot
+  // v^T P[:, c] is then P[j][c] + scale * G[c] (the trailing columns' w_c and
+  // the earlier reflectors' d_c for T alike), so a column costs one block
+  // reduction.  Row j comes from thread j through LDS, double-buffered by
+  // column parity (a slow thread may still read the previous column's).
   for (int j = 0; j < kk; ++j) {
-    // alpha = P[row j][j] (thread j, h = 0); sigma^2 over rows below j
-    if (tid == j) bc[NB] = P[0][j];
-    float s2[1] = {0.f};
+    float* rj = rowj[j & 1];
+    if (tid == j) {
+#pragma unroll
+      for (int c = 0; c < NB; ++c) rj[c] = P[0][c];
+    }
+    float acc[NB];
+#pragma unroll
+    for (int c = 0; c < NB; ++c) acc[c] = 0.f;
 #pragma unroll
     for (int h = 0; h < RPT; ++h) {
       const int row = tid + 1024 * h;
-      if (row > j && row < m) s2[0] = fmaf(P[h][j], P[h][j], s2[0]);
+      if (row > j && row < m) {
+        const float pj = P[h][j];
+#pragma unroll
+        for (int c = 0; c < NB; ++c) acc[c] = fmaf(pj, P[h][c], acc[c]);
+      }
     }
-    block_sum_f<1>(s2, (float(*)[2])red, bc + NB + 1);
-    const float alpha = bc[NB], sig2 = bc[NB + 1];
+    block_sum_f<NB>(acc, red, bc);
+    const float alpha = rj[j], sig2 = bc[j];
     float tau = 0.f, beta = alpha, scale = 0.f;
     if (sig2 > 0.f) {
       beta = -copysignf(sqrtf(alpha * alpha + sig2), alpha);
       tau = (beta - alpha) / beta;
       scale = 1.f / (alpha - beta);
     }
-    // v (rows > j) replaces column j; dots with the other columns:
-    // c > j: w_c = v^T P[:, c];  c < j: d_c = V_c^T v
-    float acc[NB];
+    float dot[NB];
 #pragma unroll
-    for (int c = 0; c < NB; ++c) acc[c] = 0.f;
+    for (int c = 0; c < NB; ++c) dot[c] = fmaf(scale, bc[c], rj[c]);
+    // v (rows > j) replaces column j; P[:, c] -= tau v w_c for c > j
 #pragma unroll
     for (int h = 0; h < RPT; ++h) {
       const int row = tid + 1024 * h;
@@ -122,32 +139,21 @@ __global__ __launch_bounds__(1024) void k_panel_qr(float* A, int64_t stride, int
         }
 #pragma unroll
         for (int c = 0; c < NB; ++c)
-          if (c != j) acc[c] = fmaf(v, P[h][c], acc[c]);
-      }
-    }
-    block_sum_f<NB>(acc, red, bc);
-#pragma unroll
-    for (int h = 0; h < RPT; ++h) {
-      const int row = tid + 1024 * h;
-      if (row >= j && row < m) {
-        const float v = row > j ? P[h][j] : 1.f;
-#pragma unroll
-        for (int c = 0; c < NB; ++c)
-          if (c > j) P[h][c] = fmaf(-tau * v, bc[c], P[h][c]);
+          if (c > j) P[h][c] = fmaf(-tau * v, dot[c], P[h][c]);
       }
     }
     if (tid == 0) {
-      // T[0:j, j] = T[0:j, 0:j] (-tau d[0:j]);  T[j][j] = tau
+      // T[0:j, j] = T[0:j, 0:j] (-tau d[0:j]);  T[j][j] = tau  (thread 0 only)
       for (int i = 0; i < j; ++i) {
         float s = 0.f;
-        for (int l = i; l < j; ++l) s = fmaf(Ts[i][l], bc[l], s);
+        for (int l = i; l < j; ++l) s = fmaf(Ts[i][l], dot[l], s);
         Ts[i][j] = -tau * s;
       }
       Ts[j][j] = tau;
       betas[j] = beta;
     }
-    __syncthreads();
   }
+  __syncthreads();
   // outputs
   float* Tm = Tout + (int64_t)blockIdx.x * NB * NB;
   if (tid < NB * NB) Tm[tid] = Ts[tid / NB][tid % NB];
