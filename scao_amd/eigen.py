@@ -18,7 +18,8 @@ kernels of csrc/eig.hip and plain batched GEMMs (rocBLAS, through torch):
 2. ``scao_eig_band_finish`` / ``scao_eig_sb2st``: band -> tridiagonal;
 3. ``scao_eig_bisect``: the kq largest eigenvalues and the clamped sum;
 4. ``scao_eig_vectors``: eigenvectors of the band matrix;
-5. back-transformation Z <- Q_0 (Q_1 (... Q_last Z)), two GEMMs per panel.
+5. back-transformation Z <- Q_0 (Q_1 (... Q_last Z)): the panels' reflectors
+   merged BT_GROUP at a time into block reflectors, three GEMMs per block.
 """
 
 from __future__ import annotations
@@ -157,11 +158,45 @@ def topk_eigh(X: Tensor, kq: int):
     L.call("scao_eig_vectors", orig.data_ptr(), n * (NB + 1), n, B, kq, w.data_ptr(),
            Z.data_ptr(), n * kq, work.data_ptr(), s)
     del work
-    # Z <- Q_0 (Q_1 (... Q_last Z)),  Q_p = I - V_p T_p V_p^T
-    for p in reversed(range(len(pcs))):
-        c0 = pcs[p]
-        r0 = c0 + NB
-        V = X[:, r0:, c0:c0 + NB]
-        Zs = Z[:, r0:, :]
-        Zs.sub_(torch.bmm(V, torch.bmm(Tall[p], torch.bmm(V.transpose(1, 2), Zs))))
+    _back_transform(X, pcs, Tall, Z)
     return w, Z, total
+
+
+BT_GROUP = 8   # panels merged into one block reflector by the back-transformation
+
+
+def _back_transform(X: Tensor, pcs: list, Tall: Tensor, Z: Tensor) -> None:
+    """Z <- Q_0 (Q_1 (... Q_last Z)), Q_p = I - V_p T_p V_p^T (the stage-1
+    reflectors), BT_GROUP panels at a time: the product of the block's
+    reflectors is one block reflector I - V T V^T with V = [V_a .. V_b] (the
+    block's panel columns of X from the first panel's row r0 down, each panel
+    zero above its own reflector rows) and T built column block by column
+    block, T[:, j] = -T[:j, :j] (V_{:j}^T V_j) T_j above the diagonal block
+    T_j (the larft recurrence for blocks).  So Z makes one pass per block
+    instead of one per panel; the update is in place.  X's panel columns above
+    each reflector (band values, already copied by band_finish) are zeroed."""
+    B = X.shape[0]
+    npan = len(pcs)
+    for b0 in reversed(range(0, npan, BT_GROUP)):
+        b1 = min(b0 + BT_GROUP, npan)
+        g = b1 - b0
+        c0 = pcs[b0]
+        r0 = c0 + NB
+        for i in range(1, g):
+            cp = pcs[b0 + i]
+            X[:, r0:cp + NB, cp:cp + NB].zero_()
+        Vb = X[:, r0:, c0:c0 + NB * g]
+        if g == 1:
+            Tb = Tall[b0]
+        else:
+            S = torch.bmm(Vb.transpose(1, 2), Vb)
+            Tb = torch.zeros(B, NB * g, NB * g, dtype=X.dtype, device=X.device)
+            for i in range(g):
+                Tb[:, NB * i:NB * (i + 1), NB * i:NB * (i + 1)] = Tall[b0 + i]
+            for j in range(1, g):
+                lo = NB * j
+                Tb[:, :lo, lo:lo + NB] = -torch.bmm(
+                    torch.bmm(Tb[:, :lo, :lo], S[:, :lo, lo:lo + NB]), Tall[b0 + j])
+        Zs = Z[:, r0:, :]
+        Y = torch.bmm(Tb, torch.bmm(Vb.transpose(1, 2), Zs))
+        Zs.baddbmm_(Vb, Y, alpha=-1.0)
