@@ -922,6 +922,7 @@ SYM_GRAM = True   # compute the lower Gram tiles only, each also writing its tra
 # bisection, inverse iteration: only the k_max vectors a factor can keep);
 # "torch" is the full torch.linalg.eigh (rocSOLVER syevd), kept for A/B runs.
 EIGEN_SOLVER = "hip"
+CONCURRENT_EIGEN = True   # the smaller dimensions' eigen batches on a second stream
 EIGEN_BATCH_BYTES = 8 << 30       # stacked eigen-stage inputs per launch (hip)
 # Optional callable run between a refresh's EMA update and its eigen stage,
 # with the list of (block, gradient, offset, row stride) being refreshed.  Used
@@ -996,6 +997,17 @@ def _refresh_diag(diag, dev, s):
         pre._touch()   # a diagonal sub-block's bias factor sits in the block table
 
 
+_SIDE_STREAMS: dict = {}
+
+
+def _side_stream(dev: torch.device) -> torch.cuda.Stream:
+    """A second stream on dev (default priority), made once per device."""
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = torch.cuda.Stream(device=dev)
+    return _SIDE_STREAMS[key]
+
+
 def _refresh_kron(kron, dev, s, eigen_only=False, ema_only=False):
     # 1) Gram -> EMA (-> requantise), chunked by staging memory
     todo = [] if eigen_only else list(kron)
@@ -1024,25 +1036,42 @@ def _refresh_kron(kron, dev, s, eigen_only=False, ema_only=False):
     eig_timer = _mark("refresh:eigh+rank")
     eig_timer.__enter__()
     hip = EIGEN_SOLVER == "hip"
-    for dim, lst in jobs.items():
-        budget = EIGEN_BATCH_BYTES if hip else EIGH_BATCH_BYTES
-        per = min(max(1, budget // (4 * dim * dim)), eigen.MAX_BATCH)
-        # vectors a factor can keep: k <= k_max (rank momentum and clamps)
-        kq = min(dim, max(leaf.k_max for leaf, _ in lst))
-        for b0 in range(0, len(lst), per):
-            part = lst[b0:b0 + per]
-            X = _eig_inputs(part, dim, dev, s)
-            if hip:
-                w, U_desc, total = eigen.topk_eigh(X, kq)
-                S_desc = w.clamp(min=0.0).float()
-            else:
-                w, V = _eigh_batched(X)
-                S_desc = w.flip(-1).clamp(min=0.0)
-                U_desc = V.flip(-1)
-                total = S_desc.sum(dim=1).double()
-            for (leaf, side), Sd, Ud, tot in zip(part, S_desc, U_desc, total):
-                spectra[(id(leaf), side)] = (Sd, Ud, tot)
-            del X
+    # With several dimensions, every batch but the largest runs on a second
+    # stream beside it (enqueued first, so it starts at once): a batch of a
+    # few small factors leaves most of the GPU idle, and its latency-bound
+    # kernels fit beside the large batch's.
+    main = torch.cuda.current_stream(dev)
+    order = sorted(jobs.items(), key=lambda kv: len(kv[1]) * kv[0] ** 2)
+    side = _side_stream(dev) if hip and CONCURRENT_EIGEN and len(order) > 1 else None
+    if side is not None:
+        side.wait_stream(main)   # the EMA codes
+    for bi, (dim, lst) in enumerate(order):
+        strm = side if side is not None and bi + 1 < len(order) else main
+        with torch.cuda.stream(strm):
+            s_b = L.stream_ptr(dev)
+            budget = EIGEN_BATCH_BYTES if hip else EIGH_BATCH_BYTES
+            per = min(max(1, budget // (4 * dim * dim)), eigen.MAX_BATCH)
+            # vectors a factor can keep: k <= k_max (rank momentum and clamps)
+            kq = min(dim, max(leaf.k_max for leaf, _ in lst))
+            for b0 in range(0, len(lst), per):
+                part = lst[b0:b0 + per]
+                X = _eig_inputs(part, dim, dev, s_b)
+                if hip:
+                    w, U_desc, total = eigen.topk_eigh(X, kq)
+                    S_desc = w.clamp(min=0.0).float()
+                else:
+                    w, V = _eigh_batched(X)
+                    S_desc = w.flip(-1).clamp(min=0.0)
+                    U_desc = V.flip(-1)
+                    total = S_desc.sum(dim=1).double()
+                if strm is not main:   # used on the current stream from here on
+                    for t in (S_desc, U_desc, total):
+                        t.record_stream(main)
+                for (leaf, side_), Sd, Ud, tot in zip(part, S_desc, U_desc, total):
+                    spectra[(id(leaf), side_)] = (Sd, Ud, tot)
+                del X
+    if side is not None:
+        main.wait_stream(side)
     # 3) adaptive rank for every (leaf, side) in one device pass + one read
     keys = [(leaf, side) for leaf, *_ in kron for side in (0, 1)]
     ranks = {}
