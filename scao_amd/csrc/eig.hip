@@ -1302,26 +1302,13 @@ __device__ __forceinline__ double block_sum_all(double x, double* red /* >= 5 */
   return r;
 }
 
-// Per matrix: Gram-Schmidt (twice) of each vector against the earlier ones of
-// its cluster -- consecutive eigenvalues whose gaps are all below tol * bnorm
-// -- in place in xall; matrices without clusters only copy the Rayleigh
-// quotients.
-__global__ __launch_bounds__(256) void k_cluster_orth(int n, int kq, double* w, const double* wr,
-                                                      const double* bnorm, double* xall) {
-  __shared__ double red[16];
-  const int mat = blockIdx.x;
-  double* wm = w + (int64_t)mat * kq;
-  double* xm = xall + (int64_t)mat * kq * n;
-  const double tol = kClusterTol * bnorm[mat];
-  bool any = false;
-  for (int i = 1; i < kq; ++i) any = any || fabs(wm[i - 1] - wm[i]) <= tol;
-  int cstart = 0;
-  for (int i = 0; any && i < kq; ++i) {
-    if (i == 0 || fabs(wm[i - 1] - wm[i]) > tol) cstart = i;
-    if (i == cstart) continue;
+// Gram-Schmidt (twice) of vectors [cs, ce) of xm against the earlier ones of
+// the cluster, in place.
+__device__ void cluster_mgs(double* xm, int n, int cs, int ce, double* red) {
+  for (int i = cs + 1; i < ce; ++i) {
     double* xi = xm + (int64_t)i * n;
     for (int pass = 0; pass < 2; ++pass) {
-      for (int jv = cstart; jv < i; ++jv) {
+      for (int jv = cs; jv < i; ++jv) {
         const double* xj = xm + (int64_t)jv * n;
         double x = 0.0;
         for (int r = threadIdx.x; r < n; r += 256) x = fma(xj[r], xi[r], x);
@@ -1336,6 +1323,119 @@ __global__ __launch_bounds__(256) void k_cluster_orth(int n, int kq, double* w, 
       for (int r = threadIdx.x; r < n; r += 256) xi[r] *= sc;
       __syncthreads();
     }
+  }
+}
+
+// One Cholesky-QR pass over the c <= CQ vectors [cs, cs+c) of xm: G = X^T X
+// (float64, through LDS in chunks of CR rows), G = R^T R, X <- X R^-1 (row by
+// row).  In exact arithmetic R is Gram-Schmidt's, so X becomes the same
+// orthonormal basis; two passes are as accurate as Gram-Schmidt twice while
+// X is far from rank-deficient.  Returns false, with X unchanged, when a pivot
+// falls below 1e-10 of its column's squared norm (X too close to
+// rank-deficient for the normal equations): the caller then uses cluster_mgs.
+constexpr int CQ = 64;   // largest cluster taken through Cholesky QR
+constexpr int CR = 32;   // rows per LDS chunk of the Gram pass
+struct CholQrLds {
+  double G[CQ][CQ + 1];
+  double chunk[CR][CQ + 1];
+  int fail;
+};
+
+__device__ bool cholqr_pass(double* xm, int n, int cs, int c, CholQrLds& S) {
+  const int tid = threadIdx.x;
+  // 1. G = X^T X: thread t accumulates cells t, t + 256, ... (a <= b only)
+  constexpr int NQ = CQ * CQ / 256;
+  double acc[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) acc[q] = 0.0;
+  for (int r0 = 0; r0 < n; r0 += CR) {
+    for (int idx = tid; idx < CR * c; idx += 256) {
+      const int v = idx / CR, r = idx % CR;
+      S.chunk[r][v] = r0 + r < n ? xm[(int64_t)(cs + v) * n + r0 + r] : 0.0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int cell = tid + 256 * q, a = cell / c, b = cell % c;
+      if (a <= b && a < c) {
+        double x = acc[q];
+        for (int r = 0; r < CR; ++r) x = fma(S.chunk[r][a], S.chunk[r][b], x);
+        acc[q] = x;
+      }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int cell = tid + 256 * q, a = cell / c, b = cell % c;
+    if (a <= b && a < c) S.G[a][b] = acc[q];
+  }
+  if (tid == 0) S.fail = 0;
+  __syncthreads();
+  // 2. G = R^T R (R into G's upper triangle), on wavefront 0: lane j owns
+  // column j
+  if (tid < 64) {
+    const int j = tid;
+    const double d0 = j < c ? S.G[j][j] : 1.0;
+    for (int k = 0; k < c; ++k) {
+      if (j == k) {
+        const double d = S.G[k][k];
+        if (!(d > 1e-10 * d0)) S.fail = 1;
+        S.G[k][k] = sqrt(fmax(d, 0.0));
+      }
+      wave_sync();
+      if (S.fail) break;
+      if (j > k && j < c) S.G[k][j] /= S.G[k][k];
+      wave_sync();
+      if (j > k && j < c)
+        for (int i = k + 1; i <= j; ++i) S.G[i][j] = fma(-S.G[k][i], S.G[k][j], S.G[i][j]);
+      wave_sync();
+    }
+  }
+  __syncthreads();
+  if (S.fail) return false;
+  // 3. X <- X R^-1: row r of X, forward substitution against R's columns
+  for (int r = tid; r < n; r += 256) {
+    double x[CQ];
+#pragma unroll
+    for (int v = 0; v < CQ; ++v) x[v] = v < c ? xm[(int64_t)(cs + v) * n + r] : 0.0;
+#pragma unroll
+    for (int j = 0; j < CQ; ++j) {
+      if (j < c) {
+        double sacc = x[j];
+#pragma unroll
+        for (int i = 0; i < j; ++i) sacc = fma(-x[i], S.G[i][j], sacc);
+        x[j] = sacc / S.G[j][j];
+        xm[(int64_t)(cs + j) * n + r] = x[j];
+      }
+    }
+  }
+  __syncthreads();
+  return true;
+}
+
+// Per matrix: the vectors of each cluster -- consecutive eigenvalues whose gaps
+// are all below tol * bnorm -- made orthonormal in place in xall (Cholesky QR
+// twice up to CQ vectors, with Gram-Schmidt as the fallback); matrices
+// without clusters only copy the Rayleigh quotients.
+__global__ __launch_bounds__(256) void k_cluster_orth(int n, int kq, double* w, const double* wr,
+                                                      const double* bnorm, double* xall) {
+  __shared__ double red[16];
+  __shared__ CholQrLds S;
+  const int mat = blockIdx.x;
+  double* wm = w + (int64_t)mat * kq;
+  double* xm = xall + (int64_t)mat * kq * n;
+  const double tol = kClusterTol * bnorm[mat];
+  for (int cs = 0; cs < kq;) {
+    int ce = cs + 1;
+    while (ce < kq && fabs(wm[ce - 1] - wm[ce]) <= tol) ++ce;
+    const int c = ce - cs;
+    if (c >= 2) {
+      bool ok = c <= CQ && cholqr_pass(xm, n, cs, c, S);
+      if (ok) ok = cholqr_pass(xm, n, cs, c, S);
+      if (!ok) cluster_mgs(xm, n, cs, ce, red);
+    }
+    cs = ce;
   }
   __syncthreads();
   // the Rayleigh quotients replace the bisection values once the clusters
