@@ -288,11 +288,23 @@ def refresh_summary(trace_csv: str, config: str, cmd: str) -> str:
         d[0] += 1
         d[1] += (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e6
     busy = sum(v[1] for v in agg.values())
+    # time with at least one kernel running (the eigen stage uses two streams)
+    union, cur_s, cur_e = 0, None, None
+    for r in win:
+        a, b = int(r["Start_Timestamp"]), int(r["End_Timestamp"])
+        if cur_e is None or a > cur_e:
+            union += 0 if cur_e is None else cur_e - cur_s
+            cur_s, cur_e = a, b
+        else:
+            cur_e = max(cur_e, b)
+    union += cur_e - cur_s
     out = [f"# Curvature refresh kernels (rocprofv3 kernel trace), {config}", "",
            "Commands (from the repository root on the box):", "", "```", cmd, "```", "",
            f"The last refresh of the run (a Phase-2 step): {len(win)} dispatches from its first "
            f"`k_gram_ema` to the `k_apply` of the update that uses it; first dispatch start to "
-           f"last dispatch end {(t1 - t0) / 1e6:.1f} ms, of which kernels run {busy:.1f} ms.", "",
+           f"last dispatch end {(t1 - t0) / 1e6:.1f} ms, with a kernel running for "
+           f"{union / 1e6:.1f} ms of it; the kernels' durations sum to {busy:.1f} ms (the eigen "
+           f"batches of different dimensions run on two streams at once).", "",
            "| kernel | dispatches | total ms | share |", "|---|---:|---:|---:|"]
     rest = [0, 0.0, 0]
     for name, (n, ms) in sorted(agg.items(), key=lambda kv: -kv[1][1]):

@@ -80,7 +80,8 @@ def test_stages_keep_the_spectrum(n):
 
 CASES = [(1, 1, "wishart"), (5, 2, "indefinite"), (16, 4, "wishart"), (17, 8, "lowrank"),
          (40, 10, "planted"), (100, 20, "indefinite"), (257, 32, "wishart"),
-         (300, 20, "ties"), (512, 64, "lowrank"), (768, 32, "wishart"),
+         (300, 20, "ties"), (300, 80, "ties"), (512, 64, "ties"), (512, 64, "lowrank"),
+         (768, 32, "wishart"),
          (1024, 128, "planted"), (2048, 64, "planted")]
 
 
