@@ -1111,6 +1111,131 @@ __device__ __forceinline__ double enter_rhs(const double* rhs, uint32_t vid, int
   return i < n ? (rhs ? rhs[i] : start_val(vid, i)) : 0.0;
 }
 
+// The band solve keeps its global stores out of the prefetch window: a wait
+// for loads with stores in flight is a wait for every outstanding operation,
+// which would expose each prefetched value's latency at every step.  The U
+// rows (and the transformed right-hand side) of UF steps are staged in LDS and
+// written out together, the back substitution's solution values likewise;
+// and every prefetch is issued unconditionally (an out-of-range one reads a
+// valid address; validity and the shift are applied where the value is
+// used), since a load issued on one branch only also makes the compiler wait
+// for all loads.
+constexpr int UF = 8;                 // steps staged between flushes (a multiple of PF)
+constexpr int UST = UF * (WC + 1);    // staged doubles per wavefront
+static_assert(UF % PF == 0, "flushes at prefetch group boundaries");
+typedef __attribute__((address_space(3))) double lds_double;
+
+// A band value about to enter the window: the raw float and its position
+// (entering row i, column c), or the right-hand side's (lane WC).
+struct Enter {
+  float raw;      // orig value (matrix lanes)
+  double rv;      // right-hand side value (lane WC)
+  bool ok, dg;    // inside the band and the matrix; on the diagonal
+};
+
+template <bool HAS_RHS>
+__device__ __forceinline__ Enter enter_load(const float* orig, const double* rhs, uint32_t vid,
+                                            int n, int j, int L) {
+  // every lane issues the same loads (clamped addresses), no branches
+  Enter e;
+  const int i = j + WR;
+  const int lj = j % WC;
+  const int c = j + 1 + ((L - (lj + 1)) % WC + WC) % WC;
+  const int dd = i - c;
+  const bool inb = i < n;
+  const bool band = L < WC && inb && c < n && dd <= NB && dd >= -NB;
+  e.dg = dd == 0;
+  e.ok = L < WC ? band : (L == WC && inb);
+  e.raw = orig[band ? (dd >= 0 ? i * OW + dd : c * OW - dd) : 0];
+  if constexpr (HAS_RHS)
+    e.rv = rhs[inb ? i : 0];
+  else
+    e.rv = start_val(vid, i);
+  return e;
+}
+
+__device__ __forceinline__ double enter_value(const Enter& e, int L, double sigma) {
+  if (!e.ok) return 0.0;
+  if (L == WC) return e.rv;
+  double v = (double)e.raw;
+  if (e.dg) v -= sigma;
+  return v;
+}
+
+// Run LEAF(s) for the slot s == p (uniform) of the window: a binary tree of
+// scalar branches, about log2(WR) compares instead of one per slot.  It is a
+// macro so that every leaf names its slot with a constant inside the solve
+// itself (the window stays in registers; a helper taking the window by
+// reference lets the compiler merge the leaves into one indexed access,
+// which moves the window to scratch memory).
+static_assert(WR == 17, "the slot tree is written for 17 window rows");
+#define SLOT_TREE(p, LEAF) \
+  if (p <= 8) {          \
+    if (p <= 4) {        \
+      if (p <= 2) {      \
+        if (p <= 1) {    \
+          if (p <= 0) {  \
+            LEAF(0)      \
+          } else {       \
+            LEAF(1)      \
+          }              \
+        } else {         \
+          LEAF(2)        \
+        }                \
+      } else {           \
+        if (p <= 3) {    \
+          LEAF(3)        \
+        } else {         \
+          LEAF(4)        \
+        }                \
+      }                  \
+    } else {             \
+      if (p <= 6) {      \
+        if (p <= 5) {    \
+          LEAF(5)        \
+        } else {         \
+          LEAF(6)        \
+        }                \
+      } else {           \
+        if (p <= 7) {    \
+          LEAF(7)        \
+        } else {         \
+          LEAF(8)        \
+        }                \
+      }                  \
+    }                    \
+  } else {               \
+    if (p <= 12) {       \
+      if (p <= 10) {     \
+        if (p <= 9) {    \
+          LEAF(9)        \
+        } else {         \
+          LEAF(10)       \
+        }                \
+      } else {           \
+        if (p <= 11) {   \
+          LEAF(11)       \
+        } else {         \
+          LEAF(12)       \
+        }                \
+      }                  \
+    } else {             \
+      if (p <= 14) {     \
+        if (p <= 13) {   \
+          LEAF(13)       \
+        } else {         \
+          LEAF(14)       \
+        }                \
+      } else {           \
+        if (p <= 15) {   \
+          LEAF(15)       \
+        } else {         \
+          LEAF(16)       \
+        }                \
+      }                  \
+    }                    \
+  }
+
 // Solve (B - sigma I) x = rhs with band LU and partial pivoting; rhs given by
 // `rhs` (NULL: start_val).  U rows (WC doubles each) and the transformed rhs
 // go to work; x (float64, normalised) to xout.  One wavefront; lanes 0..32
@@ -1120,10 +1245,11 @@ __device__ __forceinline__ double enter_rhs(const double* rhs, uint32_t vid, int
 // The window's rows are an unordered set: the pivot row is retired as U row
 // j and the entering band row takes its slot, so no rows move.  Returns the
 // norm of the solution before normalisation.
+template <bool HAS_RHS>
 __device__ __forceinline__ double band_solve(const float* __restrict__ orig, int n, double sigma,
                                              double bnorm, uint32_t vid,
                                              const double* __restrict__ rhs, double* U,
-                                             double* ys, double* xout) {
+                                             double* ys, double* xout, lds_double* st) {
   const int L = threadIdx.x & 63;
   const bool act = L < WC;          // a matrix column
   const bool rl = L == WC;          // the right-hand side
@@ -1132,12 +1258,11 @@ __device__ __forceinline__ double band_solve(const float* __restrict__ orig, int
 #pragma unroll
   for (int s = 0; s < WR; ++s)
     W[s] = act ? mval(orig, n, s, L, sigma) : (rl ? enter_rhs(rhs, vid, n, s) : 0.0);
-  double qW[PF];
+  Enter qW[PF];
 #pragma unroll
-  for (int t = 0; t < PF; ++t)
-    qW[t] = act ? enter_val(orig, n, t, L, true, sigma)
-                : (rl ? enter_rhs(rhs, vid, n, t + WR) : 0.0);
+  for (int t = 0; t < PF; ++t) qW[t] = enter_load<HAS_RHS>(orig, rhs, vid, n, t, L);
   const double tiny = 2.220446049250313e-16 * bnorm + 1e-300;
+  int jf = 0;                        // first U row not yet written out
   for (int j0 = 0; j0 < n; j0 += PF) {
 #pragma unroll
     for (int t = 0; t < PF; ++t) {
@@ -1145,27 +1270,25 @@ __device__ __forceinline__ double band_solve(const float* __restrict__ orig, int
       if (j >= n) break;
       const int lj = j % WC;
       double col[WR];
-#pragma unroll
-      for (int s = 0; s < WR; ++s) col[s] = readlane_d(W[s], lj);
+      // pivot search on the scalar unit: the high word without its sign
+      // orders |col[s]| to 20 mantissa bits (a tie keeps the lowest slot; any
+      // pivot within 2^-20 of the largest is as stable)
       int p = 0;
-      double best = fabs(col[0]);
+      uint32_t best = 0;
 #pragma unroll
-      for (int s = 1; s < WR; ++s)
-        if (fabs(col[s]) > best) {
-          best = fabs(col[s]);
+      for (int s = 0; s < WR; ++s) {
+        col[s] = readlane_d(W[s], lj);
+        const uint32_t m =
+            (uint32_t)(__builtin_bit_cast(uint64_t, col[s]) >> 32) & 0x7fffffffu;
+        if (s == 0 || m > best) {
+          best = m;
           p = s;
         }
-      p = __builtin_amdgcn_readfirstlane(p);
-      // p is uniform: scalar branches pick the pivot row (the empty asm keeps
-      // them branches instead of 17 per-lane selects)
-      double piv = col[0], prow = W[0];
-#pragma unroll
-      for (int s = 1; s < WR; ++s)
-        if (p == s) {
-          asm volatile("" ::: "memory");
-          piv = col[s];
-          prow = W[s];
-        }
+      }
+      double piv = 0.0, prow = 0.0;
+#define PICK(s_) { asm volatile("" ::: "memory"); piv = col[s_]; prow = W[s_]; }
+      SLOT_TREE(p, PICK)
+#undef PICK
       if (fabs(piv) < tiny) piv = piv < 0.0 ? -tiny : tiny;
       // every slot loses col[s] / piv times the pivot row, as col[s] * (row / piv)
       // (the pivot's own slot is overwritten below)
@@ -1173,55 +1296,73 @@ __device__ __forceinline__ double band_solve(const float* __restrict__ orig, int
 #pragma unroll
       for (int s = 0; s < WR; ++s) W[s] = fma(-col[s], q, W[s]);
       // retire the pivot row as U row j (column offset of this lane) and its
-      // right-hand side
+      // right-hand side, staged
       const int off = (L - lj + WC) % WC;
-      if (act) U[(int64_t)j * WC + off] = L == lj ? piv : prow;
-      if (rl) ys[j] = prow;
+      if (act) st[(j % UF) * (WC + 1) + off] = L == lj ? piv : prow;
+      if (rl) st[(j % UF) * (WC + 1) + WC] = prow;
       // row j + 17 (prefetched PF steps ago) takes the pivot's slot; fetch
       // step j + PF's
-      const double ent = qW[t];
-#pragma unroll
-      for (int s = 0; s < WR; ++s)
-        if (p == s) {
-          asm volatile("" ::: "memory");
-          W[s] = ent;
-        }
-      qW[t] = act ? enter_val(orig, n, j + PF, L, true, sigma)
-                  : (rl ? enter_rhs(rhs, vid, n, j + PF + WR) : 0.0);
+      const double ent = enter_value(qW[t], L, sigma);
+#define PUT(s_) { asm volatile("" ::: "memory"); W[s_] = ent; }
+      SLOT_TREE(p, PUT)
+#undef PUT
+      qW[t] = enter_load<HAS_RHS>(orig, rhs, vid, n, j + PF, L);
+    }
+    const int je = j0 + PF < n ? j0 + PF : n;
+    if (je - jf >= UF || je == n) {
+      // U rows jf .. je-1 (contiguous in U) and their right-hand sides
+      wave_sync();
+      for (int e = L; e < (je - jf) * WC; e += 64) {
+        const int r = e / WC, off = e % WC;
+        U[(int64_t)(jf + r) * WC + off] = st[r * (WC + 1) + off];
+      }
+      if (L < je - jf) ys[jf + L] = st[L * (WC + 1) + WC];
+      jf = je;
     }
   }
   __threadfence_block();
   // back substitution: x[j] = (ys[j] - sum_{c>=1} U[j][c] x[j+c]) / U[j][0];
   // lane L keeps x[row] for the row = L (mod 33) inside the window.  Row j's
   // U entries, diagonal and rhs are loaded PF steps ahead (they do not depend
-  // on x).
+  // on x); the solution values are staged UF at a time.
   double qU[PF], qD[PF], qS[PF];
+  bool qok[PF];
 #pragma unroll
   for (int t = 0; t < PF; ++t) {
     const int j = n - 1 - t;
     const int off = j >= 0 ? (L - j % WC + WC) % WC : 0;
-    qU[t] = (j >= 0 && act && off != 0 && j + off < n) ? U[(int64_t)j * WC + off] : 0.0;
-    qD[t] = j >= 0 ? U[(int64_t)j * WC] : 1.0;
-    qS[t] = j >= 0 ? ys[j] : 0.0;
+    qok[t] = j >= 0 && act && off != 0 && j + off < n;
+    qU[t] = U[qok[t] ? (int64_t)j * WC + off : 0];
+    qD[t] = U[j >= 0 ? (int64_t)j * WC : 0];
+    qS[t] = ys[j >= 0 ? j : 0];
   }
   double xv = 0.0, nrm = 0.0;
+  int jx = n;                        // xout rows jx .. n-1 are written out
   for (int j0 = n - 1; j0 >= 0; j0 -= PF) {
 #pragma unroll
     for (int t = 0; t < PF; ++t) {
       const int j = j0 - t;
       if (j < 0) break;
-      const double sm = wave_sum_d(qU[t] * xv);
+      const double sm = wave_sum_d((qok[t] ? qU[t] : 0.0) * xv);
       const double xj = (qS[t] - sm) / qD[t];
       if (L == j % WC) {
         xv = xj;
         nrm = fma(xj, xj, nrm);
-        xout[j] = xj;
+        st[(n - 1 - j) % UF] = xj;
       }
       const int jn = j - PF;
       const int off = jn >= 0 ? (L - jn % WC + WC) % WC : 0;
-      qU[t] = (jn >= 0 && act && off != 0 && jn + off < n) ? U[(int64_t)jn * WC + off] : 0.0;
-      qD[t] = jn >= 0 ? U[(int64_t)jn * WC] : 1.0;
-      qS[t] = jn >= 0 ? ys[jn] : 0.0;
+      qok[t] = jn >= 0 && act && off != 0 && jn + off < n;
+      qU[t] = U[qok[t] ? (int64_t)jn * WC + off : 0];
+      qD[t] = U[jn >= 0 ? (int64_t)jn * WC : 0];   // rows below 0 are never used
+      qS[t] = ys[jn >= 0 ? jn : 0];
+    }
+    const int jl = j0 - PF + 1 > 0 ? j0 - PF + 1 : 0;   // lowest row of the group
+    if (jx - jl >= UF || jl == 0) {
+      // rows jl .. jx-1: row j sits in slot (n - 1 - j) mod UF
+      wave_sync();
+      if (L < jx - jl) xout[jx - 1 - L] = st[(n - jx + L) % UF];
+      jx = jl;
     }
   }
   nrm = wave_sum_d(nrm);
@@ -1265,6 +1406,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 5))) voi
                                                  int nvec, int v0, const double* w,
                                                  const double* bnorm, double* work, double* xall,
                                                  double* wr) {
+  __shared__ double stage[4][UST];   // each wavefront's staged U rows / solution
   const int wv = threadIdx.x >> 6;
   const int vid = v0 + blockIdx.x * 4 + wv;
   if (vid >= nvec) return;
@@ -1284,9 +1426,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 5))) voi
   // the start vector has entries uniform in [-1, 1]: norm about sqrt(n / 3);
   // a solution that grew by less than 1e10 / |B| relative to it had a shift
   // too far from the eigenvalue to have converged: solve once more from it
-  const double growth = band_solve(om, n, sigma, bn, (uint32_t)vid, nullptr, U, ys, x);
+  lds_double* st = (lds_double*)&stage[wv][0];
+  const double growth = band_solve<false>(om, n, sigma, bn, (uint32_t)vid, nullptr, U, ys, x, st);
   if (growth * bn < 1e10 * sqrt(n / 3.0))
-    band_solve(om, n, sigma, bn, (uint32_t)vid, x, U, ys, x);
+    band_solve<true>(om, n, sigma, bn, (uint32_t)vid, x, U, ys, x, st);
   const double rq = rayleigh(om, n, x);
   if ((threadIdx.x & 63) == 0) wr[vid] = rq;
 }
