@@ -190,11 +190,14 @@ int scao_int8_ema_update(int8_t* q, double scale_in, const float* new_val, doubl
 /* ---- batched step: Phase 2 (preconditioned Adan) ---------------------- */
 /* A1  T = U_l^T G for (leaf, 256-column strip, 64-row chunk of T); also
  *     ||g||^2 (chunk 0) and ||p*decay||^2 (chunk 0 of LARS params) into slots.
- *     variant = (fast ? 1 : 0) | (p norm ? 2 : 0) | (tall ? 4 : 0): "fast"
- *     tasks promise fp32 data, SCAO_LF_VEC4, a full 256-column strip, a full
- *     64-row chunk of T and m % 32 == 0; "p norm" tasks are the chunk-0 tasks
- *     of LARS params; "tall" tasks (fast only) cover 128 rows of T from
- *     b = c0, a multiple of 128, with c0 + 128 <= k. */
+ *     variant = (fast ? 1 : 0) | (p norm ? 2 : 0) | (tall ? 4 : 0)
+ *     | (wide ? 8 : 0): "fast" tasks promise fp32 data, SCAO_LF_VEC4, a full
+ *     256-column strip, a full 64-row chunk of T and m % 32 == 0, and run on
+ *     the bf16 matrix cores with fp32 products (three-way bf16 splits); "p
+ *     norm" tasks are the chunk-0 tasks of LARS params; "tall" tasks (fast
+ *     only) cover 128 rows of T from b = c0, a multiple of 128, with
+ *     c0 + 128 <= k; "wide" tasks (fast only, not tall) cover 256 rows of T
+ *     from b = c0, a multiple of 256, with c0 + 256 <= k. */
 int scao_kron_project(const scao_task* tasks, int ntasks, const scao_leaf_desc* leaves,
                       const scao_param_desc* params, double* slots, int variant, void* stream);
 /* A2  P = T U_r, Delta = (s_l s_r^T - 1) P and nu^2 partial per 64x64 tile of P. */

@@ -38,6 +38,10 @@ namespace {
 // ||p*decay||^2 from the staged registers (every element of the strip passes
 // through exactly one thread).
 constexpr int PR = 32;           // rows per chunk
+// Whole fp32 tiles (the FAST variants) on the bf16 matrix cores
+// (project_tile_x6) with 256 threads for 64 rows of T and 512 for 128 or 256.
+constexpr bool PROJECT_X6 = true;
+constexpr int X6_NT128 = 512;
 constexpr int GP = SCAO_PROJ_COLS + 4;  // LDS pitch of the G chunk
 
 template <bool FAST, bool DO_P, int CR = 64>
@@ -185,6 +189,165 @@ __device__ __forceinline__ void project_tile(const scao_leaf_desc& L, const scao
   if (do_norms) {
     double x[2] = {g2, p2};
     block_sum<2>(x, red);
+    if (threadIdx.x == 0) {
+      slots[(int64_t)slot * SCAO_SLOT_WIDTH + 0] = x[0];
+      slots[(int64_t)slot * SCAO_SLOT_WIDTH + 1] = x[1];
+      slots[(int64_t)slot * SCAO_SLOT_WIDTH + 2] = 0.0;
+    }
+  }
+}
+
+// The same tile for whole fp32 tiles (FAST) on the bf16 matrix cores, with
+// fp32 products through three-way splits (mfma_x6): one v_mfma_f32_16x16x32
+// covers a whole 32-row chunk, so a chunk costs 6 * 16 cycles per output
+// tile against 8 * 32 for the fp32 16x16x4 form.  NT threads (NT / 64
+// waves) share the CR x 256 tile; wave w owns CW = 256 / (NT / 64) columns
+// (NJ = CW / 16 output tiles across) and all CR rows of T.
+//   * G does not pass through LDS: lane (jj, g) of wave w loads rows
+//     8g..8g+7 of the chunk at the NJ columns j0 + CW*w + NJ*jj + t, which is
+//     exactly its B operand of the NJ output tiles t (the column permutation
+//     of the fp32 form), and splits it in registers.
+//   * U_l (shared by the waves) is split by its loader and stored as three
+//     bf16 planes, column-major inside the chunk (column pitch 80 B: the 16
+//     lanes of one A-operand read hit 16 disjoint bank quads).
+// The next chunk's G, p and U_l are loaded while the current one's MFMAs run.
+template <bool DO_P, int CR, int NT>
+__device__ __forceinline__ void project_tile_x6(const scao_leaf_desc& L, const scao_param_desc& P,
+                                                int j0, int c0, int slot, double* slots) {
+  static_assert(CR == 64 || CR == 128 || CR == 256, "CR");
+  static_assert(NT == 256 || NT == 512, "NT");
+  constexpr int NQ = CR / 16;        // MFMA tiles down T
+  constexpr int CW = 256 / (NT / 64);
+  constexpr int NJ = CW / 16;        // MFMA tiles across, G columns per lane
+  constexpr int UCP = 40;            // bf16 per U_l column in LDS (32 rows + pad)
+  constexpr int UG = NT / 8;         // U_l loader threads per 4-row group
+  constexpr int UW = CR / UG;        // U_l columns per loader thread
+  static_assert(UW == 2 || UW == 4, "U_l loader width");
+  typedef float vj __attribute__((ext_vector_type(NJ)));
+  typedef __attribute__((address_space(1))) vj gvj;
+  __shared__ __attribute__((aligned(16))) __bf16 Us[3][CR][UCP];
+  __shared__ double red[2 * NT / 64];
+  const int tid = threadIdx.x;
+  const int w = tid / 64, l = tid % 64;
+  const int jj = l % 16, g = l / 16;
+  const int m = L.m, n = L.n, k = L.k;
+  const int64_t ld = L.ld;
+  const bool do_norms = (c0 == 0) && slot >= 0;
+  const bool decay = P.flags & SCAO_PF_DECAY;
+  const int gcol = j0 + CW * w + NJ * jj;
+  // U_l loader: rows 4*ua .. 4*ua+3 of the chunk, columns ub*UW .. +UW-1
+  const int ua = tid / UG, ub = tid % UG;
+
+  v4f acc[NQ][NJ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q)
+#pragma unroll
+    for (int t = 0; t < NJ; ++t) acc[q][t] = v4f{0.f, 0.f, 0.f, 0.f};
+  double g2 = 0.0, p2 = 0.0;
+
+  vj rg[8], rp[8];
+  float ru[4][UW];
+  auto load_chunk = [&](int i0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t o = L.off + (int64_t)(i0 + 8 * g + e) * ld + gcol;
+      rg[e] = __builtin_nontemporal_load((const gvj*)((const float*)P.graw + o));
+      if (DO_P) rp[e] = __builtin_nontemporal_load((const gvj*)((const float*)P.p + o));
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float* src = L.Ul + (int64_t)(i0 + 4 * ua + r) * k + c0 + ub * UW;
+      if constexpr (UW == 4) {
+        const v4f x = gld4(src);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ru[r][c] = x[c];
+      } else {
+        const v2u x = *(const gv2u*)src;
+        ru[r][0] = __uint_as_float(x[0]);
+        ru[r][1] = __uint_as_float(x[1]);
+      }
+    }
+  };
+
+  load_chunk(0);
+  for (int i0 = 0; i0 < m; i0 += PR) {
+    // this chunk's G operands, split in registers
+    bf3 bg[NJ];
+#pragma unroll
+    for (int t = 0; t < NJ; ++t) {
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = rg[e][t];
+      bg[t] = split_bf3(x);
+    }
+    if (do_norms) {
+      float a = 0.f, b = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int t = 0; t < NJ; ++t) {
+          a = fmaf(rg[e][t], rg[e][t], a);
+          if (DO_P) {
+            const float x = decay ? rp[e][t] * P.decay : rp[e][t];
+            b = fmaf(x, x, b);
+          }
+        }
+      g2 += (double)a;
+      p2 += (double)b;
+    }
+    if (i0) __syncthreads();              // the previous chunk's U_l planes are consumed
+#pragma unroll
+    for (int c = 0; c < UW; ++c) {
+      // four rows of one column: one 8-byte write per plane
+      v2u pl[3];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        uint32_t lo[3], hi[3];
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          const float x = ru[2 * h + rr][c];
+          const __bf16 b0 = (__bf16)x;
+          const float r = x - (float)b0;
+          const __bf16 b1 = (__bf16)r;
+          const __bf16 b2 = (__bf16)(r - (float)b1);
+          const uint32_t v[3] = {__builtin_bit_cast(uint16_t, b0), __builtin_bit_cast(uint16_t, b1),
+                                 __builtin_bit_cast(uint16_t, b2)};
+#pragma unroll
+          for (int pp = 0; pp < 3; ++pp) (rr ? hi : lo)[pp] = v[pp];
+        }
+#pragma unroll
+        for (int pp = 0; pp < 3; ++pp) pl[pp][h] = lo[pp] | (hi[pp] << 16);
+      }
+      const int col = ub * UW + c;
+#pragma unroll
+      for (int pp = 0; pp < 3; ++pp) *(v2u*)&Us[pp][col][4 * ua] = pl[pp];
+    }
+    __syncthreads();
+    if (i0 + PR < m) load_chunk(i0 + PR); // in flight during the MFMAs below
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      bf3 au;
+      au.h = *(const v8bf*)&Us[0][16 * q + jj][8 * g];
+      au.m = *(const v8bf*)&Us[1][16 * q + jj][8 * g];
+      au.l = *(const v8bf*)&Us[2][16 * q + jj][8 * g];
+#pragma unroll
+      for (int t = 0; t < NJ; ++t) acc[q][t] = mfma_x6(au, bg[t], acc[q][t]);
+    }
+  }
+  // T[c][j] for c = c0 + 16q + 4g + r, j = gcol + t
+#pragma unroll
+  for (int q = 0; q < NQ; ++q)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int c = c0 + 16 * q + 4 * g + r;
+      vj o;
+#pragma unroll
+      for (int t = 0; t < NJ; ++t) o[t] = acc[q][t][r];
+      *(gvj*)(L.T + (int64_t)c * n + gcol) = o;
+    }
+  if (do_norms) {
+    double x[2] = {g2, p2};
+    block_sum_n<2, NT>(x, red);
     if (threadIdx.x == 0) {
       slots[(int64_t)slot * SCAO_SLOT_WIDTH + 0] = x[0];
       slots[(int64_t)slot * SCAO_SLOT_WIDTH + 1] = x[1];
@@ -1101,6 +1264,15 @@ __global__ __launch_bounds__(256) void k_project(const scao_task* __restrict__ t
   const scao_leaf_desc L = leaves[tk.idx];
   project_tile<FAST, DO_P, CR>(L, params[L.param], tk.a, tk.b, tk.slot, slots);
 }
+template <bool DO_P, int CR, int NT>
+__global__ __launch_bounds__(NT) void k_project_x6(const scao_task* __restrict__ tasks,
+                                                   const scao_leaf_desc* __restrict__ leaves,
+                                                   const scao_param_desc* __restrict__ params,
+                                                   double* slots) {
+  const scao_task tk = tasks[blockIdx.x];
+  const scao_leaf_desc L = leaves[tk.idx];
+  project_tile_x6<DO_P, CR, NT>(L, params[L.param], tk.a, tk.b, tk.slot, slots);
+}
 __global__ __launch_bounds__(256) void k_delta(const scao_task* __restrict__ tasks,
                                                const scao_leaf_desc* __restrict__ leaves,
                                                const scao_param_desc* __restrict__ params,
@@ -1174,10 +1346,25 @@ extern "C" int scao_kron_project(const scao_task* tasks, int ntasks, const scao_
   SCAO_CHECK_ARG(ntasks >= 0, "scao_kron_project: ntasks < 0");
   if (ntasks == 0) return SCAO_OK;
   SCAO_CHECK_ARG(tasks && leaves && params && slots, "scao_kron_project: null pointer");
-  SCAO_CHECK_ARG(variant >= 0 && variant < 8 && (variant < 4 || (variant & 1)),
+  SCAO_CHECK_ARG(variant >= 0 && variant < 12 && (variant < 4 || (variant & 1)) &&
+                     (variant & 12) != 12,
                  "scao_kron_project: bad variant %d", variant);
   hipStream_t s = (hipStream_t)stream;
   dim3 g(ntasks), b(256);
+  if (PROJECT_X6 && (variant & 1)) {
+    const dim3 b512(512), b128(X6_NT128);
+    switch (variant) {
+      case 1: hipLaunchKernelGGL((k_project_x6<false, 64, 256>), g, b, 0, s, tasks, leaves, params, slots); break;
+      case 3: hipLaunchKernelGGL((k_project_x6<true, 64, 256>), g, b, 0, s, tasks, leaves, params, slots); break;
+      case 5: hipLaunchKernelGGL((k_project_x6<false, 128, X6_NT128>), g, b128, 0, s, tasks, leaves, params, slots); break;
+      case 7: hipLaunchKernelGGL((k_project_x6<true, 128, X6_NT128>), g, b128, 0, s, tasks, leaves, params, slots); break;
+      case 9: hipLaunchKernelGGL((k_project_x6<false, 256, 512>), g, b512, 0, s, tasks, leaves, params, slots); break;
+      default: hipLaunchKernelGGL((k_project_x6<true, 256, 512>), g, b512, 0, s, tasks, leaves, params, slots); break;
+    }
+    SCAO_LAUNCH_CHECK("scao_kron_project");
+    return SCAO_OK;
+  }
+  SCAO_CHECK_ARG(variant < 8, "scao_kron_project: variant %d needs the bf16 projection", variant);
   switch (variant) {
     case 0: hipLaunchKernelGGL((k_project<false, false>), g, b, 0, s, tasks, leaves, params, slots); break;
     case 1: hipLaunchKernelGGL((k_project<true, false>), g, b, 0, s, tasks, leaves, params, slots); break;

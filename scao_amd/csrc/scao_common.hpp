@@ -23,6 +23,48 @@ __device__ __forceinline__ v4f mfma16(float a, float b, v4f c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// v_mfma_f32_16x16x32_bf16.  Lane l supplies A[l%16][8*(l/16)+e] and
+// B[8*(l/16)+e][l%16] in element e; the accumulator layout is mfma16's
+// (checked on gfx950).  Products of two bf16 are exact in fp32.
+typedef __bf16 v8bf __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ v4f mfma16bf(v8bf a, v8bf b, v4f c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// fp32 products on the bf16 matrix cores: x = h + m + l exactly for every
+// finite x above ~1e-33 in magnitude (h rounds x to 8 significant bits, m the
+// remainder, and the second remainder has at most 8 bits left, so l holds it
+// exactly; both subtractions are exact).  A product x*y is then the sum of
+// nine exact bf16 products; the six kept by mfma_x6 drop m*l, l*m and l*l,
+// at most about 2^-23 |x y| together, the size of fp32's own rounding of
+// the product.
+struct bf3 {
+  v8bf h, m, l;
+};
+__device__ __forceinline__ bf3 split_bf3(const float (&x)[8]) {
+  bf3 s;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const __bf16 h = (__bf16)x[e];
+    const float r = x[e] - (float)h;
+    const __bf16 m = (__bf16)r;
+    s.h[e] = h;
+    s.m[e] = m;
+    s.l[e] = (__bf16)(r - (float)m);
+  }
+  return s;
+}
+// c + A B for fp32 A and B given as bf3 splits: six bf16 MFMAs (small terms
+// first).
+__device__ __forceinline__ v4f mfma_x6(const bf3& a, const bf3& b, v4f c) {
+  c = mfma16bf(a.m, b.m, c);
+  c = mfma16bf(a.h, b.l, c);
+  c = mfma16bf(a.l, b.h, c);
+  c = mfma16bf(a.h, b.m, c);
+  c = mfma16bf(a.m, b.h, c);
+  return mfma16bf(a.h, b.h, c);
+}
+
 // ------------------------------------------------------------- dtypes ---
 __device__ __forceinline__ float bf16_to_f(uint16_t h) {
   return __uint_as_float(((uint32_t)h) << 16);
@@ -261,6 +303,24 @@ __device__ __forceinline__ void block_sum(double (&x)[NQ], double* lds /* >= 4*N
   __syncthreads();
   if (threadIdx.x == 0)
     for (int q = 0; q < NQ; ++q) x[q] = ((lds[q] + lds[NQ + q]) + lds[2 * NQ + q]) + lds[3 * NQ + q];
+}
+// The same over an NT-thread block (waves added in order); lds >= NQ*NT/64.
+template <int NQ, int NT>
+__device__ __forceinline__ void block_sum_n(double (&x)[NQ], double* lds) {
+  constexpr int NW = NT / SCAO_WAVE;
+  const int w = threadIdx.x / SCAO_WAVE, l = threadIdx.x % SCAO_WAVE;
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) x[q] = wave_sum(x[q]);
+  __syncthreads();
+  if (l == 0)
+    for (int q = 0; q < NQ; ++q) lds[w * NQ + q] = x[q];
+  __syncthreads();
+  if (threadIdx.x == 0)
+    for (int q = 0; q < NQ; ++q) {
+      double s = lds[q];
+      for (int v = 1; v < NW; ++v) s += lds[v * NQ + q];
+      x[q] = s;
+    }
 }
 __device__ __forceinline__ float block_max(float x, float* lds) {
   const int w = threadIdx.x / SCAO_WAVE, l = threadIdx.x % SCAO_WAVE;

@@ -201,7 +201,7 @@ def _flat_chunks(numel: int) -> int:
 
 _LEAF_TASKS = ("delta", "lift")   # with proj* and apply*: idx is a block index
 _TASK_TYPES = (["adam", "delta", "lift", "dred", "dapply", "lars"] +
-               [f"proj{v}" for v in range(8)] + [f"apply{v}" for v in range(16)])
+               [f"proj{v}" for v in range(12)] + [f"apply{v}" for v in range(16)])
 
 
 def _leaf_k(leaf) -> int:
@@ -245,12 +245,15 @@ def _param_tasks(it: PItem):
             vec = _leaf_vec(it, leaf, r0, c0l)
             for j0 in range(0, n, L.PROJ_COLS):
                 whole = vec and it.fp32 and j0 + L.PROJ_COLS <= n and m % 32 == 0
-                # 128 rows of T per task where k allows (variant bit 4)
-                cr = 128 if TALL_PROJECT and whole and k % 128 == 0 else 64
+                # 128 or 256 rows of T per task where k allows (variant bits 4, 8)
+                cr = 64
+                if TALL_PROJECT and whole and k % 128 == 0:
+                    cr = 256 if WIDE_PROJECT and k % 256 == 0 else 128
                 for c0 in range(0, k, cr):
                     fast = whole and c0 + 64 <= k
                     do_p = c0 == 0 and it.lars
-                    var = (1 if fast else 0) | (2 if do_p else 0) | (4 if cr == 128 else 0)
+                    var = ((1 if fast else 0) | (2 if do_p else 0) | (4 if cr == 128 else 0)
+                           | (8 if cr == 256 else 0))
                     if c0 == 0:
                         add(f"proj{var}", (li, j0, c0, slot))
                         slot += 1
@@ -322,7 +325,7 @@ def _build_structure(items: list[PItem], cache: dict | None = None):
     the item and the module's tiling settings) and placed by offsets, so a
     step whose set of parameters changes (a parameter without a gradient,
     a rank change) costs array arithmetic, not a rebuild of every tile."""
-    knobs = (TALL_PROJECT, PIPE_STRIP_ORDER, PIPE_MIN_RANK, L2_OPERANDS, L.APPLY_GROUP)
+    knobs = (TALL_PROJECT, WIDE_PROJECT, PIPE_STRIP_ORDER, PIPE_MIN_RANK, L2_OPERANDS, L.APPLY_GROUP)
     if cache is not None and len(cache) > 4 * len(items) + 64:
         cache.clear()
     parts = {k: [] for k in _TASK_TYPES}
@@ -364,6 +367,7 @@ def _build_structure(items: list[PItem], cache: dict | None = None):
 XCDS = 8   # MI355X: 8 accelerator dies, workgroup i is dispatched to die i % 8
 PIPE_MIN_RANK = 128   # wide apply tiles of blocks with k >= this use the pipelined kernel
 TALL_PROJECT = True   # projection tasks of 128 rows of T where k % 128 == 0
+WIDE_PROJECT = True   # ... and of 256 rows where k % 256 == 0 (G streamed once)
 RECENT_STRUCTURES = 4   # whole step structures kept on the device (run_step)
 PIPE_STRIP_ORDER = True   # pipelined leaves always take the strip-major (super-tile) order
 L2_OPERANDS = 2 << 20   # bytes of W / U_r rows a die's L2 (4 MB) keeps beside the streams
@@ -702,7 +706,7 @@ def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
 
     if N["adam"]:
         _call("scao_adam_step", tp("adam"), N["adam"], P, SL, s)
-    for var in range(8):
+    for var in range(12):
         if N[f"proj{var}"]:
             _call("scao_kron_project", tp(f"proj{var}"), N[f"proj{var}"], LF, P, SL, var, s)
     if N["delta"]:

@@ -106,7 +106,7 @@ def test_diag_subblock_tasks():
     dl = [i for i, (lf, *_) in enumerate(leaves) if not lf.use_kronecker]
     assert len(dl) == 1
     d = dl[0]
-    for kind in [f"proj{v}" for v in range(8)] + ["lift"]:
+    for kind in [f"proj{v}" for v in range(12)] + ["lift"]:
         assert not any(int(t["idx"]) == d for t in arrays[kind]), kind
     dtasks = [t for t in arrays["delta"] if int(t["idx"]) == d]
     assert len(dtasks) == 1 and dtasks[0]["slot"] >= 0
