@@ -1012,29 +1012,172 @@ __global__ __launch_bounds__(256) void k_tri_info(const double* d, const double*
   }
 }
 
-// One thread per (matrix, eigenvalue index); index j (0-based, ascending) is
-// computed when j >= n - kq (the kq largest) or j < nneg (negative).
+// Multisection.  BL lanes share one eigenvalue index and each runs BS Sturm
+// counts at once, so an iteration evaluates BP = BL * BS points and shrinks
+// the bracket (BP + 1) times (about 13 iterations to fp64 resolution against
+// 53 halvings).  The counts' divisions are reciprocals (v_rcp_f64 and two
+// Newton steps, no condition-register chain as in IEEE division), so a lane's
+// BS counts interleave.  A quotient with a few ulps of error is a relative
+// perturbation of the matrix of that size, as the rounding of the divisions
+// already is (dstebz's analysis), so counts and brackets stay those of a
+// matrix within a few ulps of T.
+constexpr int BL = 4;
+constexpr int BS = 4;
+constexpr int BP = BL * BS;
+
+__device__ __forceinline__ double recip(double q) {
+  double r = __builtin_amdgcn_rcp(q);
+  double t = fma(-q, r, 1.0);
+  r = fma(r, t, r);
+  t = fma(-q, r, 1.0);
+  return fma(r, t, r);
+}
+
+// Sturm counts of T - x[t] for S points at once (as sturm above).
+template <int S>
+__device__ __forceinline__ void sturm_ms(const double* __restrict__ d,
+                                         const double* __restrict__ e2, int n,
+                                         const double (&x)[S], double pivmin, int (&c)[S]) {
+  double q[S];
+#pragma unroll
+  for (int t = 0; t < S; ++t) {
+    q[t] = d[0] - x[t];
+    if (fabs(q[t]) < pivmin) q[t] = -pivmin;
+    c[t] = q[t] < 0.0;
+  }
+  auto step = [&](double dv, double ev) {
+#pragma unroll
+    for (int t = 0; t < S; ++t) {
+      q[t] = fma(-ev, recip(q[t]), dv - x[t]);
+      if (fabs(q[t]) < pivmin) q[t] = -pivmin;
+      c[t] += q[t] < 0.0;
+    }
+  };
+  int i = 1;
+  if (n - 1 >= SG) {
+    double dn[SG], en[SG];
+#pragma unroll
+    for (int t = 0; t < SG; ++t) {
+      dn[t] = d[1 + t];
+      en[t] = e2[t];
+    }
+    for (; i + SG <= n; i += SG) {
+      double dc[SG], ec[SG];
+#pragma unroll
+      for (int t = 0; t < SG; ++t) {
+        dc[t] = dn[t];
+        ec[t] = en[t];
+      }
+      if (i + 2 * SG <= n) {
+#pragma unroll
+        for (int t = 0; t < SG; ++t) {
+          dn[t] = d[i + SG + t];
+          en[t] = e2[i + SG - 1 + t];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < SG; ++t) step(dc[t], ec[t]);
+    }
+  }
+  for (; i < n; ++i) step(d[i], e2[i - 1]);
+}
+
+// The eigenvalues wanted per matrix: the kq largest (indices n-1 .. n-kq),
+// and the negative ones not among them (indices 0 .. nneg-1), which only
+// enter the sum of the clamped spectrum.  Waves 0 .. WT-1 of a matrix serve
+// the largest, 64 / BL per wave by multisection; the rest the negative ones,
+// NB2 per lane by bisection (interleaved counts, one point each: with many
+// eigenvalues to find, the halving that needs the fewest counts is
+// cheapest), bracketed by [lo, 0] and stopped at an absolute width of
+// 1e-12 |T| (at most 1e-12 |T| n off in the sum; the largest are resolved
+// to a few ulps of themselves).  The matrix is blockIdx.x: workgroups go to
+// the XCDs round-robin by linear index, and with the matrix index slowest
+// every block with work would land on one XCD.
+constexpr int NB2 = 2;
 __global__ __launch_bounds__(256) void k_bisect(const double* d, const double* e2, int n, int kq,
                                                 const double* info, const int* nneg,
                                                 double* wall) {
-  const int j = blockIdx.x * 256 + threadIdx.x;
-  const int mat = blockIdx.y;
-  if (j >= n) return;
+  const int mat = blockIdx.x;
+  const int wv = blockIdx.y * 4 + threadIdx.x / 64;
+  const int l = threadIdx.x % 64;
   const int neg = nneg[mat];
-  if (!(j >= n - kq || j < neg)) return;
+  const int nn = neg < n - kq ? neg : n - kq;   // negative ones to find
+  const int wt = (kq + 64 / BL - 1) / (64 / BL);
   const double* dm = d + (int64_t)mat * n;
   const double* em = e2 + (int64_t)mat * n;
-  double lo = info[4 * mat + 0], hi = info[4 * mat + 1];
+  const double lo0 = info[4 * mat + 0], hi0 = info[4 * mat + 1];
   const double pivmin = info[4 * mat + 2];
-  for (int it = 0; it < 80; ++it) {
-    const double mid = 0.5 * (lo + hi);
-    if (hi - lo <= 2.0 * 2.220446049250313e-16 * fmax(fabs(lo), fabs(hi)) + pivmin) break;
-    if (sturm(dm, em, n, mid, pivmin) > j)
-      hi = mid;
-    else
-      lo = mid;
+  if (wv < wt) {
+    const int sub = l % BL;
+    const int slot = wv * (64 / BL) + l / BL;
+    const bool act = slot < kq;
+    const int j = n - 1 - (act ? slot : 0);
+    double lo = lo0, hi = hi0;
+    bool done = !act;
+    for (int it = 0; it < 40; ++it) {
+      if (hi - lo <= 2.0 * 2.220446049250313e-16 * fmax(fabs(lo), fabs(hi)) + pivmin) done = true;
+      if (__all(done)) break;
+      // points lo + h * (p + 1), p = 0 .. BP-1; this lane's are p = sub * BS + t
+      const double h = (hi - lo) / (BP + 1);
+      double x[BS];
+#pragma unroll
+      for (int t = 0; t < BS; ++t) x[t] = lo + h * (double)(sub * BS + t + 1);
+      int c[BS];
+      sturm_ms<BS>(dm, em, n, x, pivmin, c);
+      // r = number of points whose count is <= j (a prefix: counts grow with x)
+      int r = 0;
+#pragma unroll
+      for (int t = 0; t < BS; ++t) r += c[t] <= j;
+      r += __shfl_xor(r, 1);
+      r += __shfl_xor(r, 2);
+      if (!done) {
+        const double nlo = r > 0 ? lo + h * (double)r : lo;
+        const double nhi = r < BP ? lo + h * (double)(r + 1) : hi;
+        lo = nlo;
+        hi = nhi;
+      }
+    }
+    if (act && sub == 0) wall[(int64_t)mat * n + j] = 0.5 * (lo + hi);
+    return;
   }
-  wall[(int64_t)mat * n + j] = 0.5 * (lo + hi);
+  const int base = (wv - wt) * 64 * NB2;
+  if (base >= nn) return;                 // the whole wavefront
+  const double tol = 1e-12 * fmax(fabs(lo0), fabs(hi0)) + pivmin;
+  int j[NB2];
+  bool done[NB2];
+  double lo[NB2], hi[NB2];
+#pragma unroll
+  for (int t = 0; t < NB2; ++t) {
+    j[t] = base + l + 64 * t;
+    done[t] = j[t] >= nn;
+    lo[t] = lo0;
+    hi[t] = 0.0;
+  }
+  for (int it = 0; it < 64; ++it) {
+    bool all = true;
+#pragma unroll
+    for (int t = 0; t < NB2; ++t) {
+      if (hi[t] - lo[t] <= tol) done[t] = true;
+      all = all && done[t];
+    }
+    if (__all(all)) break;
+    double x[NB2];
+#pragma unroll
+    for (int t = 0; t < NB2; ++t) x[t] = 0.5 * (lo[t] + hi[t]);
+    int c[NB2];
+    sturm_ms<NB2>(dm, em, n, x, pivmin, c);
+#pragma unroll
+    for (int t = 0; t < NB2; ++t)
+      if (!done[t]) {
+        if (c[t] > j[t])
+          hi[t] = x[t];
+        else
+          lo[t] = x[t];
+      }
+  }
+#pragma unroll
+  for (int t = 0; t < NB2; ++t)
+    if (j[t] < nn) wall[(int64_t)mat * n + j[t]] = 0.5 * (lo[t] + hi[t]);
 }
 
 // The kq largest, descending, and total = trace - sum of the negative ones
@@ -1753,7 +1896,10 @@ extern "C" int scao_eig_bisect(const double* d, const double* e, int n, int batc
   double* e2 = info + 5 * (int64_t)batch;     // after nneg's batch 8-byte slots
   hipLaunchKernelGGL(k_tri_info, dim3(batch), dim3(256), 0, s, d, e, n, info, nneg, e2);
   SCAO_LAUNCH_CHECK("scao_eig_bisect/info");
-  hipLaunchKernelGGL(k_bisect, dim3((n + 255) / 256, batch), dim3(256), 0, s, d, e2, n, kq, info,
+  // wavefronts for the kq largest (64 / BL each) and for up to n - kq
+  // negative ones (64 * NB2 each)
+  const int nwave = (kq + 64 / BL - 1) / (64 / BL) + (n - kq + 64 * NB2 - 1) / (64 * NB2);
+  hipLaunchKernelGGL(k_bisect, dim3(batch, (nwave + 3) / 4), dim3(256), 0, s, d, e2, n, kq, info,
                      nneg, wall);
   SCAO_LAUNCH_CHECK("scao_eig_bisect/bisect");
   hipLaunchKernelGGL(k_bisect_finish, dim3(batch), dim3(64), 0, s, wall, n, kq, info, nneg, w,
