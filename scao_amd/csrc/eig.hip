@@ -712,7 +712,9 @@ __global__ __launch_bounds__(256) void k_band_finish(const float* A, int64_t str
 }
 
 // --------------------------------------------------------------- sb2st ---
-// Bulge chasing in float64, one workgroup of SB_W wavefronts per matrix.
+// Bulge chasing in float64, one workgroup of SB_W wavefronts per matrix (the
+// per-task chain of LDS round trips and shuffles is latency-bound, and there is
+// one matrix per CU: more sweeps in flight are the parallelism there is).
 // Task k of sweep s owns band rows q0..q0+LM-1 (q0 = s + 1 + 16k): the block
 // E = B[rows, previous block's rows] (for task 0 the single column s) and the
 // diagonal block D.  E gets the previous reflector from the right, a new
@@ -724,7 +726,7 @@ __global__ __launch_bounds__(256) void k_band_finish(const float* A, int64_t str
 //     each wavefront publishes its progress (s * 65536 + tasks done) in LDS;
 //   * the rows of task k+1 are loaded while task k computes (they need sweep
 //     s-1 to have finished task k+3, which it almost always has).
-constexpr int SB_W = 8;
+constexpr int SB_W = 16;   // 16 sweeps in flight (8: 75.8 ms, 12: 59.2, 16: 53.3 at 240 x 2048^2)
 constexpr int SB_BIG = 1 << 16;
 
 struct Sb2stLds {
