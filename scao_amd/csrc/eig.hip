@@ -82,13 +82,26 @@ __global__ __launch_bounds__(1024) void k_panel_qr(float* A, int64_t stride, int
   float* Am = A + (int64_t)blockIdx.x * stride;
   const int r0 = c0 + NB, m = n - r0;
   const int kk = m < NB ? m : NB;
+  // a row's 16 floats as four 16-byte accesses when rows are 16-byte aligned
+  // (one access instruction then touches 64 lines for 16 bytes each, against
+  // 64 lines for 4 bytes each with scalar accesses)
+  const bool vec = (n % 4) == 0 && (stride % 4) == 0 && (((uintptr_t)A) & 15) == 0;
   float P[RPT][NB];
 #pragma unroll
   for (int h = 0; h < RPT; ++h) {
     const int row = tid + 1024 * h;
+    const float* arow = Am + (int64_t)(r0 + row) * n + c0;
+    if (row < m && vec) {
 #pragma unroll
-    for (int c = 0; c < NB; ++c)
-      P[h][c] = row < m ? Am[(int64_t)(r0 + row) * n + c0 + c] : 0.f;
+      for (int c = 0; c < NB; c += 4) {
+        const v4f x = gld4(arow + c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) P[h][c + e] = x[e];
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < NB; ++c) P[h][c] = row < m ? arow[c] : 0.f;
+    }
   }
   if (tid < NB * NB) Ts[tid / NB][tid % NB] = 0.f;
   __syncthreads();
@@ -163,8 +176,16 @@ __global__ __launch_bounds__(1024) void k_panel_qr(float* A, int64_t stride, int
     const int row = tid + 1024 * h;
     if (row >= m) continue;
     float* arow = Am + (int64_t)(r0 + row) * n + c0;
+    float o[NB];
 #pragma unroll
-    for (int c = 0; c < NB; ++c) arow[c] = row > c ? (c < kk ? P[h][c] : 0.f) : (row == c ? (c < kk ? 1.f : 0.f) : 0.f);
+    for (int c = 0; c < NB; ++c) o[c] = row > c ? (c < kk ? P[h][c] : 0.f) : (row == c ? (c < kk ? 1.f : 0.f) : 0.f);
+    if (vec) {
+#pragma unroll
+      for (int c = 0; c < NB; c += 4) gst4(arow + c, v4f{o[c], o[c + 1], o[c + 2], o[c + 3]});
+    } else {
+#pragma unroll
+      for (int c = 0; c < NB; ++c) arow[c] = o[c];
+    }
     if (row < NB) {
       // R row `row`: columns c >= row, band diagonal d = NB + row - c
       float* brow = Bm + (int64_t)(r0 + row) * BW;
@@ -584,78 +605,179 @@ __global__ __launch_bounds__(256) void k_sy2sb_update_vec(float* A, int64_t sA, 
   }
 }
 
-// The panel's correction W and the next panel's columns, one workgroup per
-// matrix.  V: the panel's reflectors (m x 16, rows r0.. of A at column c0),
-// Y = A22 V (m x 16), T (16 x 16 upper):
-//   G = V^T Y (fixed-order sum over the rows), M = T^T G T,
+// The panel's correction W and the next panel's columns, one workgroup of
+// 1024 threads per matrix.  V: the panel's reflectors (m x 16, rows r0.. of A
+// at column c0), Y = A22 V (m x 16), T (16 x 16 upper):
+//   G = V^T Y (four row-quarter partial sums per 256-row chunk, added in a
+//       fixed order), M = T^T G T,
 //   W = Y T - V M / 2                          (m x 16, to Wout),
 // and, with `strip`, the next panel's columns r0..r0+15 of rows r0..:
 //   A[r0+i][r0+j] -= V[i] . W[j] + W[i] . V[j]   (j < 16).
-__global__ __launch_bounds__(256) void k_sy2sb_panel_w(float* A, int64_t sA, int n, int r0, int c0,
-                                                       const float* Y, const float* T, float* Wout,
-                                                       int strip) {
-  __shared__ float Vs[64][17], Ys[64][17];
-  __shared__ float Ts[16][17], Gs[16][17], GTs[16][17], Ms[16][17];
+// W and the strip take one thread per row (PW_RPT rows per thread), each
+// row's 16 floats as four 16-byte accesses when rows are 16-byte aligned.
+constexpr int PW_RPT = 2;    // rows per thread: m <= 2048 (larger m loops)
+__device__ __forceinline__ void ld16(const float* p, bool vec, float (&x)[16]) {
+  if (vec) {
+#pragma unroll
+    for (int c = 0; c < 16; c += 4) {
+      const v4f v = gld4(p + c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[c + e] = v[e];
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) x[c] = p[c];
+  }
+}
+__device__ __forceinline__ void st16(float* p, bool vec, const float (&x)[16]) {
+  if (vec) {
+#pragma unroll
+    for (int c = 0; c < 16; c += 4) gst4(p + c, v4f{x[c], x[c + 1], x[c + 2], x[c + 3]});
+  } else {
+#pragma unroll
+    for (int c = 0; c < 16; ++c) p[c] = x[c];
+  }
+}
+__global__ __launch_bounds__(1024) void k_sy2sb_panel_w(float* A, int64_t sA, int n, int r0, int c0,
+                                                        const float* Y, const float* T, float* Wout,
+                                                        int strip) {
+  __shared__ float Vs[256][17], Ys[256][17];
+  __shared__ float Gp[4][16][17];
+  __shared__ float Ts[16][17], GTs[16][17], Ms[16][17];
   __shared__ float Vt[16][17], Wt[16][17];
   const int mat = blockIdx.x, tid = threadIdx.x;
   const int m = n - r0;
   float* Am = A + (int64_t)mat * sA;
   const float* Ym = Y + (int64_t)mat * m * 16;
   float* Wm = Wout + (int64_t)mat * m * 16;
-  const int a = tid / 16, b = tid % 16;
-  Ts[a][b] = T[(int64_t)mat * 256 + a * 16 + b];
-  // G[a][b] = sum_i V[i][a] Y[i][b], rows in chunks of 64
+  const bool vec = (n % 4) == 0 && (sA % 4) == 0 && (c0 % 4) == 0 && (r0 % 4) == 0 &&
+                   ((((uintptr_t)A) | ((uintptr_t)Y) | ((uintptr_t)Wout)) & 15) == 0;
+  const int a = (tid / 16) % 16, b = tid % 16, p = tid / 256;
+  if (tid < 256) Ts[a][b] = T[(int64_t)mat * 256 + a * 16 + b];
+  // G[a][b] = sum_i V[i][a] Y[i][b]: chunks of 256 rows staged in LDS (the
+  // next chunk's loads in flight during the current chunk's sums); thread
+  // (p, a, b) sums rows 64p .. 64p+63 of each chunk
+  const int lr = tid / 4, lq = (tid % 4) * 4;    // loader: row lr, floats lq..lq+3
+  auto load = [&](int i0, v4f& xv, v4f& xy) {
+    const int i = i0 + lr;
+    xv = v4f{0.f, 0.f, 0.f, 0.f};
+    xy = xv;
+    if (i < m) {
+      const float* vp = Am + (int64_t)(r0 + i) * n + c0 + lq;
+      const float* yp = Ym + (int64_t)i * 16 + lq;
+      if (vec) {
+        xv = gld4(vp);
+        xy = gld4(yp);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          xv[e] = vp[e];
+          xy[e] = yp[e];
+        }
+      }
+    }
+  };
   float g = 0.f;
-  for (int i0 = 0; i0 < m; i0 += 64) {
-    __syncthreads();
-    for (int idx = tid; idx < 64 * 16; idx += 256) {
-      const int row = idx / 16, q = idx % 16, i = i0 + row;
-      Vs[row][q] = i < m ? Am[(int64_t)(r0 + i) * n + c0 + q] : 0.f;
-      Ys[row][q] = i < m ? Ym[(int64_t)i * 16 + q] : 0.f;
+  v4f xv, xy;
+  load(0, xv, xy);
+  for (int i0 = 0; i0 < m; i0 += 256) {
+    __syncthreads();                   // the previous chunk is consumed
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      Vs[lr][lq + e] = xv[e];
+      Ys[lr][lq + e] = xy[e];
     }
     __syncthreads();
-    const int rows = m - i0 < 64 ? m - i0 : 64;
-    for (int row = 0; row < rows; ++row) g = fmaf(Vs[row][a], Ys[row][b], g);
+    if (i0 + 256 < m) load(i0 + 256, xv, xy);
+    const int rows = m - i0 < 256 ? m - i0 : 256;
+    const int re = rows < 64 * p + 64 ? rows : 64 * p + 64;
+    for (int row = 64 * p; row < re; ++row) g = fmaf(Vs[row][a], Ys[row][b], g);
   }
-  Gs[a][b] = g;
+  Gp[p][a][b] = g;
   __syncthreads();
-  float x = 0.f;
-  for (int c = 0; c < 16; ++c) x = fmaf(Gs[a][c], Ts[c][b], x);
-  GTs[a][b] = x;
+  if (tid < 256) {
+    const float gg = ((Gp[0][a][b] + Gp[1][a][b]) + Gp[2][a][b]) + Gp[3][a][b];
+    Gp[0][a][b] = gg;
+  }
   __syncthreads();
-  x = 0.f;
-  for (int c = 0; c < 16; ++c) x = fmaf(Ts[c][a], GTs[c][b], x);
-  Ms[a][b] = x;
+  if (tid < 256) {
+    float x = 0.f;
+    for (int c = 0; c < 16; ++c) x = fmaf(Gp[0][a][c], Ts[c][b], x);
+    GTs[a][b] = x;
+  }
   __syncthreads();
-  // W rows: 16 rows per pass, thread (row a, column b)
-  for (int i0 = 0; i0 < m; i0 += 16) {
-    const int i = i0 + a;
-    if (i < m) {
-      const float* yr = Ym + (int64_t)i * 16;
-      const float* vr = Am + (int64_t)(r0 + i) * n + c0;
-      float yt = 0.f, vm = 0.f;
-      for (int c = 0; c < 16; ++c) {
-        yt = fmaf(yr[c], Ts[c][b], yt);
-        vm = fmaf(vr[c], Ms[c][b], vm);
+  if (tid < 256) {
+    float x = 0.f;
+    for (int c = 0; c < 16; ++c) x = fmaf(Ts[c][a], GTs[c][b], x);
+    Ms[a][b] = x;
+  }
+  __syncthreads();
+  // W rows, one thread per row
+  for (int ib = 0; ib < m; ib += 1024 * PW_RPT) {
+    float yr[PW_RPT][16], vr[PW_RPT][16];
+#pragma unroll
+    for (int h = 0; h < PW_RPT; ++h) {
+      const int i = ib + tid + 1024 * h;
+      if (i < m) {
+        ld16(Ym + (int64_t)i * 16, vec, yr[h]);
+        ld16(Am + (int64_t)(r0 + i) * n + c0, vec, vr[h]);
       }
-      const float wv = yt - 0.5f * vm;
-      Wm[(int64_t)i * 16 + b] = wv;
-      if (i0 == 0) {
-        Wt[a][b] = wv;
-        Vt[a][b] = vr[b];
+    }
+#pragma unroll
+    for (int h = 0; h < PW_RPT; ++h) {
+      const int i = ib + tid + 1024 * h;
+      if (i >= m) continue;
+      // T and M are read from LDS per row: hoisted out of the loops they
+      // would take 512 registers
+      asm volatile("" ::: "memory");
+      float w[16];
+#pragma unroll
+      for (int bb = 0; bb < 16; ++bb) {
+        float yt = 0.f, vm = 0.f;
+#pragma unroll
+        for (int c = 0; c < 16; ++c) {
+          yt = fmaf(yr[h][c], Ts[c][bb], yt);
+          vm = fmaf(vr[h][c], Ms[c][bb], vm);
+        }
+        w[bb] = yt - 0.5f * vm;
+      }
+      st16(Wm + (int64_t)i * 16, vec, w);
+      if (i < 16) {
+#pragma unroll
+        for (int bb = 0; bb < 16; ++bb) {
+          Wt[i][bb] = w[bb];
+          Vt[i][bb] = vr[h][bb];
+        }
       }
     }
   }
   if (!strip) return;
   __syncthreads();                   // W (first rows) and the V rows in LDS; W in memory
-  for (int i0 = 0; i0 < m; i0 += 16) {
-    const int i = i0 + a;
-    if (i >= m) continue;
-    const float* vr = Am + (int64_t)(r0 + i) * n + c0;
-    const float* wr = Wm + (int64_t)i * 16;
-    float d = 0.f;
-    for (int q = 0; q < 16; ++q) d = fmaf(vr[q], Wt[b][q], fmaf(wr[q], Vt[b][q], d));
-    Am[(int64_t)(r0 + i) * n + r0 + b] -= d;
+  for (int ib = 0; ib < m; ib += 1024 * PW_RPT) {
+    float vr[PW_RPT][16], wr[PW_RPT][16], ar[PW_RPT][16];
+#pragma unroll
+    for (int h = 0; h < PW_RPT; ++h) {
+      const int i = ib + tid + 1024 * h;
+      if (i < m) {
+        ld16(Am + (int64_t)(r0 + i) * n + c0, vec, vr[h]);
+        ld16(Wm + (int64_t)i * 16, vec, wr[h]);
+        ld16(Am + (int64_t)(r0 + i) * n + r0, vec, ar[h]);
+      }
+    }
+#pragma unroll
+    for (int h = 0; h < PW_RPT; ++h) {
+      const int i = ib + tid + 1024 * h;
+      if (i >= m) continue;
+      asm volatile("" ::: "memory");   // Wt and Vt read per row, as T and M above
+#pragma unroll
+      for (int bb = 0; bb < 16; ++bb) {
+        float d = 0.f;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) d = fmaf(vr[h][q], Wt[bb][q], fmaf(wr[h][q], Vt[bb][q], d));
+        ar[h][bb] -= d;
+      }
+      st16(Am + (int64_t)(r0 + i) * n + r0, vec, ar[h]);
+    }
   }
 }
 
@@ -1809,7 +1931,7 @@ extern "C" int scao_eig_sy2sb_panel_w(float* A, int64_t sA, int n, int c0, int b
                      sA >= (int64_t)n * n && (!strip || c0 + 2 * NB <= n),
                  "scao_eig_sy2sb_panel_w: bad arguments n=%d c0=%d", n, c0);
   if (batch == 0) return SCAO_OK;
-  hipLaunchKernelGGL(k_sy2sb_panel_w, dim3(batch), dim3(256), 0, (hipStream_t)stream, A, sA, n,
+  hipLaunchKernelGGL(k_sy2sb_panel_w, dim3(batch), dim3(1024), 0, (hipStream_t)stream, A, sA, n,
                      c0 + NB, c0, Y, T, W, strip);
   SCAO_LAUNCH_CHECK("scao_eig_sy2sb_panel_w");
   return SCAO_OK;
