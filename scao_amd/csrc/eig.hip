@@ -77,7 +77,8 @@ __global__ __launch_bounds__(1024) void k_panel_qr(float* A, int64_t stride, int
   __shared__ float bc[NB + 2];
   __shared__ float rowj[2][NB];
   __shared__ float Ts[NB][NB];
-  __shared__ float betas[NB];
+  __shared__ float betas[NB], taus[NB];
+  __shared__ float Ds[NB][NB + 1];
   const int tid = threadIdx.x;
   float* Am = A + (int64_t)blockIdx.x * stride;
   const int r0 = c0 + NB, m = n - r0;
@@ -156,14 +157,27 @@ __global__ __launch_bounds__(1024) void k_panel_qr(float* A, int64_t stride, int
       }
     }
     if (tid == 0) {
-      // T[0:j, j] = T[0:j, 0:j] (-tau d[0:j]);  T[j][j] = tau  (thread 0 only)
-      for (int i = 0; i < j; ++i) {
-        float s = 0.f;
-        for (int l = i; l < j; ++l) s = fmaf(Ts[i][l], dot[l], s);
-        Ts[i][j] = -tau * s;
-      }
-      Ts[j][j] = tau;
+      // the column's dots and tau for T, built after the loop
+#pragma unroll
+      for (int c = 0; c < NB; ++c) Ds[j][c] = dot[c];
+      taus[j] = tau;
       betas[j] = beta;
+    }
+  }
+  __syncthreads();
+  // T[0:j, j] = T[0:j, 0:j] (-tau_j d_j[0:j]), T[j][j] = tau_j, column by
+  // column on one wavefront (lane i: row i; the same sums in the same order
+  // as a serial build)
+  if (tid < 64) {
+    for (int j = 0; j < kk; ++j) {
+      if (tid < j) {
+        float s = 0.f;
+        for (int l = tid; l < j; ++l) s = fmaf(Ts[tid][l], Ds[j][l], s);
+        Ts[tid][j] = -taus[j] * s;
+      }
+      if (tid == j) Ts[j][j] = taus[j];
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+      __builtin_amdgcn_wave_barrier();
     }
   }
   __syncthreads();
