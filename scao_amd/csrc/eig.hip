@@ -40,7 +40,7 @@ constexpr int BW = SCAO_EIG_BANDW;   // 33: band row pitch (diagonals 0..2b)
 constexpr int OW = NB + 1;           // 17: pitch of the original band copy
 
 // ------------------------------------------------------------ panel QR ---
-// Block reduction of NV floats over a 1024-thread workgroup: every thread
+// Block reduction of NV floats over a workgroup of up to 1024 threads: every thread
 // receives the NV sums in out[] (LDS).  (A reduce-scatter across the wave's
 // lanes, 28 shuffles for 16 values instead of 96, measured slower: its
 // lane-dependent selects cost more than the shuffles they save.)
@@ -68,10 +68,12 @@ __device__ __forceinline__ void block_sum_f(float (&x)[NV], float (*red)[NV + 1]
 
 // Householder QR of the panel A[r0:n, c0:c0+NB], r0 = c0 + NB, m = n - r0
 // rows (LAPACK geqr2 + larft, forward columnwise).  Thread t holds rows
-// t + 1024 h (h < RPT) of the panel.  Outputs: V (explicit, unit lower
+// t + NT h (h < RPT) of the panel.  Outputs: V (explicit, unit lower
 // trapezoidal) over the panel of A, T (NB x NB upper), R into the band.
-template <int RPT>
-__global__ __launch_bounds__(1024) void k_panel_qr(float* A, int64_t stride, int n, int c0,
+// NT threads (256 .. 1024) hold RPT rows each: fewer waves make the per-column
+// block reductions cheaper for short panels.
+template <int RPT, int NT>
+__global__ __launch_bounds__(NT) void k_panel_qr(float* A, int64_t stride, int n, int c0,
                                                    float* Tout, float* band, int64_t bstride) {
   __shared__ float red[16][NB + 1];
   __shared__ float bc[NB + 2];
@@ -90,7 +92,7 @@ __global__ __launch_bounds__(1024) void k_panel_qr(float* A, int64_t stride, int
   float P[RPT][NB];
 #pragma unroll
   for (int h = 0; h < RPT; ++h) {
-    const int row = tid + 1024 * h;
+    const int row = tid + NT * h;
     const float* arow = Am + (int64_t)(r0 + row) * n + c0;
     if (row < m && vec) {
 #pragma unroll
@@ -123,7 +125,7 @@ __global__ __launch_bounds__(1024) void k_panel_qr(float* A, int64_t stride, int
     for (int c = 0; c < NB; ++c) acc[c] = 0.f;
 #pragma unroll
     for (int h = 0; h < RPT; ++h) {
-      const int row = tid + 1024 * h;
+      const int row = tid + NT * h;
       if (row > j && row < m) {
         const float pj = P[h][j];
 #pragma unroll
@@ -144,7 +146,7 @@ __global__ __launch_bounds__(1024) void k_panel_qr(float* A, int64_t stride, int
     // v (rows > j) replaces column j; P[:, c] -= tau v w_c for c > j
 #pragma unroll
     for (int h = 0; h < RPT; ++h) {
-      const int row = tid + 1024 * h;
+      const int row = tid + NT * h;
       if (row >= j && row < m) {
         float v = 1.f;
         if (row > j) {
@@ -187,7 +189,7 @@ __global__ __launch_bounds__(1024) void k_panel_qr(float* A, int64_t stride, int
   float* Bm = band + (int64_t)blockIdx.x * bstride;
 #pragma unroll
   for (int h = 0; h < RPT; ++h) {
-    const int row = tid + 1024 * h;
+    const int row = tid + NT * h;
     if (row >= m) continue;
     float* arow = Am + (int64_t)(r0 + row) * n + c0;
     float o[NB];
@@ -1927,12 +1929,14 @@ extern "C" int scao_eig_panel_qr(float* A, int64_t stride, int n, int c0, int ba
   const int m = n - c0 - NB;
   hipStream_t s = (hipStream_t)stream;
   float* Am = A;
-  if (m <= 1024)
-    hipLaunchKernelGGL((k_panel_qr<1>), dim3(batch), dim3(1024), 0, s, Am, stride, n, c0, T, band, bstride);
+  if (m <= 512)
+    hipLaunchKernelGGL((k_panel_qr<2, 256>), dim3(batch), dim3(256), 0, s, Am, stride, n, c0, T, band, bstride);
+  else if (m <= 1024)
+    hipLaunchKernelGGL((k_panel_qr<2, 512>), dim3(batch), dim3(512), 0, s, Am, stride, n, c0, T, band, bstride);
   else if (m <= 2048)
-    hipLaunchKernelGGL((k_panel_qr<2>), dim3(batch), dim3(1024), 0, s, Am, stride, n, c0, T, band, bstride);
+    hipLaunchKernelGGL((k_panel_qr<2, 1024>), dim3(batch), dim3(1024), 0, s, Am, stride, n, c0, T, band, bstride);
   else
-    hipLaunchKernelGGL((k_panel_qr<4>), dim3(batch), dim3(1024), 0, s, Am, stride, n, c0, T, band, bstride);
+    hipLaunchKernelGGL((k_panel_qr<4, 1024>), dim3(batch), dim3(1024), 0, s, Am, stride, n, c0, T, band, bstride);
   SCAO_LAUNCH_CHECK("scao_eig_panel_qr");
   return SCAO_OK;
 }
