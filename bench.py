@@ -345,6 +345,63 @@ def stats_summary(stats_csv: str, config: str, cmd: str, top: int = 25) -> str:
     return "\n".join(out) + "\n"
 
 
+def mfma_summary(counter_csv: str, stats_csv: str, config: str, cmd: str) -> str:
+    """Markdown MFMA utilisation of the GEMM-shaped kernels from a rocprofv3
+    --pmc run (SQ_VALU_MFMA_BUSY_CYCLES, SQ_INSTS_VALU_MFMA_MOPS_F32,
+    SQ_INSTS_VALU_MFMA_MOPS_BF16, GRBM_GUI_ACTIVE) and the kernel-trace
+    statistics of the same build (average durations).  A MOPS count is in
+    units of 512 flops; kernels whose fp32 products run as three-way bf16
+    splits (six bf16 MFMAs per fp32 product) are credited bf16 flops / 6 as
+    fp32-equivalent work, against the fp32 MFMA peak."""
+    import collections
+    import csv
+    import re
+    per = collections.defaultdict(lambda: collections.defaultdict(float))
+    meta = {}
+    for r in csv.DictReader(open(counter_csv)):
+        k = int(r["Dispatch_Id"])
+        per[k][r["Counter_Name"]] += float(r["Counter_Value"])
+        m = re.search(r"(k_[a-z_0-9]+)(<[^()]*>)?\(", r["Kernel_Name"])
+        meta[k] = m.group(1) + (m.group(2) or "")
+    times = {}
+    for r in csv.DictReader(open(stats_csv)):
+        m = re.search(r"(k_[a-z_0-9]+)(<[^()]*>)?\(", r["Name"])
+        if m:
+            times[m.group(1) + (m.group(2) or "")] = float(r["AverageNs"]) / 1e6
+    agg = collections.defaultdict(list)
+    for k, c in per.items():
+        agg[meta[k]].append(c)
+    out = [f"# MFMA utilisation of the GEMM-shaped kernels, {config} (rocprofv3 PMC)", "",
+           "Commands (a counter run and a kernel-trace run of the same build, then this "
+           "summary; from the repository root on the box):", "", "```", cmd, "```", "",
+           "`MfmaUtil` = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x 1024 SIMDs), "
+           "rocprofv3's own derived-counter formula (the CSV's GRBM_GUI_ACTIVE is the sum over "
+           "the 8 XCDs).  fp32 flops = MOPS_F32 x 512; bf16 flops = MOPS_BF16 x 512, of which "
+           "one sixth is fp32-equivalent work (fp32 products as three-way bf16 splits, six "
+           "MFMAs each).  Rate = fp32-equivalent flops / the kernel's average duration in the "
+           "trace run, against 157.3 TFLOP/s fp32 MFMA peak.", "",
+           "| kernel | dispatches | MfmaUtil | fp32 GFLOP | bf16 GFLOP | fp32-equiv. GFLOP "
+           "| avg ms | TFLOP/s | of fp32 peak |",
+           "|---|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    rows = []
+    for nm, v in agg.items():
+        n = len(v)
+        busy = sum(c["SQ_VALU_MFMA_BUSY_CYCLES"] for c in v) / n
+        gui = sum(c["GRBM_GUI_ACTIVE"] for c in v) / n
+        f32 = sum(c.get("SQ_INSTS_VALU_MFMA_MOPS_F32", 0.0) for c in v) / n * 512 / 1e9
+        b16 = sum(c.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0) for c in v) / n * 512 / 1e9
+        rows.append((nm, n, 100 * busy / (gui / 8 * 1024) if gui else 0.0, f32, b16,
+                     f32 + b16 / 6))
+    for nm, n, util, f32, b16, eq in sorted(rows, key=lambda r: -r[5]):
+        t = times.get(nm)
+        if t is None:
+            continue
+        tf = eq / t
+        out.append(f"| `{nm}` | {n} | {util:.1f}% | {f32:.1f} | {b16:.1f} | {eq:.1f} | {t:.3f} "
+                   f"| {tf:.1f} | {tf / 157.3:.2f} |")
+    return "\n".join(out) + "\n"
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -367,6 +424,9 @@ def main():
     ap.add_argument("--stats-summary", metavar="STATS_CSV", default=None,
                     help="print the markdown table of a rocprofv3 --stats kernel_stats.csv "
                          "of this bench and exit (no GPU use)")
+    ap.add_argument("--mfma-summary", nargs=2, metavar=("COUNTER_CSV", "STATS_CSV"), default=None,
+                    help="print the markdown MFMA utilisation summary of a rocprofv3 --pmc run "
+                         "and a --stats run of this bench and exit (no GPU use)")
     ap.add_argument("--pmc-command", default="",
                     help="the commands that made a summary's inputs (recorded verbatim)")
     ap.add_argument("--dominant", default="scao_kron_apply",
@@ -386,6 +446,9 @@ def main():
     args = ap.parse_args()
     if args.stats_summary:
         print(stats_summary(args.stats_summary, args.config, args.pmc_command))
+        return
+    if args.mfma_summary:
+        print(mfma_summary(*args.mfma_summary, args.config, args.pmc_command))
         return
     if args.refresh_summary:
         print(refresh_summary(args.refresh_summary, args.config, args.pmc_command))
