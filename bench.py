@@ -399,6 +399,12 @@ def mfma_summary(counter_csv: str, stats_csv: str, config: str, cmd: str) -> str
         tf = eq / t
         out.append(f"| `{nm}` | {n} | {util:.1f}% | {f32:.1f} | {b16:.1f} | {eq:.1f} | {t:.3f} "
                    f"| {tf:.1f} | {tf / 157.3:.2f} |")
+    out += ["", "Notes.  `k_gram_ema`'s average duration includes the run's first, cold refresh "
+            "(the refresh summary gives the steady per-refresh time); it computes the lower tiles "
+            "of each symmetric Gram only.  `k_project_x6` does exactly 2mnk fp32-equivalent flops "
+            "per step (six bf16 products each) and also streams p for the LARS norm.  `k_apply` "
+            "runs the back-projection's MFMAs under its streaming pass (HBM-bound).  "
+            "`k_sy2sb_update_vec` is the refresh's lower-triangle band-reduction pass."]
     return "\n".join(out) + "\n"
 
 
