@@ -938,108 +938,119 @@ __global__ __launch_bounds__(SB_W * 64) void k_sb2st(double* band, int n, double
     int q0 = s + 1, LN = 1;          // task 0: E is column s (one column)
     double ptau = 0.0;               // previous reflector (none for task 0)
     for (int k = 0; k < nt; ++k) {
-      const int LM = min(NB, n - q0);
-      // scatter this task's rows into E / D
-      for (int t = 0; t < 8; ++t) {
-        const int idx = l + 64 * t, row = idx >> 5, d = idx & 31;
-        if (row < LM) {
-          if (d <= row) {
-            S.D[row][row - d] = cur[t];
-            S.D[row - d][row] = cur[t];
-          } else if (d <= row + LN) {
-            S.E[row][LN + row - d] = cur[t];
-          }
-        }
-      }
-      // prefetch the next task's rows
-      if (k + 1 < nt) {
-        sb_wait(prog, s, min(k + 4, ntp));
-        const int q1 = q0 + LM, LM1 = min(NB, n - q1);
+      // an interior task (16 rows, a 16-column E) has every bound fixed:
+      // its instantiation drops the per-element edge tests (the kernel is
+      // bound by instruction issue)
+      auto task = [&](auto full) {
+        constexpr bool FULL = decltype(full)::value;
+        const int LM = FULL ? NB : min(NB, n - q0);
+        const int LNv = FULL ? NB : LN;
+        // scatter this task's rows into E / D
         for (int t = 0; t < 8; ++t) {
           const int idx = l + 64 * t, row = idx >> 5, d = idx & 31;
-          nxt[t] = row < LM1 ? Bm[(int64_t)(q1 + row) * BW + d] : 0.0;
+          if (row < LM) {
+            if (d <= row) {
+              S.D[row][row - d] = cur[t];
+              S.D[row - d][row] = cur[t];
+            } else if (d <= row + LNv) {
+              S.E[row][LNv + row - d] = cur[t];
+            }
+          }
         }
-      }
-      wave_sync();
-      // 1. E <- E (I - ptau pv pv^T)
-      if (ptau != 0.0) {
-        double t = 0.0;
-        if (r < LM)
-          for (int c = 4 * q; c < 4 * q + 4; ++c)
-            if (c < LN) t = fma(S.E[r][c], S.pv[c], t);
-        t = sum4(t);
-        wave_sync();
-        if (r < LM)
-          for (int c = 4 * q; c < 4 * q + 4; ++c)
-            if (c < LN) S.E[r][c] = fma(-ptau * t, S.pv[c], S.E[r][c]);
-        wave_sync();
-      }
-      // 2. reflector from E[:, 0] (length LM)
-      const int rr = l & 15;
-      const double x0 = rr < LM ? S.E[rr][0] : 0.0;
-      const double alpha = S.E[0][0];
-      const double s2 = sum16(rr >= 1 ? x0 * x0 : 0.0);
-      double tau = 0.0, beta = alpha, scale = 0.0;
-      if (s2 > 0.0) {
-        beta = -copysign(sqrt(alpha * alpha + s2), alpha);
-        tau = (beta - alpha) / beta;
-        scale = 1.0 / (alpha - beta);
-      }
-      wave_sync();
-      if (l < NB) {
-        S.v[l] = l == 0 ? 1.0 : (l < LM ? x0 * scale : 0.0);
-        if (l < LM) S.E[l][0] = l == 0 ? beta : 0.0;
-      }
-      wave_sync();
-      if (tau != 0.0) {
-        // 3. E[:, 1:] <- (I - tau v v^T) E[:, 1:]   (lane: column r, rows 4q..4q+3)
-        double w = 0.0;
-        if (r >= 1 && r < LN)
-          for (int i = 4 * q; i < 4 * q + 4; ++i)
-            if (i < LM) w = fma(S.v[i], S.E[i][r], w);
-        w = sum4(w);
-        wave_sync();
-        if (r >= 1 && r < LN)
-          for (int i = 4 * q; i < 4 * q + 4; ++i)
-            if (i < LM) S.E[i][r] = fma(-tau * S.v[i], w, S.E[i][r]);
-        // 4. D <- H D H: y = tau D v; y -= (tau/2)(y^T v) v; D -= v y^T + y v^T
-        double y = 0.0;
-        if (r < LM)
-          for (int c = 4 * q; c < 4 * q + 4; ++c)
-            if (c < LM) y = fma(S.D[r][c], S.v[c], y);
-        y = tau * sum4(y);
-        double a = (q == 0 && r < LM) ? y * S.v[r] : 0.0;
-        a += __shfl_xor(a, 4);
-        a += __shfl_xor(a, 8);
-        a += __shfl_xor(a, 16);
-        a += __shfl_xor(a, 32);
-        a *= 0.5 * tau;
-        if (q == 0 && r < LM) S.y[r] = fma(-a, S.v[r], y);
-        wave_sync();
-        if (r < LM)
-          for (int c = 4 * q; c < 4 * q + 4; ++c)
-            if (c < LM) S.D[r][c] = S.D[r][c] - (S.v[r] * S.y[c] + S.y[r] * S.v[c]);
-        wave_sync();
-      }
-      // store the rows back, then publish the task
-      for (int t = 0; t < 8; ++t) {
-        const int idx = l + 64 * t, row = idx >> 5, d = idx & 31;
-        if (row < LM) {
-          if (d <= row)
-            Bm[(int64_t)(q0 + row) * BW + d] = S.D[row][row - d];
-          else if (d <= row + LN)
-            Bm[(int64_t)(q0 + row) * BW + d] = S.E[row][LN + row - d];
+        // prefetch the next task's rows
+        if (k + 1 < nt) {
+          sb_wait(prog, s, min(k + 4, ntp));
+          const int q1 = q0 + LM, LM1 = min(NB, n - q1);
+          for (int t = 0; t < 8; ++t) {
+            const int idx = l + 64 * t, row = idx >> 5, d = idx & 31;
+            nxt[t] = row < LM1 ? Bm[(int64_t)(q1 + row) * BW + d] : 0.0;
+          }
         }
-      }
-      if (l < NB) S.pv[l] = S.v[l];
-      ptau = tau;
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      if (l == 0)
-        __hip_atomic_store(&prog[wid], s * SB_BIG + k + 1, __ATOMIC_RELEASE,
-                           __HIP_MEMORY_SCOPE_WORKGROUP);
-      wave_sync();
-      q0 += LM;
-      LN = LM;
+        wave_sync();
+        // 1. E <- E (I - ptau pv pv^T)
+        if (ptau != 0.0) {
+          double t = 0.0;
+          if (r < LM)
+            for (int c = 4 * q; c < 4 * q + 4; ++c)
+              if (c < LNv) t = fma(S.E[r][c], S.pv[c], t);
+          t = sum4(t);
+          wave_sync();
+          if (r < LM)
+            for (int c = 4 * q; c < 4 * q + 4; ++c)
+              if (c < LNv) S.E[r][c] = fma(-ptau * t, S.pv[c], S.E[r][c]);
+          wave_sync();
+        }
+        // 2. reflector from E[:, 0] (length LM)
+        const int rr = l & 15;
+        const double x0 = rr < LM ? S.E[rr][0] : 0.0;
+        const double alpha = S.E[0][0];
+        const double s2 = sum16(rr >= 1 ? x0 * x0 : 0.0);
+        double tau = 0.0, beta = alpha, scale = 0.0;
+        if (s2 > 0.0) {
+          beta = -copysign(sqrt(alpha * alpha + s2), alpha);
+          tau = (beta - alpha) / beta;
+          scale = 1.0 / (alpha - beta);
+        }
+        wave_sync();
+        if (l < NB) {
+          S.v[l] = l == 0 ? 1.0 : (l < LM ? x0 * scale : 0.0);
+          if (l < LM) S.E[l][0] = l == 0 ? beta : 0.0;
+        }
+        wave_sync();
+        if (tau != 0.0) {
+          // 3. E[:, 1:] <- (I - tau v v^T) E[:, 1:]   (lane: column r, rows 4q..4q+3)
+          double w = 0.0;
+          if (r >= 1 && r < LNv)
+            for (int i = 4 * q; i < 4 * q + 4; ++i)
+              if (i < LM) w = fma(S.v[i], S.E[i][r], w);
+          w = sum4(w);
+          wave_sync();
+          if (r >= 1 && r < LNv)
+            for (int i = 4 * q; i < 4 * q + 4; ++i)
+              if (i < LM) S.E[i][r] = fma(-tau * S.v[i], w, S.E[i][r]);
+          // 4. D <- H D H: y = tau D v; y -= (tau/2)(y^T v) v; D -= v y^T + y v^T
+          double y = 0.0;
+          if (r < LM)
+            for (int c = 4 * q; c < 4 * q + 4; ++c)
+              if (c < LM) y = fma(S.D[r][c], S.v[c], y);
+          y = tau * sum4(y);
+          double a = (q == 0 && r < LM) ? y * S.v[r] : 0.0;
+          a += __shfl_xor(a, 4);
+          a += __shfl_xor(a, 8);
+          a += __shfl_xor(a, 16);
+          a += __shfl_xor(a, 32);
+          a *= 0.5 * tau;
+          if (q == 0 && r < LM) S.y[r] = fma(-a, S.v[r], y);
+          wave_sync();
+          if (r < LM)
+            for (int c = 4 * q; c < 4 * q + 4; ++c)
+              if (c < LM) S.D[r][c] = S.D[r][c] - (S.v[r] * S.y[c] + S.y[r] * S.v[c]);
+          wave_sync();
+        }
+        // store the rows back, then publish the task
+        for (int t = 0; t < 8; ++t) {
+          const int idx = l + 64 * t, row = idx >> 5, d = idx & 31;
+          if (row < LM) {
+            if (d <= row)
+              Bm[(int64_t)(q0 + row) * BW + d] = S.D[row][row - d];
+            else if (d <= row + LNv)
+              Bm[(int64_t)(q0 + row) * BW + d] = S.E[row][LNv + row - d];
+          }
+        }
+        if (l < NB) S.pv[l] = S.v[l];
+        ptau = tau;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        if (l == 0)
+          __hip_atomic_store(&prog[wid], s * SB_BIG + k + 1, __ATOMIC_RELEASE,
+                             __HIP_MEMORY_SCOPE_WORKGROUP);
+        wave_sync();
+        q0 += LM;
+        LN = LM;
+      };
+      if (n - q0 >= NB && LN == NB)
+        task(std::true_type{});
+      else
+        task(std::false_type{});
 #pragma unroll
       for (int t = 0; t < 8; ++t) cur[t] = nxt[t];
     }
