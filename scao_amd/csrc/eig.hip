@@ -873,7 +873,11 @@ struct Sb2stLds {
   double v[NB];
   double y[NB];
   double pv[NB];
+  double junk;          // target of an interior task's out-of-window scatter
 };
+// An interior task addresses E, D and junk as offsets from E[0][0].
+constexpr int SB_D0 = NB * (NB + 1);
+constexpr int SB_JUNK = 2 * NB * (NB + 1) + 3 * NB;
 
 __device__ __forceinline__ double sum4(double x) {
   x += __shfl_xor(x, 1);
@@ -945,15 +949,31 @@ __global__ __launch_bounds__(SB_W * 64) void k_sb2st(double* band, int n, double
         constexpr bool FULL = decltype(full)::value;
         const int LM = FULL ? NB : min(NB, n - q0);
         const int LNv = FULL ? NB : LN;
-        // scatter this task's rows into E / D
-        for (int t = 0; t < 8; ++t) {
-          const int idx = l + 64 * t, row = idx >> 5, d = idx & 31;
-          if (row < LM) {
-            if (d <= row) {
-              S.D[row][row - d] = cur[t];
-              S.D[row - d][row] = cur[t];
-            } else if (d <= row + LNv) {
-              S.E[row][LNv + row - d] = cur[t];
+        // scatter this task's rows into E / D (an interior task without
+        // branches: every element goes to a selected address, out-of-window
+        // ones to junk)
+        double* const S0 = &S.E[0][0];
+        if constexpr (FULL) {
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const int idx = l + 64 * t, row = idx >> 5, d = idx & 31;
+            const bool inD = d <= row, inE = !inD && d <= row + NB;
+            const int a1 = inD ? SB_D0 + row * (NB + 1) + row - d
+                               : (inE ? row * (NB + 1) + NB + row - d : SB_JUNK);
+            const int a2 = inD ? SB_D0 + (row - d) * (NB + 1) + row : SB_JUNK;
+            S0[a1] = cur[t];
+            S0[a2] = cur[t];
+          }
+        } else {
+          for (int t = 0; t < 8; ++t) {
+            const int idx = l + 64 * t, row = idx >> 5, d = idx & 31;
+            if (row < LM) {
+              if (d <= row) {
+                S.D[row][row - d] = cur[t];
+                S.D[row - d][row] = cur[t];
+              } else if (d <= row + LNv) {
+                S.E[row][LNv + row - d] = cur[t];
+              }
             }
           }
         }
@@ -1028,13 +1048,24 @@ __global__ __launch_bounds__(SB_W * 64) void k_sb2st(double* band, int n, double
           wave_sync();
         }
         // store the rows back, then publish the task
-        for (int t = 0; t < 8; ++t) {
-          const int idx = l + 64 * t, row = idx >> 5, d = idx & 31;
-          if (row < LM) {
-            if (d <= row)
-              Bm[(int64_t)(q0 + row) * BW + d] = S.D[row][row - d];
-            else if (d <= row + LNv)
-              Bm[(int64_t)(q0 + row) * BW + d] = S.E[row][LNv + row - d];
+        if constexpr (FULL) {
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const int idx = l + 64 * t, row = idx >> 5, d = idx & 31;
+            const bool inD = d <= row;
+            const int a1 = inD ? SB_D0 + row * (NB + 1) + row - d : row * (NB + 1) + NB + row - d;
+            const double v = S0[d <= row + NB ? a1 : SB_JUNK];
+            if (d <= row + NB) Bm[(int64_t)(q0 + row) * BW + d] = v;
+          }
+        } else {
+          for (int t = 0; t < 8; ++t) {
+            const int idx = l + 64 * t, row = idx >> 5, d = idx & 31;
+            if (row < LM) {
+              if (d <= row)
+                Bm[(int64_t)(q0 + row) * BW + d] = S.D[row][row - d];
+              else if (d <= row + LNv)
+                Bm[(int64_t)(q0 + row) * BW + d] = S.E[row][LNv + row - d];
+            }
           }
         }
         if (l < NB) S.pv[l] = S.v[l];
