@@ -331,7 +331,7 @@ int scao_eig_sy2sb_update(float* A, int64_t sA, int ldA, int mr, int batch, cons
 int scao_eig_band_finish(const float* A, int64_t stride, int n, int batch, const float* band,
                          int64_t bstride, float* orig, int64_t ostride, double* band64,
                          void* stream);
-/* Band -> tridiagonal by bulge chasing in float64 (one wavefront per
+/* Band -> tridiagonal by bulge chasing in float64 (one workgroup per
  * matrix) on band64; writes the diagonal d (n) and sub-diagonal e (n-1) at
  * d + i*n, e + i*n (float64). */
 int scao_eig_sb2st(double* band64, int n, int batch, double* d, double* e, void* stream);
@@ -353,6 +353,13 @@ int scao_eig_bisect(const double* d, const double* e, int n, int batch, int kq, 
 int64_t scao_eig_vectors_work(int n, int batch, int kq);
 int scao_eig_vectors(const float* orig, int64_t ostride, int n, int batch, int kq, double* w,
                      float* Z, int64_t zstride, void* work, void* stream);
+/* Back-transformation Z <- Q_0 (Q_1 (... Q_last Z)) of the eigenvectors with
+ * the stage-1 reflectors: panel p (c0 = 16p < n - 16) holds V_p explicitly in
+ * A[c0+16:n, c0:c0+16] of each matrix (as scao_eig_panel_qr leaves it) and
+ * T_p at T + (p*batch + i)*256; Q_p = I - V_p T_p V_p^T acts on rows c0+16..
+ * of Z (n x kq row-major float32 at Z + i*zstride), in place. */
+int scao_eig_back_transform(const float* A, int64_t stride, int n, int batch, const float* T,
+                            float* Z, int64_t zstride, int kq, void* stream);
 
 /* diag_ema = fp32(diag*rho) + fp32(alpha * g*g)  (1-D preconditioners). */
 int scao_diag_ema(const scao_task* tasks, int ntasks, const scao_param_desc* params,

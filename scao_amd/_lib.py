@@ -144,6 +144,7 @@ SIGNATURES = {
     "scao_eig_bisect": (_I, [_VP, _VP, _I, _I, _I, _VP, _VP, _VP, _VP]),
     "scao_eig_vectors_work": (_I64, [_I, _I, _I]),
     "scao_eig_vectors": (_I, [_VP, _I64, _I, _I, _I, _VP, _VP, _I64, _VP, _VP]),
+    "scao_eig_back_transform": (_I, [_VP, _I64, _I, _I, _VP, _VP, _I64, _I, _VP]),
     "scao_lookahead": (_I, [_VP, _I, _VP, ctypes.c_float, _VP]),
 }
 

@@ -1958,6 +1958,139 @@ __host__ __forceinline__ int inv_chunk(int n, int64_t nvec) {
   return (int)(nvec < c ? nvec : c);
 }
 
+// ------------------------------------------------------ back-transform ---
+// Z <- Q_0 (Q_1 (... Q_last Z)), Q_p = I - V_p T_p V_p^T: the stage-1 panels'
+// reflectors (V_p explicit in A[r0:n, c0:c0+16], r0 = c0 + 16, c0 = 16p; T_p
+// from the panel QR) applied to the eigenvectors, panel by panel from the
+// last, as the batched form Z[r0:] -= V_p (T_p (V_p^T Z[r0:])).  One
+// workgroup of 16 wavefronts per (matrix, 16 columns of Z): the slice stays
+// in registers for the whole pass, wavefront w holding row tiles w, w+16, ...
+// (16 rows each) in the MFMA output layout.  Per panel: each wavefront's
+// share G_w of G = V_p^T Z on MFMA (each tile's rows are the reduction index:
+// lane row 4(l/16)+r is k-step r) and its share T_p G_w of W = T_p G; the 16
+// shares summed in LDS in a fixed order by every lane for the four values it
+// needs; then Z -= V_p W on MFMA (reduction over the panel's 16 columns,
+// column 4(l/16)+s at k-step s, so a lane's four V values are one float4).
+// A panel's first row r0 is a multiple of 16, so tiles never straddle it.
+template <int ZT, bool EXACT>
+__global__ __launch_bounds__(1024) void k_back_transform(const float* __restrict__ A, int64_t sA,
+                                                         int n, int npan, const float* __restrict__ T,
+                                                         int64_t sT, float* Z, int64_t sZ, int kq,
+                                                         int nmat) {
+  __shared__ float Wp[2][16][256];
+  // blocks in groups of 8 matrices x the slices: a matrix's slices run close
+  // together in dispatch order and on one XCD (workgroups are dealt to the
+  // XCDs round-robin by linear index), so they share its V through that L2
+  const int nsl = (kq + 15) / 16, grp = blockIdx.x / (8 * nsl), rem = blockIdx.x % (8 * nsl);
+  const int mat = 8 * grp + rem % 8, z0 = 16 * (rem / 8);
+  if (mat >= nmat) return;
+  const int tid = threadIdx.x, w = tid >> 6, l = tid & 63, g = l >> 4, jj = l & 15;
+  const float* Am = A + (int64_t)mat * sA;
+  float* Zm = Z + (int64_t)mat * sZ;
+  const int nrt = (n + 15) / 16;
+  const bool colok = EXACT || z0 + jj < kq;   // EXACT: n % 16 == 0 and kq % 16 == 0
+  // V through a buffer resource over the matrix: 32-bit offsets (one register
+  // per address instead of two), and rows past n read as zero (out of range)
+  const __amdgpu_buffer_rsrc_t rs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)Am, (short)0, n * n * 4, 0x00020000);
+  const int n4 = 4 * n, t4 = 1024 * n;         // bytes per row, per 256 rows (16 tiles)
+  const int b1 = (16 * w + 4 * g) * n4 + 4 * jj;   // step 1: rows 16w+4g+r, column c0+jj
+  const int b2 = (16 * w + jj) * n4 + 16 * g;      // step 2: row 16w+jj, columns c0+4g..
+  v4f zr[ZT];
+#pragma unroll
+  for (int t = 0; t < ZT; ++t) {
+    const int tile = w + 16 * t;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * tile + 4 * g + r;
+      zr[t][r] = (tile < nrt && (EXACT || row < n) && colok) ? Zm[(int64_t)row * kq + z0 + jj] : 0.f;
+    }
+  }
+  for (int p = npan - 1; p >= 0; --p) {
+    const int c0 = 16 * p, ft = p + 1;
+    // the lane's offsets, opaque to the compiler: each tile's addresses are
+    // formed where they are used instead of being hoisted for the whole pass
+    int o1 = b1, o2 = b2;
+    asm volatile("" : "+v"(o1), "+v"(o2));
+    // T_p as the A operand of W_w = T G_w: lane (g, jj) supplies T[jj][4g + r]
+    // at k-step r (the permutation of G's rows in its partials below)
+    float ta[4];
+    {
+      const float* Tp = T + (int64_t)p * sT + (int64_t)mat * 256 + jj * 16 + 4 * g;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ta[r] = Tp[r];
+    }
+    // G partials: A[a][k] = V[row_k][c0 + a], B[k][b] = Z[row_k][b]
+    v4f acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < ZT; ++t) {
+      const int tile = w + 16 * t;
+      if (tile >= ft && tile < nrt) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float v = __builtin_bit_cast(
+              float, __builtin_amdgcn_raw_buffer_load_b32(rs, o1 + t * t4 + r * n4, 4 * c0, 0));
+          acc = mfma16(v, zr[t][r], acc);
+        }
+      }
+      if (t & 1) asm volatile("" ::: "memory");   // two tiles' loads in flight at most
+    }
+    // W = T G = sum over wavefronts of T G_w: this wavefront's share on MFMA
+    // (G_w holds G[4g + r][jj], the B operand of k-step r), partials to LDS
+    // (double-buffered by panel parity: one barrier per panel)
+    v4f wp = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wp = mfma16(ta[r], acc[r], wp);
+    float (*Wb)[256] = Wp[p & 1];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) Wb[w][(4 * g + r) * 16 + jj] = wp[r];
+    __syncthreads();
+    // Z -= V W: A[i][k] = V[tile row i][c0 + 4(l/16) + s], B[k][j] = W[4(l/16) + s][j]
+    float wb[4];
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      const int e = (4 * g + s4) * 16 + jj;
+      float x = Wb[0][e];
+#pragma unroll
+      for (int v = 1; v < 16; ++v) x += Wb[v][e];   // fixed order
+      wb[s4] = x;
+    }
+#pragma unroll
+    for (int t = 0; t < ZT; ++t) {
+      const int tile = w + 16 * t;
+      if (tile >= ft && tile < nrt) {
+        v4f va;
+        if (EXACT) {
+          va = __builtin_bit_cast(v4f, __builtin_amdgcn_raw_buffer_load_b128(rs, o2 + t * t4,
+                                                                              4 * c0, 0));
+        } else {
+#pragma unroll
+          for (int s4 = 0; s4 < 4; ++s4)
+            va[s4] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                   rs, o2 + t * t4 + 4 * s4, 4 * c0, 0));
+        }
+        v4f dv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) dv = mfma16(va[s4], wb[s4], dv);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) zr[t][r] -= dv[r];
+      }
+      if (t & 1) asm volatile("" ::: "memory");
+    }
+  }
+  float* Zs = Zm;                  // opaque: the store addresses are not kept live
+  asm volatile("" : "+s"(Zs));     // across the pass
+#pragma unroll
+  for (int t = 0; t < ZT; ++t) {
+    const int tile = w + 16 * t;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * tile + 4 * g + r;
+      if (tile < nrt && (EXACT || row < n) && colok) Zs[(int64_t)row * kq + z0 + jj] = zr[t][r];
+    }
+  }
+}
+
 }  // namespace
 
 // ------------------------------------------------------------- C ABI ---
@@ -2129,5 +2262,43 @@ extern "C" int scao_eig_vectors(const float* orig, int64_t ostride, int n, int b
   hipLaunchKernelGGL(k_vec_out, dim3((n + 63) / 64, (kq + 63) / 64, batch), dim3(256), 0, s, n, kq,
                      xall, Z, zstride);
   SCAO_LAUNCH_CHECK("scao_eig_vectors/out");
+  return SCAO_OK;
+}
+
+extern "C" int scao_eig_back_transform(const float* A, int64_t stride, int n, int batch,
+                                       const float* T, float* Z, int64_t zstride, int kq,
+                                       void* stream) {
+  SCAO_CHECK_ARG(A && T && Z, "scao_eig_back_transform: null pointer");
+  SCAO_CHECK_ARG(batch >= 0 && batch <= 65535 && n > 0 && n <= 4096 + NB && kq > 0 && kq <= n &&
+                     stride >= (int64_t)n * n && zstride >= (int64_t)n * kq,
+                 "scao_eig_back_transform: bad arguments n=%d kq=%d", n, kq);
+  const int npan = n > NB ? (n - NB + NB - 1) / NB : 0;   // panels c0 = 0, 16, .. < n - NB
+  if (batch == 0 || npan == 0) return SCAO_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int nrt = (n + 15) / 16, zt = (nrt + 15) / 16;
+  const int nsl = (kq + 15) / 16;   // 16-column slices of Z per matrix
+  const dim3 g((batch + 7) / 8 * 8 * nsl), b(1024);
+  const int64_t sT = (int64_t)batch * NB * NB;
+  const bool exact = n % 16 == 0 && kq % 16 == 0;
+#define SCAO_BT(ZT)                                                                         \
+  if (exact)                                                                                \
+    hipLaunchKernelGGL((k_back_transform<ZT, true>), g, b, 0, s, A, stride, n, npan, T, sT, Z, \
+                       zstride, kq, batch);                                                 \
+  else                                                                                      \
+    hipLaunchKernelGGL((k_back_transform<ZT, false>), g, b, 0, s, A, stride, n, npan, T, sT, Z, \
+                       zstride, kq, batch);
+  if (zt <= 2) {
+    SCAO_BT(2)
+  } else if (zt <= 4) {
+    SCAO_BT(4)
+  } else if (zt <= 8) {
+    SCAO_BT(8)
+  } else if (zt <= 16) {
+    SCAO_BT(16)
+  } else {
+    SCAO_BT(17)
+  }
+#undef SCAO_BT
+  SCAO_LAUNCH_CHECK("scao_eig_back_transform");
   return SCAO_OK;
 }

@@ -18,8 +18,10 @@ kernels of csrc/eig.hip and plain batched GEMMs (rocBLAS, through torch):
 2. ``scao_eig_band_finish`` / ``scao_eig_sb2st``: band -> tridiagonal;
 3. ``scao_eig_bisect``: the kq largest eigenvalues and the clamped sum;
 4. ``scao_eig_vectors``: eigenvectors of the band matrix;
-5. back-transformation Z <- Q_0 (Q_1 (... Q_last Z)): the panels' reflectors
-   merged BT_GROUP at a time into block reflectors, three GEMMs per block.
+5. back-transformation Z <- Q_0 (Q_1 (... Q_last Z)): ``scao_eig_back_transform``
+   applies the panels' reflectors from the last, each matrix's Z slices held in
+   registers for the whole pass (or, with BT_KERNEL off, the reflectors merged
+   BT_GROUP at a time into block reflectors, three GEMMs per block).
 """
 
 from __future__ import annotations
@@ -158,11 +160,17 @@ def topk_eigh(X: Tensor, kq: int):
     L.call("scao_eig_vectors", orig.data_ptr(), n * (NB + 1), n, B, kq, w.data_ptr(),
            Z.data_ptr(), n * kq, work.data_ptr(), s)
     del work
-    _back_transform(X, pcs, Tall, Z)
+    if BT_KERNEL:
+        if pcs:
+            L.call("scao_eig_back_transform", X.data_ptr(), n * n, n, B, Tall.data_ptr(),
+                   Z.data_ptr(), n * kq, kq, s)
+    else:
+        _back_transform(X, pcs, Tall, Z)
     return w, Z, total
 
 
-BT_GROUP = 8   # panels merged into one block reflector by the back-transformation
+BT_KERNEL = True   # the back-transformation in one kernel (scao_eig_back_transform)
+BT_GROUP = 8   # panels merged into one block reflector by the GEMM back-transformation
 
 
 def _back_transform(X: Tensor, pcs: list, Tall: Tensor, Z: Tensor) -> None:
