@@ -27,6 +27,7 @@ constexpr int GT = SCAO_GRAM_TILE;  // 128
 constexpr int KC = 32;              // K chunk
 constexpr int LP = GT + 4;          // padded LDS row of an operand chunk
 constexpr int SP = GT + 1;          // LDS row of the staged output tile
+constexpr bool GRAM_X6 = true;      // whole fp32 tiles on the bf16 matrix cores (gram_kloop_x6)
 
 // Operand chunks X[r0:r0+128][kb:kb+32], four 4-element loads per thread,
 // held in registers (raw, in the gradient's dtype) from chunk_load until
@@ -184,6 +185,126 @@ __device__ __forceinline__ void gram_kloop(const scao_gram_desc& D, int dim, int
   }
 }
 
+// The K loop for whole fp32 tiles on the bf16 matrix cores: fp32 products as
+// six bf16 MFMAs over three-way splits (mfma_x6), one v_mfma_f32_16x16x32
+// covering a whole 32-deep chunk (6 * 16 cycles per output tile against
+// 8 * 32 for the fp32 16x16x4 form).  The loader splits each operand value
+// once and stores the three bf16 planes row-major with k contiguous (pitch
+// XCP = 40: a lane's 8 consecutive k are one 16-byte read, and the 16 lanes
+// of a read hit disjoint bank quads); the chunk buffer is single (60 KB for
+// both operands, two workgroups per CU) with the next chunk's raw values held
+// in registers across the MFMAs.  Side 1 (X = G^T) loads four consecutive k
+// of one X row (four G rows at one column: coalesced across the lanes), so
+// every plane write is 8 bytes.
+constexpr int XCP = 40;
+constexpr int XPL = GT * XCP;        // bf16 per plane
+static_assert(2 * 3 * XPL * 2 <= 2 * 2 * KC * LP * 4, "x6 planes fit the operand LDS");
+
+template <int SIDE>
+__device__ __forceinline__ void chunk_load_x6(const scao_gram_desc& D, int r0, int kb,
+                                              v4f (&x)[4]) {
+  const int tid = threadIdx.x;
+  const float* g = (const float*)D.g;
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    if (SIDE == 0) {
+      // row tid/8 + 32h, k = kb + 4(tid%8) .. +3
+      const int i = r0 + tid / 8 + 32 * h, k = kb + (tid % 8) * 4;
+      x[h] = gld4(g + D.off + (int64_t)i * D.ld + k);
+    } else {
+      // X row i = tid % 128 (a G column), k = kb + 4(tid/128 + 2h) .. +3 (G rows)
+      const int i = r0 + tid % 128, k = kb + 4 * (tid / 128 + 2 * h);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) x[h][u] = g[D.off + (int64_t)(k + u) * D.ld + i];
+    }
+  }
+}
+
+template <int SIDE>
+__device__ __forceinline__ void chunk_store_x6(__bf16* P, const v4f (&x)[4]) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int h = 0; h < 4; ++h) {
+    const int row = SIDE == 0 ? tid / 8 + 32 * h : tid % 128;
+    const int k = SIDE == 0 ? (tid % 8) * 4 : 4 * (tid / 128 + 2 * h);
+    uint32_t pk[3][2];
+#pragma unroll
+    for (int u = 0; u < 4; u += 2) {
+      uint32_t v[2][3];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float f = x[h][u + e];
+        const __bf16 b0 = (__bf16)f;
+        const float r = f - (float)b0;
+        const __bf16 b1 = (__bf16)r;
+        const __bf16 b2 = (__bf16)(r - (float)b1);
+        v[e][0] = __builtin_bit_cast(uint16_t, b0);
+        v[e][1] = __builtin_bit_cast(uint16_t, b1);
+        v[e][2] = __builtin_bit_cast(uint16_t, b2);
+      }
+#pragma unroll
+      for (int pp = 0; pp < 3; ++pp) pk[pp][u / 2] = v[0][pp] | (v[1][pp] << 16);
+    }
+#pragma unroll
+    for (int pp = 0; pp < 3; ++pp)
+      *(v2u*)&P[pp * XPL + row * XCP + k] = v2u{pk[pp][0], pk[pp][1]};
+  }
+}
+
+template <int SIDE>
+__device__ __forceinline__ void gram_kloop_x6(const scao_gram_desc& D, int K, int i0, int j0,
+                                              bool diag, __bf16* Ap, __bf16* Bp, int wr, int wc,
+                                              v4f (&tot)[4][4]) {
+  const int l = threadIdx.x % 64, jj = l % 16, g = l / 16;
+  v4f acc[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b) acc[a][b] = tot[a][b] = v4f{0.f, 0.f, 0.f, 0.f};
+  v4f xa[4], xb[4];
+  chunk_load_x6<SIDE>(D, i0, 0, xa);
+  if (!diag) chunk_load_x6<SIDE>(D, j0, 0, xb);
+  const __bf16* Bq = diag ? Ap : Bp;
+  for (int kb = 0; kb < K; kb += KC) {
+    if (kb) __syncthreads();               // the previous chunk's planes are consumed
+    chunk_store_x6<SIDE>(Ap, xa);
+    if (!diag) chunk_store_x6<SIDE>(Bp, xb);
+    __syncthreads();
+    if (kb + KC < K) {                     // in flight during the MFMAs below
+      chunk_load_x6<SIDE>(D, i0, kb + KC, xa);
+      if (!diag) chunk_load_x6<SIDE>(D, j0, kb + KC, xb);
+    }
+    bf3 bo[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const __bf16* q = Bq + (wc + 16 * b + jj) * XCP + 8 * g;
+      bo[b].h = *(const v8bf*)q;
+      bo[b].m = *(const v8bf*)(q + XPL);
+      bo[b].l = *(const v8bf*)(q + 2 * XPL);
+    }
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const __bf16* q = Ap + (wr + 16 * a + jj) * XCP + 8 * g;
+      bf3 ao;
+      ao.h = *(const v8bf*)q;
+      ao.m = *(const v8bf*)(q + XPL);
+      ao.l = *(const v8bf*)(q + 2 * XPL);
+#pragma unroll
+      for (int b = 0; b < 4; ++b) acc[a][b] = mfma_x6(ao, bo[b], acc[a][b]);
+    }
+    if ((kb + KC) % FOLD == 0 || kb + KC >= K) {
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          tot[a][b] += acc[a][b];
+          acc[a][b] = v4f{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+  }
+  __syncthreads();                         // the planes' LDS is reused by the epilogue
+}
+
 // EMA update of the output tile rows r0.., columns c0.. from the product
 // tile staged in S (S[row][col], or S[col][row] when `tr`).  A tile inside
 // a factor with dim % 4 == 0 goes 4 elements per thread and pass (one 32-bit
@@ -279,7 +400,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   const bool whole = vec && K % KC == 0 && i0 + GT <= dim && j0 + GT <= dim;
 #define SCAO_GRAM_KLOOP(DT, SIDE) \
   gram_kloop<DT, SIDE>(D, dim, K, i0, j0, diag, vec, As, Bs, wr, wc, tot)
-  if (whole && D.dtype == SCAO_F32 && D.side == 0)
+  __bf16* Ap = (__bf16*)smem;
+  __bf16* Bp = Ap + 3 * XPL;
+  if (GRAM_X6 && whole && D.dtype == SCAO_F32 && D.side == 0)
+    gram_kloop_x6<0>(D, K, i0, j0, diag, Ap, Bp, wr, wc, tot);
+  else if (GRAM_X6 && whole && D.dtype == SCAO_F32)
+    gram_kloop_x6<1>(D, K, i0, j0, diag, Ap, Bp, wr, wc, tot);
+  else if (whole && D.dtype == SCAO_F32 && D.side == 0)
     SCAO_GRAM_KLOOP(SCAO_F32, 0);
   else if (whole && D.dtype == SCAO_F32)
     SCAO_GRAM_KLOOP(SCAO_F32, 1);
