@@ -219,6 +219,56 @@ def test_config_phase2_step(name, p0):
     assert gopt._global_norm_ema == pytest.approx(ref._global_norm_ema, rel=1e-6)
 
 
+@pytest.mark.parametrize("name", ["C3_llama1b", "C4_qwen3b", "C5_llama8b"])
+def test_projection_split_products(name):
+    """The bench's projection of whole fp32 strips (64, 128 and 256 rows of T
+    per task at k = 64, 128, 256) forms T = U_l^T G with each fp32 product as
+    six bf16 MFMAs over exact three-way splits.  Every block's T, read from
+    the step's workspace, is checked against float64 elementwise relative to
+    (|U_l|^T |G|): fp32-grade accuracy (bf16 products alone would be ~1e-3
+    off)."""
+    import numpy as np
+    from scao_amd import _lib as L
+    dev = _dev()
+    c, mats, adam, gscale, outl = _layer(name)
+    shapes = {**mats, **adam}
+    params = _params(shapes, 0)
+    groups = _groups(c, {k: params[k] for k in mats}, {k: params[k] for k in adam}, warmup=5)
+    ref = R.RefSCAO(groups, precond_freq=10 ** 9, blend_steps=5, min_precond_updates=1,
+                    **PROFILE)
+    _seed_state(ref, 41, True, torch.Generator().manual_seed(7))
+    gp, gopt = _to_gpu(ref, params, groups, dev)
+    grads = _grads(shapes, 1041, gscale, outl)
+    for k in shapes:
+        gp[k].grad = grads[k].to(dev)
+    gopt.step()
+    torch.cuda.synchronize()
+    ws = gopt._ws
+    scratch = ws._bufs["leaf_scratch"]
+    tab = np.frombuffer(ws.leaf_dev.cpu().numpy().tobytes(), dtype=L.LEAF_DESC)
+    owner = {}
+    for nm in mats:
+        for leaf, *_ in P.kron_leaves(gopt.state[gp[nm]]["preconditioner"]):
+            owner[id(leaf)] = nm
+    worst, nblk = 0.0, 0
+    for (leaf, r0, c0, pi), e in zip(ws.leaves, tab):
+        if not leaf.use_kronecker or id(leaf) not in owner:
+            continue
+        m, n, k = int(e["m"]), int(e["n"]), int(e["k"])
+        off = (int(e["T"]) - scratch.data_ptr()) // 4
+        T = scratch.view(torch.float32)[off:off + k * n].view(k, n).double().cpu()
+        G = grads[owner[id(leaf)]]
+        G = G.reshape(G.shape[0], -1)[r0:r0 + m, c0:c0 + n].double()
+        U = leaf.U_l.double().cpu()
+        exact = U.T @ G
+        scale = U.abs().T @ G.abs()
+        worst = max(worst, ((T - exact).abs() / scale.clamp_min(1e-30)).max().item())
+        nblk += 1
+    assert nblk > 0
+    report("projection_split_products", name, {"blocks": nblk, "max_rel_to_abs_sum": worst})
+    assert worst < 1e-5, worst
+
+
 @pytest.mark.parametrize("name", ["C2_gpt2s", "C3_llama1b", "C4_qwen3b", "C5_llama8b"])
 def test_config_phase1_step(name):
     """One Phase-1 (Adam(W)) step of the same layer from shared seeded moments."""
