@@ -1125,49 +1125,83 @@ def _task_rows(idx, a, b, slot) -> np.ndarray:
     return t
 
 
+_GRAM_TILE_IDX: dict = {}
+
+
+def _gram_tile_idx(nt: int):
+    """(a, b, slot) of a factor's Gram tasks for nt x nt tiles (lower tiles
+    with SYM_GRAM), cached per size."""
+    key = (nt, SYM_GRAM)
+    v = _GRAM_TILE_IDX.get(key)
+    if v is None:
+        if SYM_GRAM:
+            a, b = np.tril_indices(nt)
+        else:
+            a, b = np.divmod(np.arange(nt * nt), nt)
+        v = (a.astype(np.int32), b.astype(np.int32), (a * nt + b).astype(np.int32))
+        _GRAM_TILE_IDX[key] = v
+    return v
+
+
 def _gram_chunk(chunk, dev, s):
-    descs, tasks, req_tasks, scale_ptrs = [], [], [], []
-    staging = []
-    for leaf, g, off, ld in chunk:
-        for side in (0, 1):
-            dim = leaf.m if side == 0 else leaf.n
-            nt = (dim + L.GRAM_TILE - 1) // L.GRAM_TILE
-            e = np.zeros(1, dtype=L.GRAM_DESC)[0]
-            e["g"], e["off"], e["ld"] = g.data_ptr(), off, ld
-            e["rows"], e["cols"], e["side"] = leaf.m, leaf.n, side
-            e["dtype"] = L.DTYPE_CODE[g.dtype]
-            e["ntiles"] = nt * nt
-            e["rho"], e["alpha"] = leaf.rho, 1.0 - leaf.rho
-            di = len(descs)
-            if leaf.use_int8_ema:
-                q = leaf.L_ema_q if side == 0 else leaf.R_ema_q
-                x = torch.empty(dim * dim + nt * nt, dtype=torch.float32, device=dev)
-                staging.append(x)
-                e["q"] = q.data_ptr()
-                e["scale"] = leaf._scale.data_ptr() + 8 * side
-                e["ema"] = x.data_ptr()
-                e["amax"] = x.data_ptr() + 4 * dim * dim
-                scale_ptrs.append(leaf._scale.data_ptr() + 8 * side)
-                req_tasks.append(_task_rows(di, np.arange(_flat_chunks(dim * dim)), 0, -1))
-            else:
-                e["ema"] = (leaf.L_ema if side == 0 else leaf.R_ema).data_ptr()
-                scale_ptrs.append(0)
-            e["flags"] = L.GRAM_SYM if SYM_GRAM else 0
-            if SYM_GRAM:
-                a, b = np.tril_indices(nt)
-            else:
-                a, b = np.divmod(np.arange(nt * nt), nt)
-            tasks.append(_task_rows(di, a, b, a * nt + b))
-            descs.append(e)
-    dtab = np.array(descs, dtype=L.GRAM_DESC)
+    """Gram/EMA (and requantisation) launches for a chunk of (leaf, grad,
+    offset, ld): the descriptor table is filled column by column and the int8
+    staging buffers come from one allocation (per-record host work was most
+    of the refresh's idle GPU time before its first kernel)."""
+    recs = [(leaf, g, off, ld, side) for leaf, g, off, ld in chunk for side in (0, 1)]
+    n = len(recs)
+    dtab = np.zeros(n, dtype=L.GRAM_DESC)
+    dims = np.array([lf.m if sd == 0 else lf.n for lf, _, _, _, sd in recs], dtype=np.int64)
+    nts = (dims + L.GRAM_TILE - 1) // L.GRAM_TILE
+    int8 = np.array([lf.use_int8_ema for lf, *_ in recs], dtype=bool)
+    dtab["g"] = [g.data_ptr() for _, g, _, _, _ in recs]
+    dtab["off"] = [off for _, _, off, _, _ in recs]
+    dtab["ld"] = [ld for _, _, _, ld, _ in recs]
+    dtab["rows"] = [lf.m for lf, *_ in recs]
+    dtab["cols"] = [lf.n for lf, *_ in recs]
+    dtab["side"] = [sd for *_, sd in recs]
+    dtab["dtype"] = [L.DTYPE_CODE[g.dtype] for _, g, _, _, _ in recs]
+    dtab["ntiles"] = nts * nts
+    rho = np.array([lf.rho for lf, *_ in recs], dtype=np.float64)
+    dtab["rho"], dtab["alpha"] = rho, 1.0 - rho
+    dtab["flags"] = L.GRAM_SYM if SYM_GRAM else 0
+    # int8 sides: fp32 EMA staging (dim^2) and tile maxima (nt^2), one buffer
+    sizes = np.where(int8, dims * dims + nts * nts, 0)
+    starts = np.concatenate([[0], np.cumsum(sizes)[:-1]])
+    staging = torch.empty(max(int(sizes.sum()), 1), dtype=torch.float32, device=dev)
+    base = staging.data_ptr()
+    q_ptr = np.array([(lf.L_ema_q if sd == 0 else lf.R_ema_q).data_ptr() if q8 else 0
+                      for (lf, *_, sd), q8 in zip(recs, int8)], dtype=np.uint64)
+    scale_ptrs = np.array([lf._scale.data_ptr() + 8 * sd if q8 else 0
+                           for (lf, *_, sd), q8 in zip(recs, int8)], dtype=np.uint64)
+    ema_fp32 = np.array([0 if q8 else (lf.L_ema if sd == 0 else lf.R_ema).data_ptr()
+                         for (lf, *_, sd), q8 in zip(recs, int8)], dtype=np.uint64)
+    off8 = (base + 4 * starts).astype(np.uint64)
+    dtab["q"], dtab["scale"] = q_ptr, scale_ptrs
+    dtab["ema"] = np.where(int8, off8, ema_fp32)
+    dtab["amax"] = np.where(int8, off8 + (4 * dims * dims).astype(np.uint64), 0)
+    # tasks, in record order
+    parts = [_gram_tile_idx(int(nt)) for nt in nts]
+    cnt = np.array([len(p[0]) for p in parts], dtype=np.int64)
+    tt = np.empty((int(cnt.sum()), 4), dtype=np.int32)
+    tt[:, 0] = np.repeat(np.arange(n, dtype=np.int32), cnt)
+    tt[:, 1] = np.concatenate([p[0] for p in parts])
+    tt[:, 2] = np.concatenate([p[1] for p in parts])
+    tt[:, 3] = np.concatenate([p[2] for p in parts])
     dd = L.upload(dtab, dev)
-    tt = np.concatenate(tasks).view(L.TASK).reshape(-1)
+    tt = tt.view(L.TASK).reshape(-1)
     td = L.upload(tt, dev)
     _call("scao_gram_ema", td.data_ptr(), len(tt), dd.data_ptr(), s)
-    if req_tasks:
-        rt = np.concatenate(req_tasks).view(L.TASK).reshape(-1)
+    if int8.any():
+        nch = np.array([_flat_chunks(int(d * d)) if q8 else 0 for d, q8 in zip(dims, int8)],
+                       dtype=np.int64)
+        rt = np.empty((int(nch.sum()), 4), dtype=np.int32)
+        rt[:, 0] = np.repeat(np.arange(n, dtype=np.int32), nch)
+        rt[:, 1] = np.arange(len(rt), dtype=np.int64) - np.repeat(np.cumsum(nch) - nch, nch)
+        rt[:, 2], rt[:, 3] = 0, -1
+        rt = rt.view(L.TASK).reshape(-1)
         rd = L.upload(rt, dev)
-        sp = L.upload(np.array(scale_ptrs, dtype=np.uint64), dev)
+        sp = L.upload(scale_ptrs, dev)
         _call("scao_requant", rd.data_ptr(), len(rt), dd.data_ptr(), sp.data_ptr(), s)
     del staging   # stream-ordered reuse by the caching allocator is safe
 
