@@ -28,6 +28,7 @@
 // band matrix, so only stage 1's reflectors (kept in the panels of A) are
 // applied to them.
 #include <type_traits>
+#include <utility>
 
 #include "scao_common.hpp"
 
@@ -66,12 +67,20 @@ __device__ __forceinline__ void block_sum_f(float (&x)[NV], float (*red)[NV + 1]
   __syncthreads();
 }
 
+// f(integral_constant<int, J>) for J = 0, 1, .., in order
+template <class F, int... J>
+__device__ __forceinline__ void static_for(F& f, std::integer_sequence<int, J...>) {
+  (f(std::integral_constant<int, J>{}), ...);
+}
+
 // Householder QR of the panel A[r0:n, c0:c0+NB], r0 = c0 + NB, m = n - r0
 // rows (LAPACK geqr2 + larft, forward columnwise).  Thread t holds rows
 // t + NT h (h < RPT) of the panel.  Outputs: V (explicit, unit lower
 // trapezoidal) over the panel of A, T (NB x NB upper), R into the band.
-// NT threads (256 .. 1024) hold RPT rows each: fewer waves make the per-column
-// block reductions cheaper for short panels.
+// NT threads (256 or 512, at least NB * NB for the T write) hold RPT rows
+// each: few waves keep the per-column block reductions cheap and let two
+// workgroups share a CU (480 panels of 2032 rows: 19.7 -> 11.3 ms for a
+// sweep with 256-512 threads of 4 rows instead of 512-1024 of 2).
 template <int RPT, int NT>
 __global__ __launch_bounds__(NT) void k_panel_qr(float* A, int64_t stride, int n, int c0,
                                                    float* Tout, float* band, int64_t bstride) {
@@ -114,7 +123,12 @@ __global__ __launch_bounds__(NT) void k_panel_qr(float* A, int64_t stride, int n
   // the earlier reflectors' d_c for T alike), so a column costs one block
   // reduction.  Row j comes from thread j through LDS, double-buffered by
   // column parity (a slow thread may still read the previous column's).
-  for (int j = 0; j < kk; ++j) {
+  // The columns are expanded at compile time, so every P[h][j] index is a
+  // constant and the rows stay in registers (a runtime j puts them in
+  // scratch memory once they exceed about 32 floats).
+  auto column = [&](auto jc) {
+    constexpr int j = decltype(jc)::value;
+    if (j >= kk) return;
     float* rj = rowj[j & 1];
     if (tid == j) {
 #pragma unroll
@@ -165,7 +179,8 @@ __global__ __launch_bounds__(NT) void k_panel_qr(float* A, int64_t stride, int n
       taus[j] = tau;
       betas[j] = beta;
     }
-  }
+  };
+  static_for(column, std::make_integer_sequence<int, NB>{});
   __syncthreads();
   // T[0:j, j] = T[0:j, 0:j] (-tau_j d_j[0:j]), T[j][j] = tau_j, column by
   // column on one wavefront (lane i: row i; the same sums in the same order
@@ -2107,11 +2122,11 @@ extern "C" int scao_eig_panel_qr(float* A, int64_t stride, int n, int c0, int ba
   if (m <= 512)
     hipLaunchKernelGGL((k_panel_qr<2, 256>), dim3(batch), dim3(256), 0, s, Am, stride, n, c0, T, band, bstride);
   else if (m <= 1024)
-    hipLaunchKernelGGL((k_panel_qr<2, 512>), dim3(batch), dim3(512), 0, s, Am, stride, n, c0, T, band, bstride);
+    hipLaunchKernelGGL((k_panel_qr<4, 256>), dim3(batch), dim3(256), 0, s, Am, stride, n, c0, T, band, bstride);
   else if (m <= 2048)
-    hipLaunchKernelGGL((k_panel_qr<2, 1024>), dim3(batch), dim3(1024), 0, s, Am, stride, n, c0, T, band, bstride);
+    hipLaunchKernelGGL((k_panel_qr<4, 512>), dim3(batch), dim3(512), 0, s, Am, stride, n, c0, T, band, bstride);
   else
-    hipLaunchKernelGGL((k_panel_qr<4, 1024>), dim3(batch), dim3(1024), 0, s, Am, stride, n, c0, T, band, bstride);
+    hipLaunchKernelGGL((k_panel_qr<8, 512>), dim3(batch), dim3(512), 0, s, Am, stride, n, c0, T, band, bstride);
   SCAO_LAUNCH_CHECK("scao_eig_panel_qr");
   return SCAO_OK;
 }
