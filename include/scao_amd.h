@@ -283,12 +283,13 @@ int scao_eig_prep(const scao_task* tasks, int ntasks, const scao_prep_desc* desc
  * (scao/preconditioner.py:413-426), which need every eigenvalue (for
  * utils.adaptive_rank, scao/utils.py:121-151) but only the top-k_max
  * eigenvectors.  Two-stage: the dense matrix is reduced to a band of
- * SCAO_EIG_BAND sub-diagonals by block Householder transformations (panel QR
- * here, trailing two-sided updates as plain batched GEMMs by the caller),
- * the band to tridiagonal by bulge chasing, eigenvalues by bisection on the
- * tridiagonal (float64 Sturm counts), eigenvectors by float64 inverse
- * iteration on the band matrix, back-transformed by the caller's GEMMs with
- * the stored block reflectors.  Matrix i of a batch starts at base +
+ * SCAO_EIG_BAND sub-diagonals by block Householder transformations (panel QR,
+ * panel correction and lower-triangle trailing updates here; the first panel
+ * product and the last panel's in-band update are batched GEMMs by the
+ * caller), the band to tridiagonal by bulge chasing, eigenvalues by bisection
+ * on the tridiagonal (float64 Sturm counts), eigenvectors by float64 inverse
+ * iteration on the band matrix, back-transformed with the stored block
+ * reflectors (scao_eig_back_transform).  Matrix i of a batch starts at base +
  * i * stride (elements); every matrix of one call has the same dim n. */
 #define SCAO_EIG_BAND 16
 #define SCAO_EIG_BANDW (2 * SCAO_EIG_BAND + 1)  /* band row pitch: diagonals 0..2b */
