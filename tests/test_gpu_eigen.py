@@ -123,12 +123,14 @@ def test_topk_eigh(n, kq, kind):
         assert res["proj"] < 1e-5, res
 
 
-@pytest.mark.parametrize("n,kq", [(40, 3), (100, 20), (300, 64), (512, 16), (2048, 64)])
+@pytest.mark.parametrize("n,kq", [(40, 3), (100, 20), (300, 64), (512, 16), (1000, 40), (2000, 50),
+                                  (2048, 64)])
 def test_back_transform_kernel_matches_block_reflectors(n, kq):
     """scao_eig_back_transform (panel reflectors applied in one kernel) against
     the block-reflector GEMM form on the same stage-1 output and vectors,
-    including sizes that are not multiples of 16 and a batch that does not
-    fill a group of 8 matrices."""
+    including sizes and ranks that are not multiples of 16 (the masked
+    instantiations, up to the 8-panel-group one at n = 2000) and a batch that
+    does not fill a group of 8 matrices."""
     from scao_amd import _lib as L
     from scao_amd import eigen
     dev = _dev()
