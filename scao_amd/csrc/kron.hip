@@ -870,24 +870,27 @@ __device__ __forceinline__ void apply_wide(const scao_leaf_desc& L, const scao_p
   const int kk = l / 16;
   const int jl = j0 + 64 * w + 4 * (l % 16);
 
-  // 1) prefetch.  A fused filter's EMA goes first: its keep bits are taken
-  // as soon as it lands (before the back-projection), which frees its
-  // registers for the rest of the tile.
+  // 1) the streaming loads (issued in step 2: after the back-projection's
+  // operands when k = 64, before them otherwise).  A fused filter's EMA goes
+  // first: its keep bits are taken as soon as the back-projection allows,
+  // which frees its registers for the rest of the tile.
   v4f gr[4], gm[4], mm[4], vv[4], dd[4], pp[4], par[4];
   int64_t e[4];
   const bool fmask = GF32 && (P.flags & SCAO_PF_FMASK);
+  auto load_elem = [&]() {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    e[r] = L.off + (int64_t)(i0 + 4 * kk + r) * L.ld + jl;
-    if (fmask) gm[r] = gld4_nt(P.fema + e[r]);
-    gr[r] = gld4_nt((const float*)P.graw + e[r]);
-    if (GF32 && !fused_mgrad(P)) gm[r] = gld4_nt((const float*)P.g + e[r]);
-    mm[r] = gld4_nt(P.exp_avg + e[r]);
-    vv[r] = gld4_nt(P.exp_avg_sq + e[r]);
-    dd[r] = gld4_nt(P.exp_avg_diff + e[r]);
-    pp[r] = gld4_nt(P.prev_grad + e[r]);
-    if (!LARS) par[r] = gld4_nt((const float*)P.p + e[r]);
-  }
+    for (int r = 0; r < 4; ++r) {
+      e[r] = L.off + (int64_t)(i0 + 4 * kk + r) * L.ld + jl;
+      if (fmask) gm[r] = gld4_nt(P.fema + e[r]);
+      gr[r] = gld4_nt((const float*)P.graw + e[r]);
+      if (GF32 && !fused_mgrad(P)) gm[r] = gld4_nt((const float*)P.g + e[r]);
+      mm[r] = gld4_nt(P.exp_avg + e[r]);
+      vv[r] = gld4_nt(P.exp_avg_sq + e[r]);
+      dd[r] = gld4_nt(P.exp_avg_diff + e[r]);
+      pp[r] = gld4_nt(P.prev_grad + e[r]);
+      if (!LARS) par[r] = gld4_nt((const float*)P.p + e[r]);
+    }
+  };
 
   // 2) corr = W U_r^T; reduction index c + 4*(l/16) + s for both operands
   v4f acc[4];
@@ -895,34 +898,63 @@ __device__ __forceinline__ void apply_wide(const scao_leaf_desc& L, const scao_p
   for (int t = 0; t < 4; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
   const float* __restrict__ wrow = L.W + (int64_t)(i0 + l % 16) * k + 4 * kk;
   const float* __restrict__ urow = L.Ur + (int64_t)jl * k + 4 * kk;
-  // operands of chunk c+16 are loaded while chunk c runs on MFMA
-  v4f a = gld4(wrow), b[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) b[t] = gld4(urow + (int64_t)t * k);
   uint32_t keep = 0xffffu;   // bit 4r+t: the filter keeps element (r, t)
-  if (fmask) {
-    const float thr = *P.fthr;
-    keep = 0u;
+  auto take_keep = [&]() {
+    if (fmask) {
+      const float thr = *P.fthr;
+      keep = 0u;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
+      for (int r = 0; r < 4; ++r)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) keep |= (gm[r][t] >= thr ? 1u : 0u) << (4 * r + t);
-  }
-  for (int c = 0; c < k; c += 16) {
-    const bool more = c + 16 < k;
-    v4f an = a, bn[4] = {b[0], b[1], b[2], b[3]};
-    if (more) {
-      an = gld4(wrow + c + 16);
-#pragma unroll
-      for (int t = 0; t < 4; ++t) bn[t] = gld4(urow + (int64_t)t * k + c + 16);
+        for (int t = 0; t < 4; ++t) keep |= (gm[r][t] >= thr ? 1u : 0u) << (4 * r + t);
     }
+  };
+  if (k == 64) {
+    // Every operand of the back-projection goes out before the streaming
+    // loads and the four chunks run straight-line, so each MFMA waits for its
+    // own operands only, not for the streaming loads queued behind them (the
+    // vector-memory counter completes in order).  The tile then takes about
+    // 170 registers, two waves per SIMD: faster than the streaming loads
+    // first at either two or three waves per SIMD (the same sums in the same
+    // order).
+    v4f A4[4], B4[4][4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s)
+    for (int d = 0; d < 4; ++d) {
+      A4[d] = gld4(wrow + 16 * d);
 #pragma unroll
-      for (int t = 0; t < 4; ++t) acc[t] = mfma16(a[s], b[t][s], acc[t]);
-    a = an;
+      for (int t = 0; t < 4; ++t) B4[d][t] = gld4(urow + (int64_t)t * 64 + 16 * d);
+    }
+    load_elem();
 #pragma unroll
-    for (int t = 0; t < 4; ++t) b[t] = bn[t];
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = mfma16(A4[c][s], B4[c][t][s], acc[t]);
+    take_keep();
+  } else {
+    load_elem();
+    // operands of chunk c+16 are loaded while chunk c runs on MFMA
+    v4f a = gld4(wrow), b[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) b[t] = gld4(urow + (int64_t)t * k);
+    take_keep();
+    for (int c = 0; c < k; c += 16) {
+      const bool more = c + 16 < k;
+      v4f an = a, bn[4] = {b[0], b[1], b[2], b[3]};
+      if (more) {
+        an = gld4(wrow + c + 16);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) bn[t] = gld4(urow + (int64_t)t * k + c + 16);
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) acc[t] = mfma16(a[s], b[t][s], acc[t]);
+      a = an;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) b[t] = bn[t];
+    }
   }
 
   // 3) elementwise tail
