@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define SCAO_ABI_VERSION 9
+#define SCAO_ABI_VERSION 10
 
 enum scao_status { SCAO_OK = 0, SCAO_ERR_INVALID = 1, SCAO_ERR_HIP = 2 };
 enum scao_dtype { SCAO_F32 = 0, SCAO_BF16 = 1, SCAO_F16 = 2 };
@@ -172,8 +172,9 @@ int scao_fused_kronecker_precond(const float* U_l, const float* s_l_inv4, const 
  * k*n + k*k + m*k floats must fit in it (m = n = 4096 at k = 256 does); larger
  * sizes are rejected with SCAO_ERR_INVALID.  Every call on one GPU shares that
  * GPU's array: calls on one stream are ordered, but calls that overlap on one
- * GPU (two streams, two threads) race.  Results are identical to
- * scao_fused_kronecker_precond's. */
+ * GPU (two streams, two threads) race.  The array used is the current
+ * device's; a non-null stream must belong to that device (else
+ * SCAO_ERR_INVALID).  Results are identical to scao_fused_kronecker_precond's. */
 #define SCAO_NOALLOC_SCRATCH_BYTES (16u << 20)
 int scao_fused_kronecker_precond_noalloc(const float* U_l, const float* s_l_inv4,
                                          const float* U_r, const float* s_r_inv4,
@@ -278,6 +279,30 @@ typedef struct scao_prep_desc {
 } scao_prep_desc;
 int scao_eig_prep(const scao_task* tasks, int ntasks, const scao_prep_desc* descs,
                   int ndescs, void* stream);
+/* Exactly diagonal eigh inputs (scao/preconditioner.py:413-426).  On a matrix
+ * whose off-diagonal entries are all zero, LAPACK's syevd (torch's CPU eigh)
+ * returns the diagonal values, ordered by its divide-and-conquer selection
+ * sort (for i = 0..n-2: k = first position of the minimum of d[i..n-1], ties
+ * keeping i; swap d[i], d[k] and columns i, k of the identity), and the
+ * eigenvectors +e_j in that order.  With many tied values (an int8 EMA that
+ * kept only its diagonal codes) that order decides which unit vectors are the
+ * top k, so these two entry points reproduce it instead of solving.
+ *
+ * scao_eig_offdiag: flags[i] = 1 if descriptor i's EMA (int8 codes when q is
+ * set, else the fp32 ema) has a non-zero off-diagonal entry, else 0.  Only q,
+ * ema and dim are read; max_dim >= every dim (a larger one is flagged 1);
+ * codes = 1 when every descriptor has codes (sizes the grid for 4 codes per
+ * load).  flags: ndescs device ints, cleared by the call. */
+int scao_eig_offdiag(const scao_prep_desc* descs, int ndescs, int max_dim, int codes, int* flags,
+                     void* stream);
+/* scao_eig_diag: the kq largest eigenpairs of each descriptor's eigh input X
+ * (as scao_eig_prep forms it, shift written to *shift), all of dimension n
+ * (1 <= n <= 4096 + SCAO_EIG_BAND, kq <= n), for inputs scao_eig_offdiag
+ * flagged 0: w[i*kq + j] (double, descending: the reference's flip), U + i *
+ * ustride (n x kq row-major, column j a unit vector) and total[i] = sum of
+ * max(X_jj, 0) (double).  The out field is not used. */
+int scao_eig_diag(const scao_prep_desc* descs, int ndescs, int n, int kq, double* w, float* U,
+                  int64_t ustride, double* total, void* stream);
 /* ---- eigen stage: top-k eigenpairs of a batch of symmetric matrices -----
  * Replaces the torch.linalg.eigh calls of _update_eigenfactors
  * (scao/preconditioner.py:413-426), which need every eigenvalue (for
@@ -290,7 +315,10 @@ int scao_eig_prep(const scao_task* tasks, int ntasks, const scao_prep_desc* desc
  * on the tridiagonal (float64 Sturm counts), eigenvectors by float64 inverse
  * iteration on the band matrix, back-transformed with the stored block
  * reflectors (scao_eig_back_transform).  Matrix i of a batch starts at base +
- * i * stride (elements); every matrix of one call has the same dim n. */
+ * i * stride (elements); every matrix of one call has the same dim n.  Every
+ * scao_eig_* entry point below takes 1 <= n <= 4096 + SCAO_EIG_BAND (and
+ * sy2sb_update mr in that range) and returns SCAO_ERR_INVALID otherwise; the
+ * refresh sends larger factors to the library solver. */
 #define SCAO_EIG_BAND 16
 #define SCAO_EIG_BANDW (2 * SCAO_EIG_BAND + 1)  /* band row pitch: diagonals 0..2b */
 /* Householder QR of the panel A[c0+b:n, c0:c0+b] of every matrix (A row-major,

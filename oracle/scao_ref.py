@@ -130,6 +130,41 @@ def matrix_power_neg_quarter(A: Tensor, eps: float = 1e-8) -> Tensor:
     return (V * w.pow(-0.25).unsqueeze(0)) @ V.T
 
 
+def lapack_diagonal_order(d) -> list:
+    """The column order torch.linalg.eigh (LAPACK syevd) gives diag(d).
+
+    The reference's eigh (scao/preconditioner.py:414, 423) is LAPACK's ssyevd
+    on the CPU (MKL here).  On a matrix whose off-diagonal entries are all
+    zero it does no arithmetic: the tridiagonal reduction's reflectors are
+    identities, the tridiagonal is d with a zero off-diagonal, and divide and
+    conquer (xSTEDC, or xSTEQR below 26 rows) ends with its selection sort of
+    the eigenvalues, swapping eigenvector columns with them (LAPACK 3.x
+    dstedc.f, "Use Selection Sort to minimize swaps of eigenvectors"):
+
+        for i = 0 .. n-2:  k = i, p = d[i]
+                           for j = i+1 .. n-1: if d[j] < p: k, p = j, d[j]
+                           if k != i: swap d[i], d[k] and columns i, k
+
+    Returns perm with column j of the eigenvector matrix = e_{perm[j]} (sign
+    +1) and eigenvalue j = d[perm[j]], ascending.  Tied values (many, for an
+    int8 EMA that kept only its diagonal codes) end up in the order this
+    sort leaves them, which is not a stable order.  Pinned against
+    torch.linalg.eigh in tests/test_oracle_golden.py and by the reference's
+    own diagonal refreshes (golden diag_int8).  The inner scan is numpy's
+    argmin, which returns the first position of the minimum: the same k as
+    the strict < scan from d[i]."""
+    import numpy as np
+    v = np.asarray(d, dtype=np.float64).copy()
+    n = v.size
+    perm = np.arange(n)
+    for i in range(n - 1):
+        k = i + int(np.argmin(v[i:]))
+        if k != i:
+            v[i], v[k] = v[k], v[i]
+            perm[i], perm[k] = perm[k], perm[i]
+    return perm.tolist()
+
+
 # ---------------------------------------------------------------------------
 # operator fallbacks  (reference scao/cuda/__init__.py:78-142)
 # ---------------------------------------------------------------------------

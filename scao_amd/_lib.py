@@ -21,7 +21,7 @@ import torch  # noqa: F401  -- loads torch's HIP runtime before ours
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("SCAO_AMD_LIB", os.path.join(HERE, "_lib", "libscao_amd.so"))
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 SLOT_WIDTH = 3
 FLAT_CHUNK = 4096
 PROJ_COLS = 256
@@ -131,6 +131,8 @@ SIGNATURES = {
     "scao_gram_ema": (_I, [_VP, _I, _VP, _VP]),
     "scao_requant": (_I, [_VP, _I, _VP, _VP, _VP]),
     "scao_eig_prep": (_I, [_VP, _I, _VP, _I, _VP]),
+    "scao_eig_offdiag": (_I, [_VP, _I, _I, _I, _VP, _VP]),
+    "scao_eig_diag": (_I, [_VP, _I, _I, _I, _VP, _VP, _I64, _VP, _VP]),
     "scao_diag_ema": (_I, [_VP, _I, _VP, _VP, _VP]),
     "scao_sparse_filter": (_I, [_VP, _I, _VP, _I, _VP]),
     "scao_eig_panel_qr": (_I, [_VP, _I64, _I, _I, _I, _VP, _VP, _I64, _VP]),

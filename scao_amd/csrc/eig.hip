@@ -2135,7 +2135,7 @@ extern "C" int scao_eig_sy2sb_panel_w(float* A, int64_t sA, int n, int c0, int b
                                       const float* Y, const float* T, float* W, int strip,
                                       void* stream) {
   SCAO_CHECK_ARG(A && Y && T && W, "scao_eig_sy2sb_panel_w: null pointer");
-  SCAO_CHECK_ARG(batch >= 0 && n > 0 && c0 >= 0 && c0 % NB == 0 && c0 + NB < n &&
+  SCAO_CHECK_ARG(batch >= 0 && n > 0 && n <= 4096 + NB && c0 >= 0 && c0 % NB == 0 && c0 + NB < n &&
                      sA >= (int64_t)n * n && (!strip || c0 + 2 * NB <= n),
                  "scao_eig_sy2sb_panel_w: bad arguments n=%d c0=%d", n, c0);
   if (batch == 0) return SCAO_OK;
@@ -2156,7 +2156,7 @@ extern "C" int scao_eig_sy2sb_update(float* A, int64_t sA, int ldA, int mr, int 
                                      int64_t sW, int ldW, const float* Vn, int64_t sVn, int ldVn,
                                      float* Y, int64_t sY, void* work, void* stream) {
   SCAO_CHECK_ARG(A && V && W, "scao_eig_sy2sb_update: null pointer");
-  SCAO_CHECK_ARG(batch >= 0 && batch <= 65535 && mr >= 0 && ldA >= mr && ldV >= 16 && ldW >= 16 &&
+  SCAO_CHECK_ARG(batch >= 0 && batch <= 65535 && mr >= 0 && mr <= 4096 + NB && ldA >= mr && ldV >= 16 && ldW >= 16 &&
                      (!Vn || (ldVn >= 16 && Y && work && sY >= (int64_t)mr * 16)),
                  "scao_eig_sy2sb_update: bad arguments mr=%d batch=%d", mr, batch);
   if (batch == 0 || mr == 0) return SCAO_OK;
@@ -2189,7 +2189,7 @@ extern "C" int scao_eig_band_finish(const float* A, int64_t stride, int n, int b
                                     const float* band, int64_t bstride, float* orig,
                                     int64_t ostride, double* band64, void* stream) {
   SCAO_CHECK_ARG(A && band && orig && band64, "scao_eig_band_finish: null pointer");
-  SCAO_CHECK_ARG(batch >= 0 && n > 0 && stride >= (int64_t)n * n && bstride >= (int64_t)n * BW &&
+  SCAO_CHECK_ARG(batch >= 0 && n > 0 && n <= 4096 + NB && stride >= (int64_t)n * n && bstride >= (int64_t)n * BW &&
                      ostride >= (int64_t)n * OW,
                  "scao_eig_band_finish: bad arguments");
   if (batch == 0) return SCAO_OK;
@@ -2202,7 +2202,7 @@ extern "C" int scao_eig_band_finish(const float* A, int64_t stride, int n, int b
 extern "C" int scao_eig_sb2st(double* band64, int n, int batch, double* d, double* e,
                               void* stream) {
   SCAO_CHECK_ARG(band64 && d && e, "scao_eig_sb2st: null pointer");
-  SCAO_CHECK_ARG(batch >= 0 && n > 0, "scao_eig_sb2st: bad arguments");
+  SCAO_CHECK_ARG(batch >= 0 && n > 0 && n <= 4096 + NB, "scao_eig_sb2st: bad arguments n=%d", n);
   if (batch == 0) return SCAO_OK;
   hipLaunchKernelGGL(k_sb2st, dim3(batch), dim3(SB_W * 64), 0, (hipStream_t)stream, band64, n, d,
                      e);
@@ -2219,7 +2219,8 @@ extern "C" int64_t scao_eig_bisect_work(int n, int batch) {
 extern "C" int scao_eig_bisect(const double* d, const double* e, int n, int batch, int kq, double* w,
                                double* total, void* work, void* stream) {
   SCAO_CHECK_ARG(d && e && w && total && work, "scao_eig_bisect: null pointer");
-  SCAO_CHECK_ARG(batch >= 0 && n > 0 && kq > 0 && kq <= n, "scao_eig_bisect: bad arguments");
+  SCAO_CHECK_ARG(batch >= 0 && n > 0 && n <= 4096 + NB && kq > 0 && kq <= n,
+                 "scao_eig_bisect: bad arguments n=%d kq=%d", n, kq);
   if (batch == 0) return SCAO_OK;
   hipStream_t s = (hipStream_t)stream;
   double* wall = (double*)work;
@@ -2253,7 +2254,7 @@ extern "C" int64_t scao_eig_vectors_work(int n, int batch, int kq) {
 extern "C" int scao_eig_vectors(const float* orig, int64_t ostride, int n, int batch, int kq,
                                 double* w, float* Z, int64_t zstride, void* work, void* stream) {
   SCAO_CHECK_ARG(orig && w && Z && work, "scao_eig_vectors: null pointer");
-  SCAO_CHECK_ARG(batch >= 0 && n > 0 && kq > 0 && kq <= n && ostride >= (int64_t)n * OW &&
+  SCAO_CHECK_ARG(batch >= 0 && n > 0 && n <= 4096 + NB && kq > 0 && kq <= n && ostride >= (int64_t)n * OW &&
                      zstride >= (int64_t)n * kq,
                  "scao_eig_vectors: bad arguments");
   if (batch == 0) return SCAO_OK;

@@ -609,6 +609,189 @@ __global__ __launch_bounds__(256) void k_eig_prep(const scao_task* __restrict__ 
   }
 }
 
+// ---- exactly diagonal eigh inputs -------------------------------------
+// When every off-diagonal entry of a factor is zero, LAPACK's syevd (torch's
+// CPU eigh) does no arithmetic on it: the tridiagonal reduction's reflectors
+// are all identities, so the tridiagonal is the diagonal itself with zero
+// off-diagonal, and divide and conquer (stedc; steqr below 26 rows) only
+// orders it.  That ordering is stedc's selection sort: for i = 0 .. n-2, k is
+// the first position of the minimum of d[i..n-1] (a strict < scan starting
+// from d[i], so k = i when d[i] ties the minimum), then d[i] <-> d[k] and
+// columns i <-> k of the identity are swapped.  The eigenvalues are the
+// diagonal values exactly and the eigenvectors +e_j.  Ties are common here: an
+// int8 EMA of small gradients keeps only its diagonal codes, a handful of
+// distinct values over thousands of rows, and the order the sort leaves them
+// in decides which unit vectors the top k are.
+
+constexpr int OFFDIAG_WORDS = 4096;   // 32-bit words (16 KB of int8 codes) per block
+constexpr int DIAG_MAX = 4096 + 16;   // largest factor the diagonal path takes
+
+// flags[f] |= 1 when factor f has a non-zero off-diagonal entry (int8 code or
+// fp32 value).  Grid (chunks, factors); a block covers `per` elements of one
+// factor, a 32-bit word of codes (or one float) per thread and iteration.
+// The flags must be zero beforehand.
+__global__ __launch_bounds__(256) void k_eig_offdiag(const scao_prep_desc* __restrict__ descs,
+                                                     int max_dim, int per,
+                                                     int* __restrict__ flags) {
+  const scao_prep_desc D = descs[blockIdx.y];
+  const int dim = D.dim;
+  if (dim > max_dim) {   // not covered by the grid: take the general path
+    if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(flags + blockIdx.y, 1);
+    return;
+  }
+  const int64_t n = (int64_t)dim * dim;
+  const int64_t e0 = (int64_t)blockIdx.x * per;
+  if (e0 >= n) return;
+  const int64_t e1 = e0 + per < n ? e0 + per : n;
+  const bool vec = D.q ? ((uintptr_t)D.q & 3) == 0 : true;
+  bool any = false;
+  if (D.q && vec) {
+    for (int64_t e = e0 + 4 * threadIdx.x; e < e1 && !any; e += 4 * 256) {
+      if (e + 4 <= e1) {
+        const uint32_t w = gld1((const uint32_t*)(D.q + e));
+        if (w == 0) continue;
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if ((w >> (8 * t)) & 0xffu) {
+            const int64_t x = e + t;
+            any |= x / dim != x % dim;
+          }
+      } else {
+        for (int64_t x = e; x < e1; ++x) any |= D.q[x] != 0 && x / dim != x % dim;
+      }
+    }
+  } else {
+    for (int64_t x = e0 + threadIdx.x; x < e1 && !any; x += 256) {
+      const bool nz = D.q ? D.q[x] != 0 : D.ema[x] != 0.f;
+      any |= nz && x / dim != x % dim;
+    }
+  }
+  if (__syncthreads_or(any) && threadIdx.x == 0) atomicOr(flags + blockIdx.y, 1);
+}
+
+__global__ __launch_bounds__(256) void k_flags_clear(int* flags, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) flags[i] = 0;
+}
+
+// Eigenpairs of an exactly diagonal eigh input, one block per factor: the
+// diagonal of X = deq / fp32(bias) + shift as k_eig_prep forms it (the shift
+// from k_eig_trace), ordered by the selection sort above, then flipped to
+// descending order as the reference does (scao/preconditioner.py:418-426).
+// Writes w[j] (double) and column j of U (n x kq, row-major) = e_{r_j} for the
+// kq largest, and total = sum of max(d, 0) in double.
+//
+// Each thread owns the positions p = tid (mod 256).  A step scans the owned
+// positions >= i for the first minimum (increasing p, strict <), reduces
+// (value, position) over the block (smaller value, then smaller position: the
+// first position of the minimum), and the owner of the winning position k
+// records it and moves position i's value and index into k.  Position i is
+// never read or written again after step i, and position k is only touched
+// by its owner, so one barrier per step suffices (the reduction slots
+// alternate between two buffers).
+__global__ __launch_bounds__(256) void k_eig_diag(const scao_prep_desc* __restrict__ descs, int dim,
+                                                  int kq, double* __restrict__ w, float* __restrict__ U,
+                                                  int64_t ustride, double* __restrict__ total) {
+  __shared__ float val[DIAG_MAX];
+  __shared__ int idx[DIAG_MAX];
+  __shared__ int top[DIAG_MAX];   // top[j]: row of the unit vector in column j
+  __shared__ float rv[2][4];
+  __shared__ int rp[2][4];
+  __shared__ double red[4];
+  const int f = blockIdx.x;
+  const scao_prep_desc D = descs[f];
+  const int n = D.dim;
+  if (n != dim || n < 1 || n > DIAG_MAX || kq > n) return;   // outside the call's contract
+  const int tid = threadIdx.x, lane = tid % 64, wv = tid / 64;
+  const float sf = D.q ? (float)(*D.scale) : 0.f;
+  const float eps = *D.shift;
+  double pos = 0.0;
+  for (int i = tid; i < n; i += 256) {
+    const float y = prep_val(D, sf, (int64_t)i * n + i) + eps;
+    val[i] = y;
+    idx[i] = i;
+    pos += y > 0.f ? (double)y : 0.0;
+  }
+  double acc[1] = {pos};
+  block_sum<1>(acc, red);   // ends with a barrier: val/idx are complete
+  if (tid == 0) total[f] = acc[0];
+  double* wf = w + (int64_t)f * kq;
+  for (int i = 0; i + 1 < n; ++i) {
+    // first owned position >= i
+    const int r = i % 256;
+    int p = i - r + tid + (tid < r ? 256 : 0);
+    float bv = INFINITY;
+    int bp = n;
+    if (p < n) {
+      bv = val[p];
+      bp = p;
+      for (p += 256; p < n; p += 256) {
+        const float v = val[p];
+        if (v < bv) {
+          bv = v;
+          bp = p;
+        }
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int op = __shfl_xor(bp, o, 64);
+      if (ov < bv || (ov == bv && op < bp)) {
+        bv = ov;
+        bp = op;
+      }
+    }
+    const int b = i & 1;
+    if (lane == 0) {
+      rv[b][wv] = bv;
+      rp[b][wv] = bp;
+    }
+    __syncthreads();
+    float kv = rv[b][0];
+    int k = rp[b][0];
+#pragma unroll
+    for (int q = 1; q < 4; ++q)
+      if (rv[b][q] < kv || (rv[b][q] == kv && rp[b][q] < k)) {
+        kv = rv[b][q];
+        k = rp[b][q];
+      }
+    if (k < i || k >= n) k = i;   // only reachable with NaN values
+    if (k % 256 == tid) {
+      const int j = n - 1 - i;    // column after the flip
+      if (j < kq) {
+        top[j] = idx[k];
+        wf[j] = (double)val[k];
+      }
+      if (k != i) {
+        val[k] = val[i];
+        idx[k] = idx[i];
+      }
+    }
+  }
+  if ((n - 1) % 256 == tid) {   // the last position holds the largest value
+    top[0] = idx[n - 1];
+    wf[0] = (double)val[n - 1];
+  }
+  __syncthreads();
+  float* Uf = U + (int64_t)f * ustride;
+  const int total_e = n * kq;   // <= DIAG_MAX^2
+  if (kq % 4 == 0 && ((uintptr_t)Uf & 15) == 0) {
+    for (int e = 4 * tid; e < total_e; e += 4 * 256) {
+      const int row = e / kq, j = e - row * kq;
+      v4f x;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) x[t] = top[j + t] == row ? 1.f : 0.f;
+      gst4(Uf + e, x);
+    }
+  } else {
+    for (int e = tid; e < total_e; e += 256) {
+      const int row = e / kq, j = e - row * kq;
+      Uf[e] = top[j] == row ? 1.f : 0.f;
+    }
+  }
+}
+
 // int8_ema_update pass 1: x = fp32(fp32(q*s)*rho) + v, per-block |x| max
 __global__ __launch_bounds__(256) void k_ema_pass1(const int8_t* __restrict__ q, float sf,
                                                    float rho, const float* __restrict__ v,
@@ -667,6 +850,38 @@ extern "C" int scao_eig_prep(const scao_task* tasks, int ntasks, const scao_prep
   hipLaunchKernelGGL(k_eig_trace, dim3(ndescs), dim3(256), 0, s, descs);
   hipLaunchKernelGGL(k_eig_prep, dim3(ntasks), dim3(256), 0, s, tasks, descs);
   SCAO_LAUNCH_CHECK("scao_eig_prep");
+  return SCAO_OK;
+}
+
+extern "C" int scao_eig_offdiag(const scao_prep_desc* descs, int ndescs, int max_dim, int codes,
+                                int* flags, void* stream) {
+  SCAO_CHECK_ARG(ndescs >= 0 && ndescs <= 65535, "scao_eig_offdiag: ndescs=%d outside [0, 65535]",
+                 ndescs);
+  if (ndescs == 0) return SCAO_OK;
+  SCAO_CHECK_ARG(descs && flags, "scao_eig_offdiag: null pointer");
+  SCAO_CHECK_ARG(max_dim > 0 && max_dim <= 65535, "scao_eig_offdiag: max_dim=%d", max_dim);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_flags_clear, dim3((ndescs + 255) / 256), dim3(256), 0, s, flags, ndescs);
+  const int per = OFFDIAG_WORDS * (codes ? 4 : 1);
+  const int64_t nblk = ((int64_t)max_dim * max_dim + per - 1) / per;
+  hipLaunchKernelGGL(k_eig_offdiag, dim3((unsigned)nblk, ndescs), dim3(256), 0, s, descs, max_dim,
+                     per, flags);
+  SCAO_LAUNCH_CHECK("scao_eig_offdiag");
+  return SCAO_OK;
+}
+
+extern "C" int scao_eig_diag(const scao_prep_desc* descs, int ndescs, int n, int kq, double* w,
+                             float* U, int64_t ustride, double* total, void* stream) {
+  SCAO_CHECK_ARG(ndescs >= 0 && ndescs <= 65535, "scao_eig_diag: ndescs=%d outside [0, 65535]",
+                 ndescs);
+  if (ndescs == 0) return SCAO_OK;
+  SCAO_CHECK_ARG(descs && w && U && total, "scao_eig_diag: null pointer");
+  SCAO_CHECK_ARG(n >= 1 && n <= DIAG_MAX && kq >= 1 && kq <= n && ustride >= (int64_t)n * kq,
+                 "scao_eig_diag: bad arguments n=%d kq=%d", n, kq);
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_eig_trace, dim3(ndescs), dim3(256), 0, s, descs);
+  hipLaunchKernelGGL(k_eig_diag, dim3(ndescs), dim3(256), 0, s, descs, n, kq, w, U, ustride, total);
+  SCAO_LAUNCH_CHECK("scao_eig_diag");
   return SCAO_OK;
 }
 

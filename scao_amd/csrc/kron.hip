@@ -1528,12 +1528,29 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mu;
 float* g_scratch_ptr[kMaxDevices] = {};
 
-int scratch_for_current_device(float** out) {
+// The array of the current device, which must be the device of `stream` (a
+// non-null stream of another GPU is rejected: its kernels would be handed an
+// address in the wrong GPU's copy).
+int scratch_for_current_device(hipStream_t stream, float** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) {
     scao_set_error("scao_fused_kronecker_precond_noalloc: hipGetDevice: %s", hipGetErrorString(e));
     return SCAO_ERR_HIP;
+  }
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) {
+      scao_set_error("scao_fused_kronecker_precond_noalloc: hipStreamGetDevice: %s",
+                     hipGetErrorString(e));
+      return SCAO_ERR_HIP;
+    }
+    if ((int)sdev != dev) {
+      scao_set_error("scao_fused_kronecker_precond_noalloc: stream of device %d while device %d "
+                     "is current (make the stream's device current)", (int)sdev, dev);
+      return SCAO_ERR_INVALID;
+    }
   }
   if (dev < 0 || dev >= kMaxDevices) {
     scao_set_error("scao_fused_kronecker_precond_noalloc: device %d out of range", dev);
@@ -1588,7 +1605,7 @@ extern "C" int scao_fused_kronecker_precond_noalloc(const float* U_l, const floa
                  (long long)m, (long long)n, (long long)k, (long long)need,
                  (long long)SCAO_NOALLOC_SCRATCH_BYTES);
   float* ws = nullptr;
-  const int rc = scratch_for_current_device(&ws);
+  const int rc = scratch_for_current_device((hipStream_t)stream, &ws);
   if (rc != SCAO_OK) return rc;
   return launch_fused_kronecker(U_l, s_l_inv4, U_r, s_r_inv4, G, ldG, out, m, n, k, ws,
                                 (hipStream_t)stream);

@@ -10,18 +10,16 @@ kernels of csrc/eig.hip and plain batched GEMMs (rocBLAS, through torch):
    columns, ``scao_eig_panel_qr`` factors it (Householder, V kept in the
    panel, T returned), then the trailing matrix gets the two-sided update
    A22 <- Q^T A22 Q = A22 - (V W^T + W V^T), W = X - V (T^T V^T X) / 2,
-   X = A22 V T.  With FUSED_STAGE1 the next panel's columns are updated
-   first (a thin product), the next panel is factored, and one
-   ``scao_eig_sy2sb_update`` pass over the lower triangle applies the update
-   and forms the next panel's A22 V, so each panel reads and writes half the
-   matrix once; otherwise three batched GEMMs per panel on the full matrix;
+   X = A22 V T.  The next panel's columns are updated first (a thin
+   product), the next panel is factored, and one ``scao_eig_sy2sb_update``
+   pass over the lower triangle applies the update and forms the next
+   panel's A22 V, so each panel reads and writes half the matrix once;
 2. ``scao_eig_band_finish`` / ``scao_eig_sb2st``: band -> tridiagonal;
 3. ``scao_eig_bisect``: the kq largest eigenvalues and the clamped sum;
 4. ``scao_eig_vectors``: eigenvectors of the band matrix;
 5. back-transformation Z <- Q_0 (Q_1 (... Q_last Z)): ``scao_eig_back_transform``
    applies the panels' reflectors from the last, each matrix's Z slices held in
-   registers for the whole pass (or, with BT_KERNEL off, the reflectors merged
-   BT_GROUP at a time into block reflectors, three GEMMs per block).
+   registers for the whole pass.
 """
 
 from __future__ import annotations
@@ -34,7 +32,6 @@ from . import _lib as L
 NB = L.EIG_BAND
 BW = L.EIG_BANDW
 MAX_BATCH = 65535   # matrices per call: the batch is a grid dimension
-FUSED_STAGE1 = True  # lower-triangle panel updates (scao_eig_sy2sb_update)
 
 
 def panels(n: int) -> list:
@@ -66,19 +63,8 @@ def _reduce(X: Tensor):
     Tall = torch.empty(max(len(pcs), 1), B, NB, NB, dtype=f32, device=dev)
     band = torch.zeros(B, n, BW, dtype=f32, device=dev)
     nn = n * n
-    if FUSED_STAGE1 and pcs:
+    if pcs:
         _stage1_fused(X, pcs, Tall, band, s)
-    for p, c0 in enumerate(pcs if not FUSED_STAGE1 else []):
-        L.call("scao_eig_panel_qr", X.data_ptr(), nn, n, c0, B, Tall[p].data_ptr(),
-               band.data_ptr(), n * BW, s)
-        r0 = c0 + NB
-        V = X[:, r0:, c0:c0 + NB]
-        T = Tall[p]
-        A22 = X[:, r0:, r0:]
-        Y = torch.bmm(torch.bmm(A22, V), T)                        # X = A22 V T
-        M = torch.bmm(T.transpose(1, 2), torch.bmm(V.transpose(1, 2), Y))
-        W = torch.baddbmm(Y, V, M, alpha=-0.5)                     # X - V M / 2
-        A22.baddbmm_(torch.cat([V, W], 2), torch.cat([W, V], 2).transpose(1, 2), alpha=-1.0)
     orig = torch.empty(B, n, NB + 1, dtype=f32, device=dev)
     band64 = torch.empty(B, n, BW, dtype=torch.float64, device=dev)
     L.call("scao_eig_band_finish", X.data_ptr(), nn, n, B, band.data_ptr(), n * BW,
@@ -160,51 +146,7 @@ def topk_eigh(X: Tensor, kq: int):
     L.call("scao_eig_vectors", orig.data_ptr(), n * (NB + 1), n, B, kq, w.data_ptr(),
            Z.data_ptr(), n * kq, work.data_ptr(), s)
     del work
-    if BT_KERNEL:
-        if pcs:
-            L.call("scao_eig_back_transform", X.data_ptr(), n * n, n, B, Tall.data_ptr(),
-                   Z.data_ptr(), n * kq, kq, s)
-    else:
-        _back_transform(X, pcs, Tall, Z)
+    if pcs:
+        L.call("scao_eig_back_transform", X.data_ptr(), n * n, n, B, Tall.data_ptr(),
+               Z.data_ptr(), n * kq, kq, s)
     return w, Z, total
-
-
-BT_KERNEL = True   # the back-transformation in one kernel (scao_eig_back_transform)
-BT_GROUP = 8   # panels merged into one block reflector by the GEMM back-transformation
-
-
-def _back_transform(X: Tensor, pcs: list, Tall: Tensor, Z: Tensor) -> None:
-    """Z <- Q_0 (Q_1 (... Q_last Z)), Q_p = I - V_p T_p V_p^T (the stage-1
-    reflectors), BT_GROUP panels at a time: the product of the block's
-    reflectors is one block reflector I - V T V^T with V = [V_a .. V_b] (the
-    block's panel columns of X from the first panel's row r0 down, each panel
-    zero above its own reflector rows) and T built column block by column
-    block, T[:, j] = -T[:j, :j] (V_{:j}^T V_j) T_j above the diagonal block
-    T_j (the larft recurrence for blocks).  So Z makes one pass per block
-    instead of one per panel; the update is in place.  X's panel columns above
-    each reflector (band values, already copied by band_finish) are zeroed."""
-    B = X.shape[0]
-    npan = len(pcs)
-    for b0 in reversed(range(0, npan, BT_GROUP)):
-        b1 = min(b0 + BT_GROUP, npan)
-        g = b1 - b0
-        c0 = pcs[b0]
-        r0 = c0 + NB
-        for i in range(1, g):
-            cp = pcs[b0 + i]
-            X[:, r0:cp + NB, cp:cp + NB].zero_()
-        Vb = X[:, r0:, c0:c0 + NB * g]
-        if g == 1:
-            Tb = Tall[b0]
-        else:
-            S = torch.bmm(Vb.transpose(1, 2), Vb)
-            Tb = torch.zeros(B, NB * g, NB * g, dtype=X.dtype, device=X.device)
-            for i in range(g):
-                Tb[:, NB * i:NB * (i + 1), NB * i:NB * (i + 1)] = Tall[b0 + i]
-            for j in range(1, g):
-                lo = NB * j
-                Tb[:, :lo, lo:lo + NB] = -torch.bmm(
-                    torch.bmm(Tb[:, :lo, :lo], S[:, :lo, lo:lo + NB]), Tall[b0 + j])
-        Zs = Z[:, r0:, :]
-        Y = torch.bmm(Tb, torch.bmm(Vb.transpose(1, 2), Zs))
-        Zs.baddbmm_(Vb, Y, alpha=-1.0)

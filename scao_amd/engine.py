@@ -43,7 +43,7 @@ from torch import Tensor
 from . import _lib as L
 from . import eigen
 from .preconditioner import SparsePreconditioner, leaf_epoch
-from .utils import batched_adaptive_rank, batched_adaptive_rank_topk, to_2d
+from .utils import batched_adaptive_rank_topk, to_2d
 
 
 
@@ -247,8 +247,8 @@ def _param_tasks(it: PItem):
                 whole = vec and it.fp32 and j0 + L.PROJ_COLS <= n and m % 32 == 0
                 # 128 or 256 rows of T per task where k allows (variant bits 4, 8)
                 cr = 64
-                if TALL_PROJECT and whole and k % 128 == 0:
-                    cr = 256 if WIDE_PROJECT and k % 256 == 0 else 128
+                if whole and k % 128 == 0:
+                    cr = 256 if k % 256 == 0 else 128
                 for c0 in range(0, k, cr):
                     fast = whole and c0 + 64 <= k
                     do_p = c0 == 0 and it.lars
@@ -325,7 +325,7 @@ def _build_structure(items: list[PItem], cache: dict | None = None):
     the item and the module's tiling settings) and placed by offsets, so a
     step whose set of parameters changes (a parameter without a gradient,
     a rank change) costs array arithmetic, not a rebuild of every tile."""
-    knobs = (TALL_PROJECT, WIDE_PROJECT, PIPE_STRIP_ORDER, PIPE_MIN_RANK, L2_OPERANDS, L.APPLY_GROUP)
+    knobs = (PIPE_MIN_RANK, L2_OPERANDS, L.APPLY_GROUP)
     if cache is not None and len(cache) > 4 * len(items) + 64:
         cache.clear()
     parts = {k: [] for k in _TASK_TYPES}
@@ -366,10 +366,7 @@ def _build_structure(items: list[PItem], cache: dict | None = None):
 
 XCDS = 8   # MI355X: 8 accelerator dies, workgroup i is dispatched to die i % 8
 PIPE_MIN_RANK = 128   # wide apply tiles of blocks with k >= this use the pipelined kernel
-TALL_PROJECT = True   # projection tasks of 128 rows of T where k % 128 == 0
-WIDE_PROJECT = True   # ... and of 256 rows where k % 256 == 0 (G streamed once)
 RECENT_STRUCTURES = 4   # whole step structures kept on the device (run_step)
-PIPE_STRIP_ORDER = True   # pipelined leaves always take the strip-major (super-tile) order
 L2_OPERANDS = 2 << 20   # bytes of W / U_r rows a die's L2 (4 MB) keeps beside the streams
 
 
@@ -388,7 +385,7 @@ def _wide_tiles(mw: int, nw: int, k: int, pipelined: bool = False) -> list:
     pipelined kernel's leaves always take that order: it computes two tiles
     of one strip per pass over their U_r rows."""
     rows, cols = L.APPLY_WIDE_ROWS, L.APPLY_WIDE_COLS
-    if (mw + nw) * k * 4 <= L2_OPERANDS and not (pipelined and PIPE_STRIP_ORDER):
+    if (mw + nw) * k * 4 <= L2_OPERANDS and not pipelined:
         return [(i0, j0) for i0 in range(0, mw, rows) for j0 in range(0, nw, cols)]
     half = L2_OPERANDS // 2
     s = max(1, half // (cols * k * 4))
@@ -752,24 +749,17 @@ def _filter_tasks(numels: tuple, dev) -> Tensor:
     return t
 
 
-# The candidate buffer (half a float per element, plus four counts per
-# chunk) holds the keys of the top-digit bin (a quarter octave) the previous
-# threshold fell in; with it the last refinement pass of a steady filter
-# reads about a tenth of the EMA.  False saves the memory and runs that pass
-# over the EMA; results are the same either way.
-FILTER_CANDIDATES = True
-
-
 def _filter_scratch(f, numel: int, dev) -> None:
     """The filter's device scratch on ``dev``: ``work`` (selection state,
-    zero before the first call) and ``cand`` (candidate keys, or None)."""
+    zero before the first call) and ``cand``, the candidate buffer (half a
+    float per element, plus four counts per chunk): it holds the keys of the
+    top-digit bin (a quarter octave) the previous threshold fell in, so the
+    last refinement pass of a steady filter reads about a tenth of the EMA."""
     if getattr(f, "work", None) is None or f.work.device != dev:
         f.work = torch.zeros(L.FILTER_WORK_WORDS, dtype=torch.int32, device=dev)
         f.cand = None
-    cap = _flat_chunks(numel) * (L.FILTER_REGION + 4) if FILTER_CANDIDATES else 0
-    if cap == 0:
-        f.cand = None
-    elif getattr(f, "cand", None) is None or f.cand.numel() != cap:
+    cap = _flat_chunks(numel) * (L.FILTER_REGION + 4)
+    if getattr(f, "cand", None) is None or f.cand.numel() != cap:
         f.cand = torch.empty(cap, dtype=torch.float32, device=dev)
 
 
@@ -921,20 +911,30 @@ def sparse_filter(entries) -> list:
 # --------------------------------------------------------------------------
 
 REFRESH_SCRATCH_BYTES = 2 << 30   # fp32 EMA staging per refresh chunk (int8 mode)
-SYM_GRAM = True   # compute the lower Gram tiles only, each also writing its transpose
-# The eigen stage: "hip" is scao_amd.eigen.topk_eigh (two-stage reduction,
-# bisection, inverse iteration: only the k_max vectors a factor can keep);
-# "torch" is the full torch.linalg.eigh (rocSOLVER syevd), kept for A/B runs.
-EIGEN_SOLVER = "hip"
-CONCURRENT_EIGEN = True   # the smaller dimensions' eigen batches on a second stream
-EIGEN_BATCH_BYTES = 8 << 30       # stacked eigen-stage inputs per launch (hip)
+# The eigen stage runs scao_amd.eigen.topk_eigh (two-stage reduction,
+# bisection, inverse iteration: only the k_max vectors a factor can keep) for
+# factors up to HIP_EIGEN_MAX_DIM rows, and torch.linalg.eigh on the device
+# (rocSOLVER syevd) above that.  Factors whose eigh input is exactly diagonal
+# (up to HIP_EIGEN_MAX_DIM) take the closed form of scao_eig_diag instead.
+HIP_EIGEN_MAX_DIM = 4096 + L.EIG_BAND
+EIGEN_BATCH_BYTES = 8 << 30       # stacked eigen-stage inputs per launch (HIP solver), at most
+EIGEN_BATCH_FREE_FRACTION = 4     # ... and at most 1/4 of the device memory free at the refresh
+EIGH_BATCH_BYTES = 1 << 30        # stacked eigh inputs per launch (library solver)
 # Optional callable run between a refresh's EMA update and its eigen stage,
 # with the list of (block, gradient, offset, row stride) being refreshed.  Used
 # by the parity tests to check the new EMA and then continue from the CPU
 # reference's own post-EMA state, so the eigen stage and the step that follows
 # are compared from identical inputs.
 AFTER_EMA_HOOK = None
-EIGH_BATCH_BYTES = 1 << 30        # stacked eigh inputs per launch
+
+
+def eigen_route(dim: int, diagonal: bool) -> str:
+    """Which solver takes an n x n factor: "diag" (exactly diagonal input,
+    closed form), "hip" (the batched HIP solver) or "library"
+    (torch.linalg.eigh on the device) above HIP_EIGEN_MAX_DIM."""
+    if dim > HIP_EIGEN_MAX_DIM:
+        return "library"
+    return "diag" if diagonal else "hip"
 
 
 def refresh(entries, eigen_only: bool = False, ema_only: bool = False) -> None:
@@ -1031,7 +1031,10 @@ def _refresh_kron(kron, dev, s, eigen_only=False, ema_only=False):
         for leaf, *_ in kron:
             leaf._touch()
         return
-    # 2) eigendecomposition inputs, batched by dimension
+    # 2) eigendecomposition, batched by dimension.  Factors whose eigh input
+    # is exactly diagonal (an int8 EMA of small gradients keeps only its
+    # diagonal codes) take scao_eig_diag, which reproduces LAPACK's order of
+    # tied eigenvalues; the others go to the solver their size selects.
     jobs = {}   # dim -> list of (leaf, side)
     for leaf, *_ in kron:
         jobs.setdefault(leaf.m, []).append((leaf, 0))
@@ -1039,41 +1042,58 @@ def _refresh_kron(kron, dev, s, eigen_only=False, ema_only=False):
     spectra = {}   # (id(leaf), side) -> (S_desc, U_desc, total)
     eig_timer = _mark("refresh:eigh+rank")
     eig_timer.__enter__()
-    hip = EIGEN_SOLVER == "hip"
+    diagonal = _diagonal_factors(jobs, dev, s)
     # With several dimensions, every batch but the largest runs on a second
     # stream beside it (enqueued first, so it starts at once): a batch of a
     # few small factors leaves most of the GPU idle, and its latency-bound
     # kernels fit beside the large batch's.
     main = torch.cuda.current_stream(dev)
+    # a batch's transient buffers (the stacked inputs, the band copies, the
+    # eigenvector workspace) come to about twice its inputs: keep the inputs
+    # to a quarter of what is free (the caching allocator's idle blocks count)
+    free = torch.cuda.mem_get_info(dev)[0] + (torch.cuda.memory_reserved(dev) -
+                                               torch.cuda.memory_allocated(dev))
+    hip_budget = min(EIGEN_BATCH_BYTES, free // EIGEN_BATCH_FREE_FRACTION)
     order = sorted(jobs.items(), key=lambda kv: len(kv[1]) * kv[0] ** 2)
-    side = _side_stream(dev) if hip and CONCURRENT_EIGEN and len(order) > 1 else None
+    side = _side_stream(dev) if len(order) > 1 else None
     if side is not None:
         side.wait_stream(main)   # the EMA codes
     for bi, (dim, lst) in enumerate(order):
         strm = side if side is not None and bi + 1 < len(order) else main
         with torch.cuda.stream(strm):
             s_b = L.stream_ptr(dev)
-            budget = EIGEN_BATCH_BYTES if hip else EIGH_BATCH_BYTES
-            per = min(max(1, budget // (4 * dim * dim)), eigen.MAX_BATCH)
             # vectors a factor can keep: k <= k_max (rank momentum and clamps)
             kq = min(dim, max(leaf.k_max for leaf, _ in lst))
-            for b0 in range(0, len(lst), per):
-                part = lst[b0:b0 + per]
-                X = _eig_inputs(part, dim, dev, s_b)
-                if hip:
-                    w, U_desc, total = eigen.topk_eigh(X, kq)
-                    S_desc = w.clamp(min=0.0).float()
-                else:
-                    w, V = _eigh_batched(X)
-                    S_desc = w.flip(-1).clamp(min=0.0)
-                    U_desc = V.flip(-1)
-                    total = S_desc.sum(dim=1).double()
-                if strm is not main:   # used on the current stream from here on
-                    for t in (S_desc, U_desc, total):
-                        t.record_stream(main)
-                for (leaf, side_), Sd, Ud, tot in zip(part, S_desc, U_desc, total):
-                    spectra[(id(leaf), side_)] = (Sd, Ud, tot)
-                del X
+            routes = {}
+            for key in lst:
+                r = eigen_route(dim, (id(key[0]), key[1]) in diagonal)
+                routes.setdefault(r, []).append(key)
+            for route, keys in routes.items():
+                budget = EIGH_BATCH_BYTES if route == "library" else hip_budget
+                per = len(keys) if route == "diag" else \
+                    min(max(1, budget // (4 * dim * dim)), eigen.MAX_BATCH)
+                for b0 in range(0, len(keys), per):
+                    part = keys[b0:b0 + per]
+                    if route == "diag":
+                        w, U_desc, total = _diag_eigh(part, dim, kq, dev, s_b)
+                        S_desc = w.clamp(min=0.0).float()
+                    elif route == "hip":
+                        X = _eig_inputs(part, dim, dev, s_b)
+                        w, U_desc, total = eigen.topk_eigh(X, kq)
+                        S_desc = w.clamp(min=0.0).float()
+                        del X
+                    else:
+                        X = _eig_inputs(part, dim, dev, s_b)
+                        w, V = _eigh_batched(X)
+                        S_desc = w.flip(-1).clamp(min=0.0)[:, :kq].contiguous()
+                        U_desc = V.flip(-1)[:, :, :kq].contiguous()
+                        total = w.clamp(min=0.0).sum(dim=1).double()
+                        del X, V
+                    if strm is not main:   # used on the current stream from here on
+                        for t in (S_desc, U_desc, total):
+                            t.record_stream(main)
+                    for (leaf, side_), Sd, Ud, tot in zip(part, S_desc, U_desc, total):
+                        spectra[(id(leaf), side_)] = (Sd, Ud, tot)
     if side is not None:
         main.wait_stream(side)
     # 3) adaptive rank for every (leaf, side) in one device pass + one read
@@ -1089,11 +1109,8 @@ def _refresh_kron(kron, dev, s, eigen_only=False, ema_only=False):
         eps = torch.tensor([lf.epsilon_sparse for lf, _ in lst], device=dev, dtype=torch.float64)
         kmin = torch.tensor([lf.k_min for lf, _ in lst], device=dev, dtype=torch.int64)
         kmax = torch.tensor([lf.k_max for lf, _ in lst], device=dev, dtype=torch.int64)
-        if hip:
-            tot = torch.stack([spectra[(id(lf), sd)][2] for lf, sd in lst])
-            dev_ranks.append((lst, batched_adaptive_rank_topk(S, tot, dim, eps, kmin, kmax)))
-        else:
-            dev_ranks.append((lst, batched_adaptive_rank(S, eps, kmin, kmax)))
+        tot = torch.stack([spectra[(id(lf), sd)][2] for lf, sd in lst])
+        dev_ranks.append((lst, batched_adaptive_rank_topk(S, tot, dim, eps, kmin, kmax)))
     host = torch.cat([r for _, r in dev_ranks]).cpu().tolist() if dev_ranks else []
     i = 0
     for lst, _ in dev_ranks:
@@ -1129,17 +1146,13 @@ _GRAM_TILE_IDX: dict = {}
 
 
 def _gram_tile_idx(nt: int):
-    """(a, b, slot) of a factor's Gram tasks for nt x nt tiles (lower tiles
-    with SYM_GRAM), cached per size."""
-    key = (nt, SYM_GRAM)
-    v = _GRAM_TILE_IDX.get(key)
+    """(a, b, slot) of a factor's Gram tasks for nt x nt tiles: the lower
+    tiles, each also writing its transpose (GRAM_SYM), cached per size."""
+    v = _GRAM_TILE_IDX.get(nt)
     if v is None:
-        if SYM_GRAM:
-            a, b = np.tril_indices(nt)
-        else:
-            a, b = np.divmod(np.arange(nt * nt), nt)
+        a, b = np.tril_indices(nt)
         v = (a.astype(np.int32), b.astype(np.int32), (a * nt + b).astype(np.int32))
-        _GRAM_TILE_IDX[key] = v
+        _GRAM_TILE_IDX[nt] = v
     return v
 
 
@@ -1164,7 +1177,7 @@ def _gram_chunk(chunk, dev, s):
     dtab["ntiles"] = nts * nts
     rho = np.array([lf.rho for lf, *_ in recs], dtype=np.float64)
     dtab["rho"], dtab["alpha"] = rho, 1.0 - rho
-    dtab["flags"] = L.GRAM_SYM if SYM_GRAM else 0
+    dtab["flags"] = L.GRAM_SYM
     # int8 sides: fp32 EMA staging (dim^2) and tile maxima (nt^2), one buffer
     sizes = np.where(int8, dims * dims + nts * nts, 0)
     starts = np.concatenate([[0], np.cumsum(sizes)[:-1]])
@@ -1206,31 +1219,74 @@ def _gram_chunk(chunk, dev, s):
     del staging   # stream-ordered reuse by the caching allocator is safe
 
 
-def _eig_inputs(part, dim, dev, s) -> Tensor:
-    X = torch.empty(len(part), dim, dim, dtype=torch.float32, device=dev)
-    shift = torch.empty(len(part), dtype=torch.float32, device=dev)
-    descs = []
-    nchunk = _flat_chunks(dim * dim)
+def _prep_descs(part, dim, out: Tensor | None, shift: Tensor) -> np.ndarray:
+    """PREP_DESC rows for (leaf, side) factors of one dimension: the EMA
+    source (codes and scale, or the fp32 EMA), the bias factor, a shift slot
+    and, when given, the output matrix out[i]."""
+    tab = np.zeros(len(part), dtype=L.PREP_DESC)
     for i, (leaf, side) in enumerate(part):
-        e = np.zeros(1, dtype=L.PREP_DESC)[0]
-        bias = 1.0 - leaf.rho ** leaf.precond_step
-        e["bias"] = max(bias, 1e-8)
+        e = tab[i]
+        e["bias"] = max(1.0 - leaf.rho ** leaf.precond_step, 1e-8)
         e["dim"] = dim
-        e["out"] = X[i].data_ptr()
+        if out is not None:
+            e["out"] = out[i].data_ptr()
         e["shift"] = shift.data_ptr() + 4 * i
         if leaf.use_int8_ema:
             e["q"] = (leaf.L_ema_q if side == 0 else leaf.R_ema_q).data_ptr()
             e["scale"] = leaf._scale.data_ptr() + 8 * side
         else:
             e["ema"] = (leaf.L_ema if side == 0 else leaf.R_ema).data_ptr()
-        descs.append(e)
-    dd = L.upload(np.array(descs, dtype=L.PREP_DESC), dev)
+    return tab
+
+
+def _eig_inputs(part, dim, dev, s) -> Tensor:
+    X = torch.empty(len(part), dim, dim, dtype=torch.float32, device=dev)
+    shift = torch.empty(len(part), dtype=torch.float32, device=dev)
+    dd = L.upload(_prep_descs(part, dim, X, shift), dev)
     n = len(part)
+    nchunk = _flat_chunks(dim * dim)
     tt = _task_rows(np.repeat(np.arange(n), nchunk), np.tile(np.arange(nchunk), n), 0,
                     -1).view(L.TASK).reshape(-1)
     td = L.upload(tt, dev)
-    _call("scao_eig_prep", td.data_ptr(), len(tt), dd.data_ptr(), len(descs), s)
+    _call("scao_eig_prep", td.data_ptr(), len(tt), dd.data_ptr(), n, s)
     return X
+
+
+def _diagonal_factors(jobs: dict, dev, s) -> set:
+    """(id(leaf), side) of every factor up to HIP_EIGEN_MAX_DIM rows whose EMA
+    has no non-zero off-diagonal entry: one scan of the codes on the device
+    and one read of the flags."""
+    keys = [key for dim, lst in jobs.items() if dim <= HIP_EIGEN_MAX_DIM for key in lst]
+    if not keys:
+        return set()
+    dims = [key[0].m if key[1] == 0 else key[0].n for key in keys]
+    shift = torch.empty(1, dtype=torch.float32, device=dev)   # not written by the scan
+    tab = np.concatenate([_prep_descs([key], d, None, shift) for key, d in zip(keys, dims)])
+    flags = torch.empty(len(keys), dtype=torch.int32, device=dev)
+    codes = int(all(key[0].use_int8_ema for key in keys))
+    dd = L.upload(tab, dev)
+    for c0 in range(0, len(keys), 65535):
+        c1 = min(c0 + 65535, len(keys))
+        _call("scao_eig_offdiag", dd.data_ptr() + c0 * L.PREP_DESC.itemsize, c1 - c0,
+              max(dims[c0:c1]), codes, flags.data_ptr() + 4 * c0, s)
+    host = flags.cpu().tolist()
+    return {(id(key[0]), key[1]) for key, f in zip(keys, host) if f == 0}
+
+
+def _diag_eigh(part, dim, kq, dev, s):
+    """topk_eigh's (w, U, total) for exactly diagonal factors of one dimension
+    (scao_eig_diag)."""
+    n = len(part)
+    shift = torch.empty(n, dtype=torch.float32, device=dev)
+    w = torch.empty(n, kq, dtype=torch.float64, device=dev)
+    U = torch.empty(n, dim, kq, dtype=torch.float32, device=dev)
+    total = torch.empty(n, dtype=torch.float64, device=dev)
+    dd = L.upload(_prep_descs(part, dim, None, shift), dev)
+    for c0 in range(0, n, 65535):
+        c1 = min(c0 + 65535, n)
+        _call("scao_eig_diag", dd.data_ptr() + c0 * L.PREP_DESC.itemsize, c1 - c0, dim, kq,
+              w[c0].data_ptr(), U[c0].data_ptr(), dim * kq, total[c0].data_ptr(), s)
+    return w, U, total
 
 
 def _eigh_batched(X: Tensor):

@@ -20,6 +20,10 @@ drawn param by param in group order; params from manual_seed(0)):
                    adaptive warm-up, dynamic sparsity, adaptive rank), each on
                    the fp32 or int8 small configuration the GPU feature tests
                    use; the warm-up flag is recorded per step.
+  diag_int8     -- the reference's refreshes from its initialisation at the
+                   large configurations' gradient scale (2048x2048 and
+                   512x2048, k=64, N(0,1e-3^2)): exactly diagonal int8 EMAs,
+                   unit-vector eigenfactors in LAPACK's tie order.
   ops           -- operator-level vectors (projection, int8 EMA update,
                    low-rank mm, quantise, adaptive rank, natural norm).
   c1_summary    -- the 768x3072 parity config, 100 steps: per-step norms,
@@ -274,6 +278,57 @@ def run_ckpt(scao):
         json.dump(meta, f, indent=1, sort_keys=True)
 
 
+DIAG_SHAPES = {"q": (2048, 2048), "kv": (512, 2048)}
+DIAG_CFG = dict(k_min=64, k_max=64, rho=0.999, max_precond_dim=2048, use_int8_ema=True)
+
+
+def diag_grad(shape, r: int, pi: int):
+    """Refresh r's gradient of the pi-th diag_int8 weight: N(0, 1e-3^2)."""
+    g = torch.Generator().manual_seed(5000 + 10 * r + pi)
+    return torch.randn(shape, generator=g) * 1e-3
+
+
+def run_diag(scao):
+    """The reference's own refreshes from its initialisation at the gradient
+    scale of the Llama/Qwen configurations: an int8 SparsePreconditioner on a
+    2048x2048 and a 512x2048 weight (k = 64, max_precond_dim 2048, rho
+    0.999), three update_curvature calls with N(0, 1e-3^2) gradients.  The
+    requantised EMAs keep only their diagonal codes, so every eigh input is
+    exactly diagonal and its eigenvectors are unit vectors, in the order
+    LAPACK's selection sort leaves tied values.  Stored per refresh and side:
+    each kept column's row and sign, S, the diagonal codes, the scale, the
+    count of non-zero off-diagonal codes and k."""
+    from scao.preconditioner import SparsePreconditioner
+    out, meta = {}, {"config": DIAG_CFG, "blocks": [[k, list(v)] for k, v in DIAG_SHAPES.items()],
+                     "refreshes": 3, "rows": {}}
+    for pi, (name, shape) in enumerate(DIAG_SHAPES.items()):
+        pre = SparsePreconditioner(torch.zeros(shape), **DIAG_CFG)
+        for r in range(3):
+            pre.update_curvature(diag_grad(shape, r, pi))
+            rec = {"k": pre.k, "precond_step": pre.precond_step}
+            for side, U, S, q, sc in (("L", pre.U_l, pre.S_l, pre.L_ema_q, pre.L_ema_scale),
+                                      ("R", pre.U_r, pre.S_r, pre.R_ema_q, pre.R_ema_scale)):
+                cols = torch.arange(U.shape[1])
+                rows = U.abs().argmax(0)
+                sign = U[rows, cols]
+                unit = torch.zeros_like(U)
+                unit[rows, cols] = sign
+                assert torch.equal(unit, U), "eigenvectors are not unit vectors"
+                off = int((q != 0).sum()) - int((q.diagonal() != 0).sum())
+                key = f"{name}.r{r}.{side}"
+                out[key + ".rows"] = rows.to(torch.int32)
+                out[key + ".sign"] = sign.clone()
+                out[key + ".S"] = S.clone()
+                out[key + ".diag_codes"] = q.diagonal().clone()
+                rec[side] = {"scale": sc, "offdiag_nonzero": off,
+                             "sha": hashlib.sha256(q.numpy().tobytes()).hexdigest()[:16]}
+            meta["rows"][f"{name}.r{r}"] = rec
+    save_file(out, os.path.join(HERE, "diag_int8.safetensors"))
+    with open(os.path.join(HERE, "diag_int8.json"), "w") as f:
+        json.dump(meta, f, indent=1, sort_keys=True)
+    print("diag_int8 done")
+
+
 def main(only=None):
     """Write every fixture, or only those named on the command line."""
     sys.path.insert(0, REF)
@@ -308,6 +363,8 @@ def main(only=None):
     for name, (cfg, steps) in features.items():
         if want(name):
             run_traj(scao, name, cfg, steps=steps, snap_steps=(steps,))
+    if want("diag_int8"):
+        run_diag(scao)
     if not want("traj_int8"):
         return
     run_traj(scao, "traj_int8", dict(base, use_int8_ema=True, k_min=2, k_max=8,

@@ -57,6 +57,34 @@ def test_error_path_without_gpu():
     assert L.NOALLOC_SCRATCH_BYTES == 16 << 20
 
 
+def test_eig_entry_points_reject_oversized_n():
+    """Every scao_eig_* entry point checks n <= 4096 + SCAO_EIG_BAND on the
+    host (larger factors go to the library solver), so a direct C-ABI caller
+    gets SCAO_ERR_INVALID instead of a kernel whose progress counters would
+    overflow."""
+    from scao_amd import _lib as L
+    lib = L.lib()
+    p, big = 16, 1 << 40   # non-null dummies and strides: nothing is launched
+    for n in (4096 + L.EIG_BAND + 1, 40000):
+        calls = {
+            "scao_eig_panel_qr": (p, big, n, 0, 1, p, p, big, None),
+            "scao_eig_sy2sb_panel_w": (p, big, n, 0, 1, p, p, p, 1, None),
+            "scao_eig_sy2sb_update": (p, big, n, n, 1, p, big, 16, p, big, 16, p, big, 16, p,
+                                      big, p, None),
+            "scao_eig_band_finish": (p, big, n, 1, p, big, p, big, p, None),
+            "scao_eig_sb2st": (p, n, 1, p, p, None),
+            "scao_eig_bisect": (p, p, n, 1, 8, p, p, p, None),
+            "scao_eig_vectors": (p, big, n, 1, 8, p, p, big, p, None),
+            "scao_eig_back_transform": (p, big, n, 1, p, p, big, 8, None),
+            "scao_eig_diag": (p, 1, n, 8, p, p, big, p, None),
+        }
+        for name, args in calls.items():
+            rc = getattr(lib, name)(*args)
+            assert rc == 1, (name, n, rc)
+    from scao_amd import engine
+    assert engine.HIP_EIGEN_MAX_DIM == 4096 + L.EIG_BAND
+
+
 def test_missing_library_raises(monkeypatch, tmp_path):
     from scao_amd import _lib as L
     monkeypatch.setattr(L, "LIB_PATH", str(tmp_path / "nope.so"))

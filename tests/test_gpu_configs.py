@@ -409,6 +409,106 @@ def test_config_eigen_stage(name, mat):
         assert errs[side + "_orth"] < 1e-4, errs
 
 
+def test_c3_layer_from_reference_init():
+    """C3 from the reference's own initialisation (identity EMAs, U = eye,
+    S = 1) at its gradient scale, N(0, 1e-3^2): 8 steps with a refresh every
+    2 steps (Adam at steps 1-2, blend over steps 3-4, Phase 2 after), four
+    refreshes, on the layer's q (2048^2), k (512x2048) and down (2048x8192:
+    four strided 2048^2 blocks) weights.
+
+    At this scale the int8 EMAs keep only their diagonal codes (the CPU
+    reference's off-diagonal codes are checked to be all zero), so every
+    eigh input is exactly diagonal and the reference's eigenvectors are unit
+    vectors in LAPACK's tie order.  At each refresh the GPU's new codes are
+    checked against the reference's (1 LSB, scales 1e-6) and replaced by them
+    (parity.IdenticalPostEma); then every block's U_l, U_r, S_l, S_r and k must
+    equal the reference's column for column.  Every step's update (each side
+    from its own previous parameters, as in the C1 run: an Adam step's
+    rounding at 1e-3 updates is far above a Phase-2 LARS step's size) must
+    agree elementwise at rtol 1e-4, the moments likewise, and the whole
+    trajectory at rtol 1e-4 of the cumulative update."""
+    import scao_amd
+    from scao_amd import engine
+    dev = _dev()
+    c, mats, _, gscale, _ = _layer("C3_llama1b")
+    shapes = {k: mats[k] for k in ("q", "k", "down")}
+    params = _params(shapes, 0)
+    cfg = dict(precond_freq=2, warmup_steps=2, blend_steps=2, min_precond_updates=1)
+    rgroups = [dict(params=list(params.values()), k_min=c["k"], k_max=c["k"],
+                    max_precond_dim=c["D"])]
+    ref = R.RefSCAO(rgroups, **cfg, **PROFILE)
+    gp = {k: torch.nn.Parameter(v.detach().clone().to(dev)) for k, v in params.items()}
+    gopt = scao_amd.SCAO([dict(rgroups[0], params=list(gp.values()))], **cfg, **PROFILE)
+    worst = {"step_ratio": 0.0, "moment_ratio": 0.0, "traj_ratio": 0.0, "diag_calls": 0}
+    init = {k: v.detach().clone() for k, v in params.items()}
+    prev_gpu = {k: v.detach().clone() for k, v in params.items()}
+    orig = engine._diag_eigh
+
+    def counted(part, *a):
+        worst["diag_calls"] += len(part)
+        return orig(part, *a)
+    engine._diag_eigh = counted
+    try:
+        for t in range(1, 9):
+            grads = _grads(shapes, 3000 + t, gscale, 0.0)
+            before = {k: v.detach().clone() for k, v in params.items()}
+            for k in shapes:
+                params[k].grad = grads[k]
+                gp[k].grad = grads[k].to(dev)
+            print(f"C3 from init: step {t} reference", flush=True)
+            R.EXACT_NORMS = True
+            try:
+                ref.step()
+            finally:
+                R.EXACT_NORMS = False
+            pairs = {}
+            for k in shapes:
+                if gp[k] in gopt.state:
+                    for (la, *_), (lb, *_) in zip(P.kron_leaves(ref.state[params[k]]["preconditioner"]),
+                                                  gopt.state[gp[k]]["preconditioner"].leaves()):
+                        pairs[id(lb)] = la
+            hook = P.IdenticalPostEma(pairs)
+            engine.AFTER_EMA_HOOK = hook
+            try:
+                print(f"C3 from init: step {t} GPU", flush=True)
+                gopt.step()
+            finally:
+                engine.AFTER_EMA_HOOK = None
+            torch.cuda.synchronize()
+            for k in shapes:
+                pg_new = gp[k].detach().cpu()
+                r = P.ratio(pg_new - prev_gpu[k], params[k].detach() - before[k], P.UPDATE_RTOL,
+                            P.UPDATE_ATOL, extra=torch.maximum(P.ulp(params[k]), P.ulp(pg_new)))
+                assert r <= 1.0, (t, k, "step update", r)
+                worst["step_ratio"] = max(worst["step_ratio"], r)
+                worst["traj_ratio"] = max(worst["traj_ratio"], P.assert_close(
+                    pg_new - init[k], params[k].detach() - init[k], 1e-4, 1e-5,
+                    f"C3 from init t{t} {k} cumulative update"))
+                prev_gpu[k] = pg_new
+                st_r, st_g = ref.state[params[k]], gopt.state[gp[k]]
+                for key in ("exp_avg", "exp_avg_sq", "exp_avg_diff", "prev_grad"):
+                    worst["moment_ratio"] = max(worst["moment_ratio"], P.assert_close(
+                        st_g[key], st_r[key], P.MOMENT_RTOL, P.MOMENT_ATOL, f"t{t} {k} {key}"))
+            if t % cfg["precond_freq"]:
+                continue
+            assert hook.checked == 6   # q, k and down's four blocks
+            for k in shapes:
+                pr = ref.state[params[k]]["preconditioner"]
+                pg = gopt.state[gp[k]]["preconditioner"]
+                for (la, *_), (lb, *_) in zip(P.kron_leaves(pr), pg.leaves()):
+                    for q in (la.L_ema_q, la.R_ema_q):
+                        assert int((q != 0).sum() - (q.diagonal() != 0).sum()) == 0
+                    assert lb.k == la.k and lb.precond_step == la.precond_step, (t, k)
+                    for U1, S1, U2, S2 in ((la.U_l, la.S_l, lb.U_l, lb.S_l),
+                                           (la.U_r, la.S_r, lb.U_r, lb.S_r)):
+                        assert torch.equal(U2.cpu(), U1), (t, k, "U")
+                        assert torch.equal(S2.cpu(), S1), (t, k, "S")
+    finally:
+        engine._diag_eigh = orig
+    assert worst["diag_calls"] == 4 * 6 * 2
+    report("c3_from_reference_init", "8 steps, 4 refreshes", worst)
+
+
 # ---------------------------------------------------------------- C1 ---
 
 def _c1_quantities(p, st, pre):

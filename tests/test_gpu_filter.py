@@ -141,7 +141,13 @@ def test_filter_candidate_passes(case, monkeypatch):
     if case == "q_change":
         qs[2] = 0.2
     if case == "no_buffer":
-        monkeypatch.setattr(engine, "FILTER_CANDIDATES", False)
+        # the C ABI's optional candidate buffer left out (cand = NULL)
+        orig = engine._filter_scratch
+
+        def no_cand(f, numel, dev):
+            orig(f, numel, dev)
+            f.cand = None
+        monkeypatch.setattr(engine, "_filter_scratch", no_cand)
     ref, gpu = R.RefSparseFilter(0.7), _SparseGradFilter(0.7)
     modes = []
     for t, g in enumerate(grads):

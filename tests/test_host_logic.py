@@ -505,3 +505,19 @@ def test_adaptive_rank_from_top_eigenvalues_matches_full_spectrum():
             got = batched_adaptive_rank_topk(S[:, :kq], S.double().sum(dim=1), dim, e, kmin, kmax)
             ref = R.adaptive_rank(S[0], eps, int(kmin), int(kmax))
             assert int(got) == int(want) == ref, (dim, kq, eps, trial, int(got), int(want), ref)
+
+
+def test_eigen_route_by_size_and_shape():
+    """Which solver a refresh gives an n x n factor: the closed form for an
+    exactly diagonal input, the HIP solver up to 4096 + SCAO_EIG_BAND rows,
+    the library eigh above that (diagonal or not: the closed form's LDS
+    arrays stop at the same size)."""
+    from scao_amd import engine
+    lim = engine.HIP_EIGEN_MAX_DIM
+    assert engine.eigen_route(2048, True) == "diag"
+    assert engine.eigen_route(2048, False) == "hip"
+    assert engine.eigen_route(lim, True) == "diag"
+    assert engine.eigen_route(lim, False) == "hip"
+    assert engine.eigen_route(lim + 1, False) == "library"
+    assert engine.eigen_route(lim + 1, True) == "library"
+    assert engine.eigen_route(1, True) == "diag"
