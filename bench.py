@@ -571,13 +571,16 @@ def main():
     assert all(opt.state[p].get("scao_phase_started") for p in pre_p), "not in Phase 2"
 
     # per-step distribution (the survey's definition of the metric): an event
-    # before step(), an event and a synchronisation after it, for each step
+    # right before step() (after the gradients are in place), an event and a
+    # synchronisation after it, for each step
     per_step = []
     for _ in range(max(20, args.steps)):
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        set_grads(step[0])
         e0.record()
-        one()
+        opt.step()
         e1.record()
+        step[0] += 1
         torch.cuda.synchronize()
         per_step.append(e0.elapsed_time(e1))
     per_step.sort()

@@ -58,6 +58,14 @@ EXACT_NORMS = False
 EXACT_EIGH = False
 
 
+# Test hook: when a dict, each Phase-2 parameter step stores its intermediates
+# under id(p): the update u, the decayed parameter the update is added to,
+# the LARS trust, the natural-gradient norm and the clip factor (1.0 when
+# clipping is off or not triggered).  The parity tests compare the kernels'
+# own intermediates with these.
+RECORD = None
+
+
 def _norm(x: Tensor) -> Tensor:
     """x.norm() as the reference takes it, or its correctly rounded value."""
     if EXACT_NORMS:
@@ -804,10 +812,13 @@ class RefSCAO(torch.optim.Optimizer):
             if refresh:
                 pre.update_curvature(p.grad.detach())
             gp = pre.precondition(p.grad)
+            nat, clip = None, 1.0
             if tau is not None:
                 nat = pre.natural_grad_norm(p.grad, eps=eps)
                 if nat > tau:
-                    gp = gp * (tau / nat.clamp(min=eps))
+                    factor = tau / nat.clamp(min=eps)
+                    gp = gp * factor
+                    clip = float(factor)
             bsteps = group.get("blend_steps", 50)
             b = min(1.0, ss / bsteps) if bsteps > 0 else 1.0
             geff = b * gp.float() + (1.0 - b) * grad
@@ -824,6 +835,9 @@ class RefSCAO(torch.optim.Optimizer):
             if self._use_gsnr_clip:
                 upd = gsnr_clip(upd, m, v, eps, self._gsnr_threshold)
             trust = self._lars_scale(p, upd, lars, wd) if lars > 0 else 1.0
+            if RECORD is not None:
+                RECORD[pid] = dict(upd=upd.clone(), pdec=p.data.clone(), trust=trust,
+                                   nu=None if nat is None else float(nat), clip=clip)
             p.add_(upd.to(p.dtype), alpha=-(lr * trust))
 
     def synchronize_precond(self) -> None:

@@ -107,6 +107,9 @@ class PItem:
         return self.gmom is not None or self.msrc is not None
 
 
+PARAM_RING = 4   # parameter-table staging slots (steps the host may run ahead)
+
+
 class Workspace:
     """Device buffers reused across steps (one per optimizer)."""
 
@@ -131,6 +134,42 @@ class Workspace:
         self.leaf_dev = None
         self.leaf_index = {}
         self.upd_offsets = {}
+        # parameter-table staging: PARAM_RING slots of (pinned host buffer,
+        # device buffer, event recorded after the step that last used them)
+        self._ring: list = [None] * PARAM_RING
+        self._ring_next = 0
+
+    def stage_params(self, raw: np.ndarray) -> Tensor:
+        """The step's parameter table on the device, through the next slot of
+        the staging ring.  The slot's event was recorded after the kernels of
+        the step that last used it (finish_params), so once it has completed
+        neither its host buffer (still being copied) nor its device buffer
+        (still being read) is in use; in a steady loop that step is
+        PARAM_RING steps back and the wait returns at once."""
+        nbytes = raw.nbytes
+        i = self._ring_next
+        self._ring_next = (i + 1) % PARAM_RING
+        ent = self._ring[i]
+        if ent is None or ent[0].numel() < nbytes:
+            cap = max(nbytes, 4096)
+            ent = [torch.empty(cap, dtype=torch.uint8, pin_memory=True),
+                   torch.empty(cap, dtype=torch.uint8, device=self.device), None]
+            self._ring[i] = ent
+        elif ent[2] is not None:
+            ent[2].synchronize()
+        host, dev = ent[0][:nbytes], ent[1][:nbytes]
+        host.numpy()[:] = raw.reshape(-1).view(np.uint8)
+        dev.copy_(host, non_blocking=True)
+        self._ring_slot = ent
+        return dev
+
+    def finish_params(self) -> None:
+        """Mark the staged table's slot busy until the work enqueued so far
+        (the step's kernels) has run."""
+        ent = self._ring_slot
+        if ent[2] is None:
+            ent[2] = torch.cuda.Event()
+        ent[2].record()
 
     def invalidate(self) -> None:
         """Forget the cached step structures (rebuilt on the next step)."""
@@ -633,14 +672,64 @@ def _param_table(items: list[PItem], ranges, ws: Workspace, gsnr: float | None):
         f4[rows] = np.array(head[1:] + (0.0,) + tail, dtype=np.float32)
     for i, v in dbias:
         f4[i, _DBIAS] = v
-    return raw.view(L.PARAM_DESC).reshape(n)
+    # rows sharing a group's step scalars: (group, step, phase2, scao_step,
+    # lars, rows, flags of each row beyond the group's)
+    classes = []
+    for (gid, t, ph2, ss, lars), (_, _, gflags, rows) in shared.items():
+        rows = np.array(rows, dtype=np.int64)
+        extra = cols("i4", np.int32)[rows, 1] & ~np.int32(gflags)
+        classes.append(StepClass(items[int(rows[0])].group, t, ph2, ss, lars, rows, extra))
+    return raw, classes
+
+
+@dataclass(slots=True)
+class StepClass:
+    """Rows of a step's parameter table that share a group's step scalars."""
+    group: dict
+    step: int
+    phase2: bool
+    scao_step: int
+    lars: bool
+    rows: np.ndarray
+    extra_flags: np.ndarray   # per-row flags beyond the group's (alignment, diagonal mode)
+
+
+@dataclass(slots=True)
+class StepPlan:
+    """What a plain step (no refresh, no filter or noise, no host norms)
+    leaves for the next one: its items, its parameter table and the rows'
+    classes.  While the same parameters step again with gradients of the
+    same layout, the next step only rewrites the gradient addresses and each
+    class's step scalars (run_planned_step)."""
+    items: list
+    raw: np.ndarray
+    classes: list
+    gsnr: float | None
+    epoch: int
+    moments: list   # per item: the four moment tensors the table points at
+    min_pre: list | None = None   # per class: the smallest precond_step of its rows
+
+
+def _set_class_scalars(raw: np.ndarray, cl: StepClass, gsnr) -> None:
+    head, tail, gflags = _group_scalars(cl.group, cl.step, cl.phase2, cl.scao_step, cl.lars,
+                                        gsnr)
+    a8, b8, _ = _BLOCKS["f8"]
+    a4, b4, _ = _BLOCKS["f4"]
+    ai, bi, _ = _BLOCKS["i4"]
+    raw[cl.rows, a8:b8].view(np.float64)[:, 0] = head[0]
+    f4 = raw[:, a4:b4].view(np.float32)
+    dbias = f4[cl.rows, _DBIAS].copy()
+    f4[cl.rows] = np.array(head[1:] + (0.0,) + tail, dtype=np.float32)
+    f4[cl.rows, _DBIAS] = dbias
+    raw[:, ai:bi].view(np.int32)[cl.rows, 1] = cl.extra_flags | np.int32(gflags)
 
 
 def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
-             gsnr: float | None = None) -> None:
-    """Launch one optimizer step for ``items`` (all on ws.device)."""
+             gsnr: float | None = None) -> "StepPlan | None":
+    """Launch one optimizer step for ``items`` (all on ws.device); returns
+    the step's plan (see StepPlan)."""
     if not items:
-        return
+        return None
     dev = ws.device
     f32 = torch.float32
     for it in items:
@@ -689,10 +778,39 @@ def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
         tab = _leaf_table(ws.leaves, items, ws)
         ws.leaf_dev = L.upload(tab, dev) if len(tab) else None
         ws.leaf_epoch = leaf_epoch()
-    ptab = _param_table(items, ws.slot_ranges, ws, gsnr)
-    params = L.upload(ptab, dev)
+    raw, classes = _param_table(items, ws.slot_ranges, ws, gsnr)
+    _launch_step(ws, raw, len(items), update_norm_ema)
+    ws.last_items = [it.p for it in items]   # row i of the "stat" buffer is items[i]
+    return StepPlan(items, raw, classes, gsnr, leaf_epoch(),
+                    [tuple(it.st[key] for key in _MOMENTS) for it in items])
+
+
+def run_planned_step(plan: StepPlan, gptrs: np.ndarray, ws: Workspace,
+                     update_norm_ema: bool) -> None:
+    """The next plain step of ``plan``'s parameters: every step counter has
+    advanced by one (the caller checked that no refresh or phase change is
+    due and that the gradients have the planned layout), the gradients are
+    at ``gptrs``.  Rewrites those addresses and the classes' step scalars in
+    the table and launches the same kernels as run_step."""
+    raw = plan.raw
+    a, b, _ = _BLOCKS["u8"]
+    u8 = raw[:, a:b].view(np.uint64)
+    u8[:, 1] = gptrs   # gradient the moments see (no filter or noise)
+    u8[:, 2] = gptrs   # raw gradient
+    for cl in plan.classes:
+        cl.step += 1
+        if cl.phase2:
+            cl.scao_step += 1
+        _set_class_scalars(raw, cl, plan.gsnr)
+    _launch_step(ws, raw, len(plan.items), update_norm_ema)
+
+
+def _launch_step(ws: Workspace, raw: np.ndarray, n: int, update_norm_ema: bool) -> None:
+    """Upload the parameter table and launch one step's kernels."""
+    dev = ws.device
+    params = ws.stage_params(raw)
     slots = ws.buf("slots", max(ws.nslots, 1) * 8 * L.SLOT_WIDTH)
-    stat = ws.buf("stat", len(items) * L.PARAM_STAT.itemsize)
+    stat = ws.buf("stat", n * L.PARAM_STAT.itemsize)
     s = L.stream_ptr(dev)
     T, N = ws.tasks, ws.ntasks
     P, S, SL = params.data_ptr(), stat.data_ptr(), slots.data_ptr()
@@ -711,17 +829,17 @@ def run_step(items: list[PItem], ws: Workspace, update_norm_ema: bool,
         _call("scao_kron_lift", tp("lift"), N["lift"], LF, s)
     if N["dred"]:
         _call("scao_diag_reduce", tp("dred"), N["dred"], P, SL, s)
-    _call("scao_step_finalize", P, len(items), SL, S, ws.runtime.data_ptr(), 0,
-           1 if update_norm_ema else 0, len(items), s)
+    _call("scao_step_finalize", P, n, SL, S, ws.runtime.data_ptr(), 0,
+           1 if update_norm_ema else 0, n, s)
     for var in range(16):
         if N[f"apply{var}"]:
             _call("scao_kron_apply", tp(f"apply{var}"), N[f"apply{var}"], LF, P, S, SL, var, s)
     if N["dapply"]:
         _call("scao_diag_apply", tp("dapply"), N["dapply"], P, S, SL, s)
     if N["lars"]:
-        _call("scao_step_finalize", P, len(items), SL, S, 0, 1, 0, len(items), s)
+        _call("scao_step_finalize", P, n, SL, S, 0, 1, 0, n, s)
         _call("scao_lars_write", tp("lars"), N["lars"], P, S, s)
-    ws.last_params = params   # keep descriptors alive until the next step
+    ws.finish_params()
 
 
 # --------------------------------------------------------------------------

@@ -21,6 +21,7 @@ from __future__ import annotations
 import warnings
 from typing import Callable, Iterable, Optional
 
+import numpy as np
 import torch
 from torch import Tensor
 from torch.optim import Optimizer
@@ -211,6 +212,7 @@ class SCAO(Optimizer):
         self._adaptive_rank = adaptive_rank
         self._in_warmup_global = True
         self._ws: Optional[Workspace] = None
+        self._plan = None   # engine.StepPlan of the last plain step, or None
 
     # ---------------------------------------------------------- runtime --
     @property
@@ -315,15 +317,22 @@ class SCAO(Optimizer):
             wmax = max((g.get("warmup_steps", 100) for g in self.param_groups), default=100)
             self._in_warmup_global = self._global_step <= wmax
 
-        items, refresh, filtered = [], [], []
-        for group, p in active:
-            it = self._plan_param(group, p, refresh, filtered)
-            items.append(it)
-        self._filter_and_noise(items, filtered)
-        engine.refresh(refresh)
         gsnr = self._gsnr_threshold if self._use_gsnr_clip else None
-        if ws is not None:
-            engine.run_step(items, ws, update_norm_ema=not host_norms, gsnr=gsnr)
+        if not self._planned_step(ws, host_norms, gsnr):
+            self._plan = None
+            items, refresh, filtered = [], [], []
+            for group, p in active:
+                it = self._plan_param(group, p, refresh, filtered)
+                items.append(it)
+            self._filter_and_noise(items, filtered)
+            engine.refresh(refresh)
+            if ws is not None:
+                plan = engine.run_step(items, ws, update_norm_ema=not host_norms, gsnr=gsnr)
+                if (plan is not None and not host_norms and not refresh and not filtered
+                        and self._noise_std <= 1e-9
+                        and all(it.graw is it.p.grad and it.msrc is None and it.gmom is None
+                                for it in items)):
+                    self._plan = plan
 
         self._noise_std *= self._noise_anneal
         if self._lookahead_k > 0 and self._global_step % self._lookahead_k == 0:
@@ -337,6 +346,75 @@ class SCAO(Optimizer):
             for cb in self._callbacks:
                 cb(metrics)
         return loss
+
+    def _planned_step(self, ws, host_norms: bool, gsnr) -> bool:
+        """The next step of the last plain step's parameters, when nothing
+        but the step counters changes: the same parameters (same groups, same
+        order) have gradients, contiguous and with the planned alignment; the
+        moment tensors and the parameters' storage are the planned ones; no
+        refresh is due and no phase changes (a Phase-1 class stays inside its
+        warm-up, a Phase-2 class keeps its LARS setting); no filter, noise or
+        host norms.  Then the host bookkeeping of _plan_param reduces to the
+        counters (every planned item had step t, now t + 1) and the launch
+        reuses the planned parameter table (engine.run_planned_step).
+        Returns False, changing nothing, when any of this does not hold."""
+        plan = self._plan
+        if (plan is None or ws is None or host_norms or self._sparsity > 0.0
+                or self._noise_std > 1e-9 or plan.gsnr != gsnr
+                or plan.epoch != engine.leaf_epoch()):
+            return False
+        items = plan.items
+        n = len(items)
+        gptrs = np.empty(n, dtype=np.uint64)
+        grads = []
+        i = 0
+        for g in self.param_groups:
+            for p in g["params"]:
+                gr = p.grad
+                if gr is None:
+                    continue
+                if i >= n:
+                    return False
+                it = items[i]
+                if it.p is not p or it.group is not g or gr.is_sparse or not gr.is_contiguous():
+                    return False
+                ptr = gr.data_ptr()
+                if (it.aligned and ptr & 15) or it.ptrs[0] != p.data_ptr():
+                    return False
+                gptrs[i] = ptr
+                grads.append(gr)
+                i += 1
+        if i != n:
+            return False
+        for it, moms in zip(items, plan.moments):
+            st = it.st
+            if (st["step"] != it.step or st["exp_avg"] is not moms[0]
+                    or st["exp_avg_sq"] is not moms[1] or st["exp_avg_diff"] is not moms[2]
+                    or st["prev_grad"] is not moms[3]):
+                return False
+        if plan.min_pre is None:   # precond_step only moves with a refresh
+            plan.min_pre = [min(items[r].pre.precond_step for r in cl.rows)
+                            for cl in plan.classes]
+        for cl, min_pre in zip(plan.classes, plan.min_pre):
+            g, t = cl.group, cl.step + 1
+            if t % g["precond_freq"] == 0:
+                return False
+            if cl.phase2:
+                if (t <= g["warmup_steps"] or cl.lars != (g["lars_coeff"] > 0)
+                        or min_pre < g["min_precond_updates"]):
+                    return False
+            elif t > g["warmup_steps"]:
+                return False
+        for it, gr in zip(items, grads):
+            st = it.st
+            st["step"] += 1
+            it.step += 1
+            if it.phase2:
+                st["scao_step"] += 1
+                it.scao_step += 1
+            it.graw = gr
+        engine.run_planned_step(plan, gptrs, ws, update_norm_ema=True)
+        return True
 
     def _filter_and_noise(self, items: list, filtered: list) -> None:
         """The gradient the moments see (reference :533-545): the filtered
@@ -461,6 +539,7 @@ class SCAO(Optimizer):
         """reference :758-776.  Preconditioner objects of another type (the
         reference's, or the CPU oracle's) are rebuilt from the parameter and
         its group before the portable ``_scao_precond`` entry is loaded."""
+        self._plan = None
         sd = dict(state_dict)
         extra = sd.pop("_scao_precond", {})
         rt = sd.pop("_scao_runtime", {})

@@ -165,3 +165,43 @@ class IdenticalPostEma:
                 leaf.L_ema.copy_(ref.L_ema)
                 leaf.R_ema.copy_(ref.R_ema)
             self.checked += 1
+
+
+def lars_exact(rec: dict, wd: float, c: float):
+    """The reference's LARS trust (scao/optimizer.py:371-377, float32 tensor
+    arithmetic on the two norms) with correctly rounded float32 norms of the
+    decayed parameter and the update recorded by the oracle (RECORD).
+    Returns (trust, |p|, |u|)."""
+    pn = rec["pdec"].double().norm().float()
+    un = rec["upd"].double().norm().float()
+    if float(pn) == 0.0 or float(un) == 0.0:
+        return 1.0, float(pn), float(un)
+    return float(c * pn / (un + wd * pn + 1e-8)), float(pn), float(un)
+
+
+def norm_allowance(rec: dict, trust_exact: float, lr: float) -> float:
+    """E_norm: how far the reference's own float32 norms move its update,
+    max |lr * (trust - trust_exact) * u| over the tensor (the update is
+    p_dec - lr * trust * u; only the trust depends on the norms)."""
+    return lr * abs(rec["trust"] - trust_exact) * rec["upd"].double().abs().max().item()
+
+
+def step_stats(opt) -> dict:
+    """The kernels' per-parameter intermediates of opt's last step, keyed by
+    id(parameter): the PARAM_STAT row (trust, clip, nu, unorm, pnorm, gnorm,
+    alpha, ...) and, for parameters with LARS, the staged update u read from
+    the step's workspace."""
+    import numpy as np
+    from scao_amd import _lib as L
+    out = {}
+    ws = opt._ws
+    raw = ws._bufs["stat"].cpu().numpy().tobytes()
+    rows = np.frombuffer(raw[:len(ws.last_items) * L.PARAM_STAT.itemsize], dtype=L.PARAM_STAT)
+    for i, (p, row) in enumerate(zip(ws.last_items, rows)):
+        d = {n: float(row[n]) for n in L.PARAM_STAT.names if n != "pad0"}
+        off = ws.upd_offsets.get(i)
+        if off is not None:
+            flat = ws._bufs["upd"].view(torch.float32)
+            d["upd"] = flat[off:off + p.numel()].view(p.shape).cpu()
+        out[id(p)] = d
+    return out

@@ -254,7 +254,8 @@ def test_param_table_fields_and_state_checks():
         it.ptrs = E._item_ptrs(it)
     ws.upd_offsets, ws.upd_total = {0: 0, 2: 96}, 156
     ranges = [(0, 1, 1, 2), (2, 2, 2, 2), (2, 3, 3, 4)]
-    tab = E._param_table(items, ranges, ws, None)
+    raw, classes = E._param_table(items, ranges, ws, None)
+    tab = raw.view(L.PARAM_DESC).reshape(len(items))
     f4 = np.float32
     assert tab["bc1"][0] == f4(1 - 0.9 ** 30) and tab["bc1"][1] == 0.0
     assert tab["blend"][0] == f4(0.5) and tab["omblend"][2] == f4(0.5)
@@ -275,6 +276,57 @@ def test_param_table_fields_and_state_checks():
     items[1].st["exp_avg"] = torch.zeros(32)[::2]
     with pytest.raises(ValueError, match="contiguous float32"):
         E._param_table(items, ranges, ws, None)
+
+
+def test_planned_step_table_matches_a_fresh_build():
+    """A planned step (engine.run_planned_step) rewrites only the gradient
+    addresses and each class's step scalars of the last table: after one
+    step of every counter its table is byte for byte what _param_table
+    builds from scratch at the next step (bias corrections, blend, Adam
+    alpha, flags), for Phase-1 and Phase-2 rows of two groups, a
+    diagonal-mode row's bias factor included."""
+    from scao_amd.engine import PItem
+    g1 = {"lr": 0.1, "betas": (0.9, 0.999), "beta3": 0.99, "weight_decay": 0.01, "eps": 1e-8,
+          "tau": 1.0, "lars_coeff": 1e-3, "blend_steps": 50}
+    g2 = dict(g1, lr=0.05, tau=None, lars_coeff=0.0, weight_decay=0.0, blend_steps=0)
+    ws = E.Workspace(torch.device("cpu"))
+
+    class Pre:
+        diag_ema = torch.zeros(16)
+        _diag_bias_factor = 0.25
+
+    def build(step_shift, grads):
+        items = []
+        spec = [((8, 12), True, g1, False), ((16,), False, g1, False), ((4, 3, 5), True, g2, False),
+                ((16,), True, g1, True)]
+        for i, (shape, phase2, g, diag) in enumerate(spec):
+            it = PItem(p=params[i], graw=grads[i], gmom=None, st=states[i], group=g,
+                       pre=Pre() if diag else None, phase2=phase2,
+                       step=(30 if phase2 else 3) + step_shift, scao_step=25 + step_shift,
+                       lars=phase2 and g["lars_coeff"] > 0, diag=diag)
+            it.ptrs = E._item_ptrs(it)
+            items.append(it)
+        return items
+
+    shapes = [(8, 12), (16,), (4, 3, 5), (16,)]
+    params = [torch.zeros(s) for s in shapes]
+    states = [{k: torch.zeros(s) for k in E._MOMENTS} for s in shapes]
+    ws.upd_offsets, ws.upd_total = {0: 0, 3: 96}, 112
+    ranges = [(0, 1, 1, 2), (2, 2, 2, 2), (2, 3, 3, 4), (4, 5, 5, 6)]
+    grads0 = [torch.zeros(s) for s in shapes]
+    grads1 = [torch.zeros(s) for s in shapes]
+    raw, classes = E._param_table(build(0, grads0), ranges, ws, 0.5)
+    assert len(classes) == 3
+    gptrs = np.array([g.data_ptr() for g in grads1], dtype=np.uint64)
+    a, b, _ = E._BLOCKS["u8"]
+    raw[:, a:b].view(np.uint64)[:, 1] = gptrs
+    raw[:, a:b].view(np.uint64)[:, 2] = gptrs
+    for cl in classes:
+        cl.step += 1
+        cl.scao_step += cl.phase2
+        E._set_class_scalars(raw, cl, 0.5)
+    fresh, _ = E._param_table(build(1, grads1), ranges, ws, 0.5)
+    assert raw.tobytes() == fresh.tobytes()
 
 
 def test_structure_cache_matches_fresh_builds():
