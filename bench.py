@@ -65,6 +65,14 @@ PROFILE = dict(use_int8_ema=True, sparsity=0.0, noise_std_init=0.0, async_precon
                lookahead_k=0)
 
 
+_T0 = time.perf_counter()
+
+
+def progress(msg: str) -> None:
+    """A progress line on stderr (the JSON result is the only stdout line)."""
+    print(f"bench [{time.perf_counter() - _T0:7.1f} s] {msg}", file=sys.stderr, flush=True)
+
+
 def shapes_of(cfg):
     pre, adam = [], []
     for layer in range(cfg["layers"]):
@@ -189,13 +197,81 @@ def cpu_baseline(cfg, args):
         n += 1
     dt = (time.perf_counter() - t0) / n
     npre = sum(p.numel() for p in pre)
+    progress(f"CPU steady steps: {dt * 1e3:.0f} ms per step")
+    legs = {"phase1": _cpu_phase1(params, cfg, grads, args)}
+    progress("CPU Phase-1 leg done")
+    legs["refresh"] = _cpu_refresh(opt, pre, grads[:len(pre)], args)
+    progress("CPU refresh leg done")
     return {"value": nparam / dt, "unit": "params/s", "cores": cores, "kind": "port",
+            "legs": legs,
             "sample": f"oracle (reference algorithm, torch CPU fp32) steady Phase-2 step on one "
                       f"layer's {len(pre)} preconditioned matrices ({npre / 1e6:.2f}M params) "
                       f"plus 1/{cfg['layers']} of the Adam-path group "
                       f"({(nparam - npre) / 1e6:.2f}M params): {nparam / 1e6:.2f}M params, "
                       f"{n} steps, {dt * 1e3:.0f} ms/step, {cores} threads, "
                       f"{host_description()}"}
+
+
+def _cpu_phase1(params, cfg, grads, args) -> dict:
+    """The oracle's Phase-1 (Adam) step on the same sample
+    (scao/optimizer.py:567-578): a second optimizer whose warm-up never ends."""
+    import torch
+    from oracle import scao_ref as R
+    copies = [torch.nn.Parameter(p.detach().clone()) for p in params]
+    for c, g in zip(copies, grads):
+        c.grad = g
+    opt = R.RefSCAO(copies, k_min=cfg["k"], k_max=cfg["k"], max_precond_dim=cfg["D"],
+                    warmup_steps=10 ** 9, precond_freq=10 ** 9, **PROFILE)
+    opt.step()
+    t0 = time.perf_counter()
+    n = 0
+    while n < 2 or (time.perf_counter() - t0 < args.cpu_seconds / 2 and n < 1000):
+        opt.step()
+        n += 1
+    dt = (time.perf_counter() - t0) / n
+    nparam = sum(p.numel() for p in params)
+    return {"value": nparam / dt, "unit": "params/s", "ms_per_step": dt * 1e3, "steps": n,
+            "sample": "the same params, Phase 1 (Adam(W)) steady steps"}
+
+
+def _cpu_refresh(opt, pre_params, grads, args) -> dict:
+    """The oracle's curvature refresh (scao/preconditioner.py:297-451) of the
+    sample's preconditioned blocks, one block at a time until the time budget
+    is spent (at least one), split as the reference computes it: Gram ->
+    int8 EMA -> requantise, then debias/shift, eigh, flip/clamp and adaptive
+    rank with rank momentum."""
+    import torch
+    from oracle import scao_ref as R
+
+    def leaves(pre, g2):
+        if pre.use_block_diagonal:
+            for blk, gb, _ in pre._slices(g2):
+                yield from leaves(blk, gb)
+        elif pre.use_kronecker:
+            yield pre, g2
+
+    t_ema = t_eig = 0.0
+    n, start = 0, time.perf_counter()
+    shapes = []
+    for p, g in zip(pre_params, grads):
+        for leaf, gb in leaves(opt.state[p]["preconditioner"], R.to_2d(g)[0]):
+            if n and time.perf_counter() - start > args.cpu_seconds:
+                break
+            leaf.precond_step += 1
+            t0 = time.perf_counter()
+            leaf._update_ema(gb)
+            t1 = time.perf_counter()
+            leaf._update_eigenfactors(1.0 - leaf.rho ** leaf.precond_step)
+            t2 = time.perf_counter()
+            t_ema += t1 - t0
+            t_eig += t2 - t1
+            n += 1
+            shapes.append(f"{leaf.m}x{leaf.n}")
+    return {"blocks": n, "block_shapes": sorted(set(shapes)),
+            "gram_ema_requant_s": t_ema, "eigh_rank_s": t_eig,
+            "per_block_ms": (t_ema + t_eig) / n * 1e3,
+            "sample": "update_curvature of the sample's Kronecker blocks in order, until the "
+                      "time budget is spent"}
 
 
 def pmc_summary(fetch_csv: str, write_csv: str, config: str, copy_mib: int, cmd: str) -> str:
@@ -495,10 +571,13 @@ def main():
             g = torch.where(hit, g * mult, g)
         return g
 
-    grad_sets = [[make_grad(p.shape) for p in allp] for _ in range(2)]
+    # two gradient sets, alternated step by step; one where a second would
+    # take more than 16 GB (llama8b: 28 GB beside ~190 GB of optimizer state)
+    nsets = 2 if 4 * nparams <= (16 << 30) else 1
+    grad_sets = [[make_grad(p.shape) for p in allp] for _ in range(nsets)]
 
     def set_grads(i):
-        for p, gr in zip(allp, grad_sets[i % 2]):
+        for p, gr in zip(allp, grad_sets[i % nsets]):
             p.grad = gr
 
     if args.no_refresh:
@@ -532,6 +611,7 @@ def main():
         opt.step()
         step[0] += 1
 
+    progress(f"{args.config}: {nparams / 1e6:.0f}M params, gradients ready")
     t_first = timed(one)                      # step 1: state allocation + Phase 1
     t_phase1 = timed(one)                     # step 2: Phase 1 (Adam) everywhere
     t_refresh_first = timed(one)              # step 3: Phase 1 + the first curvature refresh
@@ -540,9 +620,11 @@ def main():
     engine.TIMING = {}
     t_refresh = timed(one)                    # step 6: Phase 2 + a refresh (steady state)
     refresh_parts = engine.timing_summary()
+    refresh_routes = dict(engine.LAST_REFRESH_ROUTES)
     if args.no_refresh:                       # steps 3 and 6 were plain steps
         t_refresh, t_refresh_first, refresh_parts = None, None, {}
     engine.TIMING = None
+    progress(f"first steps and a refresh done (refresh step {t_refresh} ms)")
     for g in opt.param_groups:
         g["precond_freq"] = 10 ** 9           # steady state: no refresh in the timed region
     for _ in range(args.warmup):
@@ -568,6 +650,7 @@ def main():
     ms_instrumented = (time.perf_counter() - t1) * 1e3 / diag_steps
     per_kernel = engine.timing_summary()
     engine.TIMING = None
+    progress(f"timed steps done: {ms:.2f} ms per step")
     assert all(opt.state[p].get("scao_phase_started") for p in pre_p), "not in Phase 2"
 
     # per-step distribution (the survey's definition of the metric): an event
@@ -613,26 +696,62 @@ def main():
                   "filter_GBps_at_20B_per_elem": (20.0 * nparams / (f_ms / 1e3) / 1e9
                                                   if f_ms else None)}
 
-    # steady Phase-1 steps: a second optimizer over the same parameters whose
-    # warm-up never ends (no refresh), median of per-step event timings
+    progress("per-step distribution and filter diagnostic done")
+    # steady Phase-1 steps: the same optimizer with its warm-up held open
+    # (every parameter takes the Adam(W) step, no refresh; a second optimizer
+    # would need a second copy of the state), median of per-step event timings
     p1_ms = None
     if args.phase1_steps > 0:
-        opt1 = scao_amd.SCAO([{"params": pre_p}, {"params": adam_p}], k_min=cfg["k"],
-                             k_max=cfg["k"], max_precond_dim=cfg["D"], warmup_steps=10 ** 9,
-                             precond_freq=10 ** 9, min_precond_updates=0, **PROFILE)
+        warm = opt.param_groups[0]["warmup_steps"]
+        opt.param_groups[0]["warmup_steps"] = 10 ** 9
         p1 = []
         for i in range(2 + args.phase1_steps):
-            set_grads(i)
+            set_grads(step[0])
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             e0.record()
-            opt1.step()
+            opt.step()
             e1.record()
+            step[0] += 1
             torch.cuda.synchronize()
             if i >= 2:
                 p1.append(e0.elapsed_time(e1))
+        opt.param_groups[0]["warmup_steps"] = warm
         p1.sort()
         p1_ms = p1[len(p1) // 2]
-        del opt1
+
+    # a refresh whose EMAs get off-diagonal codes: the gradients x16
+    # (N(0, 0.016^2), exact and undone afterwards), as with the small
+    # configurations' 0.02-scale gradients; the eigen stage then runs the
+    # solver on every factor instead of the diagonal closed form
+    dense = None
+    if not args.no_refresh:
+        progress("Phase-1 steps done; dense-EMA refreshes")
+        gs = grad_sets[step[0] % nsets]
+        for gr in gs:
+            gr.mul_(16.0)
+        opt.param_groups[0]["precond_freq"] = 1
+        # the first solver refresh of the process loads the library GEMMs'
+        # code objects (a few hundred ms once); the second one is timed
+        t_dense_first = timed(one)
+        if nsets > 1:   # the other set (one set stays scaled)
+            for gr in grad_sets[step[0] % nsets]:
+                gr.mul_(16.0)
+        engine.TIMING = {}
+        torch.cuda.reset_peak_memory_stats(dev)
+        mem0 = torch.cuda.memory_allocated(dev)
+        t_dense = timed(one)
+        parts = engine.timing_summary()
+        engine.TIMING = None
+        peak = torch.cuda.max_memory_allocated(dev) - mem0
+        opt.param_groups[0]["precond_freq"] = 10 ** 9
+        for gs in grad_sets:
+            for gr in gs:
+                gr.div_(16.0)
+        dense = {"step_ms": t_dense, "first_step_ms": t_dense_first,
+                 "routes": dict(engine.LAST_REFRESH_ROUTES),
+                 "peak_extra_bytes": peak,
+                 "parts_ms": {k: {"count": c, "mean": m_, "total": t}
+                              for k, (c, m_, t) in parts.items()}}
 
     # ---- roofline of the dominant kernel --------------------------------
     dom = args.dominant
@@ -676,6 +795,8 @@ def main():
         "refresh_first_step_ms": t_refresh_first,
         "refresh_parts_ms": {k: {"count": c, "mean": m_, "total": t}
                              for k, (c, m_, t) in refresh_parts.items()},
+        "refresh_routes": refresh_routes,
+        "refresh_dense_ema": dense,
         "first_step_ms": t_first,
         "default_sparse_filter": sparse,
         "step_roofline": {"alg_bytes": step_bytes, "alg_flops": step_flops,
@@ -685,7 +806,10 @@ def main():
         "params": nparams, "precond_params": n_pre, "blocks": len(n_leaf),
         "device": torch.cuda.get_device_name(0),
     }
+    progress("GPU part done; CPU baseline")
     cpu = cpu_baseline(cfg, args) if args.cpu_baseline else None
+    if cpu is not None:   # the refresh and Phase-1 legs go to details
+        details["cpu_baseline_legs"] = cpu.pop("legs")
     out = {
         "metric": "SCAO.step ms + params/sec at Llama-1B shape; % of MFMA / HBM roofline",
         "value": nparams / (ms / 1e3),
@@ -709,6 +833,7 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "details": {"phase1_step_ms": p1_ms, "refresh_step_ms": t_refresh,
+                    "refresh_dense_ema_step_ms": dense["step_ms"] if dense else None,
                     "step_median_ms": step_dist["median_ms"], "step_p90_ms": step_dist["p90_ms"],
                     "step_hbm_frac": details["step_roofline"]["hbm_frac"],
                     "steady_step_default_filter_noise_ms": (sparse["steady_step_ms"]

@@ -1434,9 +1434,12 @@ __device__ __forceinline__ double start_val(uint32_t vid, int row) {
 
 // Prefetch distance (steps) of the band solve: the band values entering the
 // window and the U rows of the back substitution are loaded this many steps
-// before their use (a step takes a few thousand cycles, so 4 cover the memory
-// latency; fewer registers leave room for five waves per SIMD).
-constexpr int PF = 4;
+// before their use (a step takes a few thousand cycles, so 2 cover the memory
+// latency).  At 4 the kernel needs more registers than five waves per SIMD
+// leave and spills to scratch, whose allocation by the runtime can fail when
+// device memory is nearly full; at 2 it spills nothing and runs as fast
+// (38.7 ms against 40.5 ms for 4 at four waves, 480 x 2048^2, kq = 64).
+constexpr int PF = 2;
 
 // Value entering lane L's slot 0 at the end of elimination step j: row
 // j + WR, column j + 1 + ((L - (j mod WC) - 1) mod WC).
@@ -1787,7 +1790,7 @@ __device__ __forceinline__ double block_sum_all(double x, double* red /* >= 5 */
 
 // Gram-Schmidt (twice) of vectors [cs, ce) of xm against the earlier ones of
 // the cluster, in place.
-__device__ void cluster_mgs(double* xm, int n, int cs, int ce, double* red) {
+__device__ __forceinline__ void cluster_mgs(double* xm, int n, int cs, int ce, double* red) {
   for (int i = cs + 1; i < ce; ++i) {
     double* xi = xm + (int64_t)i * n;
     for (int pass = 0; pass < 2; ++pass) {
@@ -1824,7 +1827,7 @@ struct CholQrLds {
   int fail;
 };
 
-__device__ bool cholqr_pass(double* xm, int n, int cs, int c, CholQrLds& S) {
+__device__ __forceinline__ bool cholqr_pass(double* xm, int n, int cs, int c, CholQrLds& S) {
   const int tid = threadIdx.x;
   // 1. G = X^T X: thread t accumulates cells t, t + 256, ... (a <= b only)
   constexpr int NQ = CQ * CQ / 256;
@@ -1877,20 +1880,17 @@ __device__ bool cholqr_pass(double* xm, int n, int cs, int c, CholQrLds& S) {
   }
   __syncthreads();
   if (S.fail) return false;
-  // 3. X <- X R^-1: row r of X, forward substitution against R's columns
+  // 3. X <- X R^-1: row r of X, forward substitution against R's columns.
+  // The solved entries are read back from xm (this thread wrote them), not
+  // held in a private array: a c-long array of doubles would spill to
+  // scratch, and the runtime's scratch allocation for it can fail when
+  // device memory is nearly full.
   for (int r = tid; r < n; r += 256) {
-    double x[CQ];
-#pragma unroll
-    for (int v = 0; v < CQ; ++v) x[v] = v < c ? xm[(int64_t)(cs + v) * n + r] : 0.0;
-#pragma unroll
-    for (int j = 0; j < CQ; ++j) {
-      if (j < c) {
-        double sacc = x[j];
-#pragma unroll
-        for (int i = 0; i < j; ++i) sacc = fma(-x[i], S.G[i][j], sacc);
-        x[j] = sacc / S.G[j][j];
-        xm[(int64_t)(cs + j) * n + r] = x[j];
-      }
+    double* xr = xm + (int64_t)cs * n + r;
+    for (int j = 0; j < c; ++j) {
+      double sacc = xr[(int64_t)j * n];
+      for (int i = 0; i < j; ++i) sacc = fma(-xr[(int64_t)i * n], S.G[i][j], sacc);
+      xr[(int64_t)j * n] = sacc / S.G[j][j];
     }
   }
   __syncthreads();

@@ -34,6 +34,17 @@ BW = L.EIG_BANDW
 MAX_BATCH = 65535   # matrices per call: the batch is a grid dimension
 
 
+def solver_fits(n: int) -> bool:
+    """Whether topk_eigh takes an n x n factor with kernels that need no
+    scratch memory: every kernel of the solver keeps its state in registers
+    and LDS except the back-transformation when its Z slices exceed the
+    register file, which happens above 2048 rows unless n is a multiple of
+    16 (kq is, see topk_eigh) and above 4096 rows in any case.  Scratch is
+    allocated by the runtime at launch and that can fail when device memory
+    is nearly full."""
+    return 1 <= n <= 2048 or (n <= 4096 and n % 16 == 0)
+
+
 def panels(n: int) -> list:
     """Column origins of the stage-1 panels of an n x n matrix."""
     return list(range(0, n - NB, NB))
@@ -132,6 +143,8 @@ def topk_eigh(X: Tensor, kq: int):
     B, n, _ = X.shape
     if not 1 <= kq <= n:
         raise ValueError(f"topk_eigh: kq={kq} outside [1, {n}]")
+    want = kq
+    kq = min(n, -(-kq // 16) * 16)   # whole 16-column slices: the exact back-transformation
     dev = X.device
     s = L.stream_ptr(dev)
     pcs, Tall, orig, d, e = _reduce(X)
@@ -149,4 +162,6 @@ def topk_eigh(X: Tensor, kq: int):
     if pcs:
         L.call("scao_eig_back_transform", X.data_ptr(), n * n, n, B, Tall.data_ptr(),
                Z.data_ptr(), n * kq, kq, s)
+    if kq != want:
+        w, Z = w[:, :want].contiguous(), Z[:, :, :want].contiguous()
     return w, Z, total

@@ -1031,10 +1031,11 @@ def sparse_filter(entries) -> list:
 REFRESH_SCRATCH_BYTES = 2 << 30   # fp32 EMA staging per refresh chunk (int8 mode)
 # The eigen stage runs scao_amd.eigen.topk_eigh (two-stage reduction,
 # bisection, inverse iteration: only the k_max vectors a factor can keep) for
-# factors up to HIP_EIGEN_MAX_DIM rows, and torch.linalg.eigh on the device
-# (rocSOLVER syevd) above that.  Factors whose eigh input is exactly diagonal
-# (up to HIP_EIGEN_MAX_DIM) take the closed form of scao_eig_diag instead.
-HIP_EIGEN_MAX_DIM = 4096 + L.EIG_BAND
+# the sizes eigen.solver_fits accepts (up to 4096 rows), and
+# torch.linalg.eigh on the device (rocSOLVER syevd) for the others.  Factors
+# whose eigh input is exactly diagonal, up to DIAG_MAX_DIM rows, take the
+# closed form of scao_eig_diag instead.
+DIAG_MAX_DIM = 4096 + L.EIG_BAND
 EIGEN_BATCH_BYTES = 8 << 30       # stacked eigen-stage inputs per launch (HIP solver), at most
 EIGEN_BATCH_FREE_FRACTION = 4     # ... and at most 1/4 of the device memory free at the refresh
 EIGH_BATCH_BYTES = 1 << 30        # stacked eigh inputs per launch (library solver)
@@ -1044,15 +1045,18 @@ EIGH_BATCH_BYTES = 1 << 30        # stacked eigh inputs per launch (library solv
 # reference's own post-EMA state, so the eigen stage and the step that follows
 # are compared from identical inputs.
 AFTER_EMA_HOOK = None
+# factors per eigen-stage route in the last refresh (reported by bench.py)
+LAST_REFRESH_ROUTES: dict = {}
 
 
 def eigen_route(dim: int, diagonal: bool) -> str:
-    """Which solver takes an n x n factor: "diag" (exactly diagonal input,
-    closed form), "hip" (the batched HIP solver) or "library"
-    (torch.linalg.eigh on the device) above HIP_EIGEN_MAX_DIM."""
-    if dim > HIP_EIGEN_MAX_DIM:
-        return "library"
-    return "diag" if diagonal else "hip"
+    """Which solver takes an n x n factor: "diag" (exactly diagonal input up
+    to DIAG_MAX_DIM rows, closed form), "hip" (the batched HIP solver, sizes
+    eigen.solver_fits accepts) or "library" (torch.linalg.eigh on the
+    device)."""
+    if diagonal and dim <= DIAG_MAX_DIM:
+        return "diag"
+    return "hip" if eigen.solver_fits(dim) else "library"
 
 
 def refresh(entries, eigen_only: bool = False, ema_only: bool = False) -> None:
@@ -1158,6 +1162,7 @@ def _refresh_kron(kron, dev, s, eigen_only=False, ema_only=False):
         jobs.setdefault(leaf.m, []).append((leaf, 0))
         jobs.setdefault(leaf.n, []).append((leaf, 1))
     spectra = {}   # (id(leaf), side) -> (S_desc, U_desc, total)
+    LAST_REFRESH_ROUTES.clear()
     eig_timer = _mark("refresh:eigh+rank")
     eig_timer.__enter__()
     diagonal = _diagonal_factors(jobs, dev, s)
@@ -1186,6 +1191,8 @@ def _refresh_kron(kron, dev, s, eigen_only=False, ema_only=False):
             for key in lst:
                 r = eigen_route(dim, (id(key[0]), key[1]) in diagonal)
                 routes.setdefault(r, []).append(key)
+            for r, keys in routes.items():
+                LAST_REFRESH_ROUTES[r] = LAST_REFRESH_ROUTES.get(r, 0) + len(keys)
             for route, keys in routes.items():
                 budget = EIGH_BATCH_BYTES if route == "library" else hip_budget
                 per = len(keys) if route == "diag" else \
@@ -1371,10 +1378,10 @@ def _eig_inputs(part, dim, dev, s) -> Tensor:
 
 
 def _diagonal_factors(jobs: dict, dev, s) -> set:
-    """(id(leaf), side) of every factor up to HIP_EIGEN_MAX_DIM rows whose EMA
+    """(id(leaf), side) of every factor up to DIAG_MAX_DIM rows whose EMA
     has no non-zero off-diagonal entry: one scan of the codes on the device
     and one read of the flags."""
-    keys = [key for dim, lst in jobs.items() if dim <= HIP_EIGEN_MAX_DIM for key in lst]
+    keys = [key for dim, lst in jobs.items() if dim <= DIAG_MAX_DIM for key in lst]
     if not keys:
         return set()
     dims = [key[0].m if key[1] == 0 else key[0].n for key in keys]

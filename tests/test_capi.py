@@ -82,7 +82,7 @@ def test_eig_entry_points_reject_oversized_n():
             rc = getattr(lib, name)(*args)
             assert rc == 1, (name, n, rc)
     from scao_amd import engine
-    assert engine.HIP_EIGEN_MAX_DIM == 4096 + L.EIG_BAND
+    assert engine.DIAG_MAX_DIM == 4096 + L.EIG_BAND
 
 
 def test_missing_library_raises(monkeypatch, tmp_path):

@@ -561,15 +561,23 @@ def test_adaptive_rank_from_top_eigenvalues_matches_full_spectrum():
 
 def test_eigen_route_by_size_and_shape():
     """Which solver a refresh gives an n x n factor: the closed form for an
-    exactly diagonal input, the HIP solver up to 4096 + SCAO_EIG_BAND rows,
-    the library eigh above that (diagonal or not: the closed form's LDS
-    arrays stop at the same size)."""
-    from scao_amd import engine
-    lim = engine.HIP_EIGEN_MAX_DIM
+    exactly diagonal input up to 4096 + SCAO_EIG_BAND rows; the HIP solver
+    for the sizes whose kernels need no scratch memory (up to 2048 rows, and
+    multiples of 16 up to 4096); the library eigh for the rest."""
+    from scao_amd import eigen, engine
+    lim = engine.DIAG_MAX_DIM
+    assert lim == 4096 + 16
     assert engine.eigen_route(2048, True) == "diag"
     assert engine.eigen_route(2048, False) == "hip"
     assert engine.eigen_route(lim, True) == "diag"
-    assert engine.eigen_route(lim, False) == "hip"
-    assert engine.eigen_route(lim + 1, False) == "library"
+    assert engine.eigen_route(lim, False) == "library"
+    assert engine.eigen_route(4096, False) == "hip"
+    assert engine.eigen_route(4097, False) == "library"
     assert engine.eigen_route(lim + 1, True) == "library"
     assert engine.eigen_route(1, True) == "diag"
+    # ragged sizes stay on the HIP solver up to 2048 rows, whole 16-row
+    # multiples up to 4096
+    for n, fits in ((1, True), (2047, True), (2048, True), (2049, False), (2064, True),
+                    (3000, False), (3840, True), (4095, False), (4096, True), (4112, False)):
+        assert eigen.solver_fits(n) == fits, n
+        assert engine.eigen_route(n, False) == ("hip" if fits else "library"), n
