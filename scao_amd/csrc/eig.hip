@@ -1897,10 +1897,91 @@ __device__ __forceinline__ bool cholqr_pass(double* xm, int n, int cs, int c, Ch
   return true;
 }
 
+// X_b <- X_b - X_p (X_p^T X_b) for the cb vectors [b0, b0 + cb) against the
+// cp orthonormal vectors [p0, p0 + cp) (both <= CQ): the cross products
+// through LDS, 16 rows of each side per chunk (chunk rows 0-15 hold X_p's,
+// 16-31 X_b's), into S.G; then each thread updates its rows, 16 columns of
+// X_b at a time (X_p's entries read back from xm).
+__device__ __forceinline__ void cluster_project(double* xm, int n, int p0, int cp, int b0, int cb,
+                                                CholQrLds& S) {
+  static_assert(CR == 32, "two 16-row halves");
+  const int tid = threadIdx.x;
+  constexpr int NQ = CQ * CQ / 256;
+  double acc[NQ];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) acc[q] = 0.0;
+  for (int r0 = 0; r0 < n; r0 += 16) {
+    for (int idx = tid; idx < 16 * CQ; idx += 256) {
+      const int v = idx / 16, r = idx % 16;
+      S.chunk[r][v] = r0 + r < n && v < cp ? xm[(int64_t)(p0 + v) * n + r0 + r] : 0.0;
+      S.chunk[16 + r][v] = r0 + r < n && v < cb ? xm[(int64_t)(b0 + v) * n + r0 + r] : 0.0;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int cell = tid + 256 * q, a = cell / CQ, b = cell % CQ;
+      double x = acc[q];
+      for (int r = 0; r < 16; ++r) x = fma(S.chunk[r][a], S.chunk[16 + r][b], x);
+      acc[q] = x;
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int cell = tid + 256 * q;
+    S.G[cell / CQ][cell % CQ] = acc[q];
+  }
+  __syncthreads();
+  for (int r = tid; r < n; r += 256) {
+    const double* xp = xm + (int64_t)p0 * n + r;
+    double* xb = xm + (int64_t)b0 * n + r;
+    for (int j0 = 0; j0 < cb; j0 += 16) {
+      double u[16];
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) u[jj] = 0.0;
+      for (int i = 0; i < cp; ++i) {
+        const double xi = xp[(int64_t)i * n];
+#pragma unroll
+        for (int jj = 0; jj < 16; ++jj) u[jj] = fma(xi, S.G[i][j0 + jj], u[jj]);
+      }
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj)
+        if (j0 + jj < cb) xb[(int64_t)(j0 + jj) * n] -= u[jj];
+    }
+  }
+  __syncthreads();
+}
+
+// A cluster of c > CQ vectors, CQ at a time (block Gram-Schmidt with
+// Cholesky QR, twice): each slice is projected against the slices before it
+// and made orthonormal, then both steps are repeated.  Returns false, the
+// vectors partly updated, when a Cholesky QR fails (the caller then runs
+// Gram-Schmidt over the whole cluster).
+__device__ __forceinline__ bool cluster_block(double* xm, int n, int cs, int ce, CholQrLds& S) {
+  for (int b0 = cs; b0 < ce; b0 += CQ) {
+    const int cb = ce - b0 < CQ ? ce - b0 : CQ;
+    for (int pass = 0; pass < 2; ++pass) {
+      for (int p0 = cs; p0 < b0; p0 += CQ) cluster_project(xm, n, p0, CQ, b0, cb, S);
+      if (cb > 1 && !cholqr_pass(xm, n, b0, cb, S)) return false;
+      if (cb == 1) {   // one vector: its norm
+        __shared__ double red1[16];
+        double x = 0.0;
+        for (int r = threadIdx.x; r < n; r += 256) x = fma(xm[(int64_t)b0 * n + r], xm[(int64_t)b0 * n + r], x);
+        x = block_sum_all(x, red1);
+        const double sc = 1.0 / sqrt(x);
+        for (int r = threadIdx.x; r < n; r += 256) xm[(int64_t)b0 * n + r] *= sc;
+        __syncthreads();
+      }
+    }
+  }
+  return true;
+}
+
 // Per matrix: the vectors of each cluster -- consecutive eigenvalues whose gaps
 // are all below tol * bnorm -- made orthonormal in place in xall (Cholesky QR
-// twice up to CQ vectors, with Gram-Schmidt as the fallback); matrices
-// without clusters only copy the Rayleigh quotients.
+// twice up to CQ vectors, block Gram-Schmidt with Cholesky QR above; plain
+// Gram-Schmidt as the fallback); matrices without clusters only copy the
+// Rayleigh quotients.
 __global__ __launch_bounds__(256) void k_cluster_orth(int n, int kq, double* w, const double* wr,
                                                       const double* bnorm, double* xall) {
   __shared__ double red[16];
@@ -1914,8 +1995,13 @@ __global__ __launch_bounds__(256) void k_cluster_orth(int n, int kq, double* w, 
     while (ce < kq && fabs(wm[ce - 1] - wm[ce]) <= tol) ++ce;
     const int c = ce - cs;
     if (c >= 2) {
-      bool ok = c <= CQ && cholqr_pass(xm, n, cs, c, S);
-      if (ok) ok = cholqr_pass(xm, n, cs, c, S);
+      bool ok;
+      if (c <= CQ) {
+        ok = cholqr_pass(xm, n, cs, c, S);
+        if (ok) ok = cholqr_pass(xm, n, cs, c, S);
+      } else {
+        ok = cluster_block(xm, n, cs, ce, S);
+      }
       if (!ok) cluster_mgs(xm, n, cs, ce, red);
     }
     cs = ce;

@@ -1059,6 +1059,22 @@ def eigen_route(dim: int, diagonal: bool) -> str:
     return "hip" if eigen.solver_fits(dim) else "library"
 
 
+# The batched solver has a latency floor (its panel loop and bulge chasing
+# run the same number of steps for one matrix as for hundreds: 61 ms at
+# 2048^2, 205 ms at 4096^2); the library eigh takes 42 / 109 ms for one
+# matrix and about as long as the batched solver for four.  A batch of at
+# most this many matrices of at least 2048 rows goes to the library.
+LIBRARY_SMALL_BATCH = 2
+
+
+def batch_route(route: str, dim: int, count: int) -> str:
+    """The route of a dimension's batch of ``count`` factors that
+    eigen_route sent to ``route``."""
+    if route == "hip" and count <= LIBRARY_SMALL_BATCH and dim >= 2048:
+        return "library"
+    return route
+
+
 def refresh(entries, eigen_only: bool = False, ema_only: bool = False) -> None:
     """update_curvature for several preconditioners at once.
 
@@ -1191,6 +1207,8 @@ def _refresh_kron(kron, dev, s, eigen_only=False, ema_only=False):
             for key in lst:
                 r = eigen_route(dim, (id(key[0]), key[1]) in diagonal)
                 routes.setdefault(r, []).append(key)
+            if "hip" in routes and batch_route("hip", dim, len(routes["hip"])) == "library":
+                routes.setdefault("library", []).extend(routes.pop("hip"))
             for r, keys in routes.items():
                 LAST_REFRESH_ROUTES[r] = LAST_REFRESH_ROUTES.get(r, 0) + len(keys)
             for route, keys in routes.items():

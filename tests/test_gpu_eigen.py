@@ -34,6 +34,12 @@ def _matrix(n, seed, kind):
         A = G @ G.T / n + (E + E.T) / 2
     elif kind == "ties":          # diagonal with two values, like a first int8 EMA
         A = torch.diag(torch.where(torch.rand(n, generator=g) < 0.5, 126.0, 127.0).double())
+    elif kind == "neardiag":      # mostly code 127 on the diagonal, a few +-1 codes off it
+        A = torch.diag(torch.where(torch.rand(n, generator=g) < 0.02, 126.0, 127.0).double())
+        for _ in range(6):
+            i, j = torch.randint(0, n, (2,), generator=g).tolist()
+            if i != j:
+                A[i, j] = A[j, i] = 1.0 if torch.rand(1, generator=g).item() < 0.5 else -1.0
     elif kind == "planted":
         Q = torch.linalg.qr(torch.randn(n, n, generator=g, dtype=torch.float64))[0]
         lam = torch.rand(n, generator=g, dtype=torch.float64) * 0.05
@@ -83,7 +89,9 @@ CASES = [(1, 1, "wishart"), (5, 2, "indefinite"), (16, 4, "wishart"), (17, 8, "l
          (40, 10, "planted"), (100, 20, "indefinite"), (257, 32, "wishart"),
          (300, 20, "ties"), (300, 80, "ties"), (512, 64, "ties"), (512, 64, "lowrank"),
          (768, 32, "wishart"),
-         (1024, 128, "planted"), (2048, 64, "planted")]
+         (1024, 128, "planted"), (2048, 64, "planted"),
+         # tie clusters above 64 vectors (block Gram-Schmidt with Cholesky QR)
+         (1024, 200, "ties"), (2048, 256, "neardiag")]
 
 
 @pytest.mark.parametrize("n,kq,kind", CASES)
@@ -109,7 +117,7 @@ def test_topk_eigh(n, kq, kind):
     R = A.double() @ U - U * w.unsqueeze(1)
     res["resid"] = (R.norm(dim=1).amax(dim=1) / scale).max().item()
     # projector onto the top kq where the cut has a gap (not for ties)
-    if kind != "ties" and kq < n:
+    if kind not in ("ties", "neardiag") and kq < n:
         gap = ((wd[:, kq - 1] - wd[:, kq]) / scale).min().item()
         P1 = (U * w.unsqueeze(1)) @ U.transpose(1, 2)
         P2 = (Vd[:, :, :kq] * wd[:, :kq].unsqueeze(1)) @ Vd[:, :, :kq].transpose(1, 2)

@@ -581,3 +581,9 @@ def test_eigen_route_by_size_and_shape():
                     (3000, False), (3840, True), (4095, False), (4096, True), (4112, False)):
         assert eigen.solver_fits(n) == fits, n
         assert engine.eigen_route(n, False) == ("hip" if fits else "library"), n
+    # a batch of one or two large factors goes to the library (latency floor)
+    assert engine.batch_route("hip", 2048, 1) == "library"
+    assert engine.batch_route("hip", 4096, 2) == "library"
+    assert engine.batch_route("hip", 4096, 3) == "hip"
+    assert engine.batch_route("hip", 1024, 1) == "hip"
+    assert engine.batch_route("diag", 4096, 1) == "diag"
