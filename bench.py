@@ -98,6 +98,51 @@ def leaves_of(shape, D):
     return out
 
 
+def refresh_stages(cfg, parts: dict) -> list:
+    """Each refresh stage's time (the launches' events, ms) against its
+    floor at MI355X peak, from the configuration's factors:
+      gram      Gram + EMA on the matrix cores, symmetric flops dim(dim+1)K
+                per factor (K the other side of the block), at the fp32 MFMA peak;
+      requant   int8 codes from the fp32 EMA staging: 5 B per EMA element
+                (staging read, code written) at 8 TB/s;
+      offdiag   the scan for exactly diagonal factors: 1 B per code at 8 TB/s;
+      stage1    dense -> band (panel QR, panel W, trailing update): 5 B n^3/(3b)
+                per solver factor (b = 16) at 8 TB/s;
+      the rest (eig_prep, diag closed form, bulge chasing, bisection, inverse
+      iteration, back-transformation) with their times only."""
+    blocks = [lf for _, sh in shapes_of(cfg)[0] for lf in leaves_of(sh, cfg["D"])]
+    factors = [(m, n) for m, n in blocks] + [(n, m) for m, n in blocks]   # (dim, K)
+    sym_flops = sum(d * (d + 1) * k for d, k in factors)
+    ema_elems = sum(d * d for d, _ in factors)
+
+    def ms(*names):
+        return sum(parts[n]["total"] for n in names if n in parts)
+
+    st1_bytes = sum(5.0 * d ** 3 / (3 * 16) for d, _ in factors)
+    rows = [("gram", ms("scao_gram_ema"), sym_flops / FP32_MFMA_PEAK * 1e3,
+             f"{sym_flops / 1e12:.2f} TFLOP (symmetric) at the fp32 MFMA peak"),
+            ("requant", ms("scao_requant"), 5.0 * ema_elems / HBM_PEAK * 1e3,
+             f"{5.0 * ema_elems / 1e9:.2f} GB at 8 TB/s"),
+            ("offdiag", ms("scao_eig_offdiag"), 1.0 * ema_elems / HBM_PEAK * 1e3,
+             f"{ema_elems / 1e9:.2f} GB at 8 TB/s"),
+            ("stage1", ms("scao_eig_panel_qr", "scao_eig_sy2sb_panel_w", "scao_eig_sy2sb_update"),
+             st1_bytes / HBM_PEAK * 1e3 if "scao_eig_sy2sb_update" in parts else 0.0,
+             f"{st1_bytes / 1e9:.1f} GB (5 B n^3/3b per factor) at 8 TB/s")]
+    out = []
+    for name, t, floor, basis in rows:
+        if t > 0:
+            out.append({"stage": name, "ms": t, "floor_ms": floor,
+                        "frac": floor / t if floor > 0 else None, "floor_basis": basis})
+    for name, kern in (("eig_prep", "scao_eig_prep"), ("diag_closed_form", "scao_eig_diag"),
+                       ("band_finish", "scao_eig_band_finish"), ("bulge_chasing", "scao_eig_sb2st"),
+                       ("bisection", "scao_eig_bisect"), ("inverse_iteration", "scao_eig_vectors"),
+                       ("back_transform", "scao_eig_back_transform")):
+        if kern in parts:
+            out.append({"stage": name, "ms": parts[kern]["total"], "floor_ms": None,
+                        "frac": None, "floor_basis": "latency-bound"})
+    return out
+
+
 # kernel sources whose code a traffic measurement belongs to
 TRAFFIC_SOURCES = ("scao_amd/csrc/kron.hip", "scao_amd/csrc/scao_common.hpp",
                    "scao_amd/csrc/elementwise.hip")
@@ -332,11 +377,26 @@ def pmc_summary(fetch_csv: str, write_csv: str, config: str, copy_mib: int, cmd:
     return "\n".join(out)
 
 
-def refresh_summary(trace_csv: str, config: str, cmd: str) -> str:
-    """Markdown per-kernel summary of the last curvature refresh in a
-    rocprofv3 --kernel-trace CSV of this bench: the dispatches from the
-    refresh's first k_gram_ema to the next k_apply (the update that uses
-    it), grouped by kernel."""
+# kernels of the refresh by the entry point that launches them (refresh_stages)
+_REFRESH_KERNELS = {
+    "scao_gram_ema": ("k_gram_ema",), "scao_requant": ("k_requant",),
+    "scao_eig_offdiag": ("k_eig_offdiag", "k_flags_clear"),
+    "scao_eig_prep": ("k_eig_prep", "k_eig_trace"), "scao_eig_diag": ("k_eig_diag",),
+    "scao_eig_panel_qr": ("k_panel_qr",), "scao_eig_sy2sb_panel_w": ("k_sy2sb_panel_w",),
+    "scao_eig_sy2sb_update": ("k_sy2sb_update", "k_sy2sb_reduce"),
+    "scao_eig_band_finish": ("k_band_finish",), "scao_eig_sb2st": ("k_sb2st",),
+    "scao_eig_bisect": ("k_tri_info", "k_bisect"),
+    "scao_eig_vectors": ("k_band_norm", "k_inviter", "k_cluster_orth", "k_vec_out"),
+    "scao_eig_back_transform": ("k_back_transform",),
+}
+
+
+def refresh_summary(trace_csv: str, config: str, cmd: str, which: int = -1) -> str:
+    """Markdown per-kernel summary of one curvature refresh in a rocprofv3
+    --kernel-trace CSV of this bench (``which``: -1 the last, -2 the one
+    before, ...): the dispatches from the refresh's first k_gram_ema to the
+    next k_apply (the update that uses it), grouped by kernel, and each
+    stage against its floor (refresh_stages)."""
     import csv
     import re
 
@@ -354,7 +414,7 @@ def refresh_summary(trace_csv: str, config: str, cmd: str) -> str:
     starts = [i for i in grams if i == grams[0] or "k_gram_ema" not in names[i - 1] and
               not any("k_gram_ema" in names[j] or "k_requant" in names[j]
                       for j in range(max(0, i - 3), i))]
-    s0 = starts[-1]
+    s0 = starts[which]
     e0 = next(i for i in range(s0, len(rows)) if "k_apply" in names[i])
     win = rows[s0:e0]
     t0, t1 = int(win[0]["Start_Timestamp"]), int(win[-1]["End_Timestamp"])
@@ -376,7 +436,8 @@ def refresh_summary(trace_csv: str, config: str, cmd: str) -> str:
     union += cur_e - cur_s
     out = [f"# Curvature refresh kernels (rocprofv3 kernel trace), {config}", "",
            "Commands (from the repository root on the box):", "", "```", cmd, "```", "",
-           f"The last refresh of the run (a Phase-2 step): {len(win)} dispatches from its first "
+           f"Refresh {which} of the run (-1: the last; a Phase-2 step): {len(win)} dispatches "
+           f"from its first "
            f"`k_gram_ema` to the `k_apply` of the update that uses it; first dispatch start to "
            f"last dispatch end {(t1 - t0) / 1e6:.1f} ms, with a kernel running for "
            f"{union / 1e6:.1f} ms of it; the kernels' durations sum to {busy:.1f} ms (the eigen "
@@ -392,8 +453,19 @@ def refresh_summary(trace_csv: str, config: str, cmd: str) -> str:
             rest[2] += 1
     out.append(f"| other ({rest[2]} kernels) | {rest[0]} | {rest[1]:.2f} | {rest[1] / busy:.1%} |")
     gemm = [v for k, v in agg.items() if k.startswith("rocBLAS GEMM")]
-    out += ["", f"rocBLAS GEMMs together (stage-1 trailing updates and the back-transformation): "
+    out += ["", f"rocBLAS GEMMs together (stage-1 first and last panel products): "
                 f"{sum(n for n, _ in gemm)} dispatches, {sum(ms for _, ms in gemm):.1f} ms."]
+    parts = {}
+    for entry, prefixes in _REFRESH_KERNELS.items():
+        t = sum(ms for name, (_, ms) in agg.items() if name.startswith(prefixes))
+        if t > 0:
+            parts[entry] = {"total": t}
+    out += ["", "Stages against their floors (MI355X peaks; `bench.refresh_stages`):", "",
+            "| stage | ms | floor ms | fraction | floor |", "|---|---:|---:|---:|---|"]
+    for r in refresh_stages(CONFIGS[config], parts):
+        fl = f"{r['floor_ms']:.2f}" if r["floor_ms"] else "-"
+        fr = f"{r['frac']:.2f}" if r["frac"] else "-"
+        out.append(f"| {r['stage']} | {r['ms']:.2f} | {fl} | {fr} | {r['floor_basis']} |")
     return "\n".join(out) + "\n"
 
 
@@ -500,6 +572,9 @@ def main():
     ap.add_argument("--pmc-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"), default=None,
                     help="print the markdown traffic summary of two rocprofv3 --pmc runs "
                          "(FETCH_SIZE, WRITE_SIZE) of this bench and exit (no GPU use)")
+    ap.add_argument("--refresh-index", type=int, default=-1,
+                    help="which refresh --refresh-summary reads (-1: the last, -2: the one "
+                         "before, ...)")
     ap.add_argument("--refresh-summary", metavar="TRACE_CSV", default=None,
                     help="print the markdown kernel summary of the last refresh in a "
                          "rocprofv3 --kernel-trace CSV of this bench and exit (no GPU use)")
@@ -533,7 +608,8 @@ def main():
         print(mfma_summary(*args.mfma_summary, args.config, args.pmc_command))
         return
     if args.refresh_summary:
-        print(refresh_summary(args.refresh_summary, args.config, args.pmc_command))
+        print(refresh_summary(args.refresh_summary, args.config, args.pmc_command,
+                              args.refresh_index))
         return
     if args.pmc_summary:
         print(pmc_summary(*args.pmc_summary, args.config, args.copy_probe_mib or 1024,
@@ -748,6 +824,8 @@ def main():
             for gr in gs:
                 gr.div_(16.0)
         dense = {"step_ms": t_dense, "first_step_ms": t_dense_first,
+                 "stages": refresh_stages(cfg, {k: {"total": t} for k, (c, m_, t)
+                                                in parts.items()}),
                  "routes": dict(engine.LAST_REFRESH_ROUTES),
                  "peak_extra_bytes": peak,
                  "parts_ms": {k: {"count": c, "mean": m_, "total": t}
@@ -796,6 +874,8 @@ def main():
         "refresh_parts_ms": {k: {"count": c, "mean": m_, "total": t}
                              for k, (c, m_, t) in refresh_parts.items()},
         "refresh_routes": refresh_routes,
+        "refresh_stages": refresh_stages(cfg, {k: {"total": t} for k, (c, m_, t)
+                                               in refresh_parts.items()}),
         "refresh_dense_ema": dense,
         "first_step_ms": t_first,
         "default_sparse_filter": sparse,

@@ -34,6 +34,13 @@ BW = L.EIG_BANDW
 MAX_BATCH = 65535   # matrices per call: the batch is a grid dimension
 
 
+def _call(name: str, *args) -> None:
+    """L.call through the engine's launch timing (bench.py's per-kernel
+    split of the refresh)."""
+    from . import engine
+    engine._call(name, *args)
+
+
 def solver_fits(n: int) -> bool:
     """Whether topk_eigh takes an n x n factor with kernels that need no
     scratch memory: every kernel of the solver keeps its state in registers
@@ -78,12 +85,12 @@ def _reduce(X: Tensor):
         _stage1_fused(X, pcs, Tall, band, s)
     orig = torch.empty(B, n, NB + 1, dtype=f32, device=dev)
     band64 = torch.empty(B, n, BW, dtype=torch.float64, device=dev)
-    L.call("scao_eig_band_finish", X.data_ptr(), nn, n, B, band.data_ptr(), n * BW,
+    _call("scao_eig_band_finish", X.data_ptr(), nn, n, B, band.data_ptr(), n * BW,
            orig.data_ptr(), n * (NB + 1), band64.data_ptr(), s)
     del band
     d = torch.empty(B, n, dtype=torch.float64, device=dev)
     e = torch.zeros(B, n, dtype=torch.float64, device=dev)
-    L.call("scao_eig_sb2st", band64.data_ptr(), n, B, d.data_ptr(), e.data_ptr(), s)
+    _call("scao_eig_sb2st", band64.data_ptr(), n, B, d.data_ptr(), e.data_ptr(), s)
     return pcs, Tall, orig, d, e
 
 
@@ -94,7 +101,7 @@ def _stage1_fused(X: Tensor, pcs: list, Tall: Tensor, band: Tensor, s: int) -> N
     nn = n * n
     f32 = torch.float32
     base = X.data_ptr()
-    L.call("scao_eig_panel_qr", base, nn, n, 0, B, Tall[0].data_ptr(), band.data_ptr(), n * BW, s)
+    _call("scao_eig_panel_qr", base, nn, n, 0, B, Tall[0].data_ptr(), band.data_ptr(), n * BW, s)
     Y = torch.bmm(X[:, NB:, NB:], X[:, NB:, 0:NB])      # X is whole and symmetric here
     work = torch.empty(max(L.lib().scao_eig_sy2sb_work(max(n - 2 * NB, 1), B), 8),
                        dtype=torch.uint8, device=X.device)
@@ -104,20 +111,20 @@ def _stage1_fused(X: Tensor, pcs: list, Tall: Tensor, band: Tensor, s: int) -> N
         # W = Y T - V (T^T V^T Y T) / 2 and, unless last, the next panel's
         # columns (rows r0..)
         W = torch.empty(B, n - r0, NB, dtype=f32, device=X.device)
-        L.call("scao_eig_sy2sb_panel_w", base, nn, n, c0, B, Y.data_ptr(), Tall[p].data_ptr(),
+        _call("scao_eig_sy2sb_panel_w", base, nn, n, c0, B, Y.data_ptr(), Tall[p].data_ptr(),
                W.data_ptr(), 0 if last else 1, s)
         if last:                                               # the last, in-band block
             V = X[:, r0:, c0:c0 + NB]
             A22 = X[:, r0:, r0:]
             A22.baddbmm_(torch.cat([V, W], 2), torch.cat([W, V], 2).transpose(1, 2), alpha=-1.0)
             break
-        L.call("scao_eig_panel_qr", base, nn, n, r0, B, Tall[p + 1].data_ptr(),
+        _call("scao_eig_panel_qr", base, nn, n, r0, B, Tall[p + 1].data_ptr(),
                band.data_ptr(), n * BW, s)
         # the rest of the trailing matrix (rows and columns r1..) and the next Y
         r1 = r0 + NB
         mr = n - r1
         Y = torch.empty(B, mr, NB, dtype=f32, device=X.device)
-        L.call("scao_eig_sy2sb_update", base + 4 * (r1 * n + r1), nn, n, mr, B,
+        _call("scao_eig_sy2sb_update", base + 4 * (r1 * n + r1), nn, n, mr, B,
                base + 4 * (r1 * n + c0), nn, n,
                W.data_ptr() + 4 * NB * NB, W.stride(0), NB,
                base + 4 * (r1 * n + r0), nn, n,
@@ -151,16 +158,16 @@ def topk_eigh(X: Tensor, kq: int):
     w = torch.empty(B, kq, dtype=torch.float64, device=dev)
     total = torch.empty(B, dtype=torch.float64, device=dev)
     work = torch.empty(max(L.lib().scao_eig_bisect_work(n, B), 8), dtype=torch.uint8, device=dev)
-    L.call("scao_eig_bisect", d.data_ptr(), e.data_ptr(), n, B, kq, w.data_ptr(),
+    _call("scao_eig_bisect", d.data_ptr(), e.data_ptr(), n, B, kq, w.data_ptr(),
            total.data_ptr(), work.data_ptr(), s)
     Z = torch.empty(B, n, kq, dtype=torch.float32, device=dev)
     work = torch.empty(max(L.lib().scao_eig_vectors_work(n, B, kq), 8), dtype=torch.uint8,
                        device=dev)
-    L.call("scao_eig_vectors", orig.data_ptr(), n * (NB + 1), n, B, kq, w.data_ptr(),
+    _call("scao_eig_vectors", orig.data_ptr(), n * (NB + 1), n, B, kq, w.data_ptr(),
            Z.data_ptr(), n * kq, work.data_ptr(), s)
     del work
     if pcs:
-        L.call("scao_eig_back_transform", X.data_ptr(), n * n, n, B, Tall.data_ptr(),
+        _call("scao_eig_back_transform", X.data_ptr(), n * n, n, B, Tall.data_ptr(),
                Z.data_ptr(), n * kq, kq, s)
     if kq != want:
         w, Z = w[:, :want].contiguous(), Z[:, :, :want].contiguous()
