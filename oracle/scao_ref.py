@@ -66,6 +66,15 @@ EXACT_EIGH = False
 RECORD = None
 
 
+# The reference forms the preconditioned gradient G + U_l((s_l s_r^T - 1) o
+# (U_l^T G U_r)) U_r^T with float32 GEMMs; at elements where the Adan update
+# is a small difference of larger terms that rounding shows in u.  With
+# EXACT_PRECOND set, this oracle forms it in float64 from the same factors and
+# rounds it to float32 once; the multi-step parity tests use it to measure how
+# far the reference's own float32 GEMMs move its update.  Off by default.
+EXACT_PRECOND = False
+
+
 def _norm(x: Tensor) -> Tensor:
     """x.norm() as the reference takes it, or its correctly rounded value."""
     if EXACT_NORMS:
@@ -181,6 +190,10 @@ def fused_kronecker_precond(U_l: Tensor, s_l_inv4: Tensor, U_r: Tensor,
                             s_r_inv4: Tensor, G: Tensor) -> Tensor:
     """scao/cuda/__init__.py:78-99:
     P = (U_l^T G) U_r;  D = (s_l s_r^T - 1) * P;  out = G + (U_l D) U_r^T."""
+    if EXACT_PRECOND:
+        Ul, Ur, Gd = U_l.double(), U_r.double(), G.double()
+        outer = s_l_inv4.double().unsqueeze(1) * s_r_inv4.double().unsqueeze(0)
+        return (Gd + Ul @ ((outer - 1.0) * ((Ul.T @ Gd) @ Ur)) @ Ur.T).to(G.dtype)
     proj = (U_l.T @ G) @ U_r
     outer = s_l_inv4.unsqueeze(1) * s_r_inv4.unsqueeze(0)
     delta = (outer - 1.0) * proj

@@ -1045,6 +1045,12 @@ EIGH_BATCH_BYTES = 1 << 30        # stacked eigh inputs per launch (library solv
 # reference's own post-EMA state, so the eigen stage and the step that follows
 # are compared from identical inputs.
 AFTER_EMA_HOOK = None
+# Optional callable run after a refresh's eigen stage, rank selection and
+# truncation, with the same list: the parity tests check the new eigenfactors
+# against the CPU reference's and continue from the reference's, where a
+# solver's freedom (the basis of a cluster, float32 rounding of eigenvectors)
+# would otherwise carry into the steps that follow.
+AFTER_EIGEN_HOOK = None
 # factors per eigen-stage route in the last refresh (reported by bench.py)
 LAST_REFRESH_ROUTES: dict = {}
 
@@ -1275,6 +1281,8 @@ def _refresh_kron(kron, dev, s, eigen_only=False, ema_only=False):
         leaf.U_r = Ur[:, :k].contiguous()
         leaf.S_r = Sr[:k].contiguous()
         leaf._touch()
+    if AFTER_EIGEN_HOOK is not None:
+        AFTER_EIGEN_HOOK(kron)
 
 
 def _task_rows(idx, a, b, slot) -> np.ndarray:

@@ -205,3 +205,48 @@ def step_stats(opt) -> dict:
             d["upd"] = flat[off:off + p.numel()].view(p.shape).cpu()
         out[id(p)] = d
     return out
+
+
+class ReferenceEigen:
+    """engine.AFTER_EIGEN_HOOK for one step: for every refreshed block,
+    checks the GPU's new eigenfactors against the CPU reference's from the
+    same codes -- k and S (rtol 1e-4) and the spectral projector U S U^T,
+    within max(1e-4, 3 E_ref) where E_ref is how far the reference's float32
+    eigh is from float64 on the same input (computed only when needed) --
+    then gives the GPU block the reference's U, S and k, so that the steps
+    after a refresh are compared from identical factors.
+    ``pairs``: {id(gpu block): cpu block}."""
+
+    def __init__(self, pairs: dict):
+        self.pairs = pairs
+        self.worst = 0.0
+        self.checked = 0
+
+    @staticmethod
+    def _proj(U, S):
+        U = U.detach().double().cpu()
+        return (U * S.detach().double().cpu()) @ U.T
+
+    def __call__(self, kron):
+        for leaf, *_ in kron:
+            ref = self.pairs[id(leaf)]
+            dev = leaf.U_l.device
+            assert leaf.k == ref.k, (leaf.k, ref.k)
+            for side, X in zip(("l", "r"), eig_input(ref)):
+                Ug, Sg = getattr(leaf, f"U_{side}"), getattr(leaf, f"S_{side}")
+                Ur, Sr = getattr(ref, f"U_{side}"), getattr(ref, f"S_{side}")
+                torch.testing.assert_close(Sg.cpu(), Sr, rtol=1e-4, atol=0.0)
+                pr = self._proj(Ur, Sr)
+                e = ((self._proj(Ug, Sg) - pr).norm() / pr.norm()).item()
+                bound = 1e-4
+                if e > bound:   # the reference's own float32 eigh error on this input
+                    w, V = torch.linalg.eigh(X)
+                    w, V = w.flip(0)[:ref.k], V.flip(1)[:, :ref.k]
+                    e_ref = (((V * w) @ V.T - pr).norm() / pr.norm()).item()
+                    bound = max(bound, 3.0 * e_ref)
+                assert e <= bound, (side, leaf.m, leaf.n, e, bound)
+                self.worst = max(self.worst, e)
+            leaf.U_l, leaf.S_l = ref.U_l.to(dev).contiguous(), ref.S_l.to(dev).contiguous()
+            leaf.U_r, leaf.S_r = ref.U_r.to(dev).contiguous(), ref.S_r.to(dev).contiguous()
+            leaf._touch()
+            self.checked += 1
