@@ -143,6 +143,14 @@ def refresh_stages(cfg, parts: dict) -> list:
     return out
 
 
+def _stage_fracs(stages: list) -> dict:
+    """{stage: {"ms", "frac"}} from refresh_stages' rows (frac: floor / measured,
+    None for latency-bound stages)."""
+    return {r["stage"]: {"ms": round(r["ms"], 3),
+                         "frac": None if r["frac"] is None else round(r["frac"], 3)}
+            for r in stages}
+
+
 # kernel sources whose code a traffic measurement belongs to
 TRAFFIC_SOURCES = ("scao_amd/csrc/kron.hip", "scao_amd/csrc/scao_common.hpp",
                    "scao_amd/csrc/elementwise.hip")
@@ -913,11 +921,18 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "details": {"phase1_step_ms": p1_ms, "refresh_step_ms": t_refresh,
+                    "refresh_routes": refresh_routes,
+                    "refresh_stages": _stage_fracs(details["refresh_stages"]),
                     "refresh_dense_ema_step_ms": dense["step_ms"] if dense else None,
+                    "refresh_dense_ema_routes": dense["routes"] if dense else None,
+                    "refresh_dense_ema_stages": _stage_fracs(dense["stages"]) if dense else None,
+                    "refresh_dense_ema_peak_extra_GB": (dense["peak_extra_bytes"] / 1e9
+                                                        if dense else None),
                     "step_median_ms": step_dist["median_ms"], "step_p90_ms": step_dist["p90_ms"],
                     "step_hbm_frac": details["step_roofline"]["hbm_frac"],
                     "steady_step_default_filter_noise_ms": (sparse["steady_step_ms"]
-                                                            if sparse else None)},
+                                                            if sparse else None),
+                    "cpu_baseline_legs": details.get("cpu_baseline_legs")},
     }
     if args.details:
         with open(args.details, "w") as f:
