@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define SCAO_ABI_VERSION 10
+#define SCAO_ABI_VERSION 11
 
 enum scao_status { SCAO_OK = 0, SCAO_ERR_INVALID = 1, SCAO_ERR_HIP = 2 };
 enum scao_dtype { SCAO_F32 = 0, SCAO_BF16 = 1, SCAO_F16 = 2 };
@@ -110,6 +110,10 @@ typedef struct scao_leaf_desc {
   int32_t m, n, k;
   int32_t flags;            /* SCAO_LF_*                                         */
   float dbias;              /* SCAO_LF_DIAG: fp32(diagonal EMA bias factor)      */
+  uint16_t* Wb;             /* NULL, or 3 x m x k bf16: W split exactly as
+                               W = h + m + l (planes h, m, l, each m x k
+                               row-major); scao_kron_lift writes it beside W,
+                               the strip apply (variant bit 16) reads it   */
 } scao_leaf_desc;
 
 #define SCAO_LF_SINV4 1     /* Sl/Sr already hold clamp(S,1e-8)^-1/4             */
@@ -226,7 +230,14 @@ int scao_step_finalize(const scao_param_desc* params, int nparams, const double*
  *     64x64 tiles (SCAO_APPLY_TILE) at (a, b), clipped to the block.
  *     variant | 8 (with 4): the same fast tasks through a two-role pipeline,
  *     SCAO_APPLY_GROUP consecutive tasks per block (the engine's choice for
- *     k >= 128). */
+ *     k >= 128 other than 128 and 256).
+ *     variant | 16 (with 4): strip runs for k = 256 (| 32: k = 128): a task
+ *     (leaf, a, b, slot) covers min(SCAO_APPLY_GROUP, (mw - a) / TR) tiles
+ *     of TR rows x SW columns going down from row a in the column strip at
+ *     b (SW = 64, TR = 128 for k = 256; SW = 128, TR = 64 for k = 128; mw =
+ *     m - m % TR), with reduction slots slot, slot + 1, ...; b + SW <= n.
+ *     Without SCAO_PF_GF32 the leaf needs Wb (written by scao_kron_lift).
+ *     A leaf of another k, or one lacking Wb, gets NaN in its run's slots. */
 int scao_kron_apply(const scao_task* tasks, int ntasks, const scao_leaf_desc* leaves,
                     const scao_param_desc* params, const scao_param_stat* stat,
                     double* slots, int variant, void* stream);

@@ -21,7 +21,7 @@ import torch  # noqa: F401  -- loads torch's HIP runtime before ours
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("SCAO_AMD_LIB", os.path.join(HERE, "_lib", "libscao_amd.so"))
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 SLOT_WIDTH = 3
 FLAT_CHUNK = 4096
 PROJ_COLS = 256
@@ -60,7 +60,7 @@ PARAM_DESC = np.dtype([
 LEAF_DESC = np.dtype([
     ("Ul", "u8"), ("Ur", "u8"), ("Sl", "u8"), ("Sr", "u8"), ("T", "u8"), ("Delta", "u8"),
     ("W", "u8"), ("off", "i8"), ("ld", "i8"), ("param", "i4"), ("m", "i4"), ("n", "i4"),
-    ("k", "i4"), ("flags", "i4"), ("dbias", "f4"),
+    ("k", "i4"), ("flags", "i4"), ("dbias", "f4"), ("Wb", "u8"),
 ], align=True)
 
 TASK = np.dtype([("idx", "i4"), ("a", "i4"), ("b", "i4"), ("slot", "i4")], align=True)

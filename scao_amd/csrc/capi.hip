@@ -55,6 +55,7 @@ extern "C" int scao_struct_layout(int which, int64_t* out, int cap) {
       PUT(offsetof(S, T)); PUT(offsetof(S, Delta)); PUT(offsetof(S, W)); PUT(offsetof(S, off));
       PUT(offsetof(S, ld)); PUT(offsetof(S, param)); PUT(offsetof(S, m)); PUT(offsetof(S, n));
       PUT(offsetof(S, k)); PUT(offsetof(S, flags)); PUT(offsetof(S, dbias));
+      PUT(offsetof(S, Wb));
       break;
     }
     case 2: {

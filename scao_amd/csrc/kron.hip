@@ -533,6 +533,37 @@ __device__ __forceinline__ void diag_leaf_reduce(const scao_leaf_desc& L,
 // reduction runs with NH chunks of operands in flight (fully unrolled for
 // k = 16 NC, NC > 0; any multiple of 16 with one chunk of lookahead for
 // NC = 0).  Other tiles take the element-wise path.
+// W's exact three-way bf16 split (as split_bf3) into the planes h, m, l of
+// Wb (plane stride mk elements), at element o: four elements, or one.
+__device__ __forceinline__ void split3(float x, __bf16& h, __bf16& m, __bf16& l) {
+  h = (__bf16)x;
+  const float r = x - (float)h;
+  m = (__bf16)r;
+  l = (__bf16)(r - (float)m);
+}
+typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store_split4(uint16_t* wb, int64_t mk, int64_t o, const v4f& x) {
+  v4bf h, m, l;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    __bf16 a, b, c;
+    split3(x[e], a, b, c);
+    h[e] = a;
+    m[e] = b;
+    l[e] = c;
+  }
+  *(gv2u*)(wb + o) = __builtin_bit_cast(v2u, h);
+  *(gv2u*)(wb + mk + o) = __builtin_bit_cast(v2u, m);
+  *(gv2u*)(wb + 2 * mk + o) = __builtin_bit_cast(v2u, l);
+}
+__device__ __forceinline__ void store_split1(uint16_t* wb, int64_t mk, int64_t o, float x) {
+  __bf16 h, m, l;
+  split3(x, h, m, l);
+  ((gu16*)wb)[o] = __builtin_bit_cast(uint16_t, h);
+  ((gu16*)wb)[mk + o] = __builtin_bit_cast(uint16_t, m);
+  ((gu16*)wb)[2 * mk + o] = __builtin_bit_cast(uint16_t, l);
+}
+
 template <int NC>
 __device__ __forceinline__ void lift_chunks(const float* __restrict__ urow,
                                             const float* __restrict__ drow, int k,
@@ -592,7 +623,8 @@ __device__ __forceinline__ void lift_tile(const scao_leaf_desc& L, int i0, int d
 #pragma unroll
   for (int t = 0; t < 4; ++t) acc[t] = v4f{0.f, 0.f, 0.f, 0.f};
   const bool whole = k % 16 == 0 && i0 + 64 <= m && d0 + 64 <= k &&
-                     (((uintptr_t)L.Ul | (uintptr_t)L.Delta | (uintptr_t)L.W) & 15) == 0;
+                     (((uintptr_t)L.Ul | (uintptr_t)L.Delta | (uintptr_t)L.W) & 15) == 0 &&
+                     ((uintptr_t)L.Wb & 7) == 0;
   if (whole) {
     const int irow = i0 + 16 * w + (l % 16);
     const int dl = d0 + 4 * (l % 16);
@@ -607,9 +639,12 @@ __device__ __forceinline__ void lift_tile(const scao_leaf_desc& L, int i0, int d
     else
       lift_chunks<0>(urow, drow, k, acc);
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      gst4(L.W + (int64_t)(i0 + 16 * w + 4 * kk + r) * k + dl,
-           v4f{acc[0][r], acc[1][r], acc[2][r], acc[3][r]});
+    for (int r = 0; r < 4; ++r) {
+      const int64_t o = (int64_t)(i0 + 16 * w + 4 * kk + r) * k + dl;
+      const v4f x = v4f{acc[0][r], acc[1][r], acc[2][r], acc[3][r]};
+      gst4(L.W + o, x);
+      if (L.Wb) store_split4(L.Wb, (int64_t)m * k, o, x);
+    }
     return;
   }
   const int irow = i0 + 16 * w + (l % 16);
@@ -636,7 +671,10 @@ __device__ __forceinline__ void lift_tile(const scao_leaf_desc& L, int i0, int d
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
       const int d = d0 + 16 * t + (l % 16);
-      if (d < k) L.W[(int64_t)i * k + d] = acc[t][r];
+      if (d < k) {
+        L.W[(int64_t)i * k + d] = acc[t][r];
+        if (L.Wb) store_split1(L.Wb, (int64_t)m * k, (int64_t)i * k + d, acc[t][r]);
+      }
     }
   }
 }
@@ -1262,6 +1300,380 @@ __global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict_
   if (nt > 0 && w == 0 && l == 0) put_slot(nt - 1);
 }
 
+// ---------------------------------------------- strip-resident apply ---
+// Large-rank blocks (16 <= k <= 256, k % 16 == 0).  A task is a run of up to
+// SCAO_APPLY_GROUP tiles of one column strip of SW columns, TR = 8192 / SW
+// rows each (SW = 64 for k > 128, 128 otherwise), going down the block.  The
+// strip's U_r rows stay in LDS for the whole run, so the back-projection
+// reads only W rows from L2 instead of every wave refetching U_r per tile.
+// One 12-wave workgroup per CU:
+//   waves 8..11 (MFMA role): corr(s) = W[rows of tile s, :] U_r[strip, :]^T,
+//     32 rows x 64 columns per wave (two 16-row halves sharing each B
+//     operand read from LDS), A operands from L2 with chunks of lookahead;
+//   waves 0..7 (streaming role, 16 rows x 64 columns each): tile s's loads
+//     were issued during tile s-1; once corr(s) is published they run the
+//     Phase-2 tail, store, and issue tile s+1's loads.
+// The matrix cores and the Phase-2 arithmetic share each SIMD's issue, so the
+// products run as six bf16 MFMAs over exact three-way splits (mfma_x6, fp32
+// accuracy): W's planes come from scao_kron_lift (Wb), U_r's are split once
+// per run into LDS.  Three planes of U_r leave LDS for one correction
+// buffer: the streaming waves copy corr(s) to registers and release it (a
+// second barrier per tile) before the MFMA waves write corr(s+1).  The GF32
+// variants have no registers for that copy; they keep fp32 MFMAs, U_r in
+// LDS as fp32 and two correction buffers.
+// U_r row r of the strip sits at LDS row 64(r/64) + 16(r%4) + (r%64)/4, so
+// that a lane's four B rows (columns 4j + t of its 64-column group) are 16
+// rows apart, and the row pitch is 16 bytes past a multiple of 128: a 16-lane
+// read phase touches 16 distinct bank groups.
+constexpr int STRIP_LDS = 138240;   // bytes: U_r (fp32 or three bf16 planes) + buffers
+__host__ __device__ constexpr int strip_pitch(int k) { return k + 4 + ((32 - k % 32) % 32); }
+__host__ __device__ constexpr int strip_pitch_bf(int k) { return k + 8 + ((64 - k % 64) % 64); }
+__device__ __forceinline__ int strip_row(int r) { return 64 * (r / 64) + 16 * (r % 4) + (r % 64) / 4; }
+
+// fp32: corr for rows wa (and wb, 16 rows on) against the LDS strip (lane
+// base ub), k = 16 NC (NC = 0: any multiple of 16).
+template <int NC, int PD>
+__device__ __forceinline__ void strip_corr(const float* __restrict__ wa,
+                                           const float* __restrict__ wb, const float* ub, int pk,
+                                           int k, v4f (&acc)[2][4]) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[h][t] = v4f{0.f, 0.f, 0.f, 0.f};
+  if constexpr (NC > 0) {
+    v4f A[PD][2], B[2][4];
+#pragma unroll
+    for (int d = 0; d < PD && d < NC; ++d) {
+      A[d][0] = gld4(wa + 16 * d);
+      A[d][1] = gld4(wb + 16 * d);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) B[0][t] = *(const v4f*)(ub + 16 * t * pk);
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      const int d = c % PD, cur = c & 1;
+      if (c + 1 < NC) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) B[cur ^ 1][t] = *(const v4f*)(ub + 16 * t * pk + 16 * (c + 1));
+      }
+      // chunk c+1's LDS reads go out before chunk c's products (a second
+      // register set), so their latency hides behind 32 MFMAs
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          acc[0][t] = mfma16(A[d][0][s4], B[cur][t][s4], acc[0][t]);
+          acc[1][t] = mfma16(A[d][1][s4], B[cur][t][s4], acc[1][t]);
+        }
+      if (c + PD < NC) {
+        A[d][0] = gld4(wa + 16 * (c + PD));
+        A[d][1] = gld4(wb + 16 * (c + PD));
+      }
+      // keep chunk c+PD's loads here: the scheduler would otherwise sink
+      // them next to their use and expose an L2 round trip per chunk
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+    v4f a0 = gld4(wa), a1 = gld4(wb);
+    for (int c = 0; c < k; c += 16) {
+      v4f n0 = a0, n1 = a1;
+      if (c + 16 < k) {
+        n0 = gld4(wa + c + 16);
+        n1 = gld4(wb + c + 16);
+      }
+      v4f b[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) b[t] = *(const v4f*)(ub + 16 * t * pk + c);
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          acc[0][t] = mfma16(a0[s4], b[t][s4], acc[0][t]);
+          acc[1][t] = mfma16(a1[s4], b[t][s4], acc[1][t]);
+        }
+      a0 = n0;
+      a1 = n1;
+    }
+  }
+}
+
+// bf16 planes: the A operands of one 32-k chunk (both halves, three planes).
+struct strip_a {
+  bf3 a[2];
+};
+__device__ __forceinline__ v8bf gld8bf(const uint16_t* p) {
+  return __builtin_bit_cast(v8bf, gld4((const float*)p));
+}
+// wp[h][p]: the lane's row of plane p for half h (column 8*(l/16) included)
+__device__ __forceinline__ void strip_load_a(strip_a& A, const uint16_t* const (&wp)[2][3], int c) {
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    A.a[h].h = gld8bf(wp[h][0] + 32 * c);
+    A.a[h].m = gld8bf(wp[h][1] + 32 * c);
+    A.a[h].l = gld8bf(wp[h][2] + 32 * c);
+  }
+}
+__device__ __forceinline__ bf3 strip_load_b(const uint16_t* ub, int plane, int pk, int t, int c) {
+  const uint16_t* p = ub + 16 * t * pk + 32 * c;
+  bf3 b;
+  b.h = *(const v8bf*)p;
+  b.m = *(const v8bf*)(p + plane);
+  b.l = *(const v8bf*)(p + 2 * plane);
+  return b;
+}
+
+// bf16: corr for the rows of wp (two 16-row halves) against the LDS planes
+// (lane base ub, plane stride `plane`, row pitch pk), with the first PD
+// chunks of A already in A[0..PD-1].  K > 0: k, pk and plane are the
+// compile-time K, PKC, PLC and the chunk loop is unrolled; K = 0: the
+// runtime values, chunks in rotations of PD.
+template <int K, int PKC, int PLC, int PD>
+__device__ __forceinline__ void strip_corr_bf(strip_a (&A)[PD], const uint16_t* const (&wp)[2][3],
+                                              const uint16_t* ub, int plane_rt, int pk_rt,
+                                              int k_rt, v4f (&acc)[2][4]) {
+  const int pk = K ? PKC : pk_rt, plane = K ? PLC : plane_rt;
+  const int nc = (K ? K : k_rt) / 32;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[h][t] = v4f{0.f, 0.f, 0.f, 0.f};
+  bf3 B[2];
+  B[0] = strip_load_b(ub, plane, pk, 0, 0);
+#pragma unroll(K > 0 ? 8 : 1)
+  for (int c0 = 0; c0 < nc; c0 += PD) {
+#pragma unroll
+    for (int d = 0; d < PD; ++d) {
+      const int c = c0 + d;
+      if (c < nc) {
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+          const int cur = t & 1;
+          if (t < 3)
+            B[cur ^ 1] = strip_load_b(ub, plane, pk, t + 1, c);
+          else if (c + 1 < nc)
+            B[cur ^ 1] = strip_load_b(ub, plane, pk, 0, c + 1);
+          // the next B goes out before these products (its own registers)
+          __builtin_amdgcn_sched_barrier(0);
+          acc[0][t] = mfma_x6(A[d].a[0], B[cur], acc[0][t]);
+          acc[1][t] = mfma_x6(A[d].a[1], B[cur], acc[1][t]);
+        }
+        if (c + PD < nc) strip_load_a(A[d], wp, c + PD);
+        // chunk c+PD's loads stay here, PD chunks ahead of their use
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+}
+
+template <bool GF32, bool LARS, int SW>
+__global__ __launch_bounds__(768) void k_apply_strip(const scao_task* __restrict__ tasks,
+                                                     const scao_leaf_desc* __restrict__ leaves,
+                                                     const scao_param_desc* __restrict__ params,
+                                                     const scao_param_stat* __restrict__ stat,
+                                                     double* slots) {
+  constexpr bool BF = !GF32;      // bf16 products, one correction buffer
+  constexpr int TR = 8192 / SW;   // rows of a tile
+  constexpr int CB = SW + 4;      // LDS pitch of a correction row
+  constexpr int NBUF = BF ? 1 : 2;
+  constexpr int CBYTES = NBUF * TR * CB * 4;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[STRIP_LDS];
+  __shared__ double part[2][8];
+  float(*cbuf)[TR][CB] = (float(*)[TR][CB])(lds + STRIP_LDS - CBYTES);
+  const int wv = threadIdx.x / 64, l = threadIdx.x % 64;
+  const int kk = l / 16;
+  const scao_task tk = tasks[blockIdx.x];
+  const scao_leaf_desc& L = leaves[tk.idx];
+  const int k = L.k, pk = BF ? strip_pitch_bf(k) : strip_pitch(k);
+  const int mw = L.m - L.m % TR;
+  int nt = (mw - tk.a) / TR;
+  nt = nt < SCAO_APPLY_GROUP ? nt : SCAO_APPLY_GROUP;
+  if (nt <= 0) return;   // uniform over the workgroup
+  if (k != (SW == 64 ? 256 : 128) || (BF && !L.Wb)) {
+    // outside the kernel's contract (the engine never sends this): make the
+    // run's norms NaN rather than write anything
+    if (threadIdx.x < nt && tk.slot >= 0)
+      slots[(int64_t)(tk.slot + threadIdx.x) * SCAO_SLOT_WIDTH + 2] = __builtin_nan("");
+    return;
+  }
+
+  if (wv >= 8) {
+    // ---- MFMA role ----
+    constexpr int RP = TR / 32;   // 32-row groups of a tile
+    const int mwv = wv - 8, rp = mwv % RP, cg = mwv / RP;
+    const int q4 = k / 4;
+    auto put = [&](int buf, v4f (&acc)[2][4]) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          *(v4f*)&cbuf[buf][32 * rp + 16 * h + 4 * kk + r][64 * cg + 4 * (l % 16)] =
+              v4f{acc[h][0][r], acc[h][1][r], acc[h][2][r], acc[h][3][r]};
+    };
+    if constexpr (BF) {
+      // barriers: A, X_0, then (Y_{s-1}, X_s) for s = 1..nt
+      uint16_t* urb = (uint16_t*)lds;
+      const int plane = SW * pk;
+      for (int q = threadIdx.x - 512; q < SW * q4; q += 256) {
+        const int r = q / q4, c = q - r * q4;
+        const v4f x = gld4(L.Ur + (int64_t)(tk.b + r) * k + 4 * c);
+        v4bf h, m, lo;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          __bf16 a, b, cc;
+          split3(x[e], a, b, cc);
+          h[e] = a;
+          m[e] = b;
+          lo[e] = cc;
+        }
+        uint16_t* d = urb + strip_row(r) * pk + 4 * c;
+        *(v2u*)d = __builtin_bit_cast(v2u, h);
+        *(v2u*)(d + plane) = __builtin_bit_cast(v2u, m);
+        *(v2u*)(d + 2 * plane) = __builtin_bit_cast(v2u, lo);
+      }
+      const int64_t mk = (int64_t)L.m * k;
+      const uint16_t* ub = urb + (64 * cg + l % 16) * pk + 8 * kk;
+      constexpr int PD = SW == 64 ? 2 : 3;   // chunks of A lookahead (registers)
+      constexpr int PK256 = strip_pitch_bf(256), PK128 = strip_pitch_bf(128);
+      strip_a A[PD];
+      const uint16_t* wp[2][3];
+      auto rows = [&](int s) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int q = 0; q < 3; ++q)
+            wp[h][q] = L.Wb + q * mk + (int64_t)(tk.a + s * TR + 32 * rp + 16 * h + l % 16) * k +
+                       8 * kk;
+      };
+      auto first = [&](int s) {
+        rows(s);
+#pragma unroll
+        for (int d = 0; d < PD; ++d)
+          if (d < k / 32) strip_load_a(A[d], wp, d);
+      };
+      auto corr = [&](int s, v4f (&acc)[2][4]) {
+        if constexpr (SW == 64)
+          strip_corr_bf<256, PK256, SW * PK256, PD>(A, wp, ub, plane, pk, k, acc);
+        else
+          strip_corr_bf<128, PK128, SW * PK128, PD>(A, wp, ub, plane, pk, k, acc);
+      };
+      first(0);
+      __syncthreads();                                        // A: U_r planes in LDS
+      {
+        v4f acc[2][4];
+        corr(0, acc);
+        put(0, acc);
+      }
+      __syncthreads();                                        // X_0: corr(0) published
+      for (int s = 1; s <= nt; ++s) {
+        if (s < nt) first(s);                                 // loads in flight across Y
+        __syncthreads();                                      // Y_{s-1}: corr(s-1) copied
+        if (s < nt) {
+          v4f acc[2][4];
+          corr(s, acc);
+          put(0, acc);
+        }
+        __syncthreads();                                      // X_s: corr(s) published
+      }
+    } else {
+      // barriers: A, then X_s for s = 0..nt
+      float* ur = (float*)lds;
+      for (int q = threadIdx.x - 512; q < SW * q4; q += 256) {
+        const int r = q / q4, c = q - r * q4;
+        *(v4f*)&ur[strip_row(r) * pk + 4 * c] = gld4(L.Ur + (int64_t)(tk.b + r) * k + 4 * c);
+      }
+      __syncthreads();                                        // A: U_r strip in LDS
+      const float* ub = &ur[(64 * cg + l % 16) * pk + 4 * kk];
+      for (int s = 0; s < nt; ++s) {
+        v4f acc[2][4];
+        const float* __restrict__ wa =
+            L.W + (int64_t)(tk.a + s * TR + 32 * rp + l % 16) * k + 4 * kk;
+        const float* __restrict__ wb = wa + (int64_t)16 * k;
+        if constexpr (SW == 64)
+          strip_corr<16, 6>(wa, wb, ub, pk, k, acc);
+        else
+          strip_corr<8, 6>(wa, wb, ub, pk, k, acc);
+        put(s & 1, acc);
+        __syncthreads();                                      // X_s: corr(s) published
+      }
+      __syncthreads();                                        // X_nt
+    }
+    return;
+  }
+
+  // ---- streaming role ----
+  constexpr int RG = TR / 16;     // 16-row groups of a tile
+  const int w = wv, rg = w % RG, cg = w / RG;
+  const scao_param_desc& P = params[L.param];
+  const scao_param_stat& S = stat[L.param];
+  v4f gr[4], gm[4], mm[4], vv[4], dd[4], pp[4], par[4];
+  int64_t e[4];
+  const int jc = tk.b + 64 * cg + 4 * (l % 16);
+  auto prefetch = [&](int s) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      e[r] = L.off + (int64_t)(tk.a + s * TR + 16 * rg + 4 * kk + r) * L.ld + jc;
+      gr[r] = gld4_nt((const float*)P.graw + e[r]);
+      if (GF32) {
+        if (!fused_mgrad(P))
+          gm[r] = gld4_nt((const float*)P.g + e[r]);
+        else
+          gm[r] = (P.flags & SCAO_PF_FMASK) ? gld4_nt(P.fema + e[r]) : gr[r];
+      }
+      mm[r] = gld4_nt(P.exp_avg + e[r]);
+      vv[r] = gld4_nt(P.exp_avg_sq + e[r]);
+      dd[r] = gld4_nt(P.exp_avg_diff + e[r]);
+      pp[r] = gld4_nt(P.prev_grad + e[r]);
+      if (!LARS) par[r] = gld4_nt((const float*)P.p + e[r]);
+    }
+  };
+  auto put_slot = [&](int s) {
+    if (tk.slot < 0) return;
+    const double* q = part[s & 1];
+    const double u2 = ((((((q[0] + q[1]) + q[2]) + q[3]) + q[4]) + q[5]) + q[6]) + q[7];
+    const int64_t slot = tk.slot + s;
+    slots[slot * SCAO_SLOT_WIDTH + 0] = 0.0;
+    slots[slot * SCAO_SLOT_WIDTH + 1] = 0.0;
+    slots[slot * SCAO_SLOT_WIDTH + 2] = u2;
+  };
+  prefetch(0);
+  __syncthreads();                                            // A
+  __syncthreads();                                            // X_0: corr(0)
+  for (int s = 0; s < nt; ++s) {
+    if (s > 0 && w == 0 && l == 0) put_slot(s - 1);
+    v4f cr[4];
+    if constexpr (BF) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        cr[r] = *(const v4f*)&cbuf[0][16 * rg + 4 * kk + r][64 * cg + 4 * (l % 16)];
+      __syncthreads();                                        // Y_s: the buffer is free
+    }
+    float u2 = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const v4f corr =
+          BF ? cr[r] : *(const v4f*)&cbuf[s & 1][16 * rg + 4 * kk + r][64 * cg + 4 * (l % 16)];
+      if (GF32 && fused_mgrad(P)) gm[r] = finish_mgrad(P, e[r], gr[r], gm[r], 15);
+      v4f out;
+      adan4<GF32, LARS>(P, S, SCAO_F32, gr[r], gm[r], corr, mm[r], vv[r], dd[r], pp[r], par[r],
+                        out, u2, 15);
+      gst4_nt(P.exp_avg + e[r], mm[r]);
+      gst4_nt(P.exp_avg_sq + e[r], vv[r]);
+      gst4_nt(P.exp_avg_diff + e[r], dd[r]);
+      gst4_nt(P.prev_grad + e[r], GF32 ? gm[r] : gr[r]);
+      if (LARS)
+        gst4(P.upd + e[r], out);
+      else
+        gst4_nt((float*)P.p + e[r], out);
+    }
+    const double wsum = wave_sum((double)u2);
+    if (l == 0) part[s & 1][w] = wsum;
+    if (s + 1 < nt) prefetch(s + 1);
+    __syncthreads();                                          // X_{s+1}
+  }
+  if (w == 0 && l == 0) put_slot(nt - 1);
+}
+
 // Reference operator: out = G + W U_r^T (dense m x n output).
 __device__ __forceinline__ void apply_out_tile(const scao_leaf_desc& L, const float* G, float* out, int i0,
                                int j0) {
@@ -1436,9 +1848,32 @@ extern "C" int scao_kron_apply(const scao_task* tasks, int ntasks, const scao_le
   SCAO_CHECK_ARG(ntasks >= 0, "scao_kron_apply: ntasks < 0");
   if (ntasks == 0) return SCAO_OK;
   SCAO_CHECK_ARG(tasks && leaves && params && stat && slots, "scao_kron_apply: null pointer");
-  SCAO_CHECK_ARG(variant >= 0 && variant < 16 && (variant < 8 || (variant & 4)),
+  SCAO_CHECK_ARG(variant >= 0 && variant < 64 && (variant < 8 || (variant & 4)),
                  "scao_kron_apply: bad variant %d", variant);
   hipStream_t s = (hipStream_t)stream;
+  if (variant & 16) {
+    const dim3 gs(ntasks), bs(768);
+#define SCAO_APPLY_STRIP(GF, LA, SWD) \
+  hipLaunchKernelGGL((k_apply_strip<GF, LA, SWD>), gs, bs, 0, s, tasks, leaves, params, stat, slots)
+    if (variant & 32) {
+      switch (variant & 3) {
+        case 0: SCAO_APPLY_STRIP(false, false, 128); break;
+        case 1: SCAO_APPLY_STRIP(true, false, 128); break;
+        case 2: SCAO_APPLY_STRIP(false, true, 128); break;
+        default: SCAO_APPLY_STRIP(true, true, 128); break;
+      }
+    } else {
+      switch (variant & 3) {
+        case 0: SCAO_APPLY_STRIP(false, false, 64); break;
+        case 1: SCAO_APPLY_STRIP(true, false, 64); break;
+        case 2: SCAO_APPLY_STRIP(false, true, 64); break;
+        default: SCAO_APPLY_STRIP(true, true, 64); break;
+      }
+    }
+#undef SCAO_APPLY_STRIP
+    SCAO_LAUNCH_CHECK("scao_kron_apply");
+    return SCAO_OK;
+  }
   if (variant & 8) {
     const dim3 gp((ntasks + SCAO_APPLY_GROUP - 1) / SCAO_APPLY_GROUP), bp(512);
 #define SCAO_APPLY_PIPE(GF, LA) \

@@ -240,7 +240,7 @@ def _flat_chunks(numel: int) -> int:
 
 _LEAF_TASKS = ("delta", "lift")   # with proj* and apply*: idx is a block index
 _TASK_TYPES = (["adam", "delta", "lift", "dred", "dapply", "lars"] +
-               [f"proj{v}" for v in range(12)] + [f"apply{v}" for v in range(16)])
+               [f"proj{v}" for v in range(12)] + [f"apply{v}" for v in range(64)])
 
 
 def _leaf_k(leaf) -> int:
@@ -321,17 +321,29 @@ def _param_tasks(it: PItem):
             ok = (leaf.use_kronecker and _leaf_vec(it, leaf, r0, c0l) and it.fp32 and it.aligned
                   and k % 16 == 0)
             m, n, T = leaf.m, leaf.n, L.APPLY_TILE
-            # wide 16x256 tiles over the interior that they tile exactly,
-            # masked 64x64 tiles over the right column strip and the
-            # bottom row strip
-            mw = m - m % L.APPLY_WIDE_ROWS if ok else 0
-            nw = n - n % L.APPLY_WIDE_COLS if ok else 0
-            if not (mw and nw):
-                mw = nw = 0
-            wide = var | 4 | (8 if k >= PIPE_MIN_RANK else 0)
-            for i0, j0 in _wide_tiles(mw, nw, k, k >= PIPE_MIN_RANK):
-                add(f"apply{wide}", (li, i0, j0, slot))
-                slot += 1
+            if ok and k in STRIP_RANKS:
+                # runs of strip tiles over the interior they tile exactly
+                sw = 64 if k == 256 else 128
+                tr = 8192 // sw
+                mw, nw = m - m % tr, n - n % sw
+                if not (mw and nw):
+                    mw = nw = 0
+                wide = var | 4 | 16 | (32 if sw == 128 else 0)
+                for i0, j0 in _strip_runs(mw, nw, tr, sw):
+                    add(f"apply{wide}", (li, i0, j0, slot))
+                    slot += min(L.APPLY_GROUP, (mw - i0) // tr)
+            else:
+                # wide 16x256 tiles over the interior that they tile exactly,
+                # masked 64x64 tiles over the right column strip and the
+                # bottom row strip
+                mw = m - m % L.APPLY_WIDE_ROWS if ok else 0
+                nw = n - n % L.APPLY_WIDE_COLS if ok else 0
+                if not (mw and nw):
+                    mw = nw = 0
+                wide = var | 4 | (8 if k >= PIPE_MIN_RANK else 0)
+                for i0, j0 in _wide_tiles(mw, nw, k, k >= PIPE_MIN_RANK):
+                    add(f"apply{wide}", (li, i0, j0, slot))
+                    slot += 1
             for i0 in range(0, m, T):
                 for j0 in range(nw, n, T):
                     add(f"apply{var}", (li, i0, j0, slot))
@@ -438,6 +450,18 @@ def _wide_tiles(mw: int, nw: int, k: int, pipelined: bool = False) -> list:
     return out
 
 
+STRIP_RANKS = (128, 256)   # ranks of the strip apply kernel (others >= PIPE_MIN_RANK: pipelined)
+
+
+def _strip_runs(mw: int, nw: int, tr: int, sw: int) -> list:
+    """(i0, j0) of a leaf's strip-apply runs: APPLY_GROUP tiles of tr rows
+    down one strip of sw columns each, band group by band group and, within
+    one, strip by strip, so the workgroups a die runs together share the
+    band group's W rows in L2 while each keeps its strip's U_r in LDS."""
+    step = L.APPLY_GROUP * tr
+    return [(i0, j0) for i0 in range(0, mw, step) for j0 in range(0, nw, sw)]
+
+
 def _xcd_interleave(tasks: np.ndarray, group: int = 1) -> np.ndarray:
     """Order a launch's tasks (int32 rows: idx, a, b, slot) so that every tile
     of one block runs on the same die: the blocks are dealt to XCDS queues
@@ -493,7 +517,9 @@ def _leaf_table(leaves, items: list[PItem], ws: Workspace):
     sizes = []
     for (leaf, r0, c0, pi) in leaves:
         k = _leaf_k(leaf)
-        sizes.append((_align4(k * leaf.n), _align4(k * k), _align4(leaf.m * k)))
+        # W, then (strip-apply ranks) its three bf16 planes: 1.5 floats per element
+        wsz = _align4(leaf.m * k) + (_align4((3 * leaf.m * k + 1) // 2) if k in STRIP_RANKS else 0)
+        sizes.append((_align4(k * leaf.n), _align4(k * k), wsz))
     total = sum(a + b + c for a, b, c in sizes)
     scratch = ws.buf("leaf_scratch", max(total, 1) * 4)
     base = scratch.data_ptr()
@@ -518,6 +544,8 @@ def _leaf_table(leaves, items: list[PItem], ws: Workspace):
         e["T"] = base + 4 * off
         e["Delta"] = base + 4 * (off + st)
         e["W"] = base + 4 * (off + st + sd)
+        k = leaf.U_l.shape[1]
+        e["Wb"] = base + 4 * (off + st + sd + _align4(leaf.m * k)) if k in STRIP_RANKS else 0
         off += st + sd + sw
         e["m"], e["n"], e["k"] = leaf.m, leaf.n, leaf.U_l.shape[1]
         vec = _leaf_vec(it, leaf, r0, c0) and _aligned16(int(e["T"]))
@@ -831,7 +859,7 @@ def _launch_step(ws: Workspace, raw: np.ndarray, n: int, update_norm_ema: bool) 
         _call("scao_diag_reduce", tp("dred"), N["dred"], P, SL, s)
     _call("scao_step_finalize", P, n, SL, S, ws.runtime.data_ptr(), 0,
            1 if update_norm_ema else 0, n, s)
-    for var in range(16):
+    for var in range(64):
         if N[f"apply{var}"]:
             _call("scao_kron_apply", tp(f"apply{var}"), N[f"apply{var}"], LF, P, S, SL, var, s)
     if N["dapply"]:

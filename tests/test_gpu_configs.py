@@ -234,10 +234,10 @@ def test_config_phase2_step(name, p0):
     gopt.step()
     torch.cuda.synchronize()
     # the launches are the bench's: wide tiles (variant bit 4) over whole
-    # blocks, through the pipelined kernel (bit 8) at k >= 128
+    # blocks, through a two-role kernel (pipelined bit 8, strip bit 16) at k >= 128
     ws = gopt._ws
     wide = sum(n for kind, n in ws.ntasks.items() if kind.startswith("apply") and int(kind[5:]) & 4)
-    pipe = sum(n for kind, n in ws.ntasks.items() if kind.startswith("apply") and int(kind[5:]) & 8)
+    pipe = sum(n for kind, n in ws.ntasks.items() if kind.startswith("apply") and int(kind[5:]) & 24)
     assert wide > 0
     assert (pipe > 0) == (c["k"] >= engine.PIPE_MIN_RANK)
     grp = ref.param_groups[0]

@@ -162,32 +162,38 @@ CASES = {
                                     use_int8_ema=False, k_min=128, k_max=128, warmup_steps=2,
                                     blend_steps=2, precond_freq=4, min_precond_updates=1,
                                     tau=None, lars_coeff=0.0), 6),
-    # k >= 128: the pipelined (two-role) apply kernel, with LARS staging and clip
-    "pipe_k128_lars": (FAST, dict(lr=1e-3, weight_decay=0.01, max_precond_dim=512, rho=0.999,
+    # k = 128 and 256: the strip apply kernel (bf16 split products; fp32
+    # products with filtered moments, SPARSE_CASES), LARS staging and clip
+    "strip_k128_lars": (FAST, dict(lr=1e-3, weight_decay=0.01, max_precond_dim=512, rho=0.999,
                                   use_int8_ema=True, k_min=128, k_max=128, warmup_steps=2,
                                   blend_steps=3, precond_freq=4, min_precond_updates=1, tau=1.0,
                                   lars_coeff=1e-3), 7),
-    # k = 192 (a multiple of 16, not of 128): the generic-k paths of the
-    # pipelined apply (no pairs), the lift and 64-row projection chunks
+    # k = 192 (a multiple of 16, neither 128 nor 256): the pipelined apply
+    # (no pairs), the lift's and the 64-row projection's generic-k chunks
     "pipe_k192_generic": (FAST, dict(lr=1e-3, weight_decay=0.01, max_precond_dim=512,
                                      rho=0.999, use_int8_ema=True, k_min=192, k_max=192,
                                      warmup_steps=2, blend_steps=2, precond_freq=4,
                                      min_precond_updates=1, tau=1.0, lars_coeff=1e-3), 6),
-    # k = 256 on a 2048 x 1024 block: W and U_r (3 MB) exceed what the wide
-    # tiles' row-major order keeps in L2, so they run in super-tiles
-    "pipe_k256_supertile": ({"big": (2048, 1024), "ln": (1024,)},
+    # k = 256 on a 2048 x 1024 block: runs of eight 128-row tiles in 16
+    # strips, two band groups
+    "strip_k256_tall": ({"big": (2048, 1024), "ln": (1024,)},
                             dict(lr=1e-3, weight_decay=0.01, max_precond_dim=2048, rho=0.999,
                                  use_int8_ema=True, k_min=256, k_max=256, warmup_steps=2,
                                  blend_steps=2, precond_freq=4, min_precond_updates=1, tau=1.0,
                                  lars_coeff=1e-3), 6),
-    # k = 256 where a block's run of wide tiles is short (17 bands: runs of
-    # 8, 8, 1) or crosses strips (two strips, row-major): the back-projection
-    # pairs tiles of one strip and computes the others one at a time
-    "pipe_k256_ragged_runs": ({"a": (272, 256), "b": (256, 512), "ln": (256,)},
+    # k = 256 where a block's runs are short (272 rows: two 128-row tiles and
+    # a masked 16-row remainder) and a block with one band of tiles
+    "strip_k256_ragged_runs": ({"a": (272, 256), "b": (256, 512), "ln": (256,)},
                               dict(lr=1e-3, weight_decay=0.01, max_precond_dim=2048, rho=0.999,
                                    use_int8_ema=True, k_min=256, k_max=256, warmup_steps=2,
                                    blend_steps=2, precond_freq=4, min_precond_updates=1,
                                    tau=1.0, lars_coeff=1e-3), 6),
+    # k = 256 without LARS or weight decay: the strip kernel writes p itself
+    "strip_k256_nolars": ({"a": (384, 512), "ln": (512,)},
+                          dict(lr=1e-3, weight_decay=0.0, max_precond_dim=2048, rho=0.999,
+                               use_int8_ema=False, k_min=256, k_max=256, warmup_steps=2,
+                               blend_steps=2, precond_freq=4, min_precond_updates=1,
+                               tau=None, lars_coeff=0.0), 6),
 }
 
 
@@ -547,6 +553,9 @@ SPARSE_CASES = {
     "fast_k64": (FAST, dict(CASES["fast_k64"][1], sparsity=0.7)),
     "fast_k128": (FAST, dict(CASES["fast_k128_nolars"][1], sparsity=0.7, lars_coeff=1e-3,
                              tau=1.0, weight_decay=0.01)),
+    # the strip kernel's fp32-product path (filtered moments) at k = 256
+    "strip_k256": (CASES["strip_k256_ragged_runs"][0],
+                   dict(CASES["strip_k256_ragged_runs"][1], sparsity=0.7)),
 }
 
 

@@ -362,16 +362,60 @@ def test_structure_cache_matches_fresh_builds():
     assert cache
 
 
-def test_pipelined_apply_tasks():
-    """Wide tasks of blocks with k >= PIPE_MIN_RANK carry variant bit 8 and are
-    ordered in runs of APPLY_GROUP tasks of one die's queue."""
+def _phase2_items(shapes, k):
     from scao_amd.engine import PItem
     items = []
-    for shp in [(1024, 2048)] * 8 + [(512, 1536)]:
+    for shp in shapes:
         p = torch.zeros(shp)
-        pre = SparsePreconditioner(p, k_min=128, k_max=128, max_precond_dim=2048)
+        pre = SparsePreconditioner(p, k_min=k, k_max=k, max_precond_dim=2048)
         items.append(PItem(p=p, graw=p, gmom=None, st={}, group={}, pre=pre, phase2=True,
                            step=3, lars=True, leaves=list(pre.leaves())))
+    return items
+
+
+@pytest.mark.parametrize("k", [128, 256])
+def test_strip_apply_tasks(k):
+    """Blocks of rank 128 / 256 go to the strip kernel (variant bits 16, and
+    32 for k = 128): each task a run of at most APPLY_GROUP tiles of TR rows
+    down one SW-column strip; the runs tile every block interior once, their
+    slot ranges are disjoint, and a block's runs stay on one die's queue
+    (workgroup b takes queue b % XCDS)."""
+    items = _phase2_items([(1024, 2048)] * 8 + [(640, 1536)], k)
+    arrays, _, nslot, leaves = E._build_structure(items)
+    sw = 64 if k == 256 else 128
+    tr = 8192 // sw
+    var = 2 | 4 | 16 | (32 if k == 128 else 0)
+    runs = arrays[f"apply{var}"]
+    assert all(len(arrays[f"apply{v}"]) == 0 for v in (14, 6) if v != var)
+    cover = {}
+    spans = []
+    for t in runs:
+        lf = leaves[int(t["idx"])][0]
+        mw, nw = lf.m - lf.m % tr, lf.n - lf.n % sw
+        a, b = int(t["a"]), int(t["b"])
+        nt = min(L.APPLY_GROUP, (mw - a) // tr)
+        assert nt >= 1 and a % tr == 0 and b % sw == 0 and b + sw <= nw
+        for i in range(nt):
+            key = (int(t["idx"]), a + i * tr, b)
+            assert key not in cover
+            cover[key] = 1
+        spans.append((int(t["slot"]), nt))
+    assert len(cover) == sum((lf.m // tr) * (lf.n // sw) for lf, *_ in leaves)
+    spans.sort()
+    for (s0, n0), (s1, _) in zip(spans, spans[1:]):
+        assert s1 >= s0 + n0
+    assert spans[-1][0] + spans[-1][1] <= nslot
+    queue_of = {}
+    for b, t in enumerate(runs[:E.XCDS * 16]):
+        queue_of.setdefault(int(t["idx"]), b % E.XCDS)
+        assert queue_of[int(t["idx"])] == b % E.XCDS
+
+
+def test_pipelined_apply_tasks():
+    """Wide tasks of blocks with another rank >= PIPE_MIN_RANK (here 192)
+    carry variant bit 8 and are ordered in runs of APPLY_GROUP tasks of one
+    die's queue."""
+    items = _phase2_items([(1024, 2048)] * 8 + [(512, 1536)], 192)
     arrays, _, _, leaves = E._build_structure(items)
     pipe = arrays["apply14"]
     assert len(pipe) == sum(lf.m // 16 * (lf.n // 256) for lf, *_ in leaves)
