@@ -38,9 +38,8 @@ namespace {
 // ||p*decay||^2 from the staged registers (every element of the strip passes
 // through exactly one thread).
 constexpr int PR = 32;           // rows per chunk
-// Whole fp32 tiles (the FAST variants) on the bf16 matrix cores
+// Whole fp32 tiles (the FAST variants) run on the bf16 matrix cores
 // (project_tile_x6) with 256 threads for 64 rows of T and 512 for 128 or 256.
-constexpr bool PROJECT_X6 = true;
 constexpr int X6_NT128 = 512;
 constexpr int GP = SCAO_PROJ_COLS + 4;  // LDS pitch of the G chunk
 
@@ -225,7 +224,7 @@ __device__ __forceinline__ void project_tile_x6(const scao_leaf_desc& L, const s
   static_assert(UW == 2 || UW == 4, "U_l loader width");
   typedef float vj __attribute__((ext_vector_type(NJ)));
   typedef __attribute__((address_space(1))) vj gvj;
-  __shared__ __attribute__((aligned(16))) __bf16 Us[3][CR][UCP];
+  __shared__ __attribute__((aligned(16))) __bf16 Us[2][3][CR][UCP];   // by chunk parity
   __shared__ double red[2 * NT / 64];
   const int tid = threadIdx.x;
   const int w = tid / 64, l = tid % 64;
@@ -247,13 +246,15 @@ __device__ __forceinline__ void project_tile_x6(const scao_leaf_desc& L, const s
 
   vj rg[8], rp[8];
   float ru[4][UW];
-  auto load_chunk = [&](int i0) {
+  auto load_g = [&](int i0) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int64_t o = L.off + (int64_t)(i0 + 8 * g + e) * ld + gcol;
       rg[e] = __builtin_nontemporal_load((const gvj*)((const float*)P.graw + o));
       if (DO_P) rp[e] = __builtin_nontemporal_load((const gvj*)((const float*)P.p + o));
     }
+  };
+  auto load_u = [&](int i0) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const float* src = L.Ul + (int64_t)(i0 + 4 * ua + r) * k + c0 + ub * UW;
@@ -269,33 +270,10 @@ __device__ __forceinline__ void project_tile_x6(const scao_leaf_desc& L, const s
     }
   };
 
-  load_chunk(0);
-  for (int i0 = 0; i0 < m; i0 += PR) {
-    // this chunk's G operands, split in registers
-    bf3 bg[NJ];
-#pragma unroll
-    for (int t = 0; t < NJ; ++t) {
-      float x[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = rg[e][t];
-      bg[t] = split_bf3(x);
-    }
-    if (do_norms) {
-      float a = 0.f, b = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-#pragma unroll
-        for (int t = 0; t < NJ; ++t) {
-          a = fmaf(rg[e][t], rg[e][t], a);
-          if (DO_P) {
-            const float x = decay ? rp[e][t] * P.decay : rp[e][t];
-            b = fmaf(x, x, b);
-          }
-        }
-      g2 += (double)a;
-      p2 += (double)b;
-    }
-    if (i0) __syncthreads();              // the previous chunk's U_l planes are consumed
+  // U_l's planes for chunk i sit in Us[i & 1]: chunk i+1's are split and
+  // written during chunk i (its raw rows were loaded a chunk earlier), so one
+  // barrier per chunk separates a buffer's readers from its next writers
+  auto write_u = [&](int buf) {
 #pragma unroll
     for (int c = 0; c < UW; ++c) {
       // four rows of one column: one 8-byte write per plane
@@ -320,19 +298,54 @@ __device__ __forceinline__ void project_tile_x6(const scao_leaf_desc& L, const s
       }
       const int col = ub * UW + c;
 #pragma unroll
-      for (int pp = 0; pp < 3; ++pp) *(v2u*)&Us[pp][col][4 * ua] = pl[pp];
+      for (int pp = 0; pp < 3; ++pp) *(v2u*)&Us[buf][pp][col][4 * ua] = pl[pp];
     }
-    __syncthreads();
-    if (i0 + PR < m) load_chunk(i0 + PR); // in flight during the MFMAs below
+  };
+  load_g(0);
+  load_u(0);
+  write_u(0);
+  if (PR < m) load_u(PR);
+  __syncthreads();
+  for (int i0 = 0, cur = 0; i0 < m; i0 += PR, cur ^= 1) {
+    // this chunk's G operands, split in registers
+    bf3 bg[NJ];
+#pragma unroll
+    for (int t = 0; t < NJ; ++t) {
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = rg[e][t];
+      bg[t] = split_bf3(x);
+    }
+    if (do_norms) {
+      float a = 0.f, b = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+#pragma unroll
+        for (int t = 0; t < NJ; ++t) {
+          a = fmaf(rg[e][t], rg[e][t], a);
+          if (DO_P) {
+            const float x = decay ? rp[e][t] * P.decay : rp[e][t];
+            b = fmaf(x, x, b);
+          }
+        }
+      g2 += (double)a;
+      p2 += (double)b;
+    }
+    if (i0 + PR < m) {
+      write_u(cur ^ 1);                   // read after the barrier below
+      load_g(i0 + PR);                    // in flight during the MFMAs below
+      if (i0 + 2 * PR < m) load_u(i0 + 2 * PR);
+    }
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       bf3 au;
-      au.h = *(const v8bf*)&Us[0][16 * q + jj][8 * g];
-      au.m = *(const v8bf*)&Us[1][16 * q + jj][8 * g];
-      au.l = *(const v8bf*)&Us[2][16 * q + jj][8 * g];
+      au.h = *(const v8bf*)&Us[cur][0][16 * q + jj][8 * g];
+      au.m = *(const v8bf*)&Us[cur][1][16 * q + jj][8 * g];
+      au.l = *(const v8bf*)&Us[cur][2][16 * q + jj][8 * g];
 #pragma unroll
       for (int t = 0; t < NJ; ++t) acc[q][t] = mfma_x6(au, bg[t], acc[q][t]);
     }
+    __syncthreads();
   }
   // T[c][j] for c = c0 + 16q + 4g + r, j = gcol + t
 #pragma unroll
@@ -1795,7 +1808,7 @@ extern "C" int scao_kron_project(const scao_task* tasks, int ntasks, const scao_
                  "scao_kron_project: bad variant %d", variant);
   hipStream_t s = (hipStream_t)stream;
   dim3 g(ntasks), b(256);
-  if (PROJECT_X6 && (variant & 1)) {
+  if (variant & 1) {
     const dim3 b512(512), b128(X6_NT128);
     switch (variant) {
       case 1: hipLaunchKernelGGL((k_project_x6<false, 64, 256>), g, b, 0, s, tasks, leaves, params, slots); break;
