@@ -27,7 +27,6 @@ constexpr int GT = SCAO_GRAM_TILE;  // 128
 constexpr int KC = 32;              // K chunk
 constexpr int LP = GT + 4;          // padded LDS row of an operand chunk
 constexpr int SP = GT + 1;          // LDS row of the staged output tile
-constexpr bool GRAM_X6 = true;      // whole fp32 tiles on the bf16 matrix cores (gram_kloop_x6)
 
 // Operand chunks X[r0:r0+128][kb:kb+32], four 4-element loads per thread,
 // held in registers (raw, in the gradient's dtype) from chunk_load until
@@ -402,14 +401,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   gram_kloop<DT, SIDE>(D, dim, K, i0, j0, diag, vec, As, Bs, wr, wc, tot)
   __bf16* Ap = (__bf16*)smem;
   __bf16* Bp = Ap + 3 * XPL;
-  if (GRAM_X6 && whole && D.dtype == SCAO_F32 && D.side == 0)
+  if (whole && D.dtype == SCAO_F32 && D.side == 0)
     gram_kloop_x6<0>(D, K, i0, j0, diag, Ap, Bp, wr, wc, tot);
-  else if (GRAM_X6 && whole && D.dtype == SCAO_F32)
-    gram_kloop_x6<1>(D, K, i0, j0, diag, Ap, Bp, wr, wc, tot);
-  else if (whole && D.dtype == SCAO_F32 && D.side == 0)
-    SCAO_GRAM_KLOOP(SCAO_F32, 0);
   else if (whole && D.dtype == SCAO_F32)
-    SCAO_GRAM_KLOOP(SCAO_F32, 1);
+    gram_kloop_x6<1>(D, K, i0, j0, diag, Ap, Bp, wr, wc, tot);
   else if (whole && D.dtype == SCAO_BF16 && D.side == 0)
     SCAO_GRAM_KLOOP(SCAO_BF16, 0);
   else if (whole && D.dtype == SCAO_BF16)
