@@ -301,10 +301,18 @@ __device__ __forceinline__ void project_tile_x6(const scao_leaf_desc& L, const s
       for (int pp = 0; pp < 3; ++pp) *(v2u*)&Us[buf][pp][col][4 * ua] = pl[pp];
     }
   };
+  // CR = 256: the prefetches are unconditional, clamped to the last chunk
+  // (m % PR == 0 for these tiles), and pinned ahead of the MFMAs: behind a
+  // branch, the join makes the compiler wait for every load in flight, the
+  // next chunk's G included, and the scheduler sinks them among the MFMAs.
+  // The narrower tiles have half or a quarter of the MFMAs per chunk to hide
+  // loads behind and measured faster with the branch (the last chunk loads
+  // nothing).
+  const int last = m - PR;
   load_g(0);
   load_u(0);
   write_u(0);
-  if (PR < m) load_u(PR);
+  if (CR == 256 || PR < m) load_u(PR < last ? PR : last);
   __syncthreads();
   for (int i0 = 0, cur = 0; i0 < m; i0 += PR, cur ^= 1) {
     // this chunk's G operands, split in registers
@@ -331,9 +339,14 @@ __device__ __forceinline__ void project_tile_x6(const scao_leaf_desc& L, const s
       g2 += (double)a;
       p2 += (double)b;
     }
-    if (i0 + PR < m) {
-      write_u(cur ^ 1);                   // read after the barrier below
-      load_g(i0 + PR);                    // in flight during the MFMAs below
+    if constexpr (CR == 256) {
+      write_u(cur ^ 1);                   // chunk i+1's planes, read after the barrier below
+      load_g(i0 + PR < last ? i0 + PR : last);   // in flight during the MFMAs below
+      load_u(i0 + 2 * PR < last ? i0 + 2 * PR : last);
+      __builtin_amdgcn_sched_barrier(0);
+    } else if (i0 + PR < m) {
+      write_u(cur ^ 1);
+      load_g(i0 + PR);
       if (i0 + 2 * PR < m) load_u(i0 + 2 * PR);
     }
 #pragma unroll
