@@ -243,9 +243,23 @@ _TASK_TYPES = (["adam", "delta", "lift", "dred", "dapply", "lars"] +
                [f"proj{v}" for v in range(12)] + [f"apply{v}" for v in range(64)])
 
 
+STEP_WIDTHS = (64, 128, 256)   # eigenfactor widths the step kernels are built for
+
+
 def _leaf_k(leaf) -> int:
-    """Rank of a step leaf: its eigenfactor width, 0 for a diagonal sub-block."""
-    return leaf.U_l.shape[1] if leaf.use_kronecker else 0
+    """Width of a step leaf's eigenfactors in the step: its rank rounded up to
+    64, 128 or 256 (beyond 256, to a multiple of 64); 0 for a diagonal
+    sub-block.  The reference's adaptive rank moves k by -1..+4 per refresh,
+    so most ranks are no multiple of 16; a padded leaf runs the whole-tile
+    kernels on zero-padded copies of U_l and U_r (_leaf_table).  The padded
+    rows of T and P are zero, so Delta, W and nu^2 are the unpadded ones."""
+    if not leaf.use_kronecker:
+        return 0
+    k = leaf.U_l.shape[1]
+    for w in STEP_WIDTHS:
+        if k <= w:
+            return w
+    return -(-k // 64) * 64
 
 
 def _param_tasks(it: PItem):
@@ -280,7 +294,7 @@ def _param_tasks(it: PItem):
             if not leaf.use_kronecker:
                 continue
             m, n = leaf.m, leaf.n
-            k = leaf.U_l.shape[1]
+            k = _leaf_k(leaf)
             vec = _leaf_vec(it, leaf, r0, c0l)
             for j0 in range(0, n, L.PROJ_COLS):
                 whole = vec and it.fp32 and j0 + L.PROJ_COLS <= n and m % 32 == 0
@@ -306,7 +320,7 @@ def _param_tasks(it: PItem):
                         add("delta", (li, a, b, slot))
                         slot += 1
                 continue
-            k = leaf.U_l.shape[1]
+            k = _leaf_k(leaf)
             for a in range(0, k, 64):
                 for b in range(0, k, 64):
                     add("delta", (li, a, b, slot))
@@ -512,6 +526,43 @@ def _leaf_vec(it: PItem, leaf, r0: int, c0: int) -> bool:
             and it.aligned)
 
 
+def _padded_factors(leaves, ws: Workspace) -> dict:
+    """{leaf index: (U_l, U_r, S_l, S_r)} padded to _leaf_k columns for the
+    leaves whose rank is below it: U's extra columns zero, S's extra entries
+    1.0 (finite, so (s_l s_r - 1) * 0 stays 0).  Written on the current
+    stream, ahead of the step's kernels, each time the block table is built
+    (any change to the factors moves leaf_epoch, which rebuilds it)."""
+    need = []
+    for i, (leaf, *_r) in enumerate(leaves):
+        if leaf.use_kronecker and _leaf_k(leaf) != leaf.U_l.shape[1]:
+            need.append(i)
+    if not need:
+        return {}
+    sizes = []
+    for i in need:
+        leaf, kp = leaves[i][0], _leaf_k(leaves[i][0])
+        sizes.append((_align4(leaf.m * kp), _align4(leaf.n * kp), _align4(kp), _align4(kp)))
+    buf = ws.buf("leaf_pad", sum(map(sum, sizes)) * 4).view(torch.float32)
+    out, off = {}, 0
+    for i, sz in zip(need, sizes):
+        leaf, kp = leaves[i][0], _leaf_k(leaves[i][0])
+        k = leaf.U_l.shape[1]
+        views = []
+        for (src, rows), n in zip(((leaf.U_l, leaf.m), (leaf.U_r, leaf.n), (leaf.S_l, 1),
+                                   (leaf.S_r, 1)), sz):
+            v = buf[off:off + rows * kp].view(rows, kp) if src.ndim == 2 else buf[off:off + kp]
+            if src.ndim == 2:
+                v.zero_()
+                v[:, :k].copy_(src)
+            else:
+                v.fill_(1.0)
+                v[:k].copy_(src)
+            views.append(v)
+            off += n
+        out[i] = tuple(views)
+    return out
+
+
 def _leaf_table(leaves, items: list[PItem], ws: Workspace):
     """Block descriptors plus T/Delta/W scratch for every Phase-2 block."""
     sizes = []
@@ -523,6 +574,7 @@ def _leaf_table(leaves, items: list[PItem], ws: Workspace):
     total = sum(a + b + c for a, b, c in sizes)
     scratch = ws.buf("leaf_scratch", max(total, 1) * 4)
     base = scratch.data_ptr()
+    pads = _padded_factors(leaves, ws)
     tab = np.zeros(len(leaves), dtype=L.LEAF_DESC)
     off = 0
     for i, ((leaf, r0, c0, pi), (st, sd, sw)) in enumerate(zip(leaves, sizes)):
@@ -539,15 +591,20 @@ def _leaf_table(leaves, items: list[PItem], ws: Workspace):
             e["flags"] = L.LF_DIAG
             e["dbias"] = getattr(leaf, "_diag_bias_factor", 1.0)
             continue
-        e["Ul"], e["Ur"] = leaf.U_l.data_ptr(), leaf.U_r.data_ptr()
-        e["Sl"], e["Sr"] = leaf.S_l.data_ptr(), leaf.S_r.data_ptr()
+        k = _leaf_k(leaf)
+        if k == leaf.U_l.shape[1]:
+            e["Ul"], e["Ur"] = leaf.U_l.data_ptr(), leaf.U_r.data_ptr()
+            e["Sl"], e["Sr"] = leaf.S_l.data_ptr(), leaf.S_r.data_ptr()
+        else:
+            ul, ur, sl, sr = pads[i]
+            e["Ul"], e["Ur"], e["Sl"], e["Sr"] = (ul.data_ptr(), ur.data_ptr(), sl.data_ptr(),
+                                                  sr.data_ptr())
         e["T"] = base + 4 * off
         e["Delta"] = base + 4 * (off + st)
         e["W"] = base + 4 * (off + st + sd)
-        k = leaf.U_l.shape[1]
         e["Wb"] = base + 4 * (off + st + sd + _align4(leaf.m * k)) if k in STRIP_RANKS else 0
         off += st + sd + sw
-        e["m"], e["n"], e["k"] = leaf.m, leaf.n, leaf.U_l.shape[1]
+        e["m"], e["n"], e["k"] = leaf.m, leaf.n, k
         vec = _leaf_vec(it, leaf, r0, c0) and _aligned16(int(e["T"]))
         e["flags"] = L.LF_VEC4 if vec else 0
     return tab

@@ -168,9 +168,9 @@ CASES = {
                                   use_int8_ema=True, k_min=128, k_max=128, warmup_steps=2,
                                   blend_steps=3, precond_freq=4, min_precond_updates=1, tau=1.0,
                                   lars_coeff=1e-3), 7),
-    # k = 192 (a multiple of 16, neither 128 nor 256): the pipelined apply
-    # (no pairs), the lift's and the 64-row projection's generic-k chunks
-    "pipe_k192_generic": (FAST, dict(lr=1e-3, weight_decay=0.01, max_precond_dim=512,
+    # k = 192: zero-padded to the step width 256 (strip apply, 256-row
+    # projection); the padded rows of T and P are zero
+    "pad_k192": (FAST, dict(lr=1e-3, weight_decay=0.01, max_precond_dim=512,
                                      rho=0.999, use_int8_ema=True, k_min=192, k_max=192,
                                      warmup_steps=2, blend_steps=2, precond_freq=4,
                                      min_precond_updates=1, tau=1.0, lars_coeff=1e-3), 6),
@@ -188,6 +188,13 @@ CASES = {
                                    use_int8_ema=True, k_min=256, k_max=256, warmup_steps=2,
                                    blend_steps=2, precond_freq=4, min_precond_updates=1,
                                    tau=1.0, lars_coeff=1e-3), 6),
+    # k = 320, above the strip widths: the pipelined apply (no pairs), the
+    # lift's generic-k chunks and 64-row projection tiles
+    "pipe_k320": ({"a": (512, 640), "ln": (640,)},
+                  dict(lr=1e-3, weight_decay=0.01, max_precond_dim=2048, rho=0.999,
+                       use_int8_ema=True, k_min=320, k_max=320, warmup_steps=2,
+                       blend_steps=2, precond_freq=4, min_precond_updates=1, tau=1.0,
+                       lars_coeff=1e-3), 6),
     # k = 256 without LARS or weight decay: the strip kernel writes p itself
     "strip_k256_nolars": ({"a": (384, 512), "ln": (512,)},
                           dict(lr=1e-3, weight_decay=0.0, max_precond_dim=2048, rho=0.999,

@@ -412,10 +412,10 @@ def test_strip_apply_tasks(k):
 
 
 def test_pipelined_apply_tasks():
-    """Wide tasks of blocks with another rank >= PIPE_MIN_RANK (here 192)
-    carry variant bit 8 and are ordered in runs of APPLY_GROUP tasks of one
-    die's queue."""
-    items = _phase2_items([(1024, 2048)] * 8 + [(512, 1536)], 192)
+    """Wide tasks of blocks with another step width >= PIPE_MIN_RANK (here
+    320) carry variant bit 8 and are ordered in runs of APPLY_GROUP tasks of
+    one die's queue."""
+    items = _phase2_items([(1024, 2048)] * 8 + [(512, 1536)], 320)
     arrays, _, _, leaves = E._build_structure(items)
     pipe = arrays["apply14"]
     assert len(pipe) == sum(lf.m // 16 * (lf.n // 256) for lf, *_ in leaves)
@@ -631,3 +631,36 @@ def test_eigen_route_by_size_and_shape():
     assert engine.batch_route("hip", 4096, 3) == "hip"
     assert engine.batch_route("hip", 1024, 1) == "hip"
     assert engine.batch_route("diag", 4096, 1) == "diag"
+
+
+@pytest.mark.parametrize("k,width", [(1, 64), (8, 64), (50, 64), (64, 64), (65, 128), (127, 128),
+                                     (128, 128), (129, 256), (192, 256), (256, 256), (300, 320)])
+def test_step_width_pads_ranks(k, width):
+    """A block's eigenfactors enter the step at width 64, 128 or 256 (beyond,
+    a multiple of 64); a padded block gets zero-padded U copies and S copies
+    padded with 1.0, and its projection and apply tasks are the whole-tile
+    ones of that width."""
+    items = _phase2_items([(512, 768)], k)   # whole 256-column projection tiles
+    leaf = items[0].leaves[0][0]
+    assert leaf.U_l.shape[1] == k and E._leaf_k(leaf) == width
+    g = torch.Generator().manual_seed(k)
+    leaf.U_l = torch.randn(leaf.m, k, generator=g)
+    leaf.U_r = torch.randn(leaf.n, k, generator=g)
+    leaf.S_l, leaf.S_r = torch.rand(k, generator=g), torch.rand(k, generator=g)
+    ws = E.Workspace(torch.device("cpu"))
+    pads = E._padded_factors([(leaf, 0, 0, 0)], ws)
+    if width == k:
+        assert pads == {}
+    else:
+        ul, ur, sl, sr = pads[0]
+        assert ul.shape == (leaf.m, width) and ur.shape == (leaf.n, width)
+        assert torch.equal(ul[:, :k], leaf.U_l) and not ul[:, k:].any()
+        assert torch.equal(ur[:, :k], leaf.U_r) and not ur[:, k:].any()
+        assert torch.equal(sl[:k], leaf.S_l) and bool((sl[k:] == 1.0).all())
+        assert torch.equal(sr[:k], leaf.S_r) and bool((sr[k:] == 1.0).all())
+    arrays, _, _, _ = E._build_structure(items)
+    proj = [kind for kind, arr in arrays.items() if kind.startswith("proj") and len(arr)]
+    assert proj and all(int(kind[4:]) & 1 for kind in proj)        # whole-tile (bf16) tiles
+    wide = sum(len(arr) for kind, arr in arrays.items()
+               if kind.startswith("apply") and int(kind[5:]) & 4)
+    assert wide > 0
