@@ -38,7 +38,7 @@
 extern "C" {
 #endif
 
-#define SCAO_ABI_VERSION 11
+#define SCAO_ABI_VERSION 12
 
 enum scao_status { SCAO_OK = 0, SCAO_ERR_INVALID = 1, SCAO_ERR_HIP = 2 };
 enum scao_dtype { SCAO_F32 = 0, SCAO_BF16 = 1, SCAO_F16 = 2 };
@@ -163,6 +163,16 @@ int scao_struct_layout(int which, int64_t* out, int cap);
  * G has row stride ldG; out is dense m x n.  workspace: k*n + k*k + m*k
  * floats + 4 leaf/task descriptors worth of bytes given by
  * scao_fused_kronecker_workspace(). */
+/* <- scao.cuda.low_rank_precond_mm (scao/cuda/__init__.py:190-228; kernels
+ * scao/cuda/low_rank_ops.cu:239-296).  left != 0: out = (U*s) (U^T G) with U
+ * m x k; left == 0: out = (G (U*s)) U^T with U n x k; G and out m x n, all
+ * contiguous fp32 on the device, s of length k.  The products run in that
+ * order, U*s rounded to fp32 (the reference's fallback, :102-119, which is the
+ * path the reference runs).  ws: scao_low_rank_precond_mm_workspace bytes
+ * (the k x n or m x k intermediate). */
+int64_t scao_low_rank_precond_mm_workspace(int64_t m, int64_t n, int64_t k, int left);
+int scao_low_rank_precond_mm(const float* U, const float* s, const float* G, float* out,
+                             int64_t m, int64_t n, int64_t k, int left, float* ws, void* stream);
 int64_t scao_fused_kronecker_workspace(int64_t m, int64_t n, int64_t k);
 int scao_fused_kronecker_precond(const float* U_l, const float* s_l_inv4, const float* U_r,
                                  const float* s_r_inv4, const float* G, int64_t ldG, float* out,

@@ -21,7 +21,7 @@ import torch  # noqa: F401  -- loads torch's HIP runtime before ours
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.environ.get("SCAO_AMD_LIB", os.path.join(HERE, "_lib", "libscao_amd.so"))
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 SLOT_WIDTH = 3
 FLAT_CHUNK = 4096
 PROJ_COLS = 256
@@ -112,6 +112,8 @@ SIGNATURES = {
     "scao_abi_version": (_I, []),
     "scao_last_error": (ctypes.c_char_p, []),
     "scao_struct_layout": (_I, [_I, _VP, _I]),
+    "scao_low_rank_precond_mm_workspace": (_I64, [_I64, _I64, _I64, _I]),
+    "scao_low_rank_precond_mm": (_I, [_VP, _VP, _VP, _VP, _I64, _I64, _I64, _I, _VP, _VP]),
     "scao_fused_kronecker_workspace": (_I64, [_I64, _I64, _I64]),
     "scao_fused_kronecker_precond": (_I, [_VP, _VP, _VP, _VP, _VP, _I64, _VP, _I64, _I64, _I64,
                                           _VP, _VP]),

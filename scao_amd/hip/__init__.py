@@ -60,9 +60,9 @@ def fused_kronecker_precond(U_l: Tensor, s_l_inv4: Tensor, U_r: Tensor, s_r_inv4
 
 def low_rank_precond_mm(U: Tensor, s: Tensor, G: Tensor, left: bool = True) -> Tensor:
     """left=True: U diag(s) U^T G;  left=False: G U diag(s) U^T
-    (reference :190-228, whose kernel path and fallback :100-117 both compute
-    (U*s) @ (U^T @ G) and (G @ (U*s)) @ U^T).  Not on the optimizer step:
-    two plain GEMMs, run by rocBLAS on the device in that order."""
+    (reference :190-228; its fallback :102-119 computes (U*s) @ (U^T @ G)
+    and (G @ (U*s)) @ U^T).  Not on the optimizer step: two launches of the
+    library's strided fp32 GEMM in that order (scao_low_rank_precond_mm)."""
     for t, nm in ((U, "U"), (s, "s"), (G, "G")):
         _check(t, nm)
     if G.ndim != 2 or U.ndim != 2 or s.numel() != U.shape[1]:
@@ -71,10 +71,19 @@ def low_rank_precond_mm(U: Tensor, s: Tensor, G: Tensor, left: bool = True) -> T
     d = G.shape[0] if left else G.shape[1]
     if U.shape[0] != d:
         raise ValueError(f"U has {U.shape[0]} rows, G's {'rows' if left else 'columns'} are {d}")
-    Us = U * s.reshape(1, -1)
-    if left:
-        return Us @ (U.T @ G)
-    return (G @ Us) @ U.T
+    m, n = G.shape
+    k = U.shape[1]
+    out = torch.empty(m, n, dtype=torch.float32, device=G.device)
+    if m == 0 or n == 0:
+        return out
+    if k == 0:
+        return out.zero_()
+    U, s, G = U.contiguous(), s.contiguous(), G.contiguous()
+    ws = torch.empty(max(1, L.lib().scao_low_rank_precond_mm_workspace(m, n, k, int(left)) // 4),
+                     dtype=torch.float32, device=G.device)
+    L.call("scao_low_rank_precond_mm", U.data_ptr(), s.data_ptr(), G.data_ptr(), out.data_ptr(),
+           m, n, k, int(left), ws.data_ptr(), L.stream_ptr(G.device))
+    return out
 
 
 def int8_ema_update(ema_q: Tensor, ema_scale: float, new_val: Tensor, rho: float):

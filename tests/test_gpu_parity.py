@@ -771,6 +771,25 @@ def test_low_rank_precond_mm_golden_vectors():
             assert _rel(out, want) < 1e-5, (i, side)
 
 
+@pytest.mark.parametrize("m,n,k", [(70, 90, 20), (256, 64, 64), (1, 5, 3), (300, 129, 257)])
+def test_low_rank_precond_mm_shapes(m, n, k):
+    """The library's low_rank_precond_mm on shapes off the 64-tiles (edges,
+    k above one tile, a single row) against float64 on the CPU, both sides."""
+    from scao_amd.hip import low_rank_precond_mm
+    dev = _dev()
+    g = torch.Generator().manual_seed(m * 7 + n + k)
+    G = torch.randn(m, n, generator=g)
+    s = torch.rand(k, generator=g) + 0.5
+    for left in (True, False):
+        U = torch.randn(m if left else n, k, generator=g) / (k ** 0.5)
+        out = low_rank_precond_mm(U.to(dev), s.to(dev), G.to(dev), left).cpu()
+        Ud, sd, Gd = U.double(), s.double(), G.double()
+        want = (Ud * sd) @ (Ud.T @ Gd) if left else (Gd @ (Ud * sd)) @ Ud.T
+        scale = ((Ud.abs() * sd) @ (Ud.abs().T @ Gd.abs()) if left
+                 else (Gd.abs() @ (Ud.abs() * sd)) @ Ud.abs().T)
+        assert float(((out.double() - want).abs() / (scale + 1e-30)).max()) < 1e-5, (m, n, k, left)
+
+
 FEATURES = {
     # gSNR mask on the update (reference scao/optimizer.py:160-181)
     "gsnr": (dict(CASES["fp32_small"][1], use_gsnr_clip=True, gsnr_threshold=0.5), 12),
