@@ -1327,16 +1327,15 @@ __global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict_
 }
 
 // ---------------------------------------------- strip-resident apply ---
-// Large-rank blocks (16 <= k <= 256, k % 16 == 0).  A task is a run of up to
-// SCAO_APPLY_GROUP tiles of one column strip of SW columns, TR = 8192 / SW
-// rows each (SW = 64 for k > 128, 128 otherwise), going down the block.  The
-// strip's U_r rows stay in LDS for the whole run, so the back-projection
-// reads only W rows from L2 instead of every wave refetching U_r per tile.
-// One 12-wave workgroup per CU:
-//   waves 8..11 (MFMA role): corr(s) = W[rows of tile s, :] U_r[strip, :]^T,
+// Blocks of rank k = 128 or 256.  A task is a run of up to SCAO_APPLY_GROUP
+// tiles of one column strip, SW columns x TR rows each (strip_shape: 64 x 128
+// at k = 256, 128 x 64 at k = 128), going down the block.  The strip's U_r rows stay in LDS for
+// the whole run, so the back-projection reads only W rows from L2 instead of
+// every wave refetching U_r per tile.  Per workgroup:
+//   waves NS.. (MFMA role): corr(s) = W[rows of tile s, :] U_r[strip, :]^T,
 //     32 rows x 64 columns per wave (two 16-row halves sharing each B
 //     operand read from LDS), A operands from L2 with chunks of lookahead;
-//   waves 0..7 (streaming role, 16 rows x 64 columns each): tile s's loads
+//   waves 0..NS-1 (streaming role, 16 rows x 64 columns each): tile s's loads
 //     were issued during tile s-1; once corr(s) is published they run the
 //     Phase-2 tail, store, and issue tile s+1's loads.
 // The matrix cores and the Phase-2 arithmetic share each SIMD's issue, so the
@@ -1351,9 +1350,24 @@ __global__ __launch_bounds__(512) void k_apply_pipe(const scao_task* __restrict_
 // that a lane's four B rows (columns 4j + t of its 64-column group) are 16
 // rows apart, and the row pitch is 16 bytes past a multiple of 128: a 16-lane
 // read phase touches 16 distinct bank groups.
-constexpr int STRIP_LDS = 138240;   // bytes: U_r (fp32 or three bf16 planes) + buffers
 __host__ __device__ constexpr int strip_pitch(int k) { return k + 4 + ((32 - k % 32) % 32); }
 __host__ __device__ constexpr int strip_pitch_bf(int k) { return k + 8 + ((64 - k % 64) % 64); }
+// Tile shape per rank: SW columns x TR rows (8192 elements), NS = 8
+// streaming waves (16 x 64 elements each) and NM = 4 MFMA waves (32 x 64
+// each), about 135 KB of LDS: one workgroup per CU.  SW = 64 at k = 256 (what
+// LDS holds of U_r), 128 at k = 128: each W row a tile reads then serves 128
+// columns.  (64 x 64 tiles at k = 128, two workgroups per CU, measured 10%
+// slower: twice the W bytes per element.)
+template <int K> struct strip_shape {
+  static constexpr int SW = K == 256 ? 64 : 128, TR = 8192 / SW;
+  static constexpr int NS = TR * SW / 1024, NM = NS / 2, NT = 64 * (NS + NM);
+  // LDS: U_r as three bf16 planes and one correction buffer, or (GF32) as
+  // fp32 and two buffers
+  static constexpr int lds_bytes(bool bf) {
+    return bf ? 3 * SW * strip_pitch_bf(K) * 2 + TR * (SW + 4) * 4
+              : SW * strip_pitch(K) * 4 + 2 * TR * (SW + 4) * 4;
+  }
+};
 __device__ __forceinline__ int strip_row(int r) { return 64 * (r / 64) + 16 * (r % 4) + (r % 64) / 4; }
 
 // fp32: corr for rows wa (and wb, 16 rows on) against the LDS strip (lane
@@ -1492,20 +1506,22 @@ __device__ __forceinline__ void strip_corr_bf(strip_a (&A)[PD], const uint16_t* 
   }
 }
 
-template <bool GF32, bool LARS, int SW>
-__global__ __launch_bounds__(768) void k_apply_strip(const scao_task* __restrict__ tasks,
+template <bool GF32, bool LARS, int K>
+__global__ __launch_bounds__(strip_shape<K>::NT) void k_apply_strip(const scao_task* __restrict__ tasks,
                                                      const scao_leaf_desc* __restrict__ leaves,
                                                      const scao_param_desc* __restrict__ params,
                                                      const scao_param_stat* __restrict__ stat,
                                                      double* slots) {
   constexpr bool BF = !GF32;      // bf16 products, one correction buffer
-  constexpr int TR = 8192 / SW;   // rows of a tile
+  using SH = strip_shape<K>;
+  constexpr int SW = SH::SW, TR = SH::TR, NS = SH::NS, NM = SH::NM;
   constexpr int CB = SW + 4;      // LDS pitch of a correction row
   constexpr int NBUF = BF ? 1 : 2;
   constexpr int CBYTES = NBUF * TR * CB * 4;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[STRIP_LDS];
-  __shared__ double part[2][8];
-  float(*cbuf)[TR][CB] = (float(*)[TR][CB])(lds + STRIP_LDS - CBYTES);
+  constexpr int LDSB = SH::lds_bytes(BF);
+  __shared__ __attribute__((aligned(16))) unsigned char lds[LDSB];
+  __shared__ double part[2][NS];
+  float(*cbuf)[TR][CB] = (float(*)[TR][CB])(lds + LDSB - CBYTES);
   const int wv = threadIdx.x / 64, l = threadIdx.x % 64;
   const int kk = l / 16;
   const scao_task tk = tasks[blockIdx.x];
@@ -1515,7 +1531,7 @@ __global__ __launch_bounds__(768) void k_apply_strip(const scao_task* __restrict
   int nt = (mw - tk.a) / TR;
   nt = nt < SCAO_APPLY_GROUP ? nt : SCAO_APPLY_GROUP;
   if (nt <= 0) return;   // uniform over the workgroup
-  if (k != (SW == 64 ? 256 : 128) || (BF && !L.Wb)) {
+  if (k != K || (BF && !L.Wb)) {
     // outside the kernel's contract (the engine never sends this): make the
     // run's norms NaN rather than write anything
     if (threadIdx.x < nt && tk.slot >= 0)
@@ -1523,10 +1539,10 @@ __global__ __launch_bounds__(768) void k_apply_strip(const scao_task* __restrict
     return;
   }
 
-  if (wv >= 8) {
+  if (wv >= NS) {
     // ---- MFMA role ----
     constexpr int RP = TR / 32;   // 32-row groups of a tile
-    const int mwv = wv - 8, rp = mwv % RP, cg = mwv / RP;
+    const int mwv = wv - NS, rp = mwv % RP, cg = mwv / RP;
     const int q4 = k / 4;
     auto put = [&](int buf, v4f (&acc)[2][4]) {
 #pragma unroll
@@ -1540,7 +1556,7 @@ __global__ __launch_bounds__(768) void k_apply_strip(const scao_task* __restrict
       // barriers: A, X_0, then (Y_{s-1}, X_s) for s = 1..nt
       uint16_t* urb = (uint16_t*)lds;
       const int plane = SW * pk;
-      for (int q = threadIdx.x - 512; q < SW * q4; q += 256) {
+      for (int q = threadIdx.x - 64 * NS; q < SW * q4; q += 64 * NM) {
         const int r = q / q4, c = q - r * q4;
         const v4f x = gld4(L.Ur + (int64_t)(tk.b + r) * k + 4 * c);
         v4bf h, m, lo;
@@ -1559,7 +1575,7 @@ __global__ __launch_bounds__(768) void k_apply_strip(const scao_task* __restrict
       }
       const int64_t mk = (int64_t)L.m * k;
       const uint16_t* ub = urb + (64 * cg + l % 16) * pk + 8 * kk;
-      constexpr int PD = SW == 64 ? 2 : 3;   // chunks of A lookahead (registers)
+      constexpr int PD = K == 256 ? 2 : 3;   // chunks of A lookahead (registers)
       constexpr int PK256 = strip_pitch_bf(256), PK128 = strip_pitch_bf(128);
       strip_a A[PD];
       const uint16_t* wp[2][3];
@@ -1578,7 +1594,7 @@ __global__ __launch_bounds__(768) void k_apply_strip(const scao_task* __restrict
           if (d < k / 32) strip_load_a(A[d], wp, d);
       };
       auto corr = [&](int s, v4f (&acc)[2][4]) {
-        if constexpr (SW == 64)
+        if constexpr (K == 256)
           strip_corr_bf<256, PK256, SW * PK256, PD>(A, wp, ub, plane, pk, k, acc);
         else
           strip_corr_bf<128, PK128, SW * PK128, PD>(A, wp, ub, plane, pk, k, acc);
@@ -1604,7 +1620,7 @@ __global__ __launch_bounds__(768) void k_apply_strip(const scao_task* __restrict
     } else {
       // barriers: A, then X_s for s = 0..nt
       float* ur = (float*)lds;
-      for (int q = threadIdx.x - 512; q < SW * q4; q += 256) {
+      for (int q = threadIdx.x - 64 * NS; q < SW * q4; q += 64 * NM) {
         const int r = q / q4, c = q - r * q4;
         *(v4f*)&ur[strip_row(r) * pk + 4 * c] = gld4(L.Ur + (int64_t)(tk.b + r) * k + 4 * c);
       }
@@ -1615,7 +1631,7 @@ __global__ __launch_bounds__(768) void k_apply_strip(const scao_task* __restrict
         const float* __restrict__ wa =
             L.W + (int64_t)(tk.a + s * TR + 32 * rp + l % 16) * k + 4 * kk;
         const float* __restrict__ wb = wa + (int64_t)16 * k;
-        if constexpr (SW == 64)
+        if constexpr (K == 256)
           strip_corr<16, 6>(wa, wb, ub, pk, k, acc);
         else
           strip_corr<8, 6>(wa, wb, ub, pk, k, acc);
@@ -1656,7 +1672,9 @@ __global__ __launch_bounds__(768) void k_apply_strip(const scao_task* __restrict
   auto put_slot = [&](int s) {
     if (tk.slot < 0) return;
     const double* q = part[s & 1];
-    const double u2 = ((((((q[0] + q[1]) + q[2]) + q[3]) + q[4]) + q[5]) + q[6]) + q[7];
+    double u2 = q[0];
+#pragma unroll
+    for (int i = 1; i < NS; ++i) u2 += q[i];   // fixed order
     const int64_t slot = tk.slot + s;
     slots[slot * SCAO_SLOT_WIDTH + 0] = 0.0;
     slots[slot * SCAO_SLOT_WIDTH + 1] = 0.0;
@@ -1878,9 +1896,10 @@ extern "C" int scao_kron_apply(const scao_task* tasks, int ntasks, const scao_le
                  "scao_kron_apply: bad variant %d", variant);
   hipStream_t s = (hipStream_t)stream;
   if (variant & 16) {
-    const dim3 gs(ntasks), bs(768);
-#define SCAO_APPLY_STRIP(GF, LA, SWD) \
-  hipLaunchKernelGGL((k_apply_strip<GF, LA, SWD>), gs, bs, 0, s, tasks, leaves, params, stat, slots)
+    const dim3 gs(ntasks);
+#define SCAO_APPLY_STRIP(GF, LA, KR)                                                          \
+  hipLaunchKernelGGL((k_apply_strip<GF, LA, KR>), gs, dim3(strip_shape<KR>::NT), 0, s, tasks, \
+                     leaves, params, stat, slots)
     if (variant & 32) {
       switch (variant & 3) {
         case 0: SCAO_APPLY_STRIP(false, false, 128); break;
@@ -1890,10 +1909,10 @@ extern "C" int scao_kron_apply(const scao_task* tasks, int ntasks, const scao_le
       }
     } else {
       switch (variant & 3) {
-        case 0: SCAO_APPLY_STRIP(false, false, 64); break;
-        case 1: SCAO_APPLY_STRIP(true, false, 64); break;
-        case 2: SCAO_APPLY_STRIP(false, true, 64); break;
-        default: SCAO_APPLY_STRIP(true, true, 64); break;
+        case 0: SCAO_APPLY_STRIP(false, false, 256); break;
+        case 1: SCAO_APPLY_STRIP(true, false, 256); break;
+        case 2: SCAO_APPLY_STRIP(false, true, 256); break;
+        default: SCAO_APPLY_STRIP(true, true, 256); break;
       }
     }
 #undef SCAO_APPLY_STRIP

@@ -337,12 +337,11 @@ def _param_tasks(it: PItem):
             m, n, T = leaf.m, leaf.n, L.APPLY_TILE
             if ok and k in STRIP_RANKS:
                 # runs of strip tiles over the interior they tile exactly
-                sw = 64 if k == 256 else 128
-                tr = 8192 // sw
+                sw, tr = (64, 128) if k == 256 else (128, 64)   # the kernel's strip_shape
                 mw, nw = m - m % tr, n - n % sw
                 if not (mw and nw):
                     mw = nw = 0
-                wide = var | 4 | 16 | (32 if sw == 128 else 0)
+                wide = var | 4 | 16 | (32 if k == 128 else 0)
                 for i0, j0 in _strip_runs(mw, nw, tr, sw):
                     add(f"apply{wide}", (li, i0, j0, slot))
                     slot += min(L.APPLY_GROUP, (mw - i0) // tr)

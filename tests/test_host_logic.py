@@ -382,8 +382,7 @@ def test_strip_apply_tasks(k):
     (workgroup b takes queue b % XCDS)."""
     items = _phase2_items([(1024, 2048)] * 8 + [(640, 1536)], k)
     arrays, _, nslot, leaves = E._build_structure(items)
-    sw = 64 if k == 256 else 128
-    tr = 8192 // sw
+    sw, tr = (64, 128) if k == 256 else (128, 64)
     var = 2 | 4 | 16 | (32 if k == 128 else 0)
     runs = arrays[f"apply{var}"]
     assert all(len(arrays[f"apply{v}"]) == 0 for v in (14, 6) if v != var)
