@@ -1371,70 +1371,47 @@ template <int K> struct strip_shape {
 __device__ __forceinline__ int strip_row(int r) { return 64 * (r / 64) + 16 * (r % 4) + (r % 64) / 4; }
 
 // fp32: corr for rows wa (and wb, 16 rows on) against the LDS strip (lane
-// base ub), k = 16 NC (NC = 0: any multiple of 16).
+// base ub, row pitch pk), k = 16 NC.
 template <int NC, int PD>
 __device__ __forceinline__ void strip_corr(const float* __restrict__ wa,
                                            const float* __restrict__ wb, const float* ub, int pk,
-                                           int k, v4f (&acc)[2][4]) {
+                                           v4f (&acc)[2][4]) {
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[h][t] = v4f{0.f, 0.f, 0.f, 0.f};
-  if constexpr (NC > 0) {
-    v4f A[PD][2], B[2][4];
+  v4f A[PD][2], B[2][4];
 #pragma unroll
-    for (int d = 0; d < PD && d < NC; ++d) {
-      A[d][0] = gld4(wa + 16 * d);
-      A[d][1] = gld4(wb + 16 * d);
+  for (int d = 0; d < PD && d < NC; ++d) {
+    A[d][0] = gld4(wa + 16 * d);
+    A[d][1] = gld4(wb + 16 * d);
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) B[0][t] = *(const v4f*)(ub + 16 * t * pk);
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int d = c % PD, cur = c & 1;
+    if (c + 1 < NC) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) B[cur ^ 1][t] = *(const v4f*)(ub + 16 * t * pk + 16 * (c + 1));
     }
+    // chunk c+1's LDS reads go out before chunk c's products (a second
+    // register set), so their latency hides behind 32 MFMAs
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) B[0][t] = *(const v4f*)(ub + 16 * t * pk);
+    for (int s4 = 0; s4 < 4; ++s4)
 #pragma unroll
-    for (int c = 0; c < NC; ++c) {
-      const int d = c % PD, cur = c & 1;
-      if (c + 1 < NC) {
-#pragma unroll
-        for (int t = 0; t < 4; ++t) B[cur ^ 1][t] = *(const v4f*)(ub + 16 * t * pk + 16 * (c + 1));
+      for (int t = 0; t < 4; ++t) {
+        acc[0][t] = mfma16(A[d][0][s4], B[cur][t][s4], acc[0][t]);
+        acc[1][t] = mfma16(A[d][1][s4], B[cur][t][s4], acc[1][t]);
       }
-      // chunk c+1's LDS reads go out before chunk c's products (a second
-      // register set), so their latency hides behind 32 MFMAs
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          acc[0][t] = mfma16(A[d][0][s4], B[cur][t][s4], acc[0][t]);
-          acc[1][t] = mfma16(A[d][1][s4], B[cur][t][s4], acc[1][t]);
-        }
-      if (c + PD < NC) {
-        A[d][0] = gld4(wa + 16 * (c + PD));
-        A[d][1] = gld4(wb + 16 * (c + PD));
-      }
-      // keep chunk c+PD's loads here: the scheduler would otherwise sink
-      // them next to their use and expose an L2 round trip per chunk
-      __builtin_amdgcn_sched_barrier(0);
+    if (c + PD < NC) {
+      A[d][0] = gld4(wa + 16 * (c + PD));
+      A[d][1] = gld4(wb + 16 * (c + PD));
     }
-  } else {
-    v4f a0 = gld4(wa), a1 = gld4(wb);
-    for (int c = 0; c < k; c += 16) {
-      v4f n0 = a0, n1 = a1;
-      if (c + 16 < k) {
-        n0 = gld4(wa + c + 16);
-        n1 = gld4(wb + c + 16);
-      }
-      v4f b[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) b[t] = *(const v4f*)(ub + 16 * t * pk + c);
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-          acc[0][t] = mfma16(a0[s4], b[t][s4], acc[0][t]);
-          acc[1][t] = mfma16(a1[s4], b[t][s4], acc[1][t]);
-        }
-      a0 = n0;
-      a1 = n1;
-    }
+    // keep chunk c+PD's loads here: the scheduler would otherwise sink
+    // them next to their use and expose an L2 round trip per chunk
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -1464,23 +1441,20 @@ __device__ __forceinline__ bf3 strip_load_b(const uint16_t* ub, int plane, int p
 }
 
 // bf16: corr for the rows of wp (two 16-row halves) against the LDS planes
-// (lane base ub, plane stride `plane`, row pitch pk), with the first PD
-// chunks of A already in A[0..PD-1].  K > 0: k, pk and plane are the
-// compile-time K, PKC, PLC and the chunk loop is unrolled; K = 0: the
-// runtime values, chunks in rotations of PD.
+// (lane base ub, plane stride PLC, row pitch PKC), k = K, with the first PD
+// chunks of A already in A[0..PD-1]; the chunk loop is unrolled in
+// rotations of PD (every address offset a constant).
 template <int K, int PKC, int PLC, int PD>
 __device__ __forceinline__ void strip_corr_bf(strip_a (&A)[PD], const uint16_t* const (&wp)[2][3],
-                                              const uint16_t* ub, int plane_rt, int pk_rt,
-                                              int k_rt, v4f (&acc)[2][4]) {
-  const int pk = K ? PKC : pk_rt, plane = K ? PLC : plane_rt;
-  const int nc = (K ? K : k_rt) / 32;
+                                              const uint16_t* ub, v4f (&acc)[2][4]) {
+  constexpr int pk = PKC, plane = PLC, nc = K / 32;
 #pragma unroll
   for (int h = 0; h < 2; ++h)
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[h][t] = v4f{0.f, 0.f, 0.f, 0.f};
   bf3 B[2];
   B[0] = strip_load_b(ub, plane, pk, 0, 0);
-#pragma unroll(K > 0 ? 8 : 1)
+#pragma unroll
   for (int c0 = 0; c0 < nc; c0 += PD) {
 #pragma unroll
     for (int d = 0; d < PD; ++d) {
@@ -1526,7 +1500,8 @@ __global__ __launch_bounds__(strip_shape<K>::NT) void k_apply_strip(const scao_t
   const int kk = l / 16;
   const scao_task tk = tasks[blockIdx.x];
   const scao_leaf_desc& L = leaves[tk.idx];
-  const int k = L.k, pk = BF ? strip_pitch_bf(k) : strip_pitch(k);
+  const int k = L.k;             // == K past the guard below
+  constexpr int pk = BF ? strip_pitch_bf(K) : strip_pitch(K);
   const int mw = L.m - L.m % TR;
   int nt = (mw - tk.a) / TR;
   nt = nt < SCAO_APPLY_GROUP ? nt : SCAO_APPLY_GROUP;
@@ -1543,7 +1518,7 @@ __global__ __launch_bounds__(strip_shape<K>::NT) void k_apply_strip(const scao_t
     // ---- MFMA role ----
     constexpr int RP = TR / 32;   // 32-row groups of a tile
     const int mwv = wv - NS, rp = mwv % RP, cg = mwv / RP;
-    const int q4 = k / 4;
+    constexpr int q4 = K / 4;
     auto put = [&](int buf, v4f (&acc)[2][4]) {
 #pragma unroll
       for (int h = 0; h < 2; ++h)
@@ -1555,10 +1530,10 @@ __global__ __launch_bounds__(strip_shape<K>::NT) void k_apply_strip(const scao_t
     if constexpr (BF) {
       // barriers: A, X_0, then (Y_{s-1}, X_s) for s = 1..nt
       uint16_t* urb = (uint16_t*)lds;
-      const int plane = SW * pk;
+      constexpr int plane = SW * pk;
       for (int q = threadIdx.x - 64 * NS; q < SW * q4; q += 64 * NM) {
         const int r = q / q4, c = q - r * q4;
-        const v4f x = gld4(L.Ur + (int64_t)(tk.b + r) * k + 4 * c);
+        const v4f x = gld4(L.Ur + (int64_t)(tk.b + r) * K + 4 * c);
         v4bf h, m, lo;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -1573,10 +1548,9 @@ __global__ __launch_bounds__(strip_shape<K>::NT) void k_apply_strip(const scao_t
         *(v2u*)(d + plane) = __builtin_bit_cast(v2u, m);
         *(v2u*)(d + 2 * plane) = __builtin_bit_cast(v2u, lo);
       }
-      const int64_t mk = (int64_t)L.m * k;
+      const int64_t mk = (int64_t)L.m * K;
       const uint16_t* ub = urb + (64 * cg + l % 16) * pk + 8 * kk;
       constexpr int PD = K == 256 ? 2 : 3;   // chunks of A lookahead (registers)
-      constexpr int PK256 = strip_pitch_bf(256), PK128 = strip_pitch_bf(128);
       strip_a A[PD];
       const uint16_t* wp[2][3];
       auto rows = [&](int s) {
@@ -1584,20 +1558,16 @@ __global__ __launch_bounds__(strip_shape<K>::NT) void k_apply_strip(const scao_t
         for (int h = 0; h < 2; ++h)
 #pragma unroll
           for (int q = 0; q < 3; ++q)
-            wp[h][q] = L.Wb + q * mk + (int64_t)(tk.a + s * TR + 32 * rp + 16 * h + l % 16) * k +
+            wp[h][q] = L.Wb + q * mk + (int64_t)(tk.a + s * TR + 32 * rp + 16 * h + l % 16) * K +
                        8 * kk;
       };
       auto first = [&](int s) {
         rows(s);
 #pragma unroll
-        for (int d = 0; d < PD; ++d)
-          if (d < k / 32) strip_load_a(A[d], wp, d);
+        for (int d = 0; d < PD; ++d) strip_load_a(A[d], wp, d);
       };
       auto corr = [&](int s, v4f (&acc)[2][4]) {
-        if constexpr (K == 256)
-          strip_corr_bf<256, PK256, SW * PK256, PD>(A, wp, ub, plane, pk, k, acc);
-        else
-          strip_corr_bf<128, PK128, SW * PK128, PD>(A, wp, ub, plane, pk, k, acc);
+        strip_corr_bf<K, pk, plane, PD>(A, wp, ub, acc);
       };
       first(0);
       __syncthreads();                                        // A: U_r planes in LDS
@@ -1622,19 +1592,16 @@ __global__ __launch_bounds__(strip_shape<K>::NT) void k_apply_strip(const scao_t
       float* ur = (float*)lds;
       for (int q = threadIdx.x - 64 * NS; q < SW * q4; q += 64 * NM) {
         const int r = q / q4, c = q - r * q4;
-        *(v4f*)&ur[strip_row(r) * pk + 4 * c] = gld4(L.Ur + (int64_t)(tk.b + r) * k + 4 * c);
+        *(v4f*)&ur[strip_row(r) * pk + 4 * c] = gld4(L.Ur + (int64_t)(tk.b + r) * K + 4 * c);
       }
       __syncthreads();                                        // A: U_r strip in LDS
       const float* ub = &ur[(64 * cg + l % 16) * pk + 4 * kk];
       for (int s = 0; s < nt; ++s) {
         v4f acc[2][4];
         const float* __restrict__ wa =
-            L.W + (int64_t)(tk.a + s * TR + 32 * rp + l % 16) * k + 4 * kk;
-        const float* __restrict__ wb = wa + (int64_t)16 * k;
-        if constexpr (K == 256)
-          strip_corr<16, 6>(wa, wb, ub, pk, k, acc);
-        else
-          strip_corr<8, 6>(wa, wb, ub, pk, k, acc);
+            L.W + (int64_t)(tk.a + s * TR + 32 * rp + l % 16) * K + 4 * kk;
+        const float* __restrict__ wb = wa + (int64_t)16 * K;
+        strip_corr<K / 16, 6>(wa, wb, ub, pk, acc);
         put(s & 1, acc);
         __syncthreads();                                      // X_s: corr(s) published
       }
