@@ -228,22 +228,8 @@ __device__ __forceinline__ void chunk_store_x6(__bf16* P, const v4f (&x)[4]) {
     const int k = SIDE == 0 ? (tid % 8) * 4 : 4 * (tid / 128 + 2 * h);
     uint32_t pk[3][2];
 #pragma unroll
-    for (int u = 0; u < 4; u += 2) {
-      uint32_t v[2][3];
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-        const float f = x[h][u + e];
-        const __bf16 b0 = (__bf16)f;
-        const float r = f - (float)b0;
-        const __bf16 b1 = (__bf16)r;
-        const __bf16 b2 = (__bf16)(r - (float)b1);
-        v[e][0] = __builtin_bit_cast(uint16_t, b0);
-        v[e][1] = __builtin_bit_cast(uint16_t, b1);
-        v[e][2] = __builtin_bit_cast(uint16_t, b2);
-      }
-#pragma unroll
-      for (int pp = 0; pp < 3; ++pp) pk[pp][u / 2] = v[0][pp] | (v[1][pp] << 16);
-    }
+    for (int u = 0; u < 4; u += 2)
+      split3_pk(x[h][u], x[h][u + 1], pk[0][u / 2], pk[1][u / 2], pk[2][u / 2]);
 #pragma unroll
     for (int pp = 0; pp < 3; ++pp)
       *(v2u*)&P[pp * XPL + row * XCP + k] = v2u{pk[pp][0], pk[pp][1]};

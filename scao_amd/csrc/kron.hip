@@ -232,10 +232,18 @@ __device__ __forceinline__ void project_tile_x6(const scao_leaf_desc& L, const s
   const int m = L.m, n = L.n, k = L.k;
   const int64_t ld = L.ld;
   const bool do_norms = (c0 == 0) && slot >= 0;
-  const bool decay = P.flags & SCAO_PF_DECAY;
+  // x * 1.0f == x bit for bit, so no per-element select on the decay flag
+  const float dec = (P.flags & SCAO_PF_DECAY) ? P.decay : 1.0f;
   const int gcol = j0 + CW * w + NJ * jj;
   // U_l loader: rows 4*ua .. 4*ua+3 of the chunk, columns ub*UW .. +UW-1
   const int ua = tid / UG, ub = tid % UG;
+  // Every load address is a row origin shared by the block (scalar
+  // registers) plus a 32-bit lane offset fixed for the whole tile: lane
+  // (jj, g) reads rows 8g.. of the chunk at column gcol, the U_l loader rows
+  // 4ua.. at column c0 + ub*UW.
+  const uint32_t g_lane = (uint32_t)((8 * g * ld + (gcol - j0)) * (int64_t)sizeof(float));
+  const uint32_t u_lane = (uint32_t)((4 * ua * (int64_t)k + ub * UW) * (int64_t)sizeof(float));
+  const int64_t ldb = ld * (int64_t)sizeof(float), kb = k * (int64_t)sizeof(float);
 
   v4f acc[NQ][NJ];
 #pragma unroll
@@ -247,17 +255,20 @@ __device__ __forceinline__ void project_tile_x6(const scao_leaf_desc& L, const s
   vj rg[8], rp[8];
   float ru[4][UW];
   auto load_g = [&](int i0) {
+    const int64_t o = L.off + (int64_t)i0 * ld + j0;
+    const char* gb = (const char*)((const float*)P.graw + o);
+    const char* pb = (const char*)((const float*)P.p + o);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int64_t o = L.off + (int64_t)(i0 + 8 * g + e) * ld + gcol;
-      rg[e] = __builtin_nontemporal_load((const gvj*)((const float*)P.graw + o));
-      if (DO_P) rp[e] = __builtin_nontemporal_load((const gvj*)((const float*)P.p + o));
+      rg[e] = __builtin_nontemporal_load((const gvj*)(gb + e * ldb + g_lane));
+      if (DO_P) rp[e] = __builtin_nontemporal_load((const gvj*)(pb + e * ldb + g_lane));
     }
   };
   auto load_u = [&](int i0) {
+    const char* ubase = (const char*)(L.Ul + (int64_t)i0 * k + c0);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const float* src = L.Ul + (int64_t)(i0 + 4 * ua + r) * k + c0 + ub * UW;
+      const float* src = (const float*)(ubase + r * kb + u_lane);
       if constexpr (UW == 4) {
         const v4f x = gld4(src);
 #pragma unroll
@@ -280,21 +291,11 @@ __device__ __forceinline__ void project_tile_x6(const scao_leaf_desc& L, const s
       v2u pl[3];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        uint32_t lo[3], hi[3];
-#pragma unroll
-        for (int rr = 0; rr < 2; ++rr) {
-          const float x = ru[2 * h + rr][c];
-          const __bf16 b0 = (__bf16)x;
-          const float r = x - (float)b0;
-          const __bf16 b1 = (__bf16)r;
-          const __bf16 b2 = (__bf16)(r - (float)b1);
-          const uint32_t v[3] = {__builtin_bit_cast(uint16_t, b0), __builtin_bit_cast(uint16_t, b1),
-                                 __builtin_bit_cast(uint16_t, b2)};
-#pragma unroll
-          for (int pp = 0; pp < 3; ++pp) (rr ? hi : lo)[pp] = v[pp];
-        }
-#pragma unroll
-        for (int pp = 0; pp < 3; ++pp) pl[pp][h] = lo[pp] | (hi[pp] << 16);
+        uint32_t a, b, cc;
+        split3_pk(ru[2 * h][c], ru[2 * h + 1][c], a, b, cc);   // rows 2h (low), 2h+1
+        pl[0][h] = a;
+        pl[1][h] = b;
+        pl[2][h] = cc;
       }
       const int col = ub * UW + c;
 #pragma unroll
@@ -332,7 +333,7 @@ __device__ __forceinline__ void project_tile_x6(const scao_leaf_desc& L, const s
         for (int t = 0; t < NJ; ++t) {
           a = fmaf(rg[e][t], rg[e][t], a);
           if (DO_P) {
-            const float x = decay ? rp[e][t] * P.decay : rp[e][t];
+            const float x = rp[e][t] * dec;
             b = fmaf(x, x, b);
           }
         }
@@ -341,6 +342,9 @@ __device__ __forceinline__ void project_tile_x6(const scao_leaf_desc& L, const s
     }
     if constexpr (CR == 256) {
       write_u(cur ^ 1);                   // chunk i+1's planes, read after the barrier below
+      // the loads go out after the split (measured faster than letting the
+      // scheduler hoist them above it)
+      __builtin_amdgcn_sched_barrier(0);
       load_g(i0 + PR < last ? i0 + PR : last);   // in flight during the MFMAs below
       load_u(i0 + 2 * PR < last ? i0 + 2 * PR : last);
       __builtin_amdgcn_sched_barrier(0);
@@ -567,20 +571,23 @@ __device__ __forceinline__ void split3(float x, __bf16& h, __bf16& m, __bf16& l)
   m = (__bf16)r;
   l = (__bf16)(r - (float)m);
 }
-typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ void store_split4(uint16_t* wb, int64_t mk, int64_t o, const v4f& x) {
-  v4bf h, m, l;
+// four consecutive elements' planes as two packed words each
+__device__ __forceinline__ void split4_pk(const v4f& x, v2u& h, v2u& m, v2u& l) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    __bf16 a, b, c;
-    split3(x[e], a, b, c);
-    h[e] = a;
-    m[e] = b;
-    l[e] = c;
+  for (int p = 0; p < 2; ++p) {
+    uint32_t a, b, c;
+    split3_pk(x[2 * p], x[2 * p + 1], a, b, c);
+    h[p] = a;
+    m[p] = b;
+    l[p] = c;
   }
-  *(gv2u*)(wb + o) = __builtin_bit_cast(v2u, h);
-  *(gv2u*)(wb + mk + o) = __builtin_bit_cast(v2u, m);
-  *(gv2u*)(wb + 2 * mk + o) = __builtin_bit_cast(v2u, l);
+}
+__device__ __forceinline__ void store_split4(uint16_t* wb, int64_t mk, int64_t o, const v4f& x) {
+  v2u h, m, l;
+  split4_pk(x, h, m, l);
+  *(gv2u*)(wb + o) = h;
+  *(gv2u*)(wb + mk + o) = m;
+  *(gv2u*)(wb + 2 * mk + o) = l;
 }
 __device__ __forceinline__ void store_split1(uint16_t* wb, int64_t mk, int64_t o, float x) {
   __bf16 h, m, l;
@@ -1534,19 +1541,12 @@ __global__ __launch_bounds__(strip_shape<K>::NT) void k_apply_strip(const scao_t
       for (int q = threadIdx.x - 64 * NS; q < SW * q4; q += 64 * NM) {
         const int r = q / q4, c = q - r * q4;
         const v4f x = gld4(L.Ur + (int64_t)(tk.b + r) * K + 4 * c);
-        v4bf h, m, lo;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          __bf16 a, b, cc;
-          split3(x[e], a, b, cc);
-          h[e] = a;
-          m[e] = b;
-          lo[e] = cc;
-        }
+        v2u h, m, lo;
+        split4_pk(x, h, m, lo);
         uint16_t* d = urb + strip_row(r) * pk + 4 * c;
-        *(v2u*)d = __builtin_bit_cast(v2u, h);
-        *(v2u*)(d + plane) = __builtin_bit_cast(v2u, m);
-        *(v2u*)(d + 2 * plane) = __builtin_bit_cast(v2u, lo);
+        *(v2u*)d = h;
+        *(v2u*)(d + plane) = m;
+        *(v2u*)(d + 2 * plane) = lo;
       }
       const int64_t mk = (int64_t)L.m * K;
       const uint16_t* ub = urb + (64 * cg + l % 16) * pk + 8 * kk;

@@ -41,18 +41,36 @@ __device__ __forceinline__ v4f mfma16bf(v8bf a, v8bf b, v4f c) {
 struct bf3 {
   v8bf h, m, l;
 };
+typedef float v2f_t __attribute__((ext_vector_type(2)));
+typedef __bf16 v2bf_t __attribute__((ext_vector_type(2)));
+typedef unsigned int v4u_t __attribute__((ext_vector_type(4)));
+// a and b rounded to bf16 (nearest even) by one v_cvt_pk_bf16_f32, a in the
+// low half of the word
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((v2f_t){a, b}, v2bf_t));
+}
+// The three-way split of a pair, packed as the MFMA operands and LDS planes
+// hold it: word h holds a's and b's leading parts, m and l the remainders.
+// Per element it is (__bf16)x, then x - h, and so on: the same bits as one
+// scalar conversion at a time, at three conversions per two elements.
+__device__ __forceinline__ void split3_pk(float a, float b, uint32_t& h, uint32_t& m,
+                                          uint32_t& l) {
+  h = pk_bf16(a, b);
+  const float ra = a - __uint_as_float(h << 16), rb = b - __uint_as_float(h & 0xffff0000u);
+  m = pk_bf16(ra, rb);
+  l = pk_bf16(ra - __uint_as_float(m << 16), rb - __uint_as_float(m & 0xffff0000u));
+}
 __device__ __forceinline__ bf3 split_bf3(const float (&x)[8]) {
-  bf3 s;
+  v4u_t h, m, l;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const __bf16 h = (__bf16)x[e];
-    const float r = x[e] - (float)h;
-    const __bf16 m = (__bf16)r;
-    s.h[e] = h;
-    s.m[e] = m;
-    s.l[e] = (__bf16)(r - (float)m);
+  for (int p = 0; p < 4; ++p) {
+    uint32_t a, b, c;
+    split3_pk(x[2 * p], x[2 * p + 1], a, b, c);
+    h[p] = a;
+    m[p] = b;
+    l[p] = c;
   }
-  return s;
+  return bf3{__builtin_bit_cast(v8bf, h), __builtin_bit_cast(v8bf, m), __builtin_bit_cast(v8bf, l)};
 }
 // c + A B for fp32 A and B given as bf3 splits: six bf16 MFMAs (small terms
 // first).

@@ -296,8 +296,12 @@ def _param_tasks(it: PItem):
             m, n = leaf.m, leaf.n
             k = _leaf_k(leaf)
             vec = _leaf_vec(it, leaf, r0, c0l)
+            # the bf16-split tiles address a lane's rows with a 32-bit byte
+            # offset: 24 row strides + a strip, below 2^32 for rows under 2^25
+            short_rows = _cols(it.p) < (1 << 25)
             for j0 in range(0, n, L.PROJ_COLS):
-                whole = vec and it.fp32 and j0 + L.PROJ_COLS <= n and m % 32 == 0
+                whole = (vec and it.fp32 and j0 + L.PROJ_COLS <= n and m % 32 == 0
+                         and short_rows)
                 # 128 or 256 rows of T per task where k allows (variant bits 4, 8)
                 cr = 64
                 if whole and k % 128 == 0:
