@@ -894,16 +894,30 @@ struct Sb2stLds {
 constexpr int SB_D0 = NB * (NB + 1);
 constexpr int SB_JUNK = 2 * NB * (NB + 1) + 3 * NB;
 
+// Butterfly sums inside a 16-lane row by DPP moves (VALU, no LDS round
+// trip).  quad_perm [1,0,3,2] and [2,3,0,1] read lanes l^1 and l^2; once the
+// four lanes of a quad hold equal values, the half-row mirror pairs quad j
+// with quad j^1 and the row mirror half h with h^1, so the sums are the
+// xor-butterfly's operand for operand.
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double x) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, x);
+  const uint32_t lo = __builtin_amdgcn_update_dpp(0u, (uint32_t)b, CTRL, 0xf, 0xf, false);
+  const uint32_t hi = __builtin_amdgcn_update_dpp(0u, (uint32_t)(b >> 32), CTRL, 0xf, 0xf, false);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_QUAD0 = 0x00;
+constexpr int DPP_ROW_MIRROR = 0x140, DPP_HALF_MIRROR = 0x141;
 __device__ __forceinline__ double sum4(double x) {
-  x += __shfl_xor(x, 1);
-  x += __shfl_xor(x, 2);
+  x += dpp_d<DPP_XOR1>(x);
+  x += dpp_d<DPP_XOR2>(x);
   return x;
 }
+// sum over each 16-lane row, left in every lane of the row
 __device__ __forceinline__ double sum16(double x) {
-  x += __shfl_xor(x, 1);
-  x += __shfl_xor(x, 2);
-  x += __shfl_xor(x, 4);
-  x += __shfl_xor(x, 8);
+  x = sum4(x);
+  x += dpp_d<DPP_HALF_MIRROR>(x);
+  x += dpp_d<DPP_ROW_MIRROR>(x);
   return x;
 }
 // LDS traffic of one wavefront is ordered; this keeps the compiler from
@@ -1003,16 +1017,24 @@ __global__ __launch_bounds__(SB_W * 64) void k_sb2st(double* band, int n, double
         }
         wave_sync();
         // 1. E <- E (I - ptau pv pv^T)
+        // Steps 1 and 3 read and write only the lane's own four elements
+        // (the sums go through DPP), so each keeps them in registers from its
+        // read to its write; step 4 does the same with D.
         if (ptau != 0.0) {
-          double t = 0.0;
-          if (r < LM)
-            for (int c = 4 * q; c < 4 * q + 4; ++c)
-              if (c < LNv) t = fma(S.E[r][c], S.pv[c], t);
+          double t = 0.0, e4[4], p4[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int c = 4 * q + j;
+            e4[j] = S.E[r][c];
+            p4[j] = S.pv[c];
+            if (r < LM && c < LNv) t = fma(e4[j], p4[j], t);
+          }
           t = sum4(t);
-          wave_sync();
-          if (r < LM)
-            for (int c = 4 * q; c < 4 * q + 4; ++c)
-              if (c < LNv) S.E[r][c] = fma(-ptau * t, S.pv[c], S.E[r][c]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int c = 4 * q + j;
+            if (r < LM && c < LNv) S.E[r][c] = fma(-ptau * t, p4[j], e4[j]);
+          }
           wave_sync();
         }
         // 2. reflector from E[:, 0] (length LM)
@@ -1034,32 +1056,47 @@ __global__ __launch_bounds__(SB_W * 64) void k_sb2st(double* band, int n, double
         wave_sync();
         if (tau != 0.0) {
           // 3. E[:, 1:] <- (I - tau v v^T) E[:, 1:]   (lane: column r, rows 4q..4q+3)
-          double w = 0.0;
-          if (r >= 1 && r < LNv)
-            for (int i = 4 * q; i < 4 * q + 4; ++i)
-              if (i < LM) w = fma(S.v[i], S.E[i][r], w);
+          double w = 0.0, e4[4], v4[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int i = 4 * q + j;
+            v4[j] = S.v[i];
+            e4[j] = S.E[i][r];
+            if (r >= 1 && r < LNv && i < LM) w = fma(v4[j], e4[j], w);
+          }
           w = sum4(w);
-          wave_sync();
-          if (r >= 1 && r < LNv)
-            for (int i = 4 * q; i < 4 * q + 4; ++i)
-              if (i < LM) S.E[i][r] = fma(-tau * S.v[i], w, S.E[i][r]);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int i = 4 * q + j;
+            if (r >= 1 && r < LNv && i < LM) S.E[i][r] = fma(-tau * v4[j], w, e4[j]);
+          }
           // 4. D <- H D H: y = tau D v; y -= (tau/2)(y^T v) v; D -= v y^T + y v^T
-          double y = 0.0;
-          if (r < LM)
-            for (int c = 4 * q; c < 4 * q + 4; ++c)
-              if (c < LM) y = fma(S.D[r][c], S.v[c], y);
+          double y = 0.0, d4[4], vc[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int c = 4 * q + j;
+            d4[j] = S.D[r][c];
+            vc[j] = S.v[c];
+            if (r < LM && c < LM) y = fma(d4[j], vc[j], y);
+          }
           y = tau * sum4(y);
+          // y^T v over the 16 rows: lane 4r holds row r's term; copied to its
+          // quad, summed over the 16-lane row, then across the four rows
           double a = (q == 0 && r < LM) ? y * S.v[r] : 0.0;
-          a += __shfl_xor(a, 4);
-          a += __shfl_xor(a, 8);
+          a = dpp_d<DPP_QUAD0>(a);
+          a += dpp_d<DPP_HALF_MIRROR>(a);
+          a += dpp_d<DPP_ROW_MIRROR>(a);
           a += __shfl_xor(a, 16);
           a += __shfl_xor(a, 32);
           a *= 0.5 * tau;
           if (q == 0 && r < LM) S.y[r] = fma(-a, S.v[r], y);
           wave_sync();
-          if (r < LM)
-            for (int c = 4 * q; c < 4 * q + 4; ++c)
-              if (c < LM) S.D[r][c] = S.D[r][c] - (S.v[r] * S.y[c] + S.y[r] * S.v[c]);
+          const double vr = S.v[r], yr = S.y[r];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int c = 4 * q + j;
+            if (r < LM && c < LM) S.D[r][c] = d4[j] - (vr * S.y[c] + yr * vc[j]);
+          }
           wave_sync();
         }
         // store the rows back, then publish the task
