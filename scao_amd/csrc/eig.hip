@@ -40,6 +40,76 @@ constexpr int NB = SCAO_EIG_BAND;    // 16
 constexpr int BW = SCAO_EIG_BANDW;   // 33: band row pitch (diagonals 0..2b)
 constexpr int OW = NB + 1;           // 17: pitch of the original band copy
 
+// ----------------------------------------------------- cross-lane sums ---
+// Butterfly levels (every lane adds lane l^o's value) without an LDS round
+// trip, for call sites where the whole wavefront is active.  A permlane swap
+// of x with itself returns two registers holding, in every lane, the lower
+// and the upper lane of its xor-32 (permlane32) or xor-16 (permlane16) pair
+// (lane layout checked on gfx950), so their sum is that level.  DPP moves
+// give the levels inside a 16-lane row: quad_perm for xor 1 and 2, row_ror:8
+// for xor 8, row_ror:4 for xor 4 once values repeat every 8 lanes, and the
+// half-row and row mirrors for xor 4 and 8 once values are equal within
+// quads.  Each level adds the same two values as the shuffle butterfly and
+// fp addition commutes, so the sums are the same bits.
+constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_QUAD0 = 0x00;
+constexpr int DPP_ROW_MIRROR = 0x140, DPP_HALF_MIRROR = 0x141;
+constexpr int DPP_ROR4 = 0x124, DPP_ROR8 = 0x128;
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
+  return __builtin_amdgcn_update_dpp(0u, x, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __uint_as_float(dpp_u<CTRL>(__float_as_uint(x)));
+}
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double x) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, x);
+  const uint32_t lo = dpp_u<CTRL>((uint32_t)b), hi = dpp_u<CTRL>((uint32_t)(b >> 32));
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ float xor32_sum_f(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_sum_f(float x) {
+  const uint32_t u = __float_as_uint(x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+template <bool W32>
+__device__ __forceinline__ double xor_sum_d(double x) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, x);
+  const uint32_t lo = (uint32_t)b, hi = (uint32_t)(b >> 32);
+  const auto rl = W32 ? __builtin_amdgcn_permlane32_swap(lo, lo, false, false)
+                      : __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+  const auto rh = W32 ? __builtin_amdgcn_permlane32_swap(hi, hi, false, false)
+                      : __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+  const double a = __builtin_bit_cast(double, ((uint64_t)rh[0] << 32) | rl[0]);
+  const double c = __builtin_bit_cast(double, ((uint64_t)rh[1] << 32) | rl[1]);
+  return a + c;
+}
+// the sum over the wavefront in every lane, levels xor 32, 16, 8, 4, 2, 1
+__device__ __forceinline__ float wave_sum_f(float y) {
+  y = xor32_sum_f(y);
+  y = xor16_sum_f(y);
+  y += dpp_f<DPP_ROR8>(y);
+  y += dpp_f<DPP_ROR4>(y);
+  y += dpp_f<DPP_XOR2>(y);
+  y += dpp_f<DPP_XOR1>(y);
+  return y;
+}
+__device__ __forceinline__ double wave_sum_d(double y) {
+  y = xor_sum_d<true>(y);
+  y = xor_sum_d<false>(y);
+  y += dpp_d<DPP_ROR8>(y);
+  y += dpp_d<DPP_ROR4>(y);
+  y += dpp_d<DPP_XOR2>(y);
+  y += dpp_d<DPP_XOR1>(y);
+  return y;
+}
+
 // ------------------------------------------------------------ panel QR ---
 // Block reduction of NV floats over a workgroup of up to 1024 threads: every thread
 // receives the NV sums in out[] (LDS).  (A reduce-scatter across the wave's
@@ -50,10 +120,7 @@ __device__ __forceinline__ void block_sum_f(float (&x)[NV], float (*red)[NV + 1]
   const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
 #pragma unroll
   for (int v = 0; v < NV; ++v) {
-    float y = x[v];
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) y += __shfl_xor(y, o);
-    x[v] = y;
+    x[v] = wave_sum_f(x[v]);
   }
   if (lane == 0)
 #pragma unroll
@@ -894,20 +961,7 @@ struct Sb2stLds {
 constexpr int SB_D0 = NB * (NB + 1);
 constexpr int SB_JUNK = 2 * NB * (NB + 1) + 3 * NB;
 
-// Butterfly sums inside a 16-lane row by DPP moves (VALU, no LDS round
-// trip).  quad_perm [1,0,3,2] and [2,3,0,1] read lanes l^1 and l^2; once the
-// four lanes of a quad hold equal values, the half-row mirror pairs quad j
-// with quad j^1 and the row mirror half h with h^1, so the sums are the
-// xor-butterfly's operand for operand.
-template <int CTRL>
-__device__ __forceinline__ double dpp_d(double x) {
-  const uint64_t b = __builtin_bit_cast(uint64_t, x);
-  const uint32_t lo = __builtin_amdgcn_update_dpp(0u, (uint32_t)b, CTRL, 0xf, 0xf, false);
-  const uint32_t hi = __builtin_amdgcn_update_dpp(0u, (uint32_t)(b >> 32), CTRL, 0xf, 0xf, false);
-  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
-}
-constexpr int DPP_XOR1 = 0xB1, DPP_XOR2 = 0x4E, DPP_QUAD0 = 0x00;
-constexpr int DPP_ROW_MIRROR = 0x140, DPP_HALF_MIRROR = 0x141;
+// sum over each quad (xor 1, 2), left in every lane of the quad
 __device__ __forceinline__ double sum4(double x) {
   x += dpp_d<DPP_XOR1>(x);
   x += dpp_d<DPP_XOR2>(x);
@@ -1086,8 +1140,8 @@ __global__ __launch_bounds__(SB_W * 64) void k_sb2st(double* band, int n, double
           a = dpp_d<DPP_QUAD0>(a);
           a += dpp_d<DPP_HALF_MIRROR>(a);
           a += dpp_d<DPP_ROW_MIRROR>(a);
-          a += __shfl_xor(a, 16);
-          a += __shfl_xor(a, 32);
+          a = xor_sum_d<false>(a);
+          a = xor_sum_d<true>(a);
           a *= 0.5 * tau;
           if (q == 0 && r < LM) S.y[r] = fma(-a, S.v[r], y);
           wave_sync();
@@ -1445,11 +1499,6 @@ __device__ __forceinline__ double mval(const float* orig, int n, int i, int c, d
   return v;
 }
 
-__device__ __forceinline__ double wave_sum_d(double x) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) x += __shfl_xor(x, o);
-  return x;
-}
 
 __device__ __forceinline__ double readlane_d(double x, int lane) {
   const uint64_t u = __builtin_bit_cast(uint64_t, x);
