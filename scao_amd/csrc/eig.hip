@@ -887,17 +887,28 @@ __global__ __launch_bounds__(256) void k_sy2sb_reduce(const float* Pd, const flo
   const int row = e0 / 16, col = e0 % 16;
   if (UT * J + row >= mr) return;
   v4f s = {0.f, 0.f, 0.f, 0.f};
-  const int ncj = J / UCH + 1;
-  for (int c = 0; c < ncj; ++c) {
-    const v4f x = *(const v4f*)(Pd + (((int64_t)mat * nt + J) * nch + c) * (UT * 16) + e0);
+  // the terms in order; RU loads in flight at a time (one at a time, each
+  // block's chain of up to nt tiles waited on the memory latency per term)
+  constexpr int RU = 8;
+  auto add_run = [&](const float* base, int n_terms) {
+    int u0 = 0;
+    for (; u0 + RU <= n_terms; u0 += RU) {
+      v4f x[RU];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) s[t] += x[t];
-  }
-  for (int I = J + 1; I < nt; ++I) {
-    const v4f x = *(const v4f*)(Pt + (((int64_t)mat * nt + J) * nt + I) * (UT * 16) + e0);
+      for (int u = 0; u < RU; ++u) x[u] = *(const v4f*)(base + (int64_t)(u0 + u) * (UT * 16) + e0);
 #pragma unroll
-    for (int t = 0; t < 4; ++t) s[t] += x[t];
-  }
+      for (int u = 0; u < RU; ++u)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) s[t] += x[u][t];
+    }
+    for (; u0 < n_terms; ++u0) {
+      const v4f x = *(const v4f*)(base + (int64_t)u0 * (UT * 16) + e0);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) s[t] += x[t];
+    }
+  };
+  add_run(Pd + ((int64_t)mat * nt + J) * nch * (UT * 16), J / UCH + 1);
+  add_run(Pt + (((int64_t)mat * nt + J) * nt + J + 1) * (UT * 16), nt - J - 1);
   *(v4f*)(Y + (int64_t)mat * sY + (int64_t)(UT * J + row) * 16 + col) = s;
 }
 
