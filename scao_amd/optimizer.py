@@ -227,6 +227,14 @@ class SCAO(Optimizer):
         if self._ws is not None:
             self._ws.runtime[0] = float(v)
 
+    def _active(self) -> list:
+        """(group, parameter) for every parameter with a gradient, each
+        checked to live on a ROCm device."""
+        active = [(g, p) for g in self.param_groups for p in g["params"] if p.grad is not None]
+        for _, p in active:
+            require_hip(p, "parameter")
+        return active
+
     def _workspace(self, device: torch.device) -> Workspace:
         if self._ws is None:
             self._ws = Workspace(device)
@@ -294,13 +302,9 @@ class SCAO(Optimizer):
             with torch.enable_grad():
                 loss = closure()
         self._global_step += 1
-        active = [(g, p) for g in self.param_groups for p in g["params"] if p.grad is not None]
-        for _, p in active:
-            require_hip(p, "parameter")
-        device = active[0][1].device if active else None
-        ws = self._workspace(device) if device is not None else self._ws
         host_norms = (self._dynamic_sparsity or self._adaptive_warmup or self._adaptive_rank
                       or self._lazy_precond)
+        active = self._active() if host_norms else None
         avg = 0.0
         if host_norms and active:
             norms = [float(p.grad.norm()) for _, p in active]
@@ -318,7 +322,13 @@ class SCAO(Optimizer):
             self._in_warmup_global = self._global_step <= wmax
 
         gsnr = self._gsnr_threshold if self._use_gsnr_clip else None
-        if not self._planned_step(ws, host_norms, gsnr):
+        # a plain step of the planned parameters checks each of them itself
+        # (_planned_step); any other step checks and plans every parameter
+        # that has a gradient
+        if not self._planned_step(self._ws, host_norms, gsnr):
+            if active is None:
+                active = self._active()
+            ws = self._workspace(active[0][1].device) if active else self._ws
             self._plan = None
             items, refresh, filtered = [], [], []
             for group, p in active:
@@ -365,7 +375,7 @@ class SCAO(Optimizer):
             return False
         items = plan.items
         n = len(items)
-        gptrs = np.empty(n, dtype=np.uint64)
+        ptrs = []
         grads = []
         i = 0
         for g in self.param_groups:
@@ -381,11 +391,12 @@ class SCAO(Optimizer):
                 ptr = gr.data_ptr()
                 if (it.aligned and ptr & 15) or it.ptrs[0] != p.data_ptr():
                     return False
-                gptrs[i] = ptr
+                ptrs.append(ptr)
                 grads.append(gr)
                 i += 1
         if i != n:
             return False
+        gptrs = np.array(ptrs, dtype=np.uint64)
         for it, moms in zip(items, plan.moments):
             st = it.st
             if (st["step"] != it.step or st["exp_avg"] is not moms[0]
@@ -405,6 +416,9 @@ class SCAO(Optimizer):
                     return False
             elif t > g["warmup_steps"]:
                 return False
+        # the launch needs only the class counters (advanced inside); the
+        # per-parameter host counters follow once the kernels are queued
+        engine.run_planned_step(plan, gptrs, ws, update_norm_ema=True)
         for it, gr in zip(items, grads):
             st = it.st
             st["step"] += 1
@@ -413,7 +427,6 @@ class SCAO(Optimizer):
                 st["scao_step"] += 1
                 it.scao_step += 1
             it.graw = gr
-        engine.run_planned_step(plan, gptrs, ws, update_norm_ema=True)
         return True
 
     def _filter_and_noise(self, items: list, filtered: list) -> None:
