@@ -201,6 +201,42 @@ CASES = {
                                use_int8_ema=False, k_min=256, k_max=256, warmup_steps=2,
                                blend_steps=2, precond_freq=4, min_precond_updates=1,
                                tau=None, lars_coeff=0.0), 6),
+    # shapes no other case combines: odd sizes split into blocks with
+    # remainders (97 = 64 + 33, 131 = 64 + 64 + 3), a conv weight, ranks that
+    # pad to the step widths 64 (33), 128 (65) and 256 (130), and tall, thin
+    # factors
+    "sweep_odd_blocks": ({"a": (97, 131), "b": (131, 97), "conv": (8, 3, 5, 5), "v": (300,)},
+                         dict(lr=1e-2, weight_decay=0.01, max_precond_dim=64, rho=0.99,
+                              use_int8_ema=True, k_min=3, k_max=9, warmup_steps=3,
+                              blend_steps=2, precond_freq=3, min_precond_updates=1, tau=1.0,
+                              lars_coeff=1e-3), 8),
+    "sweep_pad_k33": ({"a": (130, 70), "b": (70, 130)},
+                      dict(lr=1e-3, weight_decay=0.0, max_precond_dim=256, rho=0.99,
+                           use_int8_ema=False, k_min=33, k_max=33, warmup_steps=2,
+                           blend_steps=2, precond_freq=3, min_precond_updates=1, tau=None,
+                           lars_coeff=0.0), 6),
+    "sweep_pad_k65": ({"a": (256, 192), "ln": (192,)},
+                      dict(lr=1e-3, weight_decay=0.01, max_precond_dim=512, rho=0.999,
+                           use_int8_ema=True, k_min=65, k_max=65, warmup_steps=2,
+                           blend_steps=2, precond_freq=4, min_precond_updates=1, tau=1.0,
+                           lars_coeff=1e-3), 6),
+    "sweep_pad_k130": ({"a": (320, 256)},
+                       dict(lr=1e-3, weight_decay=0.01, max_precond_dim=512, rho=0.999,
+                            use_int8_ema=False, k_min=130, k_max=130, warmup_steps=2,
+                            blend_steps=2, precond_freq=4, min_precond_updates=1, tau=0.05,
+                            lars_coeff=1e-3), 6),
+    # a rank above the block's dimensions (clamped), and 1-row / 1-column
+    # matrices beside it
+    "sweep_k_over_dim": ({"a": (48, 40), "row": (1, 200), "col": (200, 1)},
+                         dict(lr=1e-2, weight_decay=0.01, max_precond_dim=64, rho=0.99,
+                              use_int8_ema=True, k_min=64, k_max=64, warmup_steps=2,
+                              blend_steps=2, precond_freq=3, min_precond_updates=1, tau=1.0,
+                              lars_coeff=1e-3), 6),
+    "sweep_tall_thin": ({"a": (1000, 12), "b": (12, 1000)},
+                        dict(lr=1e-2, weight_decay=0.01, max_precond_dim=1024, rho=0.99,
+                             use_int8_ema=True, k_min=4, k_max=8, warmup_steps=2,
+                             blend_steps=2, precond_freq=3, min_precond_updates=1, tau=1.0,
+                             lars_coeff=1e-3), 6),
 }
 
 
