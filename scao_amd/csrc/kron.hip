@@ -395,12 +395,70 @@ __device__ __forceinline__ void project_tile_x6(const scao_leaf_desc& L, const s
 // so one float4 of a U_r row feeds all four tiles.
 constexpr int DP = 64 + 4;   // LDS pitch of a partial tile
 
+// X6 (whole tiles, n % 128 == 0): the products on the bf16 matrix cores, six
+// per fp32 product over three-way splits (as the projection), each wave's
+// quarter of n in chunks of 32 rows of U_r: lane (i, g) takes T row
+// c0 + 16q + i at columns j + 8g .. j + 8g + 7 (the A operand of row tile q)
+// and U_r rows j + 8g .. j + 8g + 7 at columns d0 + 4i .. d0 + 4i + 3 (element t
+// of each float4 is the B operand of column tile t).  The accumulator layout
+// is the fp32 form's, so the partial tiles and the epilogue are shared.
+__device__ __forceinline__ void delta_acc_x6(const scao_leaf_desc& L, int c0, int d0, int jbeg,
+                                             int jend, v4f (&acc)[4][4]) {
+  const int l = threadIdx.x % 64, i = l % 16, g = l / 16;
+  const int n = L.n, k = L.k;
+  const float* __restrict__ T = L.T;
+  const float* __restrict__ Ur = L.Ur;
+  // each operand's next-chunk load goes out as soon as its current value is
+  // split, into the same registers; on the last chunk the loads repeat it
+  // (in bounds, unused), so no branch makes the compiler wait for them
+  v4f ca[4][2], cb[8];
+  auto load_a = [&](int jb, int q, v4f (&a)[2]) {
+    const float* tp = T + (int64_t)(c0 + 16 * q + i) * n + jb + 8 * g;
+    a[0] = gld4(tp);
+    a[1] = gld4(tp + 4);
+  };
+  auto load_b = [&](int jb, v4f (&b)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) b[e] = gld4(Ur + (int64_t)(jb + 8 * g + e) * k + d0 + 4 * i);
+  };
+  if (jbeg >= jend) return;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) load_a(jbeg, q, ca[q]);
+  load_b(jbeg, cb);
+  for (int jb = jbeg; jb < jend; jb += 32) {
+    const int jn = jb + 32 < jend ? jb + 32 : jb;
+    bf3 bt[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = cb[e][t];
+      bt[t] = split_bf3(x);
+    }
+    load_b(jn, cb);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      float x[8];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[e] = ca[q][0][e];
+        x[4 + e] = ca[q][1][e];
+      }
+      const bf3 aq = split_bf3(x);
+      load_a(jn, q, ca[q]);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) acc[q][t] = mfma_x6(aq, bt[t], acc[q][t]);
+    }
+  }
+}
+
 // Ps (three partial tiles) and red live in the caller's LDS, so a kernel
 // holding both instantiations allocates them once.
-template <bool FAST>
+template <bool FAST, bool X6 = false>
 __device__ __forceinline__ void delta_tile(const scao_leaf_desc& L, float eps, int c0, int d0,
                                            int slot, double* slots, float (*Ps)[64][DP],
                                            double* red) {
+  static_assert(FAST || !X6, "X6 needs whole tiles");
   const int w = threadIdx.x / 64, l = threadIdx.x % 64;
   const int n = L.n, k = L.k;
   const int kk = l / 16;
@@ -421,43 +479,47 @@ __device__ __forceinline__ void delta_tile(const scao_leaf_desc& L, float eps, i
 #pragma unroll
     for (int t = 0; t < 4; ++t) acc[q][t] = v4f{0.f, 0.f, 0.f, 0.f};
 
-  v4f ra[4], rb[4], na[4], nb[4];
-  auto load = [&](int jb, v4f (&a)[4], v4f (&b)[4]) {
-    const int j = jb + 4 * kk;
-    int jm = 15;
-    if (!FAST)
-      for (int s2 = 0; s2 < 4; ++s2) jm = (j + s2 < jend) ? jm : (jm & ~(1 << s2));
+  if constexpr (X6) {
+    delta_acc_x6(L, c0, d0, jbeg, jend, acc);
+  } else {
+    v4f ra[4], rb[4], na[4], nb[4];
+    auto load = [&](int jb, v4f (&a)[4], v4f (&b)[4]) {
+      const int j = jb + 4 * kk;
+      int jm = 15;
+      if (!FAST)
+        for (int s2 = 0; s2 < 4; ++s2) jm = (j + s2 < jend) ? jm : (jm & ~(1 << s2));
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int c = c0 + 16 * q + (l % 16);
-      if (FAST)
-        a[q] = gld4(T + (int64_t)c * n + j);
-      else
-        a[q] = (c < k && jm) ? ldf4(T, (int64_t)c * n + j, tvec_leaf && jm == 15, jm)
-                             : v4f{0.f, 0.f, 0.f, 0.f};
-    }
+      for (int q = 0; q < 4; ++q) {
+        const int c = c0 + 16 * q + (l % 16);
+        if (FAST)
+          a[q] = gld4(T + (int64_t)c * n + j);
+        else
+          a[q] = (c < k && jm) ? ldf4(T, (int64_t)c * n + j, tvec_leaf && jm == 15, jm)
+                               : v4f{0.f, 0.f, 0.f, 0.f};
+      }
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2) {
-      if (FAST)
-        b[s2] = gld4(Ur + (int64_t)(j + s2) * k + dl);
-      else
-        b[s2] = (((jm >> s2) & 1) && dmask) ? ldf4(Ur, (int64_t)(j + s2) * k + dl, uvec, dmask)
-                                            : v4f{0.f, 0.f, 0.f, 0.f};
-    }
-  };
-  if (jbeg < jend) load(jbeg, ra, rb);
-  for (int jb = jbeg; jb < jend; jb += 16) {
-    if (jb + 16 < jend) load(jb + 16, na, nb);
+      for (int s2 = 0; s2 < 4; ++s2) {
+        if (FAST)
+          b[s2] = gld4(Ur + (int64_t)(j + s2) * k + dl);
+        else
+          b[s2] = (((jm >> s2) & 1) && dmask) ? ldf4(Ur, (int64_t)(j + s2) * k + dl, uvec, dmask)
+                                              : v4f{0.f, 0.f, 0.f, 0.f};
+      }
+    };
+    if (jbeg < jend) load(jbeg, ra, rb);
+    for (int jb = jbeg; jb < jend; jb += 16) {
+      if (jb + 16 < jend) load(jb + 16, na, nb);
 #pragma unroll
-    for (int s2 = 0; s2 < 4; ++s2)
+      for (int s2 = 0; s2 < 4; ++s2)
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
+        for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int t = 0; t < 4; ++t) acc[q][t] = mfma16(ra[q][s2], rb[s2][t], acc[q][t]);
+          for (int t = 0; t < 4; ++t) acc[q][t] = mfma16(ra[q][s2], rb[s2][t], acc[q][t]);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      ra[q] = na[q];
-      rb[q] = nb[q];
+      for (int q = 0; q < 4; ++q) {
+        ra[q] = na[q];
+        rb[q] = nb[q];
+      }
     }
   }
   // partial tiles of waves 1..3 go through LDS; wave 0 adds them in order
@@ -1728,10 +1790,10 @@ __global__ __launch_bounds__(NT) void k_project_x6(const scao_task* __restrict__
   const scao_leaf_desc L = leaves[tk.idx];
   project_tile_x6<DO_P, CR, NT>(L, params[L.param], tk.a, tk.b, tk.slot, slots);
 }
-__global__ __launch_bounds__(256) void k_delta(const scao_task* __restrict__ tasks,
-                                               const scao_leaf_desc* __restrict__ leaves,
-                                               const scao_param_desc* __restrict__ params,
-                                               double* slots) {
+// two waves per SIMD: the bf16-product tiles fit 256 registers without spilling
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_delta(
+    const scao_task* __restrict__ tasks, const scao_leaf_desc* __restrict__ leaves,
+    const scao_param_desc* __restrict__ params, double* slots) {
   const scao_task tk = tasks[blockIdx.x];
   const scao_leaf_desc L = leaves[tk.idx];
   __shared__ __attribute__((aligned(16))) float Ps[3][64][DP];
@@ -1742,7 +1804,9 @@ __global__ __launch_bounds__(256) void k_delta(const scao_task* __restrict__ tas
   }
   const bool fast = (L.flags & SCAO_LF_VEC4) && (L.k % 4 == 0) && tk.a + 64 <= L.k &&
                     tk.b + 64 <= L.k && (L.n % 64 == 0);
-  if (fast)
+  if (fast && L.n % 128 == 0)
+    delta_tile<true, true>(L, params[L.param].eps, tk.a, tk.b, tk.slot, slots, Ps, red);
+  else if (fast)
     delta_tile<true>(L, params[L.param].eps, tk.a, tk.b, tk.slot, slots, Ps, red);
   else
     delta_tile<false>(L, params[L.param].eps, tk.a, tk.b, tk.slot, slots, Ps, red);
