@@ -395,31 +395,31 @@ __device__ __forceinline__ void project_tile_x6(const scao_leaf_desc& L, const s
 // so one float4 of a U_r row feeds all four tiles.
 constexpr int DP = 64 + 4;   // LDS pitch of a partial tile
 
-// X6 (whole tiles, n % 128 == 0): the products on the bf16 matrix cores, six
-// per fp32 product over three-way splits (as the projection), each wave's
-// quarter of n in chunks of 32 rows of U_r: lane (i, g) takes T row
-// c0 + 16q + i at columns j + 8g .. j + 8g + 7 (the A operand of row tile q)
-// and U_r rows j + 8g .. j + 8g + 7 at columns d0 + 4i .. d0 + 4i + 3 (element t
-// of each float4 is the B operand of column tile t).  The accumulator layout
-// is the fp32 form's, so the partial tiles and the epilogue are shared.
-__device__ __forceinline__ void delta_acc_x6(const scao_leaf_desc& L, int c0, int d0, int jbeg,
-                                             int jend, v4f (&acc)[4][4]) {
+// acc[q][t] += sum over j in [jbeg, jend) of A[r0 + 16q + i][j] * B[j][c0 + 4i + t]
+// (i = lane % 16) for a 64 x 64 output tile, with the products on the bf16
+// matrix cores: six per fp32 product over three-way splits, as the
+// projection.  The reduction runs in chunks of 32: lane (i, g) takes A row
+// r0 + 16q + i at columns j + 8g .. j + 8g + 7 (the A operand of row tile q)
+// and B rows j + 8g .. j + 8g + 7 at columns c0 + 4i .. c0 + 4i + 3 (element t
+// of each float4 is the B operand of column tile t), so the accumulator layout
+// is the fp32 16x16x4 form's with the same column permutation.  Rows of A and
+// B are 16-byte aligned and jend - jbeg is a multiple of 32.
+__device__ __forceinline__ void mm64_x6(const float* __restrict__ A, int64_t lda,
+                                        const float* __restrict__ B, int64_t ldb, int r0, int c0,
+                                        int jbeg, int jend, v4f (&acc)[4][4]) {
   const int l = threadIdx.x % 64, i = l % 16, g = l / 16;
-  const int n = L.n, k = L.k;
-  const float* __restrict__ T = L.T;
-  const float* __restrict__ Ur = L.Ur;
   // each operand's next-chunk load goes out as soon as its current value is
   // split, into the same registers; on the last chunk the loads repeat it
   // (in bounds, unused), so no branch makes the compiler wait for them
   v4f ca[4][2], cb[8];
   auto load_a = [&](int jb, int q, v4f (&a)[2]) {
-    const float* tp = T + (int64_t)(c0 + 16 * q + i) * n + jb + 8 * g;
-    a[0] = gld4(tp);
-    a[1] = gld4(tp + 4);
+    const float* ap = A + (int64_t)(r0 + 16 * q + i) * lda + jb + 8 * g;
+    a[0] = gld4(ap);
+    a[1] = gld4(ap + 4);
   };
   auto load_b = [&](int jb, v4f (&b)[8]) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) b[e] = gld4(Ur + (int64_t)(jb + 8 * g + e) * k + d0 + 4 * i);
+    for (int e = 0; e < 8; ++e) b[e] = gld4(B + (int64_t)(jb + 8 * g + e) * ldb + c0 + 4 * i);
   };
   if (jbeg >= jend) return;
 #pragma unroll
@@ -480,7 +480,8 @@ __device__ __forceinline__ void delta_tile(const scao_leaf_desc& L, float eps, i
     for (int t = 0; t < 4; ++t) acc[q][t] = v4f{0.f, 0.f, 0.f, 0.f};
 
   if constexpr (X6) {
-    delta_acc_x6(L, c0, d0, jbeg, jend, acc);
+    // whole tiles, n % 128 == 0: each wave's quarter of n is a multiple of 32
+    mm64_x6(T, n, Ur, k, c0, d0, jbeg, jend, acc);
   } else {
     v4f ra[4], rb[4], na[4], nb[4];
     auto load = [&](int jb, v4f (&a)[4], v4f (&b)[4]) {
@@ -771,6 +772,50 @@ __device__ __forceinline__ void lift_tile(const scao_leaf_desc& L, int i0, int d
         if (L.Wb) store_split1(L.Wb, (int64_t)m * k, (int64_t)i * k + d, acc[t][r]);
       }
     }
+  }
+}
+
+// The same tile for k % 128 == 0 on whole, aligned tiles, with the products on
+// the bf16 matrix cores (mm64_x6): wave w takes the whole 64 x 64 tile over
+// its quarter of k (a multiple of 32), the four partial tiles go through LDS,
+// and wave w adds rows 16w .. 16w + 15 of them in order (((w0 + w1) + w2) + w3)
+// and writes those rows of W (and Wb).
+__device__ __forceinline__ bool lift_x6_ok(const scao_leaf_desc& L, int i0, int d0) {
+  return L.k % 128 == 0 && i0 + 64 <= L.m && d0 + 64 <= L.k &&
+         (((uintptr_t)L.Ul | (uintptr_t)L.Delta | (uintptr_t)L.W) & 15) == 0 &&
+         ((uintptr_t)L.Wb & 7) == 0;
+}
+__device__ __forceinline__ void lift_tile_x6(const scao_leaf_desc& L, int i0, int d0,
+                                             float (*Ps)[64][DP]) {
+  const int w = threadIdx.x / 64, l = threadIdx.x % 64, jj = l % 16, g = l / 16;
+  const int m = L.m, k = L.k, kq = k / 4;
+  v4f acc[4][4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc[q][t] = v4f{0.f, 0.f, 0.f, 0.f};
+  mm64_x6(L.Ul, k, L.Delta, k, i0, d0, w * kq, w * kq + kq, acc);
+  // element (16q + 4g + r, 4jj + t) of the wave's partial tile
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      *(v4f*)&Ps[w][16 * q + 4 * g + r][4 * jj] =
+          v4f{acc[q][0][r], acc[q][1][r], acc[q][2][r], acc[q][3][r]};
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = 16 * w + 4 * g + r;
+    const v4f p0 = *(const v4f*)&Ps[0][row][4 * jj];
+    const v4f p1 = *(const v4f*)&Ps[1][row][4 * jj];
+    const v4f p2 = *(const v4f*)&Ps[2][row][4 * jj];
+    const v4f p3 = *(const v4f*)&Ps[3][row][4 * jj];
+    v4f x;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) x[t] = ((p0[t] + p1[t]) + p2[t]) + p3[t];
+    const int64_t o = (int64_t)(i0 + row) * k + d0 + 4 * jj;
+    gst4(L.W + o, x);
+    if (L.Wb) store_split4(L.Wb, (int64_t)m * k, o, x);
   }
 }
 
@@ -1811,11 +1856,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
   else
     delta_tile<false>(L, params[L.param].eps, tk.a, tk.b, tk.slot, slots, Ps, red);
 }
-__global__ __launch_bounds__(256) void k_lift(const scao_task* __restrict__ tasks,
-                                              const scao_leaf_desc* __restrict__ leaves) {
+// two waves per SIMD: the bf16-product tiles fit 256 registers without spilling
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_lift(
+    const scao_task* __restrict__ tasks, const scao_leaf_desc* __restrict__ leaves) {
+  __shared__ __attribute__((aligned(16))) float Ps[4][64][DP];
   const scao_task tk = tasks[blockIdx.x];
   const scao_leaf_desc L = leaves[tk.idx];
-  lift_tile(L, tk.a, tk.b);
+  if (lift_x6_ok(L, tk.a, tk.b))
+    lift_tile_x6(L, tk.a, tk.b, Ps);
+  else
+    lift_tile(L, tk.a, tk.b);
 }
 template <bool GF32, bool LARS, bool FAST>
 __global__ __launch_bounds__(256) void k_apply(const scao_task* __restrict__ tasks,
