@@ -1602,79 +1602,15 @@ __device__ __forceinline__ double enter_value(const Enter& e, int L, double sigm
   return v;
 }
 
-// Run LEAF(s) for the slot s == p (uniform) of the window: a binary tree of
-// scalar branches, about log2(WR) compares instead of one per slot.  It is a
-// macro so that every leaf names its slot with a constant inside the solve
-// itself (the window stays in registers; a helper taking the window by
-// reference lets the compiler merge the leaves into one indexed access,
-// which moves the window to scratch memory).
-static_assert(WR == 17, "the slot tree is written for 17 window rows");
-#define SLOT_TREE(p, LEAF) \
-  if (p <= 8) {          \
-    if (p <= 4) {        \
-      if (p <= 2) {      \
-        if (p <= 1) {    \
-          if (p <= 0) {  \
-            LEAF(0)      \
-          } else {       \
-            LEAF(1)      \
-          }              \
-        } else {         \
-          LEAF(2)        \
-        }                \
-      } else {           \
-        if (p <= 3) {    \
-          LEAF(3)        \
-        } else {         \
-          LEAF(4)        \
-        }                \
-      }                  \
-    } else {             \
-      if (p <= 6) {      \
-        if (p <= 5) {    \
-          LEAF(5)        \
-        } else {         \
-          LEAF(6)        \
-        }                \
-      } else {           \
-        if (p <= 7) {    \
-          LEAF(7)        \
-        } else {         \
-          LEAF(8)        \
-        }                \
-      }                  \
-    }                    \
-  } else {               \
-    if (p <= 12) {       \
-      if (p <= 10) {     \
-        if (p <= 9) {    \
-          LEAF(9)        \
-        } else {         \
-          LEAF(10)       \
-        }                \
-      } else {           \
-        if (p <= 11) {   \
-          LEAF(11)       \
-        } else {         \
-          LEAF(12)       \
-        }                \
-      }                  \
-    } else {             \
-      if (p <= 14) {     \
-        if (p <= 13) {   \
-          LEAF(13)       \
-        } else {         \
-          LEAF(14)       \
-        }                \
-      } else {           \
-        if (p <= 15) {   \
-          LEAF(15)       \
-        } else {         \
-          LEAF(16)       \
-        }                \
-      }                  \
-    }                    \
-  }
+// The window's 17 row slots: slots 0..15 as one 16-double vector (a single
+// 1024-bit register tuple), slot 16 beside it.  Slot p (wave-uniform, known
+// only at run time) is then read and written in place through the register
+// index mode (s_set_gpr_idx_on): two moves per access, no branches.  A plain
+// 17-element array indexed at run time would move to scratch memory, and a
+// conditional write into the vector makes the compiler copy the whole tuple,
+// so every access below is unconditional.
+static_assert(WR == 17, "the window is 16 vector slots and one more");
+typedef double v16d __attribute__((ext_vector_type(16)));
 
 // Solve (B - sigma I) x = rhs with band LU and partial pivoting; rhs given by
 // `rhs` (NULL: start_val).  U rows (WC doubles each) and the transformed rhs
@@ -1693,11 +1629,15 @@ __device__ __forceinline__ double band_solve(const float* __restrict__ orig, int
   const int L = threadIdx.x & 63;
   const bool act = L < WC;          // a matrix column
   const bool rl = L == WC;          // the right-hand side
-  double W[WR];
+  v16d W;          // slots 0..15
+  double Wx;       // slot 16
   // initial window: rows 0..16, columns 0..32 (lane L <-> column L)
+  auto init = [&](int s) {
+    return act ? mval(orig, n, s, L, sigma) : (rl ? enter_rhs(rhs, vid, n, s) : 0.0);
+  };
 #pragma unroll
-  for (int s = 0; s < WR; ++s)
-    W[s] = act ? mval(orig, n, s, L, sigma) : (rl ? enter_rhs(rhs, vid, n, s) : 0.0);
+  for (int s = 0; s < 16; ++s) W[s] = init(s);
+  Wx = init(16);
   Enter qW[PF];
 #pragma unroll
   for (int t = 0; t < PF; ++t) qW[t] = enter_load<HAS_RHS>(orig, rhs, vid, n, t, L);
@@ -1717,7 +1657,7 @@ __device__ __forceinline__ double band_solve(const float* __restrict__ orig, int
       uint32_t best = 0;
 #pragma unroll
       for (int s = 0; s < WR; ++s) {
-        col[s] = readlane_d(W[s], lj);
+        col[s] = readlane_d(s < 16 ? W[s & 15] : Wx, lj);
         const uint32_t m =
             (uint32_t)(__builtin_bit_cast(uint64_t, col[s]) >> 32) & 0x7fffffffu;
         if (s == 0 || m > best) {
@@ -1725,16 +1665,17 @@ __device__ __forceinline__ double band_solve(const float* __restrict__ orig, int
           p = s;
         }
       }
-      double piv = 0.0, prow = 0.0;
-#define PICK(s_) { asm volatile("" ::: "memory"); piv = col[s_]; prow = W[s_]; }
-      SLOT_TREE(p, PICK)
-#undef PICK
+      const int pi = p & 15;
+      const bool top = p < 16;
+      const double prow = top ? W[pi] : Wx;   // this lane's entry of the pivot row
+      double piv = readlane_d(prow, lj);      // == col[p]
       if (fabs(piv) < tiny) piv = piv < 0.0 ? -tiny : tiny;
       // every slot loses col[s] / piv times the pivot row, as col[s] * (row / piv)
       // (the pivot's own slot is overwritten below)
       const double q = prow / piv;
 #pragma unroll
-      for (int s = 0; s < WR; ++s) W[s] = fma(-col[s], q, W[s]);
+      for (int s = 0; s < 16; ++s) W[s] = fma(-col[s], q, W[s]);
+      Wx = fma(-col[16], q, Wx);
       // retire the pivot row as U row j (column offset of this lane) and its
       // right-hand side, staged
       const int off = (L - lj + WC) % WC;
@@ -1743,9 +1684,8 @@ __device__ __forceinline__ double band_solve(const float* __restrict__ orig, int
       // row j + 17 (prefetched PF steps ago) takes the pivot's slot; fetch
       // step j + PF's
       const double ent = enter_value(qW[t], L, sigma);
-#define PUT(s_) { asm volatile("" ::: "memory"); W[s_] = ent; }
-      SLOT_TREE(p, PUT)
-#undef PUT
+      W[pi] = top ? ent : W[pi];
+      Wx = top ? Wx : ent;
       qW[t] = enter_load<HAS_RHS>(orig, rhs, vid, n, j + PF, L);
     }
     const int je = j0 + PF < n ? j0 + PF : n;
