@@ -1573,14 +1573,20 @@ struct Enter {
   bool ok, dg;    // inside the band and the matrix; on the diagonal
 };
 
+// Lane L's window column offset at step j: (L - j) mod WC, carried from step
+// to step (one less each step, WC - 1 after 0) instead of a division per use.
+__device__ __forceinline__ int lane_rot(int L, int j) { return ((L - j) % WC + WC) % WC; }
+__device__ __forceinline__ int rot_next(int r) { return r == 0 ? WC - 1 : r - 1; }
+
+// The band value entering step j's window in lane L's column: column
+// j + 1 + rot, rot = lane_rot(L, j + 1) (the lane's offset once step j is done).
 template <bool HAS_RHS>
 __device__ __forceinline__ Enter enter_load(const float* orig, const double* rhs, uint32_t vid,
-                                            int n, int j, int L) {
+                                            int n, int j, int L, int rot) {
   // every lane issues the same loads (clamped addresses), no branches
   Enter e;
   const int i = j + WR;
-  const int lj = j % WC;
-  const int c = j + 1 + ((L - (lj + 1)) % WC + WC) % WC;
+  const int c = j + 1 + rot;
   const int dd = i - c;
   const bool inb = i < n;
   const bool band = L < WC && inb && c < n && dd <= NB && dd >= -NB;
@@ -1640,7 +1646,9 @@ __device__ __forceinline__ double band_solve(const float* __restrict__ orig, int
   Wx = init(16);
   Enter qW[PF];
 #pragma unroll
-  for (int t = 0; t < PF; ++t) qW[t] = enter_load<HAS_RHS>(orig, rhs, vid, n, t, L);
+  for (int t = 0; t < PF; ++t) qW[t] = enter_load<HAS_RHS>(orig, rhs, vid, n, t, L, lane_rot(L, t + 1));
+  int rot_st = lane_rot(L, 0);        // this step's offset (U row staging)
+  int rot_ld = lane_rot(L, PF + 1);   // the offset of the load PF steps ahead
   const double tiny = 2.220446049250313e-16 * bnorm + 1e-300;
   int jf = 0;                        // first U row not yet written out
   for (int j0 = 0; j0 < n; j0 += PF) {
@@ -1678,7 +1686,7 @@ __device__ __forceinline__ double band_solve(const float* __restrict__ orig, int
       Wx = fma(-col[16], q, Wx);
       // retire the pivot row as U row j (column offset of this lane) and its
       // right-hand side, staged
-      const int off = (L - lj + WC) % WC;
+      const int off = rot_st;
       if (act) st[(j % UF) * (WC + 1) + off] = L == lj ? piv : prow;
       if (rl) st[(j % UF) * (WC + 1) + WC] = prow;
       // row j + 17 (prefetched PF steps ago) takes the pivot's slot; fetch
@@ -1686,7 +1694,9 @@ __device__ __forceinline__ double band_solve(const float* __restrict__ orig, int
       const double ent = enter_value(qW[t], L, sigma);
       W[pi] = top ? ent : W[pi];
       Wx = top ? Wx : ent;
-      qW[t] = enter_load<HAS_RHS>(orig, rhs, vid, n, j + PF, L);
+      qW[t] = enter_load<HAS_RHS>(orig, rhs, vid, n, j + PF, L, rot_ld);
+      rot_st = rot_next(rot_st);
+      rot_ld = rot_next(rot_ld);
     }
     const int je = j0 + PF < n ? j0 + PF : n;
     if (je - jf >= UF || je == n) {
@@ -1787,7 +1797,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(5, 5))) voi
                                                  const double* bnorm, double* work, double* xall,
                                                  double* wr) {
   __shared__ double stage[4][UST];   // each wavefront's staged U rows / solution
-  const int wv = threadIdx.x >> 6;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // uniform: scalar registers
   const int vid = v0 + blockIdx.x * 4 + wv;
   if (vid >= nvec) return;
   const int mat = vid / kq, idx = vid % kq;
