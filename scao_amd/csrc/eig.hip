@@ -1538,15 +1538,6 @@ __device__ __forceinline__ double start_val(uint32_t vid, int row) {
 // (38.7 ms against 40.5 ms for 4 at four waves, 480 x 2048^2, kq = 64).
 constexpr int PF = 2;
 
-// Value entering lane L's slot 0 at the end of elimination step j: row
-// j + WR, column j + 1 + ((L - (j mod WC) - 1) mod WC).
-__device__ __forceinline__ double enter_val(const float* orig, int n, int j, int L, bool act,
-                                            double sigma) {
-  const int lj = j % WC;
-  const int colL = j + 1 + ((L - (lj + 1)) % WC + WC) % WC;
-  return act ? mval(orig, n, j + WR, colL, sigma) : 0.0;
-}
-
 __device__ __forceinline__ double enter_rhs(const double* rhs, uint32_t vid, int n, int i) {
   return i < n ? (rhs ? rhs[i] : start_val(vid, i)) : 0.0;
 }
