@@ -54,7 +54,8 @@ class _SparseGradFilter:
     step, exact order statistics by radix select); ``__call__`` filters one
     gradient through the same entry point.  torch.quantile refuses more than
     2**24 elements, so the reference raises for such a parameter; this filter
-    computes the same statistic for any size."""
+    computes the same statistic for any size.  It refuses an empty input too
+    (reference :56); here an empty gradient is skipped and stays empty."""
 
     def __init__(self, sparsity: float = 0.7, ema: float = 0.99):
         self.sparsity, self.ema, self.mag_ema = sparsity, ema, None
