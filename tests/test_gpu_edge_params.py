@@ -91,3 +91,20 @@ def test_empty_params_change_nothing(sparsity, int8):
                 assert (st["step"], st["scao_step"]) == (sr["step"], sr["scao_step"]), (t, r.shape)
     # the run reached Phase 2 on the ordinary parameters
     assert all(with_empty.state[a]["scao_step"] > 0 for a in pa[:2])
+
+
+def test_noncontiguous_param_refused():
+    """The kernels address every parameter as a dense row-major view, so a
+    parameter whose storage is laid out otherwise (here a transposed view) is
+    refused with a clear error at its first step; the reference accepts any
+    layout."""
+    import scao_amd
+    dev = _dev()
+    p = torch.nn.Parameter(torch.randn(8, 6, device=dev).t())
+    q = torch.nn.Parameter(torch.randn(6, 5, device=dev))
+    assert not p.is_contiguous()
+    opt = scao_amd.SCAO([q, p], lr=1e-3, sparsity=0.0, noise_std_init=0.0, lookahead_k=0)
+    p.grad = torch.randn_like(p)
+    q.grad = torch.randn_like(q)
+    with pytest.raises(RuntimeError, match="contiguous"):
+        opt.step()
