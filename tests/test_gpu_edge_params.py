@@ -108,3 +108,44 @@ def test_noncontiguous_param_refused():
     q.grad = torch.randn_like(q)
     with pytest.raises(RuntimeError, match="contiguous"):
         opt.step()
+
+
+def test_param_above_2_31_elements():
+    """A 1-D parameter of 2,147,484,000 elements (past 2**31) through Phase 1
+    and the diagonal-mode Phase 2 (refreshes, LARS, the planned-step path).
+    Parameters and gradients repeat with period 1000, and every update is
+    elementwise apart from per-parameter scalars, so every output must repeat
+    too, bit for bit: an offset that wrapped at 2**31, or a tail left
+    unwritten, breaks the period past that point.  About 70 GB of device
+    memory."""
+    import scao_amd
+    dev = _dev()
+    P, K = 1000, 2147484
+    assert P * K > 2 ** 31
+    g = torch.Generator(device=dev).manual_seed(5)
+    p = torch.nn.Parameter((torch.randn(P, generator=g, device=dev) * 0.02).repeat(K))
+    opt = scao_amd.SCAO([p], lr=1e-3, weight_decay=0.01, warmup_steps=2, blend_steps=2,
+                        precond_freq=2, min_precond_updates=1, sparsity=0.0, noise_std_init=0.0,
+                        lookahead_k=0)
+
+    def periodic(x):
+        v = x.view(K, P)
+        return torch.equal(v, v[:1].expand(K, P))
+
+    for t in range(1, 6):
+        p.grad = (torch.randn(P, generator=g, device=dev) * 0.02).repeat(K)
+        opt.step()
+        torch.cuda.synchronize()
+        st = opt.state[p]
+        assert st["step"] == t
+        assert periodic(p.detach()), t
+        for key in MOMENTS:
+            assert periodic(st[key]), (t, key)
+        p.grad = None
+    assert opt.state[p]["scao_step"] > 0   # Phase 2 ran
+    # the first period moved (a step that wrote nothing would pass the check)
+    assert not torch.equal(p.detach()[:P], (torch.randn(P, generator=torch.Generator(
+        device=dev).manual_seed(5), device=dev) * 0.02))
+    # hand the memory back: later tests size their batches by the free memory
+    del opt, p
+    torch.cuda.empty_cache()
