@@ -1725,8 +1725,9 @@ __global__ __launch_bounds__(strip_shape<K>::NT) void k_apply_strip(const scao_t
   v4f gr[4], gm[4], mm[4], vv[4], dd[4], pp[4], par[4];
   int64_t e[4];
   const int jc = tk.b + 64 * cg + 4 * (l % 16);
-  auto prefetch_row = [&](int s, int r) {
-    {
+  auto prefetch = [&](int s) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
       e[r] = L.off + (int64_t)(tk.a + s * TR + 16 * rg + 4 * kk + r) * L.ld + jc;
       gr[r] = gld4_nt((const float*)P.graw + e[r]);
       if (GF32) {
@@ -1742,15 +1743,6 @@ __global__ __launch_bounds__(strip_shape<K>::NT) void k_apply_strip(const scao_t
       if (!LARS) par[r] = gld4_nt((const float*)P.p + e[r]);
     }
   };
-  auto prefetch = [&](int s) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) prefetch_row(s, r);
-  };
-  // k = 128: rows 0 and 1 of the next step are loaded as soon as their
-  // registers are free, so they are in flight during rows 1..3's arithmetic
-  // (C4 23.0 -> 21.1 ms); at k = 256 the same measured 53.5 -> 60.6 ms, so
-  // there the next step's loads all go out after the last row's stores.
-  constexpr bool EARLY = K == 128;
   auto put_slot = [&](int s) {
     if (tk.slot < 0) return;
     const double* q = part[s & 1];
@@ -1791,20 +1783,10 @@ __global__ __launch_bounds__(strip_shape<K>::NT) void k_apply_strip(const scao_t
         gst4(P.upd + e[r], out);
       else
         gst4_nt((float*)P.p + e[r], out);
-      // unconditional (the last step reloads its own rows): a load on one
-      // path only would make the compiler wait for every load at the join
-      if (EARLY && r < 2) prefetch_row(s + 1 < nt ? s + 1 : s, r);
     }
     const double wsum = wave_sum((double)u2);
     if (l == 0) part[s & 1][w] = wsum;
-    if (s + 1 < nt) {
-      if (EARLY) {
-        prefetch_row(s + 1, 2);
-        prefetch_row(s + 1, 3);
-      } else {
-        prefetch(s + 1);
-      }
-    }
+    if (s + 1 < nt) prefetch(s + 1);
     __syncthreads();                                          // X_{s+1}
   }
   if (w == 0 && l == 0) put_slot(nt - 1);
