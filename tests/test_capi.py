@@ -108,3 +108,55 @@ def test_header_constants_match_the_python_binding():
             assert getattr(L, name) == int(val), name
             seen += 1
     assert seen >= 5
+
+
+# One call per status-returning entry point whose arguments fail the host-side
+# validation (a negative count, or null pointers with a non-zero size): it
+# returns 1 and names itself in scao_last_error(), before any device call.
+N = None
+BAD_ARGS = {
+    "scao_low_rank_precond_mm": (N, N, N, N, 4, 4, 4, 1, N, N),
+    "scao_fused_kronecker_precond": (N, N, N, N, N, 4, N, 4, 4, 2, N, N),
+    "scao_fused_kronecker_precond_noalloc": (N, N, N, N, N, 4, N, 4, 4, 2, N),
+    "scao_int8_ema_update": (N, 1.0, N, 0.9, 4, N, N, N),
+    "scao_kron_project": (N, -1, N, N, N, 1, N),
+    "scao_kron_delta": (N, -1, N, N, N, N),
+    "scao_kron_lift": (N, -1, N, N),
+    "scao_diag_reduce": (N, -1, N, N, N),
+    "scao_step_finalize": (N, -1, N, N, N, 0, 0, 0, N),
+    "scao_kron_apply": (N, -1, N, N, N, N, 0, N),
+    "scao_diag_apply": (N, -1, N, N, N, N),
+    "scao_lars_write": (N, -1, N, N, N),
+    "scao_adam_step": (N, -1, N, N, N),
+    "scao_gram_ema": (N, -1, N, N),
+    "scao_requant": (N, -1, N, N, N),
+    "scao_eig_prep": (N, -1, N, 0, N),
+    "scao_eig_offdiag": (N, -1, 8, 0, N, N),
+    "scao_eig_diag": (N, 1, 8, 4, N, N, 32, N, N),
+    "scao_diag_ema": (N, -1, N, N, N),
+    "scao_sparse_filter": (N, -1, N, 0, N),
+    "scao_eig_panel_qr": (N, 64, 8, 0, 1, N, N, 8 * 33, N),
+    "scao_eig_band_finish": (N, 64, 8, 1, N, 8 * 33, N, 8 * 17, N, N),
+    "scao_eig_sy2sb_panel_w": (N, 64, 8, 0, 1, N, N, N, 0, N),
+    "scao_eig_sy2sb_update": (N, 64, 8, 8, 1, N, 64, 8, N, 16, 16, N, 64, 8, N, 128, N, N),
+    "scao_eig_sb2st": (N, 8, 1, N, N, N),
+    "scao_eig_bisect": (N, N, 8, 1, 4, N, N, N, N),
+    "scao_eig_vectors": (N, 8 * 17, 8, 1, 4, N, N, 32, N, N),
+    "scao_eig_back_transform": (N, 64, 8, 1, N, N, 32, 4, N),
+    "scao_lookahead": (N, -1, N, 0.5, N),
+}
+
+
+def test_bad_argument_table_covers_every_entry_point():
+    from scao_amd import _lib as L
+    status = {name for name, (res, _) in L.SIGNATURES.items()
+              if res is ctypes.c_int and name not in ("scao_abi_version", "scao_struct_layout")}
+    assert status == set(BAD_ARGS)
+
+
+@pytest.mark.parametrize("name", sorted(BAD_ARGS))
+def test_entry_point_rejects_bad_arguments(name):
+    from scao_amd import _lib as L
+    lib = L.lib()
+    assert getattr(lib, name)(*BAD_ARGS[name]) == 1
+    assert lib.scao_last_error().decode().startswith(name + ":")
