@@ -1148,8 +1148,12 @@ __device__ __forceinline__ void apply_wide(const scao_leaf_desc& L, const scao_p
     gst4_nt(P.exp_avg_sq + e[r], vv[r]);
     gst4_nt(P.exp_avg_diff + e[r], dd[r]);
     gst4_nt(P.prev_grad + e[r], GF32 ? gm[r] : gr[r]);
+    // the staged update streams past the caches too: it is read back only by
+    // k_lars_write, after gigabytes of other traffic, and a caching store
+    // evicts the U_r rows the tiles read from L2 (C3 step 12.17 -> 11.98 ms in
+    // alternating runs; the strip apply at k = 256 measured slower with it)
     if (LARS)
-      gst4(P.upd + e[r], out);
+      gst4_nt(P.upd + e[r], out);
     else
       gst4_nt((float*)P.p + e[r], out);
   }
